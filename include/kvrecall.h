@@ -1,0 +1,308 @@
+/*
+ * kvrecall.h -- C ABI of the MI355X (gfx950) KVMem recall hot path.
+ *
+ * One layer of recall is: page summaries (mean-K) -> GQA query-vs-summary
+ * scoring -> page softmax + head aggregation -> top-k page selection ->
+ * gather of the selected K/V pages from pinned host history into a device
+ * slot array (copy, dequantize to fp16, or requantize to q8_0).
+ *
+ * Conventions
+ *  - Plain C: pointers, sizes and enums.  No exceptions cross this boundary.
+ *  - Every entry returns kvr_status; on failure kvr_last_error() holds a
+ *    message for the calling thread.  Geometry is validated on the host before
+ *    any launch: a rejected call launches nothing.
+ *  - "dev" pointers are device memory of the context's GPU, "pinned" pointers
+ *    are page-locked host memory (hipHostMalloc, or kvr_host_alloc), "host"
+ *    pointers are ordinary host memory read during the call.
+ *  - Streams are passed as `void*` (a hipStream_t); NULL selects the
+ *    context's own streams.  Calls are asynchronous on their stream.  Device
+ *    side operand errors (a query or summary value that is non-finite or
+ *    rounds to fp16 infinity) make the selection of that call empty and are
+ *    reported by kvr_check().
+ *  - A context is used by one host thread at a time.
+ *
+ * Reference citations are relative to the KVMem 0.19.0 source tree.
+ */
+#ifndef KVRECALL_H
+#define KVRECALL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KVR_VERSION_MAJOR 0
+#define KVR_VERSION_MINOR 1
+#define KVR_MAX_INLINE_MANDATORY 64
+#define KVR_MAX_PLANES 8
+
+typedef struct kvr_context kvr_context;
+
+typedef enum kvr_status {
+    KVR_OK = 0,
+    KVR_ERR_INVALID = 1,     /* invalid argument or geometry                    */
+    KVR_ERR_NONFINITE = 2,   /* recall operand NaN/inf (recall_fp16 rejects)    */
+    KVR_ERR_RANGE = 3,       /* recall operand rounds to fp16 infinity          */
+    KVR_ERR_BUDGET = 4,      /* mandatory pages exceed the selection budget     */
+    KVR_ERR_WORKSPACE = 5,   /* borrowed workspace too small for the call       */
+    KVR_ERR_HIP = 6,         /* HIP runtime error                               */
+    KVR_ERR_SCORES = 7,      /* negative or non-finite score without signed mode*/
+    KVR_ERR_UNSUPPORTED = 8  /* format/mode combination not provided            */
+} kvr_status;
+
+typedef enum kvr_format {
+    KVR_FMT_F16 = 0,   /* binary16                                          */
+    KVR_FMT_Q8_0 = 1,  /* blocks of 32: {fp16 d; int8 qs[32]}, 34 bytes     */
+    KVR_FMT_Q4_1 = 2,  /* blocks of 32: {fp16 d; fp16 m; u8 qs[16]}, 20 bytes*/
+    KVR_FMT_F32 = 3,   /* binary32 (query and capture input only)           */
+    KVR_FMT_BF16 = 4   /* bfloat16 (query and capture input only)           */
+} kvr_format;
+
+typedef enum kvr_aggregation {
+    KVR_AGG_MEAN = 0,      /* GqaScoreAggregation::Mean                        */
+    KVR_AGG_MAX = 1,       /* GqaScoreAggregation::Max (max of probabilities)  */
+    KVR_AGG_MAX_LOGIT = 2  /* max of the group's logits, then one softmax      */
+} kvr_aggregation;
+
+typedef enum kvr_tie_rule {
+    KVR_TIE_LOWER_FIRST = 0,  /* equal scores: lower page id wins              */
+    KVR_TIE_HIGHER_FIRST = 1  /* equal scores: higher id wins (KvMemStore rule) */
+} kvr_tie_rule;
+
+typedef enum kvr_gather_mode {
+    KVR_GATHER_COPY = 0,         /* bytes unchanged                           */
+    KVR_GATHER_DEQUANT_F16 = 1,  /* decode to binary32, RNE to binary16       */
+    KVR_GATHER_REQUANT_Q8_0 = 2  /* q8_0 -> binary32 -> q8_0                   */
+} kvr_gather_mode;
+
+typedef enum kvr_copy_engine {
+    KVR_ENGINE_AUTO = 0,    /* the faster engine for the mode                 */
+    KVR_ENGINE_KERNEL = 1,  /* device-driven kernel reading pinned memory     */
+    KVR_ENGINE_SDMA = 2     /* DMA copies (host reads the selection first)    */
+} kvr_copy_engine;
+
+/* Resident key history of `lanes` independent sequences, token-major rows of
+ * kv_heads*head_dim channels.  Lane i starts at data + i*lane_stride bytes. */
+typedef struct kvr_key_history {
+    const void *data;       /* dev */
+    kvr_format format;      /* KVR_FMT_F16 or KVR_FMT_Q8_0 */
+    uint64_t tokens;        /* per lane */
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t page_tokens;
+    uint32_t lanes;         /* 0 is read as 1 */
+    size_t lane_stride;     /* bytes; 0 = tightly packed */
+} kvr_key_history;
+
+/* Query rows of one layer: element (lane, r, h, d) at
+ * data + lane*lane_stride + r*row_stride + h*head_stride + d*dim_stride. */
+typedef struct kvr_query {
+    const void *data;       /* dev */
+    kvr_format scalar;      /* KVR_FMT_F32, KVR_FMT_F16 or KVR_FMT_BF16 */
+    uint32_t rows;
+    uint32_t query_heads;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    size_t row_stride, head_stride, dim_stride, lane_stride; /* bytes */
+    float attention_scale;  /* 0 selects 1/sqrt(head_dim) */
+} kvr_query;
+
+/* One plane (K or V) of one layer's history for the gather.  Lane i reads
+ * history + i*host_lane_stride and writes slots + i*slot_lane_stride.
+ * Slot s of a lane holds the lane's s-th selected page (ascending page id)
+ * at rows [s*page_tokens, s*page_tokens + valid). */
+typedef struct kvr_plane {
+    const void *history;    /* pinned, token-major rows */
+    kvr_format format;      /* KVR_FMT_F16, KVR_FMT_Q8_0 or KVR_FMT_Q4_1 */
+    uint32_t width;         /* channels per token row */
+    uint64_t tokens;        /* per lane */
+    kvr_gather_mode mode;
+    void *slots;            /* dev */
+    size_t host_lane_stride, slot_lane_stride; /* bytes; 0 = tightly packed */
+} kvr_plane;
+
+/* One layer of recall for `lanes` sequences (kvr_recall_layer). */
+typedef struct kvr_layer_recall {
+    const kvr_key_history *keys;   /* resident keys to summarize, or NULL to
+                                      score the resident `summaries` as given */
+    uint16_t *summaries;           /* dev fp16 [lanes][pages][Hkv*D] */
+    float *means;                  /* dev, optional binary32 mean-K output */
+    uint32_t pages;                /* pages per lane (when keys is NULL) */
+    uint32_t page_tokens;          /* (when keys is NULL) */
+    uint32_t lanes;                /* (when keys is NULL; 0 is read as 1) */
+    const kvr_query *query;
+    const uint8_t *score_mask;     /* dev [pages] or NULL for all pages */
+    kvr_aggregation aggregation;
+    uint32_t k;                    /* selection budget per lane */
+    kvr_tie_rule tie_rule;
+    const uint32_t *mandatory;     /* host, <= KVR_MAX_INLINE_MANDATORY ids */
+    uint32_t n_mandatory;
+    double *scores;                /* dev [lanes][pages] */
+    uint32_t *selected;            /* dev [lanes][k], ascending ids */
+    uint32_t *count;               /* dev [lanes] */
+    const kvr_plane *planes;       /* gather targets, may be NULL */
+    uint32_t n_planes;
+    kvr_copy_engine engine;
+    int force_mfma;                /* -1 never, 0 by rows*group >= 16, 1 always */
+    void *summary_begin;           /* optional hipEvent_t recorded on the select
+                                      stream just before / after the summary */
+    void *summary_end;             /* kernel (measurement only; may be NULL)  */
+} kvr_layer_recall;
+
+/* ---- context ------------------------------------------------------------ */
+
+/* Replaces PageSoftmaxCuda(int device) (kvmem/include/kvmem/page_softmax_cuda.hpp:13)
+ * and kvmem_gpu_state_create (src/adapter/llama-kvmem-stagein.h:12). */
+kvr_status kvr_create(int device, kvr_context **out);
+/* Replaces ~PageSoftmaxCuda and kvmem_gpu_state_free (llama-kvmem-stagein.h:14):
+ * drains the context's streams, then releases what it owns. */
+kvr_status kvr_destroy(kvr_context *ctx);
+/* Thread-local message of the last failed call (stderr text of cuda_ok,
+ * llama-kvmem-stagein.cu:93-99; exception text of page_softmax.cu:15-17). */
+const char *kvr_last_error(void);
+const char *kvr_status_string(kvr_status status);
+/* Drains `stream` (NULL: both context streams) and reports the first device
+ * side operand error raised since the previous check.  Replaces
+ * kvmem_stagein_sync_checked (llama-kvmem-stagein.h:34) and the poison-flag
+ * readback of score_current_layer (page_softmax.cu:372-375). */
+kvr_status kvr_check(kvr_context *ctx, void *stream);
+/* The context's own streams (hipStream_t), for event wiring by callers. */
+void *kvr_select_stream(kvr_context *ctx);
+void *kvr_copy_stream(kvr_context *ctx);
+
+/* ---- workspace ------------------------------------------------------------ */
+
+/* Device bytes one scoring call needs for this geometry.  Replaces
+ * PageSoftmaxCuda::workspace_bytes (page_softmax_cuda.hpp:15). */
+size_t kvr_workspace_bytes(uint32_t lanes, uint32_t max_pages, uint32_t max_rows,
+                           uint32_t query_heads, uint32_t kv_heads, uint32_t head_dim);
+/* Borrow a caller-planned workspace (256-byte aligned dev memory): afterwards
+ * no call on this context allocates device memory, and a call that needs more
+ * fails with KVR_ERR_WORKSPACE before any launch.  Replaces the borrowed
+ * workspace constructor (page_softmax_cuda.hpp:16-17, page_softmax.cu:181-192). */
+kvr_status kvr_bind_workspace(kvr_context *ctx, void *workspace, size_t bytes);
+/* Device bytes currently owned or borrowed.  Replaces device_bytes()
+ * (page_softmax_cuda.hpp:28). */
+size_t kvr_device_bytes(kvr_context *ctx);
+
+/* ---- page summaries ---------------------------------------------------- */
+
+/* Per page, per channel: binary32 sum of the page's key rows in token order
+ * from zero, times (1.0f/valid_tokens); then the fp16 operand rounding of
+ * recall_fp16.  Replaces RawKvStore::capture_mean_f16 / add_mean_f32 /
+ * mean_k (kvmem/src/host/raw_kv_store.cpp:158-197, 606-625) followed by the
+ * host staging loop of PageSoftmaxCuda::score (page_softmax.cu:239-248).
+ * means: dev [lanes][pages][Hkv*D] or NULL; summaries: dev fp16, same shape. */
+kvr_status kvr_summary_build(kvr_context *ctx, const kvr_key_history *keys, float *means,
+                             uint16_t *summaries, void *stream);
+
+/* Capture-side running sum: adds n key rows at positions pos0.. of one
+ * sequence into per-page binary32 sums (a segment starting at page offset 0
+ * restarts that page's sum), one channel per thread, token order.  Replaces
+ * kvmem_meank_add (llama-kvmem-stagein.h:63, stagein.cu:270-320) and
+ * RawKvStore::write_layer_mean_k (raw_kv_store.cpp:422-441).
+ * Element (t, h, d) of k is at k + t*token_stride + h*head_stride + d*dim_stride. */
+kvr_status kvr_summary_accumulate(kvr_context *ctx, float *sums, uint32_t *counts,
+                                  uint32_t page_tokens, const void *k, kvr_format scalar,
+                                  uint64_t pos0, uint32_t n, uint32_t kv_heads,
+                                  uint32_t head_dim, size_t token_stride,
+                                  size_t head_stride, size_t dim_stride, void *stream);
+/* means = sums * (1.0f/counts), summaries = fp16 operand of means (pages with
+ * count 0 give zeros).  Replaces RawKvStore::mean_k (raw_kv_store.cpp:606-614). */
+kvr_status kvr_summary_finalize(kvr_context *ctx, const float *sums, const uint32_t *counts,
+                                uint32_t pages, uint32_t width, float *means,
+                                uint16_t *summaries, void *stream);
+
+/* ---- scoring --------------------------------------------------------------- */
+
+/* Page softmax scores of one layer: logits scale*sum_d fp16(q)*fp16(summary)
+ * in binary64, softmax over the pages of score_mask, then the head
+ * aggregation.  out += mass / (active_layers * heads) when `accumulate`,
+ * so calling it once per active layer reproduces the multi-layer sum.
+ * Replaces page_softmax_scores (kvmem/src/host/graph_recall.cpp:322-394),
+ * PageSoftmaxCuda::score / score_current_layer (page_softmax.cu:202-396) and
+ * layerwise_mean_key_scores (kvmem/src/host/layerwise_scoring.cpp:10-63).
+ * summaries: dev fp16 [lanes][pages][Hkv*D]; scores: dev [lanes][pages]. */
+kvr_status kvr_score(kvr_context *ctx, const kvr_query *q, const uint16_t *summaries,
+                     uint32_t lanes, uint32_t pages, const uint8_t *score_mask,
+                     kvr_aggregation aggregation, uint32_t active_layers, int accumulate,
+                     double *scores, int force_mfma, void *stream);
+
+/* ---- selection ------------------------------------------------------------- */
+
+/* Per lane: mandatory pages first, then the top of (score desc, id by tie
+ * rule) up to k pages; ids ascending.  Rejects (device side, empty result,
+ * KVR_ERR_SCORES at kvr_check) a negative or non-finite score unless
+ * signed_scores.  Replaces KvMemStore::pick_scored_blocks
+ * (kvmem/src/host/kvmem_store.cpp:418-451) with every page a candidate.
+ * scores: dev [lanes][pages]; selected: dev [lanes][k]; count: dev [lanes]. */
+kvr_status kvr_select_topk(kvr_context *ctx, const double *scores, uint32_t lanes,
+                           uint32_t pages, uint32_t k, const uint32_t *mandatory,
+                           uint32_t n_mandatory, kvr_tie_rule tie_rule, int signed_scores,
+                           uint32_t *selected, uint32_t *count, void *stream);
+
+/* ---- stage-in ------------------------------------------------------------ */
+
+/* Gather each lane's selected pages of every plane from pinned history into
+ * its slot array.  Reads `selected`/`count` on the device (KERNEL engine) or
+ * after waiting for them (SDMA engine).  Replaces write_block_to_gpu
+ * (src/adapter/llama-memory-kvmem.cpp:4450-4526) with kvmem_stagein_enqueue_v /
+ * kvmem_stagein_flush (src/adapter/llama-kvmem-stagein.h:41-50,
+ * stagein.cu:673-794, 861-881) and the dequant/quant kernels
+ * (stagein.cu:133-199). */
+kvr_status kvr_stage_in(kvr_context *ctx, const kvr_plane *planes, uint32_t n_planes,
+                        uint32_t lanes, uint32_t page_tokens, const uint32_t *selected,
+                        const uint32_t *count, uint32_t k, kvr_copy_engine engine,
+                        void *stream);
+
+/* ---- one layer, end to end -------------------------------------------- */
+
+/* Summaries (or resident summaries) -> scores -> selection on select_stream,
+ * then the gather on copy_stream after an event; nothing waits on the host.
+ * Replaces score_retrieval + apply_native_selection's stage-in
+ * (src/adapter/llama-memory-kvmem.cpp:4604-4653, 5011-5126). */
+kvr_status kvr_recall_layer(kvr_context *ctx, const kvr_layer_recall *desc,
+                            void *select_stream, void *copy_stream);
+
+/* ---- device copies ------------------------------------------------------- */
+
+/* One launch of n byte copies (16-byte path when aligned).  Replaces
+ * kvmem_d2d_batched (llama-kvmem-stagein.h:56, stagein.cu:236-261, 1006-1039).
+ * src/dst/nbytes are host arrays of n entries. */
+kvr_status kvr_d2d_batched(kvr_context *ctx, const void *const *src, void *const *dst,
+                           const size_t *nbytes, uint32_t n, void *stream);
+
+/* ---- memory and measurement helpers ------------------------------------ */
+
+/* Page-locked, device-mapped host memory (hipHostMalloc).  Replaces the slab
+ * pins of kvmem_stagein_gpu_ready (stagein.cu:392-405). */
+kvr_status kvr_host_alloc(size_t bytes, void **out);
+kvr_status kvr_host_free(void *ptr);
+/* Best-of-`reps` hipMemcpyAsync bandwidth of one `bytes` pinned->device copy,
+ * GB/s (10^9 B/s).  Measurement helper with no reference counterpart. */
+kvr_status kvr_h2d_peak_gbps(kvr_context *ctx, size_t bytes, int reps, double *gbps);
+
+/* ---- seeded synthetic inputs (device fill) ----------------------------- */
+/* Bit-identical to the generator of the test oracle; no reference counterpart.
+ * normal: sum of 12 uniform 24-bit fractions minus 6, rounded once. */
+kvr_status kvr_synth_normal_f16(kvr_context *ctx, uint64_t seed, uint64_t stream_id,
+                                uint64_t count, uint16_t *out, void *stream);
+kvr_status kvr_synth_scaled_normal_f16(kvr_context *ctx, uint64_t seed, uint64_t stream_id,
+                                       uint64_t rows, uint32_t width, const float *scale,
+                                       uint16_t *out, void *stream);
+kvr_status kvr_synth_normal_f32(kvr_context *ctx, uint64_t seed, uint64_t stream_id,
+                                uint64_t count, float *out, void *stream);
+kvr_status kvr_synth_q8_0(kvr_context *ctx, uint64_t seed, uint64_t stream_id,
+                          uint64_t blocks, float d_lo, float d_hi, uint8_t *out, void *stream);
+kvr_status kvr_synth_q4_1(kvr_context *ctx, uint64_t seed, uint64_t stream_id,
+                          uint64_t blocks, float d_lo, float d_hi, float m_lo, float m_hi,
+                          uint8_t *out, void *stream);
+kvr_status kvr_synth_normal_q8_0(kvr_context *ctx, uint64_t seed, uint64_t stream_id,
+                                 uint64_t blocks, uint8_t *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

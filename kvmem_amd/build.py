@@ -1,0 +1,87 @@
+"""Build the in-tree native libraries.
+
+  kvmem_amd/libkvrecall.so   HIP kernels + the C ABI of include/kvrecall.h (gfx950)
+  oracle/liboracle.so        the CPU restatement used by tests (checker only)
+  oracle/_ref/*.so           the reference's own host sources, when present
+
+Every call recompiles (no stale-object reuse).  Objects are compiled in
+parallel and linked with hipcc.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CSRC = os.path.join(ROOT, "kvmem_amd", "csrc")
+LIB = os.path.join(ROOT, "kvmem_amd", "libkvrecall.so")
+ORACLE = os.path.join(ROOT, "oracle")
+ARCH = os.environ.get("KVR_OFFLOAD_ARCH", "gfx950")
+
+SOURCES = ["kvr_kernels.hip", "kvr_capi.cpp"]
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",
+    # Packed FP32 VALU ops stay disabled: the compiler's own v_pk_* forms are
+    # not used anywhere in this library.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-I", os.path.join(ROOT, "include"), "-I", CSRC,
+]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found")
+
+
+def _run(cmd, verbose: bool):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in r.stdout.splitlines() if "packed-fp32-ops" not in l
+                    and "not a recognized feature for this target" not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"command failed ({r.returncode}): {' '.join(cmd)}\n{out}")
+    if verbose and out.strip():
+        print(out, flush=True)
+
+
+def build_library(verbose: bool = False) -> str:
+    hipcc = _hipcc()
+    tmp = tempfile.mkdtemp(prefix="kvr_build_")
+    try:
+        objs = []
+        cmds = []
+        for src in SOURCES:
+            obj = os.path.join(tmp, os.path.splitext(src)[0] + ".o")
+            objs.append(obj)
+            cmds.append([hipcc, *HIPCC_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+        with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
+            for f in [ex.submit(_run, c, verbose) for c in cmds]:
+                f.result()
+        tmp_lib = LIB + ".tmp"
+        _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp_lib, *objs], verbose)
+        os.replace(tmp_lib, LIB)
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    return LIB
+
+
+def build_oracle(verbose: bool = False) -> None:
+    jobs = str(min(8, os.cpu_count() or 1))
+    _run(["make", "-C", ORACLE, "-B", f"-j{jobs}", "all"], verbose)
+
+
+def build_all(verbose: bool = False) -> None:
+    build_library(verbose)
+    build_oracle(verbose)
+
+
+if __name__ == "__main__":
+    build_all(verbose="-v" in sys.argv)
+    print(LIB)

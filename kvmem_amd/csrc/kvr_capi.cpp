@@ -1,0 +1,960 @@
+// kvr_capi.cpp -- the extern "C" boundary (include/kvrecall.h).
+//
+// Host side: argument validation (nothing launches on a rejected call),
+// context streams/events, workspace planning, and the composition of one
+// layer's launches.  All compute is in kvr_kernels.hip.
+#include "kvrecall.h"
+
+#include "kvr_device.hpp"
+#include "kvr_internal.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+struct kvr_context {
+    int device = 0;
+    hipStream_t sel = nullptr, copy = nullptr;
+    hipEvent_t ev_sel = nullptr;   // select work done -> copy stream may read the selection
+    uint32_t *status = nullptr;    // dev [kStatusWords]
+    uint32_t epoch = 0, checked = 0;
+    uint8_t *ws = nullptr;
+    size_t ws_bytes = 0;
+    bool ws_borrowed = false;
+    // batched device copies
+    kvr::CopyOp *ops_dev = nullptr, *ops_pin = nullptr;
+    uint32_t ops_cap = 0;
+    hipEvent_t ops_ev = nullptr;
+    // SDMA stage-in
+    uint32_t *sel_pin = nullptr;
+    size_t sel_pin_cap = 0;
+    uint8_t *staging = nullptr;
+    size_t staging_bytes = 0;
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+kvr_status fail(kvr_status s, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return s;
+}
+
+kvr_status hip_fail(hipError_t e, const char *what) {
+    return fail(KVR_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define KVR_HIP(expr)                                              \
+    do {                                                           \
+        const hipError_t e_ = (expr);                              \
+        if (e_ != hipSuccess) return hip_fail(e_, #expr);          \
+    } while (0)
+
+struct DeviceGuard {
+    int previous = -1;
+    explicit DeviceGuard(int device) {
+        if (hipGetDevice(&previous) != hipSuccess) previous = -1;
+        if (previous != device) (void)hipSetDevice(device);
+    }
+    ~DeviceGuard() {
+        int now = -1;
+        if (previous >= 0 && hipGetDevice(&now) == hipSuccess && now != previous) (void)hipSetDevice(previous);
+    }
+};
+
+size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
+bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+bool pow2(uint32_t v) { return v && !(v & (v - 1)); }
+
+size_t row_bytes(kvr_format f, uint32_t width) {
+    switch (f) {
+    case KVR_FMT_F16: return size_t(width) * 2;
+    case KVR_FMT_Q8_0: return width % 32 ? 0 : size_t(width) / 32 * 34;
+    case KVR_FMT_Q4_1: return width % 32 ? 0 : size_t(width) / 32 * 20;
+    default: return 0;
+    }
+}
+
+size_t scalar_bytes(kvr_format f) {
+    return f == KVR_FMT_F32 ? 4 : (f == KVR_FMT_F16 || f == KVR_FMT_BF16) ? 2 : 0;
+}
+
+hipStream_t stream_or(void *s, hipStream_t fallback) {
+    return s ? static_cast<hipStream_t>(s) : fallback;
+}
+
+double logit_scale(float attention_scale, uint32_t dim) {
+    return attention_scale > 0 ? double(attention_scale) : 1 / std::sqrt(double(dim));
+}
+
+uint32_t page_count(uint64_t tokens, uint32_t page_tokens) {
+    return uint32_t((tokens + page_tokens - 1) / page_tokens);
+}
+
+kvr_status check_ctx(kvr_context *ctx) {
+    if (!ctx) return fail(KVR_ERR_INVALID, "null context");
+    return KVR_OK;
+}
+
+// Query geometry.  Element strides must address disjoint elements of the
+// declared scalar (native_layer_query.hpp:36-57 qualifies the same layouts).
+kvr_status check_query(const kvr_query *q, uint32_t lanes) {
+    if (!q || !q->data) return fail(KVR_ERR_INVALID, "missing query");
+    const size_t el = scalar_bytes(q->scalar);
+    if (!el) return fail(KVR_ERR_INVALID, "query scalar must be f32, f16 or bf16");
+    if (!q->rows || !q->query_heads || !q->kv_heads || !q->head_dim || q->query_heads % q->kv_heads)
+        return fail(KVR_ERR_INVALID, "invalid query geometry (rows %u, heads %u/%u, dim %u)", q->rows,
+                    q->query_heads, q->kv_heads, q->head_dim);
+    if (!std::isfinite(q->attention_scale) || q->attention_scale < 0)
+        return fail(KVR_ERR_INVALID, "attention scale must be finite and nonnegative");
+    if (!aligned(q->data, el) || q->row_stride % el || q->head_stride % el || q->dim_stride % el ||
+        q->lane_stride % el || !q->dim_stride || (q->query_heads > 1 && !q->head_stride) ||
+        (q->rows > 1 && !q->row_stride) || (lanes > 1 && !q->lane_stride))
+        return fail(KVR_ERR_INVALID, "query strides must be nonzero multiples of the scalar size");
+    return KVR_OK;
+}
+
+kvr::QueryArgs query_args(const kvr_query *q) {
+    kvr::QueryArgs a{};
+    a.data = static_cast<const uint8_t *>(q->data);
+    a.scalar = uint32_t(q->scalar);
+    a.rows = q->rows;
+    a.qheads = q->query_heads;
+    a.kvheads = q->kv_heads;
+    a.dim = q->head_dim;
+    a.row_stride = q->row_stride;
+    a.head_stride = q->head_stride;
+    a.dim_stride = q->dim_stride;
+    a.lane_stride = q->lane_stride;
+    a.scale = logit_scale(q->attention_scale, q->head_dim);
+    return a;
+}
+
+bool valu_dim_ok(uint32_t dim) { return dim % 8 == 0 && pow2(dim / 8) && dim / 8 <= 64; }
+
+kvr_status ensure_workspace(kvr_context *ctx, size_t bytes) {
+    if (bytes <= ctx->ws_bytes) return KVR_OK;
+    if (ctx->ws_borrowed)
+        return fail(KVR_ERR_WORKSPACE, "call needs %zu workspace bytes, borrowed workspace has %zu", bytes,
+                    ctx->ws_bytes);
+    KVR_HIP(hipStreamSynchronize(ctx->sel));
+    KVR_HIP(hipStreamSynchronize(ctx->copy));
+    if (ctx->ws) KVR_HIP(hipFree(ctx->ws));
+    ctx->ws = nullptr;
+    ctx->ws_bytes = 0;
+    KVR_HIP(hipMalloc(&ctx->ws, bytes));
+    ctx->ws_bytes = bytes;
+    return KVR_OK;
+}
+
+size_t logits_bytes(uint32_t lanes, uint32_t pages, uint32_t rows, uint32_t qheads) {
+    return align256(size_t(lanes) * rows * qheads * pages * sizeof(double));
+}
+size_t qpack_bytes(uint32_t lanes, uint32_t rows, uint32_t qheads, uint32_t dim) {
+    return align256(size_t(lanes) * rows * qheads * dim * sizeof(uint16_t));
+}
+
+struct Mandatory {
+    uint32_t n = 0;
+    uint32_t ids[KVR_MAX_INLINE_MANDATORY];
+};
+
+kvr_status check_mandatory(const uint32_t *ids, uint32_t n, uint32_t pages, uint32_t k, Mandatory &m) {
+    if (n && !ids) return fail(KVR_ERR_INVALID, "missing mandatory list");
+    std::vector<uint32_t> v(ids, ids + n);
+    for (uint32_t id : v)
+        if (id >= pages) return fail(KVR_ERR_INVALID, "mandatory page %u is outside %u pages", id, pages);
+    std::sort(v.begin(), v.end());
+    v.erase(std::unique(v.begin(), v.end()), v.end());
+    if (v.size() > k)
+        return fail(KVR_ERR_BUDGET, "%zu mandatory pages exceed the selection budget %u", v.size(), k);
+    if (v.size() > KVR_MAX_INLINE_MANDATORY)
+        return fail(KVR_ERR_INVALID, "at most %d mandatory pages per call", KVR_MAX_INLINE_MANDATORY);
+    m.n = uint32_t(v.size());
+    std::copy(v.begin(), v.end(), m.ids);
+    return KVR_OK;
+}
+
+struct ScorePlan {
+    kvr::QueryArgs q;
+    uint32_t lanes, pages, rows, qheads, kvheads, dim;
+    bool mfma;
+    double *logits;
+    uint16_t *qpack;
+};
+
+kvr_status plan_score(kvr_context *ctx, const kvr_query *q, uint32_t lanes, uint32_t pages,
+                      int force_mfma, ScorePlan &p) {
+    if (kvr_status s = check_query(q, lanes)) return s;
+    if (!pages) return fail(KVR_ERR_INVALID, "no pages to score");
+    p.q = query_args(q);
+    p.lanes = lanes;
+    p.pages = pages;
+    p.rows = q->rows;
+    p.qheads = q->query_heads;
+    p.kvheads = q->kv_heads;
+    p.dim = q->head_dim;
+    const uint32_t group = q->query_heads / q->kv_heads;
+    p.mfma = force_mfma > 0 || (force_mfma == 0 && uint64_t(q->rows) * group >= 16);
+    if (p.mfma && q->head_dim % 4)
+        return fail(KVR_ERR_INVALID, "matrix-core scoring needs head_dim %% 4 == 0");
+    if (!p.mfma && !valu_dim_ok(q->head_dim))
+        return fail(KVR_ERR_INVALID, "head_dim %u: vector scoring needs 8*2^i <= 512", q->head_dim);
+    const size_t lb = logits_bytes(lanes, pages, q->rows, q->query_heads);
+    const size_t qb = p.mfma ? qpack_bytes(lanes, q->rows, q->query_heads, q->head_dim) : 0;
+    if (kvr_status s = ensure_workspace(ctx, lb + qb)) return s;
+    p.logits = reinterpret_cast<double *>(ctx->ws);
+    p.qpack = reinterpret_cast<uint16_t *>(ctx->ws + lb);
+    return KVR_OK;
+}
+
+// logits -> softmax -> aggregation (+ selection).
+kvr_status enqueue_probs_and_select(kvr_context *ctx, const ScorePlan &p, const uint8_t *mask,
+                                    kvr_aggregation agg, uint32_t active_layers, int accumulate,
+                                    double *scores, bool do_select, uint32_t k, kvr_tie_rule tie,
+                                    const Mandatory &mand, uint32_t *selected, uint32_t *count,
+                                    hipStream_t s) {
+    kvr::SoftmaxArgs sm{};
+    sm.logits = p.logits;
+    sm.mask = mask;
+    sm.lanes = p.lanes;
+    sm.rows = p.rows;
+    sm.qheads = p.qheads;
+    sm.kvheads = p.kvheads;
+    sm.pages = p.pages;
+    sm.aggregation = uint32_t(agg);
+    KVR_HIP(kvr::launch_softmax(sm, s));
+    kvr::SelectArgs sa{};
+    sa.probs = p.logits;
+    sa.rows = p.rows;
+    sa.qheads = p.qheads;
+    sa.kvheads = p.kvheads;
+    sa.aggregation = uint32_t(agg);
+    sa.weight = double(active_layers) * (agg == KVR_AGG_MEAN ? p.qheads : p.kvheads);
+    sa.accumulate = accumulate;
+    sa.do_aggregate = 1;
+    sa.scores = scores;
+    sa.lanes = p.lanes;
+    sa.pages = p.pages;
+    sa.k = k;
+    sa.tie_higher_first = tie == KVR_TIE_HIGHER_FIRST;
+    sa.signed_scores = 0;
+    sa.do_select = do_select;
+    sa.n_mandatory = mand.n;
+    std::copy(mand.ids, mand.ids + mand.n, sa.mandatory);
+    sa.selected = selected;
+    sa.count = count;
+    sa.status = ctx->status;
+    sa.epoch = ctx->epoch;
+    KVR_HIP(kvr::launch_select(sa, s));
+    return KVR_OK;
+}
+
+kvr_status enqueue_logits(kvr_context *ctx, const ScorePlan &p, const uint16_t *summaries,
+                          hipStream_t s) {
+    if (p.mfma) {
+        kvr::PackQueryArgs pq{};
+        pq.q = p.q;
+        pq.lanes = p.lanes;
+        pq.out = p.qpack;
+        pq.status = ctx->status;
+        pq.epoch = ctx->epoch;
+        KVR_HIP(kvr::launch_pack_query(pq, s));
+        kvr::MfmaLogitsArgs ma{};
+        ma.qpack = p.qpack;
+        ma.summaries = summaries;
+        ma.lanes = p.lanes;
+        ma.pages = p.pages;
+        ma.rows = p.rows;
+        ma.qheads = p.qheads;
+        ma.kvheads = p.kvheads;
+        ma.dim = p.dim;
+        ma.scale = p.q.scale;
+        ma.logits = p.logits;
+        KVR_HIP(kvr::launch_logits_mfma(ma, s));
+    } else {
+        kvr::SummaryArgs a{};
+        a.src = reinterpret_cast<const uint8_t *>(summaries);
+        a.src_lane_stride = uint64_t(p.pages) * p.kvheads * p.dim * 2;
+        a.pages = p.pages;
+        a.width = p.kvheads * p.dim;
+        a.lanes = p.lanes;
+        a.q = p.q;
+        a.logits = p.logits;
+        a.status = ctx->status;
+        a.epoch = ctx->epoch;
+        KVR_HIP(kvr::launch_summary(kvr::kSrcSummary, true, a, s));
+    }
+    return KVR_OK;
+}
+
+kvr_status check_keys(const kvr_key_history *k, uint32_t &pages, size_t &lane_stride) {
+    if (!k || !k->data) return fail(KVR_ERR_INVALID, "missing key history");
+    if (k->format != KVR_FMT_F16 && k->format != KVR_FMT_Q8_0)
+        return fail(KVR_ERR_UNSUPPORTED, "key history must be f16 or q8_0");
+    if (!k->tokens || !k->kv_heads || !k->head_dim || !k->page_tokens)
+        return fail(KVR_ERR_INVALID, "empty key history geometry");
+    const uint32_t width = k->kv_heads * k->head_dim;
+    if (width % 8) return fail(KVR_ERR_INVALID, "kv_heads*head_dim must be a multiple of 8");
+    if (k->format == KVR_FMT_Q8_0 && width % 64)
+        return fail(KVR_ERR_INVALID, "q8_0 keys need kv_heads*head_dim %% 64 == 0");
+    const uint64_t p = (k->tokens + k->page_tokens - 1) / k->page_tokens;
+    if (p > 0xffffffffull) return fail(KVR_ERR_INVALID, "too many pages");
+    pages = uint32_t(p);
+    const size_t rb = row_bytes(k->format, width);
+    const uint32_t lanes = k->lanes ? k->lanes : 1;
+    lane_stride = k->lane_stride ? k->lane_stride : size_t(k->tokens) * rb;
+    if (lanes > 1 && lane_stride < size_t(k->tokens) * rb)
+        return fail(KVR_ERR_INVALID, "key lane stride overlaps");
+    const size_t need = k->format == KVR_FMT_F16 ? 16 : 4;
+    if (!aligned(k->data, need) || lane_stride % need)
+        return fail(KVR_ERR_INVALID, "key history must be %zu-byte aligned", need);
+    return KVR_OK;
+}
+
+kvr_status check_summary_out(const float *means, const uint16_t *summaries) {
+    if ((means && !aligned(means, 16)) || (summaries && !aligned(summaries, 16)))
+        return fail(KVR_ERR_INVALID, "summary outputs must be 16-byte aligned");
+    return KVR_OK;
+}
+
+kvr::SummaryArgs summary_args(kvr_context *ctx, const kvr_key_history *k, uint32_t pages,
+                              size_t lane_stride, float *means, uint16_t *summaries) {
+    kvr::SummaryArgs a{};
+    a.src = static_cast<const uint8_t *>(k->data);
+    a.src_lane_stride = lane_stride;
+    a.tokens = k->tokens;
+    a.page_tokens = k->page_tokens;
+    a.pages = pages;
+    a.width = k->kv_heads * k->head_dim;
+    a.lanes = k->lanes ? k->lanes : 1;
+    a.means = means;
+    a.summaries = summaries;
+    a.status = ctx->status;
+    a.epoch = ctx->epoch;
+    return a;
+}
+
+// ---- stage-in -------------------------------------------------------------
+
+struct PlanePlan {
+    kvr::GatherPlane g;
+    const uint8_t *host;   // pinned host pointer (SDMA engine)
+    size_t host_row;
+};
+
+kvr_status check_planes(const kvr_plane *planes, uint32_t n, uint32_t lanes, uint32_t page_tokens,
+                        uint32_t k, PlanePlan *out) {
+    if (n > KVR_MAX_PLANES) return fail(KVR_ERR_INVALID, "at most %d planes", KVR_MAX_PLANES);
+    if (n && !planes) return fail(KVR_ERR_INVALID, "missing planes");
+    for (uint32_t i = 0; i < n; ++i) {
+        const kvr_plane &p = planes[i];
+        if (!p.history || !p.slots || !p.width || !p.tokens)
+            return fail(KVR_ERR_INVALID, "plane %u: missing history, slots or geometry", i);
+        const size_t srow = row_bytes(p.format, p.width);
+        if (!srow) return fail(KVR_ERR_UNSUPPORTED, "plane %u: history format must be f16, q8_0 or q4_1 "
+                                                    "(width %% 32 == 0 for blocks)", i);
+        size_t drow = 0;
+        if (p.mode == KVR_GATHER_COPY) drow = srow;
+        else if (p.mode == KVR_GATHER_DEQUANT_F16) drow = size_t(p.width) * 2;
+        else if (p.mode == KVR_GATHER_REQUANT_Q8_0 && p.format == KVR_FMT_Q8_0) drow = srow;
+        if (!drow) return fail(KVR_ERR_UNSUPPORTED, "plane %u: gather mode not provided for this format", i);
+        if (p.mode == KVR_GATHER_DEQUANT_F16 && p.format != KVR_FMT_F16 && (p.width % 32 || !aligned(p.slots, 16)))
+            return fail(KVR_ERR_INVALID, "plane %u: dequantized slots must be 16-byte aligned", i);
+        if (p.format != KVR_FMT_F16 && p.mode != KVR_GATHER_COPY && srow * 8 > 32768)
+            return fail(KVR_ERR_INVALID, "plane %u: rows too wide for the staged decoder", i);
+        hipPointerAttribute_t attr{};
+        if (hipPointerGetAttributes(&attr, p.history) != hipSuccess || attr.type != hipMemoryTypeHost ||
+            !attr.devicePointer) {
+            (void)hipGetLastError();
+            return fail(KVR_ERR_INVALID, "plane %u: history is not pinned, device-mapped host memory", i);
+        }
+        const size_t hls = p.host_lane_stride ? p.host_lane_stride : size_t(p.tokens) * srow;
+        const size_t sls = p.slot_lane_stride ? p.slot_lane_stride : size_t(k) * page_tokens * drow;
+        if (lanes > 1 && (hls < size_t(p.tokens) * srow || sls < size_t(k) * page_tokens * drow))
+            return fail(KVR_ERR_INVALID, "plane %u: lane strides overlap", i);
+        PlanePlan &pp = out[i];
+        pp.g = kvr::GatherPlane{};
+        pp.g.src = static_cast<const uint8_t *>(attr.devicePointer);
+        pp.g.dst = static_cast<uint8_t *>(p.slots);
+        pp.g.src_lane_stride = hls;
+        pp.g.dst_lane_stride = sls;
+        pp.g.tokens = p.tokens;
+        pp.g.src_row = uint32_t(srow);
+        pp.g.dst_row = uint32_t(drow);
+        pp.g.width = p.width;
+        pp.g.format = uint32_t(p.format);
+        pp.g.mode = uint32_t(p.mode);
+        pp.host = static_cast<const uint8_t *>(p.history);
+        pp.host_row = srow;
+    }
+    return KVR_OK;
+}
+
+uint32_t chunk_rows_for(uint32_t page_tokens) { return std::min<uint32_t>(8, page_tokens); }
+
+kvr_status enqueue_gather_kernel(const PlanePlan *pp, uint32_t n, uint32_t lanes, uint32_t page_tokens,
+                                 const uint32_t *selected, const uint32_t *count, uint32_t k,
+                                 hipStream_t s) {
+    if (!n) return KVR_OK;
+    kvr::GatherArgs ga{};
+    for (uint32_t i = 0; i < n; ++i) ga.plane[i] = pp[i].g;
+    ga.n_planes = n;
+    ga.lanes = lanes;
+    ga.k = k;
+    ga.page_tokens = page_tokens;
+    ga.chunk_rows = chunk_rows_for(page_tokens);
+    ga.chunks = (page_tokens + ga.chunk_rows - 1) / ga.chunk_rows;
+    ga.selected = selected;
+    ga.count = count;
+    KVR_HIP(kvr::launch_gather(ga, s));
+    return KVR_OK;
+}
+
+// DMA engine: wait for the selection, then one hipMemcpyAsync per selected
+// page span (contiguous token rows) straight into the slots (copy modes) or
+// into a device staging area decoded by the gather kernel.
+kvr_status enqueue_gather_sdma(kvr_context *ctx, PlanePlan *pp, uint32_t n, uint32_t lanes,
+                               uint32_t page_tokens, const uint32_t *selected, const uint32_t *count,
+                               uint32_t k, hipStream_t s) {
+    if (!n) return KVR_OK;
+    const size_t words = size_t(lanes) * (k + 1);
+    if (ctx->sel_pin_cap < words) {
+        if (ctx->sel_pin) KVR_HIP(hipHostFree(ctx->sel_pin));
+        ctx->sel_pin = nullptr;
+        ctx->sel_pin_cap = 0;
+        KVR_HIP(hipHostMalloc(reinterpret_cast<void **>(&ctx->sel_pin), words * 4, hipHostMallocDefault));
+        ctx->sel_pin_cap = words;
+    }
+    KVR_HIP(hipMemcpyAsync(ctx->sel_pin, selected, size_t(lanes) * k * 4, hipMemcpyDeviceToHost, s));
+    KVR_HIP(hipMemcpyAsync(ctx->sel_pin + size_t(lanes) * k, count, size_t(lanes) * 4, hipMemcpyDeviceToHost, s));
+    KVR_HIP(hipStreamSynchronize(s));
+    size_t staged = 0;
+    for (uint32_t i = 0; i < n; ++i)
+        if (pp[i].g.mode != KVR_GATHER_COPY && pp[i].g.format != KVR_FMT_F16)
+            staged += size_t(lanes) * k * page_tokens * pp[i].host_row;
+    if (staged > ctx->staging_bytes) {
+        if (ctx->ws_borrowed) return fail(KVR_ERR_WORKSPACE, "DMA staging needs %zu bytes", staged);
+        if (ctx->staging) KVR_HIP(hipFree(ctx->staging));
+        ctx->staging = nullptr;
+        ctx->staging_bytes = 0;
+        KVR_HIP(hipMalloc(&ctx->staging, staged));
+        ctx->staging_bytes = staged;
+    }
+    size_t at = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        PlanePlan &p = pp[i];
+        const bool decode = p.g.mode != KVR_GATHER_COPY && p.g.format != KVR_FMT_F16;
+        const size_t span = size_t(page_tokens) * p.host_row;
+        for (uint32_t lane = 0; lane < lanes; ++lane) {
+            const uint32_t cnt = std::min(ctx->sel_pin[size_t(lanes) * k + lane], k);
+            for (uint32_t slot = 0; slot < cnt; ++slot) {
+                const uint32_t page = ctx->sel_pin[size_t(lane) * k + slot];
+                const uint64_t first = uint64_t(page) * page_tokens;
+                if (first >= p.g.tokens) continue;
+                const uint64_t rows = std::min<uint64_t>(page_tokens, p.g.tokens - first);
+                const uint8_t *src = p.host + lane * p.g.src_lane_stride + first * p.host_row;
+                uint8_t *dst = decode ? ctx->staging + at + (size_t(lane) * k + slot) * span
+                                      : p.g.dst + lane * p.g.dst_lane_stride + size_t(slot) * page_tokens * p.g.dst_row;
+                KVR_HIP(hipMemcpyAsync(dst, src, rows * p.host_row, hipMemcpyHostToDevice, s));
+            }
+        }
+        if (decode) {
+            kvr::GatherArgs ga{};
+            ga.plane[0] = p.g;
+            ga.plane[0].src = ctx->staging + at;
+            ga.plane[0].src_lane_stride = size_t(k) * span;
+            ga.n_planes = 1;
+            ga.lanes = lanes;
+            ga.k = k;
+            ga.page_tokens = page_tokens;
+            ga.chunk_rows = chunk_rows_for(page_tokens);
+            ga.chunks = (page_tokens + ga.chunk_rows - 1) / ga.chunk_rows;
+            ga.selected = selected;  // page ids bound each slot's valid rows
+            ga.count = count;
+            ga.src_page_stride = span;
+            KVR_HIP(kvr::launch_gather(ga, s));
+            at += size_t(lanes) * k * span;
+        }
+    }
+    return KVR_OK;
+}
+
+}  // namespace
+
+// ===========================================================================
+extern "C" {
+
+const char *kvr_last_error(void) { return g_error.c_str(); }
+
+const char *kvr_status_string(kvr_status s) {
+    switch (s) {
+    case KVR_OK: return "ok";
+    case KVR_ERR_INVALID: return "invalid argument";
+    case KVR_ERR_NONFINITE: return "nonfinite recall operand";
+    case KVR_ERR_RANGE: return "recall operand exceeds fp16 range";
+    case KVR_ERR_BUDGET: return "mandatory pages exceed the budget";
+    case KVR_ERR_WORKSPACE: return "workspace too small";
+    case KVR_ERR_HIP: return "HIP runtime error";
+    case KVR_ERR_SCORES: return "invalid score";
+    case KVR_ERR_UNSUPPORTED: return "unsupported format or mode";
+    }
+    return "unknown status";
+}
+
+kvr_status kvr_create(int device, kvr_context **out) {
+    if (!out) return fail(KVR_ERR_INVALID, "null output");
+    *out = nullptr;
+    int n = 0;
+    KVR_HIP(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n) return fail(KVR_ERR_INVALID, "device %d of %d", device, n);
+    DeviceGuard guard(device);
+    auto *ctx = new kvr_context;
+    ctx->device = device;
+    hipError_t e = hipStreamCreateWithFlags(&ctx->sel, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->copy, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->ev_sel, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->ops_ev, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipMalloc(&ctx->status, kvr::kStatusWords * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(ctx->status, 0, kvr::kStatusWords * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        kvr_destroy(ctx);
+        return hip_fail(e, "context creation");
+    }
+    *out = ctx;
+    return KVR_OK;
+}
+
+kvr_status kvr_destroy(kvr_context *ctx) {
+    if (!ctx) return KVR_OK;
+    DeviceGuard guard(ctx->device);
+    if (ctx->sel) (void)hipStreamSynchronize(ctx->sel);
+    if (ctx->copy) (void)hipStreamSynchronize(ctx->copy);
+    if (ctx->ws && !ctx->ws_borrowed) (void)hipFree(ctx->ws);
+    if (ctx->staging) (void)hipFree(ctx->staging);
+    if (ctx->status) (void)hipFree(ctx->status);
+    if (ctx->ops_dev) (void)hipFree(ctx->ops_dev);
+    if (ctx->ops_pin) (void)hipHostFree(ctx->ops_pin);
+    if (ctx->sel_pin) (void)hipHostFree(ctx->sel_pin);
+    if (ctx->ev_sel) (void)hipEventDestroy(ctx->ev_sel);
+    if (ctx->ops_ev) (void)hipEventDestroy(ctx->ops_ev);
+    if (ctx->sel) (void)hipStreamDestroy(ctx->sel);
+    if (ctx->copy) (void)hipStreamDestroy(ctx->copy);
+    delete ctx;
+    return KVR_OK;
+}
+
+void *kvr_select_stream(kvr_context *ctx) { return ctx ? ctx->sel : nullptr; }
+void *kvr_copy_stream(kvr_context *ctx) { return ctx ? ctx->copy : nullptr; }
+
+kvr_status kvr_check(kvr_context *ctx, void *stream) {
+    if (kvr_status s = check_ctx(ctx)) return s;
+    DeviceGuard guard(ctx->device);
+    if (stream) {
+        KVR_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+    } else {
+        KVR_HIP(hipStreamSynchronize(ctx->sel));
+        KVR_HIP(hipStreamSynchronize(ctx->copy));
+    }
+    uint32_t st[kvr::kStatusWords] = {};
+    KVR_HIP(hipMemcpy(st, ctx->status, sizeof st, hipMemcpyDeviceToHost));
+    const uint32_t since = ctx->checked;
+    ctx->checked = ctx->epoch;
+    if (st[kvr::kStatusNonfinite] > since)
+        return fail(KVR_ERR_NONFINITE, "nonfinite recall operand (call %u)", st[kvr::kStatusNonfinite]);
+    if (st[kvr::kStatusRange] > since)
+        return fail(KVR_ERR_RANGE, "recall operand rounds to fp16 infinity (call %u)", st[kvr::kStatusRange]);
+    if (st[kvr::kStatusScores] > since)
+        return fail(KVR_ERR_SCORES, "negative or nonfinite score (call %u)", st[kvr::kStatusScores]);
+    return KVR_OK;
+}
+
+size_t kvr_workspace_bytes(uint32_t lanes, uint32_t max_pages, uint32_t max_rows, uint32_t query_heads,
+                           uint32_t kv_heads, uint32_t head_dim) {
+    (void)kv_heads;
+    lanes = lanes ? lanes : 1;
+    return logits_bytes(lanes, max_pages, max_rows, query_heads) +
+           qpack_bytes(lanes, max_rows, query_heads, head_dim);
+}
+
+kvr_status kvr_bind_workspace(kvr_context *ctx, void *workspace, size_t bytes) {
+    if (kvr_status s = check_ctx(ctx)) return s;
+    if (!workspace || !aligned(workspace, 256) || !bytes)
+        return fail(KVR_ERR_INVALID, "borrowed workspace is missing or not 256-byte aligned");
+    DeviceGuard guard(ctx->device);
+    KVR_HIP(hipStreamSynchronize(ctx->sel));
+    KVR_HIP(hipStreamSynchronize(ctx->copy));
+    if (ctx->ws && !ctx->ws_borrowed) KVR_HIP(hipFree(ctx->ws));
+    ctx->ws = static_cast<uint8_t *>(workspace);
+    ctx->ws_bytes = bytes;
+    ctx->ws_borrowed = true;
+    return KVR_OK;
+}
+
+size_t kvr_device_bytes(kvr_context *ctx) {
+    return ctx ? ctx->ws_bytes + ctx->staging_bytes + kvr::kStatusWords * 4 + ctx->ops_cap * sizeof(kvr::CopyOp)
+               : 0;
+}
+
+kvr_status kvr_summary_build(kvr_context *ctx, const kvr_key_history *keys, float *means,
+                             uint16_t *summaries, void *stream) {
+    if (kvr_status s = check_ctx(ctx)) return s;
+    uint32_t pages;
+    size_t ls;
+    if (kvr_status s = check_keys(keys, pages, ls)) return s;
+    if (kvr_status s = check_summary_out(means, summaries)) return s;
+    if (!means && !summaries) return fail(KVR_ERR_INVALID, "no summary output");
+    DeviceGuard guard(ctx->device);
+    ++ctx->epoch;
+    const auto a = summary_args(ctx, keys, pages, ls, means, summaries);
+    KVR_HIP(kvr::launch_summary(keys->format == KVR_FMT_F16 ? kvr::kSrcKeysF16 : kvr::kSrcKeysQ8, false, a,
+                                stream_or(stream, ctx->sel)));
+    return KVR_OK;
+}
+
+
+kvr_status kvr_summary_accumulate(kvr_context *ctx, float *sums, uint32_t *counts, uint32_t page_tokens,
+                                  const void *k, kvr_format scalar, uint64_t pos0, uint32_t n,
+                                  uint32_t kv_heads, uint32_t head_dim, size_t token_stride,
+                                  size_t head_stride, size_t dim_stride, void *stream) {
+    if (kvr_status s = check_ctx(ctx)) return s;
+    const size_t el = scalar_bytes(scalar);
+    if (!sums || !counts || !k || !page_tokens || !kv_heads || !head_dim || !el)
+        return fail(KVR_ERR_INVALID, "invalid capture geometry or scalar");
+    if (!n) return KVR_OK;
+    if (!aligned(k, el) || token_stride % el || head_stride % el || dim_stride % el || !dim_stride ||
+        (n > 1 && !token_stride) || (kv_heads > 1 && !head_stride))
+        return fail(KVR_ERR_INVALID, "capture strides must be nonzero multiples of the scalar size");
+    DeviceGuard guard(ctx->device);
+    kvr::AccumulateArgs a{};
+    a.sums = sums;
+    a.counts = counts;
+    a.page_tokens = page_tokens;
+    a.width = kv_heads * head_dim;
+    a.dim = head_dim;
+    a.k = static_cast<const uint8_t *>(k);
+    a.scalar = uint32_t(scalar);
+    a.pos0 = pos0;
+    a.n = n;
+    a.token_stride = token_stride;
+    a.head_stride = head_stride;
+    a.dim_stride = dim_stride;
+    a.first_page = uint32_t(pos0 / page_tokens);
+    a.segments = uint32_t((pos0 + n - 1) / page_tokens) - a.first_page + 1;
+    KVR_HIP(kvr::launch_accumulate(a, stream_or(stream, ctx->sel)));
+    return KVR_OK;
+}
+
+kvr_status kvr_summary_finalize(kvr_context *ctx, const float *sums, const uint32_t *counts, uint32_t pages,
+                                uint32_t width, float *means, uint16_t *summaries, void *stream) {
+    if (kvr_status s = check_ctx(ctx)) return s;
+    if (!sums || !counts || !pages || !width || (!means && !summaries))
+        return fail(KVR_ERR_INVALID, "invalid summary finalize arguments");
+    DeviceGuard guard(ctx->device);
+    ++ctx->epoch;
+    kvr::FinalizeArgs a{};
+    a.sums = sums;
+    a.counts = counts;
+    a.pages = pages;
+    a.width = width;
+    a.means = means;
+    a.summaries = summaries;
+    a.status = ctx->status;
+    a.epoch = ctx->epoch;
+    KVR_HIP(kvr::launch_finalize(a, stream_or(stream, ctx->sel)));
+    return KVR_OK;
+}
+
+kvr_status kvr_score(kvr_context *ctx, const kvr_query *q, const uint16_t *summaries, uint32_t lanes,
+                     uint32_t pages, const uint8_t *score_mask, kvr_aggregation aggregation,
+                     uint32_t active_layers, int accumulate, double *scores, int force_mfma, void *stream) {
+    if (kvr_status s = check_ctx(ctx)) return s;
+    lanes = lanes ? lanes : 1;
+    if (!summaries || !scores || !aligned(summaries, 16))
+        return fail(KVR_ERR_INVALID, "summaries (16-byte aligned) and scores are required");
+    if (aggregation > KVR_AGG_MAX_LOGIT) return fail(KVR_ERR_INVALID, "unknown aggregation");
+    if (!active_layers) return fail(KVR_ERR_INVALID, "active_layers must be >= 1");
+    DeviceGuard guard(ctx->device);
+    ScorePlan p;
+    if (kvr_status s = plan_score(ctx, q, lanes, pages, force_mfma, p)) return s;
+    const hipStream_t s = stream_or(stream, ctx->sel);
+    ++ctx->epoch;
+    if (kvr_status st = enqueue_logits(ctx, p, summaries, s)) return st;
+    Mandatory none;
+    return enqueue_probs_and_select(ctx, p, score_mask, aggregation, active_layers, accumulate, scores, false, 1,
+                                    KVR_TIE_LOWER_FIRST, none, nullptr, nullptr, s);
+}
+
+kvr_status kvr_select_topk(kvr_context *ctx, const double *scores, uint32_t lanes, uint32_t pages, uint32_t k,
+                           const uint32_t *mandatory, uint32_t n_mandatory, kvr_tie_rule tie_rule,
+                           int signed_scores, uint32_t *selected, uint32_t *count, void *stream) {
+    if (kvr_status s = check_ctx(ctx)) return s;
+    lanes = lanes ? lanes : 1;
+    if (!scores || !selected || !count || !pages)
+        return fail(KVR_ERR_INVALID, "scores, selected, count and pages are required");
+    if (!k) return fail(KVR_ERR_INVALID, "invalid scored selection frame (budget 0)");
+    if (tie_rule > KVR_TIE_HIGHER_FIRST) return fail(KVR_ERR_INVALID, "unknown tie rule");
+    Mandatory m;
+    if (kvr_status s = check_mandatory(mandatory, n_mandatory, pages, k, m)) return s;
+    DeviceGuard guard(ctx->device);
+    ++ctx->epoch;
+    kvr::SelectArgs sa{};
+    sa.scores = const_cast<double *>(scores);
+    sa.lanes = lanes;
+    sa.pages = pages;
+    sa.k = k;
+    sa.tie_higher_first = tie_rule == KVR_TIE_HIGHER_FIRST;
+    sa.signed_scores = signed_scores != 0;
+    sa.do_select = 1;
+    sa.n_mandatory = m.n;
+    std::copy(m.ids, m.ids + m.n, sa.mandatory);
+    sa.selected = selected;
+    sa.count = count;
+    sa.status = ctx->status;
+    sa.epoch = ctx->epoch;
+    KVR_HIP(kvr::launch_select(sa, stream_or(stream, ctx->sel)));
+    return KVR_OK;
+}
+
+kvr_status kvr_stage_in(kvr_context *ctx, const kvr_plane *planes, uint32_t n_planes, uint32_t lanes,
+                        uint32_t page_tokens, const uint32_t *selected, const uint32_t *count, uint32_t k,
+                        kvr_copy_engine engine, void *stream) {
+    if (kvr_status s = check_ctx(ctx)) return s;
+    lanes = lanes ? lanes : 1;
+    if (!selected || !count || !k || !page_tokens)
+        return fail(KVR_ERR_INVALID, "selection, count, k and page_tokens are required");
+    if (engine > KVR_ENGINE_SDMA) return fail(KVR_ERR_INVALID, "unknown copy engine");
+    DeviceGuard guard(ctx->device);
+    PlanePlan pp[KVR_MAX_PLANES];
+    if (kvr_status s = check_planes(planes, n_planes, lanes, page_tokens, k, pp)) return s;
+    const hipStream_t s = stream_or(stream, ctx->copy);
+    if (engine == KVR_ENGINE_SDMA) return enqueue_gather_sdma(ctx, pp, n_planes, lanes, page_tokens, selected, count, k, s);
+    return enqueue_gather_kernel(pp, n_planes, lanes, page_tokens, selected, count, k, s);
+}
+
+kvr_status kvr_recall_layer(kvr_context *ctx, const kvr_layer_recall *d, void *select_stream, void *copy_stream) {
+    if (kvr_status s = check_ctx(ctx)) return s;
+    if (!d || !d->query || !d->summaries || !d->scores || !d->selected || !d->count)
+        return fail(KVR_ERR_INVALID, "recall descriptor lacks query, summaries, scores or selection outputs");
+    if (d->aggregation > KVR_AGG_MAX_LOGIT) return fail(KVR_ERR_INVALID, "unknown aggregation");
+    if (d->tie_rule > KVR_TIE_HIGHER_FIRST) return fail(KVR_ERR_INVALID, "unknown tie rule");
+    if (d->engine > KVR_ENGINE_SDMA) return fail(KVR_ERR_INVALID, "unknown copy engine");
+    if (!d->k) return fail(KVR_ERR_INVALID, "invalid scored selection frame (budget 0)");
+    uint32_t pages = d->pages, page_tokens = d->page_tokens, lanes = 1;
+    size_t key_ls = 0;
+    if (d->keys) {
+        if (kvr_status s = check_keys(d->keys, pages, key_ls)) return s;
+        page_tokens = d->keys->page_tokens;
+        lanes = d->keys->lanes ? d->keys->lanes : 1;
+        if (d->keys->kv_heads != d->query->kv_heads || d->keys->head_dim != d->query->head_dim)
+            return fail(KVR_ERR_INVALID, "key history and query disagree on kv heads or head_dim");
+    } else {
+        if (!pages || !page_tokens) return fail(KVR_ERR_INVALID, "resident summaries need pages and page_tokens");
+        lanes = d->lanes ? d->lanes : 1;
+    }
+    if (kvr_status s = check_summary_out(d->means, d->summaries)) return s;
+    Mandatory m;
+    if (kvr_status s = check_mandatory(d->mandatory, d->n_mandatory, pages, d->k, m)) return s;
+    DeviceGuard guard(ctx->device);
+    PlanePlan pp[KVR_MAX_PLANES];
+    if (kvr_status s = check_planes(d->planes, d->n_planes, lanes, page_tokens, d->k, pp)) return s;
+    ScorePlan p;
+    if (kvr_status s = plan_score(ctx, d->query, lanes, pages, d->force_mfma, p)) return s;
+    if (d->keys && !p.mfma && !valu_dim_ok(d->keys->head_dim))
+        return fail(KVR_ERR_INVALID, "head_dim %u unsupported by fused scoring", d->keys->head_dim);
+
+    const hipStream_t ss = stream_or(select_stream, ctx->sel);
+    const hipStream_t cs = stream_or(copy_stream, ctx->copy);
+    ++ctx->epoch;
+    if (d->keys) {
+        auto a = summary_args(ctx, d->keys, pages, key_ls, d->means, d->summaries);
+        const int src = d->keys->format == KVR_FMT_F16 ? kvr::kSrcKeysF16 : kvr::kSrcKeysQ8;
+        if (d->summary_begin) KVR_HIP(hipEventRecord(static_cast<hipEvent_t>(d->summary_begin), ss));
+        if (p.mfma) {
+            KVR_HIP(kvr::launch_summary(src, false, a, ss));
+        } else {
+            a.q = p.q;
+            a.logits = p.logits;
+            KVR_HIP(kvr::launch_summary(src, true, a, ss));
+        }
+        if (d->summary_end) KVR_HIP(hipEventRecord(static_cast<hipEvent_t>(d->summary_end), ss));
+        if (p.mfma)
+            if (kvr_status st = enqueue_logits(ctx, p, d->summaries, ss)) return st;
+    } else {
+        if (kvr_status st = enqueue_logits(ctx, p, d->summaries, ss)) return st;
+    }
+    if (kvr_status st = enqueue_probs_and_select(ctx, p, d->score_mask, d->aggregation, 1, 0, d->scores, true, d->k,
+                                                 d->tie_rule, m, d->selected, d->count, ss))
+        return st;
+    if (!d->n_planes) return KVR_OK;
+    if (cs != ss) {
+        KVR_HIP(hipEventRecord(ctx->ev_sel, ss));
+        KVR_HIP(hipStreamWaitEvent(cs, ctx->ev_sel, 0));
+    }
+    if (d->engine == KVR_ENGINE_SDMA)
+        return enqueue_gather_sdma(ctx, pp, d->n_planes, lanes, page_tokens, d->selected, d->count, d->k, cs);
+    return enqueue_gather_kernel(pp, d->n_planes, lanes, page_tokens, d->selected, d->count, d->k, cs);
+}
+
+kvr_status kvr_d2d_batched(kvr_context *ctx, const void *const *src, void *const *dst, const size_t *nbytes,
+                           uint32_t n, void *stream) {
+    if (kvr_status s = check_ctx(ctx)) return s;
+    if (!n) return KVR_OK;
+    if (!src || !dst || !nbytes) return fail(KVR_ERR_INVALID, "missing copy tables");
+    DeviceGuard guard(ctx->device);
+    if (ctx->ops_cap < n) {
+        KVR_HIP(hipEventSynchronize(ctx->ops_ev));
+        if (ctx->ops_dev) KVR_HIP(hipFree(ctx->ops_dev));
+        if (ctx->ops_pin) KVR_HIP(hipHostFree(ctx->ops_pin));
+        ctx->ops_dev = ctx->ops_pin = nullptr;
+        ctx->ops_cap = 0;
+        KVR_HIP(hipMalloc(&ctx->ops_dev, sizeof(kvr::CopyOp) * n));
+        KVR_HIP(hipHostMalloc(reinterpret_cast<void **>(&ctx->ops_pin), sizeof(kvr::CopyOp) * n, hipHostMallocDefault));
+        ctx->ops_cap = n;
+    } else {
+        // the previous batch's table upload must finish before the pinned table is rewritten
+        KVR_HIP(hipEventSynchronize(ctx->ops_ev));
+    }
+    for (uint32_t i = 0; i < n; ++i)
+        ctx->ops_pin[i] = kvr::CopyOp{static_cast<const uint8_t *>(src[i]), static_cast<uint8_t *>(dst[i]), nbytes[i]};
+    const hipStream_t s = stream_or(stream, ctx->sel);
+    KVR_HIP(hipMemcpyAsync(ctx->ops_dev, ctx->ops_pin, sizeof(kvr::CopyOp) * n, hipMemcpyHostToDevice, s));
+    KVR_HIP(hipEventRecord(ctx->ops_ev, s));
+    KVR_HIP(kvr::launch_copy_ops(ctx->ops_dev, n, s));
+    return KVR_OK;
+}
+
+kvr_status kvr_host_alloc(size_t bytes, void **out) {
+    if (!out || !bytes) return fail(KVR_ERR_INVALID, "invalid pinned allocation");
+    *out = nullptr;
+    KVR_HIP(hipHostMalloc(out, bytes, hipHostMallocDefault));
+    return KVR_OK;
+}
+
+kvr_status kvr_host_free(void *ptr) {
+    if (ptr) KVR_HIP(hipHostFree(ptr));
+    return KVR_OK;
+}
+
+kvr_status kvr_h2d_peak_gbps(kvr_context *ctx, size_t bytes, int reps, double *gbps) {
+    if (kvr_status s = check_ctx(ctx)) return s;
+    if (!bytes || reps < 1 || !gbps) return fail(KVR_ERR_INVALID, "invalid bandwidth probe");
+    DeviceGuard guard(ctx->device);
+    void *host = nullptr, *dev = nullptr;
+    hipEvent_t a = nullptr, b = nullptr;
+    kvr_status st = KVR_OK;
+    hipError_t e = hipHostMalloc(&host, bytes, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipMalloc(&dev, bytes);
+    if (e == hipSuccess) e = hipEventCreate(&a);
+    if (e == hipSuccess) e = hipEventCreate(&b);
+    if (e == hipSuccess) e = hipMemset(dev, 0, bytes);
+    if (e == hipSuccess) std::memset(host, 1, bytes);
+    float best = 0;
+    for (int i = 0; e == hipSuccess && i <= reps; ++i) {
+        e = hipEventRecord(a, ctx->copy);
+        if (e == hipSuccess) e = hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, ctx->copy);
+        if (e == hipSuccess) e = hipEventRecord(b, ctx->copy);
+        if (e == hipSuccess) e = hipEventSynchronize(b);
+        float ms = 0;
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+        if (e == hipSuccess && i > 0 && (best == 0 || ms < best)) best = ms;  // first copy warms up
+    }
+    if (e != hipSuccess) st = hip_fail(e, "H2D bandwidth probe");
+    else *gbps = double(bytes) / (double(best) * 1e-3) / 1e9;
+    if (a) (void)hipEventDestroy(a);
+    if (b) (void)hipEventDestroy(b);
+    if (dev) (void)hipFree(dev);
+    if (host) (void)hipHostFree(host);
+    return st;
+}
+
+// ---- synthetic inputs -----------------------------------------------------
+namespace {
+kvr_status synth(kvr_context *ctx, kvr::SynthArgs a, uint64_t seed, uint64_t sid, void *stream) {
+    if (kvr_status s = check_ctx(ctx)) return s;
+    if (!a.out) return fail(KVR_ERR_INVALID, "null synthetic output");
+    if (!a.count) return KVR_OK;
+    DeviceGuard guard(ctx->device);
+    a.base = kvr::synth_base(seed, sid);
+    KVR_HIP(kvr::launch_synth(a, stream_or(stream, ctx->sel)));
+    return KVR_OK;
+}
+}  // namespace
+
+kvr_status kvr_synth_normal_f16(kvr_context *ctx, uint64_t seed, uint64_t sid, uint64_t count, uint16_t *out,
+                                void *stream) {
+    kvr::SynthArgs a{};
+    a.kind = kvr::kSynthNormalF16;
+    a.count = count;
+    a.out = out;
+    return synth(ctx, a, seed, sid, stream);
+}
+
+kvr_status kvr_synth_scaled_normal_f16(kvr_context *ctx, uint64_t seed, uint64_t sid, uint64_t rows,
+                                       uint32_t width, const float *scale, uint16_t *out, void *stream) {
+    if (!scale || !width) return fail(KVR_ERR_INVALID, "scaled normal needs a channel scale");
+    kvr::SynthArgs a{};
+    a.kind = kvr::kSynthScaledNormalF16;
+    a.count = rows * width;
+    a.width = width;
+    a.scale = scale;
+    a.out = out;
+    return synth(ctx, a, seed, sid, stream);
+}
+
+kvr_status kvr_synth_normal_f32(kvr_context *ctx, uint64_t seed, uint64_t sid, uint64_t count, float *out,
+                                void *stream) {
+    kvr::SynthArgs a{};
+    a.kind = kvr::kSynthNormalF32;
+    a.count = count;
+    a.out = out;
+    return synth(ctx, a, seed, sid, stream);
+}
+
+kvr_status kvr_synth_q8_0(kvr_context *ctx, uint64_t seed, uint64_t sid, uint64_t blocks, float d_lo, float d_hi,
+                          uint8_t *out, void *stream) {
+    kvr::SynthArgs a{};
+    a.kind = kvr::kSynthQ8;
+    a.count = blocks;
+    a.lo = d_lo;
+    a.hi = d_hi;
+    a.out = out;
+    return synth(ctx, a, seed, sid, stream);
+}
+
+kvr_status kvr_synth_q4_1(kvr_context *ctx, uint64_t seed, uint64_t sid, uint64_t blocks, float d_lo, float d_hi,
+                          float m_lo, float m_hi, uint8_t *out, void *stream) {
+    kvr::SynthArgs a{};
+    a.kind = kvr::kSynthQ41;
+    a.count = blocks;
+    a.lo = d_lo;
+    a.hi = d_hi;
+    a.lo2 = m_lo;
+    a.hi2 = m_hi;
+    a.out = out;
+    return synth(ctx, a, seed, sid, stream);
+}
+
+kvr_status kvr_synth_normal_q8_0(kvr_context *ctx, uint64_t seed, uint64_t sid, uint64_t blocks, uint8_t *out,
+                                 void *stream) {
+    kvr::SynthArgs a{};
+    a.kind = kvr::kSynthNormalQ8;
+    a.count = blocks;
+    a.out = out;
+    return synth(ctx, a, seed, sid, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,163 @@
+// kvr_internal.hpp -- kernel argument blocks and launchers shared by the
+// C ABI (kvr_capi.cpp) and the kernels (kvr_kernels.hip).  Host side only
+// validates; every launcher assumes its arguments were checked.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace kvr {
+
+enum SummarySource : int { kSrcKeysF16 = 0, kSrcKeysQ8 = 1, kSrcSummary = 2 };
+enum Scalar : uint32_t { kScalarF16 = 0, kScalarF32 = 3, kScalarBF16 = 4 };  // kvr_format values
+enum Aggregation : uint32_t { kAggMean = 0, kAggMax = 1, kAggMaxLogit = 2 };
+
+struct QueryArgs {
+    const uint8_t *data;
+    uint32_t scalar;  // Scalar
+    uint32_t rows, qheads, kvheads, dim;
+    uint64_t row_stride, head_stride, dim_stride, lane_stride;  // bytes
+    double scale;
+};
+
+// Page summaries of `lanes` histories, optionally fused with the logits of
+// every query vector against every page.
+struct SummaryArgs {
+    const uint8_t *src;        // keys (token-major rows) or fp16 summaries
+    uint64_t src_lane_stride;  // bytes
+    uint64_t tokens;           // per lane (keys)
+    uint32_t page_tokens;
+    uint32_t pages;            // per lane
+    uint32_t width;            // kv_heads * head_dim
+    uint32_t lanes;
+    float *means;              // [lanes][pages][width] or null
+    uint16_t *summaries;       // [lanes][pages][width] or null
+    QueryArgs q;               // fused logits only
+    double *logits;            // [lanes][rows*qheads][pages]
+    uint32_t *status;
+    uint32_t epoch;
+};
+
+struct PackQueryArgs {
+    QueryArgs q;
+    uint32_t lanes;
+    uint16_t *out;  // [lanes][rows][qheads][dim] fp16
+    uint32_t *status;
+    uint32_t epoch;
+};
+
+struct MfmaLogitsArgs {
+    const uint16_t *qpack;      // [lanes][rows][qheads][dim]
+    const uint16_t *summaries;  // [lanes][pages][kvheads*dim]
+    uint32_t lanes, pages, rows, qheads, kvheads, dim;
+    double scale;
+    double *logits;             // [lanes][rows*qheads][pages]
+};
+
+struct SoftmaxArgs {
+    double *logits;            // [lanes][rows*qheads][pages], rewritten in place
+    const uint8_t *mask;       // [pages] or null
+    uint32_t lanes, rows, qheads, kvheads, pages;
+    uint32_t aggregation;
+};
+
+struct SelectArgs {
+    // aggregation (do_aggregate): scores[lane][p] (+)= sum_rows prob / weight
+    const double *probs;       // softmax output
+    uint32_t rows, qheads, kvheads;
+    uint32_t aggregation;
+    double weight;             // active_layers * heads
+    int accumulate;
+    int do_aggregate;
+    // selection (do_select)
+    double *scores;            // [lanes][pages]
+    uint32_t lanes, pages, k;
+    uint32_t tie_higher_first;
+    int signed_scores;
+    int do_select;
+    uint32_t n_mandatory;      // sorted, unique
+    uint32_t mandatory[64];
+    uint32_t *selected;        // [lanes][k]
+    uint32_t *count;           // [lanes]
+    uint32_t *status;
+    uint32_t epoch;
+};
+
+struct GatherPlane {
+    const uint8_t *src;   // device-visible pinned (or device staging) base
+    uint8_t *dst;
+    uint64_t src_lane_stride, dst_lane_stride;
+    uint64_t tokens;
+    uint32_t src_row, dst_row;  // bytes per token row
+    uint32_t width;
+    uint32_t format;            // kvr_format of the source
+    uint32_t mode;              // kvr_gather_mode
+};
+
+struct GatherArgs {
+    GatherPlane plane[8];
+    uint32_t n_planes;
+    uint32_t lanes, k, page_tokens;
+    uint32_t chunk_rows;        // token rows per workgroup
+    uint32_t chunks;            // per page
+    const uint32_t *selected;   // [lanes][k]; null -> slot i holds page i
+    const uint32_t *count;      // [lanes]; null -> k
+    uint64_t src_page_stride;   // 0: read pinned history; else staged page i at i*stride
+};
+
+struct AccumulateArgs {
+    float *sums;                // [pages][width]
+    uint32_t *counts;           // [pages]
+    uint32_t page_tokens, width, dim;
+    const uint8_t *k;
+    uint32_t scalar;
+    uint64_t pos0;
+    uint32_t n;
+    uint64_t token_stride, head_stride, dim_stride;
+    uint32_t first_page, segments;
+};
+
+struct FinalizeArgs {
+    const float *sums;
+    const uint32_t *counts;
+    uint32_t pages, width;
+    float *means;
+    uint16_t *summaries;
+    uint32_t *status;
+    uint32_t epoch;
+};
+
+struct CopyOp {
+    const uint8_t *src;
+    uint8_t *dst;
+    uint64_t bytes;
+};
+
+// ---- launchers (kvr_kernels.hip) ------------------------------------------
+hipError_t launch_summary(int source, bool fuse, const SummaryArgs &a, hipStream_t s);
+hipError_t launch_pack_query(const PackQueryArgs &a, hipStream_t s);
+hipError_t launch_logits_mfma(const MfmaLogitsArgs &a, hipStream_t s);
+hipError_t launch_softmax(const SoftmaxArgs &a, hipStream_t s);
+hipError_t launch_select(const SelectArgs &a, hipStream_t s);
+hipError_t launch_gather(const GatherArgs &a, hipStream_t s);
+hipError_t launch_accumulate(const AccumulateArgs &a, hipStream_t s);
+hipError_t launch_finalize(const FinalizeArgs &a, hipStream_t s);
+hipError_t launch_copy_ops(const CopyOp *ops, uint32_t n, hipStream_t s);
+
+enum SynthKind : int {
+    kSynthNormalF16 = 0, kSynthScaledNormalF16 = 1, kSynthNormalF32 = 2,
+    kSynthQ8 = 3, kSynthQ41 = 4, kSynthNormalQ8 = 5
+};
+struct SynthArgs {
+    int kind;
+    uint64_t base;
+    uint64_t count;    // elements, or blocks for q8_0 / q4_1
+    uint32_t width;    // scaled normal
+    const float *scale;
+    float lo, hi, lo2, hi2;
+    void *out;
+};
+hipError_t launch_synth(const SynthArgs &a, hipStream_t s);
+
+}  // namespace kvr

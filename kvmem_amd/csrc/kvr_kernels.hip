@@ -1,0 +1,841 @@
+// kvr_kernels.hip -- gfx950 kernels of the recall hot path.
+//
+// Summary kernel (HBM-bound, the dominant cost): one lane owns 8 channels of
+// one page and walks the page's token rows in order with 16-byte loads, so a
+// wave reads contiguous 1 KiB spans and every channel is summed in the
+// reference's order (binary32, token order from zero).  Scoring operands
+// cross the recall fp16 boundary; logits, softmax and aggregation run in
+// binary64 (the reference's CPU precision) so selection flips only on true
+// near-ties.  Reference citations are relative to the KVMem 0.19.0 tree.
+#include "kvr_device.hpp"
+#include "kvr_internal.hpp"
+
+#include <math.h>
+
+namespace kvr {
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kFmtF16 = 0, kFmtQ8 = 1, kFmtQ41 = 2;
+constexpr uint32_t kModeCopy = 0, kModeDequantF16 = 1, kModeRequantQ8 = 2;
+
+__device__ __forceinline__ float load_scalar(const uint8_t *p, uint32_t scalar) {
+    if (scalar == kScalarF32) return *reinterpret_cast<const float *>(p);
+    const uint16_t bits = *reinterpret_cast<const uint16_t *>(p);
+    return scalar == kScalarF16 ? h2f(bits) : bf2f(bits);
+}
+
+__device__ __forceinline__ void add_f16x8(float *acc, const u32x4 v) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        acc[2 * i] += h2f(uint16_t(v[i] & 0xffffu));
+        acc[2 * i + 1] += h2f(uint16_t(v[i] >> 16));
+    }
+}
+
+__device__ __forceinline__ void add_q8x8(float *acc, uint32_t lo, uint32_t hi, float d) {
+    // (float)q * d is exact in binary32 (8 x 11 significant bits), so the
+    // fused multiply-add below rounds exactly like "p = q*d; acc += p".
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        acc[i] += float(int8_t(lo >> (8 * i))) * d;
+        acc[4 + i] += float(int8_t(hi >> (8 * i))) * d;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Page summaries (+ fused logits).
+// Restates RawKvStore::capture_mean_f16 / add_mean_f32 + mean_k
+// (kvmem/src/host/raw_kv_store.cpp:158-197, 606-625) and, when FUSE, the
+// logit loop of page_softmax_scores (kvmem/src/host/graph_recall.cpp:355-368).
+// ---------------------------------------------------------------------------
+template <int SRC, bool FUSE>
+__global__ __launch_bounds__(256) void k_summary(SummaryArgs a) {
+    const uint32_t gpp = a.width >> 3;  // 8-channel groups per page
+    const uint64_t gid = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    const uint64_t total = uint64_t(a.lanes) * a.pages * gpp;
+    if (gid >= total) return;
+    const uint32_t cg = uint32_t(gid % gpp);
+    const uint64_t rest = gid / gpp;
+    const uint32_t page = uint32_t(rest % a.pages);
+    const uint32_t lane = uint32_t(rest / a.pages);
+    const uint32_t c0 = cg * 8;
+    uint16_t hb[8];
+
+    if (SRC == kSrcSummary) {
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(
+            a.src + lane * a.src_lane_stride + (uint64_t(page) * a.width + c0) * 2);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            hb[2 * i] = uint16_t(v[i] & 0xffffu);
+            hb[2 * i + 1] = uint16_t(v[i] >> 16);
+        }
+    } else {
+        const uint64_t t0 = uint64_t(page) * a.page_tokens;
+        const uint64_t left = a.tokens - t0;
+        const uint32_t n = left < a.page_tokens ? uint32_t(left) : a.page_tokens;
+        float acc[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+        if (SRC == kSrcKeysF16) {
+            const u32x4 *p = reinterpret_cast<const u32x4 *>(
+                a.src + lane * a.src_lane_stride + (t0 * a.width + c0) * 2);
+            const uint64_t stride = gpp;  // 16-byte words per token row
+            uint32_t t = 0;
+            constexpr int U = 16;
+            for (; t + U <= n; t += U) {
+                u32x4 v[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(p + (t + u) * stride);
+#pragma unroll
+                for (int u = 0; u < U; ++u) add_f16x8(acc, v[u]);
+            }
+            for (; t < n; ++t) add_f16x8(acc, __builtin_nontemporal_load(p + t * stride));
+        } else {
+            // q8_0 rows: lane owns 8 codes (quarter s) of block b.  Rows are
+            // 4-byte aligned (width % 64 == 0), so three aligned dwords cover
+            // the 8 codes and one more holds the block scale.
+            const uint32_t row_bytes = (a.width >> 5) * kQ8Bytes;
+            const uint8_t *base = a.src + lane * a.src_lane_stride + t0 * row_bytes;
+            const uint32_t b = cg >> 2, s = cg & 3;
+            const uint32_t o = b * kQ8Bytes + 2 + 8 * s;
+            const uint32_t w0 = o >> 2, wd = (b * kQ8Bytes) >> 2;
+            const bool sh = (o & 2) != 0, shd = ((b * kQ8Bytes) & 2) != 0;
+            uint32_t t = 0;
+            constexpr int U = 8;
+            for (; t + U <= n; t += U) {
+                uint32_t x0[U], x1[U], x2[U], dw[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const uint32_t *row = reinterpret_cast<const uint32_t *>(base + uint64_t(t + u) * row_bytes);
+                    x0[u] = __builtin_nontemporal_load(row + w0);
+                    x1[u] = __builtin_nontemporal_load(row + w0 + 1);
+                    x2[u] = sh ? __builtin_nontemporal_load(row + w0 + 2) : 0u;
+                    dw[u] = __builtin_nontemporal_load(row + wd);
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const uint32_t lo = sh ? __builtin_amdgcn_alignbyte(x1[u], x0[u], 2) : x0[u];
+                    const uint32_t hi = sh ? __builtin_amdgcn_alignbyte(x2[u], x1[u], 2) : x1[u];
+                    add_q8x8(acc, lo, hi, h2f(uint16_t(shd ? dw[u] >> 16 : dw[u] & 0xffffu)));
+                }
+            }
+            for (; t < n; ++t) {
+                const uint32_t *row = reinterpret_cast<const uint32_t *>(base + uint64_t(t) * row_bytes);
+                const uint32_t x0 = row[w0], x1 = row[w0 + 1], x2 = sh ? row[w0 + 2] : 0u, dw = row[wd];
+                const uint32_t lo = sh ? __builtin_amdgcn_alignbyte(x1, x0, 2) : x0;
+                const uint32_t hi = sh ? __builtin_amdgcn_alignbyte(x2, x1, 2) : x1;
+                add_q8x8(acc, lo, hi, h2f(uint16_t(shd ? dw >> 16 : dw & 0xffffu)));
+            }
+        }
+        const float inv = 1.0f / float(n);
+        float mean[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) mean[i] = acc[i] * inv;
+        const uint64_t out = (uint64_t(lane) * a.pages + page) * a.width + c0;
+        if (a.means) {
+            float4 *m4 = reinterpret_cast<float4 *>(a.means + out);
+            m4[0] = make_float4(mean[0], mean[1], mean[2], mean[3]);
+            m4[1] = make_float4(mean[4], mean[5], mean[6], mean[7]);
+        }
+        uint32_t bad = kOperandOk;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t e = recall16(mean[i], hb[i]);
+            bad = bad ? bad : e;
+        }
+        if (bad) raise_operand(a.status, bad, a.epoch);
+        if (a.summaries) {
+            u32x4 v;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = uint32_t(hb[2 * i]) | (uint32_t(hb[2 * i + 1]) << 16);
+            *reinterpret_cast<u32x4 *>(a.summaries + out) = v;
+        }
+    }
+
+    if (FUSE) {
+        const QueryArgs &q = a.q;
+        const uint32_t kvh = c0 / q.dim, d0 = c0 % q.dim;
+        const uint32_t group = q.qheads / q.kvheads;
+        const int lph = int(q.dim >> 3);  // lanes per kv-head slice
+        double m[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m[i] = double(h2f(hb[i]));
+        uint32_t bad = kOperandOk;
+        for (uint32_t r = 0; r < q.rows; ++r) {
+            for (uint32_t hh = 0; hh < group; ++hh) {
+                const uint32_t h = kvh * group + hh;
+                const uint8_t *qp = q.data + lane * q.lane_stride + r * q.row_stride +
+                                    h * q.head_stride + d0 * q.dim_stride;
+                double part = 0.0;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    uint16_t qb = 0;
+                    const uint32_t e = recall16(load_scalar(qp + i * q.dim_stride, q.scalar), qb);
+                    bad = bad ? bad : e;
+                    // fp16 x fp16 is exact in binary64: fma == multiply-then-add.
+                    part = fma(double(h2f(qb)), m[i], part);
+                }
+                part = group_sum(part, lph);
+                if ((cg & uint32_t(lph - 1)) == 0)
+                    a.logits[((uint64_t(lane) * q.rows + r) * q.qheads + h) * a.pages + page] =
+                        part * q.scale;
+            }
+        }
+        if (bad) raise_operand(a.status, bad, a.epoch);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Query rows -> packed fp16 operands (pack_current_query, page_softmax.cu:137-153,
+// with the recall_fp16 boundary of graph_recall.cpp:364).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_pack_query(PackQueryArgs a) {
+    const QueryArgs &q = a.q;
+    const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    const uint64_t per_lane = uint64_t(q.rows) * q.qheads * q.dim;
+    if (i >= per_lane * a.lanes) return;
+    const uint32_t lane = uint32_t(i / per_lane);
+    const uint64_t j = i % per_lane;
+    const uint32_t d = uint32_t(j % q.dim), h = uint32_t((j / q.dim) % q.qheads),
+                   r = uint32_t(j / (uint64_t(q.dim) * q.qheads));
+    uint16_t hb = 0;
+    const uint32_t e = recall16(load_scalar(q.data + lane * q.lane_stride + r * q.row_stride +
+                                                h * q.head_stride + d * q.dim_stride, q.scalar), hb);
+    if (e) raise_operand(a.status, e, a.epoch);
+    a.out[i] = hb;
+}
+
+// ---------------------------------------------------------------------------
+// Batched multi-row scoring on the matrix cores: per (lane, kv-head) the
+// logits block Q_g[M = rows*group][D] x S_g^T[D][pages] with
+// v_mfma_f64_16x16x4f64 (binary64 operands, exact fp16 products).
+// Operand lanes: A[m = l%16][k = l/16], B[k = l/16][n = l%16];
+// output register i of lane l is C[l/16 + 4i][l%16].  Lane l feeds the
+// contiguous k-range [(l/16)*D/4, (l/16+1)*D/4) of both operands.
+// One wave per 16-page tile; workgroups of four waves.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_logits_mfma(MfmaLogitsArgs a) {
+    const uint32_t wave = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const uint32_t n0 = (blockIdx.x * 4 + wave) * 16;
+    const uint32_t g = blockIdx.y, lane = blockIdx.z;
+    if (n0 >= a.pages) return;  // wave-uniform
+    const uint32_t group = a.qheads / a.kvheads;
+    const uint32_t M = a.rows * group;
+    const uint32_t ks = a.dim >> 2;
+    const uint32_t col = l & 15, kq = l >> 4;
+    const uint32_t page = n0 + col;
+    const bool pvalid = page < a.pages;
+    const uint32_t width = a.kvheads * a.dim;
+    const uint16_t *brow = a.summaries + (uint64_t(lane) * a.pages + (pvalid ? page : 0)) * width +
+                           g * a.dim + kq * ks;
+    for (uint32_t m0 = 0; m0 < M; m0 += 16) {
+        const uint32_t m = m0 + col;
+        const bool mvalid = m < M;
+        const uint32_t r = mvalid ? m / group : 0, hh = mvalid ? m % group : 0;
+        const uint16_t *arow = a.qpack + ((uint64_t(lane) * a.rows + r) * a.qheads + g * group + hh) * a.dim +
+                               kq * ks;
+        f64x4 acc = {0.0, 0.0, 0.0, 0.0};
+        for (uint32_t s = 0; s < ks; ++s) {
+            const double av = mvalid ? double(h2f(arow[s])) : 0.0;
+            const double bv = pvalid ? double(h2f(brow[s])) : 0.0;
+            acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av, bv, acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t mo = m0 + kq + 4 * i;
+            if (mo < M && pvalid) {
+                const uint32_t ro = mo / group, ho = mo % group;
+                a.logits[((uint64_t(lane) * a.rows + ro) * a.qheads + g * group + ho) * a.pages + page] =
+                    acc[i] * a.scale;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Page softmax (graph_recall.cpp:362-372).  One wave per distribution:
+// p_j = exp(l_j - max) / sum over the score-mask pages; masked pages get 0.
+// ---------------------------------------------------------------------------
+__device__ void softmax_wave(double *x, uint32_t n, const uint8_t *mask, uint32_t l) {
+    double m = -INFINITY;
+    for (uint32_t j = l; j < n; j += kWave)
+        if (!mask || mask[j]) m = fmax(m, x[j]);
+    m = wave_max(m);
+    double s = 0.0;
+    for (uint32_t j = l; j < n; j += kWave) {
+        const double e = (!mask || mask[j]) ? exp(x[j] - m) : 0.0;
+        x[j] = e;
+        s += e;
+    }
+    s = wave_sum(s);
+    for (uint32_t j = l; j < n; j += kWave) x[j] = s > 0.0 ? x[j] / s : 0.0;
+}
+
+template <class T, class Op>
+__device__ T block_reduce(T v, T *lds, Op op) {
+    // lds: >= blockDim.x/64 + 1 entries; deterministic fixed-order tree.
+    const uint32_t wave = threadIdx.x >> 6, l = threadIdx.x & 63, nw = blockDim.x >> 6;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = op(v, __shfl_xor(v, o, kWave));
+    if (l == 0) lds[wave] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        T r = lds[0];
+        for (uint32_t w = 1; w < nw; ++w) r = op(r, lds[w]);
+        lds[nw] = r;
+    }
+    __syncthreads();
+    const T r = lds[nw];
+    __syncthreads();
+    return r;
+}
+
+struct SumOp { __device__ double operator()(double a, double b) const { return a + b; } };
+struct MaxOp { __device__ double operator()(double a, double b) const { return b > a ? b : a; } };
+
+__global__ __launch_bounds__(256) void k_softmax_rows(SoftmaxArgs a) {
+    const uint64_t row = uint64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (row >= uint64_t(a.lanes) * a.rows * a.qheads) return;
+    softmax_wave(a.logits + row * a.pages, a.pages, a.mask, threadIdx.x & 63);
+}
+
+// One workgroup per (lane, row, kv-head) group.
+//  Max (graph_recall.cpp:381-389): per-head softmax, g_j = max_h p_{h,j},
+//       first row of the group := g_j / sum_j g_j.
+//  MaxLogit: m_j = max_h logit_{h,j}; first row := softmax_j(m_j).
+__global__ __launch_bounds__(256) void k_softmax_groups(SoftmaxArgs a) {
+    __shared__ double red[8];
+    const uint32_t group = a.qheads / a.kvheads;
+    const uint32_t gi = blockIdx.x;
+    const uint32_t g = gi % a.kvheads;
+    const uint64_t lr = gi / a.kvheads;  // lane*rows + r
+    double *base = a.logits + (lr * a.qheads + uint64_t(g) * group) * a.pages;
+    const uint32_t wave = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const uint32_t n = a.pages;
+    if (a.aggregation == kAggMax) {
+        for (uint32_t hh = wave; hh < group; hh += blockDim.x >> 6)
+            softmax_wave(base + uint64_t(hh) * n, n, a.mask, l);
+        __syncthreads();
+        double s = 0.0;
+        for (uint32_t j = threadIdx.x; j < n; j += blockDim.x) {
+            double gm = 0.0;
+            for (uint32_t hh = 0; hh < group; ++hh) {
+                const double p = base[uint64_t(hh) * n + j];
+                gm = p > gm ? p : gm;
+            }
+            base[j] = gm;
+            s += gm;
+        }
+        const double mass = block_reduce(s, red, SumOp());
+        for (uint32_t j = threadIdx.x; j < n; j += blockDim.x) base[j] = mass > 0.0 ? base[j] / mass : 0.0;
+    } else {
+        double mx = -INFINITY;
+        for (uint32_t j = threadIdx.x; j < n; j += blockDim.x) {
+            double gm = -INFINITY;
+            if (!a.mask || a.mask[j])
+                for (uint32_t hh = 0; hh < group; ++hh) gm = fmax(gm, base[uint64_t(hh) * n + j]);
+            base[j] = gm;
+            mx = fmax(mx, gm);
+        }
+        mx = block_reduce(mx, red, MaxOp());
+        double s = 0.0;
+        for (uint32_t j = threadIdx.x; j < n; j += blockDim.x) {
+            const double e = (!a.mask || a.mask[j]) ? exp(base[j] - mx) : 0.0;
+            base[j] = e;
+            s += e;
+        }
+        const double tot = block_reduce(s, red, SumOp());
+        for (uint32_t j = threadIdx.x; j < n; j += blockDim.x) base[j] = tot > 0.0 ? base[j] / tot : 0.0;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Aggregation + top-k, one 1024-thread workgroup per lane.
+// Aggregation sums the rows' probabilities in the reference's loop order
+// (graph_recall.cpp:375-389).  Selection restates KvMemStore::pick_scored_blocks
+// (kvmem/src/host/kvmem_store.cpp:418-451): mandatory pages first, then the
+// best (score desc, id by tie rule) up to k, output in ascending id order.
+// The k-th best key is found by an 8-pass MSB radix select over
+// order-preserving 64-bit keys; ties at the threshold are resolved by the
+// pages' rank among equal keys in id order.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t order_key(double v) {
+    uint64_t u = uint64_t(__double_as_longlong(v));
+    if ((u << 1) == 0) u = 0;  // -0.0 ranks equal to +0.0
+    return (u >> 63) ? ~u : (u | 0x8000000000000000ull);
+}
+
+__device__ __forceinline__ bool is_mandatory(const SelectArgs &a, uint32_t j) {
+    uint32_t lo = 0, hi = a.n_mandatory;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (a.mandatory[mid] < j) lo = mid + 1; else hi = mid;
+    }
+    return lo < a.n_mandatory && a.mandatory[lo] == j;
+}
+
+__device__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *total, uint32_t *lds) {
+    const uint32_t wave = threadIdx.x >> 6, l = threadIdx.x & 63, nw = blockDim.x >> 6;
+    const uint32_t incl = wave_inclusive_scan(v);
+    if (l == 63) lds[wave] = incl;
+    __syncthreads();
+    if (wave == 0) {
+        const uint32_t w = l < nw ? lds[l] : 0u;
+        const uint32_t wi = wave_inclusive_scan(w);
+        if (l < nw) lds[l] = wi - w;
+        if (l == nw - 1) lds[16] = wi;
+    }
+    __syncthreads();
+    const uint32_t r = lds[wave] + incl - v;
+    *total = lds[16];
+    __syncthreads();
+    return r;
+}
+
+__global__ __launch_bounds__(1024) void k_select(SelectArgs a) {
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t scan_lds[17];
+    __shared__ uint32_t s_digit, s_remaining;
+    const uint32_t lane = blockIdx.x, tid = threadIdx.x;
+    double *sc = a.scores + uint64_t(lane) * a.pages;
+    const uint32_t n = a.pages;
+
+    if (a.do_aggregate) {
+        const uint32_t group = a.qheads / a.kvheads;
+        const uint64_t lane_rows = uint64_t(lane) * a.rows * a.qheads;
+        for (uint32_t j = tid; j < n; j += blockDim.x) {
+            double acc = a.accumulate ? sc[j] : 0.0;
+            if (a.aggregation == kAggMean) {
+                for (uint32_t rho = 0; rho < a.rows * a.qheads; ++rho)
+                    acc += a.probs[(lane_rows + rho) * n + j] / a.weight;
+            } else {
+                for (uint32_t r = 0; r < a.rows; ++r)
+                    for (uint32_t g = 0; g < a.kvheads; ++g)
+                        acc += a.probs[(lane_rows + uint64_t(r) * a.qheads + g * group) * n + j] / a.weight;
+            }
+            sc[j] = acc;
+        }
+        __syncthreads();
+    }
+    if (!a.do_select) return;
+
+    // Reject invalid scores (pick_scored_blocks, kvmem_store.cpp:425-426).
+    int bad = 0;
+    for (uint32_t j = tid; j < n; j += blockDim.x) {
+        const double v = sc[j];
+        bad |= !__builtin_isfinite(v) || (!a.signed_scores && v < 0.0);
+    }
+    bad = __syncthreads_or(bad);
+    if (bad && tid == 0) raise_status(a.status, kStatusScores, a.epoch);
+    if (bad || epoch_failed(a.status, a.epoch)) {
+        if (tid == 0) a.count[lane] = 0;
+        return;
+    }
+
+    const uint32_t n_cand = n - a.n_mandatory;
+    const uint32_t k_eff = a.k - a.n_mandatory;  // host guarantees n_mandatory <= k
+    uint64_t thresh;
+    uint32_t remaining;
+    if (k_eff == 0) {
+        thresh = ~0ull;
+        remaining = 0;
+    } else if (k_eff >= n_cand) {
+        thresh = 0;
+        remaining = 0xffffffffu;
+    } else {
+        uint64_t prefix = 0, pmask = 0;
+        remaining = k_eff;
+        for (int pass = 0; pass < 8; ++pass) {
+            const int shift = 56 - 8 * pass;
+            if (tid < 256) hist[tid] = 0;
+            __syncthreads();
+            for (uint32_t j = tid; j < n; j += blockDim.x) {
+                if (a.n_mandatory && is_mandatory(a, j)) continue;
+                const uint64_t key = order_key(sc[j]);
+                if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+            }
+            __syncthreads();
+            if (tid < 64) {
+                // lane l covers digits 255-4l .. 252-4l, highest first
+                const uint32_t c0 = hist[255 - 4 * tid], c1 = hist[254 - 4 * tid],
+                               c2 = hist[253 - 4 * tid], c3 = hist[252 - 4 * tid];
+                const uint32_t tot = c0 + c1 + c2 + c3;
+                const uint32_t incl = wave_inclusive_scan(tot);
+                const uint32_t excl = incl - tot;
+                if (excl < remaining && remaining <= incl) {
+                    uint32_t rem = remaining - excl, d;
+                    if (rem <= c0) {
+                        d = 255 - 4 * tid;
+                    } else if (rem <= c0 + c1) {
+                        rem -= c0; d = 254 - 4 * tid;
+                    } else if (rem <= c0 + c1 + c2) {
+                        rem -= c0 + c1; d = 253 - 4 * tid;
+                    } else {
+                        rem -= c0 + c1 + c2; d = 252 - 4 * tid;
+                    }
+                    s_digit = d;
+                    s_remaining = rem;
+                }
+            }
+            __syncthreads();
+            prefix |= uint64_t(s_digit) << shift;
+            pmask |= 0xffull << shift;
+            remaining = s_remaining;
+            __syncthreads();
+        }
+        thresh = prefix;
+    }
+
+    // Compaction in id order: thread t owns the contiguous id chunk
+    // [t*C, t*C + C).
+    const uint32_t C = (n + blockDim.x - 1) / blockDim.x;
+    const uint32_t j0 = min(n, tid * C), j1 = min(n, j0 + C);
+    uint32_t n_take = 0, n_eq = 0;
+    for (uint32_t j = j0; j < j1; ++j) {
+        if (a.n_mandatory && is_mandatory(a, j)) { ++n_take; continue; }
+        const uint64_t key = order_key(sc[j]);
+        n_take += key > thresh;
+        n_eq += key == thresh;
+    }
+    uint32_t eq_total;
+    const uint32_t eq_base = block_exclusive_scan(n_eq, &eq_total, scan_lds);
+    uint32_t lo, hi;  // equal-key ranks [lo, hi) are taken
+    if (a.tie_higher_first) {
+        lo = remaining >= eq_total ? 0u : eq_total - remaining;
+        hi = eq_total;
+    } else {
+        lo = 0;
+        hi = remaining < eq_total ? remaining : eq_total;
+    }
+    const uint32_t eq_lo = max(lo, eq_base), eq_hi = min(hi, eq_base + n_eq);
+    n_take += eq_hi > eq_lo ? eq_hi - eq_lo : 0u;
+    uint32_t total;
+    uint32_t o = block_exclusive_scan(n_take, &total, scan_lds);
+    uint32_t rank = eq_base;
+    uint32_t *out = a.selected + uint64_t(lane) * a.k;
+    for (uint32_t j = j0; j < j1; ++j) {
+        bool take;
+        if (a.n_mandatory && is_mandatory(a, j)) {
+            take = true;
+        } else {
+            const uint64_t key = order_key(sc[j]);
+            if (key == thresh) {
+                take = rank >= lo && rank < hi;
+                ++rank;
+            } else {
+                take = key > thresh;
+            }
+        }
+        if (take && o < a.k) out[o++] = j;
+    }
+    if (tid == 0) a.count[lane] = min(total, a.k);
+}
+
+// ---------------------------------------------------------------------------
+// Stage-in gather.  One workgroup copies `chunk_rows` token rows of one
+// selected page of one plane.  Sources are pinned host pages read directly
+// over the host link (or staged device copies); destinations are slot rows
+// [slot*page_tokens + r] (write_block_to_gpu, llama-memory-kvmem.cpp:4464-4520).
+//   copy         bytes unchanged                       (stagein.cu:236-261)
+//   dequant_f16  q8_0: y = q*d (stagein.cu:133-143); q4_1: y = nib*d + m;
+//                then RNE binary16
+//   requant_q8_0 d = amax/127, q = roundf(x/d)          (stagein.cu:181-199)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void copy_span(const uint8_t *src, uint8_t *dst, uint32_t bytes) {
+    if (((uintptr_t(src) | uintptr_t(dst) | bytes) & 15u) == 0) {
+        const u32x4 *s = reinterpret_cast<const u32x4 *>(src);
+        u32x4 *d = reinterpret_cast<u32x4 *>(dst);
+        const uint32_t n = bytes >> 4;
+        uint32_t i = threadIdx.x;
+        for (; i + 3 * 256 < n; i += 4 * 256) {
+            const u32x4 v0 = __builtin_nontemporal_load(s + i), v1 = __builtin_nontemporal_load(s + i + 256),
+                        v2 = __builtin_nontemporal_load(s + i + 512), v3 = __builtin_nontemporal_load(s + i + 768);
+            d[i] = v0; d[i + 256] = v1; d[i + 512] = v2; d[i + 768] = v3;
+        }
+        for (; i < n; i += 256) d[i] = __builtin_nontemporal_load(s + i);
+    } else if (((uintptr_t(src) | uintptr_t(dst) | bytes) & 3u) == 0) {
+        const uint32_t *s = reinterpret_cast<const uint32_t *>(src);
+        uint32_t *d = reinterpret_cast<uint32_t *>(dst);
+        for (uint32_t i = threadIdx.x; i < bytes >> 2; i += 256) d[i] = s[i];
+    } else {
+        for (uint32_t i = threadIdx.x; i < bytes; i += 256) dst[i] = src[i];
+    }
+}
+
+__device__ __forceinline__ void decode_block(const uint8_t *blk, uint32_t fmt, float *y) {
+    const float d = h2f(ld_u16(blk));
+    if (fmt == kFmtQ8) {
+#pragma unroll
+        for (int j = 0; j < kQK; ++j) y[j] = float(int8_t(blk[2 + j])) * d;
+    } else {
+        const float m = h2f(ld_u16(blk + 2));
+#pragma unroll
+        for (int j = 0; j < kQK / 2; ++j) {
+            const uint8_t b = blk[4 + j];
+            // nib*d is exact, so fma(nib, d, m) rounds like "nib*d + m".
+            y[j] = float(b & 15) * d + m;
+            y[j + kQK / 2] = float(b >> 4) * d + m;
+        }
+    }
+}
+
+__device__ __forceinline__ void quant_block_q8(const float *x, uint8_t *blk) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kQK; ++j) amax = fmaxf(amax, fabsf(x[j]));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const uint16_t dh = f2h(d);
+    blk[0] = uint8_t(dh);
+    blk[1] = uint8_t(dh >> 8);
+#pragma unroll
+    for (int j = 0; j < kQK; ++j) blk[2 + j] = uint8_t(int8_t(roundf(x[j] * id)));
+}
+
+__global__ __launch_bounds__(256) void k_gather(GatherArgs a) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const uint32_t lane = blockIdx.y;
+    uint32_t id = blockIdx.x;
+    const uint32_t chunk = id % a.chunks;
+    id /= a.chunks;
+    const uint32_t pi = id % a.n_planes;
+    const uint32_t slot = id / a.n_planes;
+    const uint32_t cnt = a.count ? a.count[lane] : a.k;
+    if (slot >= cnt) return;
+    const GatherPlane &P = a.plane[pi];
+    const uint32_t page = a.selected ? a.selected[uint64_t(lane) * a.k + slot] : slot;
+    const uint64_t first = uint64_t(page) * a.page_tokens;
+    if (first >= P.tokens) return;
+    const uint64_t left = P.tokens - first;
+    const uint32_t valid = left < a.page_tokens ? uint32_t(left) : a.page_tokens;
+    const uint32_t r0 = chunk * a.chunk_rows;
+    if (r0 >= valid) return;
+    const uint32_t nr = min(a.chunk_rows, valid - r0);
+    // Staged sources (src_page_stride != 0) hold slot s's page at s*stride.
+    const uint8_t *src = a.src_page_stride
+        ? P.src + lane * P.src_lane_stride + uint64_t(slot) * a.src_page_stride + uint64_t(r0) * P.src_row
+        : P.src + lane * P.src_lane_stride + (first + r0) * P.src_row;
+    uint8_t *dst = P.dst + lane * P.dst_lane_stride + (uint64_t(slot) * a.page_tokens + r0) * P.dst_row;
+    const uint32_t sbytes = nr * P.src_row;
+    if (P.mode == kModeCopy || P.format == kFmtF16) {
+        copy_span(src, dst, sbytes);
+        return;
+    }
+    // Stage the packed rows in LDS, then decode whole blocks.
+    copy_span(src, lds, sbytes);
+    __syncthreads();
+    const uint32_t bpr = P.width / kQK;
+    const uint32_t bbytes = P.format == kFmtQ8 ? kQ8Bytes : kQ41Bytes;
+    const uint32_t nblocks = nr * bpr;
+    if (P.mode == kModeDequantF16) {
+        for (uint32_t b = threadIdx.x; b < nblocks; b += 256) {
+            float y[kQK];
+            decode_block(lds + b * bbytes, P.format, y);
+            u32x4 *o = reinterpret_cast<u32x4 *>(dst + uint64_t(b / bpr) * P.dst_row + (b % bpr) * 64);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                u32x4 v;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    v[i] = uint32_t(f2h(y[8 * q + 2 * i])) | (uint32_t(f2h(y[8 * q + 2 * i + 1])) << 16);
+                o[q] = v;
+            }
+        }
+    } else {
+        uint8_t *out = lds + ((sbytes + 15u) & ~15u);
+        for (uint32_t b = threadIdx.x; b < nblocks; b += 256) {
+            float y[kQK];
+            decode_block(lds + b * kQ8Bytes, kFmtQ8, y);
+            quant_block_q8(y, out + b * kQ8Bytes);
+        }
+        __syncthreads();
+        copy_span(out, dst, sbytes);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Capture-side running mean-K sums (kvmem_meank_add, stagein.cu:270-320, and
+// add_mean_f32's page restart rule, raw_kv_store.cpp:178-197).  One thread per
+// (page segment, channel), sequential over the segment's tokens.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_accumulate(AccumulateArgs a) {
+    const uint64_t gid = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (gid >= uint64_t(a.segments) * a.width) return;
+    const uint32_t c = uint32_t(gid % a.width);
+    const uint32_t page = a.first_page + uint32_t(gid / a.width);
+    const uint64_t pstart = uint64_t(page) * a.page_tokens;
+    const uint64_t s = max(a.pos0, pstart), e = min(a.pos0 + a.n, pstart + a.page_tokens);
+    const uint32_t off = uint32_t(s - pstart), take = uint32_t(e - s);
+    float *sum = a.sums + uint64_t(page) * a.width + c;
+    float acc = off == 0 ? 0.0f : *sum;
+    const uint32_t h = c / a.dim, d = c % a.dim;
+    const uint8_t *p = a.k + (s - a.pos0) * a.token_stride + h * a.head_stride + d * a.dim_stride;
+    for (uint32_t t = 0; t < take; ++t) acc += load_scalar(p + uint64_t(t) * a.token_stride, a.scalar);
+    *sum = acc;
+    if (c == 0) a.counts[page] = off == 0 ? take : max(a.counts[page], off + take);
+}
+
+__global__ __launch_bounds__(256) void k_finalize(FinalizeArgs a) {
+    const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= uint64_t(a.pages) * a.width) return;
+    const uint32_t n = a.counts[i / a.width];
+    float mean = 0.0f;
+    if (n) mean = a.sums[i] * (1.0f / float(n));
+    if (a.means) a.means[i] = mean;
+    if (a.summaries) {
+        uint16_t hb = 0;
+        const uint32_t e = recall16(mean, hb);
+        if (e) raise_operand(a.status, e, a.epoch);
+        a.summaries[i] = hb;
+    }
+}
+
+// Batched byte copies (copy_bytes, stagein.cu:236-261): one workgroup per op.
+__global__ __launch_bounds__(256) void k_copy_ops(const CopyOp *ops, uint32_t n) {
+    if (blockIdx.x >= n) return;
+    const CopyOp op = ops[blockIdx.x];
+    if (!op.src || !op.dst || !op.bytes) return;
+    for (uint64_t off = 0; off < op.bytes; off += 0x40000000ull) {
+        const uint64_t part = min(op.bytes - off, 0x40000000ull);
+        copy_span(op.src + off, op.dst + off, uint32_t(part));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Seeded synthetic inputs (same arithmetic as the oracle's generator).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_synth(SynthArgs a) {
+    const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= a.count) return;
+    switch (a.kind) {
+    case kSynthNormalF16:
+        static_cast<uint16_t *>(a.out)[i] = f2h(synth_normal(a.base, i));
+        break;
+    case kSynthScaledNormalF16:
+        static_cast<uint16_t *>(a.out)[i] = f2h(__fmul_rn(synth_normal(a.base, i), a.scale[i % a.width]));
+        break;
+    case kSynthNormalF32:
+        static_cast<float *>(a.out)[i] = synth_normal(a.base, i);
+        break;
+    case kSynthQ8: {
+        uint8_t *blk = static_cast<uint8_t *>(a.out) + i * kQ8Bytes;
+        for (int w = 0; w < 8; ++w) {
+            const uint64_t r = synth_bits(a.base, i * 9 + w);
+            for (int c = 0; c < 4; ++c)
+                blk[2 + w * 4 + c] = uint8_t(int8_t(int((r >> (16 * c)) & 0xffffu) % 255 - 127));
+        }
+        const uint16_t d = f2h(synth_lerp(a.lo, a.hi, synth_unit24(synth_bits(a.base, i * 9 + 8))));
+        blk[0] = uint8_t(d);
+        blk[1] = uint8_t(d >> 8);
+        break;
+    }
+    case kSynthQ41: {
+        uint8_t *blk = static_cast<uint8_t *>(a.out) + i * kQ41Bytes;
+        for (int w = 0; w < 2; ++w) {
+            const uint64_t r = synth_bits(a.base, i * 4 + w);
+            for (int c = 0; c < 8; ++c) blk[4 + w * 8 + c] = uint8_t(r >> (8 * c));
+        }
+        const uint16_t d = f2h(synth_lerp(a.lo, a.hi, synth_unit24(synth_bits(a.base, i * 4 + 2))));
+        const uint16_t m = f2h(synth_lerp(a.lo2, a.hi2, synth_unit24(synth_bits(a.base, i * 4 + 3))));
+        blk[0] = uint8_t(d); blk[1] = uint8_t(d >> 8);
+        blk[2] = uint8_t(m); blk[3] = uint8_t(m >> 8);
+        break;
+    }
+    case kSynthNormalQ8: {
+        float x[kQK];
+        for (int j = 0; j < kQK; ++j) x[j] = synth_normal(a.base, i * kQK + j);
+        quant_block_q8(x, static_cast<uint8_t *>(a.out) + i * kQ8Bytes);
+        break;
+    }
+    }
+}
+
+inline unsigned blocks_for(uint64_t threads, unsigned per = 256) {
+    return unsigned((threads + per - 1) / per);
+}
+
+}  // namespace
+
+// ---- launchers ------------------------------------------------------------
+hipError_t launch_summary(int source, bool fuse, const SummaryArgs &a, hipStream_t s) {
+    const uint64_t threads = uint64_t(a.lanes) * a.pages * (a.width >> 3);
+    const dim3 grid(blocks_for(threads)), block(256);
+    if (source == kSrcKeysF16 && fuse)
+        hipLaunchKernelGGL((k_summary<kSrcKeysF16, true>), grid, block, 0, s, a);
+    else if (source == kSrcKeysF16)
+        hipLaunchKernelGGL((k_summary<kSrcKeysF16, false>), grid, block, 0, s, a);
+    else if (source == kSrcKeysQ8 && fuse)
+        hipLaunchKernelGGL((k_summary<kSrcKeysQ8, true>), grid, block, 0, s, a);
+    else if (source == kSrcKeysQ8)
+        hipLaunchKernelGGL((k_summary<kSrcKeysQ8, false>), grid, block, 0, s, a);
+    else
+        hipLaunchKernelGGL((k_summary<kSrcSummary, true>), grid, block, 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_pack_query(const PackQueryArgs &a, hipStream_t s) {
+    const uint64_t n = uint64_t(a.lanes) * a.q.rows * a.q.qheads * a.q.dim;
+    hipLaunchKernelGGL(k_pack_query, dim3(blocks_for(n)), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_logits_mfma(const MfmaLogitsArgs &a, hipStream_t s) {
+    const dim3 grid((a.pages + 63) / 64, a.kvheads, a.lanes);
+    hipLaunchKernelGGL(k_logits_mfma, grid, dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_softmax(const SoftmaxArgs &a, hipStream_t s) {
+    if (a.aggregation == kAggMean) {
+        const uint64_t rows = uint64_t(a.lanes) * a.rows * a.qheads;
+        hipLaunchKernelGGL(k_softmax_rows, dim3(unsigned((rows + 3) / 4)), dim3(256), 0, s, a);
+    } else {
+        const unsigned groups = unsigned(uint64_t(a.lanes) * a.rows * a.kvheads);
+        hipLaunchKernelGGL(k_softmax_groups, dim3(groups), dim3(256), 0, s, a);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_select(const SelectArgs &a, hipStream_t s) {
+    hipLaunchKernelGGL(k_select, dim3(a.lanes), dim3(1024), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather(const GatherArgs &a, hipStream_t s) {
+    uint32_t lds = 0;
+    for (uint32_t i = 0; i < a.n_planes; ++i) {
+        const GatherPlane &p = a.plane[i];
+        if (p.mode == kModeCopy || p.format == kFmtF16) continue;
+        uint32_t need = ((a.chunk_rows * p.src_row + 15u) & ~15u);
+        if (p.mode == kModeRequantQ8) need += a.chunk_rows * p.src_row;
+        lds = need > lds ? need : lds;
+    }
+    const dim3 grid(a.k * a.n_planes * a.chunks, a.lanes);
+    hipLaunchKernelGGL(k_gather, grid, dim3(256), lds, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_accumulate(const AccumulateArgs &a, hipStream_t s) {
+    hipLaunchKernelGGL(k_accumulate, dim3(blocks_for(uint64_t(a.segments) * a.width)), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_finalize(const FinalizeArgs &a, hipStream_t s) {
+    hipLaunchKernelGGL(k_finalize, dim3(blocks_for(uint64_t(a.pages) * a.width)), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_copy_ops(const CopyOp *ops, uint32_t n, hipStream_t s) {
+    hipLaunchKernelGGL(k_copy_ops, dim3(n), dim3(256), 0, s, ops, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_synth(const SynthArgs &a, hipStream_t s) {
+    hipLaunchKernelGGL(k_synth, dim3(blocks_for(a.count)), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace kvr

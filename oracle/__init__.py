@@ -1,0 +1,380 @@
+"""ctypes bindings for the checkers: the C restatement (liboracle.so) and,
+where it was built, the reference's own host library (_ref/libkvmem_ref.so).
+
+TEST INFRASTRUCTURE ONLY.  Imported by tests/, by __graft_entry__.smoke()
+and by bench.py's CPU-baseline leg; the product package never imports it.
+Array arguments are numpy arrays; results come back as numpy arrays.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from typing import Optional, Sequence
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+OK, ERR_ARG, ERR_NONFINITE, ERR_RANGE, ERR_BUDGET = 0, 1, 2, 3, 4
+AGG_MEAN, AGG_MAX, AGG_MAX_LOGIT = 0, 1, 2
+TIE_LOWER_FIRST, TIE_HIGHER_FIRST = 0, 1
+FMT_F16, FMT_Q8_0, FMT_Q4_1 = 0, 1, 2
+GATHER_COPY, GATHER_DEQUANT_F16, GATHER_REQUANT_Q8_0 = 0, 1, 2
+QK, Q8_0_BYTES, Q4_1_BYTES = 32, 34, 20
+
+_P = C.c_void_p
+_u8, _u16, _u32, _u64 = C.c_uint8, C.c_uint16, C.c_uint32, C.c_uint64
+
+
+class OracleError(RuntimeError):
+    def __init__(self, code: int, what: str = ""):
+        super().__init__(f"oracle status {code}{': ' + what if what else ''}")
+        self.code = code
+
+
+def _ptr(a: Optional[np.ndarray]):
+    return None if a is None else a.ctypes.data_as(_P)
+
+
+def _load_oracle() -> C.CDLL:
+    path = os.path.join(HERE, "liboracle.so")
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} is not built; run __graft_entry__.build()")
+    lib = C.CDLL(path)
+    sig = {
+        "orc_f32_to_f16": (_u16, [C.c_float]),
+        "orc_f16_to_f32": (C.c_float, [_u16]),
+        "orc_recall_fp16": (C.c_int, [C.c_float, _P]),
+        "orc_page_count": (_u32, [_u64, _u32]),
+        "orc_query_score_frame": (C.c_int, [_u64, _u32, _u32, _u32, _u32, _P, _u32, _P, _P, _P, _P]),
+        "orc_row_bytes": (C.c_size_t, [C.c_int, _u32]),
+        "orc_page_summaries": (C.c_int, [_P, C.c_int, _u64, _u32, _u32, _P, _P]),
+        "orc_page_softmax_scores": (C.c_int, [_P, _P, _P, _u32, _u32, _u32, _u32, _u32, _u32, _P,
+                                              C.c_float, C.c_int, _P]),
+        "orc_page_logits": (C.c_int, [_P, _P, _u32, _u32, _u32, _u32, _u32, C.c_float, _P]),
+        "orc_pick_scored_blocks": (C.c_int, [_P, _u32, _P, _u32, _u32, C.c_int, C.c_int, _P, _P]),
+        "orc_dequant_q8_0": (None, [_P, _P]),
+        "orc_dequant_q4_1": (None, [_P, _P]),
+        "orc_quant_q8_0": (None, [_P, _P]),
+        "orc_gather_row_bytes": (C.c_size_t, [C.c_int, C.c_int, _u32]),
+        "orc_gather": (C.c_int, [_P, C.c_int, _u32, _u64, _u32, _P, _u32, C.c_int, _P]),
+        "orc_synth_bits": (_u64, [_u64, _u64, _u64]),
+        "orc_synth_normal": (C.c_double, [_u64, _u64, _u64]),
+        "orc_synth_uniform": (C.c_float, [_u64, _u64, _u64, C.c_float, C.c_float]),
+        "orc_synth_normal_f16": (None, [_u64, _u64, _u64, _P]),
+        "orc_synth_scaled_normal_f16": (None, [_u64, _u64, _u64, _u32, _P, _P]),
+        "orc_synth_normal_f32": (None, [_u64, _u64, _u64, _P]),
+        "orc_synth_uniform_f32": (None, [_u64, _u64, _u64, C.c_float, C.c_float, _P]),
+        "orc_synth_q8_0": (None, [_u64, _u64, _u64, C.c_float, C.c_float, _P]),
+        "orc_synth_q4_1": (None, [_u64, _u64, _u64, C.c_float, C.c_float, C.c_float, C.c_float, _P]),
+        "orc_synth_normal_q8_0": (None, [_u64, _u64, _u64, _P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+def _load_ref() -> Optional[C.CDLL]:
+    path = os.path.join(HERE, "_ref", "libkvmem_ref.so")
+    if not os.path.exists(path):
+        return None
+    lib = C.CDLL(path)
+    sig = {
+        "ref_last_error": (C.c_char_p, []),
+        "ref_recall_fp16": (C.c_int, [C.c_float, _P]),
+        "ref_query_score_frame": (C.c_int, [_u64, _u32, _u32, _u32, _u32, _P, _u32, _P, _P, _P, _P]),
+        "ref_scores_f16_keys": (C.c_int, [_P, _u32, _u64, _u32, _u32, _u32, _P, _P, _u32, _u32,
+                                          C.c_float, C.c_int, _P, _P, _P]),
+        "ref_scores_f32_keys": (C.c_int, [_P, _u32, _u64, _u32, _u32, _u32, _P, _P, _u32, _u32,
+                                          C.c_float, C.c_int, _P, _P, _P]),
+        "ref_scores_from_sums": (C.c_int, [_P, _u32, _u32, _u32, _u32, _u32, _P, _P, _u32, _u32,
+                                           C.c_float, C.c_int, _P, _P]),
+        "ref_layerwise_scores_f16_keys": (C.c_int, [_P, _u32, _u32, _u64, _u32, _u32, _u32, _P,
+                                                    _u32, _u32, C.c_float, _P]),
+        "ref_pick_scored_blocks": (C.c_int, [_P, _u32, _P, _u32, _u32, C.c_int, _P, _P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _load_oracle()
+ref = _load_ref()
+
+
+def _check(code: int) -> None:
+    if code != OK:
+        raise OracleError(code)
+
+
+def _ref_check(code: int) -> None:
+    if code != 0:
+        raise OracleError(code, ref.ref_last_error().decode())
+
+
+def _c(a, dtype) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+# ---- conversions -----------------------------------------------------------
+
+def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    x = _c(x, np.float32).ravel()
+    return np.array([lib.orc_f32_to_f16(float(v)) for v in x], dtype=np.uint16)
+
+
+def recall_fp16(value: float) -> float:
+    out = C.c_float()
+    _check(lib.orc_recall_fp16(value, C.byref(out)))
+    return out.value
+
+
+def query_score_frame(accepted: int, block_tokens: int, budget: int, sink: int, recent: int,
+                      fixed: Sequence[int] = (), use_ref: bool = False):
+    n = lib.orc_page_count(accepted, block_tokens)
+    starts = np.zeros(max(n, 1), np.uint64)
+    counts = np.zeros(max(n, 1), np.uint32)
+    smask = np.zeros(max(n, 1), np.uint8)
+    tmask = np.zeros(max(n, 1), np.uint8)
+    pins = _c(list(fixed) or [0], np.uint32)
+    fn = ref.ref_query_score_frame if use_ref else lib.orc_query_score_frame
+    code = fn(accepted, block_tokens, budget, sink, recent, _ptr(pins), len(fixed),
+              _ptr(starts), _ptr(counts), _ptr(smask), _ptr(tmask))
+    (_ref_check if use_ref else _check)(code)
+    return starts[:n], counts[:n], smask[:n], tmask[:n]
+
+
+# ---- summaries and scores --------------------------------------------------
+
+def row_bytes(fmt: int, width: int) -> int:
+    return lib.orc_row_bytes(fmt, width)
+
+
+def page_summaries(keys: np.ndarray, fmt: int, tokens: int, width: int, page_tokens: int):
+    """Per-page (sums, means), float32 [pages][width], for one layer."""
+    pages = lib.orc_page_count(tokens, page_tokens)
+    sums = np.zeros((pages, width), np.float32)
+    means = np.zeros((pages, width), np.float32)
+    keys = np.ascontiguousarray(keys)
+    _check(lib.orc_page_summaries(_ptr(keys), fmt, tokens, width, page_tokens, _ptr(sums), _ptr(means)))
+    return sums, means
+
+
+def page_softmax_scores(means: np.ndarray, query: np.ndarray, layer_rows: Sequence[int],
+                        query_heads: int, kv_heads: int, head_dim: int, aggregation: int,
+                        score_mask: Optional[np.ndarray] = None, scale: float = 0.0) -> np.ndarray:
+    """means [L][P][Hkv*D] float32; query [L][R][Hq][D] float32 -> double [P]."""
+    means = _c(means, np.float32)
+    query = _c(query, np.float32)
+    layers, pages = means.shape[0], means.shape[1]
+    rows = query.shape[1]
+    lr = _c(layer_rows, np.uint32)
+    out = np.zeros(pages, np.float64)
+    mask = None if score_mask is None else _c(score_mask, np.uint8)
+    _check(lib.orc_page_softmax_scores(_ptr(means), _ptr(query), _ptr(lr), layers, rows,
+                                       query_heads, kv_heads, head_dim, pages, _ptr(mask),
+                                       scale, aggregation, _ptr(out)))
+    return out
+
+
+def page_logits(means: np.ndarray, query: np.ndarray, query_heads: int, kv_heads: int,
+                head_dim: int, scale: float = 0.0) -> np.ndarray:
+    """means [P][Hkv*D]; query [R][Hq][D] -> double [R*Hq][P]."""
+    means = _c(means, np.float32)
+    query = _c(query, np.float32)
+    pages, rows = means.shape[0], query.shape[0]
+    out = np.zeros((rows * query_heads, pages), np.float64)
+    _check(lib.orc_page_logits(_ptr(means), _ptr(query), rows, query_heads, kv_heads, head_dim,
+                               pages, scale, _ptr(out)))
+    return out
+
+
+def pick_scored_blocks(scores: np.ndarray, budget: int, mandatory: Sequence[int] = (),
+                       tie_rule: int = TIE_LOWER_FIRST, signed_scores: bool = False) -> np.ndarray:
+    scores = _c(scores, np.float64)
+    n = scores.shape[0]
+    pins = _c(list(mandatory) or [0], np.uint32)
+    out = np.zeros(max(n, 1), np.uint32)
+    n_out = C.c_uint32()
+    _check(lib.orc_pick_scored_blocks(_ptr(scores), n, _ptr(pins), len(mandatory), budget,
+                                      tie_rule, int(signed_scores), _ptr(out), C.byref(n_out)))
+    return out[: n_out.value].copy()
+
+
+# ---- block formats and gather ---------------------------------------------
+
+def dequant_q8_0(block: np.ndarray) -> np.ndarray:
+    block = _c(block, np.uint8)
+    y = np.zeros(QK, np.float32)
+    lib.orc_dequant_q8_0(_ptr(block), _ptr(y))
+    return y
+
+
+def dequant_q4_1(block: np.ndarray) -> np.ndarray:
+    block = _c(block, np.uint8)
+    y = np.zeros(QK, np.float32)
+    lib.orc_dequant_q4_1(_ptr(block), _ptr(y))
+    return y
+
+
+def quant_q8_0(x: np.ndarray) -> np.ndarray:
+    x = _c(x, np.float32)
+    out = np.zeros(Q8_0_BYTES, np.uint8)
+    lib.orc_quant_q8_0(_ptr(x), _ptr(out))
+    return out
+
+
+def gather_row_bytes(src_fmt: int, mode: int, width: int) -> int:
+    return lib.orc_gather_row_bytes(src_fmt, mode, width)
+
+
+def gather(history: np.ndarray, src_fmt: int, width: int, tokens: int, page_tokens: int,
+           selected: Sequence[int], mode: int, slots: Optional[np.ndarray] = None) -> np.ndarray:
+    history = np.ascontiguousarray(history).view(np.uint8)
+    sel = _c(list(selected) or [0], np.uint32)
+    drow = gather_row_bytes(src_fmt, mode, width)
+    if slots is None:
+        slots = np.zeros(max(len(selected), 1) * page_tokens * drow, np.uint8)
+    _check(lib.orc_gather(_ptr(history), src_fmt, width, tokens, page_tokens, _ptr(sel),
+                          len(selected), mode, _ptr(slots)))
+    return slots
+
+
+# ---- synthetic inputs ------------------------------------------------------
+
+def synth_normal_f16(seed: int, stream: int, count: int) -> np.ndarray:
+    out = np.zeros(count, np.uint16)
+    lib.orc_synth_normal_f16(seed, stream, count, _ptr(out))
+    return out
+
+
+def synth_scaled_normal_f16(seed: int, stream: int, rows: int, scale: np.ndarray) -> np.ndarray:
+    scale = _c(scale, np.float32)
+    out = np.zeros(rows * scale.shape[0], np.uint16)
+    lib.orc_synth_scaled_normal_f16(seed, stream, rows, scale.shape[0], _ptr(scale), _ptr(out))
+    return out
+
+
+def synth_normal_f32(seed: int, stream: int, count: int) -> np.ndarray:
+    out = np.zeros(count, np.float32)
+    lib.orc_synth_normal_f32(seed, stream, count, _ptr(out))
+    return out
+
+
+def synth_uniform_f32(seed: int, stream: int, count: int, lo: float, hi: float) -> np.ndarray:
+    out = np.zeros(count, np.float32)
+    lib.orc_synth_uniform_f32(seed, stream, count, lo, hi, _ptr(out))
+    return out
+
+
+def synth_q8_0(seed: int, stream: int, blocks: int, d_lo: float, d_hi: float) -> np.ndarray:
+    out = np.zeros(blocks * Q8_0_BYTES, np.uint8)
+    lib.orc_synth_q8_0(seed, stream, blocks, d_lo, d_hi, _ptr(out))
+    return out
+
+
+def synth_q4_1(seed: int, stream: int, blocks: int, d_lo: float, d_hi: float, m_lo: float,
+               m_hi: float) -> np.ndarray:
+    out = np.zeros(blocks * Q4_1_BYTES, np.uint8)
+    lib.orc_synth_q4_1(seed, stream, blocks, d_lo, d_hi, m_lo, m_hi, _ptr(out))
+    return out
+
+
+def synth_normal_q8_0(seed: int, stream: int, blocks: int) -> np.ndarray:
+    out = np.zeros(blocks * Q8_0_BYTES, np.uint8)
+    lib.orc_synth_normal_q8_0(seed, stream, blocks, _ptr(out))
+    return out
+
+
+# ---- reference build (oracle/_ref) -----------------------------------------
+
+def ref_available() -> bool:
+    return ref is not None
+
+
+def ref_recall_fp16(value: float) -> float:
+    out = C.c_float()
+    _ref_check(ref.ref_recall_fp16(value, C.byref(out)))
+    return out.value
+
+
+def ref_scores_f16_keys(keys: np.ndarray, tokens: int, kv_heads: int, head_dim: int,
+                        page_tokens: int, query: np.ndarray, layer_rows: Sequence[int],
+                        query_heads: int, aggregation: int, scale: float = 0.0,
+                        score_mask: Optional[np.ndarray] = None, want_scores: bool = True):
+    """keys uint16 [L][T][Hkv*D]; query [L][R][Hq][D] -> (means [L][P][W], scores [P])."""
+    keys = _c(keys, np.uint16)
+    query = _c(query, np.float32)
+    layers, rows = keys.shape[0], query.shape[1]
+    width = kv_heads * head_dim
+    pages = (tokens + page_tokens - 1) // page_tokens
+    means = np.zeros((layers, pages, width), np.float32)
+    scores = np.zeros(pages, np.float64)
+    lr = _c(layer_rows, np.uint32)
+    mask = None if score_mask is None else _c(score_mask, np.uint8)
+    _ref_check(ref.ref_scores_f16_keys(_ptr(keys), layers, tokens, kv_heads, head_dim, page_tokens,
+                                       _ptr(query), _ptr(lr), rows, query_heads, scale, aggregation,
+                                       _ptr(mask), _ptr(means), _ptr(scores) if want_scores else None))
+    return means, scores
+
+
+def ref_scores_f32_keys(keys: np.ndarray, tokens: int, kv_heads: int, head_dim: int,
+                        page_tokens: int, query: np.ndarray, layer_rows: Sequence[int],
+                        query_heads: int, aggregation: int, scale: float = 0.0):
+    keys = _c(keys, np.float32)
+    query = _c(query, np.float32)
+    layers, rows = keys.shape[0], query.shape[1]
+    width = kv_heads * head_dim
+    pages = (tokens + page_tokens - 1) // page_tokens
+    means = np.zeros((layers, pages, width), np.float32)
+    scores = np.zeros(pages, np.float64)
+    lr = _c(layer_rows, np.uint32)
+    _ref_check(ref.ref_scores_f32_keys(_ptr(keys), layers, tokens, kv_heads, head_dim, page_tokens,
+                                       _ptr(query), _ptr(lr), rows, query_heads, scale, aggregation,
+                                       None, _ptr(means), _ptr(scores)))
+    return means, scores
+
+
+def ref_scores_from_sums(sums: np.ndarray, kv_heads: int, head_dim: int, page_tokens: int,
+                         query: np.ndarray, layer_rows: Sequence[int], query_heads: int,
+                         aggregation: int, scale: float = 0.0,
+                         score_mask: Optional[np.ndarray] = None) -> np.ndarray:
+    sums = _c(sums, np.float32)
+    query = _c(query, np.float32)
+    layers, pages = sums.shape[0], sums.shape[1]
+    rows = query.shape[1]
+    scores = np.zeros(pages, np.float64)
+    lr = _c(layer_rows, np.uint32)
+    mask = None if score_mask is None else _c(score_mask, np.uint8)
+    _ref_check(ref.ref_scores_from_sums(_ptr(sums), layers, pages, kv_heads, head_dim, page_tokens,
+                                        _ptr(query), _ptr(lr), rows, query_heads, scale,
+                                        aggregation, _ptr(mask), _ptr(scores)))
+    return scores
+
+
+def ref_layerwise_scores_f16_keys(keys: np.ndarray, layer: int, tokens: int, kv_heads: int,
+                                  head_dim: int, page_tokens: int, query: np.ndarray,
+                                  query_heads: int, scale: float = 0.0) -> np.ndarray:
+    keys = _c(keys, np.uint16)
+    query = _c(query, np.float32)
+    pages = (tokens + page_tokens - 1) // page_tokens
+    scores = np.zeros(pages, np.float64)
+    _ref_check(ref.ref_layerwise_scores_f16_keys(_ptr(keys), keys.shape[0], layer, tokens, kv_heads,
+                                                 head_dim, page_tokens, _ptr(query), query.shape[0],
+                                                 query_heads, scale, _ptr(scores)))
+    return scores
+
+
+def ref_pick_scored_blocks(scores: np.ndarray, budget: int, mandatory: Sequence[int] = (),
+                           signed_scores: bool = False) -> np.ndarray:
+    scores = _c(scores, np.float64)
+    n = scores.shape[0]
+    pins = _c(list(mandatory) or [0], np.uint32)
+    out = np.zeros(max(n, 1), np.uint32)
+    n_out = C.c_uint32()
+    _ref_check(ref.ref_pick_scored_blocks(_ptr(scores), n, _ptr(pins), len(mandatory), budget,
+                                          int(signed_scores), _ptr(out), C.byref(n_out)))
+    return out[: n_out.value].copy()

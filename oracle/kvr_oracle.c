@@ -1,0 +1,557 @@
+/*
+ * kvr_oracle.c -- CPU restatement of KVMem's recall hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY: imported by tests/, by the smoke entry point and
+ * by the benchmark's CPU-baseline leg, never by the product library.
+ *
+ * Build with plain `gcc -O2 -std=c99` for x86-64 WITHOUT -mfma / -march=native:
+ * the reference is compiled the same way, so `a*b + c` stays two roundings.
+ * Reference citations are relative to the KVMem 0.19.0 source tree.
+ */
+#include "kvr_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---------------------------------------------------------------------- */
+/* IEEE binary32 <-> binary16, round to nearest even.                       */
+/* Restates f32_to_f16 / f16_to_f32 (kvmem/src/host/raw_kv_store.cpp:43-104) */
+/* ---------------------------------------------------------------------- */
+uint16_t orc_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    const uint32_t biased = (x >> 23) & 0xffu;
+    uint32_t mant = x & 0x7fffffu;
+    if (biased == 0xffu) /* inf stays inf, NaN becomes a quiet NaN */
+        return (uint16_t)(sign | 0x7c00u | (mant ? 0x200u : 0u));
+    if ((x & 0x7fffffffu) == 0) return sign;
+    const int e = (int)biased - 127 + 15; /* binary16 biased exponent */
+    if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+    if (e <= 0) {
+        /* binary16 subnormal: value / 2^-24 rounded to an integer */
+        if (e < -10) return sign;
+        mant |= 0x800000u;
+        const uint32_t shift = (uint32_t)(14 - e);
+        uint32_t q = mant >> shift;
+        const uint32_t rest = mant & ((1u << shift) - 1u);
+        const uint32_t half = 1u << (shift - 1);
+        if (rest > half || (rest == half && (q & 1u))) q += 1;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t h = ((uint32_t)e << 10) | (mant >> 13);
+    const uint32_t rest = mant & 0x1fffu;
+    if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) h += 1; /* may carry into inf */
+    return (uint16_t)(sign | h);
+}
+
+float orc_f16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1fu;
+    const uint32_t m = h & 0x3ffu;
+    uint32_t bits;
+    if (e == 0x1f) {
+        bits = sign | 0x7f800000u | (m << 13);
+    } else if (e != 0) {
+        bits = sign | ((e + 112u) << 23) | (m << 13);
+    } else if (m == 0) {
+        bits = sign;
+    } else {
+        /* subnormal: m * 2^-24 is exact in binary32 */
+        float v = (float)m * 5.9604644775390625e-08f;
+        memcpy(&bits, &v, 4);
+        bits |= sign;
+    }
+    float out;
+    memcpy(&out, &bits, 4);
+    return out;
+}
+
+/* The fp16 operand boundary: graph_recall.cpp:295-320 (recall_fp16).
+ * Non-finite input and values that round to fp16 infinity are rejected. */
+int orc_recall_fp16(float value, float *out) {
+    if (!isfinite(value)) return ORC_ERR_NONFINITE;
+    const uint16_t h = orc_f32_to_f16(value);
+    if ((h & 0x7fffu) == 0x7c00u) return ORC_ERR_RANGE;
+    *out = orc_f16_to_f32(h);
+    return ORC_OK;
+}
+
+/* ---------------------------------------------------------------------- */
+/* Score frame: graph_recall.cpp:269-293 (query_score_frame).               */
+/* ---------------------------------------------------------------------- */
+uint32_t orc_page_count(uint64_t accepted, uint32_t block_tokens) {
+    if (!block_tokens) return 0;
+    return (uint32_t)(accepted / block_tokens + (accepted % block_tokens != 0));
+}
+
+int orc_query_score_frame(uint64_t accepted, uint32_t block_tokens, uint32_t budget,
+                          uint32_t sink, uint32_t recent, const uint32_t *fixed,
+                          uint32_t n_fixed, uint64_t *starts, uint32_t *counts,
+                          uint8_t *score_mask, uint8_t *transport_mask) {
+    if (!block_tokens || !budget) return ORC_ERR_ARG;
+    const uint64_t n64 = accepted / block_tokens + (accepted % block_tokens != 0);
+    if (n64 > 0xffffffffull) return ORC_ERR_ARG;
+    const uint32_t n = (uint32_t)n64;
+    for (uint32_t i = 0; i < n; ++i) {
+        const uint64_t start = (uint64_t)i * block_tokens;
+        const uint64_t left = accepted - start;
+        starts[i] = start;
+        counts[i] = (uint32_t)(left < block_tokens ? left : block_tokens);
+        score_mask[i] = 1;
+        transport_mask[i] = n > budget;
+    }
+    if (n > budget && (uint64_t)sink + recent < n) {
+        const uint32_t s = sink < n ? sink : n, r = recent < n ? recent : n;
+        for (uint32_t i = 0; i < s; ++i) score_mask[i] = 0;
+        for (uint32_t i = n - r; i < n; ++i) score_mask[i] = 0;
+    }
+    for (uint32_t i = 0; i < n_fixed; ++i) {
+        if (fixed[i] >= n) return ORC_ERR_ARG;
+        transport_mask[fixed[i]] = 0;
+    }
+    return ORC_OK;
+}
+
+/* ---------------------------------------------------------------------- */
+/* Block formats.                                                           */
+/* q8_0 dequant/quant: src/adapter/llama-kvmem-stagein.cu:19-29, 133-143,   */
+/* 181-199.  q4_1 ({d, m, 16 nibble bytes}; low nibble -> j, high -> j+16)  */
+/* is ggml's layout (third party, un-vendored); the nibble order matches    */
+/* the reference's q4_0 kernel (stagein.cu:145-158).                        */
+/* ---------------------------------------------------------------------- */
+static uint16_t load_u16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+static void store_u16(uint8_t *p, uint16_t v) { p[0] = (uint8_t)v; p[1] = (uint8_t)(v >> 8); }
+
+void orc_dequant_q8_0(const uint8_t *block, float *y) {
+    const float d = orc_f16_to_f32(load_u16(block));
+    const int8_t *qs = (const int8_t *)(block + 2);
+    for (int j = 0; j < ORC_QK; ++j) y[j] = (float)qs[j] * d;
+}
+
+void orc_dequant_q4_1(const uint8_t *block, float *y) {
+    const float d = orc_f16_to_f32(load_u16(block));
+    const float m = orc_f16_to_f32(load_u16(block + 2));
+    const uint8_t *qs = block + 4;
+    for (int j = 0; j < ORC_QK / 2; ++j) {
+        const float lo = (float)(qs[j] & 15) * d;
+        const float hi = (float)(qs[j] >> 4) * d;
+        y[j] = lo + m;
+        y[j + ORC_QK / 2] = hi + m;
+    }
+}
+
+void orc_quant_q8_0(const float *x, uint8_t *block) {
+    float amax = 0.0f;
+    for (int j = 0; j < ORC_QK; ++j) amax = fmaxf(amax, fabsf(x[j]));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    store_u16(block, orc_f32_to_f16(d));
+    int8_t *qs = (int8_t *)(block + 2);
+    for (int j = 0; j < ORC_QK; ++j) qs[j] = (int8_t)roundf(x[j] * id);
+}
+
+size_t orc_row_bytes(int fmt, uint32_t width) {
+    switch (fmt) {
+    case ORC_FMT_F16: return (size_t)width * 2;
+    case ORC_FMT_Q8_0: return width % ORC_QK ? 0 : (size_t)width / ORC_QK * ORC_Q8_0_BYTES;
+    case ORC_FMT_Q4_1: return width % ORC_QK ? 0 : (size_t)width / ORC_QK * ORC_Q4_1_BYTES;
+    default: return 0;
+    }
+}
+
+/* Decode one token row of `width` channels to binary32. */
+static void decode_row(const uint8_t *row, int fmt, uint32_t width, float *out) {
+    if (fmt == ORC_FMT_F16) {
+        for (uint32_t c = 0; c < width; ++c) out[c] = orc_f16_to_f32(load_u16(row + 2 * c));
+    } else if (fmt == ORC_FMT_Q8_0) {
+        for (uint32_t b = 0; b < width / ORC_QK; ++b)
+            orc_dequant_q8_0(row + (size_t)b * ORC_Q8_0_BYTES, out + (size_t)b * ORC_QK);
+    } else {
+        for (uint32_t b = 0; b < width / ORC_QK; ++b)
+            orc_dequant_q4_1(row + (size_t)b * ORC_Q4_1_BYTES, out + (size_t)b * ORC_QK);
+    }
+}
+
+/* ---------------------------------------------------------------------- */
+/* Page summaries: per channel a binary32 running sum over the page's      */
+/* tokens in token order starting from zero, then sum * (1.0f / n).        */
+/* RawKvStore::capture_mean_f16 / add_mean_f32 (raw_kv_store.cpp:158-197)  */
+/* and RawKvStore::mean_k (raw_kv_store.cpp:606-625).                      */
+/* ---------------------------------------------------------------------- */
+int orc_page_summaries(const void *keys, int fmt, uint64_t tokens, uint32_t width,
+                       uint32_t page_tokens, float *sums, float *means) {
+    const size_t row = orc_row_bytes(fmt, width);
+    if (!row || !page_tokens || !width) return ORC_ERR_ARG;
+    const uint32_t pages = orc_page_count(tokens, page_tokens);
+    float *value = (float *)malloc(sizeof(float) * width);
+    float *sum = (float *)malloc(sizeof(float) * width);
+    if (!value || !sum) { free(value); free(sum); return ORC_ERR_ARG; }
+    for (uint32_t p = 0; p < pages; ++p) {
+        const uint64_t start = (uint64_t)p * page_tokens;
+        const uint32_t n = (uint32_t)(tokens - start < page_tokens ? tokens - start : page_tokens);
+        for (uint32_t c = 0; c < width; ++c) sum[c] = 0.0f;
+        for (uint32_t t = 0; t < n; ++t) {
+            decode_row((const uint8_t *)keys + (start + t) * row, fmt, width, value);
+            for (uint32_t c = 0; c < width; ++c) sum[c] += value[c];
+        }
+        const float inv = 1.0f / (float)n;
+        for (uint32_t c = 0; c < width; ++c) {
+            if (sums) sums[(size_t)p * width + c] = sum[c];
+            if (means) means[(size_t)p * width + c] = sum[c] * inv;
+        }
+    }
+    free(value);
+    free(sum);
+    return ORC_OK;
+}
+
+/* ---------------------------------------------------------------------- */
+/* Page softmax scoring: graph_recall.cpp:322-394 (page_softmax_scores).    */
+/*   logit_j = scale * sum_d fp16(q_d) * fp16(mean_{j,d})  (double, d order) */
+/*   Mean: out_j += p_j / (A * Hq)                                          */
+/*   Max:  out_j += gmax_j / sum_j gmax_j / (A * Hkv), gmax = max over the   */
+/*         group's head probabilities                                       */
+/*   MaxLogit (literal "max of logits, then softmax" variant):               */
+/*         out_j += softmax_j(max_{h in g} logit_{h,j}) / (A * Hkv)          */
+/* Rows of all active layers are summed.  Pages outside score_mask get 0 and */
+/* stay out of every denominator.                                           */
+/* ---------------------------------------------------------------------- */
+static double page_scale(float attention_scale, uint32_t head_dim) {
+    return attention_scale > 0 ? (double)attention_scale : 1 / sqrt((double)head_dim);
+}
+
+int orc_page_softmax_scores(const float *means, const float *query,
+                            const uint32_t *layer_rows, uint32_t layers, uint32_t rows,
+                            uint32_t query_heads, uint32_t kv_heads, uint32_t head_dim,
+                            uint32_t pages, const uint8_t *score_mask,
+                            float attention_scale, int aggregation, double *out) {
+    if (!means || !query || !layer_rows || !layers || !rows || !query_heads || !kv_heads ||
+        !head_dim || query_heads % kv_heads || !out ||
+        (aggregation != ORC_AGG_MEAN && aggregation != ORC_AGG_MAX &&
+         aggregation != ORC_AGG_MAX_LOGIT))
+        return ORC_ERR_ARG;
+    for (uint32_t j = 0; j < pages; ++j) out[j] = 0;
+    uint32_t active = 0;
+    for (uint32_t l = 0; l < layers; ++l) {
+        if (layer_rows[l] > rows) return ORC_ERR_ARG;
+        active += layer_rows[l] != 0;
+    }
+    uint32_t n = 0;
+    uint32_t *enabled = (uint32_t *)malloc(sizeof(uint32_t) * (pages ? pages : 1));
+    for (uint32_t j = 0; j < pages; ++j)
+        if (!score_mask || score_mask[j]) enabled[n++] = j;
+    if (!n || !active) { free(enabled); return ORC_OK; }
+
+    const size_t kw = (size_t)kv_heads * head_dim, qw = (size_t)query_heads * head_dim;
+    const uint32_t group = query_heads / kv_heads;
+    float *m16 = (float *)malloc(sizeof(float) * n * kw);
+    float *q16 = (float *)malloc(sizeof(float) * head_dim);
+    double *logit = (double *)malloc(sizeof(double) * n);
+    double *gmax = (double *)malloc(sizeof(double) * n);
+    const double scale = page_scale(attention_scale, head_dim);
+    int status = ORC_OK;
+
+    for (uint32_t l = 0; l < layers && status == ORC_OK; ++l) {
+        if (!layer_rows[l]) continue;
+        for (uint32_t j = 0; j < n && status == ORC_OK; ++j)
+            for (size_t d = 0; d < kw && status == ORC_OK; ++d)
+                status = orc_recall_fp16(means[((size_t)l * pages + enabled[j]) * kw + d],
+                                         &m16[(size_t)j * kw + d]);
+        for (uint32_t t = 0; t < layer_rows[l] && status == ORC_OK; ++t) {
+            for (uint32_t h = 0; h < query_heads && status == ORC_OK; ++h) {
+                const uint32_t g = h / group;
+                const float *qrow = query + ((size_t)l * rows + t) * qw + (size_t)h * head_dim;
+                for (uint32_t d = 0; d < head_dim && status == ORC_OK; ++d)
+                    status = orc_recall_fp16(qrow[d], &q16[d]);
+                if (status != ORC_OK) break;
+                double maximum = -INFINITY;
+                for (uint32_t j = 0; j < n; ++j) {
+                    double dot = 0;
+                    const float *mrow = m16 + (size_t)j * kw + (size_t)g * head_dim;
+                    for (uint32_t d = 0; d < head_dim; ++d) dot += (double)q16[d] * mrow[d];
+                    logit[j] = dot * scale;
+                    if (logit[j] > maximum) maximum = logit[j];
+                }
+                if (aggregation == ORC_AGG_MAX_LOGIT) {
+                    /* running max of logits across the group's heads */
+                    for (uint32_t j = 0; j < n; ++j)
+                        gmax[j] = (h % group == 0 || logit[j] > gmax[j]) ? logit[j] : gmax[j];
+                    if (h % group != group - 1) continue;
+                    double gm = -INFINITY, denom = 0;
+                    for (uint32_t j = 0; j < n; ++j) gm = gmax[j] > gm ? gmax[j] : gm;
+                    for (uint32_t j = 0; j < n; ++j) denom += gmax[j] = exp(gmax[j] - gm);
+                    for (uint32_t j = 0; j < n; ++j)
+                        out[enabled[j]] += gmax[j] / denom / ((double)active * kv_heads);
+                    continue;
+                }
+                double denom = 0;
+                for (uint32_t j = 0; j < n; ++j) denom += logit[j] = exp(logit[j] - maximum);
+                if (aggregation == ORC_AGG_MEAN) {
+                    for (uint32_t j = 0; j < n; ++j)
+                        out[enabled[j]] += logit[j] / denom / ((double)active * query_heads);
+                } else {
+                    if (h % group == 0)
+                        for (uint32_t j = 0; j < n; ++j) gmax[j] = 0.0;
+                    for (uint32_t j = 0; j < n; ++j) {
+                        const double p = logit[j] / denom;
+                        gmax[j] = p > gmax[j] ? p : gmax[j];
+                    }
+                    if (h % group == group - 1) {
+                        double mass = 0;
+                        for (uint32_t j = 0; j < n; ++j) mass += gmax[j];
+                        for (uint32_t j = 0; j < n; ++j)
+                            out[enabled[j]] += gmax[j] / mass / ((double)active * kv_heads);
+                    }
+                }
+            }
+        }
+    }
+    free(enabled); free(m16); free(q16); free(logit); free(gmax);
+    if (status != ORC_OK)
+        for (uint32_t j = 0; j < pages; ++j) out[j] = 0;
+    return status;
+}
+
+/* Single-layer logits of every page (no mask, no softmax), double, with the
+ * same operand rounding and dot order as orc_page_softmax_scores.
+ * logits[(r * Hq + h) * pages + j]. */
+int orc_page_logits(const float *means, const float *query, uint32_t rows,
+                    uint32_t query_heads, uint32_t kv_heads, uint32_t head_dim,
+                    uint32_t pages, float attention_scale, double *logits) {
+    if (!means || !query || !rows || !query_heads || !kv_heads || !head_dim ||
+        query_heads % kv_heads || !logits)
+        return ORC_ERR_ARG;
+    const size_t kw = (size_t)kv_heads * head_dim;
+    const uint32_t group = query_heads / kv_heads;
+    const double scale = page_scale(attention_scale, head_dim);
+    for (uint32_t r = 0; r < rows; ++r)
+        for (uint32_t h = 0; h < query_heads; ++h)
+            for (uint32_t j = 0; j < pages; ++j) {
+                double dot = 0;
+                for (uint32_t d = 0; d < head_dim; ++d) {
+                    float qv, mv;
+                    int s = orc_recall_fp16(query[((size_t)r * query_heads + h) * head_dim + d], &qv);
+                    if (s) return s;
+                    s = orc_recall_fp16(means[(size_t)j * kw + (size_t)(h / group) * head_dim + d], &mv);
+                    if (s) return s;
+                    dot += (double)qv * mv;
+                }
+                logits[((size_t)r * query_heads + h) * pages + j] = dot * scale;
+            }
+    return ORC_OK;
+}
+
+/* ---------------------------------------------------------------------- */
+/* Top-k: KvMemStore::pick_scored_blocks (kvmem_store.cpp:418-451) with     */
+/* every page a candidate and no media groups.  Mandatory pages are kept    */
+/* first; the rest ranked by (score desc, page id by tie rule) fill the     */
+/* budget.  The reference's rule is HIGHER_FIRST (kvmem_store.cpp:444-446). */
+/* Output ascending ids.                                                    */
+/* ---------------------------------------------------------------------- */
+static int ranks_before(const double *s, uint32_t a, uint32_t b, int tie_rule) {
+    if (s[a] != s[b]) return s[a] > s[b];
+    return tie_rule == ORC_TIE_HIGHER_FIRST ? a > b : a < b;
+}
+
+static void rank_sort(uint32_t *ids, uint32_t *tmp, uint32_t n, const double *s, int tie) {
+    if (n < 2) return;
+    const uint32_t h = n / 2;
+    rank_sort(ids, tmp, h, s, tie);
+    rank_sort(ids + h, tmp, n - h, s, tie);
+    uint32_t i = 0, j = h, o = 0;
+    while (i < h && j < n) tmp[o++] = ranks_before(s, ids[j], ids[i], tie) ? ids[j++] : ids[i++];
+    while (i < h) tmp[o++] = ids[i++];
+    while (j < n) tmp[o++] = ids[j++];
+    memcpy(ids, tmp, sizeof(uint32_t) * n);
+}
+
+int orc_pick_scored_blocks(const double *scores, uint32_t n, const uint32_t *mandatory,
+                           uint32_t n_mandatory, uint32_t budget, int tie_rule,
+                           int signed_scores, uint32_t *out, uint32_t *n_out) {
+    *n_out = 0;
+    if (!budget || (n && !scores)) return ORC_ERR_ARG;
+    for (uint32_t i = 0; i < n; ++i)
+        if (!isfinite(scores[i]) || (!signed_scores && scores[i] < 0)) return ORC_ERR_ARG;
+    uint8_t *kept = (uint8_t *)calloc(n ? n : 1, 1);
+    uint32_t count = 0;
+    for (uint32_t i = 0; i < n_mandatory; ++i) {
+        const uint32_t id = mandatory[i];
+        if (id >= n) { free(kept); return ORC_ERR_ARG; }
+        if (kept[id]) continue;
+        if (count + 1 > budget) { free(kept); return ORC_ERR_BUDGET; }
+        kept[id] = 1;
+        ++count;
+    }
+    uint32_t *ids = (uint32_t *)malloc(sizeof(uint32_t) * (n ? n : 1));
+    uint32_t *tmp = (uint32_t *)malloc(sizeof(uint32_t) * (n ? n : 1));
+    for (uint32_t i = 0; i < n; ++i) ids[i] = i;
+    rank_sort(ids, tmp, n, scores, tie_rule);
+    for (uint32_t i = 0; i < n && count < budget; ++i)
+        if (!kept[ids[i]]) { kept[ids[i]] = 1; ++count; }
+    uint32_t o = 0;
+    for (uint32_t i = 0; i < n; ++i)
+        if (kept[i]) out[o++] = i;
+    *n_out = o;
+    free(kept); free(ids); free(tmp);
+    return ORC_OK;
+}
+
+/* ---------------------------------------------------------------------- */
+/* Gather: the selected pages' token rows, ascending page order, into       */
+/* consecutive slot rows: slot i holds page selected[i] at rows             */
+/* [i*page_tokens, i*page_tokens + valid).  Rows past a short last page are */
+/* left untouched.  write_block_to_gpu (llama-memory-kvmem.cpp:4464-4520)   */
+/* addresses cell0 = slot * block_tokens and copies valid rows per plane.   */
+/*   COPY          bytes unchanged (the reference product path)              */
+/*   DEQUANT_F16   decode to binary32, then RNE to binary16                  */
+/*   REQUANT_Q8_0  q8_0 -> binary32 -> q8_0 (quant_q8_0, stagein.cu:181-199) */
+/* ---------------------------------------------------------------------- */
+size_t orc_gather_row_bytes(int src_fmt, int mode, uint32_t width) {
+    if (mode == ORC_GATHER_COPY) return orc_row_bytes(src_fmt, width);
+    if (mode == ORC_GATHER_DEQUANT_F16) return orc_row_bytes(src_fmt, width) ? (size_t)width * 2 : 0;
+    if (mode == ORC_GATHER_REQUANT_Q8_0 && src_fmt == ORC_FMT_Q8_0)
+        return orc_row_bytes(ORC_FMT_Q8_0, width);
+    return 0;
+}
+
+int orc_gather(const uint8_t *history, int src_fmt, uint32_t width, uint64_t tokens,
+               uint32_t page_tokens, const uint32_t *selected, uint32_t k, int mode,
+               uint8_t *slots) {
+    const size_t srow = orc_row_bytes(src_fmt, width);
+    const size_t drow = orc_gather_row_bytes(src_fmt, mode, width);
+    if (!srow || !drow || !page_tokens) return ORC_ERR_ARG;
+    const uint32_t pages = orc_page_count(tokens, page_tokens);
+    for (uint32_t i = 0; i < k; ++i)
+        if (selected[i] >= pages || (i && selected[i] <= selected[i - 1])) return ORC_ERR_ARG;
+    float *row = (float *)malloc(sizeof(float) * width);
+    for (uint32_t i = 0; i < k; ++i) {
+        const uint64_t start = (uint64_t)selected[i] * page_tokens;
+        const uint32_t n = (uint32_t)(tokens - start < page_tokens ? tokens - start : page_tokens);
+        for (uint32_t t = 0; t < n; ++t) {
+            const uint8_t *src = history + (start + t) * srow;
+            uint8_t *dst = slots + ((size_t)i * page_tokens + t) * drow;
+            if (mode == ORC_GATHER_COPY) {
+                memcpy(dst, src, srow);
+                continue;
+            }
+            decode_row(src, src_fmt, width, row);
+            if (mode == ORC_GATHER_DEQUANT_F16) {
+                for (uint32_t c = 0; c < width; ++c) store_u16(dst + 2 * c, orc_f32_to_f16(row[c]));
+            } else {
+                for (uint32_t b = 0; b < width / ORC_QK; ++b)
+                    orc_quant_q8_0(row + (size_t)b * ORC_QK, dst + (size_t)b * ORC_Q8_0_BYTES);
+            }
+        }
+    }
+    free(row);
+    return ORC_OK;
+}
+
+/* ---------------------------------------------------------------------- */
+/* Seeded synthetic inputs.  Not a reference algorithm: the generator the   */
+/* device side reproduces bit for bit (integer hashing plus correctly       */
+/* rounded single operations only, no transcendental functions).            */
+/*   bits(seed, stream, c) = fmix(base(seed, stream) + (c + 1) * G)          */
+/*   normal(i): sum of 12 uniform 24-bit fractions minus 6 (Irwin-Hall:      */
+/*              mean 0, variance 1, exact in double), rounded once to fp32.  */
+/*   uniform(i): lo + u * (hi - lo) in fp32, three separate roundings.       */
+/* ---------------------------------------------------------------------- */
+#define SYN_G 0x9E3779B97F4A7C15ull
+static uint64_t fmix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+static uint64_t synth_base(uint64_t seed, uint64_t stream) {
+    return fmix64(fmix64(seed + SYN_G) ^ ((stream + 1) * 0xD1B54A32D192ED03ull));
+}
+uint64_t orc_synth_bits(uint64_t seed, uint64_t stream, uint64_t counter) {
+    return fmix64(synth_base(seed, stream) + (counter + 1) * SYN_G);
+}
+static double normal_from_base(uint64_t base, uint64_t index) {
+    int64_t total = 0;
+    for (uint64_t j = 0; j < 6; ++j) {
+        const uint64_t r = fmix64(base + (index * 6 + j + 1) * SYN_G);
+        total += (int64_t)(r >> 40) + (int64_t)((r >> 16) & 0xffffffu);
+    }
+    return (double)(total - 100663296) * 5.9604644775390625e-08; /* (S - 6*2^24) * 2^-24 */
+}
+static float unit24(uint64_t r) { return (float)(r >> 40) * 5.9604644775390625e-08f; }
+static float lerp_rn(float lo, float hi, float u) {
+    volatile float span = hi - lo;  /* volatile: three separate roundings */
+    volatile float prod = u * span;
+    return lo + prod;
+}
+double orc_synth_normal(uint64_t seed, uint64_t stream, uint64_t index) {
+    return normal_from_base(synth_base(seed, stream), index);
+}
+float orc_synth_uniform(uint64_t seed, uint64_t stream, uint64_t index, float lo, float hi) {
+    return lerp_rn(lo, hi, unit24(orc_synth_bits(seed, stream, index)));
+}
+void orc_synth_normal_f16(uint64_t seed, uint64_t stream, uint64_t count, uint16_t *out) {
+    const uint64_t base = synth_base(seed, stream);
+    for (uint64_t i = 0; i < count; ++i) out[i] = orc_f32_to_f16((float)normal_from_base(base, i));
+}
+void orc_synth_scaled_normal_f16(uint64_t seed, uint64_t stream, uint64_t rows,
+                                 uint32_t width, const float *channel_scale, uint16_t *out) {
+    const uint64_t base = synth_base(seed, stream);
+    for (uint64_t t = 0; t < rows; ++t)
+        for (uint32_t c = 0; c < width; ++c) {
+            const uint64_t i = t * width + c;
+            volatile float v = (float)normal_from_base(base, i);
+            volatile float scaled = v * channel_scale[c];
+            out[i] = orc_f32_to_f16(scaled);
+        }
+}
+void orc_synth_normal_f32(uint64_t seed, uint64_t stream, uint64_t count, float *out) {
+    const uint64_t base = synth_base(seed, stream);
+    for (uint64_t i = 0; i < count; ++i) out[i] = (float)normal_from_base(base, i);
+}
+void orc_synth_uniform_f32(uint64_t seed, uint64_t stream, uint64_t count, float lo,
+                           float hi, float *out) {
+    for (uint64_t i = 0; i < count; ++i) out[i] = orc_synth_uniform(seed, stream, i, lo, hi);
+}
+/* q8_0 block b: draws 9b..9b+7 give 32 codes (16-bit chunk % 255 - 127),   */
+/* draw 9b+8 gives the scale d ~ U(d_lo, d_hi) rounded to fp16.             */
+void orc_synth_q8_0(uint64_t seed, uint64_t stream, uint64_t blocks, float d_lo,
+                    float d_hi, uint8_t *out) {
+    const uint64_t base = synth_base(seed, stream);
+    for (uint64_t b = 0; b < blocks; ++b) {
+        uint8_t *blk = out + b * ORC_Q8_0_BYTES;
+        for (int w = 0; w < 8; ++w) {
+            const uint64_t r = fmix64(base + (b * 9 + (uint64_t)w + 1) * SYN_G);
+            for (int c = 0; c < 4; ++c)
+                blk[2 + w * 4 + c] = (uint8_t)(int8_t)((int)((r >> (16 * c)) & 0xffffu) % 255 - 127);
+        }
+        const uint64_t r = fmix64(base + (b * 9 + 8 + 1) * SYN_G);
+        store_u16(blk, orc_f32_to_f16(lerp_rn(d_lo, d_hi, unit24(r))));
+    }
+}
+/* q4_1 block b: draws 4b, 4b+1 give the 16 nibble bytes, 4b+2 the scale d, */
+/* 4b+3 the minimum m, each rounded to fp16.                                */
+void orc_synth_q4_1(uint64_t seed, uint64_t stream, uint64_t blocks, float d_lo,
+                    float d_hi, float m_lo, float m_hi, uint8_t *out) {
+    const uint64_t base = synth_base(seed, stream);
+    for (uint64_t b = 0; b < blocks; ++b) {
+        uint8_t *blk = out + b * ORC_Q4_1_BYTES;
+        for (int w = 0; w < 2; ++w) {
+            const uint64_t r = fmix64(base + (b * 4 + (uint64_t)w + 1) * SYN_G);
+            for (int c = 0; c < 8; ++c) blk[4 + w * 8 + c] = (uint8_t)(r >> (8 * c));
+        }
+        const uint64_t rd = fmix64(base + (b * 4 + 2 + 1) * SYN_G);
+        const uint64_t rm = fmix64(base + (b * 4 + 3 + 1) * SYN_G);
+        store_u16(blk, orc_f32_to_f16(lerp_rn(d_lo, d_hi, unit24(rd))));
+        store_u16(blk + 2, orc_f32_to_f16(lerp_rn(m_lo, m_hi, unit24(rm))));
+    }
+}
+/* q8_0 of N(0,1): values normal(32b + j) quantized with orc_quant_q8_0. */
+void orc_synth_normal_q8_0(uint64_t seed, uint64_t stream, uint64_t blocks, uint8_t *out) {
+    const uint64_t base = synth_base(seed, stream);
+    float x[ORC_QK];
+    for (uint64_t b = 0; b < blocks; ++b) {
+        for (int j = 0; j < ORC_QK; ++j) x[j] = (float)normal_from_base(base, b * ORC_QK + (uint64_t)j);
+        orc_quant_q8_0(x, out + b * ORC_Q8_0_BYTES);
+    }
+}

@@ -1,0 +1,122 @@
+/*
+ * kvr_oracle.h -- CPU restatement of KVMem's recall hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product library links, loads or
+ * calls this code.  It is the checker that tests/, the smoke entry point and
+ * the CPU-baseline leg of the benchmark compare the HIP path against.
+ *
+ * Plain C99, single-threaded, double accumulation exactly where the reference
+ * uses double.  Every function names the reference file:line it restates
+ * (paths relative to the KVMem 0.19.0 source tree).
+ *
+ * Parity pinning (what checks each function, besides the reference build in
+ * oracle/_ref when that is present):
+ *   orc_f32_to_f16 / orc_f16_to_f32  exhaustive fp16 round trip + RNE midpoints
+ *   orc_recall_fp16                  graph_recall_test.cpp:57-61 known answers
+ *   orc_query_score_frame            graph_recall_test.cpp:23-31 known answers
+ *   orc_page_summary_*               sequential-sum closed form (integers, exact)
+ *   orc_page_softmax_scores (Mean)   graph_recall_test.cpp:22-56, 63-84 closed forms
+ *   orc_page_softmax_scores (Max)    graph_recall_test.cpp:85-96 closed form
+ *   orc_page_softmax_scores (MaxLogit, the literal max-of-logits variant)
+ *                                    closed form on a two-page example
+ *   orc_pick_scored_blocks           brute force on tiny inputs +
+ *                                    layerwise_selection_test.cpp:184-194 ties
+ *   orc_dequant_q8_0 / orc_quant_q8_0 exact-product closed form, stagein.cu formulas
+ *   orc_dequant_q4_1                 closed form y = nib*d + m (ggml q4_1 layout;
+ *                                    no reference test holds q4_1 bytes)
+ *   orc_synth_*                      not a reference algorithm: the shared
+ *                                    seeded input generator (moments checked)
+ */
+#ifndef KVR_ORACLE_H
+#define KVR_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    ORC_OK = 0,
+    ORC_ERR_ARG = 1,       /* invalid geometry or argument            */
+    ORC_ERR_NONFINITE = 2, /* recall operand is NaN or infinite        */
+    ORC_ERR_RANGE = 3,     /* recall operand rounds to fp16 infinity   */
+    ORC_ERR_BUDGET = 4     /* mandatory pages exceed the budget        */
+};
+
+enum { ORC_AGG_MEAN = 0, ORC_AGG_MAX = 1, ORC_AGG_MAX_LOGIT = 2 };
+enum { ORC_TIE_LOWER_FIRST = 0, ORC_TIE_HIGHER_FIRST = 1 };
+
+/* History formats: token-major rows of `width` channels. */
+enum { ORC_FMT_F16 = 0, ORC_FMT_Q8_0 = 1, ORC_FMT_Q4_1 = 2 };
+/* Gather modes. */
+enum { ORC_GATHER_COPY = 0, ORC_GATHER_DEQUANT_F16 = 1, ORC_GATHER_REQUANT_Q8_0 = 2 };
+
+#define ORC_QK 32
+#define ORC_Q8_0_BYTES 34 /* {fp16 d; int8 qs[32]}            */
+#define ORC_Q4_1_BYTES 20 /* {fp16 d; fp16 m; uint8 qs[16]}   */
+
+/* ---- scalar conversions ------------------------------------------------ */
+uint16_t orc_f32_to_f16(float f);
+float orc_f16_to_f32(uint16_t h);
+int orc_recall_fp16(float value, float *out);
+
+/* ---- frame -------------------------------------------------------------- */
+uint32_t orc_page_count(uint64_t accepted, uint32_t block_tokens);
+int orc_query_score_frame(uint64_t accepted, uint32_t block_tokens, uint32_t budget,
+                          uint32_t sink, uint32_t recent, const uint32_t *fixed,
+                          uint32_t n_fixed, uint64_t *starts, uint32_t *counts,
+                          uint8_t *score_mask, uint8_t *transport_mask);
+
+/* ---- page summaries (mean-K) ------------------------------------------- */
+size_t orc_row_bytes(int fmt, uint32_t width);
+int orc_page_summaries(const void *keys, int fmt, uint64_t tokens, uint32_t width,
+                       uint32_t page_tokens, float *sums, float *means);
+
+/* ---- scoring ----------------------------------------------------------- */
+int orc_page_softmax_scores(const float *means, const float *query,
+                            const uint32_t *layer_rows, uint32_t layers, uint32_t rows,
+                            uint32_t query_heads, uint32_t kv_heads, uint32_t head_dim,
+                            uint32_t pages, const uint8_t *score_mask,
+                            float attention_scale, int aggregation, double *out);
+int orc_page_logits(const float *means, const float *query, uint32_t rows,
+                    uint32_t query_heads, uint32_t kv_heads, uint32_t head_dim,
+                    uint32_t pages, float attention_scale, double *logits);
+
+/* ---- selection ---------------------------------------------------------- */
+int orc_pick_scored_blocks(const double *scores, uint32_t n, const uint32_t *mandatory,
+                           uint32_t n_mandatory, uint32_t budget, int tie_rule,
+                           int signed_scores, uint32_t *out, uint32_t *n_out);
+
+/* ---- block formats ------------------------------------------------------ */
+void orc_dequant_q8_0(const uint8_t *block, float *y);
+void orc_dequant_q4_1(const uint8_t *block, float *y);
+void orc_quant_q8_0(const float *x, uint8_t *block);
+
+/* ---- gather ------------------------------------------------------------- */
+size_t orc_gather_row_bytes(int src_fmt, int mode, uint32_t width);
+int orc_gather(const uint8_t *history, int src_fmt, uint32_t width, uint64_t tokens,
+               uint32_t page_tokens, const uint32_t *selected, uint32_t k, int mode,
+               uint8_t *slots);
+
+/* ---- seeded synthetic inputs (shared with the device generator) ------- */
+uint64_t orc_synth_bits(uint64_t seed, uint64_t stream, uint64_t counter);
+double orc_synth_normal(uint64_t seed, uint64_t stream, uint64_t index);
+float orc_synth_uniform(uint64_t seed, uint64_t stream, uint64_t index, float lo, float hi);
+void orc_synth_normal_f16(uint64_t seed, uint64_t stream, uint64_t count, uint16_t *out);
+void orc_synth_scaled_normal_f16(uint64_t seed, uint64_t stream, uint64_t rows,
+                                 uint32_t width, const float *channel_scale, uint16_t *out);
+void orc_synth_normal_f32(uint64_t seed, uint64_t stream, uint64_t count, float *out);
+void orc_synth_uniform_f32(uint64_t seed, uint64_t stream, uint64_t count, float lo,
+                           float hi, float *out);
+void orc_synth_q8_0(uint64_t seed, uint64_t stream, uint64_t blocks, float d_lo,
+                    float d_hi, uint8_t *out);
+void orc_synth_q4_1(uint64_t seed, uint64_t stream, uint64_t blocks, float d_lo,
+                    float d_hi, float m_lo, float m_hi, uint8_t *out);
+void orc_synth_normal_q8_0(uint64_t seed, uint64_t stream, uint64_t blocks, uint8_t *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

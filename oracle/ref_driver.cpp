@@ -1,0 +1,244 @@
+// ref_driver.cpp -- extern "C" entry points over the KVMem reference host
+// library, compiled from the reference's own sources into oracle/_ref.
+//
+// TEST INFRASTRUCTURE ONLY.  This file is this project's own glue code; it
+// includes the reference's public headers at build time (the include path is
+// given by oracle/Makefile) and is never part of the product library.
+// It lets tests, the fixture generator and the CPU-baseline leg of the
+// benchmark call the reference's real functions:
+//   RawKvStore::write_layer_tokens_f16 / write_layer_mean_k / mean_k
+//                                     (kvmem/src/host/raw_kv_store.cpp)
+//   query_score_frame, recall_fp16, page_softmax_scores
+//                                     (kvmem/src/host/graph_recall.cpp)
+//   KvMemStore::pick_scored_blocks    (kvmem/src/host/kvmem_store.cpp)
+//   layerwise_mean_key_scores         (kvmem/src/host/layerwise_scoring.cpp)
+// Exceptions never cross this boundary: each entry returns 0 on success and a
+// nonzero code on a thrown exception, with the message in ref_last_error().
+#include "kvmem/graph_recall.hpp"
+#include "kvmem/kvmem_store.hpp"
+#include "kvmem/layerwise_scoring.hpp"
+#include "kvmem/raw_kv_store.hpp"
+
+#include <cstring>
+#include <exception>
+#include <memory>
+#include <numeric>
+#include <string>
+#include <vector>
+
+namespace {
+thread_local std::string g_error;
+
+template <class F> int guarded(F&& body) {
+    try {
+        body();
+        return 0;
+    } catch (const std::exception& e) {
+        g_error = e.what();
+        return 1;
+    } catch (...) {
+        g_error = "unknown exception";
+        return 1;
+    }
+}
+
+kvmem::GqaScoreAggregation aggregation(int agg) {
+    return agg == 1 ? kvmem::GqaScoreAggregation::Max : kvmem::GqaScoreAggregation::Mean;
+}
+
+// A store whose layer l holds token-major fp16 keys [tokens][width] in blocks
+// of page_tokens, written the way the capture path writes fp16 K.
+std::unique_ptr<kvmem::RawKvStore> store_from_f16(const uint16_t* keys, uint32_t layers,
+                                                  uint64_t tokens, uint32_t width,
+                                                  uint32_t page_tokens) {
+    kvmem::RawKvStoreConfig cfg;
+    cfg.n_layer = layers;
+    cfg.n_embd_k = width;
+    cfg.n_embd_v = 0;
+    cfg.block_tokens = page_tokens;
+    auto store = std::make_unique<kvmem::RawKvStore>(cfg);
+    for (uint32_t l = 0; l < layers; ++l)
+        store->write_layer_tokens_f16(0, uint32_t(tokens), l, keys + size_t(l) * tokens * width,
+                                      nullptr);
+    return store;
+}
+
+// A store whose layer l holds binary32 key rows, fed through the prefill
+// mean-K path (write_layer_mean_k: sequential binary32 adds).
+std::unique_ptr<kvmem::RawKvStore> store_from_f32(const float* keys, uint32_t layers,
+                                                  uint64_t tokens, uint32_t width,
+                                                  uint32_t page_tokens) {
+    kvmem::RawKvStoreConfig cfg;
+    cfg.n_layer = layers;
+    cfg.n_embd_k = width;
+    cfg.n_embd_v = 0;
+    cfg.block_tokens = page_tokens;
+    auto store = std::make_unique<kvmem::RawKvStore>(cfg);
+    for (uint32_t l = 0; l < layers; ++l)
+        store->write_layer_mean_k(0, uint32_t(tokens), l, keys + size_t(l) * tokens * width);
+    return store;
+}
+
+void scores_from_store(const kvmem::RawKvStore& store, uint64_t tokens, uint32_t page_tokens,
+                       const float* query, const uint32_t* layer_rows, uint32_t layers,
+                       uint32_t rows, uint32_t query_heads, uint32_t kv_heads,
+                       uint32_t head_dim, float scale, int agg, const uint8_t* score_mask,
+                       double* out) {
+    const uint32_t pages = uint32_t((tokens + page_tokens - 1) / page_tokens);
+    // A budget of every page disables the sink/recent bands, so every page is
+    // scored unless the caller masks it explicitly.
+    auto frame = kvmem::query_score_frame(tokens, page_tokens, pages, 0, 0, {});
+    if (score_mask)
+        for (uint32_t j = 0; j < pages; ++j) frame.score_mask[j] = score_mask[j];
+    kvmem::PageQueryView view;
+    view.data = query;
+    view.layer_rows = layer_rows;
+    view.layers = layers;
+    view.rows = rows;
+    view.query_heads = query_heads;
+    view.kv_heads = kv_heads;
+    view.head_dim = head_dim;
+    view.attention_scale = scale;
+    const auto result = kvmem::page_softmax_scores(store, view, frame, aggregation(agg));
+    std::memcpy(out, result.data(), sizeof(double) * result.size());
+}
+
+void copy_means(const kvmem::RawKvStore& store, uint32_t layers, uint32_t pages,
+                uint32_t width, float* means) {
+    if (!means) return;
+    for (uint32_t l = 0; l < layers; ++l)
+        for (uint32_t p = 0; p < pages; ++p)
+            store.mean_k(p, l, means + (size_t(l) * pages + p) * width);
+}
+}  // namespace
+
+extern "C" {
+
+const char* ref_last_error(void) { return g_error.c_str(); }
+
+int ref_recall_fp16(float value, float* out) {
+    return guarded([&] { *out = kvmem::recall_fp16(value); });
+}
+
+int ref_query_score_frame(uint64_t accepted, uint32_t block_tokens, uint32_t budget,
+                          uint32_t sink, uint32_t recent, const uint32_t* fixed,
+                          uint32_t n_fixed, uint64_t* starts, uint32_t* counts,
+                          uint8_t* score_mask, uint8_t* transport_mask) {
+    return guarded([&] {
+        std::vector<uint32_t> pins(fixed, fixed + n_fixed);
+        const auto f = kvmem::query_score_frame(accepted, block_tokens, budget, sink, recent, pins);
+        for (size_t i = 0; i < f.starts.size(); ++i) {
+            starts[i] = f.starts[i];
+            counts[i] = f.counts[i];
+            score_mask[i] = f.score_mask[i];
+            transport_mask[i] = f.transport_mask[i];
+        }
+    });
+}
+
+// Summaries (mean_k) and page-softmax scores from fp16 key history.
+// keys: [layers][tokens][kv_heads*head_dim] fp16; query: [layers][rows][Hq][D].
+int ref_scores_f16_keys(const uint16_t* keys, uint32_t layers, uint64_t tokens,
+                        uint32_t kv_heads, uint32_t head_dim, uint32_t page_tokens,
+                        const float* query, const uint32_t* layer_rows, uint32_t rows,
+                        uint32_t query_heads, float scale, int agg,
+                        const uint8_t* score_mask, float* means, double* scores) {
+    return guarded([&] {
+        const uint32_t width = kv_heads * head_dim;
+        auto store = store_from_f16(keys, layers, tokens, width, page_tokens);
+        copy_means(*store, layers, uint32_t((tokens + page_tokens - 1) / page_tokens), width,
+                   means);
+        if (scores)
+            scores_from_store(*store, tokens, page_tokens, query, layer_rows, layers, rows,
+                              query_heads, kv_heads, head_dim, scale, agg, score_mask, scores);
+    });
+}
+
+// The same from binary32 key rows through the prefill mean-K path.
+int ref_scores_f32_keys(const float* keys, uint32_t layers, uint64_t tokens,
+                        uint32_t kv_heads, uint32_t head_dim, uint32_t page_tokens,
+                        const float* query, const uint32_t* layer_rows, uint32_t rows,
+                        uint32_t query_heads, float scale, int agg,
+                        const uint8_t* score_mask, float* means, double* scores) {
+    return guarded([&] {
+        const uint32_t width = kv_heads * head_dim;
+        auto store = store_from_f32(keys, layers, tokens, width, page_tokens);
+        copy_means(*store, layers, uint32_t((tokens + page_tokens - 1) / page_tokens), width,
+                   means);
+        if (scores)
+            scores_from_store(*store, tokens, page_tokens, query, layer_rows, layers, rows,
+                              query_heads, kv_heads, head_dim, scale, agg, score_mask, scores);
+    });
+}
+
+// Page-softmax scores from per-page sums that each cover `page_tokens`
+// tokens (write_layer_mean_sum), i.e. mean = sum * (1/page_tokens).
+int ref_scores_from_sums(const float* sums, uint32_t layers, uint32_t pages,
+                         uint32_t kv_heads, uint32_t head_dim, uint32_t page_tokens,
+                         const float* query, const uint32_t* layer_rows, uint32_t rows,
+                         uint32_t query_heads, float scale, int agg,
+                         const uint8_t* score_mask, double* scores) {
+    return guarded([&] {
+        const uint32_t width = kv_heads * head_dim;
+        kvmem::RawKvStoreConfig cfg;
+        cfg.n_layer = layers;
+        cfg.n_embd_k = width;
+        cfg.block_tokens = page_tokens;
+        kvmem::RawKvStore store(cfg);
+        for (uint32_t l = 0; l < layers; ++l)
+            for (uint32_t p = 0; p < pages; ++p)
+                store.write_layer_mean_sum(p * page_tokens, page_tokens, l,
+                                           sums + (size_t(l) * pages + p) * width);
+        scores_from_store(store, uint64_t(pages) * page_tokens, page_tokens, query, layer_rows,
+                          layers, rows, query_heads, kv_heads, head_dim, scale, agg,
+                          score_mask, scores);
+    });
+}
+
+// Single-layer current-Q Mean scores (layerwise_mean_key_scores).
+int ref_layerwise_scores_f16_keys(const uint16_t* keys, uint32_t layers, uint32_t layer,
+                                  uint64_t tokens, uint32_t kv_heads, uint32_t head_dim,
+                                  uint32_t page_tokens, const float* query, uint32_t rows,
+                                  uint32_t query_heads, float scale, double* scores) {
+    return guarded([&] {
+        auto store = store_from_f16(keys, layers, tokens, kv_heads * head_dim, page_tokens);
+        const uint32_t pages = uint32_t((tokens + page_tokens - 1) / page_tokens);
+        auto frame = kvmem::query_score_frame(tokens, page_tokens, pages, 0, 0, {});
+        kvmem::CurrentLayerQuery q;
+        q.data = query;
+        q.layer = layer;
+        q.rows = rows;
+        q.query_heads = query_heads;
+        q.kv_heads = kv_heads;
+        q.head_dim = head_dim;
+        q.attention_scale = scale;
+        const auto result = kvmem::layerwise_mean_key_scores(*store, q, frame);
+        std::memcpy(scores, result.data(), sizeof(double) * result.size());
+    });
+}
+
+// KvMemStore::pick_scored_blocks over every page as a candidate.  The
+// reference's only tie rule is higher page id first.
+int ref_pick_scored_blocks(const double* scores, uint32_t n, const uint32_t* mandatory,
+                           uint32_t n_mandatory, uint32_t budget, int signed_scores,
+                           uint32_t* out, uint32_t* n_out) {
+    return guarded([&] {
+        kvmem::KvMemStoreConfig cfg;
+        cfg.block_tokens = 1;
+        cfg.select_budget = budget;
+        cfg.sink_blocks = 0;
+        cfg.recent_blocks = 0;
+        kvmem::KvMemStore store(cfg);
+        store.register_append(n);
+        std::vector<uint32_t> candidates(n);
+        std::iota(candidates.begin(), candidates.end(), 0u);
+        const std::vector<double> values(scores, scores + n);
+        const std::vector<uint32_t> pins(mandatory, mandatory + n_mandatory);
+        const auto picked =
+            store.pick_scored_blocks(candidates, values, pins, budget, signed_scores != 0);
+        std::memcpy(out, picked.data(), sizeof(uint32_t) * picked.size());
+        *n_out = uint32_t(picked.size());
+    });
+}
+
+}  // extern "C"
