@@ -15,7 +15,11 @@ constexpr int kWave = 64;
 __device__ __forceinline__ float h2f(uint16_t h) {
     return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }
+// The empty asm pins `f` as a rounded binary32 value: without it the
+// compiler may fold a producing multiply or fma into v_fma_mixlo_f16, which
+// rounds once to binary16 where the reference rounds to binary32 first.
 __device__ __forceinline__ uint16_t f2h(float f) {
+    asm volatile("" : "+v"(f));
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
@@ -110,9 +114,14 @@ __device__ __forceinline__ float synth_normal(uint64_t base, uint64_t index) {
 __device__ __forceinline__ float synth_unit24(uint64_t r) {
     return float(r >> 40) * 5.9604644775390625e-08f;
 }
-// lo + u * (hi - lo) with three separate roundings (no contraction).
+// lo + u * (hi - lo) with three separate roundings: contraction into a fused
+// multiply-add is switched off here (HIP's __fadd_rn/__fmul_rn are plain
+// operators that clang would otherwise fuse).
 __device__ __forceinline__ float synth_lerp(float lo, float hi, float u) {
-    return __fadd_rn(lo, __fmul_rn(u, __fsub_rn(hi, lo)));
+#pragma clang fp contract(off)
+    const float span = hi - lo;
+    const float prod = u * span;
+    return lo + prod;
 }
 
 }  // namespace kvr

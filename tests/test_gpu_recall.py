@@ -18,8 +18,9 @@ def _rel_err(a, b):
 
 
 def _pinned(arr):
-    p = K.PinnedBuffer(arr.size)
-    p.numpy()[:] = arr.view(np.uint8).ravel()
+    raw = np.ascontiguousarray(arr).view(np.uint8).ravel()
+    p = K.PinnedBuffer(raw.size)
+    p.numpy()[:] = raw
     return p
 
 
