@@ -139,6 +139,9 @@ def run(args):
 
     hip = Hip()
     ctx = K.Context(0)
+    ctx.set_option(K._capi.OPT_GATHER_WORKGROUPS, args.gather_wgs)
+    ctx.set_option(K._capi.OPT_GATHER_CHUNK_ROWS, args.chunk_rows)
+    ctx.set_option(K._capi.OPT_GATHER_THREADS, args.gather_threads)
     L, T, HKV, D, HQ, PT, KSEL, R = args.layers, 131072, 8, 128, 32, 256, 32, 1
     W = HKV * D
     P = T // PT
@@ -228,6 +231,23 @@ def run(args):
     log(f"step {ms_per_step:.3f} ms ({ms_per_step / L * 1e3:.1f} us/layer pipelined); "
         f"select {select_us:.1f} us/layer; summary kernel {kern_us:.1f} us")
 
+    # ---- select alone (no gather beside it) ---------------------------------
+    iso_sel, iso_kern = [], []
+    for rep in range(2):
+        for l in range(L):
+            hip.record(ev["sb"][l], sel_stream)
+            ctx.recall_layer(keys=keys[l], summaries=s16[l], query=queries[l], scores=scores[l],
+                             selected=sel[l], count=cnt[l], k=KSEL, aggregation=K.AGG_MEAN,
+                             summary_events=(ev["kb"][l], ev["ke"][l]))
+            hip.record(ev["se"][l], sel_stream)
+        ctx.check()
+        if rep:
+            iso_sel = [hip.elapsed_ms(ev["sb"][l], ev["se"][l]) for l in range(L)]
+            iso_kern = [hip.elapsed_ms(ev["kb"][l], ev["ke"][l]) for l in range(L)]
+    iso_select_us = float(np.mean(iso_sel)) * 1e3
+    iso_kern_us = float(np.mean(iso_kern)) * 1e3
+    log(f"select alone {iso_select_us:.1f} us/layer; summary kernel alone {iso_kern_us:.1f} us")
+
     # ---- stage-in alone (same selections, copy stream) ---------------------
     stage_ms = []
     a, b = hip.event(), hip.event()
@@ -277,8 +297,11 @@ def run(args):
             "query_rows": R, "page_tokens": PT, "pages": P, "top_k": KSEL,
             "aggregation": "mean", "gather": "fp16 K+V copy into 8192-token slots",
             "engine": args.engine, "pinned_layers": ring,
+            "gather_workgroups": args.gather_wgs or 64, "gather_chunk_rows": args.chunk_rows or 8,
         },
         "select_us_per_layer": round(select_us, 2),
+        "select_alone_us_per_layer": round(iso_select_us, 2),
+        "summary_kernel_alone_us": round(iso_kern_us, 2),
         "stagein_us_per_layer": round(stage_us, 2),
         "latency_us_per_layer": round(ms_per_step / L * 1e3, 2),
         "scored_frac_hbm": round(scored_gbps / HBM_PEAK_GBPS, 4),
@@ -312,6 +335,10 @@ def main():
     ap.add_argument("--layers", type=int, default=64)
     ap.add_argument("--seed", type=int, default=42)
     ap.add_argument("--engine", choices=["auto", "kernel", "sdma"], default="auto")
+    ap.add_argument("--gather-wgs", type=int, default=0, help="gather grid bound (0 = library default)")
+    ap.add_argument("--chunk-rows", type=int, default=0, help="gather rows per work item (0 = default)")
+    ap.add_argument("--gather-threads", type=int, default=0, help="gather workgroup size (0 = default)")
+    ap.add_argument("--skip-alone", action="store_true", help="skip the isolated select and stage-in passes")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     args = ap.parse_args()

@@ -172,6 +172,17 @@ kvr_status kvr_check(kvr_context *ctx, void *stream);
 void *kvr_select_stream(kvr_context *ctx);
 void *kvr_copy_stream(kvr_context *ctx);
 
+typedef enum kvr_option {
+    KVR_OPT_GATHER_WORKGROUPS = 1, /* grid bound of the device-driven gather (default 64) */
+    KVR_OPT_GATHER_CHUNK_ROWS = 2, /* token rows per gather work item (default 8, <= 64) */
+    KVR_OPT_GATHER_THREADS = 3     /* gather workgroup size: 64, 128 or 256 (default 256) */
+} kvr_option;
+
+/* Tuning knobs of a context; value 0 restores the default.  No reference
+ * counterpart (the reference's slab size and op table are compile-time
+ * constants, llama-kvmem-stagein.cu:32-33). */
+kvr_status kvr_set_option(kvr_context *ctx, kvr_option option, int64_t value);
+
 /* ---- workspace ------------------------------------------------------------ */
 
 /* Device bytes one scoring call needs for this geometry.  Replaces

@@ -159,6 +159,9 @@ class Context:
     def status(self, stream: Optional[int] = None) -> int:
         return lib().kvr_check(self.handle, stream)
 
+    def set_option(self, option: int, value: int) -> None:
+        check(lib().kvr_set_option(self.handle, option, value))
+
     # -- workspace ----------------------------------------------------------
     @staticmethod
     def workspace_bytes(lanes, pages, rows, query_heads, kv_heads, head_dim) -> int:

@@ -21,6 +21,7 @@ AGG_MEAN, AGG_MAX, AGG_MAX_LOGIT = range(3)
 TIE_LOWER_FIRST, TIE_HIGHER_FIRST = range(2)
 GATHER_COPY, GATHER_DEQUANT_F16, GATHER_REQUANT_Q8_0 = range(3)
 ENGINE_AUTO, ENGINE_KERNEL, ENGINE_SDMA = range(3)
+OPT_GATHER_WORKGROUPS, OPT_GATHER_CHUNK_ROWS, OPT_GATHER_THREADS = 1, 2, 3
 MAX_INLINE_MANDATORY = 64
 MAX_PLANES = 8
 
@@ -59,6 +60,7 @@ _SIGNATURES = {
     "kvr_last_error": (C.c_char_p, []),
     "kvr_status_string": (C.c_char_p, [_i]),
     "kvr_check": (_i, [_P, _P]),
+    "kvr_set_option": (_i, [_P, _i, C.c_int64]),
     "kvr_select_stream": (_P, [_P]),
     "kvr_copy_stream": (_P, [_P]),
     "kvr_workspace_bytes": (_sz, [_u32, _u32, _u32, _u32, _u32, _u32]),

@@ -31,11 +31,19 @@ struct kvr_context {
     kvr::CopyOp *ops_dev = nullptr, *ops_pin = nullptr;
     uint32_t ops_cap = 0;
     hipEvent_t ops_ev = nullptr;
-    // SDMA stage-in
+    // SDMA stage-in: span copies fan out over kDmaStreams streams (each can
+    // drive its own DMA engine) and join back into the copy stream.
+    hipStream_t dma[4] = {};
+    hipEvent_t dma_fork = nullptr, dma_join[4] = {};
+    hipStream_t readback = nullptr;  // selection readback, ordered only on the select event
     uint32_t *sel_pin = nullptr;
     size_t sel_pin_cap = 0;
     uint8_t *staging = nullptr;
     size_t staging_bytes = 0;
+    // tuning
+    uint32_t gather_wgs = 64;
+    uint32_t chunk_rows = 8;
+    uint32_t gather_threads = 256;
 };
 
 namespace {
@@ -75,6 +83,8 @@ struct DeviceGuard {
 };
 
 size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
+constexpr size_t kGatherLds = 65536;  // dynamic LDS bound of one gather workgroup
+constexpr int kDmaStreams = 4;
 bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 bool pow2(uint32_t v) { return v && !(v & (v - 1)); }
 
@@ -143,6 +153,11 @@ kvr::QueryArgs query_args(const kvr_query *q) {
 }
 
 bool valu_dim_ok(uint32_t dim) { return dim % 8 == 0 && pow2(dim / 8) && dim / 8 <= 64; }
+
+// Fused scoring stages the fp16 query rows in LDS when they fit 32 KiB.
+uint32_t stage_query(const kvr::QueryArgs &q) {
+    return uint64_t(q.rows) * q.qheads * q.dim * 2 <= 32768 ? 1u : 0u;
+}
 
 kvr_status ensure_workspace(kvr_context *ctx, size_t bytes) {
     if (bytes <= ctx->ws_bytes) return KVR_OK;
@@ -226,17 +241,27 @@ kvr_status enqueue_probs_and_select(kvr_context *ctx, const ScorePlan &p, const 
                                     double *scores, bool do_select, uint32_t k, kvr_tie_rule tie,
                                     const Mandatory &mand, uint32_t *selected, uint32_t *count,
                                     hipStream_t s) {
-    kvr::SoftmaxArgs sm{};
-    sm.logits = p.logits;
-    sm.mask = mask;
-    sm.lanes = p.lanes;
-    sm.rows = p.rows;
-    sm.qheads = p.qheads;
-    sm.kvheads = p.kvheads;
-    sm.pages = p.pages;
-    sm.aggregation = uint32_t(agg);
-    KVR_HIP(kvr::launch_softmax(sm, s));
+    // A lane with at most 64 softmax units (rows, or GQA groups) is softmaxed
+    // inside the select kernel (one wave per unit); larger ones get their own
+    // grid-wide softmax launch first.
+    const uint64_t units = uint64_t(p.rows) * (agg == KVR_AGG_MEAN ? p.qheads : p.kvheads);
+    const bool fuse = units <= 64;
+    if (!fuse) {
+        kvr::SoftmaxArgs sm{};
+        sm.logits = p.logits;
+        sm.mask = mask;
+        sm.lanes = p.lanes;
+        sm.rows = p.rows;
+        sm.qheads = p.qheads;
+        sm.kvheads = p.kvheads;
+        sm.pages = p.pages;
+        sm.aggregation = uint32_t(agg);
+        KVR_HIP(kvr::launch_softmax(sm, s));
+    }
     kvr::SelectArgs sa{};
+    sa.logits = p.logits;
+    sa.mask = mask;
+    sa.do_softmax = fuse;
     sa.probs = p.logits;
     sa.rows = p.rows;
     sa.qheads = p.qheads;
@@ -292,6 +317,7 @@ kvr_status enqueue_logits(kvr_context *ctx, const ScorePlan &p, const uint16_t *
         a.width = p.kvheads * p.dim;
         a.lanes = p.lanes;
         a.q = p.q;
+        a.q_stage = stage_query(p.q);
         a.logits = p.logits;
         a.status = ctx->status;
         a.epoch = ctx->epoch;
@@ -356,7 +382,7 @@ struct PlanePlan {
 };
 
 kvr_status check_planes(const kvr_plane *planes, uint32_t n, uint32_t lanes, uint32_t page_tokens,
-                        uint32_t k, PlanePlan *out) {
+                        uint32_t k, uint32_t chunk_rows, PlanePlan *out) {
     if (n > KVR_MAX_PLANES) return fail(KVR_ERR_INVALID, "at most %d planes", KVR_MAX_PLANES);
     if (n && !planes) return fail(KVR_ERR_INVALID, "missing planes");
     for (uint32_t i = 0; i < n; ++i) {
@@ -373,7 +399,8 @@ kvr_status check_planes(const kvr_plane *planes, uint32_t n, uint32_t lanes, uin
         if (!drow) return fail(KVR_ERR_UNSUPPORTED, "plane %u: gather mode not provided for this format", i);
         if (p.mode == KVR_GATHER_DEQUANT_F16 && p.format != KVR_FMT_F16 && (p.width % 32 || !aligned(p.slots, 16)))
             return fail(KVR_ERR_INVALID, "plane %u: dequantized slots must be 16-byte aligned", i);
-        if (p.format != KVR_FMT_F16 && p.mode != KVR_GATHER_COPY && srow * 8 > 32768)
+        (void)chunk_rows;
+        if (p.format != KVR_FMT_F16 && p.mode != KVR_GATHER_COPY && 2 * srow > kGatherLds)
             return fail(KVR_ERR_INVALID, "plane %u: rows too wide for the staged decoder", i);
         hipPointerAttribute_t attr{};
         if (hipPointerGetAttributes(&attr, p.history) != hipSuccess || attr.type != hipMemoryTypeHost ||
@@ -403,11 +430,21 @@ kvr_status check_planes(const kvr_plane *planes, uint32_t n, uint32_t lanes, uin
     return KVR_OK;
 }
 
-uint32_t chunk_rows_for(uint32_t page_tokens) { return std::min<uint32_t>(8, page_tokens); }
+constexpr uint32_t kDefaultGatherWgs = 64, kDefaultChunkRows = 8;
 
-kvr_status enqueue_gather_kernel(const PlanePlan *pp, uint32_t n, uint32_t lanes, uint32_t page_tokens,
-                                 const uint32_t *selected, const uint32_t *count, uint32_t k,
-                                 hipStream_t s) {
+// Rows per gather work item: the context's setting, bounded by the page and
+// by the LDS a staged decode needs (source rows + requantized rows).
+uint32_t gather_chunk_rows(const kvr_context *ctx, const PlanePlan *pp, uint32_t n, uint32_t page_tokens) {
+    uint32_t cr = std::min(ctx->chunk_rows, page_tokens);
+    for (uint32_t i = 0; i < n; ++i)
+        if (pp[i].g.mode != KVR_GATHER_COPY && pp[i].g.format != KVR_FMT_F16)
+            cr = std::min<uint32_t>(cr, uint32_t(kGatherLds / (2 * size_t(pp[i].g.src_row))));
+    return std::max<uint32_t>(cr, 1);
+}
+
+kvr_status enqueue_gather_kernel(kvr_context *ctx, const PlanePlan *pp, uint32_t n, uint32_t lanes,
+                                 uint32_t page_tokens, const uint32_t *selected, const uint32_t *count,
+                                 uint32_t k, hipStream_t s) {
     if (!n) return KVR_OK;
     kvr::GatherArgs ga{};
     for (uint32_t i = 0; i < n; ++i) ga.plane[i] = pp[i].g;
@@ -415,21 +452,32 @@ kvr_status enqueue_gather_kernel(const PlanePlan *pp, uint32_t n, uint32_t lanes
     ga.lanes = lanes;
     ga.k = k;
     ga.page_tokens = page_tokens;
-    ga.chunk_rows = chunk_rows_for(page_tokens);
+    ga.chunk_rows = gather_chunk_rows(ctx, pp, n, page_tokens);
     ga.chunks = (page_tokens + ga.chunk_rows - 1) / ga.chunk_rows;
     ga.selected = selected;
     ga.count = count;
+    ga.workgroups = ctx->gather_wgs;
+    ga.threads = ctx->gather_threads;
     KVR_HIP(kvr::launch_gather(ga, s));
     return KVR_OK;
 }
 
-// DMA engine: wait for the selection, then one hipMemcpyAsync per selected
-// page span (contiguous token rows) straight into the slots (copy modes) or
-// into a device staging area decoded by the gather kernel.
+// DMA engine: wait for the selection, then hipMemcpyAsync per run of
+// consecutive selected pages (contiguous in the history and in the slots),
+// spread round-robin over kDmaStreams streams that join back into `s`.
+// Copy modes land in the slots; decoding modes land in a device staging area
+// that the gather kernel then decodes HBM -> HBM.  No CU reads host memory.
+// `sel_ready`, when given, is the event after which the selection is valid:
+// the readback then waits on it alone (not on earlier copies queued on s).
 kvr_status enqueue_gather_sdma(kvr_context *ctx, PlanePlan *pp, uint32_t n, uint32_t lanes,
                                uint32_t page_tokens, const uint32_t *selected, const uint32_t *count,
-                               uint32_t k, hipStream_t s) {
+                               uint32_t k, hipStream_t s, hipEvent_t sel_ready = nullptr) {
     if (!n) return KVR_OK;
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    KVR_HIP(hipStreamIsCapturing(s, &capture));
+    if (capture != hipStreamCaptureStatusNone)
+        return fail(KVR_ERR_INVALID, "the DMA stage-in engine reads the selection on the host and cannot be "
+                                     "captured; use the kernel engine inside graphs");
     const size_t words = size_t(lanes) * (k + 1);
     if (ctx->sel_pin_cap < words) {
         if (ctx->sel_pin) KVR_HIP(hipHostFree(ctx->sel_pin));
@@ -438,9 +486,11 @@ kvr_status enqueue_gather_sdma(kvr_context *ctx, PlanePlan *pp, uint32_t n, uint
         KVR_HIP(hipHostMalloc(reinterpret_cast<void **>(&ctx->sel_pin), words * 4, hipHostMallocDefault));
         ctx->sel_pin_cap = words;
     }
-    KVR_HIP(hipMemcpyAsync(ctx->sel_pin, selected, size_t(lanes) * k * 4, hipMemcpyDeviceToHost, s));
-    KVR_HIP(hipMemcpyAsync(ctx->sel_pin + size_t(lanes) * k, count, size_t(lanes) * 4, hipMemcpyDeviceToHost, s));
-    KVR_HIP(hipStreamSynchronize(s));
+    const hipStream_t rb = sel_ready ? ctx->readback : s;
+    if (sel_ready) KVR_HIP(hipStreamWaitEvent(rb, sel_ready, 0));
+    KVR_HIP(hipMemcpyAsync(ctx->sel_pin, selected, size_t(lanes) * k * 4, hipMemcpyDeviceToHost, rb));
+    KVR_HIP(hipMemcpyAsync(ctx->sel_pin + size_t(lanes) * k, count, size_t(lanes) * 4, hipMemcpyDeviceToHost, rb));
+    KVR_HIP(hipStreamSynchronize(rb));
     size_t staged = 0;
     for (uint32_t i = 0; i < n; ++i)
         if (pp[i].g.mode != KVR_GATHER_COPY && pp[i].g.format != KVR_FMT_F16)
@@ -453,6 +503,9 @@ kvr_status enqueue_gather_sdma(kvr_context *ctx, PlanePlan *pp, uint32_t n, uint
         KVR_HIP(hipMalloc(&ctx->staging, staged));
         ctx->staging_bytes = staged;
     }
+    KVR_HIP(hipEventRecord(ctx->dma_fork, s));
+    for (int d = 0; d < kDmaStreams; ++d) KVR_HIP(hipStreamWaitEvent(ctx->dma[d], ctx->dma_fork, 0));
+    uint32_t rr = 0;
     size_t at = 0;
     for (uint32_t i = 0; i < n; ++i) {
         PlanePlan &p = pp[i];
@@ -460,34 +513,54 @@ kvr_status enqueue_gather_sdma(kvr_context *ctx, PlanePlan *pp, uint32_t n, uint
         const size_t span = size_t(page_tokens) * p.host_row;
         for (uint32_t lane = 0; lane < lanes; ++lane) {
             const uint32_t cnt = std::min(ctx->sel_pin[size_t(lanes) * k + lane], k);
-            for (uint32_t slot = 0; slot < cnt; ++slot) {
-                const uint32_t page = ctx->sel_pin[size_t(lane) * k + slot];
+            const uint32_t *ids = ctx->sel_pin + size_t(lane) * k;
+            for (uint32_t slot = 0; slot < cnt;) {
+                const uint32_t page = ids[slot];
                 const uint64_t first = uint64_t(page) * page_tokens;
-                if (first >= p.g.tokens) continue;
-                const uint64_t rows = std::min<uint64_t>(page_tokens, p.g.tokens - first);
+                if (first >= p.g.tokens) { ++slot; continue; }
+                // extend over consecutive pages that are full
+                uint32_t run = 1;
+                while (slot + run < cnt && ids[slot + run] == page + run &&
+                       uint64_t(page + run) * page_tokens < p.g.tokens &&
+                       uint64_t(page + run) * page_tokens <= p.g.tokens - page_tokens)
+                    ++run;
+                const uint64_t rows = std::min<uint64_t>(uint64_t(run) * page_tokens, p.g.tokens - first);
                 const uint8_t *src = p.host + lane * p.g.src_lane_stride + first * p.host_row;
                 uint8_t *dst = decode ? ctx->staging + at + (size_t(lane) * k + slot) * span
                                       : p.g.dst + lane * p.g.dst_lane_stride + size_t(slot) * page_tokens * p.g.dst_row;
-                KVR_HIP(hipMemcpyAsync(dst, src, rows * p.host_row, hipMemcpyHostToDevice, s));
+                KVR_HIP(hipMemcpyAsync(dst, src, rows * p.host_row, hipMemcpyHostToDevice,
+                                       ctx->dma[rr++ % kDmaStreams]));
+                slot += run;
             }
         }
-        if (decode) {
-            kvr::GatherArgs ga{};
-            ga.plane[0] = p.g;
-            ga.plane[0].src = ctx->staging + at;
-            ga.plane[0].src_lane_stride = size_t(k) * span;
-            ga.n_planes = 1;
-            ga.lanes = lanes;
-            ga.k = k;
-            ga.page_tokens = page_tokens;
-            ga.chunk_rows = chunk_rows_for(page_tokens);
-            ga.chunks = (page_tokens + ga.chunk_rows - 1) / ga.chunk_rows;
-            ga.selected = selected;  // page ids bound each slot's valid rows
-            ga.count = count;
-            ga.src_page_stride = span;
-            KVR_HIP(kvr::launch_gather(ga, s));
-            at += size_t(lanes) * k * span;
-        }
+        if (decode) at += size_t(lanes) * k * span;
+    }
+    for (int d = 0; d < kDmaStreams; ++d) {
+        KVR_HIP(hipEventRecord(ctx->dma_join[d], ctx->dma[d]));
+        KVR_HIP(hipStreamWaitEvent(s, ctx->dma_join[d], 0));
+    }
+    at = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        PlanePlan &p = pp[i];
+        if (p.g.mode == KVR_GATHER_COPY || p.g.format == KVR_FMT_F16) continue;
+        const size_t span = size_t(page_tokens) * p.host_row;
+        kvr::GatherArgs ga{};
+        ga.plane[0] = p.g;
+        ga.plane[0].src = ctx->staging + at;
+        ga.plane[0].src_lane_stride = size_t(k) * span;
+        ga.n_planes = 1;
+        ga.lanes = lanes;
+        ga.k = k;
+        ga.page_tokens = page_tokens;
+        ga.chunk_rows = gather_chunk_rows(ctx, &p, 1, page_tokens);
+        ga.chunks = (page_tokens + ga.chunk_rows - 1) / ga.chunk_rows;
+        ga.workgroups = 1024;  // HBM -> HBM: use the whole GPU
+        ga.threads = 256;
+        ga.selected = selected;  // page ids bound each slot's valid rows
+        ga.count = count;
+        ga.src_page_stride = span;
+        KVR_HIP(kvr::launch_gather(ga, s));
+        at += size_t(lanes) * k * span;
     }
     return KVR_OK;
 }
@@ -527,6 +600,12 @@ kvr_status kvr_create(int device, kvr_context **out) {
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->copy, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->ev_sel, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->ops_ev, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->dma_fork, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->readback, hipStreamNonBlocking);
+    for (int i = 0; i < kDmaStreams && e == hipSuccess; ++i) {
+        e = hipStreamCreateWithFlags(&ctx->dma[i], hipStreamNonBlocking);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->dma_join[i], hipEventDisableTiming);
+    }
     if (e == hipSuccess) e = hipMalloc(&ctx->status, kvr::kStatusWords * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMemset(ctx->status, 0, kvr::kStatusWords * sizeof(uint32_t));
     if (e == hipSuccess) e = hipDeviceSynchronize();
@@ -551,10 +630,38 @@ kvr_status kvr_destroy(kvr_context *ctx) {
     if (ctx->sel_pin) (void)hipHostFree(ctx->sel_pin);
     if (ctx->ev_sel) (void)hipEventDestroy(ctx->ev_sel);
     if (ctx->ops_ev) (void)hipEventDestroy(ctx->ops_ev);
+    for (int i = 0; i < kDmaStreams; ++i) {
+        if (ctx->dma[i]) (void)hipStreamSynchronize(ctx->dma[i]);
+        if (ctx->dma[i]) (void)hipStreamDestroy(ctx->dma[i]);
+        if (ctx->dma_join[i]) (void)hipEventDestroy(ctx->dma_join[i]);
+    }
+    if (ctx->dma_fork) (void)hipEventDestroy(ctx->dma_fork);
+    if (ctx->readback) (void)hipStreamSynchronize(ctx->readback);
+    if (ctx->readback) (void)hipStreamDestroy(ctx->readback);
     if (ctx->sel) (void)hipStreamDestroy(ctx->sel);
     if (ctx->copy) (void)hipStreamDestroy(ctx->copy);
     delete ctx;
     return KVR_OK;
+}
+
+kvr_status kvr_set_option(kvr_context *ctx, kvr_option option, int64_t value) {
+    if (kvr_status s = check_ctx(ctx)) return s;
+    switch (option) {
+    case KVR_OPT_GATHER_WORKGROUPS:
+        if (value < 0 || value > 65536) return fail(KVR_ERR_INVALID, "gather workgroups must be in [0, 65536]");
+        ctx->gather_wgs = value ? uint32_t(value) : kDefaultGatherWgs;
+        return KVR_OK;
+    case KVR_OPT_GATHER_CHUNK_ROWS:
+        if (value < 0 || value > 64) return fail(KVR_ERR_INVALID, "gather chunk rows must be in [0, 64]");
+        ctx->chunk_rows = value ? uint32_t(value) : kDefaultChunkRows;
+        return KVR_OK;
+    case KVR_OPT_GATHER_THREADS:
+        if (value != 0 && value != 64 && value != 128 && value != 256)
+            return fail(KVR_ERR_INVALID, "gather workgroup size must be 64, 128 or 256");
+        ctx->gather_threads = value ? uint32_t(value) : 256;
+        return KVR_OK;
+    }
+    return fail(KVR_ERR_INVALID, "unknown option %d", int(option));
 }
 
 void *kvr_select_stream(kvr_context *ctx) { return ctx ? ctx->sel : nullptr; }
@@ -739,10 +846,10 @@ kvr_status kvr_stage_in(kvr_context *ctx, const kvr_plane *planes, uint32_t n_pl
     if (engine > KVR_ENGINE_SDMA) return fail(KVR_ERR_INVALID, "unknown copy engine");
     DeviceGuard guard(ctx->device);
     PlanePlan pp[KVR_MAX_PLANES];
-    if (kvr_status s = check_planes(planes, n_planes, lanes, page_tokens, k, pp)) return s;
+    if (kvr_status s = check_planes(planes, n_planes, lanes, page_tokens, k, ctx->chunk_rows, pp)) return s;
     const hipStream_t s = stream_or(stream, ctx->copy);
     if (engine == KVR_ENGINE_SDMA) return enqueue_gather_sdma(ctx, pp, n_planes, lanes, page_tokens, selected, count, k, s);
-    return enqueue_gather_kernel(pp, n_planes, lanes, page_tokens, selected, count, k, s);
+    return enqueue_gather_kernel(ctx, pp, n_planes, lanes, page_tokens, selected, count, k, s);
 }
 
 kvr_status kvr_recall_layer(kvr_context *ctx, const kvr_layer_recall *d, void *select_stream, void *copy_stream) {
@@ -770,7 +877,7 @@ kvr_status kvr_recall_layer(kvr_context *ctx, const kvr_layer_recall *d, void *s
     if (kvr_status s = check_mandatory(d->mandatory, d->n_mandatory, pages, d->k, m)) return s;
     DeviceGuard guard(ctx->device);
     PlanePlan pp[KVR_MAX_PLANES];
-    if (kvr_status s = check_planes(d->planes, d->n_planes, lanes, page_tokens, d->k, pp)) return s;
+    if (kvr_status s = check_planes(d->planes, d->n_planes, lanes, page_tokens, d->k, ctx->chunk_rows, pp)) return s;
     ScorePlan p;
     if (kvr_status s = plan_score(ctx, d->query, lanes, pages, d->force_mfma, p)) return s;
     if (d->keys && !p.mfma && !valu_dim_ok(d->keys->head_dim))
@@ -787,6 +894,7 @@ kvr_status kvr_recall_layer(kvr_context *ctx, const kvr_layer_recall *d, void *s
             KVR_HIP(kvr::launch_summary(src, false, a, ss));
         } else {
             a.q = p.q;
+            a.q_stage = stage_query(p.q);
             a.logits = p.logits;
             KVR_HIP(kvr::launch_summary(src, true, a, ss));
         }
@@ -800,13 +908,12 @@ kvr_status kvr_recall_layer(kvr_context *ctx, const kvr_layer_recall *d, void *s
                                                  d->tie_rule, m, d->selected, d->count, ss))
         return st;
     if (!d->n_planes) return KVR_OK;
-    if (cs != ss) {
-        KVR_HIP(hipEventRecord(ctx->ev_sel, ss));
-        KVR_HIP(hipStreamWaitEvent(cs, ctx->ev_sel, 0));
-    }
+    KVR_HIP(hipEventRecord(ctx->ev_sel, ss));
+    if (cs != ss) KVR_HIP(hipStreamWaitEvent(cs, ctx->ev_sel, 0));
     if (d->engine == KVR_ENGINE_SDMA)
-        return enqueue_gather_sdma(ctx, pp, d->n_planes, lanes, page_tokens, d->selected, d->count, d->k, cs);
-    return enqueue_gather_kernel(pp, d->n_planes, lanes, page_tokens, d->selected, d->count, d->k, cs);
+        return enqueue_gather_sdma(ctx, pp, d->n_planes, lanes, page_tokens, d->selected, d->count, d->k, cs,
+                                   ctx->ev_sel);
+    return enqueue_gather_kernel(ctx, pp, d->n_planes, lanes, page_tokens, d->selected, d->count, d->k, cs);
 }
 
 kvr_status kvr_d2d_batched(kvr_context *ctx, const void *const *src, void *const *dst, const size_t *nbytes,

@@ -34,6 +34,7 @@ struct SummaryArgs {
     float *means;              // [lanes][pages][width] or null
     uint16_t *summaries;       // [lanes][pages][width] or null
     QueryArgs q;               // fused logits only
+    uint32_t q_stage;          // stage the query in LDS (rows*qheads*dim*2 bytes)
     double *logits;            // [lanes][rows*qheads][pages]
     uint32_t *status;
     uint32_t epoch;
@@ -63,6 +64,10 @@ struct SoftmaxArgs {
 };
 
 struct SelectArgs {
+    // softmax (do_softmax): the lane's logits rows, rewritten in place
+    double *logits;
+    const uint8_t *mask;
+    int do_softmax;
     // aggregation (do_aggregate): scores[lane][p] (+)= sum_rows prob / weight
     const double *probs;       // softmax output
     uint32_t rows, qheads, kvheads;
@@ -104,6 +109,8 @@ struct GatherArgs {
     const uint32_t *selected;   // [lanes][k]; null -> slot i holds page i
     const uint32_t *count;      // [lanes]; null -> k
     uint64_t src_page_stride;   // 0: read pinned history; else staged page i at i*stride
+    uint32_t workgroups;        // grid bound of the persistent gather
+    uint32_t threads;           // workgroup size (64, 128 or 256)
 };
 
 struct AccumulateArgs {

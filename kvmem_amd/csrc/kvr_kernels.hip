@@ -53,18 +53,28 @@ __device__ __forceinline__ void add_q8x8(float *acc, uint32_t lo, uint32_t hi, f
 // ---------------------------------------------------------------------------
 template <int SRC, bool FUSE>
 __global__ __launch_bounds__(256) void k_summary(SummaryArgs a) {
+    // FUSE with q_stage: the workgroup's first lane's query rows, already
+    // through the fp16 operand boundary, staged once in LDS.
+    extern __shared__ __align__(16) uint16_t q_lds[];
+    // Above the stage-in gather's waves when both share a CU: this kernel
+    // is on the select critical path, the gather is bound by the host link.
+    __builtin_amdgcn_s_setprio(2);
     const uint32_t gpp = a.width >> 3;  // 8-channel groups per page
     const uint64_t gid = uint64_t(blockIdx.x) * 256 + threadIdx.x;
     const uint64_t total = uint64_t(a.lanes) * a.pages * gpp;
-    if (gid >= total) return;
-    const uint32_t cg = uint32_t(gid % gpp);
-    const uint64_t rest = gid / gpp;
+    // Threads past the end still take part in the query-staging barrier.
+    const bool active = gid < total;
+    const uint64_t gclamp = active ? gid : total - 1;
+    const uint32_t cg = uint32_t(gclamp % gpp);
+    const uint64_t rest = gclamp / gpp;
     const uint32_t page = uint32_t(rest % a.pages);
     const uint32_t lane = uint32_t(rest / a.pages);
     const uint32_t c0 = cg * 8;
-    uint16_t hb[8];
+    uint16_t hb[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 
-    if (SRC == kSrcSummary) {
+    if (!active) {
+        // nothing to summarize; stays for the barrier below
+    } else if (SRC == kSrcSummary) {
         const u32x4 v = *reinterpret_cast<const u32x4 *>(
             a.src + lane * a.src_lane_stride + (uint64_t(page) * a.width + c0) * 2);
 #pragma unroll
@@ -80,19 +90,31 @@ __global__ __launch_bounds__(256) void k_summary(SummaryArgs a) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
         if (SRC == kSrcKeysF16) {
+            // Software-pipelined: the next U rows are in flight while the
+            // current U are summed (in token order).  The trip count is a
+            // runtime value, so the compiler would otherwise wait on each
+            // group's own loads.
             const u32x4 *p = reinterpret_cast<const u32x4 *>(
                 a.src + lane * a.src_lane_stride + (t0 * a.width + c0) * 2);
             const uint64_t stride = gpp;  // 16-byte words per token row
-            uint32_t t = 0;
-            constexpr int U = 16;
-            for (; t + U <= n; t += U) {
-                u32x4 v[U];
+            constexpr int U = 8;
+            const uint32_t full = n / U * U;
+            if (full) {
+                u32x4 cur[U], nxt[U];
 #pragma unroll
-                for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(p + (t + u) * stride);
+                for (int u = 0; u < U; ++u) cur[u] = __builtin_nontemporal_load(p + u * stride);
+                for (uint32_t t = U; t < full; t += U) {
 #pragma unroll
-                for (int u = 0; u < U; ++u) add_f16x8(acc, v[u]);
+                    for (int u = 0; u < U; ++u) nxt[u] = __builtin_nontemporal_load(p + (t + u) * stride);
+#pragma unroll
+                    for (int u = 0; u < U; ++u) add_f16x8(acc, cur[u]);
+#pragma unroll
+                    for (int u = 0; u < U; ++u) cur[u] = nxt[u];
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u) add_f16x8(acc, cur[u]);
             }
-            for (; t < n; ++t) add_f16x8(acc, __builtin_nontemporal_load(p + t * stride));
+            for (uint32_t t = full; t < n; ++t) add_f16x8(acc, __builtin_nontemporal_load(p + t * stride));
         } else {
             // q8_0 rows: lane owns 8 codes (quarter s) of block b.  Rows are
             // 4-byte aligned (width % 64 == 0), so three aligned dwords cover
@@ -103,10 +125,10 @@ __global__ __launch_bounds__(256) void k_summary(SummaryArgs a) {
             const uint32_t o = b * kQ8Bytes + 2 + 8 * s;
             const uint32_t w0 = o >> 2, wd = (b * kQ8Bytes) >> 2;
             const bool sh = (o & 2) != 0, shd = ((b * kQ8Bytes) & 2) != 0;
-            uint32_t t = 0;
             constexpr int U = 8;
-            for (; t + U <= n; t += U) {
-                uint32_t x0[U], x1[U], x2[U], dw[U];
+            const uint32_t full = n / U * U;
+            auto load_rows = [&](uint32_t t, uint32_t (&x0)[U], uint32_t (&x1)[U], uint32_t (&x2)[U],
+                                 uint32_t (&dw)[U]) {
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
                     const uint32_t *row = reinterpret_cast<const uint32_t *>(base + uint64_t(t + u) * row_bytes);
@@ -115,14 +137,30 @@ __global__ __launch_bounds__(256) void k_summary(SummaryArgs a) {
                     x2[u] = sh ? __builtin_nontemporal_load(row + w0 + 2) : 0u;
                     dw[u] = __builtin_nontemporal_load(row + wd);
                 }
+            };
+            auto sum_rows = [&](const uint32_t (&x0)[U], const uint32_t (&x1)[U], const uint32_t (&x2)[U],
+                                const uint32_t (&dw)[U]) {
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
                     const uint32_t lo = sh ? __builtin_amdgcn_alignbyte(x1[u], x0[u], 2) : x0[u];
                     const uint32_t hi = sh ? __builtin_amdgcn_alignbyte(x2[u], x1[u], 2) : x1[u];
                     add_q8x8(acc, lo, hi, h2f(uint16_t(shd ? dw[u] >> 16 : dw[u] & 0xffffu)));
                 }
+            };
+            if (full) {
+                uint32_t a0[U], a1[U], a2[U], ad[U], b0[U], b1[U], b2[U], bd[U];
+                load_rows(0, a0, a1, a2, ad);
+                for (uint32_t t = U; t < full; t += U) {
+                    load_rows(t, b0, b1, b2, bd);
+                    sum_rows(a0, a1, a2, ad);
+#pragma unroll
+                    for (int u = 0; u < U; ++u) {
+                        a0[u] = b0[u]; a1[u] = b1[u]; a2[u] = b2[u]; ad[u] = bd[u];
+                    }
+                }
+                sum_rows(a0, a1, a2, ad);
             }
-            for (; t < n; ++t) {
+            for (uint32_t t = full; t < n; ++t) {
                 const uint32_t *row = reinterpret_cast<const uint32_t *>(base + uint64_t(t) * row_bytes);
                 const uint32_t x0 = row[w0], x1 = row[w0 + 1], x2 = sh ? row[w0 + 2] : 0u, dw = row[wd];
                 const uint32_t lo = sh ? __builtin_amdgcn_alignbyte(x1, x0, 2) : x0;
@@ -157,6 +195,25 @@ __global__ __launch_bounds__(256) void k_summary(SummaryArgs a) {
 
     if (FUSE) {
         const QueryArgs &q = a.q;
+        // Stage the first lane's query rows after the HBM stream, while other
+        // workgroups still stream theirs, instead of delaying every first load.
+        uint32_t staged_lane = 0xffffffffu;
+        if (a.q_stage) {
+            staged_lane = uint32_t((uint64_t(blockIdx.x) * 256 / gpp) / a.pages);
+            const uint32_t nq = q.rows * q.qheads * q.dim;
+            uint32_t qbad = kOperandOk;
+            for (uint32_t i = threadIdx.x; i < nq; i += 256) {
+                const uint32_t d = i % q.dim, h = (i / q.dim) % q.qheads, r = i / (q.dim * q.qheads);
+                uint16_t qh = 0;
+                const uint32_t e = recall16(load_scalar(q.data + staged_lane * q.lane_stride + r * q.row_stride +
+                                                            h * q.head_stride + d * q.dim_stride, q.scalar), qh);
+                qbad = qbad ? qbad : e;
+                q_lds[i] = qh;
+            }
+            if (qbad) raise_operand(a.status, qbad, a.epoch);
+            __syncthreads();
+        }
+        if (!active) return;
         const uint32_t kvh = c0 / q.dim, d0 = c0 % q.dim;
         const uint32_t group = q.qheads / q.kvheads;
         const int lph = int(q.dim >> 3);  // lanes per kv-head slice
@@ -164,19 +221,29 @@ __global__ __launch_bounds__(256) void k_summary(SummaryArgs a) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) m[i] = double(h2f(hb[i]));
         uint32_t bad = kOperandOk;
+        const bool from_lds = lane == staged_lane;
         for (uint32_t r = 0; r < q.rows; ++r) {
             for (uint32_t hh = 0; hh < group; ++hh) {
                 const uint32_t h = kvh * group + hh;
-                const uint8_t *qp = q.data + lane * q.lane_stride + r * q.row_stride +
-                                    h * q.head_stride + d0 * q.dim_stride;
                 double part = 0.0;
+                if (from_lds) {
+                    const u32x4 v = *reinterpret_cast<const u32x4 *>(q_lds + (r * q.qheads + h) * q.dim + d0);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    uint16_t qb = 0;
-                    const uint32_t e = recall16(load_scalar(qp + i * q.dim_stride, q.scalar), qb);
-                    bad = bad ? bad : e;
-                    // fp16 x fp16 is exact in binary64: fma == multiply-then-add.
-                    part = fma(double(h2f(qb)), m[i], part);
+                    for (int i = 0; i < 4; ++i) {
+                        part = fma(double(h2f(uint16_t(v[i] & 0xffffu))), m[2 * i], part);
+                        part = fma(double(h2f(uint16_t(v[i] >> 16))), m[2 * i + 1], part);
+                    }
+                } else {
+                    const uint8_t *qp = q.data + lane * q.lane_stride + r * q.row_stride +
+                                        h * q.head_stride + d0 * q.dim_stride;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        uint16_t qb = 0;
+                        const uint32_t e = recall16(load_scalar(qp + i * q.dim_stride, q.scalar), qb);
+                        bad = bad ? bad : e;
+                        // fp16 x fp16 is exact in binary64: fma == multiply-then-add.
+                        part = fma(double(h2f(qb)), m[i], part);
+                    }
                 }
                 part = group_sum(part, lph);
                 if ((cg & uint32_t(lph - 1)) == 0)
@@ -259,7 +326,7 @@ __global__ __launch_bounds__(256) void k_logits_mfma(MfmaLogitsArgs a) {
 // Page softmax (graph_recall.cpp:362-372).  One wave per distribution:
 // p_j = exp(l_j - max) / sum over the score-mask pages; masked pages get 0.
 // ---------------------------------------------------------------------------
-__device__ void softmax_wave(double *x, uint32_t n, const uint8_t *mask, uint32_t l) {
+__device__ __forceinline__ void softmax_wave(double *x, uint32_t n, const uint8_t *mask, uint32_t l) {
     double m = -INFINITY;
     for (uint32_t j = l; j < n; j += kWave)
         if (!mask || mask[j]) m = fmax(m, x[j]);
@@ -294,12 +361,99 @@ __device__ T block_reduce(T v, T *lds, Op op) {
 }
 
 struct SumOp { __device__ double operator()(double a, double b) const { return a + b; } };
+struct AndOp { __device__ uint64_t operator()(uint64_t a, uint64_t b) const { return a & b; } };
+struct OrOp { __device__ uint64_t operator()(uint64_t a, uint64_t b) const { return a | b; } };
 struct MaxOp { __device__ double operator()(double a, double b) const { return b > a ? b : a; } };
 
+// The same with the row held in registers (NPL values per lane, pages <=
+// 64*NPL): one read and one write of the row.
+template <int NPL>
+__device__ __forceinline__ void softmax_wave_reg(double *x, uint32_t n, const uint8_t *mask, uint32_t l) {
+    double v[NPL];
+    double m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+        const uint32_t j = l + i * kWave;
+        const bool on = j < n && (!mask || mask[j]);
+        v[i] = on ? x[j] : -INFINITY;
+        m = fmax(m, v[i]);
+    }
+    m = wave_max(m);
+    double s = 0.0;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+        const uint32_t j = l + i * kWave;
+        const bool on = j < n && (!mask || mask[j]);
+        v[i] = on ? exp(v[i] - m) : 0.0;
+        s += v[i];
+    }
+    s = wave_sum(s);
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+        const uint32_t j = l + i * kWave;
+        if (j < n) x[j] = s > 0.0 ? v[i] / s : 0.0;
+    }
+}
+
+template <int NPL>
 __global__ __launch_bounds__(256) void k_softmax_rows(SoftmaxArgs a) {
     const uint64_t row = uint64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
     if (row >= uint64_t(a.lanes) * a.rows * a.qheads) return;
-    softmax_wave(a.logits + row * a.pages, a.pages, a.mask, threadIdx.x & 63);
+    if (NPL == 0)
+        softmax_wave(a.logits + row * a.pages, a.pages, a.mask, threadIdx.x & 63);
+    else
+        softmax_wave_reg<NPL ? NPL : 1>(a.logits + row * a.pages, a.pages, a.mask, threadIdx.x & 63);
+}
+
+// Register softmax for rows up to 1024 pages, global-memory passes beyond
+// (wider register rows would spill under the 1024-thread select kernel).
+__device__ __forceinline__ void softmax_any(double *x, uint32_t n, const uint8_t *mask, uint32_t l) {
+    if (n <= 64) softmax_wave_reg<1>(x, n, mask, l);
+    else if (n <= 128) softmax_wave_reg<2>(x, n, mask, l);
+    else if (n <= 256) softmax_wave_reg<4>(x, n, mask, l);
+    else if (n <= 512) softmax_wave_reg<8>(x, n, mask, l);
+    else if (n <= 1024) softmax_wave_reg<16>(x, n, mask, l);
+    else softmax_wave(x, n, mask, l);
+}
+
+// One GQA group by one wave (rows base + hh*n, hh < group); the result goes
+// to the group's first row.  Each lane only touches pages j == l (mod 64),
+// so its own stores are what it reads back.
+__device__ __forceinline__ void group_wave(double *base, uint32_t group, uint32_t n, const uint8_t *mask, uint32_t l,
+                           uint32_t aggregation) {
+    if (aggregation == kAggMax) {
+        for (uint32_t hh = 0; hh < group; ++hh) softmax_any(base + uint64_t(hh) * n, n, mask, l);
+        double s = 0.0;
+        for (uint32_t j = l; j < n; j += kWave) {
+            double gm = 0.0;
+            for (uint32_t hh = 0; hh < group; ++hh) {
+                const double p = base[uint64_t(hh) * n + j];
+                gm = p > gm ? p : gm;
+            }
+            base[j] = gm;
+            s += gm;
+        }
+        s = wave_sum(s);
+        for (uint32_t j = l; j < n; j += kWave) base[j] = s > 0.0 ? base[j] / s : 0.0;
+    } else {
+        double mx = -INFINITY;
+        for (uint32_t j = l; j < n; j += kWave) {
+            double gm = -INFINITY;
+            if (!mask || mask[j])
+                for (uint32_t hh = 0; hh < group; ++hh) gm = fmax(gm, base[uint64_t(hh) * n + j]);
+            base[j] = gm;
+            mx = fmax(mx, gm);
+        }
+        mx = wave_max(mx);
+        double s = 0.0;
+        for (uint32_t j = l; j < n; j += kWave) {
+            const double e = (!mask || mask[j]) ? exp(base[j] - mx) : 0.0;
+            base[j] = e;
+            s += e;
+        }
+        s = wave_sum(s);
+        for (uint32_t j = l; j < n; j += kWave) base[j] = s > 0.0 ? base[j] / s : 0.0;
+    }
 }
 
 // One workgroup per (lane, row, kv-head) group.
@@ -398,24 +552,53 @@ __device__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *total, uint32_t *
 __global__ __launch_bounds__(1024) void k_select(SelectArgs a) {
     __shared__ uint32_t hist[256];
     __shared__ uint32_t scan_lds[17];
+    __shared__ uint64_t red_lds[17];
     __shared__ uint32_t s_digit, s_remaining;
+    __shared__ bool s_exact;
     const uint32_t lane = blockIdx.x, tid = threadIdx.x;
     double *sc = a.scores + uint64_t(lane) * a.pages;
     const uint32_t n = a.pages;
 
+    if (a.do_softmax) {
+        // Page softmax of this lane's rows (Mean) or GQA groups, one wave each.
+        const uint32_t wave = tid >> 6, l = tid & 63, nw = blockDim.x >> 6;
+        const uint32_t group = a.qheads / a.kvheads;
+        double *lane_base = a.logits + uint64_t(lane) * a.rows * a.qheads * n;
+        if (a.aggregation == kAggMean) {
+            for (uint32_t rho = wave; rho < a.rows * a.qheads; rho += nw)
+                softmax_any(lane_base + uint64_t(rho) * n, n, a.mask, l);
+        } else {
+            for (uint32_t gi = wave; gi < a.rows * a.kvheads; gi += nw) {
+                const uint32_t r = gi / a.kvheads, g = gi % a.kvheads;
+                group_wave(lane_base + (uint64_t(r) * a.qheads + g * group) * n, group, n, a.mask, l,
+                           a.aggregation);
+            }
+        }
+        __syncthreads();
+    }
     if (a.do_aggregate) {
         const uint32_t group = a.qheads / a.kvheads;
         const uint64_t lane_rows = uint64_t(lane) * a.rows * a.qheads;
+        // Contributing rows in the reference's order: (row, head) for Mean,
+        // (row, kv-head group) for the group rules.  Loads are issued eight
+        // at a time; the additions stay in order.
+        const bool mean = a.aggregation == kAggMean;
+        const uint32_t nrows = mean ? a.rows * a.qheads : a.rows * a.kvheads;
         for (uint32_t j = tid; j < n; j += blockDim.x) {
             double acc = a.accumulate ? sc[j] : 0.0;
-            if (a.aggregation == kAggMean) {
-                for (uint32_t rho = 0; rho < a.rows * a.qheads; ++rho)
-                    acc += a.probs[(lane_rows + rho) * n + j] / a.weight;
-            } else {
-                for (uint32_t r = 0; r < a.rows; ++r)
-                    for (uint32_t g = 0; g < a.kvheads; ++g)
-                        acc += a.probs[(lane_rows + uint64_t(r) * a.qheads + g * group) * n + j] / a.weight;
+            const double *col = a.probs + lane_rows * n + j;
+            auto row_of = [&](uint32_t i) -> uint64_t {
+                return mean ? i : uint64_t(i / a.kvheads) * a.qheads + (i % a.kvheads) * group;
+            };
+            uint32_t i = 0;
+            for (; i + 8 <= nrows; i += 8) {
+                double v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v[u] = col[row_of(i + u) * n];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) acc += v[u] / a.weight;
             }
+            for (; i < nrows; ++i) acc += col[row_of(i) * n] / a.weight;
             sc[j] = acc;
         }
         __syncthreads();
@@ -437,68 +620,103 @@ __global__ __launch_bounds__(1024) void k_select(SelectArgs a) {
 
     const uint32_t n_cand = n - a.n_mandatory;
     const uint32_t k_eff = a.k - a.n_mandatory;  // host guarantees n_mandatory <= k
-    uint64_t thresh;
-    uint32_t remaining;
+
+    // Threshold search.  After it, with HT = thresh >> shift:
+    //   (key >> shift) >  HT            selected
+    //   (key >> shift) == HT && bucket  selected (the boundary bucket holds
+    //                                   exactly the remaining count)
+    //   key == thresh && !bucket        the first/last `remaining` equal keys
+    //                                   by id (tie rule), shift == 0
+    uint64_t thresh = 0;
+    uint32_t remaining = 0, shift = 0;
+    bool bucket = false;
     if (k_eff == 0) {
-        thresh = ~0ull;
-        remaining = 0;
+        thresh = ~0ull;  // nothing ranks
+        bucket = true;
+        shift = 0;
     } else if (k_eff >= n_cand) {
-        thresh = 0;
-        remaining = 0xffffffffu;
+        thresh = 0;      // every candidate
+        bucket = true;
     } else {
-        uint64_t prefix = 0, pmask = 0;
-        remaining = k_eff;
-        for (int pass = 0; pass < 8; ++pass) {
-            const int shift = 56 - 8 * pass;
-            if (tid < 256) hist[tid] = 0;
-            __syncthreads();
-            for (uint32_t j = tid; j < n; j += blockDim.x) {
-                if (a.n_mandatory && is_mandatory(a, j)) continue;
-                const uint64_t key = order_key(sc[j]);
-                if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
-            }
-            __syncthreads();
-            if (tid < 64) {
-                // lane l covers digits 255-4l .. 252-4l, highest first
-                const uint32_t c0 = hist[255 - 4 * tid], c1 = hist[254 - 4 * tid],
-                               c2 = hist[253 - 4 * tid], c3 = hist[252 - 4 * tid];
-                const uint32_t tot = c0 + c1 + c2 + c3;
-                const uint32_t incl = wave_inclusive_scan(tot);
-                const uint32_t excl = incl - tot;
-                if (excl < remaining && remaining <= incl) {
-                    uint32_t rem = remaining - excl, d;
-                    if (rem <= c0) {
-                        d = 255 - 4 * tid;
-                    } else if (rem <= c0 + c1) {
-                        rem -= c0; d = 254 - 4 * tid;
-                    } else if (rem <= c0 + c1 + c2) {
-                        rem -= c0 + c1; d = 253 - 4 * tid;
-                    } else {
-                        rem -= c0 + c1 + c2; d = 252 - 4 * tid;
-                    }
-                    s_digit = d;
-                    s_remaining = rem;
-                }
-            }
-            __syncthreads();
-            prefix |= uint64_t(s_digit) << shift;
-            pmask |= 0xffull << shift;
-            remaining = s_remaining;
-            __syncthreads();
+        // Leading bits shared by every candidate need no pass.
+        uint64_t and_all = ~0ull, or_all = 0;
+        for (uint32_t j = tid; j < n; j += blockDim.x) {
+            if (a.n_mandatory && is_mandatory(a, j)) continue;
+            const uint64_t key = order_key(sc[j]);
+            and_all &= key;
+            or_all |= key;
         }
-        thresh = prefix;
+        and_all = block_reduce(and_all, red_lds, AndOp());
+        or_all = block_reduce(or_all, red_lds, OrOp());
+        const uint64_t diff = and_all ^ or_all;
+        if (diff == 0) {  // all candidates equal: the tie rule decides
+            thresh = and_all;
+            remaining = k_eff;
+        } else {
+            const int top = 63 - __clzll(diff);
+            int pos = top / 8 * 8;
+            uint64_t prefix = and_all & ~((2ull << top) - 1);  // the common high bits
+            remaining = k_eff;
+            for (;; pos -= 8) {
+                const uint64_t hi_mask = pos + 8 >= 64 ? 0ull : ~0ull << (pos + 8);
+                if (tid < 256) hist[tid] = 0;
+                __syncthreads();
+                for (uint32_t j = tid; j < n; j += blockDim.x) {
+                    if (a.n_mandatory && is_mandatory(a, j)) continue;
+                    const uint64_t key = order_key(sc[j]);
+                    if ((key & hi_mask) == (prefix & hi_mask)) atomicAdd(&hist[(key >> pos) & 255u], 1u);
+                }
+                __syncthreads();
+                if (tid < 64) {
+                    // lane l covers digits 255-4l .. 252-4l, highest first
+                    const uint32_t c0 = hist[255 - 4 * tid], c1 = hist[254 - 4 * tid],
+                                   c2 = hist[253 - 4 * tid], c3 = hist[252 - 4 * tid];
+                    const uint32_t tot = c0 + c1 + c2 + c3;
+                    const uint32_t incl = wave_inclusive_scan(tot);
+                    const uint32_t excl = incl - tot;
+                    if (excl < remaining && remaining <= incl) {
+                        uint32_t rem = remaining - excl, d, cnt;
+                        if (rem <= c0) {
+                            d = 255 - 4 * tid; cnt = c0;
+                        } else if (rem <= c0 + c1) {
+                            rem -= c0; d = 254 - 4 * tid; cnt = c1;
+                        } else if (rem <= c0 + c1 + c2) {
+                            rem -= c0 + c1; d = 253 - 4 * tid; cnt = c2;
+                        } else {
+                            rem -= c0 + c1 + c2; d = 252 - 4 * tid; cnt = c3;
+                        }
+                        s_digit = d;
+                        s_remaining = rem;
+                        s_exact = rem == cnt;
+                    }
+                }
+                __syncthreads();
+                prefix |= uint64_t(s_digit) << pos;
+                remaining = s_remaining;
+                const bool exact = s_exact;
+                __syncthreads();
+                if (exact) {  // the whole boundary bucket is selected
+                    bucket = true;
+                    shift = uint32_t(pos);
+                    break;
+                }
+                if (pos == 0) break;  // full key: the tie rule picks among equals
+            }
+            thresh = prefix;
+        }
     }
 
     // Compaction in id order: thread t owns the contiguous id chunk
     // [t*C, t*C + C).
+    const uint64_t ht = shift >= 64 ? 0 : thresh >> shift;
     const uint32_t C = (n + blockDim.x - 1) / blockDim.x;
     const uint32_t j0 = min(n, tid * C), j1 = min(n, j0 + C);
     uint32_t n_take = 0, n_eq = 0;
     for (uint32_t j = j0; j < j1; ++j) {
         if (a.n_mandatory && is_mandatory(a, j)) { ++n_take; continue; }
-        const uint64_t key = order_key(sc[j]);
-        n_take += key > thresh;
-        n_eq += key == thresh;
+        const uint64_t hk = order_key(sc[j]) >> shift;
+        if (hk > ht || (hk == ht && bucket)) ++n_take;
+        else if (hk == ht) ++n_eq;
     }
     uint32_t eq_total;
     const uint32_t eq_base = block_exclusive_scan(n_eq, &eq_total, scan_lds);
@@ -521,12 +739,12 @@ __global__ __launch_bounds__(1024) void k_select(SelectArgs a) {
         if (a.n_mandatory && is_mandatory(a, j)) {
             take = true;
         } else {
-            const uint64_t key = order_key(sc[j]);
-            if (key == thresh) {
+            const uint64_t hk = order_key(sc[j]) >> shift;
+            if (hk == ht && !bucket) {
                 take = rank >= lo && rank < hi;
                 ++rank;
             } else {
-                take = key > thresh;
+                take = hk > ht || (hk == ht && bucket);
             }
         }
         if (take && o < a.k) out[o++] = j;
@@ -545,23 +763,24 @@ __global__ __launch_bounds__(1024) void k_select(SelectArgs a) {
 //   requant_q8_0 d = amax/127, q = roundf(x/d)          (stagein.cu:181-199)
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void copy_span(const uint8_t *src, uint8_t *dst, uint32_t bytes) {
+    const uint32_t nt = blockDim.x;
     if (((uintptr_t(src) | uintptr_t(dst) | bytes) & 15u) == 0) {
         const u32x4 *s = reinterpret_cast<const u32x4 *>(src);
         u32x4 *d = reinterpret_cast<u32x4 *>(dst);
         const uint32_t n = bytes >> 4;
         uint32_t i = threadIdx.x;
-        for (; i + 3 * 256 < n; i += 4 * 256) {
-            const u32x4 v0 = __builtin_nontemporal_load(s + i), v1 = __builtin_nontemporal_load(s + i + 256),
-                        v2 = __builtin_nontemporal_load(s + i + 512), v3 = __builtin_nontemporal_load(s + i + 768);
-            d[i] = v0; d[i + 256] = v1; d[i + 512] = v2; d[i + 768] = v3;
+        for (; i + 3 * nt < n; i += 4 * nt) {
+            const u32x4 v0 = __builtin_nontemporal_load(s + i), v1 = __builtin_nontemporal_load(s + i + nt),
+                        v2 = __builtin_nontemporal_load(s + i + 2 * nt), v3 = __builtin_nontemporal_load(s + i + 3 * nt);
+            d[i] = v0; d[i + nt] = v1; d[i + 2 * nt] = v2; d[i + 3 * nt] = v3;
         }
-        for (; i < n; i += 256) d[i] = __builtin_nontemporal_load(s + i);
+        for (; i < n; i += nt) d[i] = __builtin_nontemporal_load(s + i);
     } else if (((uintptr_t(src) | uintptr_t(dst) | bytes) & 3u) == 0) {
         const uint32_t *s = reinterpret_cast<const uint32_t *>(src);
         uint32_t *d = reinterpret_cast<uint32_t *>(dst);
-        for (uint32_t i = threadIdx.x; i < bytes >> 2; i += 256) d[i] = s[i];
+        for (uint32_t i = threadIdx.x; i < bytes >> 2; i += nt) d[i] = s[i];
     } else {
-        for (uint32_t i = threadIdx.x; i < bytes; i += 256) dst[i] = src[i];
+        for (uint32_t i = threadIdx.x; i < bytes; i += nt) dst[i] = src[i];
     }
 }
 
@@ -595,64 +814,72 @@ __device__ __forceinline__ void quant_block_q8(const float *x, uint8_t *blk) {
     for (int j = 0; j < kQK; ++j) blk[2 + j] = uint8_t(int8_t(roundf(x[j] * id)));
 }
 
+// Persistent: a bounded grid loops over (lane, slot, plane, chunk) items, so
+// waves parked on host-link latency occupy a few CUs instead of all of them
+// while the select stream's HBM-bound kernels run beside the gather.
 __global__ __launch_bounds__(256) void k_gather(GatherArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
-    const uint32_t lane = blockIdx.y;
-    uint32_t id = blockIdx.x;
-    const uint32_t chunk = id % a.chunks;
-    id /= a.chunks;
-    const uint32_t pi = id % a.n_planes;
-    const uint32_t slot = id / a.n_planes;
-    const uint32_t cnt = a.count ? a.count[lane] : a.k;
-    if (slot >= cnt) return;
-    const GatherPlane &P = a.plane[pi];
-    const uint32_t page = a.selected ? a.selected[uint64_t(lane) * a.k + slot] : slot;
-    const uint64_t first = uint64_t(page) * a.page_tokens;
-    if (first >= P.tokens) return;
-    const uint64_t left = P.tokens - first;
-    const uint32_t valid = left < a.page_tokens ? uint32_t(left) : a.page_tokens;
-    const uint32_t r0 = chunk * a.chunk_rows;
-    if (r0 >= valid) return;
-    const uint32_t nr = min(a.chunk_rows, valid - r0);
-    // Staged sources (src_page_stride != 0) hold slot s's page at s*stride.
-    const uint8_t *src = a.src_page_stride
-        ? P.src + lane * P.src_lane_stride + uint64_t(slot) * a.src_page_stride + uint64_t(r0) * P.src_row
-        : P.src + lane * P.src_lane_stride + (first + r0) * P.src_row;
-    uint8_t *dst = P.dst + lane * P.dst_lane_stride + (uint64_t(slot) * a.page_tokens + r0) * P.dst_row;
-    const uint32_t sbytes = nr * P.src_row;
-    if (P.mode == kModeCopy || P.format == kFmtF16) {
-        copy_span(src, dst, sbytes);
-        return;
-    }
-    // Stage the packed rows in LDS, then decode whole blocks.
-    copy_span(src, lds, sbytes);
-    __syncthreads();
-    const uint32_t bpr = P.width / kQK;
-    const uint32_t bbytes = P.format == kFmtQ8 ? kQ8Bytes : kQ41Bytes;
-    const uint32_t nblocks = nr * bpr;
-    if (P.mode == kModeDequantF16) {
-        for (uint32_t b = threadIdx.x; b < nblocks; b += 256) {
-            float y[kQK];
-            decode_block(lds + b * bbytes, P.format, y);
-            u32x4 *o = reinterpret_cast<u32x4 *>(dst + uint64_t(b / bpr) * P.dst_row + (b % bpr) * 64);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                u32x4 v;
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    v[i] = uint32_t(f2h(y[8 * q + 2 * i])) | (uint32_t(f2h(y[8 * q + 2 * i + 1])) << 16);
-                o[q] = v;
-            }
+    const uint32_t per_lane = a.k * a.n_planes * a.chunks;
+    const uint64_t total = uint64_t(a.lanes) * per_lane;
+    for (uint64_t it = blockIdx.x; it < total; it += gridDim.x) {
+        const uint32_t lane = uint32_t(it / per_lane);
+        uint32_t id = uint32_t(it % per_lane);
+        const uint32_t chunk = id % a.chunks;
+        id /= a.chunks;
+        const uint32_t pi = id % a.n_planes;
+        const uint32_t slot = id / a.n_planes;
+        const uint32_t cnt = a.count ? a.count[lane] : a.k;
+        if (slot >= cnt) continue;
+        const GatherPlane &P = a.plane[pi];
+        const uint32_t page = a.selected ? a.selected[uint64_t(lane) * a.k + slot] : slot;
+        const uint64_t first = uint64_t(page) * a.page_tokens;
+        if (first >= P.tokens) continue;
+        const uint64_t left = P.tokens - first;
+        const uint32_t valid = left < a.page_tokens ? uint32_t(left) : a.page_tokens;
+        const uint32_t r0 = chunk * a.chunk_rows;
+        if (r0 >= valid) continue;
+        const uint32_t nr = min(a.chunk_rows, valid - r0);
+        // Staged sources (src_page_stride != 0) hold slot s's page at s*stride.
+        const uint8_t *src = a.src_page_stride
+            ? P.src + lane * P.src_lane_stride + uint64_t(slot) * a.src_page_stride + uint64_t(r0) * P.src_row
+            : P.src + lane * P.src_lane_stride + (first + r0) * P.src_row;
+        uint8_t *dst = P.dst + lane * P.dst_lane_stride + (uint64_t(slot) * a.page_tokens + r0) * P.dst_row;
+        const uint32_t sbytes = nr * P.src_row;
+        if (P.mode == kModeCopy || P.format == kFmtF16) {
+            copy_span(src, dst, sbytes);
+            continue;
         }
-    } else {
-        uint8_t *out = lds + ((sbytes + 15u) & ~15u);
-        for (uint32_t b = threadIdx.x; b < nblocks; b += 256) {
-            float y[kQK];
-            decode_block(lds + b * kQ8Bytes, kFmtQ8, y);
-            quant_block_q8(y, out + b * kQ8Bytes);
-        }
+        // Stage the packed rows in LDS, then decode whole blocks.
+        copy_span(src, lds, sbytes);
         __syncthreads();
-        copy_span(out, dst, sbytes);
+        const uint32_t bpr = P.width / kQK;
+        const uint32_t bbytes = P.format == kFmtQ8 ? kQ8Bytes : kQ41Bytes;
+        const uint32_t nblocks = nr * bpr;
+        if (P.mode == kModeDequantF16) {
+            for (uint32_t b = threadIdx.x; b < nblocks; b += blockDim.x) {
+                float y[kQK];
+                decode_block(lds + b * bbytes, P.format, y);
+                u32x4 *o = reinterpret_cast<u32x4 *>(dst + uint64_t(b / bpr) * P.dst_row + (b % bpr) * 64);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    u32x4 v;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        v[i] = uint32_t(f2h(y[8 * q + 2 * i])) | (uint32_t(f2h(y[8 * q + 2 * i + 1])) << 16);
+                    o[q] = v;
+                }
+            }
+        } else {
+            uint8_t *out = lds + ((sbytes + 15u) & ~15u);
+            for (uint32_t b = threadIdx.x; b < nblocks; b += blockDim.x) {
+                float y[kQK];
+                decode_block(lds + b * kQ8Bytes, kFmtQ8, y);
+                quant_block_q8(y, out + b * kQ8Bytes);
+            }
+            __syncthreads();
+            copy_span(out, dst, sbytes);
+        }
+        __syncthreads();  // LDS is reused by the next item
     }
 }
 
@@ -761,37 +988,48 @@ inline unsigned blocks_for(uint64_t threads, unsigned per = 256) {
 
 // ---- launchers ------------------------------------------------------------
 hipError_t launch_summary(int source, bool fuse, const SummaryArgs &a, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch\'s error
     const uint64_t threads = uint64_t(a.lanes) * a.pages * (a.width >> 3);
     const dim3 grid(blocks_for(threads)), block(256);
+    const size_t lds = fuse && a.q_stage ? size_t(a.q.rows) * a.q.qheads * a.q.dim * 2 : 0;
     if (source == kSrcKeysF16 && fuse)
-        hipLaunchKernelGGL((k_summary<kSrcKeysF16, true>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((k_summary<kSrcKeysF16, true>), grid, block, lds, s, a);
     else if (source == kSrcKeysF16)
         hipLaunchKernelGGL((k_summary<kSrcKeysF16, false>), grid, block, 0, s, a);
     else if (source == kSrcKeysQ8 && fuse)
-        hipLaunchKernelGGL((k_summary<kSrcKeysQ8, true>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((k_summary<kSrcKeysQ8, true>), grid, block, lds, s, a);
     else if (source == kSrcKeysQ8)
         hipLaunchKernelGGL((k_summary<kSrcKeysQ8, false>), grid, block, 0, s, a);
     else
-        hipLaunchKernelGGL((k_summary<kSrcSummary, true>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((k_summary<kSrcSummary, true>), grid, block, lds, s, a);
     return hipGetLastError();
 }
 
 hipError_t launch_pack_query(const PackQueryArgs &a, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch\'s error
     const uint64_t n = uint64_t(a.lanes) * a.q.rows * a.q.qheads * a.q.dim;
     hipLaunchKernelGGL(k_pack_query, dim3(blocks_for(n)), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
 hipError_t launch_logits_mfma(const MfmaLogitsArgs &a, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch\'s error
     const dim3 grid((a.pages + 63) / 64, a.kvheads, a.lanes);
     hipLaunchKernelGGL(k_logits_mfma, grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
 hipError_t launch_softmax(const SoftmaxArgs &a, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch\'s error
     if (a.aggregation == kAggMean) {
         const uint64_t rows = uint64_t(a.lanes) * a.rows * a.qheads;
-        hipLaunchKernelGGL(k_softmax_rows, dim3(unsigned((rows + 3) / 4)), dim3(256), 0, s, a);
+        const dim3 grid(unsigned((rows + 3) / 4)), block(256);
+        if (a.pages <= 64) hipLaunchKernelGGL(k_softmax_rows<1>, grid, block, 0, s, a);
+        else if (a.pages <= 128) hipLaunchKernelGGL(k_softmax_rows<2>, grid, block, 0, s, a);
+        else if (a.pages <= 256) hipLaunchKernelGGL(k_softmax_rows<4>, grid, block, 0, s, a);
+        else if (a.pages <= 512) hipLaunchKernelGGL(k_softmax_rows<8>, grid, block, 0, s, a);
+        else if (a.pages <= 1024) hipLaunchKernelGGL(k_softmax_rows<16>, grid, block, 0, s, a);
+        else hipLaunchKernelGGL(k_softmax_rows<0>, grid, block, 0, s, a);
     } else {
         const unsigned groups = unsigned(uint64_t(a.lanes) * a.rows * a.kvheads);
         hipLaunchKernelGGL(k_softmax_groups, dim3(groups), dim3(256), 0, s, a);
@@ -800,11 +1038,13 @@ hipError_t launch_softmax(const SoftmaxArgs &a, hipStream_t s) {
 }
 
 hipError_t launch_select(const SelectArgs &a, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch\'s error
     hipLaunchKernelGGL(k_select, dim3(a.lanes), dim3(1024), 0, s, a);
     return hipGetLastError();
 }
 
 hipError_t launch_gather(const GatherArgs &a, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch\'s error
     uint32_t lds = 0;
     for (uint32_t i = 0; i < a.n_planes; ++i) {
         const GatherPlane &p = a.plane[i];
@@ -813,27 +1053,32 @@ hipError_t launch_gather(const GatherArgs &a, hipStream_t s) {
         if (p.mode == kModeRequantQ8) need += a.chunk_rows * p.src_row;
         lds = need > lds ? need : lds;
     }
-    const dim3 grid(a.k * a.n_planes * a.chunks, a.lanes);
-    hipLaunchKernelGGL(k_gather, grid, dim3(256), lds, s, a);
+    const uint64_t items = uint64_t(a.lanes) * a.k * a.n_planes * a.chunks;
+    const uint32_t wgs = unsigned(items < a.workgroups ? items : a.workgroups);
+    hipLaunchKernelGGL(k_gather, dim3(wgs ? wgs : 1), dim3(a.threads), lds, s, a);
     return hipGetLastError();
 }
 
 hipError_t launch_accumulate(const AccumulateArgs &a, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch\'s error
     hipLaunchKernelGGL(k_accumulate, dim3(blocks_for(uint64_t(a.segments) * a.width)), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
 hipError_t launch_finalize(const FinalizeArgs &a, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch\'s error
     hipLaunchKernelGGL(k_finalize, dim3(blocks_for(uint64_t(a.pages) * a.width)), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
 hipError_t launch_copy_ops(const CopyOp *ops, uint32_t n, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch\'s error
     hipLaunchKernelGGL(k_copy_ops, dim3(n), dim3(256), 0, s, ops, n);
     return hipGetLastError();
 }
 
 hipError_t launch_synth(const SynthArgs &a, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch\'s error
     hipLaunchKernelGGL(k_synth, dim3(blocks_for(a.count)), dim3(256), 0, s, a);
     return hipGetLastError();
 }

@@ -418,3 +418,31 @@ def test_operand_errors_empty_selection(ctx, bad, status):
                      pages=pages, page_tokens=16, scores=out, selected=sel, count=cnt, k=8)
     assert ctx.status() == 0
     assert host(cnt, np.uint32)[0] == 8
+
+
+@pytest.mark.parametrize("wgs,chunk", [(1, 1), (7, 3), (64, 8), (1000, 64)])
+def test_gather_options_do_not_change_bytes(ctx, wgs, chunk):
+    """The persistent gather's grid bound and chunk size change only the
+    schedule: every setting writes the same slots."""
+    tokens, width, pt, k = 2100, 1024, 256, 6
+    hist = _history(K.FMT_Q8_0, tokens, width, 50)
+    pin = K.PinnedBuffer(hist.size)
+    pin.numpy()[:] = hist
+    sel = np.array([0, 2, 3, 5, 7, 8], np.uint32)
+    expect = O.gather(hist, K.FMT_Q8_0, width, tokens, pt, sel, O.GATHER_DEQUANT_F16)
+    expect_rq = O.gather(hist, K.FMT_Q8_0, width, tokens, pt, sel, O.GATHER_REQUANT_Q8_0)
+    slots = zeros(expect.size, np.uint8)
+    rq = zeros(expect_rq.size, np.uint8)
+    ctx.set_option(K._capi.OPT_GATHER_WORKGROUPS, wgs)
+    ctx.set_option(K._capi.OPT_GATHER_CHUNK_ROWS, chunk)
+    try:
+        planes = [K.make_plane(pin, K.FMT_Q8_0, width, tokens, K.GATHER_DEQUANT_F16, slots),
+                  K.make_plane(pin, K.FMT_Q8_0, width, tokens, K.GATHER_REQUANT_Q8_0, rq)]
+        ctx.stage_in(planes, pt, dev(sel), dev(np.array([k], np.uint32)), k)
+        ctx.check()
+    finally:
+        ctx.set_option(K._capi.OPT_GATHER_WORKGROUPS, 0)
+        ctx.set_option(K._capi.OPT_GATHER_CHUNK_ROWS, 0)
+    assert np.array_equal(host(slots, np.uint8), expect)
+    assert np.array_equal(host(rq, np.uint8), expect_rq)
+    pin.free()
