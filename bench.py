@@ -1,33 +1,32 @@
 #!/usr/bin/env python3
 """Recall hot path on one MI355X: select + stage-in per layer at 128K context.
 
-Workload (default, "resident64"): a 64-layer stack, 131072 tokens per layer,
-8 kv-heads x head_dim 128, fp16 K and V, pages of 256 tokens (512 pages),
-one decode query row of 32 q-heads (GQA group 4), Mean head aggregation,
-top-32 pages per layer gathered (K and V) from pinned host history into an
-8192-token device slot array per layer.  K is resident in HBM for scoring;
-page summaries are rebuilt from it inside every select.
+Workload (default): a 64-layer stack, 131072 tokens per layer, 8 kv-heads x
+head_dim 128, fp16 K and V, pages of 256 tokens (512 pages), one decode query
+row of 32 q-heads (GQA group 4), Mean head aggregation, top-32 pages per
+layer gathered (K and V) from pinned host history into an 8192-token device
+slot array per layer.  K is resident in HBM for scoring; page summaries are
+rebuilt from it inside every select.
 
-One step = the whole stack: per layer kvr_recall_layer (summary + logits +
-softmax + top-k on the select stream, gather on the copy stream after an
-event), so layer l's stage-in overlaps layer l+1's select.
+Timed step: scoring + selection of the whole stack (kvr_recall_layer per
+layer without planes, one select stream, descriptors built beforehand).
 
 Reported:
-  value       scored-KV GB/s = (K bytes + fp16 summary bytes + Q bytes) per
-              layer / select time per layer (HIP events on the select stream
-              inside the timed region)
-  roofline    the summary kernel (dominant): algorithmic bytes per launch /
-              its mean duration (HIP events recorded around it by the library)
-  latency     pipelined select+stage-in time per layer = step time / layers
-  stage-in    gather GB/s per layer (separate pass) vs measured pinned H2D peak
+  value        scored-KV GB/s = layers x (K bytes + fp16 summary bytes +
+               Q bytes) / step time
+  roofline     the summary kernel (dominant): algorithmic bytes per launch /
+               its mean duration (HIP events the library records around it on
+               the select stream, inside the timed steps)
+  latency      select + stage-in per layer with every layer's stage-in on one
+               copy stream beside the following selects (latency_us_per_layer)
+  stage-in     gather GB/s per layer (separate pass) vs measured pinned H2D peak
   cpu_baseline the reference's own CPU select path (oracle/_ref: RawKvStore
-              fp16 capture + mean_k + page_softmax_scores + pick_scored_blocks),
-              single thread, on a bounded sample of layers
+               fp16 capture + mean_k + page_softmax_scores + pick_scored_blocks),
+               single thread, on a bounded sample of layers
 """
 from __future__ import annotations
 
 import argparse
-import ctypes as C
 import json
 import os
 import sys
@@ -39,44 +38,6 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0
-
-
-class Hip:
-    """The few HIP runtime calls the benchmark needs for events and copies."""
-
-    def __init__(self):
-        self.lib = C.CDLL("libamdhip64.so")
-        L = self.lib
-        L.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
-        L.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
-        L.hipEventSynchronize.argtypes = [C.c_void_p]
-        L.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
-        L.hipEventDestroy.argtypes = [C.c_void_p]
-        L.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
-        L.hipDeviceSynchronize.argtypes = []
-
-    def ok(self, e, what):
-        if e != 0:
-            raise RuntimeError(f"{what}: hip error {e}")
-
-    def event(self):
-        e = C.c_void_p()
-        self.ok(self.lib.hipEventCreate(C.byref(e)), "hipEventCreate")
-        return e.value
-
-    def record(self, ev, stream):
-        self.ok(self.lib.hipEventRecord(ev, stream), "hipEventRecord")
-
-    def elapsed_ms(self, a, b) -> float:
-        ms = C.c_float()
-        self.ok(self.lib.hipEventElapsedTime(C.byref(ms), a, b), "hipEventElapsedTime")
-        return ms.value
-
-    def d2h(self, dst, src, n):
-        self.ok(self.lib.hipMemcpy(dst, src, n, 2), "hipMemcpy D2H")
-
-    def sync(self):
-        self.ok(self.lib.hipDeviceSynchronize(), "hipDeviceSynchronize")
 
 
 def log(msg):
@@ -136,12 +97,15 @@ def _cpu_model():
 def run(args):
     import torch
     import kvmem_amd as K
+    from kvmem_amd.hip import runtime
 
-    hip = Hip()
-    ctx = K.Context(0)
-    ctx.set_option(K._capi.OPT_GATHER_WORKGROUPS, args.gather_wgs)
-    ctx.set_option(K._capi.OPT_GATHER_CHUNK_ROWS, args.chunk_rows)
-    ctx.set_option(K._capi.OPT_GATHER_THREADS, args.gather_threads)
+    hip = runtime()
+    ctxs = [K.Context(0)]
+    for c in ctxs:
+        c.set_option(K._capi.OPT_GATHER_WORKGROUPS, args.gather_wgs)
+        c.set_option(K._capi.OPT_GATHER_CHUNK_ROWS, args.chunk_rows)
+        c.set_option(K._capi.OPT_GATHER_THREADS, args.gather_threads)
+    ctx = ctxs[0]
     L, T, HKV, D, HQ, PT, KSEL, R = args.layers, 131072, 8, 128, 32, 256, 32, 1
     W = HKV * D
     P = T // PT
@@ -192,64 +156,86 @@ def run(args):
     queries = [K.make_query(dev_q[l], K.FMT_F16, R, HQ, HKV, D) for l in range(L)]
     planes = [[K.make_plane(pins[l % ring][0], K.FMT_F16, W, T, K.GATHER_COPY, kslots[l]),
                K.make_plane(pins[l % ring][1], K.FMT_F16, W, T, K.GATHER_COPY, vslots[l])] for l in range(L)]
-    ev = {n: [hip.event() for _ in range(L)] for n in ("sb", "se", "kb", "ke")}
-    step_a, step_b = hip.event(), hip.event()
-    sel_stream, copy_stream = ctx.select_stream, ctx.copy_stream
+    copy_stream = ctx.copy_stream  # every layer's stage-in, in layer order
 
-    def step(timed_events: bool):
+    # Every event recorded between two kernels of the select stream costs a
+    # few microseconds of stream time, so per-layer events go on a sample of
+    # layers (every 8th, plus the first and last for the stack's span).
+    sampled = sorted(set(range(3, L, 8)) | {0, L - 1})
+
+    def events():
+        return {n: {l: hip.event() for l in sampled} for n in ("kb", "ke", "se")}
+
+    def descriptors(ev, with_planes):
+        return [K.Context.layer_recall(keys=keys[l], summaries=s16[l], query=queries[l], scores=scores[l],
+                                       selected=sel[l], count=cnt[l], k=KSEL, aggregation=K.AGG_MEAN,
+                                       planes=planes[l] if with_planes else (), engine=engine,
+                                       summary_events=(ev["kb"][l], ev["ke"][l]) if l in ev["kb"] else (None, None),
+                                       select_end=ev["se"].get(l))
+                for l in range(L)]
+
+    def stack(descs, ev):
         for l in range(L):
-            if timed_events:
-                hip.record(ev["sb"][l], sel_stream)
-            ctx.recall_layer(keys=keys[l], summaries=s16[l], query=queries[l], scores=scores[l],
-                             selected=sel[l], count=cnt[l], k=KSEL, aggregation=K.AGG_MEAN,
-                             planes=planes[l], engine=engine,
-                             summary_events=(ev["kb"][l], ev["ke"][l]) if timed_events else (None, None))
-            if timed_events:
-                hip.record(ev["se"][l], sel_stream)
+            ctx.recall(descs[l], None, copy_stream)
 
+    def drain():
+        for c in ctxs:
+            c.check()
+
+    def layer_times(ev):
+        """sampled layers: summary kernel, summary start -> selection written"""
+        inner = [l for l in sampled if 0 < l < L - 1] or sampled
+        kern = [hip.elapsed_ms(ev["kb"][l], ev["ke"][l]) * 1e3 for l in inner]
+        selt = [hip.elapsed_ms(ev["kb"][l], ev["se"][l]) * 1e3 for l in inner]
+        return kern, selt, hip.elapsed_ms(ev["kb"][0], ev["se"][L - 1]) * 1e3
+
+    # ---- timed: scoring + selection of the whole stack ----------------------
+    ev_w = events()
+    d_w = descriptors(ev_w, False)
     for _ in range(args.warmup):
-        step(False)
-        ctx.check()
-    sel_ms, kern_ms = [], []
+        stack(d_w, ev_w)
+        drain()
+    ev_t = [events() for _ in range(args.steps)]
+    d_t = [descriptors(e, False) for e in ev_t]
+    drain()
     torch.cuda.synchronize()
-    ctx.check()
     t0 = time.perf_counter()
-    hip.record(step_a, sel_stream)
     for s in range(args.steps):
-        step(True)
-        # per-layer select / summary-kernel durations of this step
-        ctx.check()
-        sel_ms.extend(hip.elapsed_ms(ev["sb"][l], ev["se"][l]) for l in range(L))
-        kern_ms.extend(hip.elapsed_ms(ev["kb"][l], ev["ke"][l]) for l in range(L))
-    ctx.check()
+        stack(d_t[s], ev_t[s])
+    drain()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    wall_ms = (t1 - t0) * 1e3
-    ms_per_step = wall_ms / args.steps
-    select_us = float(np.mean(sel_ms)) * 1e3
-    kern_us = float(np.mean(kern_ms)) * 1e3
-    log(f"step {ms_per_step:.3f} ms ({ms_per_step / L * 1e3:.1f} us/layer pipelined); "
-        f"select {select_us:.1f} us/layer; summary kernel {kern_us:.1f} us")
+    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    kern_us, sel_us, stack_us = [], [], []
+    for e in ev_t:
+        a, b, c = layer_times(e)
+        kern_us += a
+        sel_us += b
+        stack_us.append(c)
+    kern_us_mean = float(np.mean(kern_us))
+    select_us = float(np.mean(sel_us))
+    stack_gpu_us = float(np.mean(stack_us))
+    log(f"select stack {ms_per_step:.3f} ms/step ({ms_per_step / L * 1e3:.1f} us/layer; GPU "
+        f"{stack_gpu_us / L:.1f} us/layer); per layer: summary kernel {kern_us_mean:.1f} us, "
+        f"summary start -> selection {select_us:.1f} us")
 
-    # ---- select alone (no gather beside it) ---------------------------------
-    iso_sel, iso_kern = [], []
+    # ---- pipelined recall: each layer's stage-in beside the next selects ---
+    ev_p = events()
+    d_p = descriptors(ev_p, True)
     for rep in range(2):
-        for l in range(L):
-            hip.record(ev["sb"][l], sel_stream)
-            ctx.recall_layer(keys=keys[l], summaries=s16[l], query=queries[l], scores=scores[l],
-                             selected=sel[l], count=cnt[l], k=KSEL, aggregation=K.AGG_MEAN,
-                             summary_events=(ev["kb"][l], ev["ke"][l]))
-            hip.record(ev["se"][l], sel_stream)
-        ctx.check()
-        if rep:
-            iso_sel = [hip.elapsed_ms(ev["sb"][l], ev["se"][l]) for l in range(L)]
-            iso_kern = [hip.elapsed_ms(ev["kb"][l], ev["ke"][l]) for l in range(L)]
-    iso_select_us = float(np.mean(iso_sel)) * 1e3
-    iso_kern_us = float(np.mean(iso_kern)) * 1e3
-    log(f"select alone {iso_select_us:.1f} us/layer; summary kernel alone {iso_kern_us:.1f} us")
+        drain()
+        p0 = time.perf_counter()
+        stack(d_p, ev_p)
+        drain()
+        p1 = time.perf_counter()
+    pipe_us = (p1 - p0) * 1e6 / L
+    pk, ps, _ = layer_times(ev_p)
+    pipe_kern_us, pipe_sel_us = float(np.mean(pk)), float(np.mean(ps))
+    log(f"select+stage-in pipelined {pipe_us:.1f} us/layer; beside the stage-in: summary kernel "
+        f"{pipe_kern_us:.1f} us, summary start -> selection {pipe_sel_us:.1f} us")
 
     # ---- stage-in alone (same selections, copy stream) ---------------------
-    stage_ms = []
+    stage_us = []
     a, b = hip.event(), hip.event()
     for rep in range(2):
         for l in range(L):
@@ -258,8 +244,8 @@ def run(args):
             hip.record(b, copy_stream)
             ctx.check()
             if rep:
-                stage_ms.append(hip.elapsed_ms(a, b))
-    stage_us = float(np.mean(stage_ms)) * 1e3
+                stage_us.append(hip.elapsed_ms(a, b) * 1e3)
+    stage_us = float(np.mean(stage_us))
     h2d = ctx.h2d_peak_gbps(1 << 30, 5)
     stage_gbps = stage_bytes / (stage_us * 1e-6) / 1e9
     log(f"stage-in {stage_us:.1f} us/layer = {stage_gbps:.2f} GB/s; pinned H2D peak {h2d:.2f} GB/s")
@@ -268,8 +254,8 @@ def run(args):
     assert (cnt.cpu().numpy() == KSEL).all(), "every layer must select k pages"
 
     alg_kernel_bytes = k_bytes + P * W * 2 + HQ * R * P * 8 + HQ * D * 2
-    achieved = alg_kernel_bytes / (kern_us * 1e-6) / 1e9
-    scored_gbps = geo["scored_bytes"] / (select_us * 1e-6) / 1e9
+    achieved = alg_kernel_bytes / (kern_us_mean * 1e-6) / 1e9
+    scored_gbps = L * geo["scored_bytes"] / (ms_per_step * 1e-3) / 1e9
     traffic = None
     pmc = os.path.join(ROOT, "profiles", "pmc_summary_resident64.json")
     if os.path.exists(pmc):
@@ -293,6 +279,8 @@ def run(args):
         "data": f"synthetic seeded N(0,1) (Irwin-Hall 12), seed {args.seed}",
         "config": {
             "workload": "resident-history scoring + recall, 64-layer stack at 131072 tokens",
+            "step": "summaries + scores + softmax + top-k for every layer (scored-KV throughput); "
+                    "stage-in measured pipelined and alone beside it",
             "layers": L, "tokens": T, "kv_heads": HKV, "head_dim": D, "query_heads": HQ,
             "query_rows": R, "page_tokens": PT, "pages": P, "top_k": KSEL,
             "aggregation": "mean", "gather": "fp16 K+V copy into 8192-token slots",
@@ -300,11 +288,12 @@ def run(args):
             "gather_workgroups": args.gather_wgs or 64, "gather_chunk_rows": args.chunk_rows or 8,
         },
         "select_us_per_layer": round(select_us, 2),
-        "select_alone_us_per_layer": round(iso_select_us, 2),
-        "summary_kernel_alone_us": round(iso_kern_us, 2),
-        "stagein_us_per_layer": round(stage_us, 2),
-        "latency_us_per_layer": round(ms_per_step / L * 1e3, 2),
+        "select_stack_us_per_layer": round(ms_per_step / L * 1e3, 2),
         "scored_frac_hbm": round(scored_gbps / HBM_PEAK_GBPS, 4),
+        "latency_us_per_layer": round(pipe_us, 2),
+        "select_us_beside_stagein": round(pipe_sel_us, 2),
+        "summary_kernel_beside_stagein_us": round(pipe_kern_us, 2),
+        "stagein_us_per_layer": round(stage_us, 2),
         "stagein_GBps": round(stage_gbps, 3),
         "h2d_peak_GBps": round(h2d, 3),
         "stagein_frac_h2d": round(stage_gbps / h2d, 4),
@@ -317,14 +306,54 @@ def run(args):
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
             "bytes_per_launch": alg_kernel_bytes,
-            "mean_launch_us": round(kern_us, 3),
+            "mean_launch_us": round(kern_us_mean, 3),
         },
     }
     if not args.no_cpu:
         log("CPU baseline ...")
         line["cpu_baseline"] = cpu_baseline(args, geo, gpu_sel, dev_k, dev_q)
-    ctx.close()
+    for c in ctxs:
+        c.close()
     print(json.dumps(line), flush=True)
+
+
+def pmc_pass(args):
+    """Counter pass (run under rocprofv3 --pmc): three selects of one
+    128K-token layer (fused summary kernel over 256 MiB of fp16 K) and three
+    256 MiB device copies (4096 ops of 64 KiB, k_copy_ops) that calibrate
+    FETCH_SIZE / WRITE_SIZE against known byte counts."""
+    import torch
+    import kvmem_amd as K
+    T, HKV, D, HQ, PT, KSEL = 131072, 8, 128, 32, 256, 32
+    W, P = HKV * D, T // PT
+    ctx = K.Context(0)
+    kd = torch.empty(T * W, dtype=torch.int16, device="cuda")
+    qd = torch.empty(HQ * D, dtype=torch.int16, device="cuda")
+    dst = torch.empty(T * W, dtype=torch.int16, device="cuda")
+    s16 = torch.empty(P * W, dtype=torch.int16, device="cuda")
+    scores = torch.empty(P, dtype=torch.float64, device="cuda")
+    sel = torch.empty(KSEL, dtype=torch.int32, device="cuda")
+    cnt = torch.empty(1, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    ctx.synth_normal_f16(args.seed, 1000, T * W, kd)
+    ctx.synth_normal_f16(args.seed, 3000, HQ * D, qd)
+    ctx.check()
+    keys = K.make_keys(kd, K.FMT_F16, T, HKV, D, PT)
+    query = K.make_query(qd, K.FMT_F16, 1, HQ, HKV, D)
+    for _ in range(3):
+        ctx.recall_layer(keys=keys, summaries=s16, query=query, scores=scores, selected=sel, count=cnt,
+                         k=KSEL, aggregation=K.AGG_MEAN)
+        ctx.check()
+    op = 1 << 16
+    n = T * W * 2 // op
+    srcs = [kd.data_ptr() + i * op for i in range(n)]
+    dsts = [dst.data_ptr() + i * op for i in range(n)]
+    for _ in range(3):
+        ctx.d2d_batched(srcs, dsts, [op] * n)
+        ctx.check()
+    ctx.close()
+    print(json.dumps({"pass": "pmc", "summary_bytes_read": T * W * 2 + HQ * D * 2,
+                      "copy_bytes": T * W * 2, "copy_ops": n}), flush=True)
 
 
 def main():
@@ -338,9 +367,10 @@ def main():
     ap.add_argument("--gather-wgs", type=int, default=0, help="gather grid bound (0 = library default)")
     ap.add_argument("--chunk-rows", type=int, default=0, help="gather rows per work item (0 = default)")
     ap.add_argument("--gather-threads", type=int, default=0, help="gather workgroup size (0 = default)")
-    ap.add_argument("--skip-alone", action="store_true", help="skip the isolated select and stage-in passes")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="only the short counter pass (one layer's selects + calibration copies)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -348,6 +378,9 @@ def main():
             print("bench.py measures one GPU: the recall path runs on a single MI355X in this build "
                   "(multi-GPU sharding is a design note, not a measured mode). Use --gpus 1.", flush=True)
         sys.exit(2)
+    if args.pmc_pass:
+        pmc_pass(args)
+        return
     run(args)
 
 

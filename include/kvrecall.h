@@ -18,7 +18,16 @@
  *    context's own streams.  Calls are asynchronous on their stream.  Device
  *    side operand errors (a query or summary value that is non-finite or
  *    rounds to fp16 infinity) make the selection of that call empty and are
- *    reported by kvr_check().
+ *    reported by kvr_check(); a raised error stays raised until kvr_check
+ *    reports it.
+ *  - Graph capture: the scoring, selection and kernel-engine gather entries
+ *    allocate nothing and never wait on the host once the context's
+ *    workspace is large enough, so they may be recorded into a HIP graph
+ *    (hipStreamBeginCapture on the select stream; the copy stream joins
+ *    through an event and must be joined back before capture ends).  Run
+ *    each shape once before capture, or bind a workspace: growth during
+ *    capture fails with KVR_ERR_WORKSPACE.  The DMA stage-in engine reads
+ *    the selection on the host and refuses capture.
  *  - A context is used by one host thread at a time.
  *
  * Reference citations are relative to the KVMem 0.19.0 source tree.
@@ -148,7 +157,12 @@ typedef struct kvr_layer_recall {
     int force_mfma;                /* -1 never, 0 by rows*group >= 16, 1 always */
     void *summary_begin;           /* optional hipEvent_t recorded on the select
                                       stream just before / after the summary */
-    void *summary_end;             /* kernel (measurement only; may be NULL)  */
+    void *summary_end;             /* kernel (measurement only; may be NULL;
+                                      refused while the stream is captured)  */
+    void *select_end;              /* optional hipEvent_t recorded on the select
+                                      stream once the selection is written,
+                                      before any stage-in is enqueued (same
+                                      rules as the summary events)           */
 } kvr_layer_recall;
 
 /* ---- context ------------------------------------------------------------ */

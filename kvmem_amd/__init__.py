@@ -95,6 +95,7 @@ def make_query(t, scalar: int, rows: int, query_heads: int, kv_heads: int, head_
     q.rows, q.query_heads, q.kv_heads, q.head_dim = rows, query_heads, kv_heads, head_dim
     q.row_stride, q.head_stride, q.dim_stride, q.lane_stride = (s * el for s in strides)
     q.attention_scale = attention_scale
+    q._keep = t  # the device buffer lives as long as the descriptor
     return q
 
 
@@ -105,6 +106,7 @@ def make_keys(t, fmt: int, tokens: int, kv_heads: int, head_dim: int, page_token
     k.format = fmt
     k.tokens, k.kv_heads, k.head_dim, k.page_tokens = tokens, kv_heads, head_dim, page_tokens
     k.lanes, k.lane_stride = lanes, lane_stride
+    k._keep = t
     return k
 
 
@@ -115,6 +117,7 @@ def make_plane(history, fmt: int, width: int, tokens: int, mode: int, slots,
     p.format, p.width, p.tokens, p.mode = fmt, width, tokens, mode
     p.slots = _ptr(slots)
     p.host_lane_stride, p.slot_lane_stride = host_lane_stride, slot_lane_stride
+    p._keep = (history, slots)
     return p
 
 
@@ -207,16 +210,17 @@ class Context:
         check(lib().kvr_stage_in(self.handle, arr, len(planes), lanes, page_tokens, _ptr(selected),
                                  _ptr(count), k, engine, stream))
 
-    def recall_layer(self, *, query, summaries, scores, selected, count, k, keys=None, means=None,
+    @staticmethod
+    def layer_recall(*, query, summaries, scores, selected, count, k, keys=None, means=None,
                      pages=0, page_tokens=0, lanes=0, score_mask=None, aggregation=AGG_MEAN,
                      tie_rule=TIE_LOWER_FIRST, mandatory: Sequence[int] = (), planes: Sequence = (),
-                     engine=ENGINE_AUTO, force_mfma=0, select_stream=None, copy_stream=None,
-                     summary_events=(None, None)) -> None:
+                     engine=ENGINE_AUTO, force_mfma=0, summary_events=(None, None),
+                     select_end=None) -> "_capi.LayerRecall":
+        """A kvr_layer_recall descriptor (holding what it points to), for
+        callers that issue the same layer many times."""
         d = _capi.LayerRecall()
-        keep = []
         if keys is not None:
             d.keys = C.pointer(keys)
-            keep.append(keys)
         d.summaries, d.means = _ptr(summaries), _ptr(means)
         d.pages, d.page_tokens, d.lanes = pages, page_tokens, lanes
         d.query = C.pointer(query)
@@ -229,7 +233,16 @@ class Context:
         d.planes, d.n_planes = parr, len(planes)
         d.engine, d.force_mfma = engine, force_mfma
         d.summary_begin, d.summary_end = summary_events
-        check(lib().kvr_recall_layer(self.handle, C.byref(d), select_stream, copy_stream))
+        d.select_end = select_end
+        d._keep = (keys, query, summaries, means, score_mask, scores, selected, count, mand, parr, list(planes))
+        return d
+
+    def recall(self, desc, select_stream=None, copy_stream=None) -> None:
+        """kvr_recall_layer on a prebuilt descriptor."""
+        check(lib().kvr_recall_layer(self.handle, C.byref(desc), select_stream, copy_stream))
+
+    def recall_layer(self, *, select_stream=None, copy_stream=None, **kw) -> None:
+        self.recall(self.layer_recall(**kw), select_stream, copy_stream)
 
     def d2d_batched(self, srcs: Sequence[int], dsts: Sequence[int], sizes: Sequence[int], stream=None) -> None:
         n = len(srcs)

@@ -51,7 +51,8 @@ class LayerRecall(C.Structure):
                 ("score_mask", _P), ("aggregation", _i), ("k", _u32), ("tie_rule", _i),
                 ("mandatory", C.POINTER(_u32)), ("n_mandatory", _u32), ("scores", _P),
                 ("selected", _P), ("count", _P), ("planes", C.POINTER(Plane)), ("n_planes", _u32),
-                ("engine", _i), ("force_mfma", _i), ("summary_begin", _P), ("summary_end", _P)]
+                ("engine", _i), ("force_mfma", _i), ("summary_begin", _P), ("summary_end", _P),
+                ("select_end", _P)]
 
 
 _SIGNATURES = {

@@ -23,7 +23,9 @@ struct kvr_context {
     hipStream_t sel = nullptr, copy = nullptr;
     hipEvent_t ev_sel = nullptr;   // select work done -> copy stream may read the selection
     uint32_t *status = nullptr;    // dev [kStatusWords]
-    uint32_t epoch = 0, checked = 0;
+    uint32_t *counters = nullptr;  // dev [counters_cap], zero between launches
+    uint32_t counters_cap = 0;
+    uint32_t epoch = 0;
     uint8_t *ws = nullptr;
     size_t ws_bytes = 0;
     bool ws_borrowed = false;
@@ -105,6 +107,12 @@ hipStream_t stream_or(void *s, hipStream_t fallback) {
     return s ? static_cast<hipStream_t>(s) : fallback;
 }
 
+// True while `s` records into a graph: such calls may not allocate or wait.
+bool capturing(hipStream_t s) {
+    hipStreamCaptureStatus c = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(s, &c) == hipSuccess && c != hipStreamCaptureStatusNone;
+}
+
 double logit_scale(float attention_scale, uint32_t dim) {
     return attention_scale > 0 ? double(attention_scale) : 1 / std::sqrt(double(dim));
 }
@@ -159,11 +167,14 @@ uint32_t stage_query(const kvr::QueryArgs &q) {
     return uint64_t(q.rows) * q.qheads * q.dim * 2 <= 32768 ? 1u : 0u;
 }
 
-kvr_status ensure_workspace(kvr_context *ctx, size_t bytes) {
+kvr_status ensure_workspace(kvr_context *ctx, size_t bytes, hipStream_t s) {
     if (bytes <= ctx->ws_bytes) return KVR_OK;
     if (ctx->ws_borrowed)
         return fail(KVR_ERR_WORKSPACE, "call needs %zu workspace bytes, borrowed workspace has %zu", bytes,
                     ctx->ws_bytes);
+    if (capturing(s))
+        return fail(KVR_ERR_WORKSPACE, "call needs %zu workspace bytes (have %zu) while its stream is captured; "
+                                       "run it once before capture or bind a workspace", bytes, ctx->ws_bytes);
     KVR_HIP(hipStreamSynchronize(ctx->sel));
     KVR_HIP(hipStreamSynchronize(ctx->copy));
     if (ctx->ws) KVR_HIP(hipFree(ctx->ws));
@@ -171,6 +182,25 @@ kvr_status ensure_workspace(kvr_context *ctx, size_t bytes) {
     ctx->ws_bytes = 0;
     KVR_HIP(hipMalloc(&ctx->ws, bytes));
     ctx->ws_bytes = bytes;
+    return KVR_OK;
+}
+
+// Per-lane completion counters of the softmax launch (zero between launches).
+kvr_status ensure_counters(kvr_context *ctx, uint32_t lanes, hipStream_t s) {
+    if (lanes <= ctx->counters_cap) return KVR_OK;
+    if (capturing(s))
+        return fail(KVR_ERR_WORKSPACE, "%u lanes need new counters while the stream is captured; "
+                                       "run the shape once before capture", lanes);
+    KVR_HIP(hipStreamSynchronize(ctx->sel));
+    KVR_HIP(hipStreamSynchronize(ctx->copy));
+    if (ctx->counters) KVR_HIP(hipFree(ctx->counters));
+    ctx->counters = nullptr;
+    ctx->counters_cap = 0;
+    const uint32_t cap = std::max<uint32_t>(lanes, 64);
+    KVR_HIP(hipMalloc(&ctx->counters, cap * sizeof(uint32_t)));
+    KVR_HIP(hipMemset(ctx->counters, 0, cap * sizeof(uint32_t)));
+    KVR_HIP(hipDeviceSynchronize());
+    ctx->counters_cap = cap;
     return KVR_OK;
 }
 
@@ -211,7 +241,7 @@ struct ScorePlan {
 };
 
 kvr_status plan_score(kvr_context *ctx, const kvr_query *q, uint32_t lanes, uint32_t pages,
-                      int force_mfma, ScorePlan &p) {
+                      int force_mfma, hipStream_t stream, ScorePlan &p) {
     if (kvr_status s = check_query(q, lanes)) return s;
     if (!pages) return fail(KVR_ERR_INVALID, "no pages to score");
     p.q = query_args(q);
@@ -229,7 +259,7 @@ kvr_status plan_score(kvr_context *ctx, const kvr_query *q, uint32_t lanes, uint
         return fail(KVR_ERR_INVALID, "head_dim %u: vector scoring needs 8*2^i <= 512", q->head_dim);
     const size_t lb = logits_bytes(lanes, pages, q->rows, q->query_heads);
     const size_t qb = p.mfma ? qpack_bytes(lanes, q->rows, q->query_heads, q->head_dim) : 0;
-    if (kvr_status s = ensure_workspace(ctx, lb + qb)) return s;
+    if (kvr_status s = ensure_workspace(ctx, lb + qb, stream)) return s;
     p.logits = reinterpret_cast<double *>(ctx->ws);
     p.qpack = reinterpret_cast<uint16_t *>(ctx->ws + lb);
     return KVR_OK;
@@ -241,28 +271,13 @@ kvr_status enqueue_probs_and_select(kvr_context *ctx, const ScorePlan &p, const 
                                     double *scores, bool do_select, uint32_t k, kvr_tie_rule tie,
                                     const Mandatory &mand, uint32_t *selected, uint32_t *count,
                                     hipStream_t s) {
-    // A lane with at most 64 softmax units (rows, or GQA groups) is softmaxed
-    // inside the select kernel (one wave per unit); larger ones get their own
-    // grid-wide softmax launch first.
-    const uint64_t units = uint64_t(p.rows) * (agg == KVR_AGG_MEAN ? p.qheads : p.kvheads);
-    const bool fuse = units <= 64;
-    if (!fuse) {
-        kvr::SoftmaxArgs sm{};
-        sm.logits = p.logits;
-        sm.mask = mask;
-        sm.lanes = p.lanes;
-        sm.rows = p.rows;
-        sm.qheads = p.qheads;
-        sm.kvheads = p.kvheads;
-        sm.pages = p.pages;
-        sm.aggregation = uint32_t(agg);
-        KVR_HIP(kvr::launch_softmax(sm, s));
-    }
+    if (p.lanes > 65535) return fail(KVR_ERR_INVALID, "at most 65535 lanes per call");
+    if (kvr_status st = ensure_counters(ctx, p.lanes, s)) return st;
     kvr::SelectArgs sa{};
     sa.logits = p.logits;
     sa.mask = mask;
-    sa.do_softmax = fuse;
-    sa.probs = p.logits;
+    sa.units = p.rows * (agg == KVR_AGG_MEAN ? p.qheads : p.kvheads);
+    sa.counters = ctx->counters;
     sa.rows = p.rows;
     sa.qheads = p.qheads;
     sa.kvheads = p.kvheads;
@@ -283,7 +298,7 @@ kvr_status enqueue_probs_and_select(kvr_context *ctx, const ScorePlan &p, const 
     sa.count = count;
     sa.status = ctx->status;
     sa.epoch = ctx->epoch;
-    KVR_HIP(kvr::launch_select(sa, s));
+    KVR_HIP(kvr::launch_probs(sa, s));
     return KVR_OK;
 }
 
@@ -473,9 +488,7 @@ kvr_status enqueue_gather_sdma(kvr_context *ctx, PlanePlan *pp, uint32_t n, uint
                                uint32_t page_tokens, const uint32_t *selected, const uint32_t *count,
                                uint32_t k, hipStream_t s, hipEvent_t sel_ready = nullptr) {
     if (!n) return KVR_OK;
-    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-    KVR_HIP(hipStreamIsCapturing(s, &capture));
-    if (capture != hipStreamCaptureStatusNone)
+    if (capturing(s))
         return fail(KVR_ERR_INVALID, "the DMA stage-in engine reads the selection on the host and cannot be "
                                      "captured; use the kernel engine inside graphs");
     const size_t words = size_t(lanes) * (k + 1);
@@ -625,6 +638,7 @@ kvr_status kvr_destroy(kvr_context *ctx) {
     if (ctx->ws && !ctx->ws_borrowed) (void)hipFree(ctx->ws);
     if (ctx->staging) (void)hipFree(ctx->staging);
     if (ctx->status) (void)hipFree(ctx->status);
+    if (ctx->counters) (void)hipFree(ctx->counters);
     if (ctx->ops_dev) (void)hipFree(ctx->ops_dev);
     if (ctx->ops_pin) (void)hipHostFree(ctx->ops_pin);
     if (ctx->sel_pin) (void)hipHostFree(ctx->sel_pin);
@@ -678,15 +692,16 @@ kvr_status kvr_check(kvr_context *ctx, void *stream) {
     }
     uint32_t st[kvr::kStatusWords] = {};
     KVR_HIP(hipMemcpy(st, ctx->status, sizeof st, hipMemcpyDeviceToHost));
-    const uint32_t since = ctx->checked;
-    ctx->checked = ctx->epoch;
-    if (st[kvr::kStatusNonfinite] > since)
+    // A raised word holds the number of the call that raised it (graph
+    // replays repeat the number their capture gave them); reporting clears it.
+    if (!st[kvr::kStatusNonfinite] && !st[kvr::kStatusRange] && !st[kvr::kStatusScores]) return KVR_OK;
+    KVR_HIP(hipMemset(ctx->status, 0, sizeof st));
+    KVR_HIP(hipDeviceSynchronize());
+    if (st[kvr::kStatusNonfinite])
         return fail(KVR_ERR_NONFINITE, "nonfinite recall operand (call %u)", st[kvr::kStatusNonfinite]);
-    if (st[kvr::kStatusRange] > since)
+    if (st[kvr::kStatusRange])
         return fail(KVR_ERR_RANGE, "recall operand rounds to fp16 infinity (call %u)", st[kvr::kStatusRange]);
-    if (st[kvr::kStatusScores] > since)
-        return fail(KVR_ERR_SCORES, "negative or nonfinite score (call %u)", st[kvr::kStatusScores]);
-    return KVR_OK;
+    return fail(KVR_ERR_SCORES, "negative or nonfinite score (call %u)", st[kvr::kStatusScores]);
 }
 
 size_t kvr_workspace_bytes(uint32_t lanes, uint32_t max_pages, uint32_t max_rows, uint32_t query_heads,
@@ -795,9 +810,9 @@ kvr_status kvr_score(kvr_context *ctx, const kvr_query *q, const uint16_t *summa
     if (aggregation > KVR_AGG_MAX_LOGIT) return fail(KVR_ERR_INVALID, "unknown aggregation");
     if (!active_layers) return fail(KVR_ERR_INVALID, "active_layers must be >= 1");
     DeviceGuard guard(ctx->device);
-    ScorePlan p;
-    if (kvr_status s = plan_score(ctx, q, lanes, pages, force_mfma, p)) return s;
     const hipStream_t s = stream_or(stream, ctx->sel);
+    ScorePlan p;
+    if (kvr_status st = plan_score(ctx, q, lanes, pages, force_mfma, s, p)) return st;
     ++ctx->epoch;
     if (kvr_status st = enqueue_logits(ctx, p, summaries, s)) return st;
     Mandatory none;
@@ -878,13 +893,17 @@ kvr_status kvr_recall_layer(kvr_context *ctx, const kvr_layer_recall *d, void *s
     DeviceGuard guard(ctx->device);
     PlanePlan pp[KVR_MAX_PLANES];
     if (kvr_status s = check_planes(d->planes, d->n_planes, lanes, page_tokens, d->k, ctx->chunk_rows, pp)) return s;
-    ScorePlan p;
-    if (kvr_status s = plan_score(ctx, d->query, lanes, pages, d->force_mfma, p)) return s;
-    if (d->keys && !p.mfma && !valu_dim_ok(d->keys->head_dim))
-        return fail(KVR_ERR_INVALID, "head_dim %u unsupported by fused scoring", d->keys->head_dim);
-
     const hipStream_t ss = stream_or(select_stream, ctx->sel);
     const hipStream_t cs = stream_or(copy_stream, ctx->copy);
+    if ((d->summary_begin || d->summary_end || d->select_end) && capturing(ss))
+        return fail(KVR_ERR_INVALID, "summary timing events are not recorded inside a captured graph");
+    if (d->n_planes && d->engine == KVR_ENGINE_SDMA && (capturing(ss) || capturing(cs)))
+        return fail(KVR_ERR_INVALID, "the DMA stage-in engine reads the selection on the host and cannot be "
+                                     "captured; use the kernel engine inside graphs");
+    ScorePlan p;
+    if (kvr_status s = plan_score(ctx, d->query, lanes, pages, d->force_mfma, ss, p)) return s;
+    if (d->keys && !p.mfma && !valu_dim_ok(d->keys->head_dim))
+        return fail(KVR_ERR_INVALID, "head_dim %u unsupported by fused scoring", d->keys->head_dim);
     ++ctx->epoch;
     if (d->keys) {
         auto a = summary_args(ctx, d->keys, pages, key_ls, d->means, d->summaries);
@@ -907,6 +926,7 @@ kvr_status kvr_recall_layer(kvr_context *ctx, const kvr_layer_recall *d, void *s
     if (kvr_status st = enqueue_probs_and_select(ctx, p, d->score_mask, d->aggregation, 1, 0, d->scores, true, d->k,
                                                  d->tie_rule, m, d->selected, d->count, ss))
         return st;
+    if (d->select_end) KVR_HIP(hipEventRecord(static_cast<hipEvent_t>(d->select_end), ss));
     if (!d->n_planes) return KVR_OK;
     KVR_HIP(hipEventRecord(ctx->ev_sel, ss));
     if (cs != ss) KVR_HIP(hipStreamWaitEvent(cs, ctx->ev_sel, 0));

@@ -49,34 +49,91 @@ __device__ __forceinline__ bool epoch_failed(const uint32_t *status, uint32_t ep
 }
 
 // ---- wave reductions (64 lanes) --------------------------------------------
-template <class T> __device__ __forceinline__ T wave_sum(T v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
-}
-template <class T> __device__ __forceinline__ T wave_max(T v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const T w = __shfl_xor(v, o, kWave);
-        v = w > v ? w : v;
+// Cross-lane moves are DPP (VALU) within 16-lane rows and readlane across
+// rows; no LDS permutes.  Every lane gets the same result, combined in one
+// fixed order.
+namespace dpp {
+constexpr int kQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int kQuadXor2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kHalfMirror = 0x141;   // lane i <-> 7-i within each 8 lanes
+constexpr int kMirror = 0x140;       // lane i <-> 15-i within each row
+constexpr int kRowShr = 0x110;       // + n: lane i reads lane i-n of its row
+
+template <int CTRL, class T>
+__device__ __forceinline__ T move(T v) {
+    static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit lanes");
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf,
+                                                                 false));
+    } else {
+        const uint64_t u = __builtin_bit_cast(uint64_t, v);
+        const uint32_t lo = uint32_t(__builtin_amdgcn_update_dpp(0, int(uint32_t(u)), CTRL, 0xf, 0xf, false));
+        const uint32_t hi = uint32_t(__builtin_amdgcn_update_dpp(0, int(uint32_t(u >> 32)), CTRL, 0xf, 0xf, false));
+        return __builtin_bit_cast(T, (uint64_t(hi) << 32) | lo);
     }
+}
+
+template <class T>
+__device__ __forceinline__ T readlane(T v, int lane) {
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+    } else {
+        const uint64_t u = __builtin_bit_cast(uint64_t, v);
+        const uint32_t lo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(u)), lane));
+        const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(u >> 32)), lane));
+        return __builtin_bit_cast(T, (uint64_t(hi) << 32) | lo);
+    }
+}
+
+// op over aligned groups of `width` lanes (1, 2, 4, 8 or 16), every lane
+// of a group gets its group's result.
+template <class T, class Op>
+__device__ __forceinline__ T group_reduce(T v, int width, Op op) {
+    if (width >= 2) v = op(v, move<kQuadXor1>(v));
+    if (width >= 4) v = op(v, move<kQuadXor2>(v));
+    if (width >= 8) v = op(v, move<kHalfMirror>(v));
+    if (width >= 16) v = op(v, move<kMirror>(v));
     return v;
 }
+
+template <class T, class Op>
+__device__ __forceinline__ T wave_reduce(T v, Op op) {
+    v = group_reduce(v, 16, op);
+    return op(op(readlane(v, 0), readlane(v, 16)), op(readlane(v, 32), readlane(v, 48)));
+}
+
+struct Add { template <class T> __device__ T operator()(T a, T b) const { return a + b; } };
+struct Max { template <class T> __device__ T operator()(T a, T b) const { return b > a ? b : a; } };
+struct And { template <class T> __device__ T operator()(T a, T b) const { return a & b; } };
+struct Or { template <class T> __device__ T operator()(T a, T b) const { return a | b; } };
+}  // namespace dpp
+
+template <class T> __device__ __forceinline__ T wave_sum(T v) { return dpp::wave_reduce(v, dpp::Add()); }
+template <class T> __device__ __forceinline__ T wave_max(T v) { return dpp::wave_reduce(v, dpp::Max()); }
+__device__ __forceinline__ uint64_t wave_and(uint64_t v) { return dpp::wave_reduce(v, dpp::And()); }
+__device__ __forceinline__ uint64_t wave_or(uint64_t v) { return dpp::wave_reduce(v, dpp::Or()); }
+
 // Sum over aligned groups of `width` lanes (power of two <= 64).
 template <class T> __device__ __forceinline__ T group_sum(T v, int width) {
-    for (int o = width >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    v = dpp::group_reduce(v, width < 16 ? width : 16, dpp::Add());
+    for (int o = 16; o < width; o <<= 1) v += __shfl_xor(v, o, kWave);
     return v;
 }
-// Inclusive prefix sum over the wave.
+
+// Inclusive prefix sum over the wave: rows by DPP shifts, then the totals
+// of the rows below.
 __device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v) {
-    const int lane = threadIdx.x & (kWave - 1);
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-        const uint32_t w = __shfl_up(v, o, kWave);
-        if (lane >= o) v += w;
-    }
-    return v;
+    v += dpp::move<dpp::kRowShr + 1>(v);
+    v += dpp::move<dpp::kRowShr + 2>(v);
+    v += dpp::move<dpp::kRowShr + 4>(v);
+    v += dpp::move<dpp::kRowShr + 8>(v);
+    const uint32_t t0 = dpp::readlane(v, 15), t1 = dpp::readlane(v, 31), t2 = dpp::readlane(v, 47);
+    const uint32_t row = (threadIdx.x & (kWave - 1)) >> 4;
+    return v + (row >= 1 ? t0 : 0u) + (row >= 2 ? t1 : 0u) + (row >= 3 ? t2 : 0u);
 }
+
+// The value of lane `src` (uniform `src`).
+template <class T> __device__ __forceinline__ T wave_bcast(T v, int src) { return dpp::readlane(v, src); }
 
 // ---- block formats ---------------------------------------------------------
 constexpr int kQK = 32;

@@ -56,20 +56,14 @@ struct MfmaLogitsArgs {
     double *logits;             // [lanes][rows*qheads][pages]
 };
 
-struct SoftmaxArgs {
-    double *logits;            // [lanes][rows*qheads][pages], rewritten in place
-    const uint8_t *mask;       // [pages] or null
-    uint32_t lanes, rows, qheads, kvheads, pages;
-    uint32_t aggregation;
-};
-
 struct SelectArgs {
-    // softmax (do_softmax): the lane's logits rows, rewritten in place
-    double *logits;
-    const uint8_t *mask;
-    int do_softmax;
-    // aggregation (do_aggregate): scores[lane][p] (+)= sum_rows prob / weight
-    const double *probs;       // softmax output
+    // softmax units (k_probs): the lane's logits rows, overwritten with the
+    // units' aggregation terms; `units` per lane, counted in counters[lane]
+    double *logits;            // [lanes][rows*qheads][pages]
+    const uint8_t *mask;       // [pages] or null
+    uint32_t units;
+    uint32_t *counters;        // [lanes], zero between launches
+    // aggregation (do_aggregate): scores[lane][p] (+)= sum of the terms
     uint32_t rows, qheads, kvheads;
     uint32_t aggregation;
     double weight;             // active_layers * heads
@@ -145,7 +139,9 @@ struct CopyOp {
 hipError_t launch_summary(int source, bool fuse, const SummaryArgs &a, hipStream_t s);
 hipError_t launch_pack_query(const PackQueryArgs &a, hipStream_t s);
 hipError_t launch_logits_mfma(const MfmaLogitsArgs &a, hipStream_t s);
-hipError_t launch_softmax(const SoftmaxArgs &a, hipStream_t s);
+// page softmax -> terms -> aggregation (+ selection); grid (units, lanes)
+hipError_t launch_probs(const SelectArgs &a, hipStream_t s);
+// selection over given scores, one workgroup per lane
 hipError_t launch_select(const SelectArgs &a, hipStream_t s);
 hipError_t launch_gather(const GatherArgs &a, hipStream_t s);
 hipError_t launch_accumulate(const AccumulateArgs &a, hipStream_t s);

@@ -323,198 +323,180 @@ __global__ __launch_bounds__(256) void k_logits_mfma(MfmaLogitsArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Page softmax (graph_recall.cpp:362-372).  One wave per distribution:
-// p_j = exp(l_j - max) / sum over the score-mask pages; masked pages get 0.
+// Page softmax + head aggregation + top-k in one launch
+// (graph_recall.cpp:362-394, kvmem_store.cpp:418-451).
+//
+// One workgroup per softmax unit of a lane -- a (row, q-head) for Mean, a
+// (row, kv-head group) for Max and MaxLogit -- turns its logits into the
+// unit's aggregation terms, written over the unit's first logits row:
+//   Mean      t_j = p_j / w,                   p = softmax_j(logit_j)
+//   Max       t_j = (g_j / sum_j g_j) / w,     g_j = max_h p_{h,j}
+//   MaxLogit  t_j = softmax_j(max_h logit_{h,j}) / w
+// with w = active layers x q-heads (Mean) or x kv-heads (group rules), the
+// two divisions in the reference's order.  Masked pages get probability 0.
+// The lane's last unit to finish (a device-scope counter; no workgroup ever
+// waits for another) adds the terms in the reference's row order,
+// scores_j (+)= sum_i t_{i,j}, and selects.  Exponentials, sums and
+// quotients are binary64.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void softmax_wave(double *x, uint32_t n, const uint8_t *mask, uint32_t l) {
-    double m = -INFINITY;
-    for (uint32_t j = l; j < n; j += kWave)
-        if (!mask || mask[j]) m = fmax(m, x[j]);
-    m = wave_max(m);
-    double s = 0.0;
-    for (uint32_t j = l; j < n; j += kWave) {
-        const double e = (!mask || mask[j]) ? exp(x[j] - m) : 0.0;
-        x[j] = e;
-        s += e;
-    }
-    s = wave_sum(s);
-    for (uint32_t j = l; j < n; j += kWave) x[j] = s > 0.0 ? x[j] / s : 0.0;
+// Wave-synchronous LDS: orders this wave's LDS accesses before the ones that
+// follow (lanes of one wave read what other lanes of it wrote).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
 }
 
-template <class T, class Op>
-__device__ T block_reduce(T v, T *lds, Op op) {
-    // lds: >= blockDim.x/64 + 1 entries; deterministic fixed-order tree.
-    const uint32_t wave = threadIdx.x >> 6, l = threadIdx.x & 63, nw = blockDim.x >> 6;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = op(v, __shfl_xor(v, o, kWave));
-    if (l == 0) lds[wave] = v;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        T r = lds[0];
-        for (uint32_t w = 1; w < nw; ++w) r = op(r, lds[w]);
-        lds[nw] = r;
-    }
-    __syncthreads();
-    const T r = lds[nw];
-    __syncthreads();
-    return r;
-}
+constexpr uint32_t kUnitsPerBlock = 4;    // one softmax unit per wave
+constexpr uint32_t kTailLdsPages = 8192;  // keys of up to this many pages stay in LDS
 
-struct SumOp { __device__ double operator()(double a, double b) const { return a + b; } };
-struct AndOp { __device__ uint64_t operator()(uint64_t a, uint64_t b) const { return a & b; } };
-struct OrOp { __device__ uint64_t operator()(uint64_t a, uint64_t b) const { return a | b; } };
-struct MaxOp { __device__ double operator()(double a, double b) const { return b > a ? b : a; } };
-
-// The same with the row held in registers (NPL values per lane, pages <=
-// 64*NPL): one read and one write of the row.
+// Registers: value i of a lane is page j = l + 64*i.
 template <int NPL>
-__device__ __forceinline__ void softmax_wave_reg(double *x, uint32_t n, const uint8_t *mask, uint32_t l) {
-    double v[NPL];
+__device__ __forceinline__ void wave_softmax_regs(double (&v)[NPL], const bool (&on)[NPL]) {
     double m = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < NPL; ++i) {
-        const uint32_t j = l + i * kWave;
-        const bool on = j < n && (!mask || mask[j]);
-        v[i] = on ? x[j] : -INFINITY;
-        m = fmax(m, v[i]);
-    }
+    for (int i = 0; i < NPL; ++i) m = on[i] ? fmax(m, v[i]) : m;
     m = wave_max(m);
     double s = 0.0;
 #pragma unroll
     for (int i = 0; i < NPL; ++i) {
-        const uint32_t j = l + i * kWave;
-        const bool on = j < n && (!mask || mask[j]);
-        v[i] = on ? exp(v[i] - m) : 0.0;
+        v[i] = on[i] ? exp(v[i] - m) : 0.0;
         s += v[i];
     }
     s = wave_sum(s);
 #pragma unroll
+    for (int i = 0; i < NPL; ++i) v[i] = s > 0.0 ? v[i] / s : 0.0;
+}
+
+// One unit by one wave, rows of up to 64*NPL pages held in registers.
+template <int NPL>
+__device__ __forceinline__ void unit_terms_regs(const SelectArgs &a, double *lane_base, uint32_t unit) {
+    const uint32_t n = a.pages, l = threadIdx.x & 63;
+    bool on[NPL];
+#pragma unroll
     for (int i = 0; i < NPL; ++i) {
         const uint32_t j = l + i * kWave;
-        if (j < n) x[j] = s > 0.0 ? v[i] / s : 0.0;
+        on[i] = j < n && (!a.mask || a.mask[j]);
     }
-}
-
-template <int NPL>
-__global__ __launch_bounds__(256) void k_softmax_rows(SoftmaxArgs a) {
-    const uint64_t row = uint64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    if (row >= uint64_t(a.lanes) * a.rows * a.qheads) return;
-    if (NPL == 0)
-        softmax_wave(a.logits + row * a.pages, a.pages, a.mask, threadIdx.x & 63);
-    else
-        softmax_wave_reg<NPL ? NPL : 1>(a.logits + row * a.pages, a.pages, a.mask, threadIdx.x & 63);
-}
-
-// Register softmax for rows up to 1024 pages, global-memory passes beyond
-// (wider register rows would spill under the 1024-thread select kernel).
-__device__ __forceinline__ void softmax_any(double *x, uint32_t n, const uint8_t *mask, uint32_t l) {
-    if (n <= 64) softmax_wave_reg<1>(x, n, mask, l);
-    else if (n <= 128) softmax_wave_reg<2>(x, n, mask, l);
-    else if (n <= 256) softmax_wave_reg<4>(x, n, mask, l);
-    else if (n <= 512) softmax_wave_reg<8>(x, n, mask, l);
-    else if (n <= 1024) softmax_wave_reg<16>(x, n, mask, l);
-    else softmax_wave(x, n, mask, l);
-}
-
-// One GQA group by one wave (rows base + hh*n, hh < group); the result goes
-// to the group's first row.  Each lane only touches pages j == l (mod 64),
-// so its own stores are what it reads back.
-__device__ __forceinline__ void group_wave(double *base, uint32_t group, uint32_t n, const uint8_t *mask, uint32_t l,
-                           uint32_t aggregation) {
-    if (aggregation == kAggMax) {
-        for (uint32_t hh = 0; hh < group; ++hh) softmax_any(base + uint64_t(hh) * n, n, mask, l);
-        double s = 0.0;
-        for (uint32_t j = l; j < n; j += kWave) {
-            double gm = 0.0;
-            for (uint32_t hh = 0; hh < group; ++hh) {
-                const double p = base[uint64_t(hh) * n + j];
-                gm = p > gm ? p : gm;
-            }
-            base[j] = gm;
-            s += gm;
-        }
-        s = wave_sum(s);
-        for (uint32_t j = l; j < n; j += kWave) base[j] = s > 0.0 ? base[j] / s : 0.0;
+    double t[NPL];
+    double *out;
+    if (a.aggregation == kAggMean) {
+        out = lane_base + uint64_t(unit) * n;
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) t[i] = on[i] ? out[l + i * kWave] : 0.0;
+        wave_softmax_regs(t, on);
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) t[i] = t[i] / a.weight;
     } else {
-        double mx = -INFINITY;
-        for (uint32_t j = l; j < n; j += kWave) {
-            double gm = -INFINITY;
-            if (!mask || mask[j])
-                for (uint32_t hh = 0; hh < group; ++hh) gm = fmax(gm, base[uint64_t(hh) * n + j]);
-            base[j] = gm;
-            mx = fmax(mx, gm);
+        const uint32_t group = a.qheads / a.kvheads;
+        const uint32_t r = unit / a.kvheads, g = unit % a.kvheads;
+        out = lane_base + (uint64_t(r) * a.qheads + uint64_t(g) * group) * n;
+        if (a.aggregation == kAggMax) {
+            double gm[NPL];
+#pragma unroll
+            for (int i = 0; i < NPL; ++i) gm[i] = 0.0;
+            for (uint32_t hh = 0; hh < group; ++hh) {
+                const double *row = out + uint64_t(hh) * n;
+#pragma unroll
+                for (int i = 0; i < NPL; ++i) t[i] = on[i] ? row[l + i * kWave] : 0.0;
+                wave_softmax_regs(t, on);
+#pragma unroll
+                for (int i = 0; i < NPL; ++i) gm[i] = t[i] > gm[i] ? t[i] : gm[i];
+            }
+            double mass = 0.0;
+#pragma unroll
+            for (int i = 0; i < NPL; ++i) mass += gm[i];
+            mass = wave_sum(mass);
+#pragma unroll
+            for (int i = 0; i < NPL; ++i) t[i] = (mass > 0.0 ? gm[i] / mass : 0.0) / a.weight;
+        } else {
+#pragma unroll
+            for (int i = 0; i < NPL; ++i) t[i] = -INFINITY;
+            for (uint32_t hh = 0; hh < group; ++hh) {
+                const double *row = out + uint64_t(hh) * n;
+#pragma unroll
+                for (int i = 0; i < NPL; ++i)
+                    if (on[i]) t[i] = fmax(t[i], row[l + i * kWave]);
+            }
+            wave_softmax_regs(t, on);
+#pragma unroll
+            for (int i = 0; i < NPL; ++i) t[i] = t[i] / a.weight;
         }
-        mx = wave_max(mx);
-        double s = 0.0;
-        for (uint32_t j = l; j < n; j += kWave) {
-            const double e = (!mask || mask[j]) ? exp(base[j] - mx) : 0.0;
-            base[j] = e;
-            s += e;
-        }
-        s = wave_sum(s);
-        for (uint32_t j = l; j < n; j += kWave) base[j] = s > 0.0 ? base[j] / s : 0.0;
+    }
+    // every lane rewrites only pages it read itself
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+        const uint32_t j = l + i * kWave;
+        if (j < n) out[j] = t[i];
     }
 }
 
-// One workgroup per (lane, row, kv-head) group.
-//  Max (graph_recall.cpp:381-389): per-head softmax, g_j = max_h p_{h,j},
-//       first row of the group := g_j / sum_j g_j.
-//  MaxLogit: m_j = max_h logit_{h,j}; first row := softmax_j(m_j).
-__global__ __launch_bounds__(256) void k_softmax_groups(SoftmaxArgs a) {
-    __shared__ double red[8];
+// Rows longer than 1024 pages: lane-stride passes over memory; per-head
+// statistics first, then one pass per page.  Each lane touches only pages
+// j == l (mod 64).
+__device__ __forceinline__ void unit_terms_loop(const SelectArgs &a, double *lane_base, uint32_t unit) {
+    const uint32_t n = a.pages, l = threadIdx.x & 63;
+    auto on = [&](uint32_t j) { return !a.mask || a.mask[j]; };
+    auto stats = [&](const double *row, double &m, double &s) {
+        double mm = -INFINITY;
+        for (uint32_t j = l; j < n; j += kWave) mm = on(j) ? fmax(mm, row[j]) : mm;
+        m = wave_max(mm);
+        double ss = 0.0;
+        for (uint32_t j = l; j < n; j += kWave) ss += on(j) ? exp(row[j] - m) : 0.0;
+        s = wave_sum(ss);
+    };
+    auto prob = [&](double x, double m, double s) { return s > 0.0 ? exp(x - m) / s : 0.0; };
+    if (a.aggregation == kAggMean) {
+        double *row = lane_base + uint64_t(unit) * n;
+        double m, s;
+        stats(row, m, s);
+        for (uint32_t j = l; j < n; j += kWave) row[j] = (on(j) ? prob(row[j], m, s) : 0.0) / a.weight;
+        return;
+    }
     const uint32_t group = a.qheads / a.kvheads;
-    const uint32_t gi = blockIdx.x;
-    const uint32_t g = gi % a.kvheads;
-    const uint64_t lr = gi / a.kvheads;  // lane*rows + r
-    double *base = a.logits + (lr * a.qheads + uint64_t(g) * group) * a.pages;
-    const uint32_t wave = threadIdx.x >> 6, l = threadIdx.x & 63;
-    const uint32_t n = a.pages;
+    const uint32_t r = unit / a.kvheads, g = unit % a.kvheads;
+    double *out = lane_base + (uint64_t(r) * a.qheads + uint64_t(g) * group) * n;
     if (a.aggregation == kAggMax) {
-        for (uint32_t hh = wave; hh < group; hh += blockDim.x >> 6)
-            softmax_wave(base + uint64_t(hh) * n, n, a.mask, l);
-        __syncthreads();
-        double s = 0.0;
-        for (uint32_t j = threadIdx.x; j < n; j += blockDim.x) {
+        // each head's probabilities over its own row, then g_j into the first
+        for (uint32_t hh = 0; hh < group; ++hh) {
+            double *row = out + uint64_t(hh) * n;
+            double m, s;
+            stats(row, m, s);
+            for (uint32_t j = l; j < n; j += kWave) row[j] = on(j) ? prob(row[j], m, s) : 0.0;
+        }
+        double mass = 0.0;
+        for (uint32_t j = l; j < n; j += kWave) {
             double gm = 0.0;
             for (uint32_t hh = 0; hh < group; ++hh) {
-                const double p = base[uint64_t(hh) * n + j];
+                const double p = out[uint64_t(hh) * n + j];
                 gm = p > gm ? p : gm;
             }
-            base[j] = gm;
-            s += gm;
+            out[j] = gm;
+            mass += gm;
         }
-        const double mass = block_reduce(s, red, SumOp());
-        for (uint32_t j = threadIdx.x; j < n; j += blockDim.x) base[j] = mass > 0.0 ? base[j] / mass : 0.0;
+        mass = wave_sum(mass);
+        for (uint32_t j = l; j < n; j += kWave) out[j] = (mass > 0.0 ? out[j] / mass : 0.0) / a.weight;
     } else {
-        double mx = -INFINITY;
-        for (uint32_t j = threadIdx.x; j < n; j += blockDim.x) {
+        for (uint32_t j = l; j < n; j += kWave) {
             double gm = -INFINITY;
-            if (!a.mask || a.mask[j])
-                for (uint32_t hh = 0; hh < group; ++hh) gm = fmax(gm, base[uint64_t(hh) * n + j]);
-            base[j] = gm;
-            mx = fmax(mx, gm);
+            if (on(j))
+                for (uint32_t hh = 0; hh < group; ++hh) gm = fmax(gm, out[uint64_t(hh) * n + j]);
+            out[j] = gm;
         }
-        mx = block_reduce(mx, red, MaxOp());
-        double s = 0.0;
-        for (uint32_t j = threadIdx.x; j < n; j += blockDim.x) {
-            const double e = (!a.mask || a.mask[j]) ? exp(base[j] - mx) : 0.0;
-            base[j] = e;
-            s += e;
-        }
-        const double tot = block_reduce(s, red, SumOp());
-        for (uint32_t j = threadIdx.x; j < n; j += blockDim.x) base[j] = tot > 0.0 ? base[j] / tot : 0.0;
+        double m, s;
+        stats(out, m, s);
+        for (uint32_t j = l; j < n; j += kWave) out[j] = (on(j) ? prob(out[j], m, s) : 0.0) / a.weight;
     }
 }
 
 // ---------------------------------------------------------------------------
-// Aggregation + top-k, one 1024-thread workgroup per lane.
-// Aggregation sums the rows' probabilities in the reference's loop order
-// (graph_recall.cpp:375-389).  Selection restates KvMemStore::pick_scored_blocks
+// Selection restates KvMemStore::pick_scored_blocks
 // (kvmem/src/host/kvmem_store.cpp:418-451): mandatory pages first, then the
 // best (score desc, id by tie rule) up to k, output in ascending id order.
-// The k-th best key is found by an 8-pass MSB radix select over
-// order-preserving 64-bit keys; ties at the threshold are resolved by the
-// pages' rank among equal keys in id order.
+// One wave finds the k-th best of the order-preserving 64-bit keys by an MSB
+// radix select (8-bit digits in an LDS histogram, the leading bits common to
+// every candidate skipped, early exit once the boundary bucket is taken
+// whole) and compacts in id order with wave scans; ties at the threshold are
+// resolved by rank among equal keys in id order.  No workgroup barriers.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint64_t order_key(double v) {
     uint64_t u = uint64_t(__double_as_longlong(v));
@@ -531,172 +513,123 @@ __device__ __forceinline__ bool is_mandatory(const SelectArgs &a, uint32_t j) {
     return lo < a.n_mandatory && a.mandatory[lo] == j;
 }
 
-__device__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *total, uint32_t *lds) {
-    const uint32_t wave = threadIdx.x >> 6, l = threadIdx.x & 63, nw = blockDim.x >> 6;
-    const uint32_t incl = wave_inclusive_scan(v);
-    if (l == 63) lds[wave] = incl;
-    __syncthreads();
-    if (wave == 0) {
-        const uint32_t w = l < nw ? lds[l] : 0u;
-        const uint32_t wi = wave_inclusive_scan(w);
-        if (l < nw) lds[l] = wi - w;
-        if (l == nw - 1) lds[16] = wi;
+// Dynamic LDS of the selection kernels: the lane's keys (pages <= kTailLdsPages).
+extern __shared__ __align__(16) uint64_t tail_keys[];
+
+// Histogram pass of the radix select: counts keys matching `prefix` above
+// bit pos+8 by their digit at `pos`, then finds the digit holding the
+// `remaining`-th best.  `for_each_key(f)` calls f(key) for this lane's
+// candidate keys.  Returns false when the whole boundary bucket is taken.
+template <class ForEach>
+__device__ __forceinline__ bool radix_pass(ForEach for_each_key, uint32_t *hist, int pos, uint64_t &prefix,
+                                           uint32_t &remaining) {
+    const uint32_t l = threadIdx.x & 63;
+    const uint64_t hi_mask = pos + 8 >= 64 ? 0ull : ~0ull << (pos + 8);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) hist[l + 64 * q] = 0;
+    wave_lds_sync();
+    const uint64_t want = prefix & hi_mask;
+    for_each_key([&](uint64_t key) {
+        if ((key & hi_mask) == want) atomicAdd(&hist[(key >> pos) & 255u], 1u);
+    });
+    wave_lds_sync();
+    // lane l covers digits 255-4l .. 252-4l, highest first
+    const uint32_t c0 = hist[255 - 4 * l], c1 = hist[254 - 4 * l], c2 = hist[253 - 4 * l],
+                   c3 = hist[252 - 4 * l];
+    wave_lds_sync();
+    const uint32_t tot = c0 + c1 + c2 + c3;
+    const uint32_t incl = wave_inclusive_scan(tot);
+    const uint32_t excl = incl - tot;
+    const uint64_t owner = __ballot(excl < remaining && remaining <= incl);
+    const int b = __ffsll((long long)owner) - 1;  // the one lane holding the boundary
+    uint32_t rem = remaining - excl, d, cnt;
+    if (rem <= c0) {
+        d = 255 - 4 * l; cnt = c0;
+    } else if (rem <= c0 + c1) {
+        rem -= c0; d = 254 - 4 * l; cnt = c1;
+    } else if (rem <= c0 + c1 + c2) {
+        rem -= c0 + c1; d = 253 - 4 * l; cnt = c2;
+    } else {
+        rem -= c0 + c1 + c2; d = 252 - 4 * l; cnt = c3;
     }
-    __syncthreads();
-    const uint32_t r = lds[wave] + incl - v;
-    *total = lds[16];
-    __syncthreads();
-    return r;
+    d = wave_bcast(d, b);
+    rem = wave_bcast(rem, b);
+    cnt = wave_bcast(cnt, b);
+    prefix |= uint64_t(d) << pos;
+    remaining = rem;
+    return rem != cnt;
 }
 
-__global__ __launch_bounds__(1024) void k_select(SelectArgs a) {
-    __shared__ uint32_t hist[256];
-    __shared__ uint32_t scan_lds[17];
-    __shared__ uint64_t red_lds[17];
-    __shared__ uint32_t s_digit, s_remaining;
-    __shared__ bool s_exact;
-    const uint32_t lane = blockIdx.x, tid = threadIdx.x;
-    double *sc = a.scores + uint64_t(lane) * a.pages;
-    const uint32_t n = a.pages;
-
-    if (a.do_softmax) {
-        // Page softmax of this lane's rows (Mean) or GQA groups, one wave each.
-        const uint32_t wave = tid >> 6, l = tid & 63, nw = blockDim.x >> 6;
-        const uint32_t group = a.qheads / a.kvheads;
-        double *lane_base = a.logits + uint64_t(lane) * a.rows * a.qheads * n;
-        if (a.aggregation == kAggMean) {
-            for (uint32_t rho = wave; rho < a.rows * a.qheads; rho += nw)
-                softmax_any(lane_base + uint64_t(rho) * n, n, a.mask, l);
+// Selection of one lane by one wave.  Lane l owns the id chunk
+// [l*C, l*C + C), C = ceil(pages/64); CM > 0 holds the chunk's keys in
+// registers (C <= CM), CM == 0 reads them from LDS (`lds`) or from the
+// scores.
+//
+// Threshold search.  After it, with HT = thresh >> shift:
+//   (key >> shift) >  HT            selected
+//   (key >> shift) == HT && bucket  selected (the boundary bucket holds
+//                                   exactly the remaining count)
+//   key == thresh && !bucket        the first/last `remaining` equal keys
+//                                   by id (tie rule), shift == 0
+template <int CM>
+__device__ __forceinline__ void wave_select(const SelectArgs &a, uint32_t lane, bool lds, const double *sc,
+                                            uint32_t *hist) {
+    const uint32_t l = threadIdx.x & 63, n = a.pages;
+    const uint32_t C = (n + kWave - 1) / kWave;
+    const uint32_t j0 = min(n, l * C), j1 = min(n, j0 + C);
+    auto load_key = [&](uint32_t j) -> uint64_t { return lds ? tail_keys[j] : order_key(sc[j]); };
+    auto mand = [&](uint32_t j) { return a.n_mandatory && is_mandatory(a, j); };
+    constexpr int R = CM > 0 ? CM : 1;
+    uint64_t kr[R];
+    uint32_t cand_bits = 0;  // chunk entries that are candidates (register mode)
+    if (CM > 0) {
+#pragma unroll
+        for (int c = 0; c < R; ++c) {
+            const uint32_t j = j0 + c;
+            const bool in = j < j1;
+            kr[c] = in ? load_key(j) : 0;
+            if (in && !mand(j)) cand_bits |= 1u << c;
+        }
+    }
+    // f(key) over this lane's candidates
+    auto for_each_key = [&](auto f) {
+        if (CM > 0) {
+#pragma unroll
+            for (int c = 0; c < R; ++c)
+                if (cand_bits >> c & 1u) f(kr[c]);
         } else {
-            for (uint32_t gi = wave; gi < a.rows * a.kvheads; gi += nw) {
-                const uint32_t r = gi / a.kvheads, g = gi % a.kvheads;
-                group_wave(lane_base + (uint64_t(r) * a.qheads + g * group) * n, group, n, a.mask, l,
-                           a.aggregation);
-            }
+            for (uint32_t j = j0; j < j1; ++j)
+                if (!mand(j)) f(load_key(j));
         }
-        __syncthreads();
-    }
-    if (a.do_aggregate) {
-        const uint32_t group = a.qheads / a.kvheads;
-        const uint64_t lane_rows = uint64_t(lane) * a.rows * a.qheads;
-        // Contributing rows in the reference's order: (row, head) for Mean,
-        // (row, kv-head group) for the group rules.  Loads are issued eight
-        // at a time; the additions stay in order.
-        const bool mean = a.aggregation == kAggMean;
-        const uint32_t nrows = mean ? a.rows * a.qheads : a.rows * a.kvheads;
-        for (uint32_t j = tid; j < n; j += blockDim.x) {
-            double acc = a.accumulate ? sc[j] : 0.0;
-            const double *col = a.probs + lane_rows * n + j;
-            auto row_of = [&](uint32_t i) -> uint64_t {
-                return mean ? i : uint64_t(i / a.kvheads) * a.qheads + (i % a.kvheads) * group;
-            };
-            uint32_t i = 0;
-            for (; i + 8 <= nrows; i += 8) {
-                double v[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) v[u] = col[row_of(i + u) * n];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) acc += v[u] / a.weight;
-            }
-            for (; i < nrows; ++i) acc += col[row_of(i) * n] / a.weight;
-            sc[j] = acc;
-        }
-        __syncthreads();
-    }
-    if (!a.do_select) return;
-
-    // Reject invalid scores (pick_scored_blocks, kvmem_store.cpp:425-426).
-    int bad = 0;
-    for (uint32_t j = tid; j < n; j += blockDim.x) {
-        const double v = sc[j];
-        bad |= !__builtin_isfinite(v) || (!a.signed_scores && v < 0.0);
-    }
-    bad = __syncthreads_or(bad);
-    if (bad && tid == 0) raise_status(a.status, kStatusScores, a.epoch);
-    if (bad || epoch_failed(a.status, a.epoch)) {
-        if (tid == 0) a.count[lane] = 0;
-        return;
-    }
-
+    };
     const uint32_t n_cand = n - a.n_mandatory;
     const uint32_t k_eff = a.k - a.n_mandatory;  // host guarantees n_mandatory <= k
-
-    // Threshold search.  After it, with HT = thresh >> shift:
-    //   (key >> shift) >  HT            selected
-    //   (key >> shift) == HT && bucket  selected (the boundary bucket holds
-    //                                   exactly the remaining count)
-    //   key == thresh && !bucket        the first/last `remaining` equal keys
-    //                                   by id (tie rule), shift == 0
     uint64_t thresh = 0;
     uint32_t remaining = 0, shift = 0;
     bool bucket = false;
     if (k_eff == 0) {
         thresh = ~0ull;  // nothing ranks
         bucket = true;
-        shift = 0;
     } else if (k_eff >= n_cand) {
-        thresh = 0;      // every candidate
-        bucket = true;
+        bucket = true;   // every candidate
     } else {
-        // Leading bits shared by every candidate need no pass.
         uint64_t and_all = ~0ull, or_all = 0;
-        for (uint32_t j = tid; j < n; j += blockDim.x) {
-            if (a.n_mandatory && is_mandatory(a, j)) continue;
-            const uint64_t key = order_key(sc[j]);
+        for_each_key([&](uint64_t key) {
             and_all &= key;
             or_all |= key;
-        }
-        and_all = block_reduce(and_all, red_lds, AndOp());
-        or_all = block_reduce(or_all, red_lds, OrOp());
+        });
+        and_all = wave_and(and_all);
+        or_all = wave_or(or_all);
         const uint64_t diff = and_all ^ or_all;
+        remaining = k_eff;
         if (diff == 0) {  // all candidates equal: the tie rule decides
             thresh = and_all;
-            remaining = k_eff;
         } else {
             const int top = 63 - __clzll(diff);
-            int pos = top / 8 * 8;
             uint64_t prefix = and_all & ~((2ull << top) - 1);  // the common high bits
-            remaining = k_eff;
-            for (;; pos -= 8) {
-                const uint64_t hi_mask = pos + 8 >= 64 ? 0ull : ~0ull << (pos + 8);
-                if (tid < 256) hist[tid] = 0;
-                __syncthreads();
-                for (uint32_t j = tid; j < n; j += blockDim.x) {
-                    if (a.n_mandatory && is_mandatory(a, j)) continue;
-                    const uint64_t key = order_key(sc[j]);
-                    if ((key & hi_mask) == (prefix & hi_mask)) atomicAdd(&hist[(key >> pos) & 255u], 1u);
-                }
-                __syncthreads();
-                if (tid < 64) {
-                    // lane l covers digits 255-4l .. 252-4l, highest first
-                    const uint32_t c0 = hist[255 - 4 * tid], c1 = hist[254 - 4 * tid],
-                                   c2 = hist[253 - 4 * tid], c3 = hist[252 - 4 * tid];
-                    const uint32_t tot = c0 + c1 + c2 + c3;
-                    const uint32_t incl = wave_inclusive_scan(tot);
-                    const uint32_t excl = incl - tot;
-                    if (excl < remaining && remaining <= incl) {
-                        uint32_t rem = remaining - excl, d, cnt;
-                        if (rem <= c0) {
-                            d = 255 - 4 * tid; cnt = c0;
-                        } else if (rem <= c0 + c1) {
-                            rem -= c0; d = 254 - 4 * tid; cnt = c1;
-                        } else if (rem <= c0 + c1 + c2) {
-                            rem -= c0 + c1; d = 253 - 4 * tid; cnt = c2;
-                        } else {
-                            rem -= c0 + c1 + c2; d = 252 - 4 * tid; cnt = c3;
-                        }
-                        s_digit = d;
-                        s_remaining = rem;
-                        s_exact = rem == cnt;
-                    }
-                }
-                __syncthreads();
-                prefix |= uint64_t(s_digit) << pos;
-                remaining = s_remaining;
-                const bool exact = s_exact;
-                __syncthreads();
-                if (exact) {  // the whole boundary bucket is selected
-                    bucket = true;
+            for (int pos = top / 8 * 8;; pos -= 8) {
+                if (!radix_pass(for_each_key, hist, pos, prefix, remaining)) {
+                    bucket = true;  // the whole boundary bucket is selected
                     shift = uint32_t(pos);
                     break;
                 }
@@ -706,20 +639,31 @@ __global__ __launch_bounds__(1024) void k_select(SelectArgs a) {
         }
     }
 
-    // Compaction in id order: thread t owns the contiguous id chunk
-    // [t*C, t*C + C).
-    const uint64_t ht = shift >= 64 ? 0 : thresh >> shift;
-    const uint32_t C = (n + blockDim.x - 1) / blockDim.x;
-    const uint32_t j0 = min(n, tid * C), j1 = min(n, j0 + C);
+    // Compaction in id order.
+    const uint64_t ht = thresh >> shift;
+    auto cls = [&](uint64_t key) -> int {  // 2 taken, 1 tied at the threshold, 0 not
+        const uint64_t hk = key >> shift;
+        return (hk > ht || (hk == ht && bucket)) ? 2 : (hk == ht ? 1 : 0);
+    };
     uint32_t n_take = 0, n_eq = 0;
-    for (uint32_t j = j0; j < j1; ++j) {
-        if (a.n_mandatory && is_mandatory(a, j)) { ++n_take; continue; }
-        const uint64_t hk = order_key(sc[j]) >> shift;
-        if (hk > ht || (hk == ht && bucket)) ++n_take;
-        else if (hk == ht) ++n_eq;
+    if (CM > 0) {
+#pragma unroll
+        for (int c = 0; c < R; ++c) {
+            if (j0 + c >= j1) continue;
+            const int k = (cand_bits >> c & 1u) ? cls(kr[c]) : 2;
+            n_take += k == 2;
+            n_eq += k == 1;
+        }
+    } else {
+        for (uint32_t j = j0; j < j1; ++j) {
+            const int k = mand(j) ? 2 : cls(load_key(j));
+            n_take += k == 2;
+            n_eq += k == 1;
+        }
     }
-    uint32_t eq_total;
-    const uint32_t eq_base = block_exclusive_scan(n_eq, &eq_total, scan_lds);
+    const uint32_t eq_incl = wave_inclusive_scan(n_eq);
+    const uint32_t eq_base = eq_incl - n_eq;
+    const uint32_t eq_total = wave_bcast(eq_incl, kWave - 1);
     uint32_t lo, hi;  // equal-key ranks [lo, hi) are taken
     if (a.tie_higher_first) {
         lo = remaining >= eq_total ? 0u : eq_total - remaining;
@@ -730,27 +674,151 @@ __global__ __launch_bounds__(1024) void k_select(SelectArgs a) {
     }
     const uint32_t eq_lo = max(lo, eq_base), eq_hi = min(hi, eq_base + n_eq);
     n_take += eq_hi > eq_lo ? eq_hi - eq_lo : 0u;
-    uint32_t total;
-    uint32_t o = block_exclusive_scan(n_take, &total, scan_lds);
+    const uint32_t take_incl = wave_inclusive_scan(n_take);
+    const uint32_t total = wave_bcast(take_incl, kWave - 1);
+    uint32_t o = take_incl - n_take;
     uint32_t rank = eq_base;
     uint32_t *out = a.selected + uint64_t(lane) * a.k;
-    for (uint32_t j = j0; j < j1; ++j) {
-        bool take;
-        if (a.n_mandatory && is_mandatory(a, j)) {
-            take = true;
-        } else {
-            const uint64_t hk = order_key(sc[j]) >> shift;
-            if (hk == ht && !bucket) {
-                take = rank >= lo && rank < hi;
-                ++rank;
-            } else {
-                take = hk > ht || (hk == ht && bucket);
-            }
+    auto emit = [&](uint32_t j, int k) {
+        bool take = k == 2;
+        if (k == 1) {
+            take = rank >= lo && rank < hi;
+            ++rank;
         }
         if (take && o < a.k) out[o++] = j;
+    };
+    if (CM > 0) {
+#pragma unroll
+        for (int c = 0; c < R; ++c)
+            if (j0 + c < j1) emit(j0 + c, (cand_bits >> c & 1u) ? cls(kr[c]) : 2);
+    } else {
+        for (uint32_t j = j0; j < j1; ++j) emit(j, mand(j) ? 2 : cls(load_key(j)));
     }
-    if (tid == 0) a.count[lane] = min(total, a.k);
+    if (l == 0) a.count[lane] = min(total, a.k);
 }
+
+// Aggregation (optional) by the whole workgroup, then selection by its
+// first wave.  Keys go to LDS when the lane's pages fit.
+__device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
+    __shared__ uint32_t hist[256];
+    const uint32_t tid = threadIdx.x, B = blockDim.x;
+    const uint32_t n = a.pages;
+    const bool lds = n <= kTailLdsPages;
+    double *sc = a.scores + uint64_t(lane) * n;
+    // the status of this call, read early so its latency overlaps the sums
+    const bool failed = a.do_select && tid < kWave && epoch_failed(a.status, a.epoch);
+
+    int bad = 0;
+    auto note = [&](uint32_t j, double v) {
+        bad |= !__builtin_isfinite(v) || (!a.signed_scores && v < 0.0);
+        if (lds) tail_keys[j] = order_key(v);
+    };
+    if (a.do_aggregate) {
+        // Contributing rows in the reference's order: (row, head) for Mean,
+        // (row, kv-head group) for the group rules.  Two pages per pass and
+        // up to 32 rows of loads in flight; the additions stay in order.
+        const uint32_t group = a.qheads / a.kvheads;
+        const bool mean = a.aggregation == kAggMean;
+        const uint32_t nrows = mean ? a.rows * a.qheads : a.rows * a.kvheads;
+        const double *terms = a.logits + uint64_t(lane) * a.rows * a.qheads * n;
+        auto row_of = [&](uint32_t i) -> uint64_t {
+            return mean ? i : uint64_t(i / a.kvheads) * a.qheads + (i % a.kvheads) * group;
+        };
+        for (uint32_t j0 = tid; j0 < n; j0 += 2 * B) {
+            const uint32_t j1 = j0 + B;
+            const bool has1 = j1 < n;
+            double acc0 = a.accumulate ? sc[j0] : 0.0;
+            double acc1 = has1 && a.accumulate ? sc[j1] : 0.0;
+            uint32_t i = 0;
+            for (; i + 32 <= nrows; i += 32) {
+                double v0[32], v1[32];
+#pragma unroll
+                for (int u = 0; u < 32; ++u) {
+                    const uint64_t o = row_of(i + u) * n;
+                    v0[u] = terms[o + j0];
+                    v1[u] = has1 ? terms[o + j1] : 0.0;
+                }
+#pragma unroll
+                for (int u = 0; u < 32; ++u) {
+                    acc0 += v0[u];
+                    acc1 += v1[u];
+                }
+            }
+            for (; i + 8 <= nrows; i += 8) {
+                double v0[8], v1[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const uint64_t o = row_of(i + u) * n;
+                    v0[u] = terms[o + j0];
+                    v1[u] = has1 ? terms[o + j1] : 0.0;
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    acc0 += v0[u];
+                    acc1 += v1[u];
+                }
+            }
+            for (; i < nrows; ++i) {
+                const uint64_t o = row_of(i) * n;
+                acc0 += terms[o + j0];
+                if (has1) acc1 += terms[o + j1];
+            }
+            sc[j0] = acc0;
+            note(j0, acc0);
+            if (has1) {
+                sc[j1] = acc1;
+                note(j1, acc1);
+            }
+        }
+    } else {
+        for (uint32_t j = tid; j < n; j += B) note(j, sc[j]);
+    }
+    if (!a.do_select) return;
+    // Reject invalid scores (pick_scored_blocks, kvmem_store.cpp:425-426).
+    bad = __syncthreads_or(bad);  // also publishes the LDS keys
+    if (tid >= kWave) return;
+    if (bad && tid == 0) raise_status(a.status, kStatusScores, a.epoch);
+    if (bad || failed) {
+        if (tid == 0) a.count[lane] = 0;
+        return;
+    }
+    if (n <= 16 * kWave) wave_select<16>(a, lane, lds, sc, hist);
+    else wave_select<0>(a, lane, lds, sc, hist);
+}
+
+// Softmax units -> terms; the lane's last workgroup aggregates (+ selects).
+// grid (ceil(units/4), lanes), 256 threads (a unit per wave); dynamic LDS:
+// the tail's keys.
+template <int NPL>
+__global__ __launch_bounds__(256) void k_probs(SelectArgs a) {
+    __shared__ uint32_t s_last;
+    const uint32_t lane = blockIdx.y;
+    const uint32_t unit = blockIdx.x * kUnitsPerBlock + (threadIdx.x >> 6);
+    double *lane_base = a.logits + uint64_t(lane) * a.rows * a.qheads * a.pages;
+    if (unit < a.units) {
+        if (NPL > 0)
+            unit_terms_regs<NPL ? NPL : 1>(a, lane_base, unit);
+        else
+            unit_terms_loop(a, lane_base, unit);
+    }
+    // Publish this workgroup's terms (device scope), then count it.  Only
+    // the lane's last workgroup continues; its counter is back at zero for
+    // the next launch.
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t done = atomicAdd(a.counters + lane, 1u);
+        s_last = done == gridDim.x - 1;
+        if (s_last) atomicExch(a.counters + lane, 0u);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();  // the other workgroups' terms are visible from here
+    lane_tail(a, lane);
+}
+
+// Selection over given scores (no softmax), one workgroup per lane.
+__global__ __launch_bounds__(256) void k_select(SelectArgs a) { lane_tail(a, blockIdx.x); }
 
 // ---------------------------------------------------------------------------
 // Stage-in gather.  One workgroup copies `chunk_rows` token rows of one
@@ -1019,27 +1087,23 @@ hipError_t launch_logits_mfma(const MfmaLogitsArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_softmax(const SoftmaxArgs &a, hipStream_t s) {
+hipError_t launch_probs(const SelectArgs &a, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch\'s error
-    if (a.aggregation == kAggMean) {
-        const uint64_t rows = uint64_t(a.lanes) * a.rows * a.qheads;
-        const dim3 grid(unsigned((rows + 3) / 4)), block(256);
-        if (a.pages <= 64) hipLaunchKernelGGL(k_softmax_rows<1>, grid, block, 0, s, a);
-        else if (a.pages <= 128) hipLaunchKernelGGL(k_softmax_rows<2>, grid, block, 0, s, a);
-        else if (a.pages <= 256) hipLaunchKernelGGL(k_softmax_rows<4>, grid, block, 0, s, a);
-        else if (a.pages <= 512) hipLaunchKernelGGL(k_softmax_rows<8>, grid, block, 0, s, a);
-        else if (a.pages <= 1024) hipLaunchKernelGGL(k_softmax_rows<16>, grid, block, 0, s, a);
-        else hipLaunchKernelGGL(k_softmax_rows<0>, grid, block, 0, s, a);
-    } else {
-        const unsigned groups = unsigned(uint64_t(a.lanes) * a.rows * a.kvheads);
-        hipLaunchKernelGGL(k_softmax_groups, dim3(groups), dim3(256), 0, s, a);
-    }
+    const dim3 grid((a.units + kUnitsPerBlock - 1) / kUnitsPerBlock, a.lanes), block(kUnitsPerBlock * kWave);
+    const size_t lds = a.pages <= kTailLdsPages ? size_t(a.pages) * 8 : 0;
+    if (a.pages <= 64) hipLaunchKernelGGL(k_probs<1>, grid, block, lds, s, a);
+    else if (a.pages <= 128) hipLaunchKernelGGL(k_probs<2>, grid, block, lds, s, a);
+    else if (a.pages <= 256) hipLaunchKernelGGL(k_probs<4>, grid, block, lds, s, a);
+    else if (a.pages <= 512) hipLaunchKernelGGL(k_probs<8>, grid, block, lds, s, a);
+    else if (a.pages <= 1024) hipLaunchKernelGGL(k_probs<16>, grid, block, lds, s, a);
+    else hipLaunchKernelGGL(k_probs<0>, grid, block, lds, s, a);
     return hipGetLastError();
 }
 
 hipError_t launch_select(const SelectArgs &a, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch\'s error
-    hipLaunchKernelGGL(k_select, dim3(a.lanes), dim3(1024), 0, s, a);
+    const size_t lds = a.pages <= kTailLdsPages ? size_t(a.pages) * 8 : 0;
+    hipLaunchKernelGGL(k_select, dim3(a.lanes), dim3(256), lds, s, a);
     return hipGetLastError();
 }
 

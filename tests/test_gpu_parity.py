@@ -168,6 +168,33 @@ def test_score_mask_and_accumulate(ctx):
         assert np.all(got[mask == 0] == 0)
 
 
+@pytest.mark.parametrize("pages", [3000, 5000, 9000])
+@pytest.mark.parametrize("agg", [K.AGG_MEAN, K.AGG_MAX, K.AGG_MAX_LOGIT])
+def test_scored_selection_long_rows(ctx, pages, agg):
+    """Softmax rows held in registers (<= 4096 pages), in memory passes with
+    keys in LDS (<= 8192) and with keys recomputed from scores (> 8192), each
+    through softmax -> aggregation -> selection in one call, with a mask and
+    mandatory pages."""
+    rows, dim, qh, kvh, k, pt = 2, 64, 8, 2, 64, 16
+    means, query = _score_inputs(pages, rows, dim, qh, kvh, closed_form=False)
+    mask = (np.arange(pages) % 11 != 5).astype(np.uint8)
+    mand = (0, pages - 1)
+    expect = O.page_softmax_scores(means, query, [rows], qh, kvh, dim, agg, score_mask=mask)
+    s16 = dev(means[0].astype(np.float16).view(np.uint16))
+    qd, md = dev(query[0]), dev(mask)  # held: the descriptors keep raw pointers
+    out = zeros(pages, np.float64)
+    sel = zeros(k, np.uint32)
+    cnt = zeros(1, np.uint32)
+    ctx.recall_layer(query=K.make_query(qd, K.FMT_F32, rows, qh, kvh, dim), summaries=s16,
+                     pages=pages, page_tokens=pt, scores=out, selected=sel, count=cnt, k=k,
+                     aggregation=agg, score_mask=md, mandatory=mand, tie_rule=K.TIE_LOWER_FIRST)
+    ctx.check()
+    got = host(out, np.float64)
+    assert _rel_err(got, expect) <= REL
+    assert host(cnt, np.uint32)[0] == k
+    assert np.array_equal(host(sel, np.uint32), O.pick_scored_blocks(expect, k, mand, O.TIE_LOWER_FIRST))
+
+
 def test_mfma_and_vector_logits_agree(ctx):
     pages, rows, dim, qh, kvh = 1024, 4, 128, 40, 8
     means, query = _score_inputs(pages, rows, dim, qh, kvh, closed_form=False)
