@@ -285,7 +285,7 @@ def run(args):
             "query_rows": R, "page_tokens": PT, "pages": P, "top_k": KSEL,
             "aggregation": "mean", "gather": "fp16 K+V copy into 8192-token slots",
             "engine": args.engine, "pinned_layers": ring,
-            "gather_workgroups": args.gather_wgs or 64, "gather_chunk_rows": args.chunk_rows or 8,
+            "gather_workgroups": args.gather_wgs or 8, "gather_chunk_rows": args.chunk_rows or 8,
         },
         "select_us_per_layer": round(select_us, 2),
         "select_stack_us_per_layer": round(ms_per_step / L * 1e3, 2),
@@ -363,7 +363,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=64)
     ap.add_argument("--seed", type=int, default=42)
-    ap.add_argument("--engine", choices=["auto", "kernel", "sdma"], default="auto")
+    ap.add_argument("--engine", choices=["auto", "kernel", "sdma"], default="kernel")
     ap.add_argument("--gather-wgs", type=int, default=0, help="gather grid bound (0 = library default)")
     ap.add_argument("--chunk-rows", type=int, default=0, help="gather rows per work item (0 = default)")
     ap.add_argument("--gather-threads", type=int, default=0, help="gather workgroup size (0 = default)")

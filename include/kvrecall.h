@@ -187,7 +187,7 @@ void *kvr_select_stream(kvr_context *ctx);
 void *kvr_copy_stream(kvr_context *ctx);
 
 typedef enum kvr_option {
-    KVR_OPT_GATHER_WORKGROUPS = 1, /* grid bound of the device-driven gather (default 64) */
+    KVR_OPT_GATHER_WORKGROUPS = 1, /* grid bound of the device-driven gather (default 8) */
     KVR_OPT_GATHER_CHUNK_ROWS = 2, /* token rows per gather work item (default 8, <= 64) */
     KVR_OPT_GATHER_THREADS = 3     /* gather workgroup size: 64, 128 or 256 (default 256) */
 } kvr_option;

@@ -43,7 +43,7 @@ struct kvr_context {
     uint8_t *staging = nullptr;
     size_t staging_bytes = 0;
     // tuning
-    uint32_t gather_wgs = 64;
+    uint32_t gather_wgs = 8;
     uint32_t chunk_rows = 8;
     uint32_t gather_threads = 256;
 };
@@ -445,7 +445,7 @@ kvr_status check_planes(const kvr_plane *planes, uint32_t n, uint32_t lanes, uin
     return KVR_OK;
 }
 
-constexpr uint32_t kDefaultGatherWgs = 64, kDefaultChunkRows = 8;
+constexpr uint32_t kDefaultGatherWgs = 8, kDefaultChunkRows = 8;
 
 // Rows per gather work item: the context's setting, bounded by the page and
 // by the LDS a staged decode needs (source rows + requantized rows).
