@@ -1,0 +1,213 @@
+// kvmem_hip.hpp -- C++ host layer of the MI355X recall path, over the C ABI
+// of kvrecall.h.  It keeps the shapes of KVMem's own host interfaces for this
+// path so an adapter can swap them in:
+//   PageSoftmaxHip       for PageSoftmaxCuda  (kvmem/include/kvmem/page_softmax_cuda.hpp:10-32)
+//   query_score_frame    (kvmem/include/kvmem/graph_recall.hpp:18-28, graph_recall.cpp:269-293)
+//   kvmem_stagein_* / kvmem_d2d_batched / kvmem_meank_*
+//                        for src/adapter/llama-kvmem-stagein.h:12-68 (bool + stderr)
+//   RecallTransfer       the MemoryTransfer contract (kvmem/include/kvmem/memory_contract.hpp:175-187)
+//   SummaryCapture       the capture side of the attn-qk hook (src/adapter/llama-kvmem-hooks.h:74-98)
+// Errors follow the reference: std::invalid_argument for geometry and
+// operand errors, std::length_error for workspace limits, std::runtime_error
+// for device failures.  Reference paths are relative to the KVMem 0.19.0 tree.
+#pragma once
+
+#include "kvrecall.h"
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <string>
+#include <vector>
+
+namespace kvmem_hip {
+
+enum class GqaScoreAggregation { Mean, Max, MaxLogit };
+enum class TieRule { LowerFirst, HigherFirst };
+
+// One accepted logical index: page starts/counts and the score and transport
+// masks (graph_recall.hpp:18-24).
+struct QueryScoreFrame {
+    std::vector<uint64_t> starts;
+    std::vector<uint32_t> counts;
+    std::vector<uint8_t> score_mask;
+    std::vector<uint8_t> transport_mask;
+    uint64_t accepted_through = 0;
+};
+
+// graph_recall.cpp:269-293: pages of `block_tokens` over `accepted_through`
+// tokens; when there are more pages than the budget, sink and recent pages
+// leave the softmax and every page is a transport candidate except the
+// fixed ones.
+QueryScoreFrame query_score_frame(uint64_t accepted_through, uint32_t block_tokens, uint32_t budget_blocks,
+                                  uint32_t sink_blocks, uint32_t recent_blocks,
+                                  const std::vector<uint32_t> &fixed_blocks);
+
+// Host binary32 Query rows in layer/row/head/channel order; rows beyond
+// layer_rows[layer] are absent (graph_recall.hpp:30-38).
+struct PageQueryView {
+    const float *data = nullptr;
+    const uint32_t *layer_rows = nullptr;
+    uint32_t layers = 0, rows = 0, query_heads = 0, kv_heads = 0, head_dim = 0;
+    const float *const *layer_data = nullptr;  // optional per-layer storage
+    float attention_scale = 0;                 // 0 selects 1/sqrt(head_dim)
+};
+
+// A borrowed device Query of one layer, strides in bytes
+// (native_layer_query.hpp:12-25).
+enum class NativeQueryScalar { Float32, Float16, BFloat16 };
+struct NativeCurrentLayerQuery {
+    const void *data = nullptr;
+    size_t bytes = 0;
+    uint32_t layer = 0, rows = 0, query_heads = 0, kv_heads = 0, head_dim = 0;
+    float attention_scale = 0;
+    NativeQueryScalar scalar = NativeQueryScalar::Float32;
+    size_t row_stride = 0, head_stride = 0, dimension_stride = 0;
+};
+// Positive, non-overlapping strides within `bytes` (native_layer_query.hpp:36-58).
+void validate_native_layer_query(const NativeCurrentLayerQuery &q);
+
+// Device-resident page summaries, the GPU stand-in for RawKvStore's mean-K:
+// per layer fp16 [pages][kv_heads*head_dim] (the recall_fp16 values), as
+// written by kvr_summary_build / kvr_summary_finalize.
+struct PageSummaries {
+    std::vector<const uint16_t *> layers;
+    uint32_t pages = 0, page_tokens = 0, kv_heads = 0, head_dim = 0;
+};
+
+// The page-softmax scorer (page_softmax_cuda.hpp:10-32): synchronous on
+// return, owned by one adapter, one device.
+class PageSoftmaxHip {
+public:
+    explicit PageSoftmaxHip(int device);
+    // Device bytes of a borrowed workspace for up to `max_blocks` pages;
+    // score() then never allocates and rejects larger calls before a launch.
+    static size_t workspace_bytes(uint32_t max_blocks, uint32_t query_heads, uint32_t kv_heads,
+                                  uint32_t head_dim);
+    PageSoftmaxHip(int device, void *workspace, size_t bytes, uint32_t max_blocks, uint32_t query_heads,
+                   uint32_t kv_heads, uint32_t head_dim);
+    ~PageSoftmaxHip();
+    PageSoftmaxHip(const PageSoftmaxHip &) = delete;
+    PageSoftmaxHip &operator=(const PageSoftmaxHip &) = delete;
+
+    // page_softmax_scores over every layer with rows (graph_recall.cpp:322-394).
+    std::vector<double> score(const PageSummaries &, PageQueryView, const QueryScoreFrame &,
+                              GqaScoreAggregation = GqaScoreAggregation::Mean);
+    // One layer's native Query on its producer stream, Mean
+    // (page_softmax.cu:281-396).  The stream must not be capturing.
+    std::vector<double> score_current_layer(const PageSummaries &, NativeCurrentLayerQuery,
+                                            const QueryScoreFrame &, void *producer_stream);
+    // pick_scored_blocks (kvmem_store.cpp:418-451) on the device: mandatory
+    // pages first, then by score with the tie rule; ascending ids.
+    std::vector<uint32_t> pick(const std::vector<double> &scores, uint32_t budget,
+                               const std::vector<uint32_t> &mandatory = {},
+                               TieRule tie = TieRule::LowerFirst, bool signed_scores = false);
+    size_t device_bytes() const;
+    kvr_context *context() const;
+
+private:
+    struct Impl;
+    std::unique_ptr<Impl> impl_;
+};
+
+// ---- stage-in entry points (llama-kvmem-stagein.h) ------------------------
+// bool results with the failure on stderr, one state per execution domain
+// (thread).  The product path sends packed K and V record bytes through
+// enqueue_v: they are copied into a pinned 32 MiB slab (the caller's buffer
+// is reusable on return) and flush moves them into their cache rows with one
+// device launch that reads the pinned slab directly.
+struct kvmem_gpu_state;
+kvmem_gpu_state *kvmem_gpu_state_create();  // also made current on this thread
+void kvmem_gpu_state_free(kvmem_gpu_state *state);
+void kvmem_gpu_state_make_current(kvmem_gpu_state *state);
+
+bool kvmem_stagein_gpu_ready(size_t n_f32, size_t n_packed = 0);
+void kvmem_stagein_gpu_free();
+bool kvmem_stagein_h2d_bytes(void *gpu_dst, const void *host, size_t n);
+void kvmem_stagein_sync();
+bool kvmem_stagein_sync_checked();
+bool kvmem_stagein_enqueue_v(const void *packed, size_t nbytes, uint8_t *dst, int64_t *set_us);
+bool kvmem_stagein_flush(int64_t *copy_us, int64_t *rope_us, int64_t *hadamard_us, int64_t *set_us);
+bool kvmem_d2d_batched(const void *const *src, void *const *dst, const size_t *nbytes, int n);
+
+// Decode running mean-K (stagein.cu:270-320, 1041-1114): one binary32 sum of
+// n_embd channels per layer on the device, added in token order and zeroed
+// by kvmem_meank_zero.  `ty` is the K element type (F32, F16 or BF16; the
+// reference passes a ggml_type); channel c = head*ne0 + dim of token t is at
+// gpu_k + (tok0+t)*nb2 + head*nb1 + dim*nb0.
+bool kvmem_meank_ready(uint32_t n_layer, uint32_t n_embd);
+void kvmem_meank_free();
+void kvmem_meank_zero(uint32_t il);
+bool kvmem_meank_add(uint32_t il, kvr_format ty, const void *gpu_k, uint32_t tok0, uint32_t n_keep,
+                     uint32_t n_embd, int64_t ne0, size_t nb0, size_t nb1, size_t nb2);
+bool kvmem_meank_d2h(uint32_t il, float *host, uint32_t n_embd);
+
+// ---- MemoryTransfer for recall (memory_contract.hpp:175-187) --------------
+enum class TransferStatus { Pending, Complete, Failed };
+struct TransferPoll {
+    TransferStatus status = TransferStatus::Pending;
+    std::string error;
+};
+enum class AbortResult { PreviousViewPreserved, SessionInvalidated };
+
+// Restores one layer's selected pages into the slot arrays.  The pages' home
+// is the pinned history, so there is nothing to spill: start_spill only
+// marks the spill phase done.  start_restore enqueues kvr_stage_in on the
+// transfer's stream (after `ready`, an event of the producer of the
+// selection, when given); poll never blocks; publish requires a completed
+// restore; abort drains before returning.
+class RecallTransfer {
+public:
+    RecallTransfer(kvr_context *ctx, std::vector<kvr_plane> planes, uint32_t lanes, uint32_t page_tokens,
+                   const uint32_t *selected, const uint32_t *count, uint32_t k,
+                   kvr_copy_engine engine = KVR_ENGINE_KERNEL, void *stream = nullptr, void *ready = nullptr);
+    ~RecallTransfer();
+    RecallTransfer(const RecallTransfer &) = delete;
+    RecallTransfer &operator=(const RecallTransfer &) = delete;
+    void start_spill();
+    TransferPoll poll();
+    void start_restore();
+    void publish();
+    AbortResult abort() noexcept;
+    bool published() const { return phase_ == Phase::Published; }
+
+private:
+    enum class Phase { Prepared, Spilled, Restoring, Ready, Published, Failed, Aborted };
+    kvr_context *ctx_;
+    std::vector<kvr_plane> planes_;
+    uint32_t lanes_, page_tokens_, k_;
+    const uint32_t *selected_, *count_;
+    kvr_copy_engine engine_;
+    void *stream_, *ready_;
+    void *done_ = nullptr;  // hipEvent_t
+    Phase phase_ = Phase::Prepared;
+    std::string error_;
+};
+
+// Capture side of the attn-qk hook: captured K rows of each layer go into
+// device running sums (kvr_summary_accumulate), and finalized pages become
+// the fp16 summaries a PageSummaries points at (kvr_summary_finalize).
+class SummaryCapture {
+public:
+    SummaryCapture(kvr_context *ctx, uint32_t layers, uint32_t max_pages, uint32_t page_tokens,
+                   uint32_t kv_heads, uint32_t head_dim);
+    ~SummaryCapture();
+    SummaryCapture(const SummaryCapture &) = delete;
+    SummaryCapture &operator=(const SummaryCapture &) = delete;
+    // Rows [pos0, pos0+n) of layer `layer`; element (t, h, d) at
+    // k + t*token_stride + h*head_stride + d*dim_stride (bytes).
+    void capture(uint32_t layer, const void *k, kvr_format scalar, uint64_t pos0, uint32_t n,
+                 size_t token_stride, size_t head_stride, size_t dim_stride, void *stream = nullptr);
+    // fp16 summaries of the first `pages` pages of every layer.
+    PageSummaries finalize(uint32_t pages, void *stream = nullptr);
+    const float *means(uint32_t layer) const;
+
+private:
+    kvr_context *ctx_;
+    uint32_t layers_, max_pages_, page_tokens_, kv_heads_, head_dim_;
+    float *sums_ = nullptr, *means_ = nullptr;
+    uint32_t *counts_ = nullptr;
+    uint16_t *summaries_ = nullptr;
+};
+
+}  // namespace kvmem_hip

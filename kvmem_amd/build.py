@@ -1,6 +1,8 @@
 """Build the in-tree native libraries.
 
   kvmem_amd/libkvrecall.so   HIP kernels + the C ABI of include/kvrecall.h (gfx950)
+  kvmem_amd/libkvmem_hip.so  C++ host layer (include/kvmem_hip/kvmem_hip.hpp) over it
+  tests/cpp/build/test_host  C++ test of the host layer (links the oracle as checker)
   oracle/liboracle.so        the CPU restatement used by tests (checker only)
   oracle/_ref/*.so           the reference's own host sources, when present
 
@@ -19,6 +21,10 @@ from concurrent.futures import ThreadPoolExecutor
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "kvmem_amd", "csrc")
 LIB = os.path.join(ROOT, "kvmem_amd", "libkvrecall.so")
+HOST_LIB = os.path.join(ROOT, "kvmem_amd", "libkvmem_hip.so")
+HOST_SRC = os.path.join(ROOT, "kvmem_amd", "host", "kvmem_hip.cpp")
+HOST_TEST_SRC = os.path.join(ROOT, "tests", "cpp", "test_host.cpp")
+HOST_TEST = os.path.join(ROOT, "tests", "cpp", "build", "test_host")
 ORACLE = os.path.join(ROOT, "oracle")
 ARCH = os.environ.get("KVR_OFFLOAD_ARCH", "gfx950")
 
@@ -72,6 +78,30 @@ def build_library(verbose: bool = False) -> str:
     return LIB
 
 
+def build_host(verbose: bool = False) -> str:
+    """The C++ host layer: host code only, linked against libkvrecall.so."""
+    hipcc = _hipcc()
+    tmp = HOST_LIB + ".tmp"
+    _run([hipcc, "-O2", "-fPIC", "-shared", "-std=c++17", "-Wall", "-I", os.path.join(ROOT, "include"),
+          HOST_SRC, "-o", tmp, "-L", os.path.dirname(LIB), "-lkvrecall", "-Wl,-rpath,$ORIGIN"], verbose)
+    os.replace(tmp, HOST_LIB)
+    return HOST_LIB
+
+
+def build_host_test(verbose: bool = False) -> str:
+    """tests/cpp/test_host.cpp against the host layer, the C ABI and the oracle."""
+    hipcc = _hipcc()
+    os.makedirs(os.path.dirname(HOST_TEST), exist_ok=True)
+    tmp = HOST_TEST + ".tmp"
+    libdir = os.path.dirname(LIB)
+    _run([hipcc, "-O2", "-std=c++17", "-Wall", "-I", os.path.join(ROOT, "include"), "-I", ORACLE, HOST_TEST_SRC,
+          "-o", tmp, "-L", libdir, "-lkvmem_hip", "-lkvrecall", "-L", ORACLE, "-loracle",
+          f"-Wl,-rpath,{libdir}", f"-Wl,-rpath,{ORACLE}", "-Wl,-rpath,$ORIGIN/../../../kvmem_amd",
+          "-Wl,-rpath,$ORIGIN/../../../oracle"], verbose)
+    os.replace(tmp, HOST_TEST)
+    return HOST_TEST
+
+
 def build_oracle(verbose: bool = False) -> None:
     jobs = str(min(8, os.cpu_count() or 1))
     _run(["make", "-C", ORACLE, "-B", f"-j{jobs}", "all"], verbose)
@@ -79,7 +109,9 @@ def build_oracle(verbose: bool = False) -> None:
 
 def build_all(verbose: bool = False) -> None:
     build_library(verbose)
+    build_host(verbose)
     build_oracle(verbose)
+    build_host_test(verbose)
 
 
 if __name__ == "__main__":

@@ -185,6 +185,8 @@ kvr_status ensure_workspace(kvr_context *ctx, size_t bytes, hipStream_t s) {
     return KVR_OK;
 }
 
+constexpr uint32_t kInitialCounters = 64;
+
 // Per-lane completion counters of the softmax launch (zero between launches).
 kvr_status ensure_counters(kvr_context *ctx, uint32_t lanes, hipStream_t s) {
     if (lanes <= ctx->counters_cap) return KVR_OK;
@@ -196,7 +198,7 @@ kvr_status ensure_counters(kvr_context *ctx, uint32_t lanes, hipStream_t s) {
     if (ctx->counters) KVR_HIP(hipFree(ctx->counters));
     ctx->counters = nullptr;
     ctx->counters_cap = 0;
-    const uint32_t cap = std::max<uint32_t>(lanes, 64);
+    const uint32_t cap = std::max<uint32_t>(lanes, kInitialCounters);
     KVR_HIP(hipMalloc(&ctx->counters, cap * sizeof(uint32_t)));
     KVR_HIP(hipMemset(ctx->counters, 0, cap * sizeof(uint32_t)));
     KVR_HIP(hipDeviceSynchronize());
@@ -621,6 +623,11 @@ kvr_status kvr_create(int device, kvr_context **out) {
     }
     if (e == hipSuccess) e = hipMalloc(&ctx->status, kvr::kStatusWords * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMemset(ctx->status, 0, kvr::kStatusWords * sizeof(uint32_t));
+    // select counters for up to 64 lanes, so calls on a borrowed workspace
+    // never allocate
+    if (e == hipSuccess) e = hipMalloc(&ctx->counters, kInitialCounters * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(ctx->counters, 0, kInitialCounters * sizeof(uint32_t));
+    if (e == hipSuccess) ctx->counters_cap = kInitialCounters;
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         kvr_destroy(ctx);

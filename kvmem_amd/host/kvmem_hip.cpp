@@ -1,0 +1,827 @@
+// kvmem_hip.cpp -- C++ host layer over the recall C ABI (include/kvrecall.h).
+// Everything on the device goes through kvr_* calls; this file only
+// validates, stages host operands, owns buffers and translates statuses into
+// the exception and bool conventions of KVMem's own interfaces.
+#include "kvmem_hip/kvmem_hip.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <array>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <limits>
+#include <stdexcept>
+
+namespace kvmem_hip {
+namespace {
+
+[[noreturn]] void throw_status(kvr_status s, const char *what) {
+    std::string msg = std::string(what) + ": " + kvr_last_error();
+    switch (s) {
+    case KVR_ERR_WORKSPACE: throw std::length_error(msg);
+    case KVR_ERR_HIP: throw std::runtime_error(msg);
+    default: throw std::invalid_argument(msg);
+    }
+}
+void ok(kvr_status s, const char *what) {
+    if (s != KVR_OK) throw_status(s, what);
+}
+void hip_ok(hipError_t e, const char *what) {
+    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+void require(bool cond, const char *msg) {
+    if (!cond) throw std::invalid_argument(msg);
+}
+size_t align256(size_t b) {
+    if (b > std::numeric_limits<size_t>::max() - 255) throw std::length_error("workspace size overflow");
+    return (b + 255) / 256 * 256;
+}
+
+struct DeviceBinding {
+    int previous = 0;
+    explicit DeviceBinding(int device) {
+        hip_ok(hipGetDevice(&previous), "hipGetDevice");
+        hip_ok(hipSetDevice(device), "hipSetDevice");
+    }
+    ~DeviceBinding() { (void)hipSetDevice(previous); }
+};
+
+// Drains a stream on scope exit unless disarmed: a throwing call leaves no
+// work in flight over buffers it owns.
+struct StreamDrain {
+    hipStream_t stream;
+    bool armed = true;
+    ~StreamDrain() {
+        if (armed) (void)hipStreamSynchronize(stream);
+    }
+};
+
+bool capturing(hipStream_t s) {
+    hipStreamCaptureStatus c = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(s, &c) == hipSuccess && c != hipStreamCaptureStatusNone;
+}
+
+kvr_format query_format(NativeQueryScalar s) {
+    switch (s) {
+    case NativeQueryScalar::Float32: return KVR_FMT_F32;
+    case NativeQueryScalar::Float16: return KVR_FMT_F16;
+    case NativeQueryScalar::BFloat16: return KVR_FMT_BF16;
+    }
+    throw std::invalid_argument("unknown native Query scalar");
+}
+size_t query_scalar_bytes(NativeQueryScalar s) { return s == NativeQueryScalar::Float32 ? 4 : 2; }
+
+kvr_aggregation to_kvr(GqaScoreAggregation a) {
+    switch (a) {
+    case GqaScoreAggregation::Mean: return KVR_AGG_MEAN;
+    case GqaScoreAggregation::Max: return KVR_AGG_MAX;
+    case GqaScoreAggregation::MaxLogit: return KVR_AGG_MAX_LOGIT;
+    }
+    throw std::invalid_argument("invalid page softmax GQA aggregation");
+}
+
+constexpr uint32_t kRowsPerLaunch = 64;           // query rows scored per kvr_score call
+constexpr size_t kLogitsBudget = size_t(64) << 20;  // binary64 logits per call
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+QueryScoreFrame query_score_frame(uint64_t accepted, uint32_t block_tokens, uint32_t budget, uint32_t sink,
+                                  uint32_t recent, const std::vector<uint32_t> &fixed) {
+    require(block_tokens && budget, "invalid Query score budget or block size");
+    const uint64_t pages = (accepted + block_tokens - 1) / block_tokens;
+    require(pages <= std::numeric_limits<uint32_t>::max(), "Query index exceeds logical page capacity");
+    const size_t n = size_t(pages);
+    QueryScoreFrame f;
+    f.accepted_through = accepted;
+    f.starts.resize(n);
+    f.counts.resize(n);
+    for (size_t i = 0; i < n; ++i) {
+        f.starts[i] = uint64_t(i) * block_tokens;
+        f.counts[i] = uint32_t(std::min<uint64_t>(block_tokens, accepted - f.starts[i]));
+    }
+    const bool over = pages > budget;
+    f.score_mask.assign(n, 1);
+    f.transport_mask.assign(n, over ? 1 : 0);
+    if (over && uint64_t(sink) + recent < pages) {
+        std::fill(f.score_mask.begin(), f.score_mask.begin() + std::min<size_t>(sink, n), uint8_t(0));
+        std::fill(f.score_mask.end() - std::min<size_t>(recent, n), f.score_mask.end(), uint8_t(0));
+    }
+    for (uint32_t id : fixed) {
+        require(id < pages, "fixed Query block is outside the accepted index");
+        f.transport_mask[id] = 0;
+    }
+    return f;
+}
+
+void validate_native_layer_query(const NativeCurrentLayerQuery &q) {
+    const size_t el = query_scalar_bytes(q.scalar);
+    if (!q.data || !q.rows || !q.query_heads || !q.kv_heads || !q.head_dim || q.query_heads % q.kv_heads ||
+        !std::isfinite(q.attention_scale) || q.attention_scale < 0 ||
+        reinterpret_cast<uintptr_t>(q.data) % el)
+        throw std::invalid_argument("invalid native current-layer Query geometry");
+    // Axes by increasing stride must not overlap: each stride is at least the
+    // extent of the faster axes.
+    std::array<std::pair<size_t, uint32_t>, 3> axes{
+        {{q.row_stride, q.rows}, {q.head_stride, q.query_heads}, {q.dimension_stride, q.head_dim}}};
+    std::sort(axes.begin(), axes.end());
+    size_t extent = el;
+    for (const auto &ax : axes) {
+        const size_t stride = ax.first, count = ax.second;
+        if (!stride || stride % el || (count > 1 && stride < extent))
+            throw std::invalid_argument("overlapping or overflowing native Query strides");
+        if (count > 1 && stride > (std::numeric_limits<size_t>::max() - extent) / (count - 1))
+            throw std::invalid_argument("overlapping or overflowing native Query strides");
+        extent += stride * (count - 1);
+    }
+    if (extent > q.bytes) throw std::invalid_argument("native Query exceeds its declared byte extent");
+}
+
+// ---------------------------------------------------------------------------
+struct PageSoftmaxHip::Impl {
+    int device = 0;
+    kvr_context *ctx = nullptr;
+    bool borrowed = false;
+    uint32_t max_blocks = 0, qheads = 0, kvheads = 0, dim = 0;
+    // device buffers: owned (grown on demand) or carved from the workspace
+    float *q = nullptr;
+    size_t q_cap = 0;  // floats
+    uint8_t *mask = nullptr;
+    double *scores = nullptr;
+    uint32_t *sel = nullptr, *cnt = nullptr;
+    size_t page_cap = 0;
+    std::vector<void *> owned;
+
+    ~Impl() {
+        if (ctx) {
+            (void)hipSetDevice(device);
+            (void)kvr_check(ctx, nullptr);
+        }
+        for (void *p : owned) (void)hipFree(p);
+        if (ctx) (void)kvr_destroy(ctx);
+    }
+
+    hipStream_t stream() const { return static_cast<hipStream_t>(kvr_select_stream(ctx)); }
+
+    void reserve(uint32_t rows, uint32_t pages) {
+        const size_t qf = size_t(rows) * qheads * dim;
+        if (borrowed) {
+            if (qf > q_cap || pages > page_cap)
+                throw std::length_error("page softmax exceeds its planned device workspace");
+            return;
+        }
+        hip_ok(hipStreamSynchronize(stream()), "hipStreamSynchronize");
+        if (qf > q_cap) {
+            void *p = nullptr;
+            hip_ok(hipMalloc(&p, qf * sizeof(float)), "hipMalloc query");
+            owned.push_back(p);
+            q = static_cast<float *>(p);
+            q_cap = qf;
+        }
+        if (pages > page_cap) {
+            const size_t bytes = align256(pages) + align256(size_t(pages) * 8) + align256(size_t(pages) * 4) + 256;
+            void *p = nullptr;
+            hip_ok(hipMalloc(&p, bytes), "hipMalloc scores");
+            owned.push_back(p);
+            uint8_t *b = static_cast<uint8_t *>(p);
+            mask = b;
+            scores = reinterpret_cast<double *>(b + align256(pages));
+            sel = reinterpret_cast<uint32_t *>(b + align256(pages) + align256(size_t(pages) * 8));
+            cnt = reinterpret_cast<uint32_t *>(b + bytes - 256);
+            page_cap = pages;
+        }
+    }
+
+    static size_t carve_bytes(uint32_t max_blocks, uint32_t qheads, uint32_t dim) {
+        return align256(size_t(kRowsPerLaunch) * qheads * dim * sizeof(float)) + align256(max_blocks) +
+               align256(size_t(max_blocks) * 8) + align256(size_t(max_blocks) * 4) + 256;
+    }
+
+    // Rows of one kvr_score call within the logits budget of the workspace.
+    uint32_t rows_per_call(uint32_t pages) const {
+        const size_t row_bytes = size_t(pages) * qheads * sizeof(double);
+        if (row_bytes > kLogitsBudget) throw std::length_error("page softmax needs a larger per-row logits budget");
+        return uint32_t(std::max<size_t>(1, std::min<size_t>(kRowsPerLaunch, kLogitsBudget / row_bytes)));
+    }
+
+    void check_frame(const PageSummaries &s, const QueryScoreFrame &f) const {
+        const size_t n = f.starts.size();
+        require(n && f.counts.size() == n && f.score_mask.size() == n && f.transport_mask.size() == n,
+                "page softmax frame geometry mismatch");
+        require(n <= s.pages && s.page_tokens && s.kv_heads == kvheads && s.head_dim == dim,
+                "page softmax summaries do not cover the frame");
+        for (size_t b = 0; b < n; ++b)
+            require(f.counts[b] && f.starts[b] == uint64_t(b) * s.page_tokens && f.starts[b] <= f.accepted_through &&
+                        f.counts[b] <= f.accepted_through - f.starts[b],
+                    "invalid accepted Query extent");
+    }
+
+    std::vector<double> fetch(uint32_t pages, hipStream_t s) {
+        std::vector<double> out(pages);
+        hip_ok(hipMemcpyAsync(out.data(), scores, size_t(pages) * 8, hipMemcpyDeviceToHost, s), "scores D2H");
+        hip_ok(hipStreamSynchronize(s), "hipStreamSynchronize");
+        ok(kvr_check(ctx, s), "page softmax");
+        return out;
+    }
+};
+
+PageSoftmaxHip::PageSoftmaxHip(int device) : impl_(new Impl) {
+    impl_->device = device;
+    DeviceBinding bind(device);
+    ok(kvr_create(device, &impl_->ctx), "page softmax context");
+}
+
+size_t PageSoftmaxHip::workspace_bytes(uint32_t max_blocks, uint32_t qheads, uint32_t kvheads, uint32_t dim) {
+    require(max_blocks && qheads && kvheads && dim && qheads % kvheads == 0 &&
+                size_t(max_blocks) * qheads * sizeof(double) <= kLogitsBudget,
+            "invalid planned page softmax geometry");
+    const uint32_t rows =
+        uint32_t(std::min<size_t>(kRowsPerLaunch, kLogitsBudget / (size_t(max_blocks) * qheads * sizeof(double))));
+    return align256(kvr_workspace_bytes(1, max_blocks, rows, qheads, kvheads, dim)) +
+           Impl::carve_bytes(max_blocks, qheads, dim);
+}
+
+PageSoftmaxHip::PageSoftmaxHip(int device, void *workspace, size_t bytes, uint32_t max_blocks, uint32_t qheads,
+                               uint32_t kvheads, uint32_t dim)
+    : impl_(new Impl) {
+    const size_t need = workspace_bytes(max_blocks, qheads, kvheads, dim);
+    if (!workspace || reinterpret_cast<uintptr_t>(workspace) % 256 || bytes < need)
+        throw std::invalid_argument("page softmax borrowed workspace is missing, unaligned or too small");
+    Impl &m = *impl_;
+    m.device = device;
+    m.borrowed = true;
+    m.max_blocks = max_blocks;
+    m.qheads = qheads;
+    m.kvheads = kvheads;
+    m.dim = dim;
+    DeviceBinding bind(device);
+    ok(kvr_create(device, &m.ctx), "page softmax context");
+    const uint32_t rows =
+        uint32_t(std::min<size_t>(kRowsPerLaunch, kLogitsBudget / (size_t(max_blocks) * qheads * sizeof(double))));
+    const size_t ws = align256(kvr_workspace_bytes(1, max_blocks, rows, qheads, kvheads, dim));
+    ok(kvr_bind_workspace(m.ctx, workspace, ws), "page softmax workspace");
+    uint8_t *b = static_cast<uint8_t *>(workspace) + ws;
+    m.q = reinterpret_cast<float *>(b);
+    m.q_cap = size_t(rows) * qheads * dim;
+    b += align256(size_t(kRowsPerLaunch) * qheads * dim * sizeof(float));
+    m.mask = b;
+    b += align256(max_blocks);
+    m.scores = reinterpret_cast<double *>(b);
+    b += align256(size_t(max_blocks) * 8);
+    m.sel = reinterpret_cast<uint32_t *>(b);
+    b += align256(size_t(max_blocks) * 4);
+    m.cnt = reinterpret_cast<uint32_t *>(b);
+    m.page_cap = max_blocks;
+}
+
+PageSoftmaxHip::~PageSoftmaxHip() = default;
+
+std::vector<double> PageSoftmaxHip::score(const PageSummaries &sums, PageQueryView v, const QueryScoreFrame &frame,
+                                          GqaScoreAggregation aggregation) {
+    Impl &m = *impl_;
+    const kvr_aggregation agg = to_kvr(aggregation);
+    require((v.data || v.layer_data) && v.layer_rows && v.layers && v.rows && v.head_dim && v.kv_heads &&
+                v.query_heads && v.query_heads % v.kv_heads == 0 && v.layers == sums.layers.size(),
+            "page softmax geometry mismatch");
+    if (!m.borrowed) {
+        m.qheads = v.query_heads;
+        m.kvheads = v.kv_heads;
+        m.dim = v.head_dim;
+    }
+    require(v.query_heads == m.qheads && v.kv_heads == m.kvheads && v.head_dim == m.dim,
+            "page softmax geometry mismatch");
+    m.check_frame(sums, frame);
+    const uint32_t n = uint32_t(frame.starts.size());
+    std::vector<double> result(n, 0.0);
+    if (std::none_of(frame.score_mask.begin(), frame.score_mask.end(), [](uint8_t x) { return x != 0; }))
+        return result;
+    uint32_t active = 0;
+    for (uint32_t l = 0; l < v.layers; ++l) {
+        require(v.layer_rows[l] <= v.rows, "page softmax row count exceeds its storage");
+        active += v.layer_rows[l] != 0;
+    }
+    if (!active) return result;
+    DeviceBinding bind(m.device);
+    uint32_t batch = std::min(m.rows_per_call(n), v.rows);
+    if (m.borrowed) batch = std::min<uint32_t>(batch, uint32_t(m.q_cap / (size_t(m.qheads) * m.dim)));
+    m.reserve(batch, n);
+    const hipStream_t s = m.stream();
+    StreamDrain drain{s};
+    const size_t qw = size_t(v.query_heads) * v.head_dim;
+    hip_ok(hipMemcpyAsync(m.mask, frame.score_mask.data(), n, hipMemcpyHostToDevice, s), "mask H2D");
+    bool accumulate = false;
+    for (uint32_t l = 0; l < v.layers; ++l) {
+        if (!v.layer_rows[l]) continue;
+        require(sums.layers[l] != nullptr, "page softmax missing active layer storage");
+        const float *base = v.layer_data ? v.layer_data[l] : v.data + size_t(l) * v.rows * qw;
+        require(base != nullptr, "missing active Query layer storage");
+        for (uint32_t r0 = 0; r0 < v.layer_rows[l]; r0 += batch) {
+            const uint32_t rows = std::min(batch, v.layer_rows[l] - r0);
+            hip_ok(hipMemcpyAsync(m.q, base + size_t(r0) * qw, size_t(rows) * qw * sizeof(float),
+                                  hipMemcpyHostToDevice, s),
+                   "query H2D");
+            kvr_query q{};
+            q.data = m.q;
+            q.scalar = KVR_FMT_F32;
+            q.rows = rows;
+            q.query_heads = v.query_heads;
+            q.kv_heads = v.kv_heads;
+            q.head_dim = v.head_dim;
+            q.row_stride = qw * sizeof(float);
+            q.head_stride = size_t(v.head_dim) * sizeof(float);
+            q.dim_stride = sizeof(float);
+            q.attention_scale = v.attention_scale;
+            ok(kvr_score(m.ctx, &q, sums.layers[l], 1, n, m.mask, agg, active, accumulate, m.scores, 0, s),
+               "page softmax");
+            accumulate = true;
+        }
+    }
+    result = m.fetch(n, s);
+    drain.armed = false;
+    return result;
+}
+
+std::vector<double> PageSoftmaxHip::score_current_layer(const PageSummaries &sums, NativeCurrentLayerQuery q,
+                                                        const QueryScoreFrame &frame, void *producer_stream) {
+    Impl &m = *impl_;
+    validate_native_layer_query(q);
+    require(q.layer < sums.layers.size() && sums.layers[q.layer], "native Query layer has no summaries");
+    if (!m.borrowed) {
+        m.qheads = q.query_heads;
+        m.kvheads = q.kv_heads;
+        m.dim = q.head_dim;
+    }
+    require(q.query_heads == m.qheads && q.kv_heads == m.kvheads && q.head_dim == m.dim,
+            "native Query or score frame geometry mismatch");
+    m.check_frame(sums, frame);
+    const uint32_t n = uint32_t(frame.starts.size());
+    DeviceBinding bind(m.device);
+    const hipStream_t s = producer_stream ? static_cast<hipStream_t>(producer_stream) : m.stream();
+    if (capturing(s)) throw std::invalid_argument("native Query selection requires an eager stream");
+    hipPointerAttribute_t attr{};
+    const hipError_t pe = hipPointerGetAttributes(&attr, q.data);
+    if (pe != hipSuccess) (void)hipGetLastError();  // unknown to the runtime: ordinary host memory
+    if (pe != hipSuccess || attr.type != hipMemoryTypeDevice || attr.device != m.device)
+        throw std::invalid_argument("native Query is not stored on its scoring device");
+    if (size_t(q.rows) * q.query_heads * n * sizeof(double) > kLogitsBudget)
+        throw std::length_error("native Query exceeds planned logits range");
+    m.reserve(0, n);
+    StreamDrain drain{s};
+    hip_ok(hipMemcpyAsync(m.mask, frame.score_mask.data(), n, hipMemcpyHostToDevice, s), "mask H2D");
+    kvr_query kq{};
+    kq.data = q.data;
+    kq.scalar = query_format(q.scalar);
+    kq.rows = q.rows;
+    kq.query_heads = q.query_heads;
+    kq.kv_heads = q.kv_heads;
+    kq.head_dim = q.head_dim;
+    kq.row_stride = q.row_stride;
+    kq.head_stride = q.head_stride;
+    kq.dim_stride = q.dimension_stride;
+    kq.attention_scale = q.attention_scale;
+    ok(kvr_score(m.ctx, &kq, sums.layers[q.layer], 1, n, m.mask, KVR_AGG_MEAN, 1, 0, m.scores, 0, s),
+       "page softmax");
+    auto out = m.fetch(n, s);
+    drain.armed = false;
+    return out;
+}
+
+std::vector<uint32_t> PageSoftmaxHip::pick(const std::vector<double> &scores, uint32_t budget,
+                                           const std::vector<uint32_t> &mandatory, TieRule tie,
+                                           bool signed_scores) {
+    Impl &m = *impl_;
+    const uint32_t n = uint32_t(scores.size());
+    require(budget, "invalid scored selection frame (budget 0)");
+    require(mandatory.size() <= KVR_MAX_INLINE_MANDATORY, "more mandatory pages than one call carries");
+    if (!n) return {};
+    std::vector<uint32_t> mand(mandatory);
+    std::sort(mand.begin(), mand.end());
+    mand.erase(std::unique(mand.begin(), mand.end()), mand.end());
+    for (uint32_t id : mand) require(id < n, "mandatory page outside the scored index");
+    if (mand.size() > budget) throw std::invalid_argument("mandatory pages exceed the selection budget");
+    const uint32_t k = std::min(budget, n);
+    DeviceBinding bind(m.device);
+    m.reserve(0, n);
+    const hipStream_t s = m.stream();
+    StreamDrain drain{s};
+    hip_ok(hipMemcpyAsync(m.scores, scores.data(), size_t(n) * 8, hipMemcpyHostToDevice, s), "scores H2D");
+    ok(kvr_select_topk(m.ctx, m.scores, 1, n, k, mand.data(), uint32_t(mand.size()),
+                       tie == TieRule::HigherFirst ? KVR_TIE_HIGHER_FIRST : KVR_TIE_LOWER_FIRST, signed_scores,
+                       m.sel, m.cnt, s),
+       "pick scored blocks");
+    std::vector<uint32_t> out(k);
+    uint32_t count = 0;
+    hip_ok(hipMemcpyAsync(out.data(), m.sel, size_t(k) * 4, hipMemcpyDeviceToHost, s), "selection D2H");
+    hip_ok(hipMemcpyAsync(&count, m.cnt, 4, hipMemcpyDeviceToHost, s), "count D2H");
+    hip_ok(hipStreamSynchronize(s), "hipStreamSynchronize");
+    drain.armed = false;
+    const kvr_status st = kvr_check(m.ctx, s);
+    if (st == KVR_ERR_SCORES) throw std::invalid_argument("scores must be finite and non-negative");
+    ok(st, "pick scored blocks");
+    out.resize(count);
+    return out;
+}
+
+size_t PageSoftmaxHip::device_bytes() const {
+    size_t b = kvr_device_bytes(impl_->ctx);
+    if (!impl_->borrowed) b += impl_->q_cap * sizeof(float) + (impl_->page_cap ? impl_->page_cap * 13 + 256 : 0);
+    return b;
+}
+
+kvr_context *PageSoftmaxHip::context() const { return impl_->ctx; }
+
+// ---------------------------------------------------------------------------
+// Stage-in entry points.
+struct kvmem_gpu_state {
+    kvr_context *ctx = nullptr;
+    // two pinned slabs: one fills while the other's copy is in flight
+    static constexpr size_t kSlab = size_t(32) << 20;
+    uint8_t *slab[2] = {nullptr, nullptr};
+    hipEvent_t slab_done[2] = {nullptr, nullptr};
+    bool slab_busy[2] = {false, false};
+    int cur = 0;
+    size_t used = 0;
+    std::vector<const void *> src;
+    std::vector<void *> dst;
+    std::vector<size_t> bytes;
+    // decode running mean-K
+    float *acc = nullptr;
+    uint32_t *acc_count = nullptr;
+    uint32_t n_layer = 0, n_embd = 0;
+    std::vector<uint64_t> acc_pos;
+};
+
+namespace {
+thread_local kvmem_gpu_state *g_state = nullptr;
+
+bool report(const char *what, const char *detail) {
+    std::fprintf(stderr, "kvmem stage-in: %s: %s\n", what, detail);
+    return false;
+}
+bool report_kvr(const char *what) { return report(what, kvr_last_error()); }
+bool report_hip(const char *what, hipError_t e) { return report(what, hipGetErrorString(e)); }
+
+hipStream_t copy_stream(kvmem_gpu_state *st) { return static_cast<hipStream_t>(kvr_copy_stream(st->ctx)); }
+
+void release_slabs(kvmem_gpu_state *st) {
+    for (int i = 0; i < 2; ++i) {
+        if (st->slab_done[i]) {
+            (void)hipEventSynchronize(st->slab_done[i]);
+            (void)hipEventDestroy(st->slab_done[i]);
+            st->slab_done[i] = nullptr;
+        }
+        if (st->slab[i]) (void)kvr_host_free(st->slab[i]);
+        st->slab[i] = nullptr;
+        st->slab_busy[i] = false;
+    }
+    st->used = 0;
+    st->src.clear();
+    st->dst.clear();
+    st->bytes.clear();
+}
+
+int64_t micros_since(std::chrono::steady_clock::time_point t0) {
+    return std::chrono::duration_cast<std::chrono::microseconds>(std::chrono::steady_clock::now() - t0).count();
+}
+}  // namespace
+
+kvmem_gpu_state *kvmem_gpu_state_create() {
+    auto *st = new kvmem_gpu_state;
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || kvr_create(device, &st->ctx) != KVR_OK) {
+        report_kvr("state create");
+        delete st;
+        return nullptr;
+    }
+    if (!g_state) g_state = st;
+    return st;
+}
+
+void kvmem_gpu_state_free(kvmem_gpu_state *st) {
+    if (!st) return;
+    if (st->ctx) (void)kvr_check(st->ctx, nullptr);
+    release_slabs(st);
+    if (st->acc) (void)hipFree(st->acc);
+    if (st->acc_count) (void)hipFree(st->acc_count);
+    if (st->ctx) (void)kvr_destroy(st->ctx);
+    if (g_state == st) g_state = nullptr;
+    delete st;
+}
+
+void kvmem_gpu_state_make_current(kvmem_gpu_state *st) { g_state = st; }
+
+bool kvmem_stagein_gpu_ready(size_t, size_t) {
+    if (!g_state && !kvmem_gpu_state_create()) return false;
+    kvmem_gpu_state *st = g_state;
+    for (int i = 0; i < 2; ++i) {
+        if (st->slab[i]) continue;
+        void *p = nullptr;
+        if (kvr_host_alloc(kvmem_gpu_state::kSlab, &p) != KVR_OK) return report_kvr("pinned slab");
+        st->slab[i] = static_cast<uint8_t *>(p);
+        if (hipError_t e = hipEventCreateWithFlags(&st->slab_done[i], hipEventDisableTiming); e != hipSuccess)
+            return report_hip("slab event", e);
+    }
+    return true;
+}
+
+void kvmem_stagein_gpu_free() {
+    if (!g_state) return;
+    kvmem_stagein_sync();
+    release_slabs(g_state);
+}
+
+bool kvmem_stagein_h2d_bytes(void *gpu_dst, const void *host, size_t n) {
+    if (!g_state || !gpu_dst || !host) return report("h2d", "stage-in is not ready or a pointer is null");
+    if (!n) return true;
+    const hipStream_t s = copy_stream(g_state);
+    if (hipError_t e = hipMemcpyAsync(gpu_dst, host, n, hipMemcpyHostToDevice, s); e != hipSuccess)
+        return report_hip("h2d", e);
+    if (hipError_t e = hipStreamSynchronize(s); e != hipSuccess) return report_hip("h2d fence", e);
+    return true;
+}
+
+void kvmem_stagein_sync() {
+    if (g_state) (void)hipStreamSynchronize(copy_stream(g_state));
+}
+
+bool kvmem_stagein_sync_checked() {
+    if (!g_state) return report("sync", "stage-in is not ready");
+    if (kvr_check(g_state->ctx, kvr_copy_stream(g_state->ctx)) != KVR_OK) return report_kvr("sync");
+    return true;
+}
+
+bool kvmem_stagein_flush(int64_t *copy_us, int64_t *rope_us, int64_t *hadamard_us, int64_t *set_us) {
+    const auto t0 = std::chrono::steady_clock::now();
+    if (rope_us) *rope_us = 0;
+    if (hadamard_us) *hadamard_us = 0;
+    kvmem_gpu_state *st = g_state;
+    if (!st) return report("flush", "stage-in is not ready");
+    if (st->src.empty()) return true;
+    const hipStream_t s = copy_stream(st);
+    // one launch moves every queued record from the pinned slab to its rows
+    if (kvr_d2d_batched(st->ctx, st->src.data(), st->dst.data(), st->bytes.data(), uint32_t(st->src.size()), s) !=
+        KVR_OK)
+        return report_kvr("flush");
+    if (hipError_t e = hipEventRecord(st->slab_done[st->cur], s); e != hipSuccess) return report_hip("flush", e);
+    st->slab_busy[st->cur] = true;
+    st->src.clear();
+    st->dst.clear();
+    st->bytes.clear();
+    st->used = 0;
+    st->cur ^= 1;
+    if (st->slab_busy[st->cur]) {
+        // the other slab's copy must have read it before it is refilled
+        if (hipError_t e = hipEventSynchronize(st->slab_done[st->cur]); e != hipSuccess)
+            return report_hip("slab reuse", e);
+        st->slab_busy[st->cur] = false;
+    }
+    if (copy_us) *copy_us += micros_since(t0);
+    (void)set_us;  // the copy is the set: no separate phase
+    return true;
+}
+
+bool kvmem_stagein_enqueue_v(const void *packed, size_t nbytes, uint8_t *dst, int64_t *set_us) {
+    const auto t0 = std::chrono::steady_clock::now();
+    kvmem_gpu_state *st = g_state;
+    if (!st || !st->slab[0]) return report("enqueue", "stage-in is not ready");
+    if (!packed || !dst) return report("enqueue", "null record or destination");
+    if (!nbytes) return true;
+    if (nbytes > kvmem_gpu_state::kSlab) return report("enqueue", "record larger than the 32 MiB slab");
+    if (st->used + nbytes > kvmem_gpu_state::kSlab || st->src.size() >= 8192)
+        if (!kvmem_stagein_flush(nullptr, nullptr, nullptr, nullptr)) return false;
+    uint8_t *slot = st->slab[st->cur] + st->used;
+    std::memcpy(slot, packed, nbytes);
+    st->src.push_back(slot);
+    st->dst.push_back(dst);
+    st->bytes.push_back(nbytes);
+    st->used += (nbytes + 15) / 16 * 16;  // keep records 16-byte aligned in the slab
+    if (set_us) *set_us += micros_since(t0);
+    return true;
+}
+
+bool kvmem_d2d_batched(const void *const *src, void *const *dst, const size_t *nbytes, int n) {
+    if (!g_state && !kvmem_gpu_state_create()) return false;
+    if (n < 0) return report("d2d", "negative op count");
+    if (kvr_d2d_batched(g_state->ctx, src, dst, nbytes, uint32_t(n), kvr_copy_stream(g_state->ctx)) != KVR_OK)
+        return report_kvr("d2d");
+    return true;
+}
+
+bool kvmem_meank_ready(uint32_t n_layer, uint32_t n_embd) {
+    if (!n_layer || !n_embd) return false;
+    if (!g_state && !kvmem_gpu_state_create()) return false;
+    kvmem_gpu_state *st = g_state;
+    if (st->acc && st->n_layer == n_layer && st->n_embd == n_embd) return true;
+    kvmem_meank_free();
+    const size_t bytes = size_t(n_layer) * n_embd * sizeof(float);
+    if (hipError_t e = hipMalloc(&st->acc, bytes); e != hipSuccess) {
+        st->acc = nullptr;
+        return report_hip("meank acc", e);
+    }
+    if (hipError_t e = hipMalloc(&st->acc_count, size_t(n_layer) * sizeof(uint32_t)); e != hipSuccess) {
+        st->acc_count = nullptr;
+        kvmem_meank_free();
+        return report_hip("meank count", e);
+    }
+    st->n_layer = n_layer;
+    st->n_embd = n_embd;
+    st->acc_pos.assign(n_layer, 0);
+    const hipStream_t s = copy_stream(st);
+    if (hipMemsetAsync(st->acc, 0, bytes, s) != hipSuccess ||
+        hipMemsetAsync(st->acc_count, 0, size_t(n_layer) * sizeof(uint32_t), s) != hipSuccess) {
+        kvmem_meank_free();
+        return report("meank", "zeroing failed");
+    }
+    return true;
+}
+
+void kvmem_meank_free() {
+    kvmem_gpu_state *st = g_state;
+    if (!st) return;
+    if (st->acc || st->acc_count) (void)hipStreamSynchronize(copy_stream(st));
+    if (st->acc) (void)hipFree(st->acc);
+    if (st->acc_count) (void)hipFree(st->acc_count);
+    st->acc = nullptr;
+    st->acc_count = nullptr;
+    st->n_layer = st->n_embd = 0;
+    st->acc_pos.clear();
+}
+
+void kvmem_meank_zero(uint32_t il) {
+    kvmem_gpu_state *st = g_state;
+    if (!st || !st->acc || il >= st->n_layer) return;
+    (void)hipMemsetAsync(st->acc + size_t(il) * st->n_embd, 0, size_t(st->n_embd) * sizeof(float), copy_stream(st));
+    st->acc_pos[il] = 0;
+}
+
+bool kvmem_meank_add(uint32_t il, kvr_format ty, const void *gpu_k, uint32_t tok0, uint32_t n_keep,
+                     uint32_t n_embd, int64_t ne0, size_t nb0, size_t nb1, size_t nb2) {
+    kvmem_gpu_state *st = g_state;
+    if (!st || !st->acc || !gpu_k || !n_keep || !n_embd || ne0 <= 0 || il >= st->n_layer || n_embd != st->n_embd ||
+        n_embd % uint64_t(ne0))
+        return false;
+    // One running sum per layer: a single page as long as the layer's
+    // position counter, which kvmem_meank_zero resets (position 0 restarts).
+    const uint8_t *k = static_cast<const uint8_t *>(gpu_k) + size_t(tok0) * nb2;
+    const uint32_t heads = uint32_t(n_embd / uint64_t(ne0));
+    if (kvr_summary_accumulate(st->ctx, st->acc + size_t(il) * n_embd, st->acc_count + il, 0xffffffffu, k, ty,
+                               st->acc_pos[il], n_keep, heads, uint32_t(ne0), nb2, nb1, nb0,
+                               kvr_copy_stream(st->ctx)) != KVR_OK)
+        return report_kvr("meank add");
+    st->acc_pos[il] += n_keep;
+    return true;
+}
+
+bool kvmem_meank_d2h(uint32_t il, float *host, uint32_t n_embd) {
+    kvmem_gpu_state *st = g_state;
+    if (!st || !st->acc || !host || il >= st->n_layer || n_embd != st->n_embd) return false;
+    const hipStream_t s = copy_stream(st);
+    if (hipError_t e = hipMemcpyAsync(host, st->acc + size_t(il) * n_embd, size_t(n_embd) * sizeof(float),
+                                      hipMemcpyDeviceToHost, s);
+        e != hipSuccess)
+        return report_hip("meank D2H", e);
+    if (hipError_t e = hipStreamSynchronize(s); e != hipSuccess) return report_hip("meank D2H", e);
+    return true;
+}
+
+// ---------------------------------------------------------------------------
+RecallTransfer::RecallTransfer(kvr_context *ctx, std::vector<kvr_plane> planes, uint32_t lanes, uint32_t page_tokens,
+                               const uint32_t *selected, const uint32_t *count, uint32_t k, kvr_copy_engine engine,
+                               void *stream, void *ready)
+    : ctx_(ctx), planes_(std::move(planes)), lanes_(lanes ? lanes : 1), page_tokens_(page_tokens), k_(k),
+      selected_(selected), count_(count), engine_(engine), stream_(stream), ready_(ready) {
+    require(ctx_ && !planes_.empty() && planes_.size() <= KVR_MAX_PLANES && page_tokens_ && k_ && selected_ &&
+                count_,
+            "invalid recall transfer plan");
+    if (!stream_) stream_ = kvr_copy_stream(ctx_);
+    hipEvent_t ev = nullptr;
+    hip_ok(hipEventCreateWithFlags(&ev, hipEventDisableTiming), "transfer event");
+    done_ = ev;
+}
+
+RecallTransfer::~RecallTransfer() {
+    (void)abort();
+    if (done_) (void)hipEventDestroy(static_cast<hipEvent_t>(done_));
+}
+
+void RecallTransfer::start_spill() {
+    if (phase_ != Phase::Prepared) throw std::logic_error("spill starts once, from a prepared transfer");
+    phase_ = Phase::Spilled;
+}
+
+void RecallTransfer::start_restore() {
+    if (phase_ != Phase::Spilled) throw std::logic_error("restore starts after the spill completed");
+    const hipStream_t s = static_cast<hipStream_t>(stream_);
+    if (ready_) hip_ok(hipStreamWaitEvent(s, static_cast<hipEvent_t>(ready_), 0), "selection event");
+    ok(kvr_stage_in(ctx_, planes_.data(), uint32_t(planes_.size()), lanes_, page_tokens_, selected_, count_, k_,
+                    engine_, s),
+       "recall restore");
+    hip_ok(hipEventRecord(static_cast<hipEvent_t>(done_), s), "transfer event");
+    phase_ = Phase::Restoring;
+}
+
+TransferPoll RecallTransfer::poll() {
+    TransferPoll p;
+    switch (phase_) {
+    case Phase::Prepared: return p;
+    case Phase::Spilled:
+    case Phase::Ready:
+    case Phase::Published: p.status = TransferStatus::Complete; return p;
+    case Phase::Failed:
+    case Phase::Aborted:
+        p.status = TransferStatus::Failed;
+        p.error = error_.empty() ? "transfer aborted" : error_;
+        return p;
+    case Phase::Restoring: break;
+    }
+    const hipError_t e = hipEventQuery(static_cast<hipEvent_t>(done_));
+    if (e == hipErrorNotReady) return p;
+    if (e == hipSuccess) {
+        if (kvr_check(ctx_, stream_) == KVR_OK) {
+            phase_ = Phase::Ready;
+            p.status = TransferStatus::Complete;
+            return p;
+        }
+        error_ = kvr_last_error();
+    } else {
+        error_ = hipGetErrorString(e);
+    }
+    phase_ = Phase::Failed;
+    p.status = TransferStatus::Failed;
+    p.error = error_;
+    return p;
+}
+
+void RecallTransfer::publish() {
+    if (phase_ != Phase::Ready) throw std::logic_error("publish needs a completed restore");
+    phase_ = Phase::Published;
+}
+
+AbortResult RecallTransfer::abort() noexcept {
+    if (phase_ == Phase::Restoring) (void)hipEventSynchronize(static_cast<hipEvent_t>(done_));
+    const bool touched = phase_ == Phase::Restoring || phase_ == Phase::Ready || phase_ == Phase::Failed;
+    if (phase_ != Phase::Published) phase_ = Phase::Aborted;
+    return touched ? AbortResult::SessionInvalidated : AbortResult::PreviousViewPreserved;
+}
+
+// ---------------------------------------------------------------------------
+SummaryCapture::SummaryCapture(kvr_context *ctx, uint32_t layers, uint32_t max_pages, uint32_t page_tokens,
+                               uint32_t kv_heads, uint32_t head_dim)
+    : ctx_(ctx), layers_(layers), max_pages_(max_pages), page_tokens_(page_tokens), kv_heads_(kv_heads),
+      head_dim_(head_dim) {
+    require(ctx_ && layers_ && max_pages_ && page_tokens_ && kv_heads_ && head_dim_, "invalid capture geometry");
+    const size_t cells = size_t(layers_) * max_pages_ * kv_heads_ * head_dim_;
+    hip_ok(hipMalloc(&sums_, cells * sizeof(float)), "capture sums");
+    hip_ok(hipMalloc(&means_, cells * sizeof(float)), "capture means");
+    hip_ok(hipMalloc(&summaries_, cells * sizeof(uint16_t)), "capture summaries");
+    hip_ok(hipMalloc(&counts_, size_t(layers_) * max_pages_ * sizeof(uint32_t)), "capture counts");
+    hip_ok(hipMemset(counts_, 0, size_t(layers_) * max_pages_ * sizeof(uint32_t)), "capture counts");
+}
+
+SummaryCapture::~SummaryCapture() {
+    (void)kvr_check(ctx_, nullptr);
+    (void)hipFree(sums_);
+    (void)hipFree(means_);
+    (void)hipFree(summaries_);
+    (void)hipFree(counts_);
+}
+
+void SummaryCapture::capture(uint32_t layer, const void *k, kvr_format scalar, uint64_t pos0, uint32_t n,
+                             size_t token_stride, size_t head_stride, size_t dim_stride, void *stream) {
+    require(layer < layers_, "capture layer outside the stack");
+    if (!n) return;
+    require(pos0 + n <= uint64_t(max_pages_) * page_tokens_, "capture beyond the planned pages");
+    const size_t width = size_t(kv_heads_) * head_dim_;
+    ok(kvr_summary_accumulate(ctx_, sums_ + size_t(layer) * max_pages_ * width, counts_ + size_t(layer) * max_pages_,
+                              page_tokens_, k, scalar, pos0, n, kv_heads_, head_dim_, token_stride, head_stride,
+                              dim_stride, stream),
+       "summary capture");
+}
+
+PageSummaries SummaryCapture::finalize(uint32_t pages, void *stream) {
+    require(pages && pages <= max_pages_, "finalize beyond the planned pages");
+    const size_t width = size_t(kv_heads_) * head_dim_;
+    PageSummaries out;
+    out.pages = pages;
+    out.page_tokens = page_tokens_;
+    out.kv_heads = kv_heads_;
+    out.head_dim = head_dim_;
+    for (uint32_t l = 0; l < layers_; ++l) {
+        const size_t off = size_t(l) * max_pages_ * width;
+        ok(kvr_summary_finalize(ctx_, sums_ + off, counts_ + size_t(l) * max_pages_, pages, uint32_t(width),
+                                means_ + off, summaries_ + off, stream),
+           "summary finalize");
+        out.layers.push_back(summaries_ + off);
+    }
+    return out;
+}
+
+const float *SummaryCapture::means(uint32_t layer) const {
+    require(layer < layers_, "capture layer outside the stack");
+    return means_ + size_t(layer) * max_pages_ * kv_heads_ * head_dim_;
+}
+
+}  // namespace kvmem_hip

@@ -1,0 +1,531 @@
+// Tests of the C++ host layer (include/kvmem_hip/kvmem_hip.hpp), written like
+// the reference's own C++ tests (kvmem/tests/graph_recall_test.cpp,
+// graph_recall_cuda_test.cpp): plain main, `require`, exceptions as failures.
+// The oracle (oracle/kvr_oracle.h) is the checker.
+//   test_host --cpu   host-only checks (no device calls)
+//   test_host --gpu   scorer, selection, stage-in, transfer and capture on cuda:0
+#include "kvmem_hip/kvmem_hip.hpp"
+#include "kvr_oracle.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <iostream>
+#include <numeric>
+#include <random>
+#include <stdexcept>
+#include <string>
+#include <thread>
+#include <vector>
+
+namespace kh = kvmem_hip;
+
+namespace {
+
+void require(bool ok, const std::string &msg) {
+    if (!ok) throw std::runtime_error(msg);
+}
+template <class E, class F> void rejects(F f, const std::string &msg) {
+    bool thrown = false;
+    try {
+        f();
+    } catch (const E &) {
+        thrown = true;
+    }
+    require(thrown, msg);
+}
+void hip(hipError_t e, const char *what) {
+    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+template <class T> struct Dev {
+    T *p = nullptr;
+    size_t n = 0;
+    explicit Dev(size_t count) : n(count) { hip(hipMalloc(&p, std::max<size_t>(1, n) * sizeof(T)), "hipMalloc"); }
+    Dev(const std::vector<T> &h) : Dev(h.size()) { up(h); }
+    ~Dev() { (void)hipFree(p); }
+    Dev(const Dev &) = delete;
+    void up(const std::vector<T> &h) {
+        hip(hipMemcpy(p, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice), "H2D");
+    }
+    std::vector<T> down() const {
+        std::vector<T> h(n);
+        hip(hipMemcpy(h.data(), p, n * sizeof(T), hipMemcpyDeviceToHost), "D2H");
+        return h;
+    }
+};
+
+double rel_err(const std::vector<double> &a, const std::vector<double> &b) {
+    double w = 0;
+    for (size_t i = 0; i < a.size(); ++i) w = std::max(w, std::abs(a[i] - b[i]) / std::max(std::abs(b[i]), 1e-300));
+    return w;
+}
+
+// ---- host-only -------------------------------------------------------------
+void frames() {
+    // graph_recall_test.cpp:23-31
+    auto frame = kh::query_score_frame(12, 4, 2, 0, 0, {2});
+    require(frame.score_mask == std::vector<uint8_t>({1, 1, 1}), "mandatory changed softmax denominator");
+    require(frame.transport_mask == std::vector<uint8_t>({1, 1, 0}), "mandatory transported graph mass");
+    auto small = kh::query_score_frame(11, 4, 4, 1, 1, {0, 2});
+    require(small.score_mask == std::vector<uint8_t>({1, 1, 1}) &&
+                small.transport_mask == std::vector<uint8_t>({0, 0, 0}) && small.counts.back() == 3,
+            "small-history or partial-tail domain mismatch");
+    auto constrained = kh::query_score_frame(12, 4, 2, 1, 1, {0, 2});
+    require(constrained.score_mask == std::vector<uint8_t>({0, 1, 0}), "keep-band score mask mismatch");
+    rejects<std::invalid_argument>([] { kh::query_score_frame(12, 0, 2, 0, 0, {}); }, "zero block size accepted");
+    rejects<std::invalid_argument>([] { kh::query_score_frame(12, 4, 0, 0, 0, {}); }, "zero budget accepted");
+    rejects<std::invalid_argument>([] { kh::query_score_frame(12, 4, 2, 0, 0, {3}); }, "outside fixed block accepted");
+    // against the oracle on random frames
+    std::mt19937_64 rng(7);
+    for (int trial = 0; trial < 300; ++trial) {
+        const uint64_t accepted = rng() % 5000;
+        const uint32_t bt = 1 + rng() % 300, budget = 1 + rng() % 40, sink = rng() % 5, recent = rng() % 5;
+        const uint32_t pages = uint32_t((accepted + bt - 1) / bt);
+        std::vector<uint32_t> fixed;
+        for (uint32_t i = 0; pages && i < 3; ++i) fixed.push_back(uint32_t(rng() % pages));
+        auto f = kh::query_score_frame(accepted, bt, budget, sink, recent, fixed);
+        std::vector<uint64_t> st(pages + 1);
+        std::vector<uint32_t> ct(pages + 1);
+        std::vector<uint8_t> sm(pages + 1), tm(pages + 1);
+        require(orc_query_score_frame(accepted, bt, budget, sink, recent, fixed.data(), uint32_t(fixed.size()),
+                                      st.data(), ct.data(), sm.data(), tm.data()) == ORC_OK,
+                "oracle frame failed");
+        for (uint32_t i = 0; i < pages; ++i)
+            require(f.starts[i] == st[i] && f.counts[i] == ct[i] && f.score_mask[i] == sm[i] &&
+                        f.transport_mask[i] == tm[i],
+                    "frame differs from the oracle");
+    }
+}
+
+void native_query_geometry() {
+    alignas(16) static uint16_t storage[4 * 8 * 64];
+    kh::NativeCurrentLayerQuery q;
+    q.data = storage;
+    q.bytes = sizeof storage;
+    q.rows = 4;
+    q.query_heads = 8;
+    q.kv_heads = 2;
+    q.head_dim = 64;
+    q.scalar = kh::NativeQueryScalar::Float16;
+    q.row_stride = 8 * 64 * 2;
+    q.head_stride = 64 * 2;
+    q.dimension_stride = 2;
+    kh::validate_native_layer_query(q);
+    auto heads_outer = q;  // [head][row][dim] is a valid permutation
+    heads_outer.head_stride = 4 * 64 * 2;
+    heads_outer.row_stride = 64 * 2;
+    kh::validate_native_layer_query(heads_outer);
+    auto overlap = q;
+    overlap.row_stride = 64 * 2;
+    rejects<std::invalid_argument>([&] { kh::validate_native_layer_query(overlap); }, "overlapping strides accepted");
+    auto small = q;
+    small.bytes = sizeof storage - 2;
+    rejects<std::invalid_argument>([&] { kh::validate_native_layer_query(small); }, "extent overflow accepted");
+    auto group = q;
+    group.kv_heads = 3;
+    rejects<std::invalid_argument>([&] { kh::validate_native_layer_query(group); }, "ragged GQA group accepted");
+    auto misaligned = q;
+    misaligned.data = reinterpret_cast<const uint8_t *>(storage) + 1;
+    rejects<std::invalid_argument>([&] { kh::validate_native_layer_query(misaligned); }, "misaligned Query accepted");
+}
+
+void workspace_geometry() {
+    const size_t a = kh::PageSoftmaxHip::workspace_bytes(7, 8, 2, 256);
+    const size_t b = kh::PageSoftmaxHip::workspace_bytes(8192, 8, 2, 256);
+    require(a > 0 && b > a && a % 256 == 0, "workspace arithmetic");
+    rejects<std::invalid_argument>([] { kh::PageSoftmaxHip::workspace_bytes(0, 8, 2, 64); }, "zero pages planned");
+    rejects<std::invalid_argument>([] { kh::PageSoftmaxHip::workspace_bytes(8, 6, 4, 64); }, "ragged group planned");
+    rejects<std::invalid_argument>([] { kh::PageSoftmaxHip::workspace_bytes(1u << 22, 32, 8, 128); },
+                                   "logits beyond 64 MiB planned");
+}
+
+void stagein_without_state() {
+    uint8_t b = 0;
+    require(!kh::kvmem_stagein_enqueue_v(&b, 1, &b, nullptr), "enqueue accepted before gpu_ready");
+    require(!kh::kvmem_stagein_sync_checked(), "sync_checked without a state");
+}
+
+// ---- device ----------------------------------------------------------------
+struct Stack {
+    uint32_t layers, pages, rows, dim, qheads, kvheads;
+    std::vector<float> means;  // [layers][pages][kw]
+    std::vector<float> query;  // [layers][rows][qheads][dim]
+    std::vector<Dev<uint16_t> *> dev;
+    kh::PageSummaries sums;
+    ~Stack() {
+        for (auto *d : dev) delete d;
+    }
+};
+
+// graph_recall_cuda_test.cpp:18-35 closed-form inputs: per-block key sums of
+// four tokens, mean = sum * (1/4).
+void build_stack(Stack &s) {
+    const size_t kw = size_t(s.kvheads) * s.dim, qw = size_t(s.qheads) * s.dim;
+    s.means.assign(size_t(s.layers) * s.pages * kw, 0.f);
+    for (uint32_t l = 0; l < s.layers; ++l)
+        for (uint32_t b = 0; b < s.pages; ++b)
+            for (size_t d = 0; d < kw; ++d)
+                s.means[(size_t(l) * s.pages + b) * kw + d] =
+                    float(int((b * 13 + d * 7 + l * 11) % 101) - 50) / 16 * (1.0f / 4);
+    s.query.resize(size_t(s.layers) * s.rows * qw);
+    for (size_t d = 0; d < s.query.size(); ++d) s.query[d] = float(int((d * 17) % 127) - 63) / 32;
+    s.sums.pages = s.pages;
+    s.sums.page_tokens = 4;
+    s.sums.kv_heads = s.kvheads;
+    s.sums.head_dim = s.dim;
+    for (uint32_t l = 0; l < s.layers; ++l) {
+        std::vector<uint16_t> h(size_t(s.pages) * kw);
+        for (size_t i = 0; i < h.size(); ++i) h[i] = orc_f32_to_f16(s.means[size_t(l) * s.pages * kw + i]);
+        s.dev.push_back(new Dev<uint16_t>(h));
+        s.sums.layers.push_back(s.dev.back()->p);
+    }
+}
+
+void qualification() {
+    kh::PageSoftmaxHip scorer(0);
+    struct Shape { uint32_t blocks, rows, dim, qheads, kvheads; };
+    for (auto agg : {kh::GqaScoreAggregation::Mean, kh::GqaScoreAggregation::Max, kh::GqaScoreAggregation::MaxLogit})
+        for (auto sh : {Shape{7, 129, 256, 8, 2}, Shape{8192, 2, 64, 4, 1}, Shape{8193, 2, 64, 4, 1},
+                        Shape{32769, 1, 64, 2, 1}}) {
+            Stack s{2, sh.blocks, sh.rows, sh.dim, sh.qheads, sh.kvheads};
+            build_stack(s);
+            const uint32_t counts[]{sh.rows, sh.rows};
+            auto frame = kh::query_score_frame(uint64_t(sh.blocks) * 4, 4, 3, 1, 1, {0, sh.blocks - 1});
+            kh::PageQueryView view{s.query.data(), counts, 2, sh.rows, sh.qheads, sh.kvheads, sh.dim};
+            std::vector<double> expected(sh.blocks);
+            const int oagg = agg == kh::GqaScoreAggregation::Mean ? ORC_AGG_MEAN
+                             : agg == kh::GqaScoreAggregation::Max ? ORC_AGG_MAX : ORC_AGG_MAX_LOGIT;
+            require(orc_page_softmax_scores(s.means.data(), s.query.data(), counts, 2, sh.rows, sh.qheads,
+                                            sh.kvheads, sh.dim, sh.blocks, frame.score_mask.data(), 0, oagg,
+                                            expected.data()) == ORC_OK,
+                    "oracle scores failed");
+            const auto actual = scorer.score(s.sums, view, frame, agg);
+            require(actual.size() == expected.size(), "score length");
+            for (size_t b = 0; b < actual.size(); ++b)
+                require(std::isfinite(actual[b]) && std::abs(actual[b] - expected[b]) <= 2e-6 + expected[b] * 3e-5,
+                        "page softmax differs from the oracle beyond the reference bound");
+            const double err = rel_err(actual, expected);
+            require(err <= 1e-9, "page softmax differs from the oracle beyond 1e-9");
+            const double mass = std::accumulate(actual.begin(), actual.end(), 0.0);
+            if (agg != kh::GqaScoreAggregation::MaxLogit)
+                require(std::abs(mass - sh.rows) <= sh.rows * 1e-12 * 64, "softmax mass was lost");
+            if (sh.blocks == 7) {
+                const size_t bytes = kh::PageSoftmaxHip::workspace_bytes(sh.blocks, sh.qheads, sh.kvheads, sh.dim);
+                Dev<uint8_t> ws(bytes);
+                kh::PageSoftmaxHip borrowed(0, ws.p, bytes, sh.blocks, sh.qheads, sh.kvheads, sh.dim);
+                const auto planned = borrowed.score(s.sums, view, frame, agg);
+                require(rel_err(planned, expected) <= 1e-9, "planned workspace differs from the oracle");
+                require(borrowed.device_bytes() <= bytes, "borrowed scorer owns device memory");
+                Stack big{2, 8, sh.rows, sh.dim, sh.qheads, sh.kvheads};
+                build_stack(big);
+                auto f8 = kh::query_score_frame(8 * 4, 4, 3, 1, 1, {});
+                rejects<std::length_error>([&] { borrowed.score(big.sums, view, f8, agg); },
+                                           "borrowed workspace grew");
+            }
+            std::cout << "  agg=" << int(agg) << " pages=" << sh.blocks << " rows=" << sh.rows << " D=" << sh.dim
+                      << " rel_err=" << err << "\n";
+        }
+    Stack s{2, 16, 2, 64, 4, 1};
+    build_stack(s);
+    const uint32_t counts[]{2, 2};
+    kh::PageQueryView view{s.query.data(), counts, 2, 2, 4, 1, 64};
+    auto short_frame = kh::query_score_frame(17 * 4, 4, 3, 0, 0, {});
+    rejects<std::invalid_argument>([&] { scorer.score(s.sums, view, short_frame); }, "frame beyond summaries accepted");
+    kh::PageQueryView bad = view;
+    bad.kv_heads = 3;
+    auto frame = kh::query_score_frame(16 * 4, 4, 3, 0, 0, {});
+    rejects<std::invalid_argument>([&] { scorer.score(s.sums, bad, frame); }, "ragged heads accepted");
+}
+
+void current_layer() {
+    kh::PageSoftmaxHip scorer(0);
+    const uint32_t pages = 300, rows = 3, qh = 8, kvh = 2, dim = 64;
+    Stack s{2, pages, rows, dim, qh, kvh};
+    build_stack(s);
+    // layer 1's query rows as fp16 in [head][row][dim] order on the device
+    const size_t qw = size_t(qh) * dim;
+    std::vector<uint16_t> qh16(size_t(qh) * rows * dim);
+    std::vector<float> qf(size_t(rows) * qw);
+    for (uint32_t r = 0; r < rows; ++r)
+        for (uint32_t h = 0; h < qh; ++h)
+            for (uint32_t d = 0; d < dim; ++d) {
+                const float x = s.query[size_t(rows) * qw + r * qw + h * dim + d];
+                const uint16_t b = orc_f32_to_f16(x);
+                qh16[(size_t(h) * rows + r) * dim + d] = b;
+                qf[r * qw + h * dim + d] = orc_f16_to_f32(b);
+            }
+    Dev<uint16_t> qd(qh16);
+    kh::NativeCurrentLayerQuery q;
+    q.data = qd.p;
+    q.bytes = qh16.size() * 2;
+    q.layer = 1;
+    q.rows = rows;
+    q.query_heads = qh;
+    q.kv_heads = kvh;
+    q.head_dim = dim;
+    q.scalar = kh::NativeQueryScalar::Float16;
+    q.row_stride = dim * 2;
+    q.head_stride = size_t(rows) * dim * 2;
+    q.dimension_stride = 2;
+    auto frame = kh::query_score_frame(uint64_t(pages) * 4, 4, 10, 2, 3, {});
+    hipStream_t producer;
+    hip(hipStreamCreateWithFlags(&producer, hipStreamNonBlocking), "stream");
+    const auto got = scorer.score_current_layer(s.sums, q, frame, producer);
+    hip(hipStreamDestroy(producer), "stream");
+    const uint32_t one[]{rows};
+    std::vector<double> expected(pages);
+    require(orc_page_softmax_scores(s.means.data() + size_t(pages) * kvh * dim, qf.data(), one, 1, rows, qh, kvh,
+                                    dim, pages, frame.score_mask.data(), 0, ORC_AGG_MEAN, expected.data()) == ORC_OK,
+            "oracle scores failed");
+    require(rel_err(got, expected) <= 1e-9, "current-layer scores differ from the oracle");
+    for (uint32_t j = 0; j < pages; ++j)
+        if (!frame.score_mask[j]) require(got[j] == 0.0, "masked page scored");
+    std::vector<float> host_q(size_t(rows) * qw);
+    kh::NativeCurrentLayerQuery on_host = q;
+    on_host.data = host_q.data();
+    on_host.bytes = host_q.size() * 4;
+    on_host.scalar = kh::NativeQueryScalar::Float32;
+    on_host.row_stride = qw * 4;
+    on_host.head_stride = dim * 4;
+    on_host.dimension_stride = 4;
+    rejects<std::invalid_argument>([&] { scorer.score_current_layer(s.sums, on_host, frame, nullptr); },
+                                   "host Query accepted as device Query");
+}
+
+void pick() {
+    kh::PageSoftmaxHip scorer(0);
+    std::mt19937_64 rng(11);
+    for (int trial = 0; trial < 60; ++trial) {
+        const uint32_t n = 1 + uint32_t(rng() % 3000), budget = 1 + uint32_t(rng() % 100);
+        std::vector<double> scores(n);
+        std::uniform_real_distribution<double> u(0, 1);
+        for (auto &x : scores) x = u(rng);
+        for (uint32_t i = 0; i < n / 3; ++i) scores[rng() % n] = scores[rng() % n];  // exact ties
+        std::vector<uint32_t> mand;
+        for (uint32_t i = 0; i < std::min<uint32_t>({3, budget, n}); ++i) mand.push_back(uint32_t(rng() % n));
+        std::sort(mand.begin(), mand.end());
+        mand.erase(std::unique(mand.begin(), mand.end()), mand.end());
+        for (auto tie : {kh::TieRule::LowerFirst, kh::TieRule::HigherFirst}) {
+            const auto got = scorer.pick(scores, budget, mand, tie);
+            std::vector<uint32_t> want(std::min(budget, n) + 1);
+            uint32_t nw = 0;
+            require(orc_pick_scored_blocks(scores.data(), n, mand.data(), uint32_t(mand.size()), budget,
+                                           tie == kh::TieRule::HigherFirst ? ORC_TIE_HIGHER_FIRST
+                                                                           : ORC_TIE_LOWER_FIRST,
+                                           0, want.data(), &nw) == ORC_OK,
+                    "oracle pick failed");
+            want.resize(nw);
+            require(got == want, "selection differs from the oracle");
+        }
+    }
+    // layerwise_selection_test.cpp:184-194: equal mass over six pages keeps {4,5}
+    require(scorer.pick(std::vector<double>(6, 1.0 / 6), 2, {}, kh::TieRule::HigherFirst) ==
+                std::vector<uint32_t>({4, 5}),
+            "reference tie rule");
+    // graph_recall_test.cpp:101-105: signed order
+    require(scorer.pick({-.8, -.2, -.5}, 2, {}, kh::TieRule::HigherFirst, true) == std::vector<uint32_t>({1, 2}),
+            "signed order");
+    rejects<std::invalid_argument>([&] { scorer.pick({-.8, -.2, -.5}, 2); }, "negative scores accepted");
+    rejects<std::invalid_argument>([&] { scorer.pick({1, 2, 3}, 1, {0, 1}); }, "mandatory over budget accepted");
+    require(scorer.pick({3, 1, 2}, 10) == std::vector<uint32_t>({0, 1, 2}), "budget above page count");
+}
+
+void stagein() {
+    require(kh::kvmem_stagein_gpu_ready(0, 0), "gpu_ready");
+    const size_t total = size_t(48) << 20;
+    Dev<uint8_t> dst(total);
+    hip(hipMemset(dst.p, 0, total), "memset");
+    std::mt19937_64 rng(5);
+    std::vector<uint8_t> want(total, 0);
+    size_t off = 0;
+    int records = 0;
+    while (off < total - (1 << 20)) {
+        const size_t n = 1 + rng() % (600 << 10);
+        std::vector<uint8_t> rec(n);
+        for (auto &b : rec) b = uint8_t(rng());
+        require(kh::kvmem_stagein_enqueue_v(rec.data(), n, dst.p + off, nullptr), "enqueue_v");
+        std::memcpy(want.data() + off, rec.data(), n);
+        std::fill(rec.begin(), rec.end(), 0);  // the caller's buffer is reusable on return
+        off += n + rng() % 64;
+        ++records;
+    }
+    int64_t copy_us = 0, rope_us = -1, had_us = -1, set_us = 0;
+    require(kh::kvmem_stagein_flush(&copy_us, &rope_us, &had_us, &set_us), "flush");
+    require(kh::kvmem_stagein_sync_checked(), "sync_checked");
+    require(dst.down() == want, "staged bytes differ");
+    std::vector<uint8_t> host(4096);
+    for (size_t i = 0; i < host.size(); ++i) host[i] = uint8_t(i * 7);
+    require(kh::kvmem_stagein_h2d_bytes(dst.p + 123, host.data(), host.size()), "h2d_bytes");
+    std::vector<const void *> src{dst.p + 123};
+    std::vector<void *> to{dst.p + (40 << 20)};
+    std::vector<size_t> nb{host.size()};
+    require(kh::kvmem_d2d_batched(src.data(), to.data(), nb.data(), 1), "d2d");
+    require(kh::kvmem_stagein_sync_checked(), "sync_checked");
+    const auto back = dst.down();
+    require(std::equal(host.begin(), host.end(), back.begin() + 123) &&
+                std::equal(host.begin(), host.end(), back.begin() + (40 << 20)),
+            "h2d / d2d bytes differ");
+    std::cout << "  " << records << " records, " << off << " bytes through two 32 MiB slabs\n";
+}
+
+void meank() {
+    const uint32_t layers = 2, heads = 2, dim = 64, embd = heads * dim, tokens = 10;
+    require(kh::kvmem_meank_ready(layers, embd), "meank_ready");
+    // fp16 K [token][head][dim] with padding between tokens
+    const size_t nb0 = 2, nb1 = dim * 2, nb2 = embd * 2 + 32;
+    std::vector<uint16_t> k(tokens * nb2 / 2);
+    orc_synth_normal_f16(3, 9, k.size(), k.data());
+    Dev<uint16_t> kd(k);
+    require(kh::kvmem_meank_add(1, KVR_FMT_F16, kd.p, 0, 4, embd, dim, nb0, nb1, nb2), "meank add");
+    require(kh::kvmem_meank_add(1, KVR_FMT_F16, kd.p, 4, 6, embd, dim, nb0, nb1, nb2), "meank add");
+    std::vector<float> got(embd), want(embd, 0.f);
+    require(kh::kvmem_meank_d2h(1, got.data(), embd), "meank d2h");
+    for (uint32_t c = 0; c < embd; ++c)
+        for (uint32_t t = 0; t < tokens; ++t)
+            want[c] += orc_f16_to_f32(k[(t * nb2 + (c / dim) * nb1 + (c % dim) * nb0) / 2]);
+    require(std::memcmp(got.data(), want.data(), embd * 4) == 0, "running mean-K differs from the token-order sum");
+    kh::kvmem_meank_zero(1);
+    require(kh::kvmem_meank_d2h(1, got.data(), embd), "meank d2h");
+    require(std::all_of(got.begin(), got.end(), [](float x) { return x == 0.f; }), "meank_zero left values");
+    require(!kh::kvmem_meank_add(5, KVR_FMT_F16, kd.p, 0, 1, embd, dim, nb0, nb1, nb2), "layer out of range");
+    kh::kvmem_meank_free();
+}
+
+void transfer() {
+    kvr_context *ctx = nullptr;
+    require(kvr_create(0, &ctx) == KVR_OK, "context");
+    const uint32_t T = 4096, W = 256, PT = 256, P = T / PT, K = 5;
+    std::vector<uint16_t> hist(size_t(T) * W);
+    orc_synth_normal_f16(4, 1, hist.size(), hist.data());
+    void *pin = nullptr;
+    require(kvr_host_alloc(hist.size() * 2, &pin) == KVR_OK, "pinned");
+    std::memcpy(pin, hist.data(), hist.size() * 2);
+    std::vector<double> scores(P);
+    for (uint32_t j = 0; j < P; ++j) scores[j] = double((j * 7) % P);
+    Dev<double> sd(scores);
+    Dev<uint32_t> sel(K), cnt(1);
+    Dev<uint16_t> slots(size_t(K) * PT * W);
+    require(kvr_select_topk(ctx, sd.p, 1, P, K, nullptr, 0, KVR_TIE_LOWER_FIRST, 0, sel.p, cnt.p, nullptr) == KVR_OK,
+            "select");
+    kvr_plane plane{};
+    plane.history = pin;
+    plane.format = KVR_FMT_F16;
+    plane.width = W;
+    plane.tokens = T;
+    plane.mode = KVR_GATHER_COPY;
+    plane.slots = slots.p;
+    hipEvent_t ready;
+    hip(hipEventCreateWithFlags(&ready, hipEventDisableTiming), "event");
+    hip(hipEventRecord(ready, static_cast<hipStream_t>(kvr_select_stream(ctx))), "event");
+    {
+        kh::RecallTransfer t(ctx, {plane}, 1, PT, sel.p, cnt.p, K, KVR_ENGINE_KERNEL, nullptr, ready);
+        require(t.poll().status == kh::TransferStatus::Pending, "pending before spill");
+        rejects<std::logic_error>([&] { t.start_restore(); }, "restore before spill accepted");
+        t.start_spill();
+        require(t.poll().status == kh::TransferStatus::Complete, "spill completes at once");
+        rejects<std::logic_error>([&] { t.publish(); }, "publish before restore accepted");
+        t.start_restore();
+        const auto t0 = std::chrono::steady_clock::now();
+        kh::TransferPoll p;
+        while ((p = t.poll()).status == kh::TransferStatus::Pending) {
+            require(std::chrono::steady_clock::now() - t0 < std::chrono::seconds(10), "restore never completed");
+            std::this_thread::sleep_for(std::chrono::microseconds(100));
+        }
+        require(p.status == kh::TransferStatus::Complete, "restore failed: " + p.error);
+        t.publish();
+        require(t.published(), "published");
+    }
+    const auto picked = sel.down();
+    std::vector<uint8_t> want(size_t(K) * PT * W * 2);
+    require(orc_gather(reinterpret_cast<const uint8_t *>(hist.data()), ORC_FMT_F16, W, T, PT, picked.data(), K,
+                       ORC_GATHER_COPY, want.data()) == ORC_OK,
+            "oracle gather");
+    const auto got = slots.down();
+    require(std::memcmp(got.data(), want.data(), want.size()) == 0, "restored slots differ from the oracle gather");
+    {
+        kh::RecallTransfer fresh(ctx, {plane}, 1, PT, sel.p, cnt.p, K);
+        require(fresh.abort() == kh::AbortResult::PreviousViewPreserved, "abort before restore keeps the view");
+        kh::RecallTransfer used(ctx, {plane}, 1, PT, sel.p, cnt.p, K);
+        used.start_spill();
+        used.start_restore();
+        require(used.abort() == kh::AbortResult::SessionInvalidated, "abort after restore invalidates");
+        require(used.poll().status == kh::TransferStatus::Failed, "aborted transfer polls failed");
+    }
+    hip(hipEventDestroy(ready), "event");
+    require(kvr_check(ctx, nullptr) == KVR_OK, "check");
+    kvr_host_free(pin);
+    kvr_destroy(ctx);
+}
+
+void capture() {
+    kvr_context *ctx = nullptr;
+    require(kvr_create(0, &ctx) == KVR_OK, "context");
+    const uint32_t layers = 2, pages = 16, pt = 64, kvh = 2, dim = 64, W = kvh * dim, T = pages * pt - 19;
+    kh::SummaryCapture cap(ctx, layers, pages, pt, kvh, dim);
+    std::vector<std::vector<float>> k(layers);
+    std::vector<Dev<float> *> kd;
+    for (uint32_t l = 0; l < layers; ++l) {
+        k[l].resize(size_t(T) * W);
+        orc_synth_normal_f32(8, 20 + l, k[l].size(), k[l].data());
+        kd.push_back(new Dev<float>(k[l]));
+    }
+    std::mt19937_64 rng(2);
+    for (uint32_t l = 0; l < layers; ++l)
+        for (uint32_t pos = 0; pos < T;) {
+            const uint32_t n = std::min<uint32_t>(T - pos, 1 + uint32_t(rng() % 150));
+            cap.capture(l, kd[l]->p + size_t(pos) * W, KVR_FMT_F32, pos, n, W * 4, dim * 4, 4);
+            pos += n;
+        }
+    const uint32_t full = (T + pt - 1) / pt;
+    auto sums = cap.finalize(full);
+    require(sums.layers.size() == layers && sums.pages == full, "finalized geometry");
+    require(kvr_check(ctx, nullptr) == KVR_OK, "check");
+    for (uint32_t l = 0; l < layers; ++l) {
+        std::vector<float> means(size_t(full) * W);
+        std::vector<uint16_t> s16(size_t(full) * W);
+        hip(hipMemcpy(means.data(), cap.means(l), means.size() * 4, hipMemcpyDeviceToHost), "D2H");
+        hip(hipMemcpy(s16.data(), sums.layers[l], s16.size() * 2, hipMemcpyDeviceToHost), "D2H");
+        for (uint32_t p = 0; p < full; ++p) {
+            const uint32_t t0 = p * pt, n = std::min(pt, T - t0);
+            for (uint32_t c = 0; c < W; ++c) {
+                float acc = 0.f;
+                for (uint32_t t = 0; t < n; ++t) acc += k[l][size_t(t0 + t) * W + c];
+                const float mean = acc * (1.0f / float(n));
+                require(std::memcmp(&means[size_t(p) * W + c], &mean, 4) == 0, "captured mean-K differs");
+                require(s16[size_t(p) * W + c] == orc_f32_to_f16(mean), "captured fp16 summary differs");
+            }
+        }
+    }
+    for (auto *d : kd) delete d;
+    kvr_destroy(ctx);
+}
+
+}  // namespace
+
+int main(int argc, char **argv) {
+    const bool gpu = argc > 1 && std::string(argv[1]) == "--gpu";
+    std::vector<std::pair<const char *, std::function<void()>>> tests = {
+        {"frames", frames}, {"native_query_geometry", native_query_geometry},
+        {"workspace_geometry", workspace_geometry}, {"stagein_without_state", stagein_without_state}};
+    if (gpu)
+        tests = {{"qualification", qualification}, {"current_layer", current_layer}, {"pick", pick},
+                 {"stagein", stagein},           {"meank", meank},                 {"transfer", transfer},
+                 {"capture", capture}};
+    for (auto &[name, fn] : tests) {
+        std::cout << "RUN  " << name << std::endl;
+        try {
+            fn();
+        } catch (const std::exception &e) {
+            std::cout << "FAIL " << name << ": " << e.what() << std::endl;
+            return 1;
+        }
+        std::cout << "PASS " << name << std::endl;
+    }
+    return 0;
+}
