@@ -187,6 +187,7 @@ private:
 // Capture side of the attn-qk hook: captured K rows of each layer go into
 // device running sums (kvr_summary_accumulate), and finalized pages become
 // the fp16 summaries a PageSummaries points at (kvr_summary_finalize).
+// The context must outlive the capture (and a RecallTransfer).
 class SummaryCapture {
 public:
     SummaryCapture(kvr_context *ctx, uint32_t layers, uint32_t max_pages, uint32_t page_tokens,

@@ -467,6 +467,7 @@ void capture() {
     kvr_context *ctx = nullptr;
     require(kvr_create(0, &ctx) == KVR_OK, "context");
     const uint32_t layers = 2, pages = 16, pt = 64, kvh = 2, dim = 64, W = kvh * dim, T = pages * pt - 19;
+    {  // the capture is destroyed before its context
     kh::SummaryCapture cap(ctx, layers, pages, pt, kvh, dim);
     std::vector<std::vector<float>> k(layers);
     std::vector<Dev<float> *> kd;
@@ -503,6 +504,7 @@ void capture() {
         }
     }
     for (auto *d : kd) delete d;
+    }
     kvr_destroy(ctx);
 }
 
