@@ -8,15 +8,16 @@ layer gathered (K and V) from pinned host history into an 8192-token device
 slot array per layer.  K is resident in HBM for scoring; page summaries are
 rebuilt from it inside every select.
 
-Timed step: scoring + selection of the whole stack (kvr_recall_layer per
-layer without planes, one select stream, descriptors built beforehand).
+Timed step: scoring + selection of the whole stack, one kvr_recall_stack
+call (layer l's softmax/top-k inside layer l+1's summary launch, one select
+stream, descriptors built beforehand).
 
 Reported:
   value        scored-KV GB/s = layers x (K bytes + fp16 summary bytes +
                Q bytes) / step time
-  roofline     the summary kernel (dominant): algorithmic bytes per launch /
+  roofline     the stack launch (dominant): algorithmic bytes per launch /
                its mean duration (HIP events the library records around it on
-               the select stream, inside the timed steps)
+               the select stream, inside the timed steps, on sampled layers)
   latency      select + stage-in per layer with every layer's stage-in on one
                copy stream beside the following selects (latency_us_per_layer)
   stage-in     gather GB/s per layer (separate pass) vs measured pinned H2D peak
@@ -175,12 +176,16 @@ def run(args):
                 for l in range(L)]
 
     def stack(descs, ev):
-        for l in range(L):
-            ctx.recall(descs[l], None, copy_stream)
+        # one call per stack: layer l's softmax/top-k runs inside layer l+1's
+        # summary launch
+        keep.append(ctx.recall_stack(descs, None, copy_stream))
+
+    keep = []
 
     def drain():
         for c in ctxs:
             c.check()
+        keep.clear()
 
     def layer_times(ev):
         """sampled layers: summary kernel, summary start -> selection written"""
@@ -253,7 +258,11 @@ def run(args):
     gpu_sel = sel.cpu().numpy().view(np.uint32)
     assert (cnt.cpu().numpy() == KSEL).all(), "every layer must select k pages"
 
-    alg_kernel_bytes = k_bytes + P * W * 2 + HQ * R * P * 8 + HQ * D * 2
+    # one stack launch: this layer's K read, fp16 summaries and logits
+    # written, Q read; the previous layer's logits read, terms written and
+    # read back, scores written
+    logit_bytes = HQ * R * P * 8
+    alg_kernel_bytes = k_bytes + P * W * 2 + logit_bytes + HQ * D * 2 + 3 * logit_bytes + P * 8
     achieved = alg_kernel_bytes / (kern_us_mean * 1e-6) / 1e9
     scored_gbps = L * geo["scored_bytes"] / (ms_per_step * 1e-3) / 1e9
     traffic = None
@@ -299,7 +308,7 @@ def run(args):
         "stagein_frac_h2d": round(stage_gbps / h2d, 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": "k_summary<f16, fused logits>",
+            "kernel": "k_summary_probs<f16> (layer l summaries + fused logits, layer l-1 softmax/top-k)",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
@@ -318,10 +327,11 @@ def run(args):
 
 
 def pmc_pass(args):
-    """Counter pass (run under rocprofv3 --pmc): three selects of one
-    128K-token layer (fused summary kernel over 256 MiB of fp16 K) and three
-    256 MiB device copies (4096 ops of 64 KiB, k_copy_ops) that calibrate
-    FETCH_SIZE / WRITE_SIZE against known byte counts."""
+    """Counter pass (run under rocprofv3 --pmc): a 4-layer stack over one
+    128K-token layer (k_summary, then three k_summary_probs launches over
+    256 MiB of fp16 K each, then k_probs) and three 256 MiB device copies
+    (4096 ops of 64 KiB, k_copy_ops) that calibrate FETCH_SIZE / WRITE_SIZE
+    against known byte counts."""
     import torch
     import kvmem_amd as K
     T, HKV, D, HQ, PT, KSEL = 131072, 8, 128, 32, 256, 32
@@ -340,10 +350,12 @@ def pmc_pass(args):
     ctx.check()
     keys = K.make_keys(kd, K.FMT_F16, T, HKV, D, PT)
     query = K.make_query(qd, K.FMT_F16, 1, HQ, HKV, D)
-    for _ in range(3):
-        ctx.recall_layer(keys=keys, summaries=s16, query=query, scores=scores, selected=sel, count=cnt,
-                         k=KSEL, aggregation=K.AGG_MEAN)
-        ctx.check()
+    desc = K.Context.layer_recall(keys=keys, summaries=s16, query=query, scores=scores, selected=sel, count=cnt,
+                                  k=KSEL, aggregation=K.AGG_MEAN)
+    # a 4-layer stack over the same layer: launches 2..4 are k_summary_probs
+    keep = ctx.recall_stack([desc] * 4)
+    ctx.check()
+    del keep
     op = 1 << 16
     n = T * W * 2 // op
     srcs = [kd.data_ptr() + i * op for i in range(n)]

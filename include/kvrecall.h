@@ -291,6 +291,17 @@ kvr_status kvr_stage_in(kvr_context *ctx, const kvr_plane *planes, uint32_t n_pl
 kvr_status kvr_recall_layer(kvr_context *ctx, const kvr_layer_recall *desc,
                             void *select_stream, void *copy_stream);
 
+/* n layers of recall in order, with results identical to n kvr_recall_layer
+ * calls.  When every layer takes the fused vector scoring path with one
+ * geometry, layer l's softmax and selection run inside layer l+1's summary
+ * launch (the context then keeps two logits buffers), so each layer's
+ * selection, select_end event and stage-in follow the next layer's launch;
+ * a layer's summary events bracket that shared launch.  Otherwise the layers
+ * run one after another.  Replaces the per-layer loop of the adapter's layer
+ * stack (score l+1 while l streams in, llama-memory-kvmem.cpp:5011-5126). */
+kvr_status kvr_recall_stack(kvr_context *ctx, const kvr_layer_recall *layers, uint32_t n,
+                            void *select_stream, void *copy_stream);
+
 /* ---- device copies ------------------------------------------------------- */
 
 /* One launch of n byte copies (16-byte path when aligned).  Replaces

@@ -244,6 +244,15 @@ class Context:
     def recall_layer(self, *, select_stream=None, copy_stream=None, **kw) -> None:
         self.recall(self.layer_recall(**kw), select_stream, copy_stream)
 
+    def recall_stack(self, descs: Sequence, select_stream=None, copy_stream=None):
+        """kvr_recall_stack over prebuilt descriptors (Context.layer_recall).
+        Returns the descriptor array, which the caller keeps until the work
+        has run."""
+        arr = (_capi.LayerRecall * len(descs))(*descs)
+        arr._keep = list(descs)
+        check(lib().kvr_recall_stack(self.handle, arr, len(descs), select_stream, copy_stream))
+        return arr
+
     def d2d_batched(self, srcs: Sequence[int], dsts: Sequence[int], sizes: Sequence[int], stream=None) -> None:
         n = len(srcs)
         s = (C.c_void_p * max(1, n))(*srcs)

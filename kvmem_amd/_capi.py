@@ -74,6 +74,7 @@ _SIGNATURES = {
     "kvr_select_topk": (_i, [_P, _P, _u32, _u32, _u32, C.POINTER(_u32), _u32, _i, _i, _P, _P, _P]),
     "kvr_stage_in": (_i, [_P, C.POINTER(Plane), _u32, _u32, _u32, _P, _P, _u32, _i, _P]),
     "kvr_recall_layer": (_i, [_P, C.POINTER(LayerRecall), _P, _P]),
+    "kvr_recall_stack": (_i, [_P, C.POINTER(LayerRecall), _u32, _P, _P]),
     "kvr_d2d_batched": (_i, [_P, C.POINTER(_P), C.POINTER(_P), C.POINTER(_sz), _u32, _P]),
     "kvr_host_alloc": (_i, [_sz, C.POINTER(_P)]),
     "kvr_host_free": (_i, [_P]),

@@ -268,13 +268,9 @@ kvr_status plan_score(kvr_context *ctx, const kvr_query *q, uint32_t lanes, uint
 }
 
 // logits -> softmax -> aggregation (+ selection).
-kvr_status enqueue_probs_and_select(kvr_context *ctx, const ScorePlan &p, const uint8_t *mask,
-                                    kvr_aggregation agg, uint32_t active_layers, int accumulate,
-                                    double *scores, bool do_select, uint32_t k, kvr_tie_rule tie,
-                                    const Mandatory &mand, uint32_t *selected, uint32_t *count,
-                                    hipStream_t s) {
-    if (p.lanes > 65535) return fail(KVR_ERR_INVALID, "at most 65535 lanes per call");
-    if (kvr_status st = ensure_counters(ctx, p.lanes, s)) return st;
+kvr::SelectArgs make_select_args(kvr_context *ctx, const ScorePlan &p, const uint8_t *mask, kvr_aggregation agg,
+                                 uint32_t active_layers, int accumulate, double *scores, bool do_select, uint32_t k,
+                                 kvr_tie_rule tie, const Mandatory &mand, uint32_t *selected, uint32_t *count) {
     kvr::SelectArgs sa{};
     sa.logits = p.logits;
     sa.mask = mask;
@@ -300,8 +296,36 @@ kvr_status enqueue_probs_and_select(kvr_context *ctx, const ScorePlan &p, const 
     sa.count = count;
     sa.status = ctx->status;
     sa.epoch = ctx->epoch;
+    return sa;
+}
+
+kvr_status enqueue_probs_and_select(kvr_context *ctx, const ScorePlan &p, const uint8_t *mask,
+                                    kvr_aggregation agg, uint32_t active_layers, int accumulate,
+                                    double *scores, bool do_select, uint32_t k, kvr_tie_rule tie,
+                                    const Mandatory &mand, uint32_t *selected, uint32_t *count,
+                                    hipStream_t s) {
+    if (p.lanes > 65535) return fail(KVR_ERR_INVALID, "at most 65535 lanes per call");
+    if (kvr_status st = ensure_counters(ctx, p.lanes, s)) return st;
+    const kvr::SelectArgs sa = make_select_args(ctx, p, mask, agg, active_layers, accumulate, scores, do_select, k,
+                                                tie, mand, selected, count);
     KVR_HIP(kvr::launch_probs(sa, s));
     return KVR_OK;
+}
+
+// Resident fp16 summaries as the source of the fused logits (no mean-K).
+kvr::SummaryArgs resident_args(kvr_context *ctx, const ScorePlan &p, const uint16_t *summaries) {
+    kvr::SummaryArgs a{};
+    a.src = reinterpret_cast<const uint8_t *>(summaries);
+    a.src_lane_stride = uint64_t(p.pages) * p.kvheads * p.dim * 2;
+    a.pages = p.pages;
+    a.width = p.kvheads * p.dim;
+    a.lanes = p.lanes;
+    a.q = p.q;
+    a.q_stage = stage_query(p.q);
+    a.logits = p.logits;
+    a.status = ctx->status;
+    a.epoch = ctx->epoch;
+    return a;
 }
 
 kvr_status enqueue_logits(kvr_context *ctx, const ScorePlan &p, const uint16_t *summaries,
@@ -327,18 +351,7 @@ kvr_status enqueue_logits(kvr_context *ctx, const ScorePlan &p, const uint16_t *
         ma.logits = p.logits;
         KVR_HIP(kvr::launch_logits_mfma(ma, s));
     } else {
-        kvr::SummaryArgs a{};
-        a.src = reinterpret_cast<const uint8_t *>(summaries);
-        a.src_lane_stride = uint64_t(p.pages) * p.kvheads * p.dim * 2;
-        a.pages = p.pages;
-        a.width = p.kvheads * p.dim;
-        a.lanes = p.lanes;
-        a.q = p.q;
-        a.q_stage = stage_query(p.q);
-        a.logits = p.logits;
-        a.status = ctx->status;
-        a.epoch = ctx->epoch;
-        KVR_HIP(kvr::launch_summary(kvr::kSrcSummary, true, a, s));
+        KVR_HIP(kvr::launch_summary(kvr::kSrcSummary, true, resident_args(ctx, p, summaries), s));
     }
     return KVR_OK;
 }
@@ -874,55 +887,83 @@ kvr_status kvr_stage_in(kvr_context *ctx, const kvr_plane *planes, uint32_t n_pl
     return enqueue_gather_kernel(ctx, pp, n_planes, lanes, page_tokens, selected, count, k, s);
 }
 
-kvr_status kvr_recall_layer(kvr_context *ctx, const kvr_layer_recall *d, void *select_stream, void *copy_stream) {
-    if (kvr_status s = check_ctx(ctx)) return s;
+namespace {
+
+// One validated layer of recall: everything checked, nothing enqueued.
+struct LayerPlan {
+    const kvr_layer_recall *d = nullptr;
+    uint32_t pages = 0, page_tokens = 0, lanes = 1;
+    size_t key_ls = 0;
+    Mandatory m;
+    PlanePlan pp[KVR_MAX_PLANES];
+    ScorePlan p;
+    int src = kvr::kSrcSummary;
+};
+
+kvr_status plan_layer(kvr_context *ctx, const kvr_layer_recall *d, hipStream_t ss, hipStream_t cs, LayerPlan &L) {
     if (!d || !d->query || !d->summaries || !d->scores || !d->selected || !d->count)
         return fail(KVR_ERR_INVALID, "recall descriptor lacks query, summaries, scores or selection outputs");
     if (d->aggregation > KVR_AGG_MAX_LOGIT) return fail(KVR_ERR_INVALID, "unknown aggregation");
     if (d->tie_rule > KVR_TIE_HIGHER_FIRST) return fail(KVR_ERR_INVALID, "unknown tie rule");
     if (d->engine > KVR_ENGINE_SDMA) return fail(KVR_ERR_INVALID, "unknown copy engine");
     if (!d->k) return fail(KVR_ERR_INVALID, "invalid scored selection frame (budget 0)");
-    uint32_t pages = d->pages, page_tokens = d->page_tokens, lanes = 1;
-    size_t key_ls = 0;
+    L.d = d;
+    L.pages = d->pages;
+    L.page_tokens = d->page_tokens;
     if (d->keys) {
-        if (kvr_status s = check_keys(d->keys, pages, key_ls)) return s;
-        page_tokens = d->keys->page_tokens;
-        lanes = d->keys->lanes ? d->keys->lanes : 1;
+        if (kvr_status s = check_keys(d->keys, L.pages, L.key_ls)) return s;
+        L.page_tokens = d->keys->page_tokens;
+        L.lanes = d->keys->lanes ? d->keys->lanes : 1;
+        L.src = d->keys->format == KVR_FMT_F16 ? kvr::kSrcKeysF16 : kvr::kSrcKeysQ8;
         if (d->keys->kv_heads != d->query->kv_heads || d->keys->head_dim != d->query->head_dim)
             return fail(KVR_ERR_INVALID, "key history and query disagree on kv heads or head_dim");
     } else {
-        if (!pages || !page_tokens) return fail(KVR_ERR_INVALID, "resident summaries need pages and page_tokens");
-        lanes = d->lanes ? d->lanes : 1;
+        if (!L.pages || !L.page_tokens) return fail(KVR_ERR_INVALID, "resident summaries need pages and page_tokens");
+        L.lanes = d->lanes ? d->lanes : 1;
     }
     if (kvr_status s = check_summary_out(d->means, d->summaries)) return s;
-    Mandatory m;
-    if (kvr_status s = check_mandatory(d->mandatory, d->n_mandatory, pages, d->k, m)) return s;
-    DeviceGuard guard(ctx->device);
-    PlanePlan pp[KVR_MAX_PLANES];
-    if (kvr_status s = check_planes(d->planes, d->n_planes, lanes, page_tokens, d->k, ctx->chunk_rows, pp)) return s;
-    const hipStream_t ss = stream_or(select_stream, ctx->sel);
-    const hipStream_t cs = stream_or(copy_stream, ctx->copy);
+    if (kvr_status s = check_mandatory(d->mandatory, d->n_mandatory, L.pages, d->k, L.m)) return s;
+    if (kvr_status s = check_planes(d->planes, d->n_planes, L.lanes, L.page_tokens, d->k, ctx->chunk_rows, L.pp))
+        return s;
     if ((d->summary_begin || d->summary_end || d->select_end) && capturing(ss))
         return fail(KVR_ERR_INVALID, "summary timing events are not recorded inside a captured graph");
     if (d->n_planes && d->engine == KVR_ENGINE_SDMA && (capturing(ss) || capturing(cs)))
         return fail(KVR_ERR_INVALID, "the DMA stage-in engine reads the selection on the host and cannot be "
                                      "captured; use the kernel engine inside graphs");
-    ScorePlan p;
-    if (kvr_status s = plan_score(ctx, d->query, lanes, pages, d->force_mfma, ss, p)) return s;
-    if (d->keys && !p.mfma && !valu_dim_ok(d->keys->head_dim))
+    if (kvr_status s = plan_score(ctx, d->query, L.lanes, L.pages, d->force_mfma, ss, L.p)) return s;
+    if (d->keys && !L.p.mfma && !valu_dim_ok(d->keys->head_dim))
         return fail(KVR_ERR_INVALID, "head_dim %u unsupported by fused scoring", d->keys->head_dim);
+    return KVR_OK;
+}
+
+// The layer's selection is written on ss: its timing event, then its
+// stage-in on cs after an event.
+kvr_status enqueue_stage(kvr_context *ctx, LayerPlan &L, hipStream_t ss, hipStream_t cs) {
+    const kvr_layer_recall *d = L.d;
+    if (d->select_end) KVR_HIP(hipEventRecord(static_cast<hipEvent_t>(d->select_end), ss));
+    if (!d->n_planes) return KVR_OK;
+    KVR_HIP(hipEventRecord(ctx->ev_sel, ss));
+    if (cs != ss) KVR_HIP(hipStreamWaitEvent(cs, ctx->ev_sel, 0));
+    if (d->engine == KVR_ENGINE_SDMA)
+        return enqueue_gather_sdma(ctx, L.pp, d->n_planes, L.lanes, L.page_tokens, d->selected, d->count, d->k, cs,
+                                   ctx->ev_sel);
+    return enqueue_gather_kernel(ctx, L.pp, d->n_planes, L.lanes, L.page_tokens, d->selected, d->count, d->k, cs);
+}
+
+kvr_status enqueue_layer(kvr_context *ctx, LayerPlan &L, hipStream_t ss, hipStream_t cs) {
+    const kvr_layer_recall *d = L.d;
+    ScorePlan &p = L.p;
     ++ctx->epoch;
     if (d->keys) {
-        auto a = summary_args(ctx, d->keys, pages, key_ls, d->means, d->summaries);
-        const int src = d->keys->format == KVR_FMT_F16 ? kvr::kSrcKeysF16 : kvr::kSrcKeysQ8;
+        auto a = summary_args(ctx, d->keys, L.pages, L.key_ls, d->means, d->summaries);
         if (d->summary_begin) KVR_HIP(hipEventRecord(static_cast<hipEvent_t>(d->summary_begin), ss));
         if (p.mfma) {
-            KVR_HIP(kvr::launch_summary(src, false, a, ss));
+            KVR_HIP(kvr::launch_summary(L.src, false, a, ss));
         } else {
             a.q = p.q;
             a.q_stage = stage_query(p.q);
             a.logits = p.logits;
-            KVR_HIP(kvr::launch_summary(src, true, a, ss));
+            KVR_HIP(kvr::launch_summary(L.src, true, a, ss));
         }
         if (d->summary_end) KVR_HIP(hipEventRecord(static_cast<hipEvent_t>(d->summary_end), ss));
         if (p.mfma)
@@ -931,16 +972,82 @@ kvr_status kvr_recall_layer(kvr_context *ctx, const kvr_layer_recall *d, void *s
         if (kvr_status st = enqueue_logits(ctx, p, d->summaries, ss)) return st;
     }
     if (kvr_status st = enqueue_probs_and_select(ctx, p, d->score_mask, d->aggregation, 1, 0, d->scores, true, d->k,
-                                                 d->tie_rule, m, d->selected, d->count, ss))
+                                                 d->tie_rule, L.m, d->selected, d->count, ss))
         return st;
-    if (d->select_end) KVR_HIP(hipEventRecord(static_cast<hipEvent_t>(d->select_end), ss));
-    if (!d->n_planes) return KVR_OK;
-    KVR_HIP(hipEventRecord(ctx->ev_sel, ss));
-    if (cs != ss) KVR_HIP(hipStreamWaitEvent(cs, ctx->ev_sel, 0));
-    if (d->engine == KVR_ENGINE_SDMA)
-        return enqueue_gather_sdma(ctx, pp, d->n_planes, lanes, page_tokens, d->selected, d->count, d->k, cs,
-                                   ctx->ev_sel);
-    return enqueue_gather_kernel(ctx, pp, d->n_planes, lanes, page_tokens, d->selected, d->count, d->k, cs);
+    return enqueue_stage(ctx, L, ss, cs);
+}
+
+}  // namespace
+
+kvr_status kvr_recall_layer(kvr_context *ctx, const kvr_layer_recall *d, void *select_stream, void *copy_stream) {
+    if (kvr_status s = check_ctx(ctx)) return s;
+    DeviceGuard guard(ctx->device);
+    const hipStream_t ss = stream_or(select_stream, ctx->sel);
+    const hipStream_t cs = stream_or(copy_stream, ctx->copy);
+    LayerPlan L;
+    if (kvr_status s = plan_layer(ctx, d, ss, cs, L)) return s;
+    return enqueue_layer(ctx, L, ss, cs);
+}
+
+kvr_status kvr_recall_stack(kvr_context *ctx, const kvr_layer_recall *layers, uint32_t n, void *select_stream,
+                            void *copy_stream) {
+    if (kvr_status s = check_ctx(ctx)) return s;
+    if (!n) return KVR_OK;
+    if (!layers) return fail(KVR_ERR_INVALID, "missing layer descriptors");
+    DeviceGuard guard(ctx->device);
+    const hipStream_t ss = stream_or(select_stream, ctx->sel);
+    const hipStream_t cs = stream_or(copy_stream, ctx->copy);
+    std::vector<LayerPlan> plans(n);
+    for (uint32_t l = 0; l < n; ++l)
+        if (kvr_status s = plan_layer(ctx, &layers[l], ss, cs, plans[l])) return s;
+    // Layer l's softmax/selection rides in layer l+1's summary launch when
+    // every layer takes the fused (vector) scoring path with one geometry.
+    const ScorePlan &p0 = plans[0].p;
+    bool fuse = n > 1;
+    for (const LayerPlan &L : plans)
+        fuse = fuse && !L.p.mfma && L.p.lanes == p0.lanes && L.p.pages == p0.pages && L.p.rows == p0.rows &&
+               L.p.qheads == p0.qheads && L.p.kvheads == p0.kvheads && L.p.dim == p0.dim;
+    if (!fuse) {
+        for (LayerPlan &L : plans)
+            if (kvr_status s = enqueue_layer(ctx, L, ss, cs)) return s;
+        return KVR_OK;
+    }
+    if (p0.lanes > 65535) return fail(KVR_ERR_INVALID, "at most 65535 lanes per call");
+    // two logits buffers and two counter sets, alternating between layers
+    const size_t lb = logits_bytes(p0.lanes, p0.pages, p0.rows, p0.qheads);
+    if (kvr_status s = ensure_workspace(ctx, 2 * lb, ss)) return s;
+    if (kvr_status s = ensure_counters(ctx, 2 * p0.lanes, ss)) return s;
+    double *logits[2] = {reinterpret_cast<double *>(ctx->ws), reinterpret_cast<double *>(ctx->ws + lb)};
+    kvr::SelectArgs prev{};
+    for (uint32_t l = 0; l <= n; ++l) {
+        kvr::SelectArgs cur{};
+        if (l < n) {
+            LayerPlan &L = plans[l];
+            const kvr_layer_recall *d = L.d;
+            ++ctx->epoch;
+            L.p.logits = logits[l & 1];
+            kvr::SummaryArgs a = d->keys ? summary_args(ctx, d->keys, L.pages, L.key_ls, d->means, d->summaries)
+                                         : resident_args(ctx, L.p, d->summaries);
+            a.q = L.p.q;
+            a.q_stage = stage_query(L.p.q);
+            a.logits = L.p.logits;
+            cur = make_select_args(ctx, L.p, d->score_mask, d->aggregation, 1, 0, d->scores, true, d->k, d->tie_rule,
+                                   L.m, d->selected, d->count);
+            cur.counters = ctx->counters + (l & 1) * p0.lanes;
+            if (d->summary_begin) KVR_HIP(hipEventRecord(static_cast<hipEvent_t>(d->summary_begin), ss));
+            if (l == 0)
+                KVR_HIP(kvr::launch_summary(L.src, true, a, ss));
+            else
+                KVR_HIP(kvr::launch_summary_probs(L.src, a, prev, ss));
+            if (d->summary_end) KVR_HIP(hipEventRecord(static_cast<hipEvent_t>(d->summary_end), ss));
+        } else {
+            KVR_HIP(kvr::launch_probs(prev, ss));
+        }
+        if (l > 0)
+            if (kvr_status s = enqueue_stage(ctx, plans[l - 1], ss, cs)) return s;
+        prev = cur;
+    }
+    return KVR_OK;
 }
 
 kvr_status kvr_d2d_batched(kvr_context *ctx, const void *const *src, void *const *dst, const size_t *nbytes,

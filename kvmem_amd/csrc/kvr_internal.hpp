@@ -143,6 +143,9 @@ hipError_t launch_logits_mfma(const MfmaLogitsArgs &a, hipStream_t s);
 hipError_t launch_probs(const SelectArgs &a, hipStream_t s);
 // selection over given scores, one workgroup per lane
 hipError_t launch_select(const SelectArgs &a, hipStream_t s);
+// one stack launch: `pa`'s softmax/selection beside `sa`'s summaries with
+// fused logits (sa.q and sa.logits set)
+hipError_t launch_summary_probs(int source, const SummaryArgs &sa, const SelectArgs &pa, hipStream_t s);
 hipError_t launch_gather(const GatherArgs &a, hipStream_t s);
 hipError_t launch_accumulate(const AccumulateArgs &a, hipStream_t s);
 hipError_t launch_finalize(const FinalizeArgs &a, hipStream_t s);

@@ -51,16 +51,18 @@ __device__ __forceinline__ void add_q8x8(float *acc, uint32_t lo, uint32_t hi, f
 // (kvmem/src/host/raw_kv_store.cpp:158-197, 606-625) and, when FUSE, the
 // logit loop of page_softmax_scores (kvmem/src/host/graph_recall.cpp:355-368).
 // ---------------------------------------------------------------------------
+// FUSE with q_stage: the workgroup's first lane's query rows, already
+// through the fp16 operand boundary, staged once in dynamic LDS.
+extern __shared__ __align__(16) uint16_t q_lds[];
+
+// One 256-thread block of the summary grid (`block` = its index in it).
 template <int SRC, bool FUSE>
-__global__ __launch_bounds__(256) void k_summary(SummaryArgs a) {
-    // FUSE with q_stage: the workgroup's first lane's query rows, already
-    // through the fp16 operand boundary, staged once in LDS.
-    extern __shared__ __align__(16) uint16_t q_lds[];
+__device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t block) {
     // Above the stage-in gather's waves when both share a CU: this kernel
     // is on the select critical path, the gather is bound by the host link.
     __builtin_amdgcn_s_setprio(2);
     const uint32_t gpp = a.width >> 3;  // 8-channel groups per page
-    const uint64_t gid = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    const uint64_t gid = uint64_t(block) * 256 + threadIdx.x;
     const uint64_t total = uint64_t(a.lanes) * a.pages * gpp;
     // Threads past the end still take part in the query-staging barrier.
     const bool active = gid < total;
@@ -199,7 +201,7 @@ __global__ __launch_bounds__(256) void k_summary(SummaryArgs a) {
         // workgroups still stream theirs, instead of delaying every first load.
         uint32_t staged_lane = 0xffffffffu;
         if (a.q_stage) {
-            staged_lane = uint32_t((uint64_t(blockIdx.x) * 256 / gpp) / a.pages);
+            staged_lane = uint32_t((uint64_t(block) * 256 / gpp) / a.pages);
             const uint32_t nq = q.rows * q.qheads * q.dim;
             uint32_t qbad = kOperandOk;
             for (uint32_t i = threadIdx.x; i < nq; i += 256) {
@@ -253,6 +255,11 @@ __global__ __launch_bounds__(256) void k_summary(SummaryArgs a) {
         }
         if (bad) raise_operand(a.status, bad, a.epoch);
     }
+}
+
+template <int SRC, bool FUSE>
+__global__ __launch_bounds__(256) void k_summary(SummaryArgs a) {
+    summary_block<SRC, FUSE>(a, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -790,10 +797,10 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
 // grid (ceil(units/4), lanes), 256 threads (a unit per wave); dynamic LDS:
 // the tail's keys.
 template <int NPL>
-__global__ __launch_bounds__(256) void k_probs(SelectArgs a) {
+__device__ __forceinline__ void probs_block(const SelectArgs &a, uint32_t unit_block, uint32_t lane,
+                                            uint32_t blocks_per_lane) {
     __shared__ uint32_t s_last;
-    const uint32_t lane = blockIdx.y;
-    const uint32_t unit = blockIdx.x * kUnitsPerBlock + (threadIdx.x >> 6);
+    const uint32_t unit = unit_block * kUnitsPerBlock + (threadIdx.x >> 6);
     double *lane_base = a.logits + uint64_t(lane) * a.rows * a.qheads * a.pages;
     if (unit < a.units) {
         if (NPL > 0)
@@ -808,13 +815,36 @@ __global__ __launch_bounds__(256) void k_probs(SelectArgs a) {
     __syncthreads();
     if (threadIdx.x == 0) {
         const uint32_t done = atomicAdd(a.counters + lane, 1u);
-        s_last = done == gridDim.x - 1;
+        s_last = done == blocks_per_lane - 1;
         if (s_last) atomicExch(a.counters + lane, 0u);
     }
     __syncthreads();
     if (!s_last) return;
     __threadfence();  // the other workgroups' terms are visible from here
     lane_tail(a, lane);
+}
+
+template <int NPL>
+__global__ __launch_bounds__(256) void k_probs(SelectArgs a) {
+    probs_block<NPL>(a, blockIdx.x, blockIdx.y, gridDim.x);
+}
+
+// One launch of a layer stack: this layer's summary blocks with fused
+// logits (blocks [0, summary_blocks), laid out as in k_summary), then the
+// previous layer's softmax units and selection (lane-major).  The two share
+// no memory: the logits buffers and counters alternate between consecutive
+// layers.
+template <int SRC, int NPL>
+__global__ __launch_bounds__(256) void k_summary_probs(SummaryArgs s, SelectArgs p, uint32_t summary_blocks) {
+    if (blockIdx.x >= summary_blocks) {
+        // default wave priority: below the summary's streaming waves on a
+        // shared CU; these have the whole summary launch to finish in
+        const uint32_t per_lane = (p.units + kUnitsPerBlock - 1) / kUnitsPerBlock;
+        const uint32_t b = blockIdx.x - summary_blocks;
+        probs_block<NPL>(p, b % per_lane, b / per_lane, per_lane);
+        return;
+    }
+    summary_block<SRC, true>(s, blockIdx.x);
 }
 
 // Selection over given scores (no softmax), one workgroup per lane.
@@ -1097,6 +1127,34 @@ hipError_t launch_probs(const SelectArgs &a, hipStream_t s) {
     else if (a.pages <= 512) hipLaunchKernelGGL(k_probs<8>, grid, block, lds, s, a);
     else if (a.pages <= 1024) hipLaunchKernelGGL(k_probs<16>, grid, block, lds, s, a);
     else hipLaunchKernelGGL(k_probs<0>, grid, block, lds, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_summary_probs(int source, const SummaryArgs &sa, const SelectArgs &pa, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch\'s error
+    const uint32_t per_lane = (pa.units + kUnitsPerBlock - 1) / kUnitsPerBlock;
+    const uint32_t probs_blocks = per_lane * pa.lanes;
+    const uint64_t threads = uint64_t(sa.lanes) * sa.pages * (sa.width >> 3);
+    const uint32_t summary_blocks = blocks_for(threads);
+    const dim3 grid(unsigned(summary_blocks + probs_blocks)), block(256);
+    const size_t q_lds_bytes = sa.q_stage ? size_t(sa.q.rows) * sa.q.qheads * sa.q.dim * 2 : 0;
+    const size_t keys = pa.pages <= kTailLdsPages ? size_t(pa.pages) * 8 : 0;
+    const size_t lds = q_lds_bytes > keys ? q_lds_bytes : keys;
+    auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, lds, s, sa, pa, summary_blocks); };
+    const bool f16 = source == kSrcKeysF16, q8 = source == kSrcKeysQ8;
+    if (pa.pages <= 256) {
+        if (f16) go(k_summary_probs<kSrcKeysF16, 4>); else if (q8) go(k_summary_probs<kSrcKeysQ8, 4>);
+        else go(k_summary_probs<kSrcSummary, 4>);
+    } else if (pa.pages <= 512) {
+        if (f16) go(k_summary_probs<kSrcKeysF16, 8>); else if (q8) go(k_summary_probs<kSrcKeysQ8, 8>);
+        else go(k_summary_probs<kSrcSummary, 8>);
+    } else if (pa.pages <= 1024) {
+        if (f16) go(k_summary_probs<kSrcKeysF16, 16>); else if (q8) go(k_summary_probs<kSrcKeysQ8, 16>);
+        else go(k_summary_probs<kSrcSummary, 16>);
+    } else {
+        if (f16) go(k_summary_probs<kSrcKeysF16, 0>); else if (q8) go(k_summary_probs<kSrcKeysQ8, 0>);
+        else go(k_summary_probs<kSrcSummary, 0>);
+    }
     return hipGetLastError();
 }
 
