@@ -294,7 +294,7 @@ def run(args):
             "query_rows": R, "page_tokens": PT, "pages": P, "top_k": KSEL,
             "aggregation": "mean", "gather": "fp16 K+V copy into 8192-token slots",
             "engine": args.engine, "pinned_layers": ring,
-            "gather_workgroups": args.gather_wgs or 8, "gather_chunk_rows": args.chunk_rows or 8,
+            "gather_workgroups": args.gather_wgs or "16 x 64 threads (copy default)", "gather_chunk_rows": args.chunk_rows or 8,
         },
         "select_us_per_layer": round(select_us, 2),
         "select_stack_us_per_layer": round(ms_per_step / L * 1e3, 2),
@@ -368,6 +368,205 @@ def pmc_pass(args):
                       "copy_bytes": T * W * 2, "copy_ops": n}), flush=True)
 
 
+# ---------------------------------------------------------------------------
+# The other workloads (--workload).  Each prints one JSON line of the same
+# shape: value = scored-KV GB/s of the select stack, plus the per-layer
+# select latency, select+stage-in pipelined latency and stage-in GB/s.
+WORKLOADS = {
+    # one 32768-token layer, K = N(0,1) x per-channel U(0.5, 2), Max, top-16
+    "single32k": dict(layers=1, repeat=64, lanes=1, T=32768, HQ=32, HKV=8, D=128, PT=256, R=1, K=16,
+                      agg="max", kfmt="f16_scaled", vfmt="f16", kmode="copy", vmode="copy", resident=False),
+    # q8_0 K (scores from dequantized K) + q4_1-layout V, dequantized on gather
+    "k8v4": dict(layers=16, repeat=1, lanes=1, T=131072, HQ=32, HKV=8, D=128, PT=256, R=1, K=32,
+                 agg="mean", kfmt="q8_0", vfmt="q4_1", kmode="dequant", vmode="dequant", resident=False),
+    # 8 lanes x 262144 tokens, 40/8 heads, 4 query rows (matrix-core logits), top-64 per lane
+    "lanes8": dict(layers=1, repeat=8, lanes=8, T=262144, HQ=40, HKV=8, D=128, PT=256, R=4, K=64,
+                   agg="mean", kfmt="f16", vfmt="f16", kmode="copy", vmode="copy", resident=False),
+    # 40 layers x 1048576 tokens, 16/2 heads, D 256, q8_0 K + fp16 V, resident
+    # summaries, top-48 (pinned history aliased over a ring of 4 layers)
+    "layerwise40": dict(layers=40, repeat=1, lanes=1, T=1048576, HQ=16, HKV=2, D=256, PT=256, R=1, K=48,
+                        agg="mean", kfmt="q8_0", vfmt="f16", kmode="dequant", vmode="copy", resident=True,
+                        ring=4),
+}
+
+
+def run_workload(args):
+    import torch
+    import kvmem_amd as K
+    from kvmem_amd.hip import runtime
+
+    w = WORKLOADS[args.workload]
+    hip = runtime()
+    ctx = K.Context(0)
+    ctx.set_option(K._capi.OPT_GATHER_WORKGROUPS, args.gather_wgs)
+    ctx.set_option(K._capi.OPT_GATHER_CHUNK_ROWS, args.chunk_rows)
+    ctx.set_option(K._capi.OPT_GATHER_THREADS, args.gather_threads)
+    L, NL, T, HQ, HKV, D, PT, R, KSEL = w["layers"], w["lanes"], w["T"], w["HQ"], w["HKV"], w["D"], w["PT"], \
+        w["R"], w["K"]
+    W, P = HKV * D, T // PT
+    ring = w.get("ring", L)
+    fmt = {"f16": K.FMT_F16, "f16_scaled": K.FMT_F16, "q8_0": K.FMT_Q8_0, "q4_1": K.FMT_Q4_1}
+    row = lambda f: K.row_bytes(fmt[f], W)
+    kfmt, vfmt = fmt[w["kfmt"]], fmt[w["vfmt"]]
+    mode = {"copy": K.GATHER_COPY, "dequant": K.GATHER_DEQUANT_F16}
+    agg = {"mean": K.AGG_MEAN, "max": K.AGG_MAX}[w["agg"]]
+    seed = args.seed
+    log(f"workload {args.workload}: {L} layer(s) x {NL} lane(s) x {T} tokens, Hq {HQ}/Hkv {HKV}, D {D}, "
+        f"page {PT} ({P} pages), {R} query row(s), top-{KSEL}, K {w['kfmt']}, V {w['vfmt']}")
+
+    def synth(f, sid, nrows, out):
+        n = nrows * W
+        if f == "f16":
+            ctx.synth_normal_f16(seed, sid, n, out)
+        elif f == "f16_scaled":
+            # per-(kv-head, dim) channel scale U(0.5, 2)
+            scale = torch.from_numpy(np.random.default_rng(seed + sid).uniform(0.5, 2.0, W).astype(np.float32))
+            scale = scale.cuda()
+            torch.cuda.synchronize()
+            ctx.synth_scaled_normal_f16(seed, sid, nrows, W, scale, out)
+        elif f == "q8_0":
+            if w["resident"]:
+                ctx.synth_normal_q8_0(seed, sid, n // 32, out)
+            else:
+                ctx.synth_q8_0(seed, sid, n // 32, 0.01, 0.05, out)
+        elif f == "q4_1":
+            ctx.synth_q4_1(seed, sid, n // 32, 0.01, 0.05, -0.4, 0.0, out)
+        ctx.check()
+
+    lane_rows = NL * T
+    kb, vb = lane_rows * row(w["kfmt"]), lane_rows * row(w["vfmt"])
+    pins, s16, dev_k = [], [], []
+    tmp = torch.empty(max(kb, vb), dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    for r in range(ring):
+        pk, pv = K.PinnedBuffer(kb), K.PinnedBuffer(vb)
+        synth(w["kfmt"], 1000 + r, lane_rows, tmp)
+        hip.d2h(pk.ptr, tmp.data_ptr(), kb)
+        if w["resident"]:
+            srow = torch.empty(NL * P * W, dtype=torch.int16, device="cuda")
+            torch.cuda.synchronize()
+            ctx.summary_build(K.make_keys(tmp, kfmt, T, HKV, D, PT, lanes=NL), None, srow)
+            ctx.check()
+            s16.append(srow)
+        synth(w["vfmt"], 2000 + r, lane_rows, tmp)
+        hip.d2h(pv.ptr, tmp.data_ptr(), vb)
+        pins.append((pk, pv))
+    del tmp
+    if not w["resident"]:
+        for l in range(L):
+            t = torch.empty(kb, dtype=torch.uint8, device="cuda")
+            torch.cuda.synchronize()
+            synth(w["kfmt"], 1000 + l % ring, lane_rows, t)
+            dev_k.append(t)
+    else:
+        s16 = [s16[l % ring].clone() for l in range(L)]
+    qd = []
+    for l in range(L):
+        q = torch.empty(NL * R * HQ * D, dtype=torch.int16, device="cuda")
+        torch.cuda.synchronize()
+        ctx.synth_normal_f16(seed, 3000 + l, q.numel(), q)
+        qd.append(q)
+    if not w["resident"]:
+        s16 = [torch.empty(NL * P * W, dtype=torch.int16, device="cuda") for _ in range(L)]
+    scores = [torch.empty(NL * P, dtype=torch.float64, device="cuda") for _ in range(L)]
+    sel = [torch.empty(NL * KSEL, dtype=torch.int32, device="cuda") for _ in range(L)]
+    cnt = [torch.empty(NL, dtype=torch.int32, device="cuda") for _ in range(L)]
+    kslots = [torch.empty(NL * KSEL * PT * K.gather_row_bytes(kfmt, mode[w["kmode"]], W), dtype=torch.uint8,
+                          device="cuda") for _ in range(L)]
+    vslots = [torch.empty(NL * KSEL * PT * K.gather_row_bytes(vfmt, mode[w["vmode"]], W), dtype=torch.uint8,
+                          device="cuda") for _ in range(L)]
+    torch.cuda.synchronize()
+    ctx.check()
+    log(f"inputs ready ({ring} pinned K/V set(s) of {kb >> 20} + {vb >> 20} MiB)")
+
+    def desc(l, with_planes, ev=(None, None), se=None):
+        planes = [K.make_plane(pins[l % ring][0], kfmt, W, T, mode[w["kmode"]], kslots[l]),
+                  K.make_plane(pins[l % ring][1], vfmt, W, T, mode[w["vmode"]], vslots[l])]
+        src = dict(keys=None, pages=P, page_tokens=PT, lanes=NL) if w["resident"] else \
+            dict(keys=K.make_keys(dev_k[l], kfmt, T, HKV, D, PT, lanes=NL))
+        return K.Context.layer_recall(summaries=s16[l], query=K.make_query(qd[l], K.FMT_F16, R, HQ, HKV, D, lanes=NL),
+                                      scores=scores[l], selected=sel[l], count=cnt[l], k=KSEL, aggregation=agg,
+                                      planes=planes if with_planes else (), summary_events=ev, select_end=se,
+                                      **src)
+
+    # (a) select latency of one layer: summary start -> selection written
+    ev_a, ev_b = hip.event(), hip.event()
+    lat = []
+    for rep in range(max(3, args.steps)):
+        for l in range(min(L, 4)):
+            ctx.recall(desc(l, False, (ev_a, None), ev_b))
+            ctx.check()
+            if rep:
+                lat.append(hip.elapsed_ms(ev_a, ev_b) * 1e3)
+    select_us = float(np.median(lat))
+    # (b) timed: the select stack (each layer `repeat` times)
+    order = [l for l in range(L) for _ in range(w["repeat"])]
+    descs = [desc(l, False) for l in order]
+    for _ in range(args.warmup):
+        keep = ctx.recall_stack(descs)
+        ctx.check()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        keep = ctx.recall_stack(descs)
+    ctx.check()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    del keep
+    k_read = 0 if w["resident"] else lane_rows * row(w["kfmt"])
+    scored_layer = k_read + NL * P * W * 2 + NL * R * HQ * D * 2
+    value = len(order) * scored_layer / (ms_per_step * 1e-3) / 1e9
+    log(f"select {select_us:.1f} us/layer; stack {ms_per_step * 1e3 / len(order):.1f} us/layer = {value:.1f} GB/s")
+    # (c) select + stage-in pipelined over the layers
+    pdescs = [desc(l, True) for l in range(L)]
+    for rep in range(2):
+        ctx.check()
+        p0 = time.perf_counter()
+        keep = ctx.recall_stack(pdescs, None, ctx.copy_stream)
+        ctx.check()
+        pipe_us = (time.perf_counter() - p0) * 1e6 / L
+    del keep
+    # (d) stage-in alone
+    stage = []
+    for rep in range(2):
+        for l in range(L):
+            planes = [K.make_plane(pins[l % ring][0], kfmt, W, T, mode[w["kmode"]], kslots[l]),
+                      K.make_plane(pins[l % ring][1], vfmt, W, T, mode[w["vmode"]], vslots[l])]
+            hip.record(ev_a, ctx.copy_stream)
+            ctx.stage_in(planes, PT, sel[l], cnt[l], KSEL, lanes=NL)
+            hip.record(ev_b, ctx.copy_stream)
+            ctx.check()
+            if rep:
+                stage.append(hip.elapsed_ms(ev_a, ev_b) * 1e3)
+    stage_us = float(np.mean(stage))
+    stage_bytes = NL * KSEL * PT * (row(w["kfmt"]) + row(w["vfmt"]))
+    h2d = ctx.h2d_peak_gbps(1 << 30, 5)
+    stage_gbps = stage_bytes / (stage_us * 1e-6) / 1e9
+    log(f"pipelined {pipe_us:.1f} us/layer; stage-in {stage_us:.1f} us/layer = {stage_gbps:.2f} GB/s "
+        f"(H2D peak {h2d:.2f})")
+    line = {
+        "metric": "select+stage-in latency/layer at 128K ctx; scored-KV GB/s vs HBM peak",
+        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16/q8_0/q4_1 operands, f32 summaries, f64 scores",
+        "data": f"synthetic seeded (device generator), seed {seed}",
+        "config": {"workload": args.workload, **{k: v for k, v in w.items()}, "stack_layers": len(order)},
+        "select_us_per_layer": round(select_us, 2),
+        "select_stack_us_per_layer": round(ms_per_step * 1e3 / len(order), 2),
+        "scored_frac_hbm": round(value / HBM_PEAK_GBPS, 4),
+        "latency_us_per_layer": round(pipe_us, 2),
+        "stagein_us_per_layer": round(stage_us, 2),
+        "stagein_bytes_per_layer": stage_bytes,
+        "stagein_GBps": round(stage_gbps, 3), "h2d_peak_GBps": round(h2d, 3),
+        "stagein_frac_h2d": round(stage_gbps / h2d, 4),
+    }
+    for pk, pv in pins:
+        pk.free()
+        pv.free()
+    ctx.close()
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -381,6 +580,9 @@ def main():
     ap.add_argument("--gather-threads", type=int, default=0, help="gather workgroup size (0 = default)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--workload", choices=["resident64", *WORKLOADS], default="resident64",
+                    help="resident64 (default): the 64-layer 128K stack; the others are the remaining "
+                         "workloads, each measured the same way")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="only the short counter pass (one layer's selects + calibration copies)")
     args = ap.parse_args()
@@ -392,6 +594,9 @@ def main():
         sys.exit(2)
     if args.pmc_pass:
         pmc_pass(args)
+        return
+    if args.workload != "resident64":
+        run_workload(args)
         return
     run(args)
 

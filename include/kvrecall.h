@@ -156,8 +156,10 @@ typedef struct kvr_layer_recall {
     kvr_copy_engine engine;
     int force_mfma;                /* -1 never, 0 by rows*group >= 16, 1 always */
     void *summary_begin;           /* optional hipEvent_t recorded on the select
-                                      stream just before / after the summary */
-    void *summary_end;             /* kernel (measurement only; may be NULL;
+                                      stream just before / after the summary
+                                      kernel (with resident summaries: the
+                                      logits kernel) */
+    void *summary_end;             /* (measurement only; may be NULL;
                                       refused while the stream is captured)  */
     void *select_end;              /* optional hipEvent_t recorded on the select
                                       stream once the selection is written,
@@ -187,9 +189,11 @@ void *kvr_select_stream(kvr_context *ctx);
 void *kvr_copy_stream(kvr_context *ctx);
 
 typedef enum kvr_option {
-    KVR_OPT_GATHER_WORKGROUPS = 1, /* grid bound of the device-driven gather (default 8) */
+    KVR_OPT_GATHER_WORKGROUPS = 1, /* grid bound of the device-driven gather (default: 16
+                                      for copies, 32 when a plane decodes) */
     KVR_OPT_GATHER_CHUNK_ROWS = 2, /* token rows per gather work item (default 8, <= 64) */
-    KVR_OPT_GATHER_THREADS = 3     /* gather workgroup size: 64, 128 or 256 (default 256) */
+    KVR_OPT_GATHER_THREADS = 3     /* gather workgroup size: 64, 128 or 256 (default: 64
+                                      for copies, 256 when a plane decodes) */
 } kvr_option;
 
 /* Tuning knobs of a context; value 0 restores the default.  No reference

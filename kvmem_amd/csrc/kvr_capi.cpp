@@ -43,9 +43,9 @@ struct kvr_context {
     uint8_t *staging = nullptr;
     size_t staging_bytes = 0;
     // tuning
-    uint32_t gather_wgs = 8;
+    uint32_t gather_wgs = 0;  // 0: by mode (kDefaultGatherWgs / kDefaultDecodeGatherWgs)
     uint32_t chunk_rows = 8;
-    uint32_t gather_threads = 256;
+    uint32_t gather_threads = 0;  // 0: by mode
 };
 
 namespace {
@@ -430,7 +430,7 @@ kvr_status check_planes(const kvr_plane *planes, uint32_t n, uint32_t lanes, uin
         if (p.mode == KVR_GATHER_DEQUANT_F16 && p.format != KVR_FMT_F16 && (p.width % 32 || !aligned(p.slots, 16)))
             return fail(KVR_ERR_INVALID, "plane %u: dequantized slots must be 16-byte aligned", i);
         (void)chunk_rows;
-        if (p.format != KVR_FMT_F16 && p.mode != KVR_GATHER_COPY && 2 * srow > kGatherLds)
+        if (p.format != KVR_FMT_F16 && p.mode != KVR_GATHER_COPY && 4 * (srow + 16) > kGatherLds)
             return fail(KVR_ERR_INVALID, "plane %u: rows too wide for the staged decoder", i);
         hipPointerAttribute_t attr{};
         if (hipPointerGetAttributes(&attr, p.history) != hipSuccess || attr.type != hipMemoryTypeHost ||
@@ -460,15 +460,24 @@ kvr_status check_planes(const kvr_plane *planes, uint32_t n, uint32_t lanes, uin
     return KVR_OK;
 }
 
-constexpr uint32_t kDefaultGatherWgs = 8, kDefaultChunkRows = 8;
+// Copies fill the host link with one wave on each of 16 CUs (so they take
+// little from the summary kernel beside them); decoding planes need more
+// waves to hide their ALU work behind the link.
+constexpr uint32_t kDefaultGatherWgs = 16, kDefaultGatherThreads = 64;               // copies
+constexpr uint32_t kDefaultDecodeGatherWgs = 32, kDefaultDecodeGatherThreads = 256;  // decoding planes
+constexpr uint32_t kDefaultChunkRows = 8;
 
 // Rows per gather work item: the context's setting, bounded by the page and
 // by the LDS a staged decode needs (source rows + requantized rows).
-uint32_t gather_chunk_rows(const kvr_context *ctx, const PlanePlan *pp, uint32_t n, uint32_t page_tokens) {
-    uint32_t cr = std::min(ctx->chunk_rows, page_tokens);
+// Rows per gather item: the option, bounded so that every wave's LDS slice
+// of a decoding plane fits the workgroup's LDS.
+uint32_t gather_chunk_rows(uint32_t chunk_rows, uint32_t threads, const PlanePlan *pp, uint32_t n,
+                           uint32_t page_tokens) {
+    uint32_t cr = std::min(chunk_rows, page_tokens);
+    const size_t waves = threads / 64;
     for (uint32_t i = 0; i < n; ++i)
         if (pp[i].g.mode != KVR_GATHER_COPY && pp[i].g.format != KVR_FMT_F16)
-            cr = std::min<uint32_t>(cr, uint32_t(kGatherLds / (2 * size_t(pp[i].g.src_row))));
+            cr = std::min<uint32_t>(cr, uint32_t(kGatherLds / (waves * (size_t(pp[i].g.src_row) + 16))));
     return std::max<uint32_t>(cr, 1);
 }
 
@@ -482,12 +491,16 @@ kvr_status enqueue_gather_kernel(kvr_context *ctx, const PlanePlan *pp, uint32_t
     ga.lanes = lanes;
     ga.k = k;
     ga.page_tokens = page_tokens;
-    ga.chunk_rows = gather_chunk_rows(ctx, pp, n, page_tokens);
+    ga.chunk_rows = gather_chunk_rows(ctx->chunk_rows, 256, pp, n, page_tokens);
     ga.chunks = (page_tokens + ga.chunk_rows - 1) / ga.chunk_rows;
     ga.selected = selected;
     ga.count = count;
-    ga.workgroups = ctx->gather_wgs;
-    ga.threads = ctx->gather_threads;
+    bool decode = false;
+    for (uint32_t i = 0; i < n; ++i)
+        decode = decode || (pp[i].g.mode != KVR_GATHER_COPY && pp[i].g.format != KVR_FMT_F16);
+    ga.workgroups = ctx->gather_wgs ? ctx->gather_wgs : decode ? kDefaultDecodeGatherWgs : kDefaultGatherWgs;
+    ga.threads = ctx->gather_threads ? ctx->gather_threads : decode ? kDefaultDecodeGatherThreads
+                                                                     : kDefaultGatherThreads;
     KVR_HIP(kvr::launch_gather(ga, s));
     return KVR_OK;
 }
@@ -580,7 +593,7 @@ kvr_status enqueue_gather_sdma(kvr_context *ctx, PlanePlan *pp, uint32_t n, uint
         ga.lanes = lanes;
         ga.k = k;
         ga.page_tokens = page_tokens;
-        ga.chunk_rows = gather_chunk_rows(ctx, &p, 1, page_tokens);
+        ga.chunk_rows = gather_chunk_rows(ctx->chunk_rows, 256, &p, 1, page_tokens);
         ga.chunks = (page_tokens + ga.chunk_rows - 1) / ga.chunk_rows;
         ga.workgroups = 1024;  // HBM -> HBM: use the whole GPU
         ga.threads = 256;
@@ -683,7 +696,7 @@ kvr_status kvr_set_option(kvr_context *ctx, kvr_option option, int64_t value) {
     switch (option) {
     case KVR_OPT_GATHER_WORKGROUPS:
         if (value < 0 || value > 65536) return fail(KVR_ERR_INVALID, "gather workgroups must be in [0, 65536]");
-        ctx->gather_wgs = value ? uint32_t(value) : kDefaultGatherWgs;
+        ctx->gather_wgs = uint32_t(value);
         return KVR_OK;
     case KVR_OPT_GATHER_CHUNK_ROWS:
         if (value < 0 || value > 64) return fail(KVR_ERR_INVALID, "gather chunk rows must be in [0, 64]");
@@ -692,7 +705,7 @@ kvr_status kvr_set_option(kvr_context *ctx, kvr_option option, int64_t value) {
     case KVR_OPT_GATHER_THREADS:
         if (value != 0 && value != 64 && value != 128 && value != 256)
             return fail(KVR_ERR_INVALID, "gather workgroup size must be 64, 128 or 256");
-        ctx->gather_threads = value ? uint32_t(value) : 256;
+        ctx->gather_threads = uint32_t(value);
         return KVR_OK;
     }
     return fail(KVR_ERR_INVALID, "unknown option %d", int(option));
@@ -969,7 +982,10 @@ kvr_status enqueue_layer(kvr_context *ctx, LayerPlan &L, hipStream_t ss, hipStre
         if (p.mfma)
             if (kvr_status st = enqueue_logits(ctx, p, d->summaries, ss)) return st;
     } else {
+        // resident summaries: the events bracket the logits launch
+        if (d->summary_begin) KVR_HIP(hipEventRecord(static_cast<hipEvent_t>(d->summary_begin), ss));
         if (kvr_status st = enqueue_logits(ctx, p, d->summaries, ss)) return st;
+        if (d->summary_end) KVR_HIP(hipEventRecord(static_cast<hipEvent_t>(d->summary_end), ss));
     }
     if (kvr_status st = enqueue_probs_and_select(ctx, p, d->score_mask, d->aggregation, 1, 0, d->scores, true, d->k,
                                                  d->tie_rule, L.m, d->selected, d->count, ss))

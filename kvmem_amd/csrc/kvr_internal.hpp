@@ -105,6 +105,7 @@ struct GatherArgs {
     uint64_t src_page_stride;   // 0: read pinned history; else staged page i at i*stride
     uint32_t workgroups;        // grid bound of the persistent gather
     uint32_t threads;           // workgroup size (64, 128 or 256)
+    uint32_t lds_per_wave;      // staging bytes per wave (set by the launcher)
 };
 
 struct AccumulateArgs {

@@ -915,11 +915,53 @@ __device__ __forceinline__ void quant_block_q8(const float *x, uint8_t *blk) {
 // Persistent: a bounded grid loops over (lane, slot, plane, chunk) items, so
 // waves parked on host-link latency occupy a few CUs instead of all of them
 // while the select stream's HBM-bound kernels run beside the gather.
+// Dynamic LDS of the gather: one staging slice per wave.
+extern __shared__ __align__(16) uint8_t gather_lds[];
+
+// One wave copies `bytes` from src to dst: 16-byte lanes with up to 16
+// loads (16 KiB per wave) in flight before the stores when both ends and
+// the size are 16-byte aligned.
+__device__ __forceinline__ void wave_copy(const uint8_t *src, uint8_t *dst, uint32_t bytes) {
+    const uint32_t l = threadIdx.x & 63;
+    if (((uintptr_t(src) | uintptr_t(dst) | bytes) & 15u) == 0) {
+        const u32x4 *s = reinterpret_cast<const u32x4 *>(src);
+        u32x4 *d = reinterpret_cast<u32x4 *>(dst);
+        const uint32_t n = bytes >> 4;
+        constexpr uint32_t B = 16;
+        // Every load of a batch is issued before its stores; lanes past the
+        // end of the last, partial batch re-read the final vector (clamped,
+        // so no load is predicated and none waits for another).
+        for (uint32_t base = 0; base < n; base += B * kWave) {
+            u32x4 v[B];
+#pragma unroll
+            for (uint32_t u = 0; u < B; ++u) v[u] = __builtin_nontemporal_load(s + min(base + u * kWave + l, n - 1));
+#pragma unroll
+            for (uint32_t u = 0; u < B; ++u) {
+                const uint32_t i = base + u * kWave + l;
+                if (i < n) d[i] = v[u];
+            }
+        }
+    } else if (((uintptr_t(src) | uintptr_t(dst) | bytes) & 3u) == 0) {
+        const uint32_t *s = reinterpret_cast<const uint32_t *>(src);
+        uint32_t *d = reinterpret_cast<uint32_t *>(dst);
+        for (uint32_t i = l; i < bytes >> 2; i += kWave) d[i] = s[i];
+    } else {
+        for (uint32_t i = l; i < bytes; i += kWave) dst[i] = src[i];
+    }
+}
+
+// Persistent gather, one work item per wave at a time: (lane, slot, plane,
+// chunk of chunk_rows rows).  Copies go straight from the source rows to the
+// slot rows; decoding modes stage the packed rows in the wave's LDS slice
+// (no workgroup barrier), decode whole blocks from there and write fp16
+// rows, or requantize in place and copy the slice out.
 __global__ __launch_bounds__(256) void k_gather(GatherArgs a) {
-    extern __shared__ __align__(16) uint8_t lds[];
+    const uint32_t wave = threadIdx.x >> 6, l = threadIdx.x & 63, wpb = blockDim.x >> 6;
+    uint8_t *wl = gather_lds + wave * a.lds_per_wave;
     const uint32_t per_lane = a.k * a.n_planes * a.chunks;
     const uint64_t total = uint64_t(a.lanes) * per_lane;
-    for (uint64_t it = blockIdx.x; it < total; it += gridDim.x) {
+    const uint64_t step = uint64_t(gridDim.x) * wpb;
+    for (uint64_t it = uint64_t(blockIdx.x) * wpb + wave; it < total; it += step) {
         const uint32_t lane = uint32_t(it / per_lane);
         uint32_t id = uint32_t(it % per_lane);
         const uint32_t chunk = id % a.chunks;
@@ -944,19 +986,18 @@ __global__ __launch_bounds__(256) void k_gather(GatherArgs a) {
         uint8_t *dst = P.dst + lane * P.dst_lane_stride + (uint64_t(slot) * a.page_tokens + r0) * P.dst_row;
         const uint32_t sbytes = nr * P.src_row;
         if (P.mode == kModeCopy || P.format == kFmtF16) {
-            copy_span(src, dst, sbytes);
+            wave_copy(src, dst, sbytes);
             continue;
         }
-        // Stage the packed rows in LDS, then decode whole blocks.
-        copy_span(src, lds, sbytes);
-        __syncthreads();
+        wave_copy(src, wl, sbytes);
+        wave_lds_sync();
         const uint32_t bpr = P.width / kQK;
         const uint32_t bbytes = P.format == kFmtQ8 ? kQ8Bytes : kQ41Bytes;
         const uint32_t nblocks = nr * bpr;
         if (P.mode == kModeDequantF16) {
-            for (uint32_t b = threadIdx.x; b < nblocks; b += blockDim.x) {
+            for (uint32_t b = l; b < nblocks; b += kWave) {
                 float y[kQK];
-                decode_block(lds + b * bbytes, P.format, y);
+                decode_block(wl + b * bbytes, P.format, y);
                 u32x4 *o = reinterpret_cast<u32x4 *>(dst + uint64_t(b / bpr) * P.dst_row + (b % bpr) * 64);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -968,16 +1009,16 @@ __global__ __launch_bounds__(256) void k_gather(GatherArgs a) {
                 }
             }
         } else {
-            uint8_t *out = lds + ((sbytes + 15u) & ~15u);
-            for (uint32_t b = threadIdx.x; b < nblocks; b += blockDim.x) {
+            // each lane requantizes its own blocks in place, then the slice goes out
+            for (uint32_t b = l; b < nblocks; b += kWave) {
                 float y[kQK];
-                decode_block(lds + b * kQ8Bytes, kFmtQ8, y);
-                quant_block_q8(y, out + b * kQ8Bytes);
+                decode_block(wl + b * kQ8Bytes, kFmtQ8, y);
+                quant_block_q8(y, wl + b * kQ8Bytes);
             }
-            __syncthreads();
-            copy_span(out, dst, sbytes);
+            wave_lds_sync();
+            wave_copy(wl, dst, sbytes);
         }
-        __syncthreads();  // LDS is reused by the next item
+        wave_lds_sync();  // the slice is refilled by the next item
     }
 }
 
@@ -1167,17 +1208,19 @@ hipError_t launch_select(const SelectArgs &a, hipStream_t s) {
 
 hipError_t launch_gather(const GatherArgs &a, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch\'s error
-    uint32_t lds = 0;
+    GatherArgs g = a;
+    g.lds_per_wave = 0;
     for (uint32_t i = 0; i < a.n_planes; ++i) {
         const GatherPlane &p = a.plane[i];
         if (p.mode == kModeCopy || p.format == kFmtF16) continue;
-        uint32_t need = ((a.chunk_rows * p.src_row + 15u) & ~15u);
-        if (p.mode == kModeRequantQ8) need += a.chunk_rows * p.src_row;
-        lds = need > lds ? need : lds;
+        const uint32_t need = (a.chunk_rows * p.src_row + 15u) & ~15u;
+        g.lds_per_wave = need > g.lds_per_wave ? need : g.lds_per_wave;
     }
+    const uint32_t wpb = a.threads / kWave;
     const uint64_t items = uint64_t(a.lanes) * a.k * a.n_planes * a.chunks;
-    const uint32_t wgs = unsigned(items < a.workgroups ? items : a.workgroups);
-    hipLaunchKernelGGL(k_gather, dim3(wgs ? wgs : 1), dim3(a.threads), lds, s, a);
+    const uint64_t blocks = (items + wpb - 1) / wpb;
+    const uint32_t wgs = unsigned(blocks < a.workgroups ? blocks : a.workgroups);
+    hipLaunchKernelGGL(k_gather, dim3(wgs ? wgs : 1), dim3(a.threads), size_t(g.lds_per_wave) * wpb, s, g);
     return hipGetLastError();
 }
 

@@ -447,29 +447,42 @@ def test_operand_errors_empty_selection(ctx, bad, status):
     assert host(cnt, np.uint32)[0] == 8
 
 
-@pytest.mark.parametrize("wgs,chunk", [(1, 1), (7, 3), (64, 8), (1000, 64)])
-def test_gather_options_do_not_change_bytes(ctx, wgs, chunk):
-    """The persistent gather's grid bound and chunk size change only the
-    schedule: every setting writes the same slots."""
+@pytest.mark.parametrize("wgs,chunk,threads", [(1, 1, 64), (7, 3, 128), (64, 8, 256), (1000, 64, 64), (0, 0, 0)])
+def test_gather_options_do_not_change_bytes(ctx, wgs, chunk, threads):
+    """The persistent gather's grid bound, chunk size and workgroup size
+    change only the schedule: every setting writes the same slots (decoding
+    and copying planes, partial last pages and partial last batches)."""
     tokens, width, pt, k = 2100, 1024, 256, 6
     hist = _history(K.FMT_Q8_0, tokens, width, 50)
+    hist16 = _history(K.FMT_F16, tokens, width, 51)
     pin = K.PinnedBuffer(hist.size)
     pin.numpy()[:] = hist
+    pin16 = K.PinnedBuffer(hist16.size)
+    pin16.numpy()[:] = hist16
     sel = np.array([0, 2, 3, 5, 7, 8], np.uint32)
     expect = O.gather(hist, K.FMT_Q8_0, width, tokens, pt, sel, O.GATHER_DEQUANT_F16)
     expect_rq = O.gather(hist, K.FMT_Q8_0, width, tokens, pt, sel, O.GATHER_REQUANT_Q8_0)
+    expect16 = O.gather(hist16, K.FMT_F16, width, tokens, pt, sel, O.GATHER_COPY)
     slots = zeros(expect.size, np.uint8)
     rq = zeros(expect_rq.size, np.uint8)
+    cp = zeros(expect16.size, np.uint8)
     ctx.set_option(K._capi.OPT_GATHER_WORKGROUPS, wgs)
     ctx.set_option(K._capi.OPT_GATHER_CHUNK_ROWS, chunk)
+    ctx.set_option(K._capi.OPT_GATHER_THREADS, threads)
     try:
         planes = [K.make_plane(pin, K.FMT_Q8_0, width, tokens, K.GATHER_DEQUANT_F16, slots),
-                  K.make_plane(pin, K.FMT_Q8_0, width, tokens, K.GATHER_REQUANT_Q8_0, rq)]
+                  K.make_plane(pin, K.FMT_Q8_0, width, tokens, K.GATHER_REQUANT_Q8_0, rq),
+                  K.make_plane(pin16, K.FMT_F16, width, tokens, K.GATHER_COPY, cp)]
         ctx.stage_in(planes, pt, dev(sel), dev(np.array([k], np.uint32)), k)
+        ctx.check()
+        ctx.stage_in(planes[2:], pt, dev(sel), dev(np.array([k], np.uint32)), k)  # copy-only defaults
         ctx.check()
     finally:
         ctx.set_option(K._capi.OPT_GATHER_WORKGROUPS, 0)
         ctx.set_option(K._capi.OPT_GATHER_CHUNK_ROWS, 0)
+        ctx.set_option(K._capi.OPT_GATHER_THREADS, 0)
     assert np.array_equal(host(slots, np.uint8), expect)
     assert np.array_equal(host(rq, np.uint8), expect_rq)
+    assert np.array_equal(host(cp, np.uint8), expect16)
     pin.free()
+    pin16.free()
