@@ -266,7 +266,7 @@ def run(args):
     achieved = alg_kernel_bytes / (kern_us_mean * 1e-6) / 1e9
     scored_gbps = L * geo["scored_bytes"] / (ms_per_step * 1e-3) / 1e9
     traffic = None
-    pmc = os.path.join(ROOT, "profiles", "pmc_summary_resident64.json")
+    pmc = os.path.join(ROOT, "profiles", "pmc_stack_resident64.json")
     if os.path.exists(pmc):
         try:
             traffic = json.load(open(pmc)).get("traffic_bytes_per_launch")

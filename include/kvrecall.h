@@ -301,8 +301,9 @@ kvr_status kvr_recall_layer(kvr_context *ctx, const kvr_layer_recall *desc,
  * launch (the context then keeps two logits buffers), so each layer's
  * selection, select_end event and stage-in follow the next layer's launch;
  * a layer's summary events bracket that shared launch.  Otherwise the layers
- * run one after another.  Replaces the per-layer loop of the adapter's layer
- * stack (score l+1 while l streams in, llama-memory-kvmem.cpp:5011-5126). */
+ * run one after another.  Replaces one select_layerwise_history call per
+ * attention layer (kvmem/src/host/layerwise_selection.cpp:185-199), each
+ * followed by that layer's stage-in. */
 kvr_status kvr_recall_stack(kvr_context *ctx, const kvr_layer_recall *layers, uint32_t n,
                             void *select_stream, void *copy_stream);
 
