@@ -157,6 +157,8 @@ kvr::QueryArgs query_args(const kvr_query *q) {
     a.dim_stride = q->dim_stride;
     a.lane_stride = q->lane_stride;
     a.scale = logit_scale(q->attention_scale, q->head_dim);
+    const uint64_t esz = a.scalar == kvr::kScalarF32 ? 4 : 2;
+    a.dense = a.dim_stride == esz && a.head_stride == esz * a.dim && a.row_stride == esz * a.dim * a.qheads;
     return a;
 }
 
@@ -212,6 +214,8 @@ size_t logits_bytes(uint32_t lanes, uint32_t pages, uint32_t rows, uint32_t qhea
 size_t qpack_bytes(uint32_t lanes, uint32_t rows, uint32_t qheads, uint32_t dim) {
     return align256(size_t(lanes) * rows * qheads * dim * sizeof(uint16_t));
 }
+
+static_assert(kvr::kMaxMandatory == KVR_MAX_INLINE_MANDATORY, "inline mandatory capacity");
 
 struct Mandatory {
     uint32_t n = 0;

@@ -43,9 +43,34 @@ __device__ __forceinline__ void raise_operand(uint32_t *status, uint32_t code, u
     if (code == kOperandNonfinite) raise_status(status, kStatusNonfinite, epoch);
     if (code == kOperandRange) raise_status(status, kStatusRange, epoch);
 }
+// Device-scope (all XCDs) relaxed stores and loads: they write through and
+// read past the XCD's own L2, so data published this way between
+// workgroups of one launch needs neither an L2 writeback on the writer's
+// side nor an L2 invalidate on the reader's, only the stores' completion.
+template <class T> __device__ __forceinline__ void store_device(T *p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T> __device__ __forceinline__ T load_device(const T *p) {
+    return __hip_atomic_load(const_cast<T *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Waits until this thread's vector memory operations have completed
+// (s_waitcnt vmcnt(0); expcnt and lgkmcnt left at their maxima).
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 __device__ __forceinline__ bool epoch_failed(const uint32_t *status, uint32_t epoch) {
-    return status[kStatusNonfinite] == epoch || status[kStatusRange] == epoch ||
-           status[kStatusScores] == epoch;
+    // all three loads in flight together
+    const uint32_t s0 = load_device(status + kStatusNonfinite), s1 = load_device(status + kStatusRange),
+                   s2 = load_device(status + kStatusScores);
+    return (s0 == epoch) | (s1 == epoch) | (s2 == epoch);
+}
+
+// Workgroup barrier that orders LDS only.  __syncthreads() also waits for
+// the thread's outstanding global stores, a full memory round trip when
+// HBM is busy; use this one where the barrier publishes LDS and nothing else.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // ---- wave reductions (64 lanes) --------------------------------------------
@@ -53,6 +78,7 @@ __device__ __forceinline__ bool epoch_failed(const uint32_t *status, uint32_t ep
 // rows; no LDS permutes.  Every lane gets the same result, combined in one
 // fixed order.
 namespace dpp {
+constexpr int kQuadBcast0 = 0x00;    // quad_perm [0,0,0,0]
 constexpr int kQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]
 constexpr int kQuadXor2 = 0x4E;      // quad_perm [2,3,0,1]
 constexpr int kHalfMirror = 0x141;   // lane i <-> 7-i within each 8 lanes

@@ -10,6 +10,7 @@
 namespace kvr {
 
 enum SummarySource : int { kSrcKeysF16 = 0, kSrcKeysQ8 = 1, kSrcSummary = 2 };
+constexpr uint32_t kMaxMandatory = 64;  // inline mandatory pages per call
 enum Scalar : uint32_t { kScalarF16 = 0, kScalarF32 = 3, kScalarBF16 = 4 };  // kvr_format values
 enum Aggregation : uint32_t { kAggMean = 0, kAggMax = 1, kAggMaxLogit = 2 };
 
@@ -19,6 +20,7 @@ struct QueryArgs {
     uint32_t rows, qheads, kvheads, dim;
     uint64_t row_stride, head_stride, dim_stride, lane_stride;  // bytes
     double scale;
+    uint32_t dense;  // (row, head, dim) packed: element i sits at i * element size
 };
 
 // Page summaries of `lanes` histories, optionally fused with the logits of
@@ -76,7 +78,7 @@ struct SelectArgs {
     int signed_scores;
     int do_select;
     uint32_t n_mandatory;      // sorted, unique
-    uint32_t mandatory[64];
+    uint32_t mandatory[kMaxMandatory];
     uint32_t *selected;        // [lanes][k]
     uint32_t *count;           // [lanes]
     uint32_t *status;

@@ -17,6 +17,9 @@ namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef double f64x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+// 12-byte loads need only dword alignment on gfx950 (global_load_dwordx3).
+typedef u32x3 u32x3a __attribute__((aligned(4)));
 
 constexpr uint32_t kFmtF16 = 0, kFmtQ8 = 1, kFmtQ41 = 2;
 constexpr uint32_t kModeCopy = 0, kModeDequantF16 = 1, kModeRequantQ8 = 2;
@@ -25,6 +28,24 @@ __device__ __forceinline__ float load_scalar(const uint8_t *p, uint32_t scalar) 
     if (scalar == kScalarF32) return *reinterpret_cast<const float *>(p);
     const uint16_t bits = *reinterpret_cast<const uint16_t *>(p);
     return scalar == kScalarF16 ? h2f(bits) : bf2f(bits);
+}
+
+// Raw bits of one query element (f32, or f16/bf16 in the low half), so its
+// load can issue long before the value is converted.
+__device__ __forceinline__ uint32_t load_raw(const uint8_t *p, uint32_t scalar) {
+    return scalar == kScalarF32 ? *reinterpret_cast<const uint32_t *>(p)
+                                : uint32_t(*reinterpret_cast<const uint16_t *>(p));
+}
+__device__ __forceinline__ float raw_value(uint32_t raw, uint32_t scalar) {
+    if (scalar == kScalarF32) return __uint_as_float(raw);
+    return scalar == kScalarF16 ? h2f(uint16_t(raw)) : bf2f(uint16_t(raw));
+}
+// Element i of one lane's query rows in (row, head, dim) order.
+__device__ __forceinline__ const uint8_t *query_elem(const QueryArgs &q, uint32_t lane, uint32_t i) {
+    const uint8_t *base = q.data + lane * q.lane_stride;
+    if (q.dense) return base + uint64_t(i) * (q.scalar == kScalarF32 ? 4 : 2);
+    const uint32_t d = i % q.dim, h = (i / q.dim) % q.qheads, r = i / (q.dim * q.qheads);
+    return base + r * q.row_stride + h * q.head_stride + d * q.dim_stride;
 }
 
 __device__ __forceinline__ void add_f16x8(float *acc, const u32x4 v) {
@@ -43,6 +64,41 @@ __device__ __forceinline__ void add_q8x8(float *acc, uint32_t lo, uint32_t hi, f
         acc[i] += float(int8_t(lo >> (8 * i))) * d;
         acc[4 + i] += float(int8_t(hi >> (8 * i))) * d;
     }
+}
+
+// Consumes rows 0..n-1 (n >= 1) in order through a ring of D loads in
+// flight: row t's load issues D rows before row t is used.  Loads past the
+// end are clamped to row n-1 (in bounds, never used), so no load sits behind
+// a branch and the loads issue back to back.
+// Ring depths of the summary streams: 12 rows of 16-byte loads (fp16) and
+// 32 rows of 12-byte loads (q8_0).  Deeper fp16 rings make the register
+// allocator copy ring slots whose loads are still in flight.
+constexpr int kF16Rows = 12, kQ8Rows = 32;
+template <int D, class Load, class Use>
+__device__ __forceinline__ void stream_rows(uint32_t n, Load load, Use use) {
+    decltype(load(0u)) ring[D];
+    // The prologue's loads must issue in ring order: the wait before each
+    // use counts loads still outstanding, so a reordered prologue would make
+    // the first use of every pass wait for all of them.
+#pragma unroll
+    for (int u = 0; u < D; ++u) {
+        ring[u] = load(min(uint32_t(u), n - 1));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    uint32_t t = 0;
+    for (; t + D < n; t += D) {
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+            use(ring[u]);
+            ring[u] = load(min(t + D + u, n - 1));
+            // keeps each use beside its refill: hoisting the conversions of
+            // later rows would wait for their loads before any refill issues
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < D; ++u)
+        if (t + u < n) use(ring[u]);
 }
 
 // ---------------------------------------------------------------------------
@@ -73,6 +129,25 @@ __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t blo
     const uint32_t lane = uint32_t(rest / a.pages);
     const uint32_t c0 = cg * 8;
     uint16_t hb[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    float mean[8];
+    uint32_t sbad = kOperandOk;
+
+    // FUSE with q_stage: the workgroup stages its first lane's query rows in
+    // LDS.  The first kQueryPrefetch elements per thread are loaded here,
+    // ahead of the key stream, and reach LDS after it, so neither the stream
+    // nor the epilogue waits on a query round trip.
+    constexpr uint32_t kQueryPrefetch = 16;
+    uint32_t qraw[kQueryPrefetch];
+    uint32_t staged_lane = 0xffffffffu, nq = 0;
+    if (FUSE && a.q_stage) {
+        staged_lane = uint32_t((uint64_t(block) * 256 / gpp) / a.pages);
+        nq = a.q.rows * a.q.qheads * a.q.dim;
+#pragma unroll
+        for (uint32_t j = 0; j < kQueryPrefetch; ++j) {
+            const uint32_t i = min(threadIdx.x + 256 * j, nq - 1);  // in bounds; extras unused
+            qraw[j] = load_raw(query_elem(a.q, staged_lane, i), a.q.scalar);
+        }
+    }
 
     if (!active) {
         // nothing to summarize; stays for the barrier below
@@ -92,130 +167,84 @@ __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t blo
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
         if (SRC == kSrcKeysF16) {
-            // Software-pipelined: the next U rows are in flight while the
-            // current U are summed (in token order).  The trip count is a
-            // runtime value, so the compiler would otherwise wait on each
-            // group's own loads.
             const u32x4 *p = reinterpret_cast<const u32x4 *>(
                 a.src + lane * a.src_lane_stride + (t0 * a.width + c0) * 2);
             const uint64_t stride = gpp;  // 16-byte words per token row
-            constexpr int U = 8;
-            const uint32_t full = n / U * U;
-            if (full) {
-                u32x4 cur[U], nxt[U];
-#pragma unroll
-                for (int u = 0; u < U; ++u) cur[u] = __builtin_nontemporal_load(p + u * stride);
-                for (uint32_t t = U; t < full; t += U) {
-#pragma unroll
-                    for (int u = 0; u < U; ++u) nxt[u] = __builtin_nontemporal_load(p + (t + u) * stride);
-#pragma unroll
-                    for (int u = 0; u < U; ++u) add_f16x8(acc, cur[u]);
-#pragma unroll
-                    for (int u = 0; u < U; ++u) cur[u] = nxt[u];
-                }
-#pragma unroll
-                for (int u = 0; u < U; ++u) add_f16x8(acc, cur[u]);
-            }
-            for (uint32_t t = full; t < n; ++t) add_f16x8(acc, __builtin_nontemporal_load(p + t * stride));
+            stream_rows<kF16Rows>(
+                n, [&](uint32_t t) { return __builtin_nontemporal_load(p + t * stride); },
+                [&](const u32x4 v) { add_f16x8(acc, v); });
         } else {
-            // q8_0 rows: lane owns 8 codes (quarter s) of block b.  Rows are
-            // 4-byte aligned (width % 64 == 0), so three aligned dwords cover
-            // the 8 codes and one more holds the block scale.
+            // q8_0 rows: lane owns 8 codes (quarter s) of block b, and the
+            // block's four lanes (one quad) read the dword-aligned 36 bytes
+            // around its 34 with one 12-byte load each: lane s takes dwords
+            // [2s, 2s+3) of the span.  Even blocks start on a dword (codes at
+            // span byte 2+8s), odd blocks two bytes into one (span starts two
+            // bytes early, codes at 4+8s).  The fp16 scale sits in lane 0's
+            // first dword and reaches the others by a quad broadcast.
             const uint32_t row_bytes = (a.width >> 5) * kQ8Bytes;
             const uint8_t *base = a.src + lane * a.src_lane_stride + t0 * row_bytes;
             const uint32_t b = cg >> 2, s = cg & 3;
-            const uint32_t o = b * kQ8Bytes + 2 + 8 * s;
-            const uint32_t w0 = o >> 2, wd = (b * kQ8Bytes) >> 2;
-            const bool sh = (o & 2) != 0, shd = ((b * kQ8Bytes) & 2) != 0;
-            constexpr int U = 8;
-            const uint32_t full = n / U * U;
-            auto load_rows = [&](uint32_t t, uint32_t (&x0)[U], uint32_t (&x1)[U], uint32_t (&x2)[U],
-                                 uint32_t (&dw)[U]) {
-#pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    const uint32_t *row = reinterpret_cast<const uint32_t *>(base + uint64_t(t + u) * row_bytes);
-                    x0[u] = __builtin_nontemporal_load(row + w0);
-                    x1[u] = __builtin_nontemporal_load(row + w0 + 1);
-                    x2[u] = sh ? __builtin_nontemporal_load(row + w0 + 2) : 0u;
-                    dw[u] = __builtin_nontemporal_load(row + wd);
-                }
+            const uint32_t span = ((b * kQ8Bytes) & ~3u) + 8 * s;
+            const bool odd = (b & 1) != 0;
+            auto load_row = [&](uint32_t t) {
+                return __builtin_nontemporal_load(reinterpret_cast<const u32x3a *>(base + uint64_t(t) * row_bytes + span));
             };
-            auto sum_rows = [&](const uint32_t (&x0)[U], const uint32_t (&x1)[U], const uint32_t (&x2)[U],
-                                const uint32_t (&dw)[U]) {
-#pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    const uint32_t lo = sh ? __builtin_amdgcn_alignbyte(x1[u], x0[u], 2) : x0[u];
-                    const uint32_t hi = sh ? __builtin_amdgcn_alignbyte(x2[u], x1[u], 2) : x1[u];
-                    add_q8x8(acc, lo, hi, h2f(uint16_t(shd ? dw[u] >> 16 : dw[u] & 0xffffu)));
-                }
+            auto sum_row = [&](const u32x3 x) {
+                const uint32_t lo = odd ? x[1] : __builtin_amdgcn_alignbyte(x[1], x[0], 2);
+                const uint32_t hi = odd ? x[2] : __builtin_amdgcn_alignbyte(x[2], x[1], 2);
+                const uint32_t dw = dpp::move<dpp::kQuadBcast0>(x[0]);
+                add_q8x8(acc, lo, hi, h2f(uint16_t(odd ? dw >> 16 : dw & 0xffffu)));
             };
-            if (full) {
-                uint32_t a0[U], a1[U], a2[U], ad[U], b0[U], b1[U], b2[U], bd[U];
-                load_rows(0, a0, a1, a2, ad);
-                for (uint32_t t = U; t < full; t += U) {
-                    load_rows(t, b0, b1, b2, bd);
-                    sum_rows(a0, a1, a2, ad);
-#pragma unroll
-                    for (int u = 0; u < U; ++u) {
-                        a0[u] = b0[u]; a1[u] = b1[u]; a2[u] = b2[u]; ad[u] = bd[u];
-                    }
-                }
-                sum_rows(a0, a1, a2, ad);
-            }
-            for (uint32_t t = full; t < n; ++t) {
-                const uint32_t *row = reinterpret_cast<const uint32_t *>(base + uint64_t(t) * row_bytes);
-                const uint32_t x0 = row[w0], x1 = row[w0 + 1], x2 = sh ? row[w0 + 2] : 0u, dw = row[wd];
-                const uint32_t lo = sh ? __builtin_amdgcn_alignbyte(x1, x0, 2) : x0;
-                const uint32_t hi = sh ? __builtin_amdgcn_alignbyte(x2, x1, 2) : x1;
-                add_q8x8(acc, lo, hi, h2f(uint16_t(shd ? dw >> 16 : dw & 0xffffu)));
-            }
+            stream_rows<kQ8Rows>(n, load_row, sum_row);
         }
         const float inv = 1.0f / float(n);
-        float mean[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) mean[i] = acc[i] * inv;
-        const uint64_t out = (uint64_t(lane) * a.pages + page) * a.width + c0;
-        if (a.means) {
-            float4 *m4 = reinterpret_cast<float4 *>(a.means + out);
-            m4[0] = make_float4(mean[0], mean[1], mean[2], mean[3]);
-            m4[1] = make_float4(mean[4], mean[5], mean[6], mean[7]);
-        }
-        uint32_t bad = kOperandOk;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
+            mean[i] = acc[i] * inv;
             const uint32_t e = recall16(mean[i], hb[i]);
-            bad = bad ? bad : e;
-        }
-        if (bad) raise_operand(a.status, bad, a.epoch);
-        if (a.summaries) {
-            u32x4 v;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) v[i] = uint32_t(hb[2 * i]) | (uint32_t(hb[2 * i + 1]) << 16);
-            *reinterpret_cast<u32x4 *>(a.summaries + out) = v;
+            sbad = sbad ? sbad : e;
         }
     }
 
-    if (FUSE) {
+    // The staged query reaches LDS before this thread stores anything: a
+    // wait for its loads placed after a store would also wait for the store.
+    if (FUSE && a.q_stage) {
         const QueryArgs &q = a.q;
-        // Stage the first lane's query rows after the HBM stream, while other
-        // workgroups still stream theirs, instead of delaying every first load.
-        uint32_t staged_lane = 0xffffffffu;
-        if (a.q_stage) {
-            staged_lane = uint32_t((uint64_t(block) * 256 / gpp) / a.pages);
-            const uint32_t nq = q.rows * q.qheads * q.dim;
+        {
             uint32_t qbad = kOperandOk;
-            for (uint32_t i = threadIdx.x; i < nq; i += 256) {
-                const uint32_t d = i % q.dim, h = (i / q.dim) % q.qheads, r = i / (q.dim * q.qheads);
+#pragma unroll
+            for (uint32_t j = 0; j < kQueryPrefetch; ++j) {
+                const uint32_t i = threadIdx.x + 256 * j;
                 uint16_t qh = 0;
-                const uint32_t e = recall16(load_scalar(q.data + staged_lane * q.lane_stride + r * q.row_stride +
-                                                            h * q.head_stride + d * q.dim_stride, q.scalar), qh);
-                qbad = qbad ? qbad : e;
-                q_lds[i] = qh;
+                const uint32_t e = recall16(raw_value(qraw[j], q.scalar), qh);
+                if (i < nq) {
+                    qbad = qbad ? qbad : e;
+                    q_lds[i] = qh;
+                }
+            }
+            // the rest, 16 loads in flight per pass
+            for (uint32_t base = threadIdx.x + 256 * kQueryPrefetch; base < nq; base += 256 * kQueryPrefetch) {
+#pragma unroll
+                for (uint32_t j = 0; j < kQueryPrefetch; ++j)
+                    qraw[j] = load_raw(query_elem(q, staged_lane, min(base + 256 * j, nq - 1)), q.scalar);
+#pragma unroll
+                for (uint32_t j = 0; j < kQueryPrefetch; ++j) {
+                    const uint32_t i = base + 256 * j;
+                    uint16_t qh = 0;
+                    const uint32_t e = recall16(raw_value(qraw[j], q.scalar), qh);
+                    if (i < nq) {
+                        qbad = qbad ? qbad : e;
+                        q_lds[i] = qh;
+                    }
+                }
             }
             if (qbad) raise_operand(a.status, qbad, a.epoch);
-            __syncthreads();
         }
-        if (!active) return;
+    }
+
+    if (FUSE && a.q_stage) lds_barrier();
+    if (FUSE && active) {
+        const QueryArgs &q = a.q;
         const uint32_t kvh = c0 / q.dim, d0 = c0 % q.dim;
         const uint32_t group = q.qheads / q.kvheads;
         const int lph = int(q.dim >> 3);  // lanes per kv-head slice
@@ -224,36 +253,65 @@ __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t blo
         for (int i = 0; i < 8; ++i) m[i] = double(h2f(hb[i]));
         uint32_t bad = kOperandOk;
         const bool from_lds = lane == staged_lane;
+        const bool writer = (cg & uint32_t(lph - 1)) == 0;
+        // Four heads of the kv-head's group at a time (the last pass repeats
+        // the group's last head and does not store it), so their loads and
+        // cross-lane sums overlap.
         for (uint32_t r = 0; r < q.rows; ++r) {
-            for (uint32_t hh = 0; hh < group; ++hh) {
-                const uint32_t h = kvh * group + hh;
-                double part = 0.0;
-                if (from_lds) {
-                    const u32x4 v = *reinterpret_cast<const u32x4 *>(q_lds + (r * q.qheads + h) * q.dim + d0);
+            for (uint32_t h0 = 0; h0 < group; h0 += 4) {
+                double part[4];
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        part = fma(double(h2f(uint16_t(v[i] & 0xffffu))), m[2 * i], part);
-                        part = fma(double(h2f(uint16_t(v[i] >> 16))), m[2 * i + 1], part);
-                    }
-                } else {
-                    const uint8_t *qp = q.data + lane * q.lane_stride + r * q.row_stride +
-                                        h * q.head_stride + d0 * q.dim_stride;
+                for (uint32_t u = 0; u < 4; ++u) {
+                    const uint32_t h = kvh * group + min(h0 + u, group - 1);
+                    part[u] = 0.0;
+                    if (from_lds) {
+                        const u32x4 v = *reinterpret_cast<const u32x4 *>(q_lds + (r * q.qheads + h) * q.dim + d0);
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        uint16_t qb = 0;
-                        const uint32_t e = recall16(load_scalar(qp + i * q.dim_stride, q.scalar), qb);
-                        bad = bad ? bad : e;
-                        // fp16 x fp16 is exact in binary64: fma == multiply-then-add.
-                        part = fma(double(h2f(qb)), m[i], part);
+                        for (int i = 0; i < 4; ++i) {
+                            part[u] = fma(double(h2f(uint16_t(v[i] & 0xffffu))), m[2 * i], part[u]);
+                            part[u] = fma(double(h2f(uint16_t(v[i] >> 16))), m[2 * i + 1], part[u]);
+                        }
+                    } else {
+                        const uint8_t *qp = q.data + lane * q.lane_stride + r * q.row_stride +
+                                            h * q.head_stride + d0 * q.dim_stride;
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) {
+                            uint16_t qb = 0;
+                            const uint32_t e = recall16(load_scalar(qp + i * q.dim_stride, q.scalar), qb);
+                            bad = bad ? bad : e;
+                            // fp16 x fp16 is exact in binary64: fma == multiply-then-add.
+                            part[u] = fma(double(h2f(qb)), m[i], part[u]);
+                        }
                     }
                 }
-                part = group_sum(part, lph);
-                if ((cg & uint32_t(lph - 1)) == 0)
-                    a.logits[((uint64_t(lane) * q.rows + r) * q.qheads + h) * a.pages + page] =
-                        part * q.scale;
+#pragma unroll
+                for (uint32_t u = 0; u < 4; ++u) part[u] = group_sum(part[u], lph);
+#pragma unroll
+                for (uint32_t u = 0; u < 4; ++u)
+                    if (writer && h0 + u < group)
+                        a.logits[((uint64_t(lane) * q.rows + r) * q.qheads + kvh * group + h0 + u) * a.pages + page] =
+                            part[u] * q.scale;
             }
         }
         if (bad) raise_operand(a.status, bad, a.epoch);
+    }
+
+    // Summary stores last: nothing after them reuses their registers, so no
+    // wait for their completion lands inside the fused epilogue.
+    if (active && SRC != kSrcSummary) {
+        const uint64_t out = (uint64_t(lane) * a.pages + page) * a.width + c0;
+        if (a.means) {
+            float4 *m4 = reinterpret_cast<float4 *>(a.means + out);
+            m4[0] = make_float4(mean[0], mean[1], mean[2], mean[3]);
+            m4[1] = make_float4(mean[4], mean[5], mean[6], mean[7]);
+        }
+        if (sbad) raise_operand(a.status, sbad, a.epoch);
+        if (a.summaries) {
+            u32x4 v;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = uint32_t(hb[2 * i]) | (uint32_t(hb[2 * i + 1]) << 16);
+            *reinterpret_cast<u32x4 *>(a.summaries + out) = v;
+        }
     }
 }
 
@@ -377,19 +435,31 @@ __device__ __forceinline__ void wave_softmax_regs(double (&v)[NPL], const bool (
 // One unit by one wave, rows of up to 64*NPL pages held in registers.
 template <int NPL>
 __device__ __forceinline__ void unit_terms_regs(const SelectArgs &a, double *lane_base, uint32_t unit) {
+    // Loads are unconditional with indices clamped into the row (values past
+    // the row are read, then dropped): a load behind a per-lane branch would
+    // wait for itself before the next one issues.
     const uint32_t n = a.pages, l = threadIdx.x & 63;
+    auto at = [&](uint32_t i) { return min(l + uint32_t(i) * kWave, n - 1); };
     bool on[NPL];
+    uint8_t mv[NPL];
+    if (a.mask) {
 #pragma unroll
-    for (int i = 0; i < NPL; ++i) {
-        const uint32_t j = l + i * kWave;
-        on[i] = j < n && (!a.mask || a.mask[j]);
+        for (int i = 0; i < NPL; ++i) mv[i] = a.mask[at(i)];
+    } else {
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) mv[i] = 1;
     }
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) on[i] = l + i * kWave < n && mv[i];
     double t[NPL];
     double *out;
     if (a.aggregation == kAggMean) {
         out = lane_base + uint64_t(unit) * n;
 #pragma unroll
-        for (int i = 0; i < NPL; ++i) t[i] = on[i] ? out[l + i * kWave] : 0.0;
+        for (int i = 0; i < NPL; ++i) {
+            const double x = out[at(i)];
+            t[i] = on[i] ? x : 0.0;
+        }
         wave_softmax_regs(t, on);
 #pragma unroll
         for (int i = 0; i < NPL; ++i) t[i] = t[i] / a.weight;
@@ -404,7 +474,10 @@ __device__ __forceinline__ void unit_terms_regs(const SelectArgs &a, double *lan
             for (uint32_t hh = 0; hh < group; ++hh) {
                 const double *row = out + uint64_t(hh) * n;
 #pragma unroll
-                for (int i = 0; i < NPL; ++i) t[i] = on[i] ? row[l + i * kWave] : 0.0;
+                for (int i = 0; i < NPL; ++i) {
+                    const double x = row[at(i)];
+                    t[i] = on[i] ? x : 0.0;
+                }
                 wave_softmax_regs(t, on);
 #pragma unroll
                 for (int i = 0; i < NPL; ++i) gm[i] = t[i] > gm[i] ? t[i] : gm[i];
@@ -421,8 +494,10 @@ __device__ __forceinline__ void unit_terms_regs(const SelectArgs &a, double *lan
             for (uint32_t hh = 0; hh < group; ++hh) {
                 const double *row = out + uint64_t(hh) * n;
 #pragma unroll
-                for (int i = 0; i < NPL; ++i)
-                    if (on[i]) t[i] = fmax(t[i], row[l + i * kWave]);
+                for (int i = 0; i < NPL; ++i) {
+                    const double x = row[at(i)];
+                    t[i] = fmax(t[i], on[i] ? x : -INFINITY);
+                }
             }
             wave_softmax_regs(t, on);
 #pragma unroll
@@ -433,7 +508,7 @@ __device__ __forceinline__ void unit_terms_regs(const SelectArgs &a, double *lan
 #pragma unroll
     for (int i = 0; i < NPL; ++i) {
         const uint32_t j = l + i * kWave;
-        if (j < n) out[j] = t[i];
+        if (j < n) store_device(out + j, t[i]);
     }
 }
 
@@ -443,20 +518,22 @@ __device__ __forceinline__ void unit_terms_regs(const SelectArgs &a, double *lan
 __device__ __forceinline__ void unit_terms_loop(const SelectArgs &a, double *lane_base, uint32_t unit) {
     const uint32_t n = a.pages, l = threadIdx.x & 63;
     auto on = [&](uint32_t j) { return !a.mask || a.mask[j]; };
-    auto stats = [&](const double *row, double &m, double &s) {
+    // `own`: the row holds values this lane stored at device scope
+    auto stats = [&](const double *row, double &m, double &s, bool own) {
+        auto at = [&](uint32_t j) { return own ? load_device(row + j) : row[j]; };
         double mm = -INFINITY;
-        for (uint32_t j = l; j < n; j += kWave) mm = on(j) ? fmax(mm, row[j]) : mm;
+        for (uint32_t j = l; j < n; j += kWave) mm = on(j) ? fmax(mm, at(j)) : mm;
         m = wave_max(mm);
         double ss = 0.0;
-        for (uint32_t j = l; j < n; j += kWave) ss += on(j) ? exp(row[j] - m) : 0.0;
+        for (uint32_t j = l; j < n; j += kWave) ss += on(j) ? exp(at(j) - m) : 0.0;
         s = wave_sum(ss);
     };
     auto prob = [&](double x, double m, double s) { return s > 0.0 ? exp(x - m) / s : 0.0; };
     if (a.aggregation == kAggMean) {
         double *row = lane_base + uint64_t(unit) * n;
         double m, s;
-        stats(row, m, s);
-        for (uint32_t j = l; j < n; j += kWave) row[j] = (on(j) ? prob(row[j], m, s) : 0.0) / a.weight;
+        stats(row, m, s, false);
+        for (uint32_t j = l; j < n; j += kWave) store_device(row + j, (on(j) ? prob(row[j], m, s) : 0.0) / a.weight);
         return;
     }
     const uint32_t group = a.qheads / a.kvheads;
@@ -467,31 +544,33 @@ __device__ __forceinline__ void unit_terms_loop(const SelectArgs &a, double *lan
         for (uint32_t hh = 0; hh < group; ++hh) {
             double *row = out + uint64_t(hh) * n;
             double m, s;
-            stats(row, m, s);
-            for (uint32_t j = l; j < n; j += kWave) row[j] = on(j) ? prob(row[j], m, s) : 0.0;
+            stats(row, m, s, false);
+            for (uint32_t j = l; j < n; j += kWave) store_device(row + j, on(j) ? prob(row[j], m, s) : 0.0);
         }
         double mass = 0.0;
         for (uint32_t j = l; j < n; j += kWave) {
             double gm = 0.0;
             for (uint32_t hh = 0; hh < group; ++hh) {
-                const double p = out[uint64_t(hh) * n + j];
+                const double p = load_device(out + uint64_t(hh) * n + j);
                 gm = p > gm ? p : gm;
             }
-            out[j] = gm;
+            store_device(out + j, gm);
             mass += gm;
         }
         mass = wave_sum(mass);
-        for (uint32_t j = l; j < n; j += kWave) out[j] = (mass > 0.0 ? out[j] / mass : 0.0) / a.weight;
+        for (uint32_t j = l; j < n; j += kWave)
+            store_device(out + j, (mass > 0.0 ? load_device(out + j) / mass : 0.0) / a.weight);
     } else {
         for (uint32_t j = l; j < n; j += kWave) {
             double gm = -INFINITY;
             if (on(j))
                 for (uint32_t hh = 0; hh < group; ++hh) gm = fmax(gm, out[uint64_t(hh) * n + j]);
-            out[j] = gm;
+            store_device(out + j, gm);
         }
         double m, s;
-        stats(out, m, s);
-        for (uint32_t j = l; j < n; j += kWave) out[j] = (on(j) ? prob(out[j], m, s) : 0.0) / a.weight;
+        stats(out, m, s, true);
+        for (uint32_t j = l; j < n; j += kWave)
+            store_device(out + j, (on(j) ? prob(load_device(out + j), m, s) : 0.0) / a.weight);
     }
 }
 
@@ -511,14 +590,24 @@ __device__ __forceinline__ uint64_t order_key(double v) {
     return (u >> 63) ? ~u : (u | 0x8000000000000000ull);
 }
 
-__device__ __forceinline__ bool is_mandatory(const SelectArgs &a, uint32_t j) {
-    uint32_t lo = 0, hi = a.n_mandatory;
-    while (lo < hi) {
-        const uint32_t mid = (lo + hi) >> 1;
-        if (a.mandatory[mid] < j) lo = mid + 1; else hi = mid;
+// Mandatory pages (ascending, at most 64, copied to LDS) met in ascending
+// page order: each query advances a cursor, so a lane's walk over its chunk
+// reads the list once.
+struct MandatoryCursor {
+    const uint32_t *ids;
+    uint32_t p, n;
+    __device__ __forceinline__ MandatoryCursor(const uint32_t *m, uint32_t count, uint32_t first) : ids(m), p(0), n(count) {
+        uint32_t hi = n;  // first entry >= `first`
+        while (p < hi) {
+            const uint32_t mid = (p + hi) >> 1;
+            if (ids[mid] < first) p = mid + 1; else hi = mid;
+        }
     }
-    return lo < a.n_mandatory && a.mandatory[lo] == j;
-}
+    __device__ __forceinline__ bool at(uint32_t j) {
+        while (p < n && ids[p] < j) ++p;
+        return p < n && ids[p] == j;
+    }
+};
 
 // Dynamic LDS of the selection kernels: the lane's keys (pages <= kTailLdsPages).
 extern __shared__ __align__(16) uint64_t tail_keys[];
@@ -580,22 +669,23 @@ __device__ __forceinline__ bool radix_pass(ForEach for_each_key, uint32_t *hist,
 //                                   by id (tie rule), shift == 0
 template <int CM>
 __device__ __forceinline__ void wave_select(const SelectArgs &a, uint32_t lane, bool lds, const double *sc,
-                                            uint32_t *hist) {
+                                            uint32_t *hist, const uint32_t *mand_ids) {
     const uint32_t l = threadIdx.x & 63, n = a.pages;
     const uint32_t C = (n + kWave - 1) / kWave;
     const uint32_t j0 = min(n, l * C), j1 = min(n, j0 + C);
     auto load_key = [&](uint32_t j) -> uint64_t { return lds ? tail_keys[j] : order_key(sc[j]); };
-    auto mand = [&](uint32_t j) { return a.n_mandatory && is_mandatory(a, j); };
+    const MandatoryCursor mand0(mand_ids, a.n_mandatory, j0);
     constexpr int R = CM > 0 ? CM : 1;
     uint64_t kr[R];
     uint32_t cand_bits = 0;  // chunk entries that are candidates (register mode)
     if (CM > 0) {
+        MandatoryCursor mand = mand0;
 #pragma unroll
         for (int c = 0; c < R; ++c) {
             const uint32_t j = j0 + c;
             const bool in = j < j1;
             kr[c] = in ? load_key(j) : 0;
-            if (in && !mand(j)) cand_bits |= 1u << c;
+            if (in && !mand.at(j)) cand_bits |= 1u << c;
         }
     }
     // f(key) over this lane's candidates
@@ -605,8 +695,9 @@ __device__ __forceinline__ void wave_select(const SelectArgs &a, uint32_t lane, 
             for (int c = 0; c < R; ++c)
                 if (cand_bits >> c & 1u) f(kr[c]);
         } else {
+            MandatoryCursor mand = mand0;
             for (uint32_t j = j0; j < j1; ++j)
-                if (!mand(j)) f(load_key(j));
+                if (!mand.at(j)) f(load_key(j));
         }
     };
     const uint32_t n_cand = n - a.n_mandatory;
@@ -662,8 +753,9 @@ __device__ __forceinline__ void wave_select(const SelectArgs &a, uint32_t lane, 
             n_eq += k == 1;
         }
     } else {
+        MandatoryCursor mand = mand0;
         for (uint32_t j = j0; j < j1; ++j) {
-            const int k = mand(j) ? 2 : cls(load_key(j));
+            const int k = mand.at(j) ? 2 : cls(load_key(j));
             n_take += k == 2;
             n_eq += k == 1;
         }
@@ -699,7 +791,8 @@ __device__ __forceinline__ void wave_select(const SelectArgs &a, uint32_t lane, 
         for (int c = 0; c < R; ++c)
             if (j0 + c < j1) emit(j0 + c, (cand_bits >> c & 1u) ? cls(kr[c]) : 2);
     } else {
-        for (uint32_t j = j0; j < j1; ++j) emit(j, mand(j) ? 2 : cls(load_key(j)));
+        MandatoryCursor mand = mand0;
+        for (uint32_t j = j0; j < j1; ++j) emit(j, mand.at(j) ? 2 : cls(load_key(j)));
     }
     if (l == 0) a.count[lane] = min(total, a.k);
 }
@@ -708,6 +801,7 @@ __device__ __forceinline__ void wave_select(const SelectArgs &a, uint32_t lane, 
 // first wave.  Keys go to LDS when the lane's pages fit.
 __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
     __shared__ uint32_t hist[256];
+    __shared__ uint32_t mand_ids[kMaxMandatory];
     const uint32_t tid = threadIdx.x, B = blockDim.x;
     const uint32_t n = a.pages;
     const bool lds = n <= kTailLdsPages;
@@ -742,8 +836,8 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
 #pragma unroll
                 for (int u = 0; u < 32; ++u) {
                     const uint64_t o = row_of(i + u) * n;
-                    v0[u] = terms[o + j0];
-                    v1[u] = has1 ? terms[o + j1] : 0.0;
+                    v0[u] = load_device(terms + o + j0);
+                    v1[u] = has1 ? load_device(terms + o + j1) : 0.0;
                 }
 #pragma unroll
                 for (int u = 0; u < 32; ++u) {
@@ -756,8 +850,8 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
                     const uint64_t o = row_of(i + u) * n;
-                    v0[u] = terms[o + j0];
-                    v1[u] = has1 ? terms[o + j1] : 0.0;
+                    v0[u] = load_device(terms + o + j0);
+                    v1[u] = has1 ? load_device(terms + o + j1) : 0.0;
                 }
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
@@ -767,8 +861,8 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
             }
             for (; i < nrows; ++i) {
                 const uint64_t o = row_of(i) * n;
-                acc0 += terms[o + j0];
-                if (has1) acc1 += terms[o + j1];
+                acc0 += load_device(terms + o + j0);
+                if (has1) acc1 += load_device(terms + o + j1);
             }
             sc[j0] = acc0;
             note(j0, acc0);
@@ -789,8 +883,10 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
         if (tid == 0) a.count[lane] = 0;
         return;
     }
-    if (n <= 16 * kWave) wave_select<16>(a, lane, lds, sc, hist);
-    else wave_select<0>(a, lane, lds, sc, hist);
+    if (tid < a.n_mandatory) mand_ids[tid] = a.mandatory[tid];
+    wave_lds_sync();
+    if (n <= 16 * kWave) wave_select<16>(a, lane, lds, sc, hist, mand_ids);
+    else wave_select<0>(a, lane, lds, sc, hist, mand_ids);
 }
 
 // Softmax units -> terms; the lane's last workgroup aggregates (+ selects).
@@ -808,10 +904,10 @@ __device__ __forceinline__ void probs_block(const SelectArgs &a, uint32_t unit_b
         else
             unit_terms_loop(a, lane_base, unit);
     }
-    // Publish this workgroup's terms (device scope), then count it.  Only
-    // the lane's last workgroup continues; its counter is back at zero for
-    // the next launch.
-    __threadfence();
+    // Publish this workgroup's terms (stored at device scope: complete once
+    // every thread's stores are), then count it.  Only the lane's last
+    // workgroup continues; its counter is back at zero for the next launch.
+    wait_vmem();
     __syncthreads();
     if (threadIdx.x == 0) {
         const uint32_t done = atomicAdd(a.counters + lane, 1u);
@@ -820,7 +916,7 @@ __device__ __forceinline__ void probs_block(const SelectArgs &a, uint32_t unit_b
     }
     __syncthreads();
     if (!s_last) return;
-    __threadfence();  // the other workgroups' terms are visible from here
+    // the tail reads the terms and status words at device scope
     lane_tail(a, lane);
 }
 

@@ -74,7 +74,8 @@ def test_summary_f16_bit_exact(ctx, tokens, page_tokens, kvh, dim):
     assert np.array_equal(host(s16, np.uint16), means.ravel().astype(np.float16).view(np.uint16))
 
 
-@pytest.mark.parametrize("tokens,page_tokens,kvh,dim", [(4000, 256, 8, 128), (700, 64, 2, 256), (130, 32, 1, 64)])
+@pytest.mark.parametrize("tokens,page_tokens,kvh,dim", [(4000, 256, 8, 128), (700, 64, 2, 256), (130, 32, 1, 64),
+                                                        (1000, 24, 4, 64)])
 def test_summary_q8_0_bit_exact(ctx, tokens, page_tokens, kvh, dim):
     w = kvh * dim
     keys = O.synth_q8_0(SEED, 2, tokens * w // 32, 0.01, 0.05)
