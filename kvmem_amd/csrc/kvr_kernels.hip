@@ -411,7 +411,10 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_wave_barrier();
 }
 
-constexpr uint32_t kUnitsPerBlock = 4;    // one softmax unit per wave
+// Softmax units per 256-thread workgroup: one per wave for rows held in
+// registers (up to 1024 pages), the whole workgroup for longer rows.
+constexpr uint32_t kUnitsPerBlock = 4;
+__host__ __device__ constexpr uint32_t units_per_block(uint32_t pages) { return pages <= 1024 ? kUnitsPerBlock : 1; }
 constexpr uint32_t kTailLdsPages = 8192;  // keys of up to this many pages stay in LDS
 
 // Registers: value i of a lane is page j = l + 64*i.
@@ -512,65 +515,136 @@ __device__ __forceinline__ void unit_terms_regs(const SelectArgs &a, double *lan
     }
 }
 
-// Rows longer than 1024 pages: lane-stride passes over memory; per-head
-// statistics first, then one pass per page.  Each lane touches only pages
-// j == l (mod 64).
+// Workgroup-wide max and sum (waves by DPP, then the four wave results in
+// wave order through LDS).
+__device__ __forceinline__ double block_max(double v) {
+    __shared__ double part[4];
+    v = wave_max(v);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
+    lds_barrier();
+    v = fmax(fmax(part[0], part[1]), fmax(part[2], part[3]));
+    lds_barrier();
+    return v;
+}
+__device__ __forceinline__ double block_sum(double v) {
+    __shared__ double part[4];
+    v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
+    lds_barrier();
+    v = ((part[0] + part[1]) + part[2]) + part[3];
+    lds_barrier();
+    return v;
+}
+
+// Rows longer than 1024 pages: one unit per 256-thread workgroup, passes
+// over memory in tiles of 16 values per thread (4096 pages per tile), the
+// tile's loads in flight together; per-head statistics first, then one pass
+// per page.  Thread t touches only pages j == t (mod 256).  Values this
+// thread stored are re-read at device scope.
 __device__ __forceinline__ void unit_terms_loop(const SelectArgs &a, double *lane_base, uint32_t unit) {
-    const uint32_t n = a.pages, l = threadIdx.x & 63;
-    auto on = [&](uint32_t j) { return !a.mask || a.mask[j]; };
-    // `own`: the row holds values this lane stored at device scope
-    auto stats = [&](const double *row, double &m, double &s, bool own) {
-        auto at = [&](uint32_t j) { return own ? load_device(row + j) : row[j]; };
+    constexpr int T = 16;
+    constexpr uint32_t S = 256;  // threads per unit
+    const uint32_t n = a.pages, l = threadIdx.x;
+    // f(j, value, on) for this lane's pages j < n of `row`
+    auto tiles = [&](const double *row, bool own, auto f) {
+        for (uint32_t base = 0; base < n; base += S * T) {
+            double x[T];
+            bool on[T];
+            if (a.mask) {
+                uint8_t mk[T];
+#pragma unroll
+                for (int i = 0; i < T; ++i) {
+                    const uint32_t j = min(base + l + i * S, n - 1);
+                    x[i] = own ? load_device(row + j) : row[j];
+                    mk[i] = a.mask[j];
+                }
+#pragma unroll
+                for (int i = 0; i < T; ++i) on[i] = mk[i] != 0;
+            } else {
+#pragma unroll
+                for (int i = 0; i < T; ++i) {
+                    const uint32_t j = min(base + l + i * S, n - 1);
+                    x[i] = own ? load_device(row + j) : row[j];
+                    on[i] = true;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < T; ++i) {
+                const uint32_t j = base + l + i * S;
+                if (j < n) f(j, x[i], on[i]);
+            }
+        }
+    };
+    auto stats = [&](const double *row, bool own, double &m, double &s) {
         double mm = -INFINITY;
-        for (uint32_t j = l; j < n; j += kWave) mm = on(j) ? fmax(mm, at(j)) : mm;
-        m = wave_max(mm);
+        tiles(row, own, [&](uint32_t, double x, bool on) { mm = on ? fmax(mm, x) : mm; });
+        m = block_max(mm);
         double ss = 0.0;
-        for (uint32_t j = l; j < n; j += kWave) ss += on(j) ? exp(at(j) - m) : 0.0;
-        s = wave_sum(ss);
+        tiles(row, own, [&](uint32_t, double x, bool on) { ss += on ? exp(x - m) : 0.0; });
+        s = block_sum(ss);
     };
     auto prob = [&](double x, double m, double s) { return s > 0.0 ? exp(x - m) / s : 0.0; };
     if (a.aggregation == kAggMean) {
         double *row = lane_base + uint64_t(unit) * n;
         double m, s;
-        stats(row, m, s, false);
-        for (uint32_t j = l; j < n; j += kWave) store_device(row + j, (on(j) ? prob(row[j], m, s) : 0.0) / a.weight);
+        stats(row, false, m, s);
+        tiles(row, false, [&](uint32_t j, double x, bool on) {
+            store_device(row + j, (on ? prob(x, m, s) : 0.0) / a.weight);
+        });
         return;
     }
     const uint32_t group = a.qheads / a.kvheads;
     const uint32_t r = unit / a.kvheads, g = unit % a.kvheads;
     double *out = lane_base + (uint64_t(r) * a.qheads + uint64_t(g) * group) * n;
+    // g_j = max over the group's rows of value(hh, j), into out[j]
+    auto group_max = [&](bool own, double init, auto value) {
+        double total = 0.0;
+        for (uint32_t base = 0; base < n; base += S * T) {
+            double gm[T];
+#pragma unroll
+            for (int i = 0; i < T; ++i) gm[i] = init;
+            for (uint32_t hh = 0; hh < group; ++hh) {
+                const double *row = out + uint64_t(hh) * n;
+                double x[T];
+#pragma unroll
+                for (int i = 0; i < T; ++i) {
+                    const uint32_t j = min(base + l + i * S, n - 1);
+                    x[i] = own ? load_device(row + j) : row[j];
+                }
+#pragma unroll
+                for (int i = 0; i < T; ++i) gm[i] = value(gm[i], x[i]);
+            }
+#pragma unroll
+            for (int i = 0; i < T; ++i) {
+                const uint32_t j = base + l + i * S;
+                if (j < n) {
+                    store_device(out + j, gm[i]);
+                    total += gm[i];
+                }
+            }
+        }
+        return total;
+    };
     if (a.aggregation == kAggMax) {
         // each head's probabilities over its own row, then g_j into the first
         for (uint32_t hh = 0; hh < group; ++hh) {
             double *row = out + uint64_t(hh) * n;
             double m, s;
-            stats(row, m, s, false);
-            for (uint32_t j = l; j < n; j += kWave) store_device(row + j, on(j) ? prob(row[j], m, s) : 0.0);
+            stats(row, false, m, s);
+            tiles(row, false, [&](uint32_t j, double x, bool on) { store_device(row + j, on ? prob(x, m, s) : 0.0); });
         }
-        double mass = 0.0;
-        for (uint32_t j = l; j < n; j += kWave) {
-            double gm = 0.0;
-            for (uint32_t hh = 0; hh < group; ++hh) {
-                const double p = load_device(out + uint64_t(hh) * n + j);
-                gm = p > gm ? p : gm;
-            }
-            store_device(out + j, gm);
-            mass += gm;
-        }
-        mass = wave_sum(mass);
-        for (uint32_t j = l; j < n; j += kWave)
-            store_device(out + j, (mass > 0.0 ? load_device(out + j) / mass : 0.0) / a.weight);
+        // masked pages hold probability 0 in every row, so their g_j is 0
+        const double mass = block_sum(group_max(true, 0.0, [](double gm, double p) { return p > gm ? p : gm; }));
+        tiles(out, true, [&](uint32_t j, double x, bool) {
+            store_device(out + j, (mass > 0.0 ? x / mass : 0.0) / a.weight);
+        });
     } else {
-        for (uint32_t j = l; j < n; j += kWave) {
-            double gm = -INFINITY;
-            if (on(j))
-                for (uint32_t hh = 0; hh < group; ++hh) gm = fmax(gm, out[uint64_t(hh) * n + j]);
-            store_device(out + j, gm);
-        }
+        group_max(false, -INFINITY, [](double gm, double x) { return fmax(gm, x); });
         double m, s;
-        stats(out, m, s, true);
-        for (uint32_t j = l; j < n; j += kWave)
-            store_device(out + j, (on(j) ? prob(load_device(out + j), m, s) : 0.0) / a.weight);
+        stats(out, true, m, s);
+        tiles(out, true, [&](uint32_t j, double x, bool on) {
+            store_device(out + j, (on ? prob(x, m, s) : 0.0) / a.weight);
+        });
     }
 }
 
@@ -578,11 +652,13 @@ __device__ __forceinline__ void unit_terms_loop(const SelectArgs &a, double *lan
 // Selection restates KvMemStore::pick_scored_blocks
 // (kvmem/src/host/kvmem_store.cpp:418-451): mandatory pages first, then the
 // best (score desc, id by tie rule) up to k, output in ascending id order.
-// One wave finds the k-th best of the order-preserving 64-bit keys by an MSB
+// The k-th best of the order-preserving 64-bit keys is found by an MSB
 // radix select (8-bit digits in an LDS histogram, the leading bits common to
 // every candidate skipped, early exit once the boundary bucket is taken
-// whole) and compacts in id order with wave scans; ties at the threshold are
-// resolved by rank among equal keys in id order.  No workgroup barriers.
+// whole), then the pages are compacted in id order with scans; ties at the
+// threshold are resolved by rank among equal keys in id order.  One wave
+// does it for up to 1024 pages (no workgroup barriers), the whole
+// workgroup for longer rows.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint64_t order_key(double v) {
     uint64_t u = uint64_t(__double_as_longlong(v));
@@ -612,6 +688,35 @@ struct MandatoryCursor {
 // Dynamic LDS of the selection kernels: the lane's keys (pages <= kTailLdsPages).
 extern __shared__ __align__(16) uint64_t tail_keys[];
 
+// One wave finds, in a complete 256-bin digit histogram, the digit `d`
+// holding the `remaining`-th best key, the rank `rem` within it and its
+// count `cnt` (every lane gets them).
+__device__ __forceinline__ void radix_find(const uint32_t *hist, uint32_t remaining, uint32_t &d, uint32_t &rem,
+                                           uint32_t &cnt) {
+    const uint32_t l = threadIdx.x & 63;
+    // lane l covers digits 255-4l .. 252-4l, highest first
+    const uint32_t c0 = hist[255 - 4 * l], c1 = hist[254 - 4 * l], c2 = hist[253 - 4 * l],
+                   c3 = hist[252 - 4 * l];
+    const uint32_t tot = c0 + c1 + c2 + c3;
+    const uint32_t incl = wave_inclusive_scan(tot);
+    const uint32_t excl = incl - tot;
+    const uint64_t owner = __ballot(excl < remaining && remaining <= incl);
+    const int b = __ffsll((long long)owner) - 1;  // the one lane holding the boundary
+    rem = remaining - excl;
+    if (rem <= c0) {
+        d = 255 - 4 * l; cnt = c0;
+    } else if (rem <= c0 + c1) {
+        rem -= c0; d = 254 - 4 * l; cnt = c1;
+    } else if (rem <= c0 + c1 + c2) {
+        rem -= c0 + c1; d = 253 - 4 * l; cnt = c2;
+    } else {
+        rem -= c0 + c1 + c2; d = 252 - 4 * l; cnt = c3;
+    }
+    d = wave_bcast(d, b);
+    rem = wave_bcast(rem, b);
+    cnt = wave_bcast(cnt, b);
+}
+
 // Histogram pass of the radix select: counts keys matching `prefix` above
 // bit pos+8 by their digit at `pos`, then finds the digit holding the
 // `remaining`-th best.  `for_each_key(f)` calls f(key) for this lane's
@@ -629,57 +734,57 @@ __device__ __forceinline__ bool radix_pass(ForEach for_each_key, uint32_t *hist,
         if ((key & hi_mask) == want) atomicAdd(&hist[(key >> pos) & 255u], 1u);
     });
     wave_lds_sync();
-    // lane l covers digits 255-4l .. 252-4l, highest first
-    const uint32_t c0 = hist[255 - 4 * l], c1 = hist[254 - 4 * l], c2 = hist[253 - 4 * l],
-                   c3 = hist[252 - 4 * l];
+    uint32_t d, rem, cnt;
+    radix_find(hist, remaining, d, rem, cnt);
     wave_lds_sync();
-    const uint32_t tot = c0 + c1 + c2 + c3;
-    const uint32_t incl = wave_inclusive_scan(tot);
-    const uint32_t excl = incl - tot;
-    const uint64_t owner = __ballot(excl < remaining && remaining <= incl);
-    const int b = __ffsll((long long)owner) - 1;  // the one lane holding the boundary
-    uint32_t rem = remaining - excl, d, cnt;
-    if (rem <= c0) {
-        d = 255 - 4 * l; cnt = c0;
-    } else if (rem <= c0 + c1) {
-        rem -= c0; d = 254 - 4 * l; cnt = c1;
-    } else if (rem <= c0 + c1 + c2) {
-        rem -= c0 + c1; d = 253 - 4 * l; cnt = c2;
-    } else {
-        rem -= c0 + c1 + c2; d = 252 - 4 * l; cnt = c3;
-    }
-    d = wave_bcast(d, b);
-    rem = wave_bcast(rem, b);
-    cnt = wave_bcast(cnt, b);
     prefix |= uint64_t(d) << pos;
     remaining = rem;
     return rem != cnt;
 }
 
-// Selection of one lane by one wave.  Lane l owns the id chunk
-// [l*C, l*C + C), C = ceil(pages/64); CM > 0 holds the chunk's keys in
-// registers (C <= CM), CM == 0 reads them from LDS (`lds`) or from the
-// scores.
-//
 // Threshold search.  After it, with HT = thresh >> shift:
 //   (key >> shift) >  HT            selected
 //   (key >> shift) == HT && bucket  selected (the boundary bucket holds
 //                                   exactly the remaining count)
 //   key == thresh && !bucket        the first/last `remaining` equal keys
 //                                   by id (tie rule), shift == 0
-template <int CM>
+struct Threshold {
+    uint64_t thresh = 0;
+    uint32_t remaining = 0, shift = 0;
+    bool bucket = false;
+    __device__ __forceinline__ int cls(uint64_t key) const {  // 2 taken, 1 tied at the threshold, 0 not
+        const uint64_t hk = key >> shift, ht = thresh >> shift;
+        return (hk > ht || (hk == ht && bucket)) ? 2 : (hk == ht ? 1 : 0);
+    }
+};
+
+// Equal-key ranks [lo, hi) taken by the tie rule among eq_total keys tied at
+// the threshold (in id order).
+__device__ __forceinline__ void tie_window(const SelectArgs &a, uint32_t remaining, uint32_t eq_total, uint32_t &lo,
+                                          uint32_t &hi) {
+    if (a.tie_higher_first) {
+        lo = remaining >= eq_total ? 0u : eq_total - remaining;
+        hi = eq_total;
+    } else {
+        lo = 0;
+        hi = remaining < eq_total ? remaining : eq_total;
+    }
+}
+
+// Selection of one lane by one wave, for up to 16*64 pages.  Lane l owns the
+// id chunk [l*C, l*C + C), C = ceil(pages/64) <= 16, and holds its keys in
+// registers.
 __device__ __forceinline__ void wave_select(const SelectArgs &a, uint32_t lane, bool lds, const double *sc,
                                             uint32_t *hist, const uint32_t *mand_ids) {
+    constexpr int R = 16;
     const uint32_t l = threadIdx.x & 63, n = a.pages;
     const uint32_t C = (n + kWave - 1) / kWave;
     const uint32_t j0 = min(n, l * C), j1 = min(n, j0 + C);
     auto load_key = [&](uint32_t j) -> uint64_t { return lds ? tail_keys[j] : order_key(sc[j]); };
-    const MandatoryCursor mand0(mand_ids, a.n_mandatory, j0);
-    constexpr int R = CM > 0 ? CM : 1;
     uint64_t kr[R];
-    uint32_t cand_bits = 0;  // chunk entries that are candidates (register mode)
-    if (CM > 0) {
-        MandatoryCursor mand = mand0;
+    uint32_t cand_bits = 0;  // chunk entries that are candidates
+    {
+        MandatoryCursor mand(mand_ids, a.n_mandatory, j0);
 #pragma unroll
         for (int c = 0; c < R; ++c) {
             const uint32_t j = j0 + c;
@@ -688,28 +793,19 @@ __device__ __forceinline__ void wave_select(const SelectArgs &a, uint32_t lane, 
             if (in && !mand.at(j)) cand_bits |= 1u << c;
         }
     }
-    // f(key) over this lane's candidates
     auto for_each_key = [&](auto f) {
-        if (CM > 0) {
 #pragma unroll
-            for (int c = 0; c < R; ++c)
-                if (cand_bits >> c & 1u) f(kr[c]);
-        } else {
-            MandatoryCursor mand = mand0;
-            for (uint32_t j = j0; j < j1; ++j)
-                if (!mand.at(j)) f(load_key(j));
-        }
+        for (int c = 0; c < R; ++c)
+            if (cand_bits >> c & 1u) f(kr[c]);
     };
     const uint32_t n_cand = n - a.n_mandatory;
     const uint32_t k_eff = a.k - a.n_mandatory;  // host guarantees n_mandatory <= k
-    uint64_t thresh = 0;
-    uint32_t remaining = 0, shift = 0;
-    bool bucket = false;
+    Threshold t;
     if (k_eff == 0) {
-        thresh = ~0ull;  // nothing ranks
-        bucket = true;
+        t.thresh = ~0ull;  // nothing ranks
+        t.bucket = true;
     } else if (k_eff >= n_cand) {
-        bucket = true;   // every candidate
+        t.bucket = true;   // every candidate
     } else {
         uint64_t and_all = ~0ull, or_all = 0;
         for_each_key([&](uint64_t key) {
@@ -719,58 +815,38 @@ __device__ __forceinline__ void wave_select(const SelectArgs &a, uint32_t lane, 
         and_all = wave_and(and_all);
         or_all = wave_or(or_all);
         const uint64_t diff = and_all ^ or_all;
-        remaining = k_eff;
+        t.remaining = k_eff;
         if (diff == 0) {  // all candidates equal: the tie rule decides
-            thresh = and_all;
+            t.thresh = and_all;
         } else {
             const int top = 63 - __clzll(diff);
             uint64_t prefix = and_all & ~((2ull << top) - 1);  // the common high bits
             for (int pos = top / 8 * 8;; pos -= 8) {
-                if (!radix_pass(for_each_key, hist, pos, prefix, remaining)) {
-                    bucket = true;  // the whole boundary bucket is selected
-                    shift = uint32_t(pos);
+                if (!radix_pass(for_each_key, hist, pos, prefix, t.remaining)) {
+                    t.bucket = true;  // the whole boundary bucket is selected
+                    t.shift = uint32_t(pos);
                     break;
                 }
                 if (pos == 0) break;  // full key: the tie rule picks among equals
             }
-            thresh = prefix;
+            t.thresh = prefix;
         }
     }
 
     // Compaction in id order.
-    const uint64_t ht = thresh >> shift;
-    auto cls = [&](uint64_t key) -> int {  // 2 taken, 1 tied at the threshold, 0 not
-        const uint64_t hk = key >> shift;
-        return (hk > ht || (hk == ht && bucket)) ? 2 : (hk == ht ? 1 : 0);
-    };
     uint32_t n_take = 0, n_eq = 0;
-    if (CM > 0) {
 #pragma unroll
-        for (int c = 0; c < R; ++c) {
-            if (j0 + c >= j1) continue;
-            const int k = (cand_bits >> c & 1u) ? cls(kr[c]) : 2;
-            n_take += k == 2;
-            n_eq += k == 1;
-        }
-    } else {
-        MandatoryCursor mand = mand0;
-        for (uint32_t j = j0; j < j1; ++j) {
-            const int k = mand.at(j) ? 2 : cls(load_key(j));
-            n_take += k == 2;
-            n_eq += k == 1;
-        }
+    for (int c = 0; c < R; ++c) {
+        if (j0 + c >= j1) continue;
+        const int k = (cand_bits >> c & 1u) ? t.cls(kr[c]) : 2;
+        n_take += k == 2;
+        n_eq += k == 1;
     }
     const uint32_t eq_incl = wave_inclusive_scan(n_eq);
     const uint32_t eq_base = eq_incl - n_eq;
     const uint32_t eq_total = wave_bcast(eq_incl, kWave - 1);
-    uint32_t lo, hi;  // equal-key ranks [lo, hi) are taken
-    if (a.tie_higher_first) {
-        lo = remaining >= eq_total ? 0u : eq_total - remaining;
-        hi = eq_total;
-    } else {
-        lo = 0;
-        hi = remaining < eq_total ? remaining : eq_total;
-    }
+    uint32_t lo, hi;
+    tie_window(a, t.remaining, eq_total, lo, hi);
     const uint32_t eq_lo = max(lo, eq_base), eq_hi = min(hi, eq_base + n_eq);
     n_take += eq_hi > eq_lo ? eq_hi - eq_lo : 0u;
     const uint32_t take_incl = wave_inclusive_scan(n_take);
@@ -786,15 +862,161 @@ __device__ __forceinline__ void wave_select(const SelectArgs &a, uint32_t lane, 
         }
         if (take && o < a.k) out[o++] = j;
     };
-    if (CM > 0) {
 #pragma unroll
-        for (int c = 0; c < R; ++c)
-            if (j0 + c < j1) emit(j0 + c, (cand_bits >> c & 1u) ? cls(kr[c]) : 2);
-    } else {
-        MandatoryCursor mand = mand0;
-        for (uint32_t j = j0; j < j1; ++j) emit(j, mand.at(j) ? 2 : cls(load_key(j)));
-    }
+    for (int c = 0; c < R; ++c)
+        if (j0 + c < j1) emit(j0 + c, (cand_bits >> c & 1u) ? t.cls(kr[c]) : 2);
     if (l == 0) a.count[lane] = min(total, a.k);
+}
+
+// Selection of one lane by the whole workgroup (256 threads), for rows
+// longer than 1024 pages: the same threshold search and compaction as
+// wave_select, with thread t owning the id chunk [t*C, t*C + C),
+// C = ceil(pages/256), keys read 8 at a time from LDS or the scores.
+__device__ __forceinline__ void wg_select(const SelectArgs &a, uint32_t lane, bool lds, const double *sc,
+                                          uint32_t *hist, const uint32_t *mand_ids) {
+    constexpr uint32_t B = 256, W = B / kWave;
+    __shared__ uint64_t s_red[2][W];
+    __shared__ uint32_t s_ctl[3];
+    __shared__ uint32_t s_scan[W];
+    const uint32_t tid = threadIdx.x, w = tid / kWave, l = tid % kWave;
+    const uint32_t n = a.pages, C = (n + B - 1) / B;
+    const uint32_t j0 = min(n, tid * C), j1 = min(n, j0 + C);
+    auto load_key = [&](uint32_t j) -> uint64_t { return lds ? tail_keys[j] : order_key(sc[j]); };
+    const MandatoryCursor mand0(mand_ids, a.n_mandatory, j0);
+    // chunks of up to 64 ids (rows up to 16384 pages) keep their mandatory
+    // pages as a bit mask, walked once; longer chunks walk the list per pass
+    const bool masked = C <= 64;
+    uint64_t mand_bits = 0;
+    if (masked && a.n_mandatory) {
+        MandatoryCursor mand = mand0;
+        for (uint32_t j = j0; j < j1; ++j)
+            if (mand.at(j)) mand_bits |= 1ull << (j - j0);
+    }
+    // f(j, key, candidate) over this thread's chunk in id order
+    auto chunk = [&](auto f) {
+        MandatoryCursor mand = mand0;
+        for (uint32_t b = j0; b < j1; b += 8) {
+            uint64_t kk[8];
+#pragma unroll
+            for (uint32_t u = 0; u < 8; ++u) kk[u] = load_key(min(b + u, j1 - 1));
+#pragma unroll
+            for (uint32_t u = 0; u < 8; ++u) {
+                const uint32_t j = b + u;
+                if (j < j1) f(j, kk[u], masked ? !(mand_bits >> (j - j0) & 1ull) : !mand.at(j));
+            }
+        }
+    };
+    // exclusive prefix and total of v over the workgroup in thread order
+    auto scan = [&](uint32_t v, uint32_t &excl, uint32_t &total) {
+        const uint32_t incl = wave_inclusive_scan(v);
+        if (l == kWave - 1) s_scan[w] = incl;
+        lds_barrier();
+        uint32_t before = 0, tot = 0;
+#pragma unroll
+        for (uint32_t i = 0; i < W; ++i) {
+            const uint32_t x = s_scan[i];
+            before += i < w ? x : 0u;
+            tot += x;
+        }
+        lds_barrier();
+        excl = before + incl - v;
+        total = tot;
+    };
+    const uint32_t n_cand = n - a.n_mandatory;
+    const uint32_t k_eff = a.k - a.n_mandatory;
+    Threshold t;
+    if (k_eff == 0) {
+        t.thresh = ~0ull;
+        t.bucket = true;
+    } else if (k_eff >= n_cand) {
+        t.bucket = true;
+    } else {
+        uint64_t and_all = ~0ull, or_all = 0;
+        chunk([&](uint32_t, uint64_t key, bool cand) {
+            if (cand) {
+                and_all &= key;
+                or_all |= key;
+            }
+        });
+        and_all = wave_and(and_all);
+        or_all = wave_or(or_all);
+        if (l == 0) {
+            s_red[0][w] = and_all;
+            s_red[1][w] = or_all;
+        }
+        lds_barrier();
+#pragma unroll
+        for (uint32_t i = 0; i < W; ++i) {
+            and_all &= s_red[0][i];
+            or_all |= s_red[1][i];
+        }
+        const uint64_t diff = and_all ^ or_all;
+        t.remaining = k_eff;
+        if (diff == 0) {
+            t.thresh = and_all;
+        } else {
+            const int top = 63 - __clzll(diff);
+            uint64_t prefix = and_all & ~((2ull << top) - 1);
+            for (int pos = top / 8 * 8;; pos -= 8) {
+                const uint64_t hi_mask = pos + 8 >= 64 ? 0ull : ~0ull << (pos + 8);
+                const uint64_t want = prefix & hi_mask;
+                hist[tid] = 0;
+                lds_barrier();
+                chunk([&](uint32_t, uint64_t key, bool cand) {
+                    if (cand && (key & hi_mask) == want) atomicAdd(&hist[(key >> pos) & 255u], 1u);
+                });
+                lds_barrier();
+                if (w == 0) {
+                    uint32_t d, rem, cnt;
+                    radix_find(hist, t.remaining, d, rem, cnt);
+                    if (l == 0) {
+                        s_ctl[0] = d;
+                        s_ctl[1] = rem;
+                        s_ctl[2] = cnt;
+                    }
+                }
+                lds_barrier();
+                const uint32_t d = s_ctl[0], rem = s_ctl[1], cnt = s_ctl[2];
+                lds_barrier();  // hist and s_ctl are rewritten by the next pass
+                prefix |= uint64_t(d) << pos;
+                t.remaining = rem;
+                if (rem == cnt) {
+                    t.bucket = true;
+                    t.shift = uint32_t(pos);
+                    break;
+                }
+                if (pos == 0) break;
+            }
+            t.thresh = prefix;
+        }
+    }
+
+    uint32_t n_take = 0, n_eq = 0;
+    chunk([&](uint32_t, uint64_t key, bool cand) {
+        const int k = cand ? t.cls(key) : 2;
+        n_take += k == 2;
+        n_eq += k == 1;
+    });
+    uint32_t eq_base, eq_total;
+    scan(n_eq, eq_base, eq_total);
+    uint32_t lo, hi;
+    tie_window(a, t.remaining, eq_total, lo, hi);
+    const uint32_t eq_lo = max(lo, eq_base), eq_hi = min(hi, eq_base + n_eq);
+    n_take += eq_hi > eq_lo ? eq_hi - eq_lo : 0u;
+    uint32_t o, total;
+    scan(n_take, o, total);
+    uint32_t rank = eq_base;
+    uint32_t *out = a.selected + uint64_t(lane) * a.k;
+    chunk([&](uint32_t j, uint64_t key, bool cand) {
+        const int k = cand ? t.cls(key) : 2;
+        bool take = k == 2;
+        if (k == 1) {
+            take = rank >= lo && rank < hi;
+            ++rank;
+        }
+        if (take && o < a.k) out[o++] = j;
+    });
+    if (tid == 0) a.count[lane] = min(total, a.k);
 }
 
 // Aggregation (optional) by the whole workgroup, then selection by its
@@ -807,7 +1029,7 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
     const bool lds = n <= kTailLdsPages;
     double *sc = a.scores + uint64_t(lane) * n;
     // the status of this call, read early so its latency overlaps the sums
-    const bool failed = a.do_select && tid < kWave && epoch_failed(a.status, a.epoch);
+    bool failed = a.do_select && tid < kWave && epoch_failed(a.status, a.epoch);
 
     int bad = 0;
     auto note = [&](uint32_t j, double v) {
@@ -828,6 +1050,7 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
         for (uint32_t j0 = tid; j0 < n; j0 += 2 * B) {
             const uint32_t j1 = j0 + B;
             const bool has1 = j1 < n;
+            const uint32_t j1c = has1 ? j1 : j0;  // loads stay unconditional; acc1 is dropped when !has1
             double acc0 = a.accumulate ? sc[j0] : 0.0;
             double acc1 = has1 && a.accumulate ? sc[j1] : 0.0;
             uint32_t i = 0;
@@ -837,10 +1060,24 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
                 for (int u = 0; u < 32; ++u) {
                     const uint64_t o = row_of(i + u) * n;
                     v0[u] = load_device(terms + o + j0);
-                    v1[u] = has1 ? load_device(terms + o + j1) : 0.0;
+                    v1[u] = load_device(terms + o + j1c);
                 }
 #pragma unroll
                 for (int u = 0; u < 32; ++u) {
+                    acc0 += v0[u];
+                    acc1 += v1[u];
+                }
+            }
+            for (; i + 16 <= nrows; i += 16) {
+                double v0[16], v1[16];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) {
+                    const uint64_t o = row_of(i + u) * n;
+                    v0[u] = load_device(terms + o + j0);
+                    v1[u] = load_device(terms + o + j1c);
+                }
+#pragma unroll
+                for (int u = 0; u < 16; ++u) {
                     acc0 += v0[u];
                     acc1 += v1[u];
                 }
@@ -851,7 +1088,7 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
                 for (int u = 0; u < 8; ++u) {
                     const uint64_t o = row_of(i + u) * n;
                     v0[u] = load_device(terms + o + j0);
-                    v1[u] = has1 ? load_device(terms + o + j1) : 0.0;
+                    v1[u] = load_device(terms + o + j1c);
                 }
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
@@ -877,16 +1114,22 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
     if (!a.do_select) return;
     // Reject invalid scores (pick_scored_blocks, kvmem_store.cpp:425-426).
     bad = __syncthreads_or(bad);  // also publishes the LDS keys
-    if (tid >= kWave) return;
+    const bool wide = n > 16 * kWave;
+    if (wide) failed = __syncthreads_or(failed);
+    else if (tid >= kWave) return;
     if (bad && tid == 0) raise_status(a.status, kStatusScores, a.epoch);
     if (bad || failed) {
         if (tid == 0) a.count[lane] = 0;
         return;
     }
     if (tid < a.n_mandatory) mand_ids[tid] = a.mandatory[tid];
-    wave_lds_sync();
-    if (n <= 16 * kWave) wave_select<16>(a, lane, lds, sc, hist, mand_ids);
-    else wave_select<0>(a, lane, lds, sc, hist, mand_ids);
+    if (wide) {
+        lds_barrier();
+        wg_select(a, lane, lds, sc, hist, mand_ids);
+    } else {
+        wave_lds_sync();
+        wave_select(a, lane, lds, sc, hist, mand_ids);
+    }
 }
 
 // Softmax units -> terms; the lane's last workgroup aggregates (+ selects).
@@ -896,7 +1139,7 @@ template <int NPL>
 __device__ __forceinline__ void probs_block(const SelectArgs &a, uint32_t unit_block, uint32_t lane,
                                             uint32_t blocks_per_lane) {
     __shared__ uint32_t s_last;
-    const uint32_t unit = unit_block * kUnitsPerBlock + (threadIdx.x >> 6);
+    const uint32_t unit = NPL > 0 ? unit_block * kUnitsPerBlock + (threadIdx.x >> 6) : unit_block;
     double *lane_base = a.logits + uint64_t(lane) * a.rows * a.qheads * a.pages;
     if (unit < a.units) {
         if (NPL > 0)
@@ -935,7 +1178,8 @@ __global__ __launch_bounds__(256) void k_summary_probs(SummaryArgs s, SelectArgs
     if (blockIdx.x >= summary_blocks) {
         // default wave priority: below the summary's streaming waves on a
         // shared CU; these have the whole summary launch to finish in
-        const uint32_t per_lane = (p.units + kUnitsPerBlock - 1) / kUnitsPerBlock;
+        const uint32_t upb = NPL > 0 ? kUnitsPerBlock : 1;
+        const uint32_t per_lane = (p.units + upb - 1) / upb;
         const uint32_t b = blockIdx.x - summary_blocks;
         probs_block<NPL>(p, b % per_lane, b / per_lane, per_lane);
         return;
@@ -1256,7 +1500,8 @@ hipError_t launch_logits_mfma(const MfmaLogitsArgs &a, hipStream_t s) {
 
 hipError_t launch_probs(const SelectArgs &a, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch\'s error
-    const dim3 grid((a.units + kUnitsPerBlock - 1) / kUnitsPerBlock, a.lanes), block(kUnitsPerBlock * kWave);
+    const uint32_t upb = units_per_block(a.pages);
+    const dim3 grid((a.units + upb - 1) / upb, a.lanes), block(256);
     const size_t lds = a.pages <= kTailLdsPages ? size_t(a.pages) * 8 : 0;
     if (a.pages <= 64) hipLaunchKernelGGL(k_probs<1>, grid, block, lds, s, a);
     else if (a.pages <= 128) hipLaunchKernelGGL(k_probs<2>, grid, block, lds, s, a);
@@ -1269,7 +1514,8 @@ hipError_t launch_probs(const SelectArgs &a, hipStream_t s) {
 
 hipError_t launch_summary_probs(int source, const SummaryArgs &sa, const SelectArgs &pa, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch\'s error
-    const uint32_t per_lane = (pa.units + kUnitsPerBlock - 1) / kUnitsPerBlock;
+    const uint32_t upb = units_per_block(pa.pages);
+    const uint32_t per_lane = (pa.units + upb - 1) / upb;
     const uint32_t probs_blocks = per_lane * pa.lanes;
     const uint64_t threads = uint64_t(sa.lanes) * sa.pages * (sa.width >> 3);
     const uint32_t summary_blocks = blocks_for(threads);

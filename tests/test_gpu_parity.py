@@ -267,6 +267,29 @@ def test_select_matches_oracle(ctx, tie):
             assert np.array_equal(sel[0, :cnt[0]], expect)
 
 
+@pytest.mark.parametrize("tie", [K.TIE_LOWER_FIRST, K.TIE_HIGHER_FIRST])
+def test_select_long_rows_edges(ctx, tie):
+    """Rows over 1024 pages (workgroup selection) at the LDS and mandatory-mask
+    boundaries, all-equal scores, a budget taken whole by mandatory pages,
+    and a budget above the candidate count."""
+    rng = np.random.default_rng(SEED + 1)
+    mand20 = lambda pages: tuple(sorted(set(rng.choice(pages, 20, replace=False).tolist())))
+    for pages in (1025, 8192, 8193, 16384, 16385):
+        scores = np.round(rng.random(pages), 3)  # ~1000 distinct values: heavy ties
+        for k, mand in ((64, ()), (64, mand20(pages)), (20, mand20(pages)), (pages - 3, (0, 1))):
+            st, sel, cnt = _select(ctx, scores, k, mandatory=mand, tie=tie)
+            assert st == 0
+            expect = O.pick_scored_blocks(scores, k, mand, tie)
+            assert cnt[0] == expect.size, (pages, k, len(mand))
+            assert np.array_equal(sel[0, :cnt[0]], expect), (pages, k, len(mand))
+    for pages in (3000, 20000):
+        flat = np.full(pages, 0.25)
+        for k, mand in ((50, ()), (50, (7, pages - 1))):
+            st, sel, cnt = _select(ctx, flat, k, mandatory=mand, tie=tie)
+            assert st == 0
+            assert np.array_equal(sel[0, :cnt[0]], O.pick_scored_blocks(flat, k, mand, tie))
+
+
 def test_select_reference_tie_rule(ctx):
     """layerwise_selection_test.cpp:184-194: equal mass over six pages with a
     budget of two keeps {4, 5} under the reference (higher id first) rule."""
