@@ -159,6 +159,8 @@ kvr::QueryArgs query_args(const kvr_query *q) {
     a.scale = logit_scale(q->attention_scale, q->head_dim);
     const uint64_t esz = a.scalar == kvr::kScalarF32 ? 4 : 2;
     a.dense = a.dim_stride == esz && a.head_stride == esz * a.dim && a.row_stride == esz * a.dim * a.qheads;
+    a.packed16 = a.dense && a.scalar == kvr::kScalarF16 && reinterpret_cast<uintptr_t>(a.data) % 16 == 0 &&
+                 a.lane_stride % 16 == 0 && (uint64_t(a.rows) * a.qheads * a.dim) % 8 == 0;
     return a;
 }
 

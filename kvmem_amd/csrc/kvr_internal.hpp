@@ -21,6 +21,7 @@ struct QueryArgs {
     uint64_t row_stride, head_stride, dim_stride, lane_stride;  // bytes
     double scale;
     uint32_t dense;  // (row, head, dim) packed: element i sits at i * element size
+    uint32_t packed16;  // dense fp16 with 16-byte aligned lanes: loadable 8 elements at a time
 };
 
 // Page summaries of `lanes` histories, optionally fused with the logits of

@@ -136,16 +136,27 @@ __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t blo
     // LDS.  The first kQueryPrefetch elements per thread are loaded here,
     // ahead of the key stream, and reach LDS after it, so neither the stream
     // nor the epilogue waits on a query round trip.
-    constexpr uint32_t kQueryPrefetch = 16;
+    // Packed fp16 rows of up to 4096 elements take two 16-byte loads per
+    // thread (qvec); other queries kQueryPrefetch single elements (qraw).
+    constexpr uint32_t kQueryPrefetch = 16, kQueryVec = 2;
     uint32_t qraw[kQueryPrefetch];
+    u32x4 qvec[kQueryVec];
     uint32_t staged_lane = 0xffffffffu, nq = 0;
+    bool qv = false;
     if (FUSE && a.q_stage) {
         staged_lane = uint32_t((uint64_t(block) * 256 / gpp) / a.pages);
         nq = a.q.rows * a.q.qheads * a.q.dim;
+        qv = a.q.packed16 && nq <= 256 * 8 * kQueryVec;
+        if (qv) {
+            const u32x4 *qp = reinterpret_cast<const u32x4 *>(a.q.data + staged_lane * a.q.lane_stride);
 #pragma unroll
-        for (uint32_t j = 0; j < kQueryPrefetch; ++j) {
-            const uint32_t i = min(threadIdx.x + 256 * j, nq - 1);  // in bounds; extras unused
-            qraw[j] = load_raw(query_elem(a.q, staged_lane, i), a.q.scalar);
+            for (uint32_t j = 0; j < kQueryVec; ++j) qvec[j] = qp[min(threadIdx.x + 256 * j, nq / 8 - 1)];
+        } else {
+#pragma unroll
+            for (uint32_t j = 0; j < kQueryPrefetch; ++j) {
+                const uint32_t i = min(threadIdx.x + 256 * j, nq - 1);  // in bounds; extras unused
+                qraw[j] = load_raw(query_elem(a.q, staged_lane, i), a.q.scalar);
+            }
         }
     }
 
@@ -208,7 +219,23 @@ __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t blo
 
     // The staged query reaches LDS before this thread stores anything: a
     // wait for its loads placed after a store would also wait for the store.
-    if (FUSE && a.q_stage) {
+    if (FUSE && a.q_stage && qv) {
+        // a finite fp16 value passes the recall boundary unchanged
+        uint32_t qbad = kOperandOk;
+#pragma unroll
+        for (uint32_t j = 0; j < kQueryVec; ++j) {
+            const uint32_t i8 = threadIdx.x + 256 * j;
+            if (i8 < nq / 8) {
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const uint32_t e = qvec[j][w] & 0x7c007c00u;
+                    if ((e & 0xffffu) == 0x7c00u || (e >> 16) == 0x7c00u) qbad = kOperandNonfinite;
+                }
+                *reinterpret_cast<u32x4 *>(q_lds + 8 * i8) = qvec[j];
+            }
+        }
+        if (qbad) raise_operand(a.status, qbad, a.epoch);
+    } else if (FUSE && a.q_stage) {
         const QueryArgs &q = a.q;
         {
             uint32_t qbad = kOperandOk;
