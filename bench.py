@@ -108,6 +108,7 @@ def run(args):
         c.set_option(K._capi.OPT_GATHER_THREADS, args.gather_threads)
     ctx = ctxs[0]
     L, T, HKV, D, HQ, PT, KSEL, R = args.layers, 131072, 8, 128, 32, 256, 32, 1
+    G = K._capi.STACK_GROUP  # layers per stack launch
     W = HKV * D
     P = T // PT
     geo = dict(L=L, T=T, HKV=HKV, D=D, HQ=HQ, PT=PT, K=KSEL)
@@ -161,8 +162,8 @@ def run(args):
 
     # Every event recorded between two kernels of the select stream costs a
     # few microseconds of stream time, so per-layer events go on a sample of
-    # layers (every 8th, plus the first and last for the stack's span).
-    sampled = sorted(set(range(3, L, 8)) | {0, L - 1})
+    # layers (three inside the stack, plus the first and last for its span).
+    sampled = sorted({0, L // 4, L // 2, 3 * L // 4, L - 1})
 
     def events():
         return {n: {l: hip.event() for l in sampled} for n in ("kb", "ke", "se")}
@@ -221,7 +222,7 @@ def run(args):
     select_us = float(np.mean(sel_us))
     stack_gpu_us = float(np.mean(stack_us))
     log(f"select stack {ms_per_step:.3f} ms/step ({ms_per_step / L * 1e3:.1f} us/layer; GPU "
-        f"{stack_gpu_us / L:.1f} us/layer); per layer: summary kernel {kern_us_mean:.1f} us, "
+        f"{stack_gpu_us / L:.1f} us/layer); stack launch ({G} layers) {kern_us_mean:.1f} us, "
         f"summary start -> selection {select_us:.1f} us")
 
     # ---- pipelined recall: each layer's stage-in beside the next selects ---
@@ -236,7 +237,7 @@ def run(args):
     pipe_us = (p1 - p0) * 1e6 / L
     pk, ps, _ = layer_times(ev_p)
     pipe_kern_us, pipe_sel_us = float(np.mean(pk)), float(np.mean(ps))
-    log(f"select+stage-in pipelined {pipe_us:.1f} us/layer; beside the stage-in: summary kernel "
+    log(f"select+stage-in pipelined {pipe_us:.1f} us/layer; beside the stage-in: stack launch "
         f"{pipe_kern_us:.1f} us, summary start -> selection {pipe_sel_us:.1f} us")
 
     # ---- stage-in alone (same selections, copy stream) ---------------------
@@ -258,11 +259,11 @@ def run(args):
     gpu_sel = sel.cpu().numpy().view(np.uint32)
     assert (cnt.cpu().numpy() == KSEL).all(), "every layer must select k pages"
 
-    # one stack launch: this layer's K read, fp16 summaries and logits
-    # written, Q read; the previous layer's logits read, terms written and
-    # read back, scores written
+    # one stack launch, per layer of its group: the layer's K read, fp16
+    # summaries and logits written, Q read; per layer of the previous group:
+    # logits read, terms written and read back, scores written
     logit_bytes = HQ * R * P * 8
-    alg_kernel_bytes = k_bytes + P * W * 2 + logit_bytes + HQ * D * 2 + 3 * logit_bytes + P * 8
+    alg_kernel_bytes = G * (k_bytes + P * W * 2 + logit_bytes + HQ * D * 2 + 3 * logit_bytes + P * 8)
     achieved = alg_kernel_bytes / (kern_us_mean * 1e-6) / 1e9
     scored_gbps = L * geo["scored_bytes"] / (ms_per_step * 1e-3) / 1e9
     traffic = None
@@ -308,7 +309,8 @@ def run(args):
         "stagein_frac_h2d": round(stage_gbps / h2d, 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": "k_summary_probs<f16> (layer l summaries + fused logits, layer l-1 softmax/top-k)",
+            "kernel": f"k_stack_group<f16> ({G} layers' summaries + fused logits, the previous {G} layers' "
+                      "softmax/top-k)",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
@@ -327,11 +329,12 @@ def run(args):
 
 
 def pmc_pass(args):
-    """Counter pass (run under rocprofv3 --pmc): a 4-layer stack over one
-    128K-token layer (k_summary, then three k_summary_probs launches over
-    256 MiB of fp16 K each, then k_probs) and three 256 MiB device copies
-    (4096 ops of 64 KiB, k_copy_ops) that calibrate FETCH_SIZE / WRITE_SIZE
-    against known byte counts."""
+    """Counter pass (run under rocprofv3 --pmc): a stack of three launch
+    groups over one 128K-token layer (k_stack_group: the first group's
+    summaries alone, then the second group's beside the first group's
+    selections, then the second group's selections alone) and three 256 MiB
+    device copies (4096 ops of 64 KiB, k_copy_ops) that calibrate
+    FETCH_SIZE / WRITE_SIZE against known byte counts."""
     import torch
     import kvmem_amd as K
     T, HKV, D, HQ, PT, KSEL = 131072, 8, 128, 32, 256, 32
@@ -352,8 +355,8 @@ def pmc_pass(args):
     query = K.make_query(qd, K.FMT_F16, 1, HQ, HKV, D)
     desc = K.Context.layer_recall(keys=keys, summaries=s16, query=query, scores=scores, selected=sel, count=cnt,
                                   k=KSEL, aggregation=K.AGG_MEAN)
-    # a 4-layer stack over the same layer: launches 2..4 are k_summary_probs
-    keep = ctx.recall_stack([desc] * 4)
+    # two full groups over the same layer: the middle launch is the steady state
+    keep = ctx.recall_stack([desc] * (2 * K._capi.STACK_GROUP))
     ctx.check()
     del keep
     op = 1 << 16

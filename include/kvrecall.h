@@ -46,6 +46,8 @@ extern "C" {
 #define KVR_VERSION_MINOR 1
 #define KVR_MAX_INLINE_MANDATORY 64
 #define KVR_MAX_PLANES 8
+/* Layers whose summaries share one launch in kvr_recall_stack. */
+#define KVR_STACK_GROUP 4
 
 typedef struct kvr_context kvr_context;
 
@@ -297,13 +299,16 @@ kvr_status kvr_recall_layer(kvr_context *ctx, const kvr_layer_recall *desc,
 
 /* n layers of recall in order, with results identical to n kvr_recall_layer
  * calls.  When every layer takes the fused vector scoring path with one
- * geometry, layer l's softmax and selection run inside layer l+1's summary
- * launch (the context then keeps two logits buffers), so each layer's
- * selection, select_end event and stage-in follow the next layer's launch;
- * a layer's summary events bracket that shared launch.  Otherwise the layers
- * run one after another.  Replaces one select_layerwise_history call per
- * attention layer (kvmem/src/host/layerwise_selection.cpp:185-199), each
- * followed by that layer's stage-in. */
+ * geometry, the layers go in groups of up to KVR_STACK_GROUP consecutive
+ * layers with one summary source, one launch per group: group g's summaries
+ * run beside group g-1's softmax units and selections (the context then
+ * keeps 2*KVR_STACK_GROUP logits buffers: a borrowed workspace needs
+ * 2*KVR_STACK_GROUP times kvr_workspace_bytes of one layer).  Each layer's selection, select_end event
+ * and stage-in therefore follow the next group's launch, and a layer's
+ * summary events bracket its group's launch.  Otherwise the layers run one
+ * after another.  Replaces one select_layerwise_history call per attention
+ * layer (kvmem/src/host/layerwise_selection.cpp:185-199), each followed by
+ * that layer's stage-in. */
 kvr_status kvr_recall_stack(kvr_context *ctx, const kvr_layer_recall *layers, uint32_t n,
                             void *select_stream, void *copy_stream);
 

@@ -24,6 +24,7 @@ ENGINE_AUTO, ENGINE_KERNEL, ENGINE_SDMA = range(3)
 OPT_GATHER_WORKGROUPS, OPT_GATHER_CHUNK_ROWS, OPT_GATHER_THREADS = 1, 2, 3
 MAX_INLINE_MANDATORY = 64
 MAX_PLANES = 8
+STACK_GROUP = 4
 
 _P = C.c_void_p
 _u32, _u64, _sz, _i = C.c_uint32, C.c_uint64, C.c_size_t, C.c_int

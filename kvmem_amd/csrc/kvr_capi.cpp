@@ -218,6 +218,7 @@ size_t qpack_bytes(uint32_t lanes, uint32_t rows, uint32_t qheads, uint32_t dim)
 }
 
 static_assert(kvr::kMaxMandatory == KVR_MAX_INLINE_MANDATORY, "inline mandatory capacity");
+static_assert(kvr::kStackGroup == KVR_STACK_GROUP, "layers per stack launch");
 
 struct Mandatory {
     uint32_t n = 0;
@@ -1035,39 +1036,60 @@ kvr_status kvr_recall_stack(kvr_context *ctx, const kvr_layer_recall *layers, ui
         return KVR_OK;
     }
     if (p0.lanes > 65535) return fail(KVR_ERR_INVALID, "at most 65535 lanes per call");
-    // two logits buffers and two counter sets, alternating between layers
+    // Launches take groups of up to kStackGroup consecutive layers with one
+    // summary source.  Group k's summaries run beside group k-1's softmax
+    // units and selections, so two groups' logits buffers and counter sets
+    // are live at once: 2 * kStackGroup of each, alternating by group.
+    constexpr uint32_t G = kvr::kStackGroup;
     const size_t lb = logits_bytes(p0.lanes, p0.pages, p0.rows, p0.qheads);
-    if (kvr_status s = ensure_workspace(ctx, 2 * lb, ss)) return s;
-    if (kvr_status s = ensure_counters(ctx, 2 * p0.lanes, ss)) return s;
-    double *logits[2] = {reinterpret_cast<double *>(ctx->ws), reinterpret_cast<double *>(ctx->ws + lb)};
-    kvr::SelectArgs prev{};
-    for (uint32_t l = 0; l <= n; ++l) {
-        kvr::SelectArgs cur{};
-        if (l < n) {
-            LayerPlan &L = plans[l];
+    if (kvr_status s = ensure_workspace(ctx, 2 * G * lb, ss)) return s;
+    if (kvr_status s = ensure_counters(ctx, 2 * G * p0.lanes, ss)) return s;
+    std::vector<uint32_t> first;  // first layer of each group
+    for (uint32_t l = 0; l < n; ++l)
+        if (first.empty() || l - first.back() == G || plans[l].src != plans[first.back()].src) first.push_back(l);
+    const uint32_t groups = uint32_t(first.size());
+    first.push_back(n);
+    const uint32_t nq = p0.rows * p0.qheads * p0.dim;
+    kvr::StackGroupArgs g{};
+    // enough softmax workgroups per lane for the most units an aggregation
+    // has (rows * q-heads); workgroups past a layer's units only count in
+    const uint32_t upb = kvr::units_per_block(p0.pages);
+    g.probs_per_lane = (p0.rows * p0.qheads + upb - 1) / upb;
+    g.q_slot = (nq + 7) / 8 * 8;
+    int prev_src = plans[0].src;
+    for (uint32_t k = 0; k <= groups; ++k) {
+        // the previous group's selections ride in this launch
+        g.mp = g.m;  // g.p holds that group's selections from the previous pass
+        g.m = k < groups ? first[k + 1] - first[k] : 0;
+        kvr::SelectArgs cur[G];
+        const uint32_t set = (k & 1) * G;
+        for (uint32_t i = 0; i < g.m; ++i) {
+            LayerPlan &L = plans[first[k] + i];
             const kvr_layer_recall *d = L.d;
             ++ctx->epoch;
-            L.p.logits = logits[l & 1];
+            L.p.logits = reinterpret_cast<double *>(ctx->ws + (set + i) * lb);
             kvr::SummaryArgs a = d->keys ? summary_args(ctx, d->keys, L.pages, L.key_ls, d->means, d->summaries)
                                          : resident_args(ctx, L.p, d->summaries);
             a.q = L.p.q;
             a.q_stage = stage_query(L.p.q);
             a.logits = L.p.logits;
-            cur = make_select_args(ctx, L.p, d->score_mask, d->aggregation, 1, 0, d->scores, true, d->k, d->tie_rule,
-                                   L.m, d->selected, d->count);
-            cur.counters = ctx->counters + (l & 1) * p0.lanes;
+            g.s[i] = a;
+            cur[i] = make_select_args(ctx, L.p, d->score_mask, d->aggregation, 1, 0, d->scores, true, d->k,
+                                      d->tie_rule, L.m, d->selected, d->count);
+            cur[i].counters = ctx->counters + (set + i) * p0.lanes;
             if (d->summary_begin) KVR_HIP(hipEventRecord(static_cast<hipEvent_t>(d->summary_begin), ss));
-            if (l == 0)
-                KVR_HIP(kvr::launch_summary(L.src, true, a, ss));
-            else
-                KVR_HIP(kvr::launch_summary_probs(L.src, a, prev, ss));
-            if (d->summary_end) KVR_HIP(hipEventRecord(static_cast<hipEvent_t>(d->summary_end), ss));
-        } else {
-            KVR_HIP(kvr::launch_probs(prev, ss));
         }
-        if (l > 0)
-            if (kvr_status s = enqueue_stage(ctx, plans[l - 1], ss, cs)) return s;
-        prev = cur;
+        const int src = g.m ? plans[first[k]].src : prev_src;
+        KVR_HIP(kvr::launch_stack_group(src, g, ss));
+        for (uint32_t i = 0; i < g.m; ++i) {
+            const kvr_layer_recall *d = plans[first[k] + i].d;
+            if (d->summary_end) KVR_HIP(hipEventRecord(static_cast<hipEvent_t>(d->summary_end), ss));
+        }
+        if (k > 0)
+            for (uint32_t l = first[k - 1]; l < first[k]; ++l)
+                if (kvr_status s = enqueue_stage(ctx, plans[l], ss, cs)) return s;
+        for (uint32_t i = 0; i < g.m; ++i) g.p[i] = cur[i];
+        prev_src = src;
     }
     return KVR_OK;
 }

@@ -86,6 +86,23 @@ struct SelectArgs {
     uint32_t epoch;
 };
 
+// Softmax units per 256-thread workgroup: one per wave for rows held in
+// registers (up to 1024 pages), the whole workgroup for longer rows.
+constexpr uint32_t kUnitsPerBlock = 4;
+__host__ __device__ constexpr uint32_t units_per_block(uint32_t pages) { return pages <= 1024 ? kUnitsPerBlock : 1; }
+
+// One launch of a layer stack (k_stack_group): the summaries of m layers
+// and the softmax units and selections of the previous group's mp layers.
+constexpr uint32_t kStackGroup = 4;
+struct StackGroupArgs {
+    SummaryArgs s[kStackGroup];
+    SelectArgs p[kStackGroup];
+    uint32_t m, mp;
+    uint32_t summary_blocks;  // workgroups of one layer's summaries
+    uint32_t probs_per_lane;  // softmax workgroups per lane and layer
+    uint32_t q_slot;          // elements of one LDS query staging buffer (multiple of 8)
+};
+
 struct GatherPlane {
     const uint8_t *src;   // device-visible pinned (or device staging) base
     uint8_t *dst;
@@ -149,7 +166,7 @@ hipError_t launch_probs(const SelectArgs &a, hipStream_t s);
 hipError_t launch_select(const SelectArgs &a, hipStream_t s);
 // one stack launch: `pa`'s softmax/selection beside `sa`'s summaries with
 // fused logits (sa.q and sa.logits set)
-hipError_t launch_summary_probs(int source, const SummaryArgs &sa, const SelectArgs &pa, hipStream_t s);
+hipError_t launch_stack_group(int source, StackGroupArgs g, hipStream_t s);
 hipError_t launch_gather(const GatherArgs &a, hipStream_t s);
 hipError_t launch_accumulate(const AccumulateArgs &a, hipStream_t s);
 hipError_t launch_finalize(const FinalizeArgs &a, hipStream_t s);

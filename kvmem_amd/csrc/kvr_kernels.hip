@@ -109,11 +109,11 @@ __device__ __forceinline__ void stream_rows(uint32_t n, Load load, Use use) {
 // ---------------------------------------------------------------------------
 // FUSE with q_stage: the workgroup's first lane's query rows, already
 // through the fp16 operand boundary, staged once in dynamic LDS.
-extern __shared__ __align__(16) uint16_t q_lds[];
+extern __shared__ __align__(16) uint16_t q_lds_buf[];
 
 // One 256-thread block of the summary grid (`block` = its index in it).
 template <int SRC, bool FUSE>
-__device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t block) {
+__device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t block, uint16_t *q_lds) {
     // Above the stage-in gather's waves when both share a CU: this kernel
     // is on the select critical path, the gather is bound by the host link.
     __builtin_amdgcn_s_setprio(2);
@@ -344,7 +344,7 @@ __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t blo
 
 template <int SRC, bool FUSE>
 __global__ __launch_bounds__(256) void k_summary(SummaryArgs a) {
-    summary_block<SRC, FUSE>(a, blockIdx.x);
+    summary_block<SRC, FUSE>(a, blockIdx.x, q_lds_buf);
 }
 
 // ---------------------------------------------------------------------------
@@ -438,10 +438,7 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_wave_barrier();
 }
 
-// Softmax units per 256-thread workgroup: one per wave for rows held in
-// registers (up to 1024 pages), the whole workgroup for longer rows.
-constexpr uint32_t kUnitsPerBlock = 4;
-__host__ __device__ constexpr uint32_t units_per_block(uint32_t pages) { return pages <= 1024 ? kUnitsPerBlock : 1; }
+
 constexpr uint32_t kTailLdsPages = 8192;  // keys of up to this many pages stay in LDS
 
 // Registers: value i of a lane is page j = l + 64*i.
@@ -1195,23 +1192,24 @@ __global__ __launch_bounds__(256) void k_probs(SelectArgs a) {
     probs_block<NPL>(a, blockIdx.x, blockIdx.y, gridDim.x);
 }
 
-// One launch of a layer stack: this layer's summary blocks with fused
-// logits (blocks [0, summary_blocks), laid out as in k_summary), then the
-// previous layer's softmax units and selection (lane-major).  The two share
-// no memory: the logits buffers and counters alternate between consecutive
-// layers.
+// One launch of a layer stack: the summary workgroups of a group of up to
+// kStackGroup consecutive layers (blocks [0, summary_blocks); each walks the
+// group's layers in order with the layout of k_summary), then the previous
+// group's softmax units and selections (layer-major, then lane-major).  The
+// query staging alternates between two LDS buffers, so a layer's staging
+// never overwrites rows the previous layer's epilogue may still read.
 template <int SRC, int NPL>
-__global__ __launch_bounds__(256) void k_summary_probs(SummaryArgs s, SelectArgs p, uint32_t summary_blocks) {
-    if (blockIdx.x >= summary_blocks) {
+__global__ __launch_bounds__(256) void k_stack_group(StackGroupArgs g) {
+    const uint32_t sb = g.m ? g.summary_blocks : 0;
+    if (blockIdx.x >= sb) {
         // default wave priority: below the summary's streaming waves on a
-        // shared CU; these have the whole summary launch to finish in
-        const uint32_t upb = NPL > 0 ? kUnitsPerBlock : 1;
-        const uint32_t per_lane = (p.units + upb - 1) / upb;
-        const uint32_t b = blockIdx.x - summary_blocks;
-        probs_block<NPL>(p, b % per_lane, b / per_lane, per_lane);
+        // shared CU; these have the whole launch to finish in
+        const uint32_t per_layer = g.probs_per_lane * g.p[0].lanes;
+        const uint32_t b = blockIdx.x - sb, i = b / per_layer, r = b % per_layer;
+        probs_block<NPL>(g.p[i], r % g.probs_per_lane, r / g.probs_per_lane, g.probs_per_lane);
         return;
     }
-    summary_block<SRC, true>(s, blockIdx.x);
+    for (uint32_t i = 0; i < g.m; ++i) summary_block<SRC, true>(g.s[i], blockIdx.x, q_lds_buf + (i & 1) * g.q_slot);
 }
 
 // Selection over given scores (no softmax), one workgroup per lane.
@@ -1497,7 +1495,7 @@ hipError_t launch_summary(int source, bool fuse, const SummaryArgs &a, hipStream
     (void)hipGetLastError();  // report only this launch\'s error
     const uint64_t threads = uint64_t(a.lanes) * a.pages * (a.width >> 3);
     const dim3 grid(blocks_for(threads)), block(256);
-    const size_t lds = fuse && a.q_stage ? size_t(a.q.rows) * a.q.qheads * a.q.dim * 2 : 0;
+    const size_t lds = fuse && a.q_stage ? size_t(a.q.rows) * a.q.qheads * a.q.dim * 2 : 0;  // q_lds_buf
     if (source == kSrcKeysF16 && fuse)
         hipLaunchKernelGGL((k_summary<kSrcKeysF16, true>), grid, block, lds, s, a);
     else if (source == kSrcKeysF16)
@@ -1539,31 +1537,32 @@ hipError_t launch_probs(const SelectArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_summary_probs(int source, const SummaryArgs &sa, const SelectArgs &pa, hipStream_t s) {
+hipError_t launch_stack_group(int source, StackGroupArgs g, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch\'s error
-    const uint32_t upb = units_per_block(pa.pages);
-    const uint32_t per_lane = (pa.units + upb - 1) / upb;
-    const uint32_t probs_blocks = per_lane * pa.lanes;
-    const uint64_t threads = uint64_t(sa.lanes) * sa.pages * (sa.width >> 3);
-    const uint32_t summary_blocks = blocks_for(threads);
-    const dim3 grid(unsigned(summary_blocks + probs_blocks)), block(256);
-    const size_t q_lds_bytes = sa.q_stage ? size_t(sa.q.rows) * sa.q.qheads * sa.q.dim * 2 : 0;
-    const size_t keys = pa.pages <= kTailLdsPages ? size_t(pa.pages) * 8 : 0;
+    const SummaryArgs &sa = g.s[0];
+    const SelectArgs &pa = g.p[0];
+    g.summary_blocks = g.m ? blocks_for(uint64_t(sa.lanes) * sa.pages * (sa.width >> 3)) : 0;
+    const uint32_t sb = g.summary_blocks;
+    const uint32_t probs_blocks = g.mp ? g.mp * g.probs_per_lane * pa.lanes : 0;
+    const dim3 grid(unsigned(sb + probs_blocks)), block(256);
+    const size_t q_lds_bytes = g.m && sa.q_stage ? size_t(2) * g.q_slot * 2 : 0;
+    const size_t keys = g.mp && pa.pages <= kTailLdsPages ? size_t(pa.pages) * 8 : 0;
     const size_t lds = q_lds_bytes > keys ? q_lds_bytes : keys;
-    auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, lds, s, sa, pa, summary_blocks); };
+    const uint32_t pages = g.mp ? pa.pages : sa.pages;
+    auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, lds, s, g); };
     const bool f16 = source == kSrcKeysF16, q8 = source == kSrcKeysQ8;
-    if (pa.pages <= 256) {
-        if (f16) go(k_summary_probs<kSrcKeysF16, 4>); else if (q8) go(k_summary_probs<kSrcKeysQ8, 4>);
-        else go(k_summary_probs<kSrcSummary, 4>);
-    } else if (pa.pages <= 512) {
-        if (f16) go(k_summary_probs<kSrcKeysF16, 8>); else if (q8) go(k_summary_probs<kSrcKeysQ8, 8>);
-        else go(k_summary_probs<kSrcSummary, 8>);
-    } else if (pa.pages <= 1024) {
-        if (f16) go(k_summary_probs<kSrcKeysF16, 16>); else if (q8) go(k_summary_probs<kSrcKeysQ8, 16>);
-        else go(k_summary_probs<kSrcSummary, 16>);
+    if (pages <= 256) {
+        if (f16) go(k_stack_group<kSrcKeysF16, 4>); else if (q8) go(k_stack_group<kSrcKeysQ8, 4>);
+        else go(k_stack_group<kSrcSummary, 4>);
+    } else if (pages <= 512) {
+        if (f16) go(k_stack_group<kSrcKeysF16, 8>); else if (q8) go(k_stack_group<kSrcKeysQ8, 8>);
+        else go(k_stack_group<kSrcSummary, 8>);
+    } else if (pages <= 1024) {
+        if (f16) go(k_stack_group<kSrcKeysF16, 16>); else if (q8) go(k_stack_group<kSrcKeysQ8, 16>);
+        else go(k_stack_group<kSrcSummary, 16>);
     } else {
-        if (f16) go(k_summary_probs<kSrcKeysF16, 0>); else if (q8) go(k_summary_probs<kSrcKeysQ8, 0>);
-        else go(k_summary_probs<kSrcSummary, 0>);
+        if (f16) go(k_stack_group<kSrcKeysF16, 0>); else if (q8) go(k_stack_group<kSrcKeysQ8, 0>);
+        else go(k_stack_group<kSrcSummary, 0>);
     }
     return hipGetLastError();
 }
