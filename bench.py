@@ -329,8 +329,8 @@ def run(args):
 
 
 def pmc_pass(args):
-    """Counter pass (run under rocprofv3 --pmc): a stack of three launch
-    groups over one 128K-token layer (k_stack_group: the first group's
+    """Counter pass (run under rocprofv3 --pmc): a stack of eight distinct
+    128K-token layers in three launches (k_stack_group: the first group's
     summaries alone, then the second group's beside the first group's
     selections, then the second group's selections alone) and three 256 MiB
     device copies (4096 ops of 64 KiB, k_copy_ops) that calibrate
@@ -339,35 +339,36 @@ def pmc_pass(args):
     import kvmem_amd as K
     T, HKV, D, HQ, PT, KSEL = 131072, 8, 128, 32, 256, 32
     W, P = HKV * D, T // PT
+    L = 2 * K._capi.STACK_GROUP
     ctx = K.Context(0)
-    kd = torch.empty(T * W, dtype=torch.int16, device="cuda")
-    qd = torch.empty(HQ * D, dtype=torch.int16, device="cuda")
+    kd = torch.empty((L, T * W), dtype=torch.int16, device="cuda")
+    qd = torch.empty((L, HQ * D), dtype=torch.int16, device="cuda")
     dst = torch.empty(T * W, dtype=torch.int16, device="cuda")
-    s16 = torch.empty(P * W, dtype=torch.int16, device="cuda")
-    scores = torch.empty(P, dtype=torch.float64, device="cuda")
-    sel = torch.empty(KSEL, dtype=torch.int32, device="cuda")
-    cnt = torch.empty(1, dtype=torch.int32, device="cuda")
+    s16 = torch.empty((L, P * W), dtype=torch.int16, device="cuda")
+    scores = torch.empty((L, P), dtype=torch.float64, device="cuda")
+    sel = torch.empty((L, KSEL), dtype=torch.int32, device="cuda")
+    cnt = torch.empty((L, 1), dtype=torch.int32, device="cuda")
     torch.cuda.synchronize()
-    ctx.synth_normal_f16(args.seed, 1000, T * W, kd)
-    ctx.synth_normal_f16(args.seed, 3000, HQ * D, qd)
+    for l in range(L):
+        ctx.synth_normal_f16(args.seed, 1000 + l, T * W, kd[l])
+        ctx.synth_normal_f16(args.seed, 3000 + l, HQ * D, qd[l])
     ctx.check()
-    keys = K.make_keys(kd, K.FMT_F16, T, HKV, D, PT)
-    query = K.make_query(qd, K.FMT_F16, 1, HQ, HKV, D)
-    desc = K.Context.layer_recall(keys=keys, summaries=s16, query=query, scores=scores, selected=sel, count=cnt,
-                                  k=KSEL, aggregation=K.AGG_MEAN)
-    # two full groups over the same layer: the middle launch is the steady state
-    keep = ctx.recall_stack([desc] * (2 * K._capi.STACK_GROUP))
+    descs = [K.Context.layer_recall(keys=K.make_keys(kd[l], K.FMT_F16, T, HKV, D, PT),
+                                    summaries=s16[l], query=K.make_query(qd[l], K.FMT_F16, 1, HQ, HKV, D),
+                                    scores=scores[l], selected=sel[l], count=cnt[l], k=KSEL,
+                                    aggregation=K.AGG_MEAN) for l in range(L)]
+    keep = ctx.recall_stack(descs)
     ctx.check()
     del keep
     op = 1 << 16
     n = T * W * 2 // op
-    srcs = [kd.data_ptr() + i * op for i in range(n)]
+    srcs = [kd[0].data_ptr() + i * op for i in range(n)]
     dsts = [dst.data_ptr() + i * op for i in range(n)]
     for _ in range(3):
         ctx.d2d_batched(srcs, dsts, [op] * n)
         ctx.check()
     ctx.close()
-    print(json.dumps({"pass": "pmc", "summary_bytes_read": T * W * 2 + HQ * D * 2,
+    print(json.dumps({"pass": "pmc", "layers": L, "summary_bytes_read": T * W * 2 + HQ * D * 2,
                       "copy_bytes": T * W * 2, "copy_ops": n}), flush=True)
 
 
