@@ -1036,10 +1036,13 @@ kvr_status kvr_recall_stack(kvr_context *ctx, const kvr_layer_recall *layers, ui
         return KVR_OK;
     }
     if (p0.lanes > 65535) return fail(KVR_ERR_INVALID, "at most 65535 lanes per call");
-    // Launches take groups of up to kStackGroup consecutive layers with one
-    // summary source.  Group k's summaries run beside group k-1's softmax
-    // units and selections, so two groups' logits buffers and counter sets
-    // are live at once: 2 * kStackGroup of each, alternating by group.
+    // Layers go in groups of up to kStackGroup consecutive layers with one
+    // summary source; group k's summaries run in one launch beside group
+    // k-1's softmax workgroups.  Key-history layers get their logits from
+    // those softmax workgroups (computed from the stored summaries), resident
+    // summaries from their own summary workgroups.  Two groups are in flight
+    // at a time, so 2 * kStackGroup logits buffers and counter sets rotate by
+    // layer.
     constexpr uint32_t G = kvr::kStackGroup;
     const size_t lb = logits_bytes(p0.lanes, p0.pages, p0.rows, p0.qheads);
     if (kvr_status s = ensure_workspace(ctx, 2 * G * lb, ss)) return s;
@@ -1049,34 +1052,37 @@ kvr_status kvr_recall_stack(kvr_context *ctx, const kvr_layer_recall *layers, ui
         if (first.empty() || l - first.back() == G || plans[l].src != plans[first.back()].src) first.push_back(l);
     const uint32_t groups = uint32_t(first.size());
     first.push_back(n);
-    const uint32_t nq = p0.rows * p0.qheads * p0.dim;
     kvr::StackGroupArgs g{};
     // enough softmax workgroups per lane for the most units an aggregation
     // has (rows * q-heads); workgroups past a layer's units only count in
     const uint32_t upb = kvr::units_per_block(p0.pages);
     g.probs_per_lane = (p0.rows * p0.qheads + upb - 1) / upb;
-    g.q_slot = (nq + 7) / 8 * 8;
+    g.q_slot = (p0.rows * p0.qheads * p0.dim + 7) / 8 * 8;
     int prev_src = plans[0].src;
     for (uint32_t k = 0; k <= groups; ++k) {
-        // the previous group's selections ride in this launch
         g.mp = g.m;  // g.p holds that group's selections from the previous pass
         g.m = k < groups ? first[k + 1] - first[k] : 0;
         kvr::SelectArgs cur[G];
-        const uint32_t set = (k & 1) * G;
         for (uint32_t i = 0; i < g.m; ++i) {
-            LayerPlan &L = plans[first[k] + i];
+            const uint32_t l = first[k] + i;
+            LayerPlan &L = plans[l];
             const kvr_layer_recall *d = L.d;
             ++ctx->epoch;
-            L.p.logits = reinterpret_cast<double *>(ctx->ws + (set + i) * lb);
-            kvr::SummaryArgs a = d->keys ? summary_args(ctx, d->keys, L.pages, L.key_ls, d->means, d->summaries)
-                                         : resident_args(ctx, L.p, d->summaries);
+            L.p.logits = reinterpret_cast<double *>(ctx->ws + (l % (2 * G)) * lb);
+            const bool resident = L.src == kvr::kSrcSummary;
+            kvr::SummaryArgs a = resident ? resident_args(ctx, L.p, d->summaries)
+                                          : summary_args(ctx, d->keys, L.pages, L.key_ls, d->means, d->summaries);
             a.q = L.p.q;
             a.q_stage = stage_query(L.p.q);
             a.logits = L.p.logits;
             g.s[i] = a;
             cur[i] = make_select_args(ctx, L.p, d->score_mask, d->aggregation, 1, 0, d->scores, true, d->k,
                                       d->tie_rule, L.m, d->selected, d->count);
-            cur[i].counters = ctx->counters + (set + i) * p0.lanes;
+            cur[i].counters = ctx->counters + (l % (2 * G)) * p0.lanes;
+            if (!resident) {
+                cur[i].summaries = d->summaries;
+                cur[i].q = L.p.q;
+            }
             if (d->summary_begin) KVR_HIP(hipEventRecord(static_cast<hipEvent_t>(d->summary_begin), ss));
         }
         const int src = g.m ? plans[first[k]].src : prev_src;

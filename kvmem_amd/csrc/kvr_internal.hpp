@@ -84,6 +84,10 @@ struct SelectArgs {
     uint32_t *count;           // [lanes]
     uint32_t *status;
     uint32_t epoch;
+    // layer stacks: the softmax workgroups compute the logits themselves
+    // from the fp16 summaries and the query (null: the logits are given)
+    const uint16_t *summaries;  // [lanes][pages][kvheads*dim]
+    QueryArgs q;
 };
 
 // Softmax units per 256-thread workgroup: one per wave for rows held in

@@ -459,9 +459,112 @@ __device__ __forceinline__ void wave_softmax_regs(double (&v)[NPL], const bool (
     for (int i = 0; i < NPL; ++i) v[i] = s > 0.0 ? v[i] / s : 0.0;
 }
 
+// Logits rows of q-heads [h0, h0 + nh) (nh <= 4, one kv-head's) for query
+// row r of `lane`, computed from the stored fp16 summaries into rows
+// dst + hh*pages: LDS, or global memory at device scope.  The wave's lanes
+// split like the fused summary epilogue's (dim/8 lanes per page, 8 dims
+// each, the same cross-lane sum), so the values are bit-identical to the
+// fused path's.  Pages are shared among `waves` waves (this one is `wave`).
+template <bool LDS>
+__device__ __forceinline__ void logits_rows(const SelectArgs &a, uint32_t lane, uint32_t r, uint32_t h0, uint32_t nh,
+                                            uint32_t wave, uint32_t waves, double *dst) {
+    const QueryArgs &q = a.q;
+    const uint32_t l = threadIdx.x & 63, lph = q.dim >> 3, ppw = kWave / lph;
+    const uint32_t k = l % lph, sub = l / lph;
+    const uint32_t group = q.qheads / q.kvheads, kvh = h0 / group, W = q.kvheads * q.dim, n = a.pages;
+    double qd[4][8];
+    uint32_t bad = kOperandOk;
+#pragma unroll
+    for (uint32_t hh = 0; hh < 4; ++hh) {
+        const uint32_t h = h0 + min(hh, nh - 1);
+        const uint8_t *qp = q.data + lane * q.lane_stride + r * q.row_stride + h * q.head_stride + 8 * k * q.dim_stride;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            uint16_t qb = 0;
+            const uint32_t e = recall16(load_scalar(qp + i * q.dim_stride, q.scalar), qb);
+            bad = bad ? bad : e;
+            qd[hh][i] = double(h2f(qb));
+        }
+    }
+    if (bad) raise_operand(a.status, bad, a.epoch);
+    const uint16_t *S = a.summaries + uint64_t(lane) * n * W + kvh * q.dim + 8 * k;
+    constexpr uint32_t U = 16;
+    const uint32_t step = ppw * waves;
+    for (uint32_t base = wave * ppw + sub; base < n + sub; base += step * U) {
+        u32x4 x[U];
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u)
+            x[u] = *reinterpret_cast<const u32x4 *>(S + uint64_t(min(base + u * step, n - 1)) * W);
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+            const uint32_t j = base + u * step;
+            double m[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                m[2 * i] = double(h2f(uint16_t(x[u][i] & 0xffffu)));
+                m[2 * i + 1] = double(h2f(uint16_t(x[u][i] >> 16)));
+            }
+#pragma unroll
+            for (uint32_t hh = 0; hh < 4; ++hh) {
+                if (hh >= nh) break;
+                double part = 0.0;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) part = fma(qd[hh][i], m[i], part);
+                part = group_sum(part, int(lph));
+                if (k == 0 && j < n) {
+                    if (LDS) dst[uint64_t(hh) * n + j] = part * q.scale;
+                    else store_device(dst + uint64_t(hh) * n + j, part * q.scale);
+                }
+            }
+        }
+    }
+}
+
+// The logits rows of units [u0, u1) of one lane, by all waves of the
+// workgroup together: for Mean, runs of up to four units on one query row
+// and kv-head share their summary loads; for Max and MaxLogit each unit
+// needs its kv-head's group of q-heads, four heads per pass.  LDS: row i of
+// `rows` holds local row i (unit u0 + i for Mean, head hh of unit u0 + i at
+// i*group + hh otherwise); else the rows go to the lane's logits rows.
+template <bool LDS>
+__device__ __forceinline__ void units_logits(const SelectArgs &a, uint32_t lane, uint32_t u0, uint32_t u1,
+                                             double *rows) {
+    const uint32_t wave = threadIdx.x >> 6, waves = blockDim.x >> 6, n = a.pages;
+    const uint32_t group = a.qheads / a.kvheads;
+    double *lane_rows = a.logits + uint64_t(lane) * a.rows * a.qheads * n;
+    if (a.aggregation == kAggMean) {
+        for (uint32_t u = u0; u < u1;) {
+            const uint32_t r = u / a.qheads, h = u % a.qheads, kv_end = (h / group + 1) * group;
+            const uint32_t nh = min(min(4u, u1 - u), kv_end - h);
+            logits_rows<LDS>(a, lane, r, h, nh, wave, waves, LDS ? rows + uint64_t(u - u0) * n : lane_rows + uint64_t(u) * n);
+            u += nh;
+        }
+        return;
+    }
+    for (uint32_t u = u0; u < u1; ++u) {
+        const uint32_t r = u / a.kvheads, g = u % a.kvheads;
+        for (uint32_t h0 = g * group; h0 < (g + 1) * group; h0 += 4)
+            logits_rows<LDS>(a, lane, r, h0, min(4u, (g + 1) * group - h0), wave, waves,
+                             LDS ? rows + (uint64_t(u - u0) * group + (h0 - g * group)) * n
+                                 : lane_rows + (uint64_t(r) * a.qheads + h0) * n);
+    }
+}
+
+// LDS logits rows of a softmax workgroup (layer stacks, up to 1024 pages):
+// one row per unit for Mean, the group's rows per unit otherwise, if they fit.
+constexpr uint32_t kProbsLdsBytes = 64 * 1024;
+__host__ __device__ constexpr uint32_t probs_lds_rows(uint32_t aggregation, uint32_t group) {
+    return kUnitsPerBlock * (aggregation == kAggMean ? 1 : group);
+}
+__host__ __device__ constexpr bool probs_lds_fits(uint32_t aggregation, uint32_t group, uint32_t pages) {
+    return pages <= 1024 && uint64_t(probs_lds_rows(aggregation, group)) * pages * 8 <= kProbsLdsBytes;
+}
+extern __shared__ __align__(16) double probs_lds[];
+
 // One unit by one wave, rows of up to 64*NPL pages held in registers.
 template <int NPL>
-__device__ __forceinline__ void unit_terms_regs(const SelectArgs &a, double *lane_base, uint32_t unit) {
+__device__ __forceinline__ void unit_terms_regs(const SelectArgs &a, double *lane_base, uint32_t unit,
+                                                const double *lrows) {
     // Loads are unconditional with indices clamped into the row (values past
     // the row are read, then dropped): a load behind a per-lane branch would
     // wait for itself before the next one issues.
@@ -480,11 +583,15 @@ __device__ __forceinline__ void unit_terms_regs(const SelectArgs &a, double *lan
     for (int i = 0; i < NPL; ++i) on[i] = l + i * kWave < n && mv[i];
     double t[NPL];
     double *out;
+    // logits computed in this launch: from this workgroup's LDS rows
+    // (`lrows`: the unit's first row) or at device scope
+    auto logit = [&](const double *row, uint32_t j) { return a.summaries ? load_device(row + j) : row[j]; };
+    auto lds_row = [&](uint32_t hh) { return lrows + uint64_t(hh) * n; };
     if (a.aggregation == kAggMean) {
         out = lane_base + uint64_t(unit) * n;
 #pragma unroll
         for (int i = 0; i < NPL; ++i) {
-            const double x = out[at(i)];
+            const double x = lrows ? lrows[at(i)] : logit(out, at(i));
             t[i] = on[i] ? x : 0.0;
         }
         wave_softmax_regs(t, on);
@@ -502,7 +609,7 @@ __device__ __forceinline__ void unit_terms_regs(const SelectArgs &a, double *lan
                 const double *row = out + uint64_t(hh) * n;
 #pragma unroll
                 for (int i = 0; i < NPL; ++i) {
-                    const double x = row[at(i)];
+                    const double x = lrows ? lds_row(hh)[at(i)] : logit(row, at(i));
                     t[i] = on[i] ? x : 0.0;
                 }
                 wave_softmax_regs(t, on);
@@ -522,7 +629,7 @@ __device__ __forceinline__ void unit_terms_regs(const SelectArgs &a, double *lan
                 const double *row = out + uint64_t(hh) * n;
 #pragma unroll
                 for (int i = 0; i < NPL; ++i) {
-                    const double x = row[at(i)];
+                    const double x = lrows ? lds_row(hh)[at(i)] : logit(row, at(i));
                     t[i] = fmax(t[i], on[i] ? x : -INFINITY);
                 }
             }
@@ -579,7 +686,7 @@ __device__ __forceinline__ void unit_terms_loop(const SelectArgs &a, double *lan
 #pragma unroll
                 for (int i = 0; i < T; ++i) {
                     const uint32_t j = min(base + l + i * S, n - 1);
-                    x[i] = own ? load_device(row + j) : row[j];
+                    x[i] = own || a.summaries ? load_device(row + j) : row[j];
                     mk[i] = a.mask[j];
                 }
 #pragma unroll
@@ -588,7 +695,7 @@ __device__ __forceinline__ void unit_terms_loop(const SelectArgs &a, double *lan
 #pragma unroll
                 for (int i = 0; i < T; ++i) {
                     const uint32_t j = min(base + l + i * S, n - 1);
-                    x[i] = own ? load_device(row + j) : row[j];
+                    x[i] = own || a.summaries ? load_device(row + j) : row[j];
                     on[i] = true;
                 }
             }
@@ -633,7 +740,7 @@ __device__ __forceinline__ void unit_terms_loop(const SelectArgs &a, double *lan
 #pragma unroll
                 for (int i = 0; i < T; ++i) {
                     const uint32_t j = min(base + l + i * S, n - 1);
-                    x[i] = own ? load_device(row + j) : row[j];
+                    x[i] = own || a.summaries ? load_device(row + j) : row[j];
                 }
 #pragma unroll
                 for (int i = 0; i < T; ++i) gm[i] = value(gm[i], x[i]);
@@ -1165,9 +1272,26 @@ __device__ __forceinline__ void probs_block(const SelectArgs &a, uint32_t unit_b
     __shared__ uint32_t s_last;
     const uint32_t unit = NPL > 0 ? unit_block * kUnitsPerBlock + (threadIdx.x >> 6) : unit_block;
     double *lane_base = a.logits + uint64_t(lane) * a.rows * a.qheads * a.pages;
+    const uint32_t group = a.qheads / a.kvheads;
+    const bool lds_logits = a.summaries && NPL > 0 && probs_lds_fits(a.aggregation, group, a.pages);
+    if (a.summaries) {
+        // the logits of this workgroup's units first, by all its waves
+        const uint32_t u0 = NPL > 0 ? unit_block * kUnitsPerBlock : unit_block;
+        const uint32_t u1 = min(a.units, u0 + (NPL > 0 ? kUnitsPerBlock : 1));
+        if (lds_logits) {
+            units_logits<true>(a, lane, u0, u1, probs_lds);
+        } else {
+            units_logits<false>(a, lane, u0, u1, nullptr);
+            wait_vmem();  // stored at device scope: complete, so visible to the reads below
+        }
+        __syncthreads();
+    }
     if (unit < a.units) {
+        const double *lrows = lds_logits ? probs_lds + uint64_t(threadIdx.x >> 6) * (a.aggregation == kAggMean ? 1 : group) *
+                                                           a.pages
+                                         : nullptr;
         if (NPL > 0)
-            unit_terms_regs<NPL ? NPL : 1>(a, lane_base, unit);
+            unit_terms_regs<NPL ? NPL : 1>(a, lane_base, unit, lrows);
         else
             unit_terms_loop(a, lane_base, unit);
     }
@@ -1195,9 +1319,12 @@ __global__ __launch_bounds__(256) void k_probs(SelectArgs a) {
 // One launch of a layer stack: the summary workgroups of a group of up to
 // kStackGroup consecutive layers (blocks [0, summary_blocks); each walks the
 // group's layers in order with the layout of k_summary), then the previous
-// group's softmax units and selections (layer-major, then lane-major).  The
-// query staging alternates between two LDS buffers, so a layer's staging
-// never overwrites rows the previous layer's epilogue may still read.
+// group's softmax workgroups (layer-major, then lane-major).  Key-history
+// layers get their logits from those softmax workgroups, which compute them
+// from the stored summaries before their units; resident-summary layers get
+// them from the summary workgroups (query staging alternates between two
+// LDS buffers, so a layer's staging never overwrites rows the previous
+// layer's epilogue may still read).
 template <int SRC, int NPL>
 __global__ __launch_bounds__(256) void k_stack_group(StackGroupArgs g) {
     const uint32_t sb = g.m ? g.summary_blocks : 0;
@@ -1209,7 +1336,10 @@ __global__ __launch_bounds__(256) void k_stack_group(StackGroupArgs g) {
         probs_block<NPL>(g.p[i], r % g.probs_per_lane, r / g.probs_per_lane, g.probs_per_lane);
         return;
     }
-    for (uint32_t i = 0; i < g.m; ++i) summary_block<SRC, true>(g.s[i], blockIdx.x, q_lds_buf + (i & 1) * g.q_slot);
+    // Key histories leave the logits to the softmax workgroups of the next
+    // launch; resident summaries have no stream, so they compute theirs here.
+    constexpr bool fuse = SRC == kSrcSummary;
+    for (uint32_t i = 0; i < g.m; ++i) summary_block<SRC, fuse>(g.s[i], blockIdx.x, q_lds_buf + (i & 1) * g.q_slot);
 }
 
 // Selection over given scores (no softmax), one workgroup per lane.
@@ -1545,9 +1675,17 @@ hipError_t launch_stack_group(int source, StackGroupArgs g, hipStream_t s) {
     const uint32_t sb = g.summary_blocks;
     const uint32_t probs_blocks = g.mp ? g.mp * g.probs_per_lane * pa.lanes : 0;
     const dim3 grid(unsigned(sb + probs_blocks)), block(256);
-    const size_t q_lds_bytes = g.m && sa.q_stage ? size_t(2) * g.q_slot * 2 : 0;
-    const size_t keys = g.mp && pa.pages <= kTailLdsPages ? size_t(pa.pages) * 8 : 0;
-    const size_t lds = q_lds_bytes > keys ? q_lds_bytes : keys;
+    const size_t q_lds_bytes = g.m && source == kSrcSummary && sa.q_stage ? size_t(2) * g.q_slot * 2 : 0;
+    const size_t keys = g.mp && pa.pages <= kTailLdsPages ? size_t(pa.pages) * 8 : 0;  // the tails' keys
+    size_t lds = q_lds_bytes > keys ? q_lds_bytes : keys;
+    for (uint32_t i = 0; i < g.mp; ++i) {  // softmax workgroups' logits rows
+        const SelectArgs &p = g.p[i];
+        const uint32_t group = p.qheads / p.kvheads;
+        if (p.summaries && probs_lds_fits(p.aggregation, group, p.pages)) {
+            const size_t rows = size_t(probs_lds_rows(p.aggregation, group)) * p.pages * 8;
+            lds = rows > lds ? rows : lds;
+        }
+    }
     const uint32_t pages = g.mp ? pa.pages : sa.pages;
     auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, lds, s, g); };
     const bool f16 = source == kSrcKeysF16, q8 = source == kSrcKeysQ8;
