@@ -465,13 +465,16 @@ __device__ __forceinline__ void wave_softmax_regs(double (&v)[NPL], const bool (
 // split like the fused summary epilogue's (dim/8 lanes per page, 8 dims
 // each, the same cross-lane sum), so the values are bit-identical to the
 // fused path's.  Pages are shared among `waves` waves (this one is `wave`).
-template <bool LDS>
-__device__ __forceinline__ void logits_rows(const SelectArgs &a, uint32_t lane, uint32_t r, uint32_t h0, uint32_t nh,
-                                            uint32_t wave, uint32_t waves, double *dst) {
+template <bool LDS, int LPH>
+__device__ __forceinline__ void logits_rows_t(const SelectArgs &a, uint32_t lane, uint32_t r, uint32_t h0, uint32_t nh,
+                                              uint32_t wave, uint32_t waves, double *dst) {
     const QueryArgs &q = a.q;
-    const uint32_t l = threadIdx.x & 63, lph = q.dim >> 3, ppw = kWave / lph;
+    const uint32_t lph = LPH > 0 ? uint32_t(LPH) : q.dim >> 3;
+    const uint32_t l = threadIdx.x & 63, ppw = kWave / lph;
     const uint32_t k = l % lph, sub = l / lph;
     const uint32_t group = q.qheads / q.kvheads, kvh = h0 / group, W = q.kvheads * q.dim, n = a.pages;
+    const double scale = q.scale;
+    // all four heads are computed (past nh: repeats of the last), nh stored
     double qd[4][8];
     uint32_t bad = kOperandOk;
 #pragma unroll
@@ -488,7 +491,7 @@ __device__ __forceinline__ void logits_rows(const SelectArgs &a, uint32_t lane, 
     }
     if (bad) raise_operand(a.status, bad, a.epoch);
     const uint16_t *S = a.summaries + uint64_t(lane) * n * W + kvh * q.dim + 8 * k;
-    constexpr uint32_t U = 16;
+    constexpr uint32_t U = 8;
     const uint32_t step = ppw * waves;
     for (uint32_t base = wave * ppw + sub; base < n + sub; base += step * U) {
         u32x4 x[U];
@@ -504,28 +507,41 @@ __device__ __forceinline__ void logits_rows(const SelectArgs &a, uint32_t lane, 
                 m[2 * i] = double(h2f(uint16_t(x[u][i] & 0xffffu)));
                 m[2 * i + 1] = double(h2f(uint16_t(x[u][i] >> 16)));
             }
+            double part[4];
 #pragma unroll
             for (uint32_t hh = 0; hh < 4; ++hh) {
-                if (hh >= nh) break;
-                double part = 0.0;
+                part[hh] = 0.0;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) part = fma(qd[hh][i], m[i], part);
-                part = group_sum(part, int(lph));
-                if (k == 0 && j < n) {
-                    if (LDS) dst[uint64_t(hh) * n + j] = part * q.scale;
-                    else store_device(dst + uint64_t(hh) * n + j, part * q.scale);
+                for (int i = 0; i < 8; ++i) part[hh] = fma(qd[hh][i], m[i], part[hh]);
+            }
+#pragma unroll
+            for (uint32_t hh = 0; hh < 4; ++hh) part[hh] = group_sum(part[hh], int(lph));
+            if (k == 0 && j < n) {
+#pragma unroll
+                for (uint32_t hh = 0; hh < 4; ++hh) {
+                    if (hh < nh) {
+                        if (LDS) dst[uint64_t(hh) * n + j] = part[hh] * scale;
+                        else store_device(dst + uint64_t(hh) * n + j, part[hh] * scale);
+                    }
                 }
             }
         }
     }
 }
 
-// The logits rows of units [u0, u1) of one lane, by all waves of the
-// workgroup together: for Mean, runs of up to four units on one query row
-// and kv-head share their summary loads; for Max and MaxLogit each unit
-// needs its kv-head's group of q-heads, four heads per pass.  LDS: row i of
-// `rows` holds local row i (unit u0 + i for Mean, head hh of unit u0 + i at
-// i*group + hh otherwise); else the rows go to the lane's logits rows.
+// Lanes per page fixed at compile time for head_dim 64, 128 and 256, so the
+// cross-lane sums are straight DPP sequences.
+template <bool LDS>
+__device__ __forceinline__ void logits_rows(const SelectArgs &a, uint32_t lane, uint32_t r, uint32_t h0, uint32_t nh,
+                                            uint32_t wave, uint32_t waves, double *dst) {
+    switch (a.q.dim) {
+    case 64: logits_rows_t<LDS, 8>(a, lane, r, h0, nh, wave, waves, dst); break;
+    case 128: logits_rows_t<LDS, 16>(a, lane, r, h0, nh, wave, waves, dst); break;
+    case 256: logits_rows_t<LDS, 32>(a, lane, r, h0, nh, wave, waves, dst); break;
+    default: logits_rows_t<LDS, 0>(a, lane, r, h0, nh, wave, waves, dst); break;
+    }
+}
+
 template <bool LDS>
 __device__ __forceinline__ void units_logits(const SelectArgs &a, uint32_t lane, uint32_t u0, uint32_t u1,
                                              double *rows) {
@@ -1266,15 +1282,17 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
 // Softmax units -> terms; the lane's last workgroup aggregates (+ selects).
 // grid (ceil(units/4), lanes), 256 threads (a unit per wave); dynamic LDS:
 // the tail's keys.
-template <int NPL>
+// LOGITS: a.summaries may ask for the logits to be computed here (layer
+// stacks); k_probs always gets them given.
+template <int NPL, bool LOGITS>
 __device__ __forceinline__ void probs_block(const SelectArgs &a, uint32_t unit_block, uint32_t lane,
                                             uint32_t blocks_per_lane) {
     __shared__ uint32_t s_last;
     const uint32_t unit = NPL > 0 ? unit_block * kUnitsPerBlock + (threadIdx.x >> 6) : unit_block;
     double *lane_base = a.logits + uint64_t(lane) * a.rows * a.qheads * a.pages;
     const uint32_t group = a.qheads / a.kvheads;
-    const bool lds_logits = a.summaries && NPL > 0 && probs_lds_fits(a.aggregation, group, a.pages);
-    if (a.summaries) {
+    const bool lds_logits = LOGITS && a.summaries && NPL > 0 && probs_lds_fits(a.aggregation, group, a.pages);
+    if (LOGITS && a.summaries) {
         // the logits of this workgroup's units first, by all its waves
         const uint32_t u0 = NPL > 0 ? unit_block * kUnitsPerBlock : unit_block;
         const uint32_t u1 = min(a.units, u0 + (NPL > 0 ? kUnitsPerBlock : 1));
@@ -1313,7 +1331,7 @@ __device__ __forceinline__ void probs_block(const SelectArgs &a, uint32_t unit_b
 
 template <int NPL>
 __global__ __launch_bounds__(256) void k_probs(SelectArgs a) {
-    probs_block<NPL>(a, blockIdx.x, blockIdx.y, gridDim.x);
+    probs_block<NPL, false>(a, blockIdx.x, blockIdx.y, gridDim.x);
 }
 
 // One launch of a layer stack: the summary workgroups of a group of up to
@@ -1333,7 +1351,7 @@ __global__ __launch_bounds__(256) void k_stack_group(StackGroupArgs g) {
         // shared CU; these have the whole launch to finish in
         const uint32_t per_layer = g.probs_per_lane * g.p[0].lanes;
         const uint32_t b = blockIdx.x - sb, i = b / per_layer, r = b % per_layer;
-        probs_block<NPL>(g.p[i], r % g.probs_per_lane, r / g.probs_per_lane, g.probs_per_lane);
+        probs_block<NPL, true>(g.p[i], r % g.probs_per_lane, r / g.probs_per_lane, g.probs_per_lane);
         return;
     }
     // Key histories leave the logits to the softmax workgroups of the next

@@ -132,6 +132,18 @@ def test_stack_long_rows_and_single_layer(ctx):
         one.free()
 
 
+@pytest.mark.parametrize("agg", [K.AGG_MEAN, K.AGG_MAX])
+def test_stack_long_rows_from_keys(ctx, agg):
+    """2048 pages per layer from key histories: the softmax workgroups
+    compute the logits of long rows into memory, not LDS."""
+    st = Stack(5, T=2048 * 16, HQ=8, HKV=2, D=64, PT=16, KSEL=32, sid=940)
+    try:
+        eager, stacked = _per_layer_then_stack(ctx, st, agg=agg, mandatory=(1, 2047))
+        _same(eager, stacked)
+    finally:
+        st.free()
+
+
 def test_stack_matrix_core_fallback(ctx):
     """rows*group >= 16 takes the matrix-core logits: the stack runs layer by layer."""
     st = Stack(3, T=8192, HQ=40, HKV=8, R=4, KSEL=8, sid=970)
