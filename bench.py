@@ -259,11 +259,11 @@ def run(args):
     gpu_sel = sel.cpu().numpy().view(np.uint32)
     assert (cnt.cpu().numpy() == KSEL).all(), "every layer must select k pages"
 
-    # one stack launch, per layer of its group: the layer's K read, fp16
-    # summaries and logits written, Q read; per layer of the previous group:
-    # logits read, terms written and read back, scores written
+    # one stack launch, per layer of its group: the layer's K read and fp16
+    # summaries written; per layer of the previous group: summaries and Q
+    # read (logits stay in LDS), terms written and read back, scores written
     logit_bytes = HQ * R * P * 8
-    alg_kernel_bytes = G * (k_bytes + P * W * 2 + logit_bytes + HQ * D * 2 + 3 * logit_bytes + P * 8)
+    alg_kernel_bytes = G * (k_bytes + 2 * P * W * 2 + HQ * D * 2 + 2 * logit_bytes + P * 8)
     achieved = alg_kernel_bytes / (kern_us_mean * 1e-6) / 1e9
     scored_gbps = L * geo["scored_bytes"] / (ms_per_step * 1e-3) / 1e9
     traffic = None
@@ -309,8 +309,8 @@ def run(args):
         "stagein_frac_h2d": round(stage_gbps / h2d, 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": f"k_stack_group<f16> ({G} layers' summaries + fused logits, the previous {G} layers' "
-                      "softmax/top-k)",
+            "kernel": f"k_stack_group<f16> ({G} layers' summaries beside the previous {G} layers' "
+                      "logits, softmax and top-k)",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
