@@ -376,31 +376,56 @@ __global__ __launch_bounds__(256) void k_pack_query(PackQueryArgs a) {
 // contiguous k-range [(l/16)*D/4, (l/16+1)*D/4) of both operands.
 // One wave per 16-page tile; workgroups of four waves.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_logits_mfma(MfmaLogitsArgs a) {
+// KS: the k-range per lane group (head_dim / 4) at compile time for
+// head_dim 64, 128 and 256 (0: at run time).  Each lane's operand halves are
+// loaded unconditionally (clamped rows and pages, zeroed after), the page
+// operand once for all row tiles, so no load waits behind another.
+template <int KS>
+__device__ __forceinline__ void logits_mfma_wave(const MfmaLogitsArgs &a) {
     const uint32_t wave = threadIdx.x >> 6, l = threadIdx.x & 63;
     const uint32_t n0 = (blockIdx.x * 4 + wave) * 16;
     const uint32_t g = blockIdx.y, lane = blockIdx.z;
     if (n0 >= a.pages) return;  // wave-uniform
     const uint32_t group = a.qheads / a.kvheads;
     const uint32_t M = a.rows * group;
-    const uint32_t ks = a.dim >> 2;
+    const uint32_t ks = KS > 0 ? uint32_t(KS) : a.dim >> 2;
     const uint32_t col = l & 15, kq = l >> 4;
     const uint32_t page = n0 + col;
     const bool pvalid = page < a.pages;
     const uint32_t width = a.kvheads * a.dim;
     const uint16_t *brow = a.summaries + (uint64_t(lane) * a.pages + (pvalid ? page : 0)) * width +
                            g * a.dim + kq * ks;
+    constexpr int R = KS > 0 ? KS : 1;
+    uint16_t bh[R];
+    if (KS > 0) {
+#pragma unroll
+        for (int s = 0; s < R; ++s) bh[s] = brow[s];
+    }
     for (uint32_t m0 = 0; m0 < M; m0 += 16) {
         const uint32_t m = m0 + col;
         const bool mvalid = m < M;
-        const uint32_t r = mvalid ? m / group : 0, hh = mvalid ? m % group : 0;
+        const uint32_t mr = mvalid ? m : M - 1;
+        const uint32_t r = mr / group, hh = mr % group;
         const uint16_t *arow = a.qpack + ((uint64_t(lane) * a.rows + r) * a.qheads + g * group + hh) * a.dim +
                                kq * ks;
         f64x4 acc = {0.0, 0.0, 0.0, 0.0};
-        for (uint32_t s = 0; s < ks; ++s) {
-            const double av = mvalid ? double(h2f(arow[s])) : 0.0;
-            const double bv = pvalid ? double(h2f(brow[s])) : 0.0;
-            acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av, bv, acc, 0, 0, 0);
+        if (KS > 0) {
+            uint16_t ah[R];
+#pragma unroll
+            for (int s = 0; s < R; ++s) ah[s] = arow[s];
+#pragma unroll
+            for (int s = 0; s < R; ++s) {
+                const double av = mvalid ? double(h2f(ah[s])) : 0.0;
+                const double bv = pvalid ? double(h2f(bh[s])) : 0.0;
+                acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av, bv, acc, 0, 0, 0);
+            }
+        } else {
+            for (uint32_t s = 0; s < ks; ++s) {
+                const uint16_t ahs = arow[s], bhs = brow[s];
+                const double av = mvalid ? double(h2f(ahs)) : 0.0;
+                const double bv = pvalid ? double(h2f(bhs)) : 0.0;
+                acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av, bv, acc, 0, 0, 0);
+            }
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -411,6 +436,15 @@ __global__ __launch_bounds__(256) void k_logits_mfma(MfmaLogitsArgs a) {
                     acc[i] * a.scale;
             }
         }
+    }
+}
+
+__global__ __launch_bounds__(256) void k_logits_mfma(MfmaLogitsArgs a) {
+    switch (a.dim) {
+    case 64: logits_mfma_wave<16>(a); break;
+    case 128: logits_mfma_wave<32>(a); break;
+    case 256: logits_mfma_wave<64>(a); break;
+    default: logits_mfma_wave<0>(a); break;
     }
 }
 
