@@ -196,6 +196,20 @@ def test_scored_selection_long_rows(ctx, pages, agg):
     assert np.array_equal(host(sel, np.uint32), O.pick_scored_blocks(expect, k, mand, O.TIE_LOWER_FIRST))
 
 
+@pytest.mark.parametrize("pages,rows,dim,qh,kvh", [(300, 4, 96, 8, 2), (77, 16, 36, 4, 4)])
+def test_mfma_other_head_dims(ctx, pages, rows, dim, qh, kvh):
+    """Head dims the matrix-core path handles with a run-time k-range (the
+    vector path needs dim/8 to be a power of two)."""
+    means, query = _score_inputs(pages, rows, dim, qh, kvh, closed_form=False)
+    expect = O.page_softmax_scores(means, query, [rows], qh, kvh, dim, K.AGG_MEAN)
+    s16 = dev(means[0].astype(np.float16).view(np.uint16))
+    q = dev(query[0])
+    out = zeros(pages, np.float64)
+    ctx.score(K.make_query(q, K.FMT_F32, rows, qh, kvh, dim), s16, pages, out, force_mfma=1)
+    ctx.check()
+    assert _rel_err(host(out, np.float64), expect) <= REL
+
+
 def test_mfma_and_vector_logits_agree(ctx):
     pages, rows, dim, qh, kvh = 1024, 4, 128, 40, 8
     means, query = _score_inputs(pages, rows, dim, qh, kvh, closed_form=False)
