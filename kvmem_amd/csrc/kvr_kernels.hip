@@ -1368,6 +1368,145 @@ __global__ __launch_bounds__(256) void k_probs(SelectArgs a) {
     probs_block<NPL, false>(a, blockIdx.x, blockIdx.y, gridDim.x);
 }
 
+// The summary workgroups of a key-history stack group: every layer of the
+// group has the geometry of the first, so a thread owns the same 8 channels
+// of the same page in each, and one ring of loads runs through the layers'
+// rows back to back -- the next layer's first rows are in flight while this
+// layer's last ones are summed, so a layer boundary costs no load latency.
+// Sums restart at each layer's first row (binary32, token order, as in
+// summary_block).
+template <int SRC>
+__device__ __forceinline__ void stack_summaries(const StackGroupArgs &g, uint32_t block) {
+    __builtin_amdgcn_s_setprio(2);
+    const SummaryArgs &a = g.s[0];
+    const uint32_t gpp = a.width >> 3;
+    const uint64_t gid = uint64_t(block) * 256 + threadIdx.x;
+    if (gid >= uint64_t(a.lanes) * a.pages * gpp) return;  // no barriers follow
+    const uint32_t cg = uint32_t(gid % gpp);
+    const uint64_t rest = gid / gpp;
+    const uint32_t page = uint32_t(rest % a.pages);
+    const uint32_t lane = uint32_t(rest / a.pages);
+    const uint32_t c0 = cg * 8;
+    const uint64_t t0 = uint64_t(page) * a.page_tokens;
+    const uint64_t tail = a.tokens - t0;
+    const uint32_t n = tail < a.page_tokens ? uint32_t(tail) : a.page_tokens;
+    const uint32_t m = g.m;
+    // this thread's first row of each layer, and the row stride
+    const uint32_t row_bytes = SRC == kSrcKeysF16 ? a.width * 2 : (a.width >> 5) * kQ8Bytes;
+    const uint32_t b = cg >> 2, s = cg & 3;  // q8_0: block and quarter (see summary_block)
+    const uint32_t col = SRC == kSrcKeysF16 ? c0 * 2 : ((b * kQ8Bytes) & ~3u) + 8 * s;
+    const bool odd = (b & 1) != 0;
+    // per-layer fields, read with constant indices (entries past m are
+    // never used)
+    const uint8_t *first[kStackGroup];
+    float *means[kStackGroup];
+    uint16_t *sums[kStackGroup];
+    uint32_t epoch[kStackGroup];
+#pragma unroll
+    for (uint32_t i = 0; i < kStackGroup; ++i) {
+        first[i] = g.s[i].src + lane * g.s[i].src_lane_stride + t0 * row_bytes + col;
+        means[i] = g.s[i].means;
+        sums[i] = g.s[i].summaries;
+        epoch[i] = g.s[i].epoch;
+    }
+    auto pick = [](uint32_t i, auto v0, auto v1, auto v2, auto v3) { return i == 1 ? v1 : i == 2 ? v2 : i == 3 ? v3 : v0; };
+    auto layer_first = [&](uint32_t i) { return pick(i, first[0], first[1], first[2], first[3]); };
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+    auto finish = [&](uint32_t i) {
+        float *mo = pick(i, means[0], means[1], means[2], means[3]);
+        uint16_t *so = pick(i, sums[0], sums[1], sums[2], sums[3]);
+        const float inv = 1.0f / float(n);
+        float mean[8];
+        uint16_t hb[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        uint32_t bad = kOperandOk;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            mean[k] = acc[k] * inv;
+            const uint32_t e = recall16(mean[k], hb[k]);
+            bad = bad ? bad : e;
+            acc[k] = 0.0f;
+        }
+        const uint64_t out = (uint64_t(lane) * a.pages + page) * a.width + c0;
+        if (mo) {
+            float4 *m4 = reinterpret_cast<float4 *>(mo + out);
+            m4[0] = make_float4(mean[0], mean[1], mean[2], mean[3]);
+            m4[1] = make_float4(mean[4], mean[5], mean[6], mean[7]);
+        }
+        if (bad) raise_operand(a.status, bad, pick(i, epoch[0], epoch[1], epoch[2], epoch[3]));
+        if (so) {
+            u32x4 v;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[k] = uint32_t(hb[2 * k]) | (uint32_t(hb[2 * k + 1]) << 16);
+            *reinterpret_cast<u32x4 *>(so + out) = v;
+        }
+    };
+    // Row u of a chunk is summed only when it is a real row (pad rows re-read
+    // the layer's last row and add zeros: acc is never -0, so acc + (+-0) is
+    // acc bit for bit).
+    auto consume = [&](const auto v, bool real) {
+        if constexpr (SRC == kSrcKeysF16) {
+            u32x4 w;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) w[k] = real ? v[k] : 0u;
+            add_f16x8(acc, w);
+        } else {
+            const uint32_t lo = odd ? v[1] : __builtin_amdgcn_alignbyte(v[1], v[0], 2);
+            const uint32_t hi = odd ? v[2] : __builtin_amdgcn_alignbyte(v[2], v[1], 2);
+            const uint32_t dw = dpp::move<dpp::kQuadBcast0>(v[0]);
+            const uint32_t d = odd ? dw >> 16 : dw & 0xffffu;
+            add_q8x8(acc, real ? lo : 0u, real ? hi : 0u, h2f(uint16_t(real ? d : 0u)));
+        }
+    };
+    auto load = [&](const uint8_t *p) {
+        if constexpr (SRC == kSrcKeysF16)
+            return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+        else
+            return __builtin_nontemporal_load(reinterpret_cast<const u32x3a *>(p));
+    };
+    // Each layer is read in chunks of D rows, the last one padded: then a
+    // layer ends on a chunk boundary, its epilogue runs once outside the
+    // unrolled steps, and the next chunk's loads (the next layer's first
+    // rows at a boundary) are already in flight when it runs.  A chunk is
+    // (layer li, first row r0); `left` = n - 1 - r0 rows follow its first.
+    constexpr int D = SRC == kSrcKeysF16 ? kF16Rows : kQ8Rows;
+    const uint32_t per_layer = (n + D - 1) / D;
+    const uint32_t chunks = m * per_layer;
+    const uint8_t *cp = first[0];
+    uint32_t left = n - 1;
+    auto row_ptr = [&](uint32_t u) { return cp + uint64_t(min(u, left)) * row_bytes; };
+    decltype(load(cp)) ring[D];
+#pragma unroll
+    for (int u = 0; u < D; ++u) {
+        ring[u] = load(row_ptr(u));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    uint32_t li = 0, lc = 0;  // layer and chunk within it of the ring's rows
+    for (uint32_t c = 0; c + 1 < chunks; ++c) {
+        const uint32_t real_left = left;
+        const bool wrap = lc + 1 == per_layer;
+        cp = wrap ? layer_first(li + 1) : cp + uint64_t(D) * row_bytes;
+        left = wrap ? n - 1 : left - D;
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+            consume(ring[u], uint32_t(u) <= real_left);
+            ring[u] = load(row_ptr(u));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (wrap) {
+            finish(li);
+            ++li;
+            lc = 0;
+        } else {
+            ++lc;
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < D; ++u) consume(ring[u], uint32_t(u) <= left);
+    finish(li);
+}
+
 // One launch of a layer stack: the summary workgroups of a group of up to
 // kStackGroup consecutive layers (blocks [0, summary_blocks); each walks the
 // group's layers in order with the layout of k_summary), then the previous
@@ -1390,8 +1529,11 @@ __global__ __launch_bounds__(256) void k_stack_group(StackGroupArgs g) {
     }
     // Key histories leave the logits to the softmax workgroups of the next
     // launch; resident summaries have no stream, so they compute theirs here.
-    constexpr bool fuse = SRC == kSrcSummary;
-    for (uint32_t i = 0; i < g.m; ++i) summary_block<SRC, fuse>(g.s[i], blockIdx.x, q_lds_buf + (i & 1) * g.q_slot);
+    if constexpr (SRC == kSrcSummary) {
+        for (uint32_t i = 0; i < g.m; ++i) summary_block<SRC, true>(g.s[i], blockIdx.x, q_lds_buf + (i & 1) * g.q_slot);
+    } else {
+        stack_summaries<SRC>(g, blockIdx.x);
+    }
 }
 
 // Selection over given scores (no softmax), one workgroup per lane.
