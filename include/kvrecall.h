@@ -68,7 +68,14 @@ typedef enum kvr_format {
     KVR_FMT_Q8_0 = 1,  /* blocks of 32: {fp16 d; int8 qs[32]}, 34 bytes     */
     KVR_FMT_Q4_1 = 2,  /* blocks of 32: {fp16 d; fp16 m; u8 qs[16]}, 20 bytes*/
     KVR_FMT_F32 = 3,   /* binary32 (query and capture input only)           */
-    KVR_FMT_BF16 = 4   /* bfloat16 (query and capture input only)           */
+    KVR_FMT_BF16 = 4,  /* bfloat16 (query and capture input only)           */
+    KVR_FMT_Q4_0 = 5,  /* blocks of 32: {fp16 d; u8 qs[16]}, 18 bytes;
+                          element i: ((qs[i%16] >> (i<16 ? 0 : 4)) & 15) - 8,
+                          times d (attention keys only)                    */
+    KVR_FMT_Q5_0 = 6   /* blocks of 32: {fp16 d; u8 qh[4]; u8 qs[16]}, 22
+                          bytes; the q4_0 nibble plus bit i of qh (little
+                          endian) as bit 4, minus 16, times d (attention
+                          keys only)                                       */
 } kvr_format;
 
 typedef enum kvr_aggregation {
@@ -311,6 +318,52 @@ kvr_status kvr_recall_layer(kvr_context *ctx, const kvr_layer_recall *desc,
  * that layer's stage-in. */
 kvr_status kvr_recall_stack(kvr_context *ctx, const kvr_layer_recall *layers, uint32_t n,
                             void *select_stream, void *copy_stream);
+
+/* ---- sampled attention (attention-feedback observer) --------------------- */
+
+/* One layer's sampled attention: for each sampled query row, the softmax of
+ * every query head over all key tokens, summed per page of page_tokens
+ * tokens and averaged over the heads.  Query element (r, h, d) at
+ * q + r*q_row_stride + h*q_head_stride + d*size; the key row of token t and
+ * kv-head g at k + t*k_row_stride + g*k_head_stride (head_dim values, in
+ * blocks of 32 for the quantized formats); additive mask element (r, t) at
+ * mask + r*mask_row_stride + t*size.  Logit = scale*dot, then
+ * softcap*tanh(logit/softcap) when softcap > 0, plus the mask; a token with
+ * a non-finite mask value is left out. */
+typedef struct kvr_attention_sample {
+    const void *q;             /* dev */
+    kvr_format q_format;       /* KVR_FMT_F32, KVR_FMT_F16 or KVR_FMT_BF16 */
+    size_t q_row_stride, q_head_stride;     /* bytes */
+    const void *k;             /* dev */
+    kvr_format k_format;       /* F16, BF16, F32 (16-byte aligned rows) or
+                                  Q8_0, Q4_0, Q5_0 (2-byte aligned rows)  */
+    size_t k_row_stride, k_head_stride;     /* bytes */
+    const void *mask;          /* dev */
+    kvr_format mask_format;    /* KVR_FMT_F32, KVR_FMT_F16 or KVR_FMT_BF16 */
+    size_t mask_row_stride;    /* bytes */
+    uint32_t head_dim;         /* multiple of 32, at most 256 */
+    uint32_t query_heads, kv_heads;
+    uint32_t tokens, page_tokens;
+    float scale, softcap;
+    const uint32_t *rows;      /* host: the sampled query (and mask) rows */
+    uint32_t n_rows;
+} kvr_attention_sample;
+
+/* Workspace of kvr_attention_page_mass for n_rows sampled rows: up to
+ * KVR_ATTENTION_ROWS rows go in one launch, fewer when their page
+ * log-sum-exp table would pass 32 MiB. */
+#define KVR_ATTENTION_ROWS 64
+size_t kvr_attention_workspace_bytes(uint32_t n_rows, uint32_t query_heads, uint32_t pages);
+
+/* mass: dev float [n_rows][ceil(tokens/page_tokens)], row i for rows[i].
+ * A query head whose every token is masked gives NaN for its row, as in the
+ * reference.  Unsupported formats or head_dim: KVR_ERR_UNSUPPORTED (the
+ * reference's score() returns false).  Replaces
+ * llama_kvmem_attention_cuda::score (src/adapter/llama-kvmem-attention-cuda.h:9-16,
+ * .cu:148-193: page_lse, normalize, average at :59-126); asynchronous on
+ * `stream` (NULL: the context's select stream). */
+kvr_status kvr_attention_page_mass(kvr_context *ctx, const kvr_attention_sample *sample, float *mass,
+                                   void *stream);
 
 /* ---- device copies ------------------------------------------------------- */
 

@@ -253,6 +253,23 @@ class Context:
         check(lib().kvr_recall_stack(self.handle, arr, len(descs), select_stream, copy_stream))
         return arr
 
+    def attention_page_mass(self, *, q, q_format: int, q_row_stride: int, q_head_stride: int, k, k_format: int,
+                            k_row_stride: int, k_head_stride: int, mask, mask_format: int, mask_row_stride: int,
+                            head_dim: int, query_heads: int, kv_heads: int, tokens: int, page_tokens: int,
+                            scale: float, softcap: float, rows: Sequence[int], mass, stream=None) -> None:
+        """kvr_attention_page_mass: device tensors (or addresses) with byte
+        strides; `mass` is float32 [len(rows)][pages] on the device."""
+        r = (C.c_uint32 * max(1, len(rows)))(*rows)
+        a = _capi.AttentionSample(_ptr(q), q_format, q_row_stride, q_head_stride, _ptr(k), k_format, k_row_stride,
+                                  k_head_stride, _ptr(mask), mask_format, mask_row_stride, head_dim, query_heads,
+                                  kv_heads, tokens, page_tokens, scale, softcap,
+                                  C.cast(r, C.POINTER(C.c_uint32)), len(rows))
+        check(lib().kvr_attention_page_mass(self.handle, C.byref(a), _ptr(mass), stream))
+
+    @staticmethod
+    def attention_workspace_bytes(n_rows: int, query_heads: int, pages: int) -> int:
+        return lib().kvr_attention_workspace_bytes(n_rows, query_heads, pages)
+
     def d2d_batched(self, srcs: Sequence[int], dsts: Sequence[int], sizes: Sequence[int], stream=None) -> None:
         n = len(srcs)
         s = (C.c_void_p * max(1, n))(*srcs)

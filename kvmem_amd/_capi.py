@@ -16,7 +16,7 @@ HEADER = os.path.join(ROOT, "include", "kvrecall.h")
 
 # enums
 OK, ERR_INVALID, ERR_NONFINITE, ERR_RANGE, ERR_BUDGET, ERR_WORKSPACE, ERR_HIP, ERR_SCORES, ERR_UNSUPPORTED = range(9)
-FMT_F16, FMT_Q8_0, FMT_Q4_1, FMT_F32, FMT_BF16 = range(5)
+FMT_F16, FMT_Q8_0, FMT_Q4_1, FMT_F32, FMT_BF16, FMT_Q4_0, FMT_Q5_0 = range(7)
 AGG_MEAN, AGG_MAX, AGG_MAX_LOGIT = range(3)
 TIE_LOWER_FIRST, TIE_HIGHER_FIRST = range(2)
 GATHER_COPY, GATHER_DEQUANT_F16, GATHER_REQUANT_Q8_0 = range(3)
@@ -25,6 +25,7 @@ OPT_GATHER_WORKGROUPS, OPT_GATHER_CHUNK_ROWS, OPT_GATHER_THREADS = 1, 2, 3
 MAX_INLINE_MANDATORY = 64
 MAX_PLANES = 8
 STACK_GROUP = 4
+ATTENTION_ROWS = 64
 
 _P = C.c_void_p
 _u32, _u64, _sz, _i = C.c_uint32, C.c_uint64, C.c_size_t, C.c_int
@@ -56,6 +57,14 @@ class LayerRecall(C.Structure):
                 ("select_end", _P)]
 
 
+class AttentionSample(C.Structure):
+    _fields_ = [("q", _P), ("q_format", _i), ("q_row_stride", _sz), ("q_head_stride", _sz),
+                ("k", _P), ("k_format", _i), ("k_row_stride", _sz), ("k_head_stride", _sz),
+                ("mask", _P), ("mask_format", _i), ("mask_row_stride", _sz), ("head_dim", _u32),
+                ("query_heads", _u32), ("kv_heads", _u32), ("tokens", _u32), ("page_tokens", _u32),
+                ("scale", C.c_float), ("softcap", C.c_float), ("rows", C.POINTER(_u32)), ("n_rows", _u32)]
+
+
 _SIGNATURES = {
     "kvr_create": (_i, [_i, C.POINTER(_P)]),
     "kvr_destroy": (_i, [_P]),
@@ -76,6 +85,8 @@ _SIGNATURES = {
     "kvr_stage_in": (_i, [_P, C.POINTER(Plane), _u32, _u32, _u32, _P, _P, _u32, _i, _P]),
     "kvr_recall_layer": (_i, [_P, C.POINTER(LayerRecall), _P, _P]),
     "kvr_recall_stack": (_i, [_P, C.POINTER(LayerRecall), _u32, _P, _P]),
+    "kvr_attention_workspace_bytes": (_sz, [_u32, _u32, _u32]),
+    "kvr_attention_page_mass": (_i, [_P, C.POINTER(AttentionSample), _P, _P]),
     "kvr_d2d_batched": (_i, [_P, C.POINTER(_P), C.POINTER(_P), C.POINTER(_sz), _u32, _P]),
     "kvr_host_alloc": (_i, [_sz, C.POINTER(_P)]),
     "kvr_host_free": (_i, [_P]),

@@ -1100,6 +1100,110 @@ kvr_status kvr_recall_stack(kvr_context *ctx, const kvr_layer_recall *layers, ui
     return KVR_OK;
 }
 
+// ---- sampled attention ------------------------------------------------------
+
+namespace {
+
+constexpr size_t kAttnBudget = size_t(32) << 20;  // page log-sum-exp bytes per launch
+
+uint32_t attention_rows_per_launch(uint32_t n_rows, uint32_t heads, uint32_t pages) {
+    const size_t per_row = std::max<size_t>(1, size_t(heads) * pages * sizeof(float));
+    const size_t fit = std::max<size_t>(1, kAttnBudget / per_row);
+    return uint32_t(std::min<size_t>({size_t(n_rows), fit, size_t(kvr::kAttnRows)}));
+}
+
+bool attention_key_format(kvr_format f) {
+    return f == KVR_FMT_F16 || f == KVR_FMT_BF16 || f == KVR_FMT_F32 || f == KVR_FMT_Q8_0 || f == KVR_FMT_Q4_0 ||
+           f == KVR_FMT_Q5_0;
+}
+
+size_t attention_key_row_bytes(kvr_format f, uint32_t dim) {
+    switch (f) {
+    case KVR_FMT_F16:
+    case KVR_FMT_BF16: return size_t(dim) * 2;
+    case KVR_FMT_F32: return size_t(dim) * 4;
+    case KVR_FMT_Q8_0: return size_t(dim) / 32 * 34;
+    case KVR_FMT_Q4_0: return size_t(dim) / 32 * 18;
+    case KVR_FMT_Q5_0: return size_t(dim) / 32 * 22;
+    default: return 0;
+    }
+}
+
+}  // namespace
+
+size_t kvr_attention_workspace_bytes(uint32_t n_rows, uint32_t query_heads, uint32_t pages) {
+    if (!n_rows || !query_heads || !pages) return 0;
+    const uint32_t rows = attention_rows_per_launch(n_rows, query_heads, pages);
+    return align256(size_t(rows) * query_heads * pages * sizeof(float));
+}
+
+kvr_status kvr_attention_page_mass(kvr_context *ctx, const kvr_attention_sample *a, float *mass, void *stream) {
+    if (kvr_status s = check_ctx(ctx)) return s;
+    if (!a) return fail(KVR_ERR_INVALID, "missing attention sample");
+    // What the reference's score() declines (returns false for).
+    const size_t qel = scalar_bytes(a->q_format), mel = scalar_bytes(a->mask_format);
+    if (!qel || !mel || !attention_key_format(a->k_format))
+        return fail(KVR_ERR_UNSUPPORTED, "attention needs f32/f16/bf16 query and mask, f16/bf16/f32/q8_0/q4_0/q5_0 keys");
+    if (!a->head_dim || a->head_dim % 32 || a->head_dim > 256)
+        return fail(KVR_ERR_UNSUPPORTED, "attention head_dim %u: needs a multiple of 32, at most 256", a->head_dim);
+    if (!a->q || !a->k || !a->mask || !mass) return fail(KVR_ERR_INVALID, "missing attention operand");
+    if (!a->n_rows || !a->rows) return fail(KVR_ERR_INVALID, "no sampled rows");
+    if (!a->query_heads || !a->kv_heads || a->query_heads % a->kv_heads)
+        return fail(KVR_ERR_INVALID, "query heads %u not a multiple of kv heads %u", a->query_heads, a->kv_heads);
+    if (!a->tokens || !a->page_tokens) return fail(KVR_ERR_INVALID, "attention needs tokens and page_tokens");
+    if (!std::isfinite(a->scale) || !std::isfinite(a->softcap) || a->softcap < 0)
+        return fail(KVR_ERR_INVALID, "attention scale and softcap must be finite, softcap nonnegative");
+    if (!aligned(a->q, qel) || a->q_row_stride % qel || a->q_head_stride % qel || !aligned(a->mask, mel) ||
+        a->mask_row_stride % mel)
+        return fail(KVR_ERR_INVALID, "query and mask strides must be multiples of their scalar size");
+    const bool quant = a->k_format == KVR_FMT_Q8_0 || a->k_format == KVR_FMT_Q4_0 || a->k_format == KVR_FMT_Q5_0;
+    const size_t kal = quant ? 2 : 16;
+    if (!aligned(a->k, kal) || a->k_row_stride % kal || a->k_head_stride % kal)
+        return fail(KVR_ERR_INVALID, "key rows and heads must start on %zu-byte boundaries", kal);
+    const size_t krow = attention_key_row_bytes(a->k_format, a->head_dim);
+    if ((a->kv_heads > 1 && a->k_head_stride < krow) ||
+        (a->tokens > 1 && a->k_row_stride < size_t(a->kv_heads - 1) * a->k_head_stride + krow))
+        return fail(KVR_ERR_INVALID, "key strides overlap rows of %zu bytes", krow);
+    const uint32_t pages = page_count(a->tokens, a->page_tokens);
+    if (uint64_t(pages) * a->kv_heads > 0x7fffffffu) return fail(KVR_ERR_INVALID, "too many attention pages");
+    const uint32_t group = a->query_heads / a->kv_heads;
+    const uint32_t chunk = attention_rows_per_launch(a->n_rows, a->query_heads, pages);
+    if (uint64_t(chunk) * group > 65535u * 4u) return fail(KVR_ERR_INVALID, "query group too large");
+    DeviceGuard guard(ctx->device);
+    const hipStream_t s = stream_or(stream, ctx->sel);
+    if (kvr_status st = ensure_workspace(ctx, kvr_attention_workspace_bytes(a->n_rows, a->query_heads, pages), s))
+        return st;
+    kvr::AttnArgs g{};
+    g.q = static_cast<const uint8_t *>(a->q);
+    g.q_row_stride = a->q_row_stride;
+    g.q_head_stride = a->q_head_stride;
+    g.k = static_cast<const uint8_t *>(a->k);
+    g.k_row_stride = a->k_row_stride;
+    g.k_head_stride = a->k_head_stride;
+    g.mask = static_cast<const uint8_t *>(a->mask);
+    g.mask_row_stride = a->mask_row_stride;
+    g.q_scalar = uint32_t(a->q_format);
+    g.mask_scalar = uint32_t(a->mask_format);
+    g.k_format = uint32_t(a->k_format);
+    g.dim = a->head_dim;
+    g.heads = a->query_heads;
+    g.kvheads = a->kv_heads;
+    g.group = group;
+    g.tokens = a->tokens;
+    g.page_tokens = a->page_tokens;
+    g.pages = pages;
+    g.scale = a->scale;
+    g.softcap = a->softcap;
+    g.lse = reinterpret_cast<float *>(ctx->ws);
+    for (uint32_t first = 0; first < a->n_rows; first += chunk) {
+        g.n_rows = std::min(chunk, a->n_rows - first);
+        std::copy(a->rows + first, a->rows + first + g.n_rows, g.rows);
+        g.mass = mass + size_t(first) * pages;
+        KVR_HIP(kvr::launch_attention(g, s));
+    }
+    return KVR_OK;
+}
+
 kvr_status kvr_d2d_batched(kvr_context *ctx, const void *const *src, void *const *dst, const size_t *nbytes,
                            uint32_t n, void *stream) {
     if (kvr_status s = check_ctx(ctx)) return s;

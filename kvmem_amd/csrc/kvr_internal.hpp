@@ -191,4 +191,28 @@ struct SynthArgs {
 };
 hipError_t launch_synth(const SynthArgs &a, hipStream_t s);
 
+// Sampled attention page masses (kvr_attention.hip).  Key formats are
+// kvr_format values; query and mask scalars are Scalar values.
+enum KeyFormat : uint32_t { kKeyF16 = 0, kKeyQ8 = 1, kKeyF32 = 3, kKeyBF16 = 4, kKeyQ4 = 5, kKeyQ5 = 6 };
+constexpr uint32_t kAttnRows = 64;  // sampled rows per launch (kernarg table)
+struct AttnArgs {
+    const uint8_t *q;
+    uint64_t q_row_stride, q_head_stride;
+    const uint8_t *k;
+    uint64_t k_row_stride, k_head_stride;
+    const uint8_t *mask;
+    uint64_t mask_row_stride;
+    uint32_t q_scalar, mask_scalar, k_format;
+    uint32_t dim, heads, kvheads, group;
+    uint32_t tokens, page_tokens, pages;
+    float scale, softcap;
+    float *lse;       // [n_rows][heads][pages]
+    float *mass;      // [n_rows][pages], this launch's first row
+    uint32_t n_rows;  // <= kAttnRows
+    uint32_t rows[kAttnRows];
+};
+// Both launches of one batch of rows: page log-sum-exps, then the
+// normalized, head-averaged masses.
+hipError_t launch_attention(const AttnArgs &a, hipStream_t s);
+
 }  // namespace kvr

@@ -17,9 +17,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 OK, ERR_ARG, ERR_NONFINITE, ERR_RANGE, ERR_BUDGET = 0, 1, 2, 3, 4
 AGG_MEAN, AGG_MAX, AGG_MAX_LOGIT = 0, 1, 2
 TIE_LOWER_FIRST, TIE_HIGHER_FIRST = 0, 1
-FMT_F16, FMT_Q8_0, FMT_Q4_1 = 0, 1, 2
+FMT_F16, FMT_Q8_0, FMT_Q4_1, FMT_F32, FMT_BF16, FMT_Q4_0, FMT_Q5_0 = range(7)
 GATHER_COPY, GATHER_DEQUANT_F16, GATHER_REQUANT_Q8_0 = 0, 1, 2
-QK, Q8_0_BYTES, Q4_1_BYTES = 32, 34, 20
+QK, Q8_0_BYTES, Q4_1_BYTES, Q4_0_BYTES, Q5_0_BYTES = 32, 34, 20, 18, 22
 
 _P = C.c_void_p
 _u8, _u16, _u32, _u64 = C.c_uint8, C.c_uint16, C.c_uint32, C.c_uint64
@@ -55,6 +55,11 @@ def _load_oracle() -> C.CDLL:
         "orc_dequant_q8_0": (None, [_P, _P]),
         "orc_dequant_q4_1": (None, [_P, _P]),
         "orc_quant_q8_0": (None, [_P, _P]),
+        "orc_dequant_q4_0": (None, [_P, _P]),
+        "orc_dequant_q5_0": (None, [_P, _P]),
+        "orc_attention_page_mass": (C.c_int, [_P, C.c_int, C.c_size_t, C.c_size_t, _P, C.c_int, C.c_size_t,
+                                              C.c_size_t, _P, C.c_int, C.c_size_t, _u32, _u32, _u32, _u32,
+                                              _u32, C.c_float, C.c_float, _P, _u32, _P]),
         "orc_gather_row_bytes": (C.c_size_t, [C.c_int, C.c_int, _u32]),
         "orc_gather": (C.c_int, [_P, C.c_int, _u32, _u64, _u32, _P, _u32, C.c_int, _P]),
         "orc_synth_bits": (_u64, [_u64, _u64, _u64]),
@@ -218,6 +223,38 @@ def dequant_q4_1(block: np.ndarray) -> np.ndarray:
     y = np.zeros(QK, np.float32)
     lib.orc_dequant_q4_1(_ptr(block), _ptr(y))
     return y
+
+
+def dequant_q4_0(block: np.ndarray) -> np.ndarray:
+    block = _c(block, np.uint8)
+    y = np.zeros(QK, np.float32)
+    lib.orc_dequant_q4_0(_ptr(block), _ptr(y))
+    return y
+
+
+def dequant_q5_0(block: np.ndarray) -> np.ndarray:
+    block = _c(block, np.uint8)
+    y = np.zeros(QK, np.float32)
+    lib.orc_dequant_q5_0(_ptr(block), _ptr(y))
+    return y
+
+
+def attention_page_mass(q: np.ndarray, q_fmt: int, q_row_stride: int, q_head_stride: int,
+                        k: np.ndarray, k_fmt: int, k_row_stride: int, k_head_stride: int,
+                        mask: np.ndarray, mask_fmt: int, mask_row_stride: int, head_dim: int,
+                        query_heads: int, kv_heads: int, tokens: int, page_tokens: int,
+                        scale: float, softcap: float, rows: Sequence[int]) -> np.ndarray:
+    """Masses [len(rows)][pages] (float64).  q, k, mask are the operands' raw
+    bytes (uint8 views) with byte strides, as the device entry point takes."""
+    q, k, mask = _c(q.view(np.uint8), np.uint8), _c(k.view(np.uint8), np.uint8), _c(mask.view(np.uint8), np.uint8)
+    r = _c(np.asarray(rows), np.uint32)
+    pages = (tokens + page_tokens - 1) // page_tokens
+    out = np.zeros((len(r), pages), np.float64)
+    _check(lib.orc_attention_page_mass(_ptr(q), q_fmt, q_row_stride, q_head_stride, _ptr(k), k_fmt,
+                                       k_row_stride, k_head_stride, _ptr(mask), mask_fmt, mask_row_stride,
+                                       head_dim, query_heads, kv_heads, tokens, page_tokens, scale, softcap,
+                                       _ptr(r), len(r), _ptr(out)))
+    return out
 
 
 def quant_q8_0(x: np.ndarray) -> np.ndarray:

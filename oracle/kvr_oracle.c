@@ -555,3 +555,112 @@ void orc_synth_normal_q8_0(uint64_t seed, uint64_t stream, uint64_t blocks, uint
         orc_quant_q8_0(x, out + b * ORC_Q8_0_BYTES);
     }
 }
+
+/* ---------------------------------------------------------------------- */
+/* Sampled attention page masses: the dense FP64 statement the reference  */
+/* checks its GPU sampler against (src/adapter/llama-kvmem-attention.cpp:  */
+/* 44-96, KVMEM_ATTENTION_VERIFY): per sampled row and query head, logits  */
+/* of every token with a finite mask value, scale*dot in double, optional  */
+/* softcap*tanh(x/softcap), plus the mask; softmax over all tokens; the     */
+/* probabilities summed per page and divided by the head count.  Key       */
+/* decoding follows llama-kvmem-attention-cuda.cu:31-56 (q8_0, q4_0, q5_0   */
+/* blocks; f32/f16/bf16 scalars), element products exact in binary32.      */
+/* ---------------------------------------------------------------------- */
+void orc_dequant_q4_0(const uint8_t *block, float *y) {
+    const float d = orc_f16_to_f32(load_u16(block));
+    const uint8_t *qs = block + 2;
+    for (int j = 0; j < ORC_QK; ++j) {
+        const int code = (qs[j % 16] >> (j < 16 ? 0 : 4)) & 15;
+        y[j] = (float)(code - 8) * d;
+    }
+}
+
+void orc_dequant_q5_0(const uint8_t *block, float *y) {
+    const float d = orc_f16_to_f32(load_u16(block));
+    const uint8_t *qh = block + 2, *qs = block + 6;
+    for (int j = 0; j < ORC_QK; ++j) {
+        const int low = (qs[j % 16] >> (j < 16 ? 0 : 4)) & 15;
+        const int high = (qh[j / 8] >> (j % 8)) & 1;
+        y[j] = (float)((low | (high << 4)) - 16) * d;
+    }
+}
+
+static float attn_scalar(const uint8_t *p, int fmt, size_t i) {
+    if (fmt == ORC_FMT_F32) {
+        float v;
+        memcpy(&v, p + 4 * i, 4);
+        return v;
+    }
+    const uint16_t h = load_u16(p + 2 * i);
+    if (fmt == ORC_FMT_F16) return orc_f16_to_f32(h);
+    const uint32_t bits = (uint32_t)h << 16;
+    float v;
+    memcpy(&v, &bits, 4);
+    return v;
+}
+
+static int attn_scalar_fmt(int fmt) { return fmt == ORC_FMT_F32 || fmt == ORC_FMT_F16 || fmt == ORC_FMT_BF16; }
+
+static void attn_key(const uint8_t *row, int fmt, uint32_t dim, float *out) {
+    for (uint32_t b = 0; b < dim / ORC_QK; ++b) {
+        float *y = out + (size_t)b * ORC_QK;
+        if (fmt == ORC_FMT_Q8_0) orc_dequant_q8_0(row + (size_t)b * ORC_Q8_0_BYTES, y);
+        else if (fmt == ORC_FMT_Q4_0) orc_dequant_q4_0(row + (size_t)b * ORC_Q4_0_BYTES, y);
+        else if (fmt == ORC_FMT_Q5_0) orc_dequant_q5_0(row + (size_t)b * ORC_Q5_0_BYTES, y);
+        else
+            for (uint32_t j = 0; j < ORC_QK; ++j) y[j] = attn_scalar(row, fmt, (size_t)b * ORC_QK + j);
+    }
+}
+
+int orc_attention_page_mass(const uint8_t *q, int q_fmt, size_t q_row_stride, size_t q_head_stride,
+                            const uint8_t *k, int k_fmt, size_t k_row_stride, size_t k_head_stride,
+                            const uint8_t *mask, int mask_fmt, size_t mask_row_stride,
+                            uint32_t head_dim, uint32_t query_heads, uint32_t kv_heads,
+                            uint32_t tokens, uint32_t page_tokens, float scale, float softcap,
+                            const uint32_t *rows, uint32_t n_rows, double *out) {
+    const int key_ok = attn_scalar_fmt(k_fmt) || k_fmt == ORC_FMT_Q8_0 || k_fmt == ORC_FMT_Q4_0 ||
+                       k_fmt == ORC_FMT_Q5_0;
+    if (!q || !k || !mask || !rows || !out || !attn_scalar_fmt(q_fmt) || !attn_scalar_fmt(mask_fmt) || !key_ok ||
+        !head_dim || head_dim % ORC_QK || !query_heads || !kv_heads || query_heads % kv_heads || !tokens ||
+        !page_tokens)
+        return ORC_ERR_ARG;
+    const uint32_t pages = (uint32_t)(((uint64_t)tokens + page_tokens - 1) / page_tokens);
+    const uint32_t group = query_heads / kv_heads;
+    float *query = (float *)malloc(sizeof(float) * head_dim);
+    float *key = (float *)malloc(sizeof(float) * head_dim);
+    float *bias = (float *)malloc(sizeof(float) * tokens);
+    double *logits = (double *)malloc(sizeof(double) * tokens);
+    if (!query || !key || !bias || !logits) {
+        free(query), free(key), free(bias), free(logits);
+        return ORC_ERR_ARG;
+    }
+    for (uint32_t s = 0; s < n_rows; ++s) {
+        double *expected = out + (size_t)s * pages;
+        for (uint32_t p = 0; p < pages; ++p) expected[p] = 0.0;
+        const uint8_t *mrow = mask + (size_t)rows[s] * mask_row_stride;
+        for (uint32_t t = 0; t < tokens; ++t) bias[t] = attn_scalar(mrow, mask_fmt, t);
+        for (uint32_t h = 0; h < query_heads; ++h) {
+            const uint8_t *qrow = q + (size_t)rows[s] * q_row_stride + (size_t)h * q_head_stride;
+            for (uint32_t d = 0; d < head_dim; ++d) query[d] = attn_scalar(qrow, q_fmt, d);
+            double maximum = -INFINITY;
+            for (uint32_t t = 0; t < tokens; ++t) {
+                if (!isfinite(bias[t])) {
+                    logits[t] = -INFINITY;
+                    continue;
+                }
+                attn_key(k + (size_t)t * k_row_stride + (size_t)(h / group) * k_head_stride, k_fmt, head_dim, key);
+                double dot = 0.0;
+                for (uint32_t d = 0; d < head_dim; ++d) dot += (double)query[d] * key[d];
+                dot *= scale;
+                if (softcap > 0) dot = softcap * tanh(dot / softcap);
+                logits[t] = dot + bias[t];
+                if (logits[t] > maximum) maximum = logits[t];
+            }
+            double denominator = 0.0;
+            for (uint32_t t = 0; t < tokens; ++t) denominator += logits[t] = exp(logits[t] - maximum);
+            for (uint32_t t = 0; t < tokens; ++t) expected[t / page_tokens] += logits[t] / denominator / query_heads;
+        }
+    }
+    free(query), free(key), free(bias), free(logits);
+    return ORC_OK;
+}

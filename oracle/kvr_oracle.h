@@ -24,6 +24,13 @@
  *   orc_dequant_q8_0 / orc_quant_q8_0 exact-product closed form, stagein.cu formulas
  *   orc_dequant_q4_1                 closed form y = nib*d + m (ggml q4_1 layout;
  *                                    no reference test holds q4_1 bytes)
+ *   orc_dequant_q4_0 / q5_0          hand-built blocks with known codes (the
+ *                                    layouts of llama-kvmem-attention-cuda.cu:31-56)
+ *   orc_attention_page_mass          closed forms (uniform logits -> token
+ *                                    shares, two-token logistic, softcap tanh,
+ *                                    masked tokens and pages, mass sums to 1)
+ *                                    and a per-page log-sum-exp restatement
+ *                                    computed independently in the tests
  *   orc_synth_*                      not a reference algorithm: the shared
  *                                    seeded input generator (moments checked)
  */
@@ -48,14 +55,19 @@ enum {
 enum { ORC_AGG_MEAN = 0, ORC_AGG_MAX = 1, ORC_AGG_MAX_LOGIT = 2 };
 enum { ORC_TIE_LOWER_FIRST = 0, ORC_TIE_HIGHER_FIRST = 1 };
 
-/* History formats: token-major rows of `width` channels. */
-enum { ORC_FMT_F16 = 0, ORC_FMT_Q8_0 = 1, ORC_FMT_Q4_1 = 2 };
+/* History formats: token-major rows of `width` channels.  F32 and BF16 are
+ * query/mask scalars and attention key formats; Q4_0 and Q5_0 attention key
+ * formats only (same values as the library's kvr_format). */
+enum { ORC_FMT_F16 = 0, ORC_FMT_Q8_0 = 1, ORC_FMT_Q4_1 = 2, ORC_FMT_F32 = 3, ORC_FMT_BF16 = 4,
+       ORC_FMT_Q4_0 = 5, ORC_FMT_Q5_0 = 6 };
 /* Gather modes. */
 enum { ORC_GATHER_COPY = 0, ORC_GATHER_DEQUANT_F16 = 1, ORC_GATHER_REQUANT_Q8_0 = 2 };
 
 #define ORC_QK 32
 #define ORC_Q8_0_BYTES 34 /* {fp16 d; int8 qs[32]}            */
 #define ORC_Q4_1_BYTES 20 /* {fp16 d; fp16 m; uint8 qs[16]}   */
+#define ORC_Q4_0_BYTES 18 /* {fp16 d; uint8 qs[16]}           */
+#define ORC_Q5_0_BYTES 22 /* {fp16 d; uint8 qh[4]; uint8 qs[16]} */
 
 /* ---- scalar conversions ------------------------------------------------ */
 uint16_t orc_f32_to_f16(float f);
@@ -93,6 +105,18 @@ int orc_pick_scored_blocks(const double *scores, uint32_t n, const uint32_t *man
 void orc_dequant_q8_0(const uint8_t *block, float *y);
 void orc_dequant_q4_1(const uint8_t *block, float *y);
 void orc_quant_q8_0(const float *x, uint8_t *block);
+void orc_dequant_q4_0(const uint8_t *block, float *y);
+void orc_dequant_q5_0(const uint8_t *block, float *y);
+
+/* ---- sampled attention (attention-feedback observer) ------------------ */
+/* out: double [n_rows][ceil(tokens/page_tokens)].  Operands are host copies
+ * of the device layouts (byte strides as in kvr_attention_sample). */
+int orc_attention_page_mass(const uint8_t *q, int q_fmt, size_t q_row_stride, size_t q_head_stride,
+                            const uint8_t *k, int k_fmt, size_t k_row_stride, size_t k_head_stride,
+                            const uint8_t *mask, int mask_fmt, size_t mask_row_stride,
+                            uint32_t head_dim, uint32_t query_heads, uint32_t kv_heads,
+                            uint32_t tokens, uint32_t page_tokens, float scale, float softcap,
+                            const uint32_t *rows, uint32_t n_rows, double *out);
 
 /* ---- gather ------------------------------------------------------------- */
 size_t orc_gather_row_bytes(int src_fmt, int mode, uint32_t width);
