@@ -571,6 +571,112 @@ def run_workload(args):
     print(json.dumps(line), flush=True)
 
 
+# ---------------------------------------------------------------------------
+# Sampled attention page masses (--workload attn128k / attn128k_q8): one
+# layer's attention-feedback observer at 131072 tokens, 8 kv-heads x 128,
+# 32 query heads, 4 sampled rows (every 128th row of a 512-row ubatch),
+# causal fp16 mask, pages of 256 tokens.
+ATTN_WORKLOADS = {"attn128k": "f16", "attn128k_q8": "q8_0"}
+
+
+def run_attention(args):
+    import torch
+    import kvmem_amd as K
+    import oracle as O
+    from kvmem_amd.hip import runtime
+
+    hip = runtime()
+    ctx = K.Context(0)
+    kname = ATTN_WORKLOADS[args.workload]
+    T, HKV, HQ, D, PT, UB = 131072, 8, 32, 128, 256, 512
+    rows = [127, 255, 383, 511]
+    P = T // PT
+    kfmt = {"f16": K.FMT_F16, "q8_0": K.FMT_Q8_0}[kname]
+    hrow = D * 2 if kname == "f16" else D // 32 * 34
+    krow = HKV * hrow
+    kdev = torch.empty(T * krow, dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    if kname == "f16":
+        ctx.synth_normal_f16(args.seed, 5000, T * HKV * D, kdev)
+    else:
+        ctx.synth_normal_q8_0(args.seed, 5001, T * HKV * D // 32, kdev)
+    ctx.check()
+    q = torch.empty(UB * HQ * D, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    ctx.synth_normal_f32(args.seed, 5002, q.numel(), q)
+    ctx.check()
+    # causal mask of the ubatch's last 512 positions: row r sees t <= T-UB+r
+    t_idx = torch.arange(T, device="cuda")[None, :]
+    r_idx = torch.arange(UB, device="cuda")[:, None]
+    mask = torch.where(t_idx <= T - UB + r_idx, 0.0, float("-inf")).to(torch.float16).contiguous()
+    mass = torch.empty(len(rows) * P, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    scale = 1 / np.sqrt(D)
+    log(f"workload {args.workload}: {T} tokens, Hq {HQ}/Hkv {HKV}, D {D}, K {kname}, page {PT} ({P} pages), "
+        f"{len(rows)} sampled rows of a {UB}-row ubatch, causal f16 mask")
+
+    def call():
+        ctx.attention_page_mass(q=q, q_format=K.FMT_F32, q_row_stride=HQ * D * 4, q_head_stride=D * 4, k=kdev,
+                                k_format=kfmt, k_row_stride=krow, k_head_stride=hrow, mask=mask,
+                                mask_format=K.FMT_F16, mask_row_stride=T * 2, head_dim=D, query_heads=HQ,
+                                kv_heads=HKV, tokens=T, page_tokens=PT, scale=scale, softcap=0.0, rows=rows,
+                                mass=mass)
+
+    ev_a, ev_b = hip.event(), hip.event()
+    for _ in range(args.warmup):
+        call()
+    ctx.check()
+    times = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        hip.record(ev_a, ctx.select_stream)
+        call()
+        hip.record(ev_b, ctx.select_stream)
+        ctx.check()
+        times.append(hip.elapsed_ms(ev_a, ev_b) * 1e3)
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    call_us = float(np.mean(times))
+    R = len(rows)
+    alg = T * krow + R * HQ * D * 4 + R * T * 2 + 2 * R * HQ * P * 4 + R * P * 4
+    achieved = alg / (call_us * 1e-6) / 1e9
+    got = mass.cpu().numpy().reshape(R, P)
+    log(f"call {call_us:.1f} us (events, both launches) = {achieved:.1f} GB/s algorithmic; "
+        f"mass sums {got.sum(axis=1).round(6).tolist()}")
+    line = {
+        "metric": "sampled attention page masses at 128K ctx: key GB/s vs HBM peak",
+        "value": round(achieved, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": f"{kname} keys, f32 query, f16 mask, f32 arithmetic",
+        "data": f"synthetic seeded (device generator), seed {args.seed}",
+        "config": {"workload": args.workload, "tokens": T, "kv_heads": HKV, "query_heads": HQ, "head_dim": D,
+                   "page_tokens": PT, "pages": P, "sampled_rows": rows, "ubatch": UB, "key_format": kname},
+        "roofline": {"bound": "hbm", "kernel": "k_attn_lse + k_attn_mass (one call)",
+                     "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None, "bytes_per_call": alg,
+                     "mean_call_us": round(call_us, 3)},
+    }
+    if not args.no_cpu:
+        # the FP64 dense restatement on one sampled row, scaled to the call
+        kh = kdev.cpu().numpy()
+        qh = q.cpu().numpy().view(np.uint8)
+        mh = mask.cpu().numpy().view(np.uint8)
+        c0 = time.perf_counter()
+        want = O.attention_page_mass(qh, O.FMT_F32, HQ * D * 4, D * 4, kh, kfmt, krow, hrow, mh, O.FMT_F16, T * 2,
+                                     D, HQ, HKV, T, PT, scale, 0.0, rows[-1:])
+        cpu_s = time.perf_counter() - c0
+        err = float(np.max(np.abs(got[-1] - want[0])))
+        line["cpu_baseline"] = {"value": round(alg / (cpu_s * R) / 1e9, 4), "unit": "GB/s", "cores": 1,
+                                "kind": "port",
+                                "sample": f"1 of {R} sampled rows (row {rows[-1]}), full layer, FP64 dense "
+                                          f"restatement, {cpu_s:.2f} s, single thread; scaled to {R} rows",
+                                "max_abs_diff_vs_gpu": err}
+        log(f"cpu: {cpu_s:.2f} s for one row; max |gpu - oracle| = {err:.3e}")
+    ctx.close()
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -584,7 +690,7 @@ def main():
     ap.add_argument("--gather-threads", type=int, default=0, help="gather workgroup size (0 = default)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workload", choices=["resident64", *WORKLOADS], default="resident64",
+    ap.add_argument("--workload", choices=["resident64", *WORKLOADS, *ATTN_WORKLOADS], default="resident64",
                     help="resident64 (default): the 64-layer 128K stack; the others are the remaining "
                          "workloads, each measured the same way")
     ap.add_argument("--pmc-pass", action="store_true",
@@ -598,6 +704,9 @@ def main():
         sys.exit(2)
     if args.pmc_pass:
         pmc_pass(args)
+        return
+    if args.workload in ATTN_WORKLOADS:
+        run_attention(args)
         return
     if args.workload != "resident64":
         run_workload(args)

@@ -26,15 +26,29 @@ namespace {
 
 constexpr int kAttnThreads = 256;
 constexpr int kAttnWaves = kAttnThreads / kWave;
-constexpr uint32_t kAttnMaxDim = 256;
 
 typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ float scalar_at(const uint8_t *p, uint32_t scalar, uint32_t i) {
-    if (scalar == kScalarF32) return reinterpret_cast<const float *>(p)[i];
-    const uint16_t h = reinterpret_cast<const uint16_t *>(p)[i];
-    return scalar == kScalarF16 ? h2f(h) : bf2f(h);
+// Element i of a row of binary32, binary16 or bfloat16 scalars is read
+// through the dword that holds it (one load instruction whatever the
+// format; a per-format branch would wait for each load where it joins):
+// scalar_word gives that dword and the element's bit offset in it,
+// scalar_value converts.  Loads are issued first and converted after.
+__device__ __forceinline__ const uint32_t *scalar_word(const uint8_t *p, uint32_t scalar, uint32_t i,
+                                                       uint32_t &shift) {
+    const uint32_t lead = uint32_t(reinterpret_cast<uintptr_t>(p) & 3u);
+    const uint32_t at = lead + (scalar == kScalarF32 ? 4u : 2u) * i;  // bytes past the dword below p
+    shift = (at & 2u) * 8u;
+    return reinterpret_cast<const uint32_t *>(p - lead) + (at >> 2);
+}
+// Straight-line (masks, not selects: a uniform select can become a branch,
+// which would split the block the loads are scheduled in).
+__device__ __forceinline__ float scalar_value(uint32_t w, uint32_t shift, uint32_t scalar) {
+    const uint32_t h = (w >> shift) & 0xffffu;
+    const uint32_t m32 = 0u - uint32_t(scalar == kScalarF32), m16 = 0u - uint32_t(scalar == kScalarF16);
+    const uint32_t bits = (w & m32) | (__float_as_uint(h2f(uint16_t(h))) & m16) | ((h << 16) & ~(m32 | m16));
+    return __uint_as_float(bits);
 }
 
 // Bytes of one 32-value block and the dword-aligned words that hold it.
@@ -70,9 +84,8 @@ __device__ __forceinline__ RawBlock<KF> load_block(const uint8_t *row, uint32_t 
         for (uint32_t i = 0; i < RawBlock<KF>::kVec; ++i) r.v[i] = reinterpret_cast<const u32x4 *>(p)[i];
     } else {
         constexpr uint32_t B = KeyBlock<KF>::kBytes, n = RawBlock<KF>::kWords;
-        const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-        const uint32_t *base = reinterpret_cast<const uint32_t *>(a & ~uintptr_t(3));
-        r.odd = uint32_t(a & 2);
+        r.odd = uint32_t(reinterpret_cast<uintptr_t>(p) & 2u);
+        const uint32_t *base = reinterpret_cast<const uint32_t *>(p - r.odd);  // keeps the global address space
         const u32x4a lo = *reinterpret_cast<const u32x4a *>(base);
 #pragma unroll
         for (uint32_t i = 0; i < 4; ++i) r.w[i] = lo[i];
@@ -147,166 +160,301 @@ __device__ __forceinline__ void decode_block(const RawBlock<KF> &r, float *out) 
     }
 }
 
-// One page of one kv-head for a tile of NP (row, query head) pairs: pair
-// p0 + i is sampled row (p0+i)/group and query head kv*group + (p0+i)%group.
-template <int KF, int NP>
-__global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
-    __shared__ float qs[NP * kAttnMaxDim];
-    __shared__ float red[2][kAttnWaves][NP];
-    const uint32_t page = blockIdx.x % a.pages, kv = blockIdx.x / a.pages;
-    const uint32_t p0 = blockIdx.y * NP, npairs = a.n_rows * a.group;
-    const uint32_t dim = a.dim, tid = threadIdx.x;
-    for (uint32_t i = tid; i < NP * dim; i += kAttnThreads) {
-        const uint32_t p = p0 + i / dim;
-        float v = 0.0f;
-        if (p < npairs) {
-            const uint32_t r = a.rows[p / a.group], h = kv * a.group + p % a.group;
-            v = scalar_at(a.q + r * a.q_row_stride + h * a.q_head_stride, a.q_scalar, i % dim);
-        }
-        qs[i] = v;
-    }
-    const uint8_t *mask_row[NP];
-#pragma unroll
-    for (int i = 0; i < NP; ++i) {
-        const uint32_t p = min(p0 + i, npairs - 1);
-        mask_row[i] = a.mask + a.rows[p / a.group] * a.mask_row_stride;
-    }
-    lds_barrier();
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t kPairTile = 16;   // (row, query head) pairs per workgroup: the MFMA's M
+constexpr uint32_t kTokenTile = 16;  // tokens per MFMA: its N
+constexpr float kLog2e = 1.44269504088896340736f, kLn2 = 0.693147180559945309417f;
 
-    float m[NP], s[NP];
-#pragma unroll
-    for (int i = 0; i < NP; ++i) {
-        m[i] = -__builtin_inff();
-        s[i] = 0.0f;
+// A group of pages of one kv-head for a tile of 16 (row, query head) pairs
+// on the matrix cores: v_mfma_f32_16x16x4f32 multiplies 16 pairs' queries
+// (16 x 4 dims) by 16 tokens' keys (4 dims x 16 tokens) and accumulates
+// over the head dim.  Lane l supplies A[pair l%16][k = l/16] and B[k =
+// l/16][token l%16]; in round r the k index g = l/16 walks the 32 dims of
+// key block 4r+g, so each lane decodes whole blocks of its own token (the
+// same dot product, summed in another order).  The lane receives D[pair
+// 4*(l/16)+i][token l%16], i = 0..3.  Pair p0+m is sampled row (p0+m)/group
+// and query head kv*group + (p0+m)%group.
+//
+// The workgroup's 16-token tiles, page after page, are dealt to its waves
+// in turn (flat tile f goes to wave f%4), and each wave streams its tiles
+// through one ring of loads across the pages.  Lanes keep a running max
+// and rescaled sum per pair in base 2; where a wave's next tile is on
+// another page it folds its 16 lanes per pair and leaves the page's partial
+// in LDS.  One barrier at the end, then the four waves' partials of each
+// (page, pair) give its log-sum-exp.
+constexpr uint32_t kMaxPageGroup = 16;
+template <int KF, int R>
+__global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
+    __shared__ float part[2][kMaxPageGroup][kAttnWaves][kPairTile];  // max, sum
+    const uint32_t groups = (a.pages + a.page_group - 1) / a.page_group;
+    const uint32_t kv = blockIdx.x / groups, pg0 = (blockIdx.x % groups) * a.page_group;
+    const uint32_t npg = min(a.page_group, a.pages - pg0);
+    const uint32_t p0 = blockIdx.y * kPairTile, npairs = a.n_rows * a.group;
+    const uint32_t tid = threadIdx.x, lane = tid % kWave;
+    // the wave index as a scalar: tile and page arithmetic stays on the
+    // scalar unit
+    const uint32_t w = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const uint32_t col = lane % 16, kg = lane / 16;
+    const uint32_t nb = a.dim / 32;
+    const uint32_t T = (a.page_tokens + kTokenTile - 1) / kTokenTile;  // tiles per page
+    const uint32_t nflat = npg * T;
+    for (uint32_t i = tid; i < npg * kAttnWaves * kPairTile; i += kAttnThreads) {
+        (&part[0][0][0][0])[i] = -__builtin_inff();
+        (&part[1][0][0][0])[i] = 0.0f;
     }
-    const uint32_t t0 = page * a.page_tokens;
-    const uint32_t t1 = min(t0 + a.page_tokens, a.tokens);
-    const uint32_t nb = dim / 32;
-    for (uint32_t t = t0 + tid; t < t1; t += kAttnThreads) {
-        float bias[NP];
+    auto pair_row = [&](uint32_t p) { return a.rows[p / a.group]; };
+    auto block_of = [&](uint32_t r) { return min(4 * r + kg, nb - 1); };
+    // wave-local tile k is flat tile w + 4k: page pg0 + flat/T, tile flat%T;
+    // tokens past the page or the sequence are clamped to the last token
+    // (in bounds) and not counted
+    auto tile_page = [&](uint32_t k) { return min(w + kAttnWaves * k, nflat - 1) / T; };
+    auto tile_token = [&](uint32_t k, bool &live) {
+        const uint32_t f = w + kAttnWaves * k, fc = min(f, nflat - 1);
+        const uint32_t pg = pg0 + fc / T;
+        const uint32_t t = pg * a.page_tokens + (fc % T) * kTokenTile + col;
+        const uint32_t end = min(pg * a.page_tokens + a.page_tokens, a.tokens);
+        live = f < nflat && t < end;
+        return min(t, end - 1);
+    };
+    const uint8_t *mrow[4];
 #pragma unroll
-        for (int i = 0; i < NP; ++i) bias[i] = scalar_at(mask_row[i], a.mask_scalar, t);
-        const uint8_t *row = a.k + t * a.k_row_stride + kv * a.k_head_stride;
-        float acc[NP];
+    for (int i = 0; i < 4; ++i) mrow[i] = a.mask + uint64_t(pair_row(min(p0 + 4 * kg + i, npairs - 1))) * a.mask_row_stride;
+
+    // ring of two slots: a tile's slot is decoded and refilled with the
+    // wave's tile two on before its MFMAs run
+    RawBlock<KF> ring[2][R];
+    u32x4 bw[2];  // mask words (one register tuple per slot)
+    uint32_t bsh[2][4];
+    auto issue = [&](int slot, uint32_t k) {
+        bool live;
+        const uint32_t t = tile_token(k, live);
+        const uint8_t *row = a.k + uint64_t(t) * a.k_row_stride + uint64_t(kv) * a.k_head_stride;
 #pragma unroll
-        for (int i = 0; i < NP; ++i) acc[i] = 0.0f;
-        RawBlock<KF> cur = load_block<KF>(row, 0);
-        for (uint32_t b = 0; b < nb; ++b) {
-            // next block's loads go out before this block is used
-            const RawBlock<KF> next = load_block<KF>(row, min(b + 1, nb - 1));
-            float kv32[32];
-            decode_block<KF>(cur, kv32);
+        for (int r = 0; r < R; ++r) ring[slot][r] = load_block<KF>(row, block_of(r));
 #pragma unroll
-            for (int i = 0; i < NP; ++i) {
-                const float4 *qv = reinterpret_cast<const float4 *>(qs + i * dim + 32 * b);
+        for (int i = 0; i < 4; ++i) bw[slot][i] = *scalar_word(mrow[i], a.mask_scalar, t, bsh[slot][i]);
+    };
+    // A operand: pair p0+col, the 32 dims of block 4r+kg (zero past the
+    // head dim or the pairs).  Its loads go first, then the ring's first
+    // two tiles, then the conversion: the loop is entered with exactly the
+    // two slots' loads outstanding, in slot order, as at its back edge.
+    float qa[R][32];
+    {
+        const uint32_t p = p0 + col;
+        const uint32_t pc = min(p, npairs - 1);
+        const uint8_t *qrow = a.q + uint64_t(pair_row(pc)) * a.q_row_stride +
+                              uint64_t(kv * a.group + pc % a.group) * a.q_head_stride;
+        uint32_t qw[R][32], qs[R][32];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float4 q4 = qv[j];
-                    acc[i] = __builtin_fmaf(q4.x, kv32[4 * j], acc[i]);
-                    acc[i] = __builtin_fmaf(q4.y, kv32[4 * j + 1], acc[i]);
-                    acc[i] = __builtin_fmaf(q4.z, kv32[4 * j + 2], acc[i]);
-                    acc[i] = __builtin_fmaf(q4.w, kv32[4 * j + 3], acc[i]);
-                }
-            }
-            cur = next;
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int s = 0; s < 32; ++s) qw[r][s] = *scalar_word(qrow, a.q_scalar, 32 * block_of(r) + s, qs[r][s]);
+        __builtin_amdgcn_sched_barrier(0);
+        issue(0, 0);
+        issue(1, 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const bool on = p < npairs && 4 * r + kg < nb;
+#pragma unroll
+            for (int s = 0; s < 32; ++s) qa[r][s] = on ? scalar_value(qw[r][s], qs[r][s], a.q_scalar) : 0.0f;
         }
+    }
+    lds_barrier();  // partials initialized
+
+    float m[4], sm[4];
 #pragma unroll
-        for (int i = 0; i < NP; ++i) {
-            if (!__builtin_isfinite(bias[i])) continue;
-            float l = acc[i] * a.scale;
+    for (int i = 0; i < 4; ++i) {
+        m[i] = -__builtin_inff();
+        sm[i] = 0.0f;
+    }
+    const uint32_t nk = nflat > w ? (nflat - w + kAttnWaves - 1) / kAttnWaves : 0;  // this wave's tiles
+    auto process = [&](int slot, uint32_t k) {
+        float kv32[R][32];
+#pragma unroll
+        for (int r = 0; r < R; ++r) decode_block<KF>(ring[slot][r], kv32[r]);
+        float bias[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            bias[i] = scalar_value(bw[slot][i], bsh[slot][i], a.mask_scalar);
+            // pinned here: the slot's old words are consumed before its
+            // refill is issued (a conversion sunk past it would keep both
+            // live, and the refill would land in registers that the loop's
+            // back edge copies, waiting for the loads)
+            asm volatile("" : "+v"(bias[i]));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        issue(slot, k + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        // two accumulation chains (even and odd k-steps) keep two MFMAs of
+        // the wave in flight; k-steps past the head dim have zero queries
+        f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int s = 0; s < 32; s += 2) {
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[r][s], kv32[r][s], acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[r][s + 1], kv32[r][s + 1], acc1, 0, 0, 0);
+            }
+        bool live;
+        (void)tile_token(k, live);
+        // running max and sum in base 2: logits times log2(e), v_exp_f32
+        // (branch-free: a token left out has l = -inf, so nm = m and the
+        // sum is kept as it is)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const bool use = live && __builtin_isfinite(bias[i]);
+            float l = (acc0[i] + acc1[i]) * a.scale;
             if (a.softcap > 0.0f) l = a.softcap * tanhf(l / a.softcap);
-            l += bias[i];
+            l = use ? (l + bias[i]) * kLog2e : -__builtin_inff();
             const float nm = fmaxf(m[i], l);
-            s[i] = s[i] * expf(m[i] - nm) + expf(l - nm);
+            const float keep = m[i] == nm ? 1.0f : __builtin_amdgcn_exp2f(m[i] - nm);
+            sm[i] = sm[i] * keep + (use ? __builtin_amdgcn_exp2f(l - nm) : 0.0f);
             m[i] = nm;
         }
-    }
-
-    // Page log-sum-exp of each pair: max over the workgroup, then the sum of
-    // the lanes' partial sums rescaled to it (lanes that saw no token add 0).
-    const uint32_t w = tid / kWave, lane = tid % kWave;
+        // this wave's last tile of the page: fold the 16 lanes of each row
+        // (same pairs, different tokens) into the page's partial
+        // (the branch holds temporaries and LDS stores only: running values
+        // changed inside it would need merging copies at the loop's back
+        // edge, which wait for the ring's loads)
+        const uint32_t pl = tile_page(k);
+        const bool last = k < nk && (k + 1 == nk || tile_page(k + 1) != pl);  // (padding tiles never flush)
+        if (last) {
 #pragma unroll
-    for (int i = 0; i < NP; ++i) {
-        const float wm = wave_max(m[i]);
-        if (lane == 0) red[0][w][i] = wm;
+            for (int i = 0; i < 4; ++i) {
+                const float rm = dpp::group_reduce(m[i], 16, dpp::Max());
+                const float e = dpp::group_reduce(sm[i] > 0.0f ? sm[i] * __builtin_amdgcn_exp2f(m[i] - rm) : 0.0f,
+                                                  16, dpp::Add());
+                if (col == 0) {
+                    part[0][pl][w][4 * kg + i] = rm;
+                    part[1][pl][w][4 * kg + i] = e;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            m[i] = last ? -__builtin_inff() : m[i];
+            sm[i] = last ? 0.0f : sm[i];
+        }
+    };
+    // straight-line body (a skipped call would make the ring slots' values
+    // path-dependent, and the copies that merge them wait for the loads):
+    // a tile past the wave's last is computed and not counted
+    for (uint32_t k = 0; k < nk; k += 2) {
+        process(0, k);
+        process(1, k + 1);
     }
     lds_barrier();
+    for (uint32_t i = tid; i < npg * kPairTile; i += kAttnThreads) {
+        const uint32_t pl = i / kPairTile, pr = i % kPairTile, p = p0 + pr;
+        if (p >= npairs) continue;
+        float mx = part[0][pl][0][pr];
 #pragma unroll
-    for (int i = 0; i < NP; ++i) {
-        float mx = red[0][0][i];
+        for (int v = 1; v < kAttnWaves; ++v) mx = fmaxf(mx, part[0][pl][v][pr]);
+        float total = 0.0f;
 #pragma unroll
-        for (int j = 1; j < kAttnWaves; ++j) mx = fmaxf(mx, red[0][j][i]);
-        const float e = wave_sum(s[i] > 0.0f ? s[i] * expf(m[i] - mx) : 0.0f);
-        if (lane == 0) red[1][w][i] = e;
-    }
-    lds_barrier();
-    if (tid < NP && p0 + tid < npairs) {
-        const uint32_t p = p0 + tid;
-        float mx = red[0][0][tid], total = 0.0f;
-#pragma unroll
-        for (int j = 1; j < kAttnWaves; ++j) mx = fmaxf(mx, red[0][j][tid]);
-#pragma unroll
-        for (int j = 0; j < kAttnWaves; ++j) total += red[1][j][tid];
+        for (int v = 0; v < kAttnWaves; ++v) {
+            const float sv = part[1][pl][v][pr];
+            total += sv > 0.0f ? sv * __builtin_amdgcn_exp2f(part[0][pl][v][pr] - mx) : 0.0f;
+        }
+        // back to base e: lse = (max2 + log2(total)) * ln 2
         const uint32_t r = p / a.group, h = kv * a.group + p % a.group;
-        a.lse[(uint64_t(r) * a.heads + h) * a.pages + page] = total > 0.0f ? mx + logf(total) : -__builtin_inff();
+        a.lse[(uint64_t(r) * a.heads + h) * a.pages + pg0 + pl] =
+            total > 0.0f ? (mx + __builtin_amdgcn_logf(total)) * kLn2 : -__builtin_inff();
     }
 }
 
-// Masses of one sampled row: per head, the max and 1/sum of exp over pages
-// (one wave per head), then for each page the head average of
-// exp(lse - max) * (1/sum).
+// Masses of one sampled row over a chunk of 256 pages.  Every workgroup of
+// the row first takes, for each head, the max of its page log-sum-exps and
+// 1/sum of exp(lse - max): each wave takes four heads at a time with all
+// their pages' loads in flight (up to 512 pages per pass, a running max and
+// rescaled sum beyond).  Then, for each page of its chunk, the head average
+// of exp(lse - max) * (1/sum): the reference's normalize and average
+// kernels.
+constexpr uint32_t kMassPages = 256;
+constexpr int kMassHeads = 4;
 __global__ __launch_bounds__(kAttnThreads) void k_attn_mass(AttnArgs a) {
     extern __shared__ float norm[];  // [heads][2]
-    const uint32_t r = blockIdx.x, tid = threadIdx.x, w = tid / kWave, lane = tid % kWave;
+    const uint32_t r = blockIdx.y, tid = threadIdx.x, lane = tid % kWave;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(tid / kWave);
     const float *lse = a.lse + uint64_t(r) * a.heads * a.pages;
-    for (uint32_t h = w; h < a.heads; h += kAttnWaves) {
-        const float *row = lse + uint64_t(h) * a.pages;
-        float mx = -__builtin_inff();
-        for (uint32_t p = lane; p < a.pages; p += kWave) mx = fmaxf(mx, row[p]);
-        mx = wave_max(mx);
-        float sum = 0.0f;
-        for (uint32_t p = lane; p < a.pages; p += kWave) sum += expf(row[p] - mx);
-        sum = wave_sum(sum);
-        if (lane == 0) {
-            norm[2 * h] = mx;
-            norm[2 * h + 1] = 1.0f / sum;
+    for (uint32_t h0 = w * kMassHeads; h0 < a.heads; h0 += kAttnWaves * kMassHeads) {
+        float mx[kMassHeads], sum[kMassHeads];
+#pragma unroll
+        for (int j = 0; j < kMassHeads; ++j) {
+            mx[j] = -__builtin_inff();
+            sum[j] = 0.0f;
+        }
+        for (uint32_t q0 = 0; q0 < a.pages; q0 += 8 * kWave) {
+            float v[kMassHeads][8];
+#pragma unroll
+            for (int j = 0; j < kMassHeads; ++j) {
+                const float *row = lse + uint64_t(min(h0 + j, a.heads - 1)) * a.pages;
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const uint32_t p = q0 + u * kWave + lane;
+                    v[j][u] = p < a.pages ? row[p] : -__builtin_inff();
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < kMassHeads; ++j) {
+                float cm = v[j][0];
+#pragma unroll
+                for (int u = 1; u < 8; ++u) cm = fmaxf(cm, v[j][u]);
+                const float nm = fmaxf(mx[j], cm);
+                float add = 0.0f;
+#pragma unroll
+                for (int u = 0; u < 8; ++u) add += v[j][u] > -__builtin_inff() ? expf(v[j][u] - nm) : 0.0f;
+                sum[j] = (sum[j] > 0.0f ? sum[j] * expf(mx[j] - nm) : 0.0f) + add;
+                mx[j] = nm;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kMassHeads; ++j) {
+            const float wm = wave_max(mx[j]);
+            const float ws = wave_sum(sum[j] > 0.0f ? sum[j] * expf(mx[j] - wm) : 0.0f);
+            if (lane == 0 && h0 + j < a.heads) {
+                // a head whose every page is -inf: max -inf, 1/sum NaN (as
+                // the reference's normalize gives)
+                norm[2 * (h0 + j)] = wm;
+                norm[2 * (h0 + j) + 1] = wm > -__builtin_inff() ? 1.0f / ws : __builtin_nanf("");
+            }
         }
     }
     lds_barrier();
-    for (uint32_t p = tid; p < a.pages; p += kAttnThreads) {
-        float acc = 0.0f;
-        for (uint32_t h = 0; h < a.heads; ++h) acc += expf(lse[uint64_t(h) * a.pages + p] - norm[2 * h]) * norm[2 * h + 1];
-        a.mass[uint64_t(r) * a.pages + p] = acc / float(a.heads);
-    }
+    const uint32_t p = blockIdx.x * kMassPages + tid;
+    if (p >= a.pages) return;
+    float acc = 0.0f;
+#pragma unroll 8
+    for (uint32_t h = 0; h < a.heads; ++h) acc += expf(lse[uint64_t(h) * a.pages + p] - norm[2 * h]) * norm[2 * h + 1];
+    a.mass[uint64_t(r) * a.pages + p] = acc / float(a.heads);
 }
 
 template <int KF>
-hipError_t launch_lse(const AttnArgs &a, uint32_t np, hipStream_t s) {
+hipError_t launch_lse(const AttnArgs &a, hipStream_t s) {
     const uint32_t npairs = a.n_rows * a.group;
-    const dim3 grid(a.kvheads * a.pages, (npairs + np - 1) / np);
-    if (np == 4) hipLaunchKernelGGL((k_attn_lse<KF, 4>), grid, dim3(kAttnThreads), 0, s, a);
-    else if (np == 8) hipLaunchKernelGGL((k_attn_lse<KF, 8>), grid, dim3(kAttnThreads), 0, s, a);
-    else hipLaunchKernelGGL((k_attn_lse<KF, 16>), grid, dim3(kAttnThreads), 0, s, a);
+    const dim3 grid(a.kvheads * ((a.pages + a.page_group - 1) / a.page_group), (npairs + kPairTile - 1) / kPairTile);
+    if (a.dim <= 128) hipLaunchKernelGGL((k_attn_lse<KF, 1>), grid, dim3(kAttnThreads), 0, s, a);
+    else hipLaunchKernelGGL((k_attn_lse<KF, 2>), grid, dim3(kAttnThreads), 0, s, a);
     return hipGetLastError();
 }
 
 }  // namespace
 
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s) {
-    const uint32_t npairs = a.n_rows * a.group;
-    const uint32_t np = npairs <= 4 ? 4 : npairs <= 8 ? 8 : 16;
     hipError_t e = hipErrorInvalidValue;
     switch (a.k_format) {
-    case kKeyF16: e = launch_lse<kKeyF16>(a, np, s); break;
-    case kKeyBF16: e = launch_lse<kKeyBF16>(a, np, s); break;
-    case kKeyF32: e = launch_lse<kKeyF32>(a, np, s); break;
-    case kKeyQ8: e = launch_lse<kKeyQ8>(a, np, s); break;
-    case kKeyQ4: e = launch_lse<kKeyQ4>(a, np, s); break;
-    case kKeyQ5: e = launch_lse<kKeyQ5>(a, np, s); break;
+    case kKeyF16: e = launch_lse<kKeyF16>(a, s); break;
+    case kKeyBF16: e = launch_lse<kKeyBF16>(a, s); break;
+    case kKeyF32: e = launch_lse<kKeyF32>(a, s); break;
+    case kKeyQ8: e = launch_lse<kKeyQ8>(a, s); break;
+    case kKeyQ4: e = launch_lse<kKeyQ4>(a, s); break;
+    case kKeyQ5: e = launch_lse<kKeyQ5>(a, s); break;
     default: break;
     }
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_attn_mass, dim3(a.n_rows), dim3(kAttnThreads), size_t(a.heads) * 2 * sizeof(float), s, a);
+    const dim3 grid((a.pages + kMassPages - 1) / kMassPages, a.n_rows);
+    hipLaunchKernelGGL(k_attn_mass, grid, dim3(kAttnThreads), size_t(a.heads) * 2 * sizeof(float), s, a);
     return hipGetLastError();
 }
 

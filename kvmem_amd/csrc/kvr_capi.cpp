@@ -1148,8 +1148,9 @@ kvr_status kvr_attention_page_mass(kvr_context *ctx, const kvr_attention_sample 
         return fail(KVR_ERR_UNSUPPORTED, "attention head_dim %u: needs a multiple of 32, at most 256", a->head_dim);
     if (!a->q || !a->k || !a->mask || !mass) return fail(KVR_ERR_INVALID, "missing attention operand");
     if (!a->n_rows || !a->rows) return fail(KVR_ERR_INVALID, "no sampled rows");
-    if (!a->query_heads || !a->kv_heads || a->query_heads % a->kv_heads)
-        return fail(KVR_ERR_INVALID, "query heads %u not a multiple of kv heads %u", a->query_heads, a->kv_heads);
+    if (!a->query_heads || !a->kv_heads || a->query_heads % a->kv_heads || a->query_heads > 4096)
+        return fail(KVR_ERR_INVALID, "query heads %u: need a multiple of kv heads %u, at most 4096", a->query_heads,
+                    a->kv_heads);
     if (!a->tokens || !a->page_tokens) return fail(KVR_ERR_INVALID, "attention needs tokens and page_tokens");
     if (!std::isfinite(a->scale) || !std::isfinite(a->softcap) || a->softcap < 0)
         return fail(KVR_ERR_INVALID, "attention scale and softcap must be finite, softcap nonnegative");
@@ -1168,7 +1169,6 @@ kvr_status kvr_attention_page_mass(kvr_context *ctx, const kvr_attention_sample 
     if (uint64_t(pages) * a->kv_heads > 0x7fffffffu) return fail(KVR_ERR_INVALID, "too many attention pages");
     const uint32_t group = a->query_heads / a->kv_heads;
     const uint32_t chunk = attention_rows_per_launch(a->n_rows, a->query_heads, pages);
-    if (uint64_t(chunk) * group > 65535u * 4u) return fail(KVR_ERR_INVALID, "query group too large");
     DeviceGuard guard(ctx->device);
     const hipStream_t s = stream_or(stream, ctx->sel);
     if (kvr_status st = ensure_workspace(ctx, kvr_attention_workspace_bytes(a->n_rows, a->query_heads, pages), s))
@@ -1192,6 +1192,8 @@ kvr_status kvr_attention_page_mass(kvr_context *ctx, const kvr_attention_sample 
     g.tokens = a->tokens;
     g.page_tokens = a->page_tokens;
     g.pages = pages;
+    // pages per workgroup: about 1024 workgroups per pair tile, at most 16
+    g.page_group = uint32_t(std::min<uint64_t>(16, std::max<uint64_t>(1, uint64_t(pages) * a->kv_heads / 1024)));
     g.scale = a->scale;
     g.softcap = a->softcap;
     g.lse = reinterpret_cast<float *>(ctx->ws);

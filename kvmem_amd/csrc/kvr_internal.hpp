@@ -205,6 +205,7 @@ struct AttnArgs {
     uint32_t q_scalar, mask_scalar, k_format;
     uint32_t dim, heads, kvheads, group;
     uint32_t tokens, page_tokens, pages;
+    uint32_t page_group;  // pages per workgroup, 1..16
     float scale, softcap;
     float *lse;       // [n_rows][heads][pages]
     float *mass;      // [n_rows][pages], this launch's first row
