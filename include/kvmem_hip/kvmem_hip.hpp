@@ -211,4 +211,38 @@ private:
     uint16_t *summaries_ = nullptr;
 };
 
+// ---- sampled attention (src/adapter/llama-kvmem-attention-cuda.h:9-16) ----
+// An engine tensor as the sampler reads it: element type, element counts
+// ne[0..2] and byte strides nb[1..2] (ggml's order: ne[0] the head dim,
+// ne[1] rows or tokens, ne[2] heads; a mask is [tokens][rows]).
+struct AttentionTensor {
+    const void *data = nullptr;
+    kvr_format type = KVR_FMT_F32;
+    int64_t ne[3] = {0, 0, 0};
+    size_t nb[3] = {0, 0, 0};
+};
+
+// llama_kvmem_attention_cuda: sampled attention page masses of one layer
+// from its represented Q, native K and mask, without a token attention
+// matrix.  Q and K on one device; a mask elsewhere (host memory) has its
+// sampled rows staged.  Synchronous on return.
+class AttentionSamplerHip {
+public:
+    AttentionSamplerHip();
+    ~AttentionSamplerHip();
+    AttentionSamplerHip(const AttentionSamplerHip &) = delete;
+    AttentionSamplerHip &operator=(const AttentionSamplerHip &) = delete;
+    // false when the sampler does not serve these operands (types, head
+    // dim, Q and K not on one device), as the reference's score() declines;
+    // else output[i][page] for sampled row rows[i].  HIP errors throw
+    // std::runtime_error; a call on another device than the first throws.
+    bool score(const AttentionTensor &q, const AttentionTensor &k, const AttentionTensor &mask, float scale,
+               float softcap, uint32_t block, const std::vector<uint32_t> &rows,
+               std::vector<std::vector<float>> &output);
+
+private:
+    struct Impl;
+    std::unique_ptr<Impl> impl_;
+};
+
 }  // namespace kvmem_hip

@@ -347,6 +347,9 @@ typedef struct kvr_attention_sample {
     float scale, softcap;
     const uint32_t *rows;      /* host: the sampled query (and mask) rows */
     uint32_t n_rows;
+    const uint32_t *mask_rows; /* host, optional: mask row of each sample when
+                                  it differs from rows[i] (a mask staged row
+                                  by row); NULL: rows[i]                      */
 } kvr_attention_sample;
 
 /* Workspace of kvr_attention_page_mass for n_rows sampled rows: up to

@@ -256,14 +256,17 @@ class Context:
     def attention_page_mass(self, *, q, q_format: int, q_row_stride: int, q_head_stride: int, k, k_format: int,
                             k_row_stride: int, k_head_stride: int, mask, mask_format: int, mask_row_stride: int,
                             head_dim: int, query_heads: int, kv_heads: int, tokens: int, page_tokens: int,
-                            scale: float, softcap: float, rows: Sequence[int], mass, stream=None) -> None:
+                            scale: float, softcap: float, rows: Sequence[int], mass, stream=None,
+                            mask_rows: Optional[Sequence[int]] = None) -> None:
         """kvr_attention_page_mass: device tensors (or addresses) with byte
         strides; `mass` is float32 [len(rows)][pages] on the device."""
         r = (C.c_uint32 * max(1, len(rows)))(*rows)
+        mr = None if mask_rows is None else (C.c_uint32 * max(1, len(mask_rows)))(*mask_rows)
         a = _capi.AttentionSample(_ptr(q), q_format, q_row_stride, q_head_stride, _ptr(k), k_format, k_row_stride,
                                   k_head_stride, _ptr(mask), mask_format, mask_row_stride, head_dim, query_heads,
                                   kv_heads, tokens, page_tokens, scale, softcap,
-                                  C.cast(r, C.POINTER(C.c_uint32)), len(rows))
+                                  C.cast(r, C.POINTER(C.c_uint32)), len(rows),
+                                  None if mr is None else C.cast(mr, C.POINTER(C.c_uint32)))
         check(lib().kvr_attention_page_mass(self.handle, C.byref(a), _ptr(mass), stream))
 
     @staticmethod

@@ -62,7 +62,8 @@ class AttentionSample(C.Structure):
                 ("k", _P), ("k_format", _i), ("k_row_stride", _sz), ("k_head_stride", _sz),
                 ("mask", _P), ("mask_format", _i), ("mask_row_stride", _sz), ("head_dim", _u32),
                 ("query_heads", _u32), ("kv_heads", _u32), ("tokens", _u32), ("page_tokens", _u32),
-                ("scale", C.c_float), ("softcap", C.c_float), ("rows", C.POINTER(_u32)), ("n_rows", _u32)]
+                ("scale", C.c_float), ("softcap", C.c_float), ("rows", C.POINTER(_u32)), ("n_rows", _u32),
+                ("mask_rows", C.POINTER(_u32))]
 
 
 _SIGNATURES = {

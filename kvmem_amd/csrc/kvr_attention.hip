@@ -218,7 +218,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
     };
     const uint8_t *mrow[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) mrow[i] = a.mask + uint64_t(pair_row(min(p0 + 4 * kg + i, npairs - 1))) * a.mask_row_stride;
+    for (int i = 0; i < 4; ++i)
+        mrow[i] = a.mask + uint64_t(a.mask_rows[min(p0 + 4 * kg + i, npairs - 1) / a.group]) * a.mask_row_stride;
 
     // ring of two slots: a tile's slot is decoded and refilled with the
     // wave's tile two on before its MFMAs run

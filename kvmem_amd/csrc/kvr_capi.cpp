@@ -1200,6 +1200,8 @@ kvr_status kvr_attention_page_mass(kvr_context *ctx, const kvr_attention_sample 
     for (uint32_t first = 0; first < a->n_rows; first += chunk) {
         g.n_rows = std::min(chunk, a->n_rows - first);
         std::copy(a->rows + first, a->rows + first + g.n_rows, g.rows);
+        const uint32_t *mr = a->mask_rows ? a->mask_rows : a->rows;
+        std::copy(mr + first, mr + first + g.n_rows, g.mask_rows);
         g.mass = mass + size_t(first) * pages;
         KVR_HIP(kvr::launch_attention(g, s));
     }

@@ -210,7 +210,8 @@ struct AttnArgs {
     float *lse;       // [n_rows][heads][pages]
     float *mass;      // [n_rows][pages], this launch's first row
     uint32_t n_rows;  // <= kAttnRows
-    uint32_t rows[kAttnRows];
+    uint32_t rows[kAttnRows];       // query rows
+    uint32_t mask_rows[kAttnRows];  // mask rows
 };
 // Both launches of one batch of rows: page log-sum-exps, then the
 // normalized, head-averaged masses.

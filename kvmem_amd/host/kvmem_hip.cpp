@@ -824,4 +824,125 @@ const float *SummaryCapture::means(uint32_t layer) const {
     return means_ + size_t(layer) * max_pages_ * kv_heads_ * head_dim_;
 }
 
+// ---------------------------------------------------------------------------
+// Sampled attention (llama-kvmem-attention-cuda.cu:148-193 is the interface
+// mirrored: score() declines with false, stages a mask that is not on the
+// device, and returns host masses).
+namespace {
+bool on_device(const void *p, int &device) {
+    hipPointerAttribute_t attr{};
+    if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+        (void)hipGetLastError();  // unknown to the runtime: host memory
+        return false;
+    }
+    if (attr.type != hipMemoryTypeDevice && attr.type != hipMemoryTypeManaged) return false;
+    device = attr.device;
+    return true;
+}
+}  // namespace
+
+struct AttentionSamplerHip::Impl {
+    int device = -1;
+    kvr_context *ctx = nullptr;
+    void *mask = nullptr, *out = nullptr;
+    size_t mask_bytes = 0, out_bytes = 0;
+    void grow(void *&buf, size_t &have, size_t need) {
+        if (need <= have) return;
+        if (buf) hip_ok(hipFree(buf), "hipFree");
+        buf = nullptr;
+        have = 0;
+        hip_ok(hipMalloc(&buf, need), "hipMalloc");
+        have = need;
+    }
+    ~Impl() {
+        if (device < 0) return;
+        DeviceBinding bind(device);
+        if (mask) (void)hipFree(mask);
+        if (out) (void)hipFree(out);
+        if (ctx) kvr_destroy(ctx);
+    }
+};
+
+AttentionSamplerHip::AttentionSamplerHip() : impl_(new Impl) {}
+AttentionSamplerHip::~AttentionSamplerHip() = default;
+
+bool AttentionSamplerHip::score(const AttentionTensor &q, const AttentionTensor &k, const AttentionTensor &mask,
+                                float scale, float softcap, uint32_t block, const std::vector<uint32_t> &rows,
+                                std::vector<std::vector<float>> &output) {
+    auto scalar = [](kvr_format f) { return f == KVR_FMT_F32 || f == KVR_FMT_F16 || f == KVR_FMT_BF16; };
+    const bool key_ok = scalar(k.type) || k.type == KVR_FMT_Q8_0 || k.type == KVR_FMT_Q4_0 || k.type == KVR_FMT_Q5_0;
+    if (!scalar(q.type) || !scalar(mask.type) || !key_ok || q.ne[0] > 256 || q.ne[0] % 32 || q.ne[0] <= 0)
+        return false;
+    int device = -1, key_device = -1, mask_device = -1;
+    if (!on_device(q.data, device) || !on_device(k.data, key_device) || device != key_device) return false;
+    Impl &m = *impl_;
+    if (m.device < 0) {
+        m.device = device;
+        DeviceBinding bind(device);
+        if (kvr_create(device, &m.ctx) != KVR_OK) {
+            m.device = -1;
+            throw std::runtime_error(std::string("attention sampler context: ") + kvr_last_error());
+        }
+    }
+    if (m.device != device) throw std::runtime_error("attention sampler changed device");
+    require(block > 0 && k.ne[1] > 0 && q.ne[2] > 0 && k.ne[2] > 0, "attention sampler geometry");
+    DeviceBinding bind(device);
+    const uint32_t tokens = uint32_t(k.ne[1]), pages = (tokens + block - 1) / block, n = uint32_t(rows.size());
+    output.assign(n, std::vector<float>(pages));
+    if (!n) return true;
+    const size_t mel = mask.type == KVR_FMT_F32 ? 4 : 2, mrow = size_t(mask.ne[0]) * mel;
+    require(mask.ne[0] >= int64_t(tokens), "mask rows shorter than the keys");
+    kvr_attention_sample a{};
+    a.q = q.data;
+    a.q_format = q.type;
+    a.q_row_stride = q.nb[1];
+    a.q_head_stride = q.nb[2];
+    a.k = k.data;
+    a.k_format = k.type;
+    a.k_row_stride = k.nb[1];
+    a.k_head_stride = k.nb[2];
+    a.mask_format = mask.type;
+    a.head_dim = uint32_t(q.ne[0]);
+    a.query_heads = uint32_t(q.ne[2]);
+    a.kv_heads = uint32_t(k.ne[2]);
+    a.tokens = tokens;
+    a.page_tokens = block;
+    a.scale = scale;
+    a.softcap = softcap;
+    a.rows = rows.data();
+    a.n_rows = n;
+    const hipStream_t s = static_cast<hipStream_t>(kvr_select_stream(m.ctx));
+    StreamDrain drain{s};
+    std::vector<uint32_t> staged_rows;
+    if (on_device(mask.data, mask_device) && mask_device == device) {
+        a.mask = mask.data;
+        a.mask_row_stride = mask.nb[1];
+    } else {
+        // the sampled rows only, one after another (the reference's staged
+        // mask, llama-kvmem-attention-cuda.cu:163-172)
+        m.grow(m.mask, m.mask_bytes, size_t(n) * mrow);
+        std::vector<uint8_t> host(size_t(n) * mrow);
+        for (uint32_t i = 0; i < n; ++i)
+            std::memcpy(host.data() + size_t(i) * mrow,
+                        static_cast<const uint8_t *>(mask.data) + size_t(rows[i]) * mask.nb[1], mrow);
+        hip_ok(hipMemcpyAsync(m.mask, host.data(), host.size(), hipMemcpyHostToDevice, s), "mask H2D");
+        hip_ok(hipStreamSynchronize(s), "mask H2D");
+        staged_rows.resize(n);
+        for (uint32_t i = 0; i < n; ++i) staged_rows[i] = i;
+        a.mask = m.mask;
+        a.mask_row_stride = mrow;
+        a.mask_rows = staged_rows.data();
+    }
+    m.grow(m.out, m.out_bytes, size_t(n) * pages * sizeof(float));
+    const kvr_status st = kvr_attention_page_mass(m.ctx, &a, static_cast<float *>(m.out), s);
+    if (st == KVR_ERR_UNSUPPORTED) return false;
+    ok(st, "kvr_attention_page_mass");
+    std::vector<float> host(size_t(n) * pages);
+    hip_ok(hipMemcpyAsync(host.data(), m.out, host.size() * sizeof(float), hipMemcpyDeviceToHost, s), "mass D2H");
+    hip_ok(hipStreamSynchronize(s), "mass D2H");
+    drain.armed = false;
+    for (uint32_t i = 0; i < n; ++i) std::copy_n(host.data() + size_t(i) * pages, pages, output[i].data());
+    return true;
+}
+
 }  // namespace kvmem_hip

@@ -508,6 +508,66 @@ void capture() {
     kvr_destroy(ctx);
 }
 
+// AttentionSamplerHip (llama_kvmem_attention_cuda::score): q8_0 keys, f32
+// Q, f16 causal mask on the device and staged from host memory, against the
+// oracle's dense FP64 masses; declines what the reference declines.
+void attention() {
+    const uint32_t dim = 64, heads = 8, kvh = 2, tokens = 700, block = 64, qrows = 12;
+    const uint32_t pages = (tokens + block - 1) / block, hb = dim / 32 * 34, krow = kvh * hb;
+    std::vector<uint8_t> k(size_t(tokens) * krow);
+    orc_synth_q8_0(9, 40, uint64_t(tokens) * kvh * dim / 32, 0.01f, 0.05f, k.data());
+    std::vector<float> q(size_t(qrows) * heads * dim);
+    orc_synth_normal_f32(9, 41, q.size(), q.data());
+    std::vector<uint16_t> mask(size_t(qrows) * tokens);
+    for (uint32_t r = 0; r < qrows; ++r)
+        for (uint32_t t = 0; t < tokens; ++t)
+            mask[size_t(r) * tokens + t] = t <= tokens - qrows + r ? 0 : 0xfc00;  // 0 or -inf
+    Dev<uint8_t> kd(k);
+    Dev<float> qd(q);
+    Dev<uint16_t> md(mask);
+    kh::AttentionTensor tq, tk, tm;
+    tq.data = qd.p, tq.type = KVR_FMT_F32, tq.ne[0] = dim, tq.ne[1] = qrows, tq.ne[2] = heads;
+    tq.nb[1] = size_t(heads) * dim * 4, tq.nb[2] = size_t(dim) * 4;
+    tk.data = kd.p, tk.type = KVR_FMT_Q8_0, tk.ne[0] = dim, tk.ne[1] = tokens, tk.ne[2] = kvh;
+    tk.nb[1] = krow, tk.nb[2] = hb;
+    tm.data = md.p, tm.type = KVR_FMT_F16, tm.ne[0] = tokens, tm.ne[1] = qrows, tm.nb[1] = size_t(tokens) * 2;
+    const std::vector<uint32_t> rows = {11, 3, 7};
+    const float scale = 0.125f;
+    std::vector<double> want(rows.size() * pages);
+    require(orc_attention_page_mass(reinterpret_cast<const uint8_t *>(q.data()), ORC_FMT_F32, tq.nb[1], tq.nb[2],
+                                    k.data(), ORC_FMT_Q8_0, krow, hb,
+                                    reinterpret_cast<const uint8_t *>(mask.data()), ORC_FMT_F16, tm.nb[1], dim,
+                                    heads, kvh, tokens, block, scale, 0.0f, rows.data(), uint32_t(rows.size()),
+                                    want.data()) == ORC_OK,
+            "oracle attention");
+    kh::AttentionSamplerHip sampler;
+    auto check = [&](const std::vector<std::vector<float>> &got, const char *what) {
+        require(got.size() == rows.size(), what);
+        for (size_t i = 0; i < rows.size(); ++i)
+            for (uint32_t p = 0; p < pages; ++p) {
+                const double w = want[i * pages + p], g = got[i][p];
+                if (!(std::fabs(g - w) <= 1e-6 + 2e-4 * std::fabs(w)))
+                    throw std::runtime_error(std::string(what) + ": mass differs from the oracle");
+            }
+    };
+    std::vector<std::vector<float>> out;
+    require(sampler.score(tq, tk, tm, scale, 0.0f, block, rows, out), "device mask declined");
+    check(out, "device mask");
+    kh::AttentionTensor th = tm;
+    th.data = mask.data();  // host memory: the sampled rows are staged
+    require(sampler.score(tq, tk, th, scale, 0.0f, block, rows, out), "host mask declined");
+    check(out, "staged mask");
+    kh::AttentionTensor bad = tq;
+    bad.ne[0] = 48;
+    require(!sampler.score(bad, tk, tm, scale, 0.0f, block, rows, out), "head dim 48 accepted");
+    bad = tq;
+    bad.data = q.data();  // Q in host memory
+    require(!sampler.score(bad, tk, tm, scale, 0.0f, block, rows, out), "host Q accepted");
+    bad = tk;
+    bad.type = KVR_FMT_Q4_1;
+    require(!sampler.score(tq, bad, tm, scale, 0.0f, block, rows, out), "q4_1 keys accepted");
+}
+
 }  // namespace
 
 int main(int argc, char **argv) {
@@ -518,7 +578,7 @@ int main(int argc, char **argv) {
     if (gpu)
         tests = {{"qualification", qualification}, {"current_layer", current_layer}, {"pick", pick},
                  {"stagein", stagein},           {"meank", meank},                 {"transfer", transfer},
-                 {"capture", capture}};
+                 {"capture", capture}, {"attention", attention}};
     for (auto &[name, fn] : tests) {
         std::cout << "RUN  " << name << std::endl;
         try {
