@@ -71,7 +71,8 @@ typedef enum kvr_format {
     KVR_FMT_BF16 = 4,  /* bfloat16 (query and capture input only)           */
     KVR_FMT_Q4_0 = 5,  /* blocks of 32: {fp16 d; u8 qs[16]}, 18 bytes;
                           element i: ((qs[i%16] >> (i<16 ? 0 : 4)) & 15) - 8,
-                          times d (attention keys only)                    */
+                          times d (attention keys, gather copy and raw-K
+                          transform)                                       */
     KVR_FMT_Q5_0 = 6   /* blocks of 32: {fp16 d; u8 qh[4]; u8 qs[16]}, 22
                           bytes; the q4_0 nibble plus bit i of qh (little
                           endian) as bit 4, minus 16, times d (attention
@@ -92,8 +93,26 @@ typedef enum kvr_tie_rule {
 typedef enum kvr_gather_mode {
     KVR_GATHER_COPY = 0,         /* bytes unchanged                           */
     KVR_GATHER_DEQUANT_F16 = 1,  /* decode to binary32, RNE to binary16       */
-    KVR_GATHER_REQUANT_Q8_0 = 2  /* q8_0 -> binary32 -> q8_0                   */
+    KVR_GATHER_REQUANT_Q8_0 = 2, /* q8_0 -> binary32 -> q8_0                   */
+    KVR_GATHER_ROPE_FWHT = 3     /* raw K (q8_0 or q4_0): decode, NeoX RoPE at
+                                    the token's position, Walsh-Hadamard
+                                    transform, requantize to the source format
+                                    (plane.rope holds the parameters)         */
 } kvr_gather_mode;
+
+/* Parameters of KVR_GATHER_ROPE_FWHT (kvmem_stagein_enqueue_k,
+ * src/adapter/llama-kvmem-stagein.h:37-42).  Token t of the history has
+ * position pos_base + t.  In each head of head_dim values, pairs (i, i +
+ * n_rot/2) for i < n_rot/2 rotate by (position * theta[i]); then each run of
+ * fwht values of the row (0: none) is scaled by 1/sqrt(fwht) and
+ * Walsh-Hadamard transformed. */
+typedef struct kvr_rope {
+    uint32_t head_dim;     /* width is a multiple of it */
+    uint32_t n_rot;        /* even, at most head_dim (0: no rotation) */
+    const float *theta;    /* dev, n_rot/2 values */
+    uint32_t fwht;         /* 0, 64, 128, 256 or 512; divides width */
+    int64_t pos_base;
+} kvr_rope;
 
 typedef enum kvr_copy_engine {
     KVR_ENGINE_AUTO = 0,    /* the faster engine for the mode                 */
@@ -133,12 +152,13 @@ typedef struct kvr_query {
  * at rows [s*page_tokens, s*page_tokens + valid). */
 typedef struct kvr_plane {
     const void *history;    /* pinned, token-major rows */
-    kvr_format format;      /* KVR_FMT_F16, KVR_FMT_Q8_0 or KVR_FMT_Q4_1 */
+    kvr_format format;      /* KVR_FMT_F16, KVR_FMT_Q8_0, KVR_FMT_Q4_1 or KVR_FMT_Q4_0 */
     uint32_t width;         /* channels per token row */
     uint64_t tokens;        /* per lane */
     kvr_gather_mode mode;
     void *slots;            /* dev */
     size_t host_lane_stride, slot_lane_stride; /* bytes; 0 = tightly packed */
+    const kvr_rope *rope;   /* KVR_GATHER_ROPE_FWHT only (else ignored) */
 } kvr_plane;
 
 /* One layer of recall for `lanes` sequences (kvr_recall_layer). */

@@ -17,14 +17,15 @@ import numpy as np
 
 from . import _capi
 from ._capi import (AGG_MAX, AGG_MAX_LOGIT, AGG_MEAN, ENGINE_AUTO, ENGINE_KERNEL, ENGINE_SDMA,
-                    FMT_BF16, FMT_F16, FMT_F32, FMT_Q4_1, FMT_Q8_0, GATHER_COPY, GATHER_DEQUANT_F16,
-                    GATHER_REQUANT_Q8_0, TIE_HIGHER_FIRST, TIE_LOWER_FIRST, KvrError, check, lib)
+                    FMT_BF16, FMT_F16, FMT_F32, FMT_Q4_0, FMT_Q4_1, FMT_Q5_0, FMT_Q8_0, GATHER_COPY,
+                    GATHER_DEQUANT_F16, GATHER_REQUANT_Q8_0, GATHER_ROPE_FWHT, TIE_HIGHER_FIRST,
+                    TIE_LOWER_FIRST, KvrError, check, lib)
 
 __all__ = [
     "Context", "PinnedBuffer", "KvrError", "row_bytes", "gather_row_bytes",
     "AGG_MEAN", "AGG_MAX", "AGG_MAX_LOGIT", "TIE_LOWER_FIRST", "TIE_HIGHER_FIRST",
-    "FMT_F16", "FMT_Q8_0", "FMT_Q4_1", "FMT_F32", "FMT_BF16",
-    "GATHER_COPY", "GATHER_DEQUANT_F16", "GATHER_REQUANT_Q8_0",
+    "FMT_F16", "FMT_Q8_0", "FMT_Q4_1", "FMT_F32", "FMT_BF16", "FMT_Q4_0", "FMT_Q5_0",
+    "GATHER_COPY", "GATHER_DEQUANT_F16", "GATHER_REQUANT_Q8_0", "GATHER_ROPE_FWHT",
     "ENGINE_AUTO", "ENGINE_KERNEL", "ENGINE_SDMA",
 ]
 
@@ -38,6 +39,8 @@ def row_bytes(fmt: int, width: int) -> int:
         return width // 32 * 34
     if fmt == FMT_Q4_1:
         return width // 32 * 20
+    if fmt == FMT_Q4_0:
+        return width // 32 * 18
     raise ValueError(f"no row format {fmt}")
 
 
@@ -111,13 +114,21 @@ def make_keys(t, fmt: int, tokens: int, kv_heads: int, head_dim: int, page_token
 
 
 def make_plane(history, fmt: int, width: int, tokens: int, mode: int, slots,
-               host_lane_stride: int = 0, slot_lane_stride: int = 0):
+               host_lane_stride: int = 0, slot_lane_stride: int = 0, rope: Optional[dict] = None):
+    """rope (for GATHER_ROPE_FWHT): dict(head_dim, n_rot, theta (device
+    float32 tensor of n_rot/2 values), fwht, pos_base)."""
     p = _capi.Plane()
     p.history = _ptr(history)
     p.format, p.width, p.tokens, p.mode = fmt, width, tokens, mode
     p.slots = _ptr(slots)
     p.host_lane_stride, p.slot_lane_stride = host_lane_stride, slot_lane_stride
-    p._keep = (history, slots)
+    keep = [history, slots]
+    if rope is not None:
+        r = _capi.Rope(rope["head_dim"], rope.get("n_rot", 0), _ptr(rope.get("theta")), rope.get("fwht", 0),
+                       rope.get("pos_base", 0))
+        p.rope = C.pointer(r)
+        keep += [r, rope.get("theta")]
+    p._keep = tuple(keep)
     return p
 
 

@@ -19,7 +19,7 @@ OK, ERR_INVALID, ERR_NONFINITE, ERR_RANGE, ERR_BUDGET, ERR_WORKSPACE, ERR_HIP, E
 FMT_F16, FMT_Q8_0, FMT_Q4_1, FMT_F32, FMT_BF16, FMT_Q4_0, FMT_Q5_0 = range(7)
 AGG_MEAN, AGG_MAX, AGG_MAX_LOGIT = range(3)
 TIE_LOWER_FIRST, TIE_HIGHER_FIRST = range(2)
-GATHER_COPY, GATHER_DEQUANT_F16, GATHER_REQUANT_Q8_0 = range(3)
+GATHER_COPY, GATHER_DEQUANT_F16, GATHER_REQUANT_Q8_0, GATHER_ROPE_FWHT = range(4)
 ENGINE_AUTO, ENGINE_KERNEL, ENGINE_SDMA = range(3)
 OPT_GATHER_WORKGROUPS, OPT_GATHER_CHUNK_ROWS, OPT_GATHER_THREADS = 1, 2, 3
 MAX_INLINE_MANDATORY = 64
@@ -42,9 +42,14 @@ class Query(C.Structure):
                 ("dim_stride", _sz), ("lane_stride", _sz), ("attention_scale", C.c_float)]
 
 
+class Rope(C.Structure):
+    _fields_ = [("head_dim", _u32), ("n_rot", _u32), ("theta", _P), ("fwht", _u32), ("pos_base", C.c_int64)]
+
+
 class Plane(C.Structure):
     _fields_ = [("history", _P), ("format", _i), ("width", _u32), ("tokens", _u64), ("mode", _i),
-                ("slots", _P), ("host_lane_stride", _sz), ("slot_lane_stride", _sz)]
+                ("slots", _P), ("host_lane_stride", _sz), ("slot_lane_stride", _sz),
+                ("rope", C.POINTER(Rope))]
 
 
 class LayerRecall(C.Structure):

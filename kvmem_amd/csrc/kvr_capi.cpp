@@ -95,6 +95,7 @@ size_t row_bytes(kvr_format f, uint32_t width) {
     case KVR_FMT_F16: return size_t(width) * 2;
     case KVR_FMT_Q8_0: return width % 32 ? 0 : size_t(width) / 32 * 34;
     case KVR_FMT_Q4_1: return width % 32 ? 0 : size_t(width) / 32 * 20;
+    case KVR_FMT_Q4_0: return width % 32 ? 0 : size_t(width) / 32 * 18;
     default: return 0;
     }
 }
@@ -427,13 +428,29 @@ kvr_status check_planes(const kvr_plane *planes, uint32_t n, uint32_t lanes, uin
         if (!p.history || !p.slots || !p.width || !p.tokens)
             return fail(KVR_ERR_INVALID, "plane %u: missing history, slots or geometry", i);
         const size_t srow = row_bytes(p.format, p.width);
-        if (!srow) return fail(KVR_ERR_UNSUPPORTED, "plane %u: history format must be f16, q8_0 or q4_1 "
+        if (!srow) return fail(KVR_ERR_UNSUPPORTED, "plane %u: history format must be f16, q8_0, q4_1 or q4_0 "
                                                     "(width %% 32 == 0 for blocks)", i);
+        const bool raw_k = p.mode == KVR_GATHER_ROPE_FWHT;
         size_t drow = 0;
         if (p.mode == KVR_GATHER_COPY) drow = srow;
-        else if (p.mode == KVR_GATHER_DEQUANT_F16) drow = size_t(p.width) * 2;
+        else if (p.mode == KVR_GATHER_DEQUANT_F16 && p.format != KVR_FMT_Q4_0) drow = size_t(p.width) * 2;
         else if (p.mode == KVR_GATHER_REQUANT_Q8_0 && p.format == KVR_FMT_Q8_0) drow = srow;
+        else if (raw_k && (p.format == KVR_FMT_Q8_0 || p.format == KVR_FMT_Q4_0)) drow = srow;
         if (!drow) return fail(KVR_ERR_UNSUPPORTED, "plane %u: gather mode not provided for this format", i);
+        if (raw_k) {
+            // kvmem_stagein_enqueue_k / rope_neox / fwht_ok (stagein.cu:477-479, 534-541, 817-831)
+            const kvr_rope *r = p.rope;
+            if (!r || !r->head_dim || p.width % r->head_dim || r->n_rot % 2 || r->n_rot > r->head_dim ||
+                (r->n_rot && !r->theta))
+                return fail(KVR_ERR_INVALID, "plane %u: raw-K transform needs head_dim dividing the width, an even "
+                                             "n_rot <= head_dim and its theta", i);
+            if (r->fwht && ((r->fwht != 64 && r->fwht != 128 && r->fwht != 256 && r->fwht != 512) ||
+                            p.width % r->fwht))
+                return fail(KVR_ERR_INVALID, "plane %u: Walsh-Hadamard size must be 64, 128, 256 or 512 and "
+                                             "divide the width", i);
+            if (4 * (srow + 16 + size_t(p.width) * 4) > kGatherLds)
+                return fail(KVR_ERR_INVALID, "plane %u: rows too wide for the raw-K transform", i);
+        }
         if (p.mode == KVR_GATHER_DEQUANT_F16 && p.format != KVR_FMT_F16 && (p.width % 32 || !aligned(p.slots, 16)))
             return fail(KVR_ERR_INVALID, "plane %u: dequantized slots must be 16-byte aligned", i);
         (void)chunk_rows;
@@ -461,6 +478,14 @@ kvr_status check_planes(const kvr_plane *planes, uint32_t n, uint32_t lanes, uin
         pp.g.width = p.width;
         pp.g.format = uint32_t(p.format);
         pp.g.mode = uint32_t(p.mode);
+        if (raw_k) {
+            pp.g.theta = p.rope->theta;
+            pp.g.head_dim = p.rope->head_dim;
+            pp.g.n_rot = p.rope->n_rot;
+            pp.g.fwht = p.rope->fwht;
+            pp.g.fwht_scale = p.rope->fwht ? 1.0f / std::sqrt(float(p.rope->fwht)) : 1.0f;
+            pp.g.pos_base = p.rope->pos_base;
+        }
         pp.host = static_cast<const uint8_t *>(p.history);
         pp.host_row = srow;
     }
@@ -482,9 +507,12 @@ uint32_t gather_chunk_rows(uint32_t chunk_rows, uint32_t threads, const PlanePla
                            uint32_t page_tokens) {
     uint32_t cr = std::min(chunk_rows, page_tokens);
     const size_t waves = threads / 64;
-    for (uint32_t i = 0; i < n; ++i)
-        if (pp[i].g.mode != KVR_GATHER_COPY && pp[i].g.format != KVR_FMT_F16)
-            cr = std::min<uint32_t>(cr, uint32_t(kGatherLds / (waves * (size_t(pp[i].g.src_row) + 16))));
+    for (uint32_t i = 0; i < n; ++i) {
+        if (pp[i].g.mode == KVR_GATHER_COPY || pp[i].g.format == KVR_FMT_F16) continue;
+        // the raw-K transform also keeps one binary32 row per wave
+        const size_t fixed = pp[i].g.mode == KVR_GATHER_ROPE_FWHT ? size_t(pp[i].g.width) * 4 : 0;
+        cr = std::min<uint32_t>(cr, uint32_t((kGatherLds / waves - fixed) / (size_t(pp[i].g.src_row) + 16)));
+    }
     return std::max<uint32_t>(cr, 1);
 }
 

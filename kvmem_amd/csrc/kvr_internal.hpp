@@ -116,6 +116,11 @@ struct GatherPlane {
     uint32_t width;
     uint32_t format;            // kvr_format of the source
     uint32_t mode;              // kvr_gather_mode
+    // raw-K transform (mode 3): rotation and Walsh-Hadamard parameters
+    const float *theta;         // [n_rot/2]
+    uint32_t head_dim, n_rot, fwht;
+    float fwht_scale;           // 1/sqrt(fwht) in binary32
+    int64_t pos_base;           // position of history token 0
 };
 
 struct GatherArgs {

@@ -21,8 +21,9 @@ typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
 // 12-byte loads need only dword alignment on gfx950 (global_load_dwordx3).
 typedef u32x3 u32x3a __attribute__((aligned(4)));
 
-constexpr uint32_t kFmtF16 = 0, kFmtQ8 = 1, kFmtQ41 = 2;
-constexpr uint32_t kModeCopy = 0, kModeDequantF16 = 1, kModeRequantQ8 = 2;
+constexpr uint32_t kFmtF16 = 0, kFmtQ8 = 1, kFmtQ41 = 2, kFmtQ40 = 5;
+constexpr uint32_t kModeCopy = 0, kModeDequantF16 = 1, kModeRequantQ8 = 2, kModeRopeFwht = 3;
+constexpr uint32_t kQ40Bytes = 18;  // {fp16 d; uint8 qs[16]}
 
 __device__ __forceinline__ float load_scalar(const uint8_t *p, uint32_t scalar) {
     if (scalar == kScalarF32) return *reinterpret_cast<const float *>(p);
@@ -1576,6 +1577,14 @@ __device__ __forceinline__ void decode_block(const uint8_t *blk, uint32_t fmt, f
     if (fmt == kFmtQ8) {
 #pragma unroll
         for (int j = 0; j < kQK; ++j) y[j] = float(int8_t(blk[2 + j])) * d;
+    } else if (fmt == kFmtQ40) {
+        // (nib - 8) * d, low nibbles first (stagein.cu:145-158)
+#pragma unroll
+        for (int j = 0; j < kQK / 2; ++j) {
+            const uint8_t b = blk[2 + j];
+            y[j] = float(int(b & 15) - 8) * d;
+            y[j + kQK / 2] = float(int(b >> 4) - 8) * d;
+        }
     } else {
         const float m = h2f(ld_u16(blk + 2));
 #pragma unroll
@@ -1599,6 +1608,118 @@ __device__ __forceinline__ void quant_block_q8(const float *x, uint8_t *blk) {
     blk[1] = uint8_t(dh >> 8);
 #pragma unroll
     for (int j = 0; j < kQK; ++j) blk[2 + j] = uint8_t(int8_t(roundf(x[j] * id)));
+}
+
+// q4_0 (stagein.cu:201-234): the value of largest magnitude (first of
+// equals) sets d = v / -8; codes (int)(x*id + 8.5) capped at 15, the
+// multiply-add fused (explicitly, so it does not depend on contraction).
+__device__ __forceinline__ void quant_block_q40(const float *x, uint8_t *blk) {
+    float amax = 0.0f, vmax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kQK; ++j) {
+        const float v = x[j];
+        const bool more = amax < fabsf(v);
+        amax = more ? fabsf(v) : amax;
+        vmax = more ? v : vmax;
+    }
+    const float d = vmax / -8.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const uint16_t dh = f2h(d);
+    blk[0] = uint8_t(dh);
+    blk[1] = uint8_t(dh >> 8);
+#pragma unroll
+    for (int j = 0; j < kQK / 2; ++j) {
+        const int x0 = min(int(__builtin_fmaf(x[j], id, 8.5f)), 15);
+        const int x1 = min(int(__builtin_fmaf(x[j + kQK / 2], id, 8.5f)), 15);
+        blk[2 + j] = uint8_t((x0 & 15) | ((x1 & 15) << 4));
+    }
+}
+
+// sin and cos of a binary32 angle, each rounded once to binary32 from a
+// binary64 evaluation: reduction by the nearest multiple k of pi/2
+// (Cody-Waite, pi/2 in two binary64 parts, fused), Taylor polynomials of
+// degree 21 (sin) and 20 (cos) on |r| <= pi/4 (truncation below 1e-24),
+// then the quadrant k mod 4.  Written from those series; the oracle runs
+// the same operations, so the results agree bit for bit.
+__device__ __forceinline__ void rope_sincos(float angle, float &s, float &c) {
+    const double x = angle;
+    const double k = __builtin_rint(x * 0.6366197723675814);
+    double r = __builtin_fma(-k, 1.5707963267948966, x);
+    r = __builtin_fma(-k, 6.123233995736766e-17, r);
+    const double r2 = r * r;
+    double ps = 1.9572941063391263e-20;
+    ps = __builtin_fma(ps, r2, -8.22063524662433e-18);
+    ps = __builtin_fma(ps, r2, 2.8114572543455206e-15);
+    ps = __builtin_fma(ps, r2, -7.647163731819816e-13);
+    ps = __builtin_fma(ps, r2, 1.6059043836821613e-10);
+    ps = __builtin_fma(ps, r2, -2.505210838544172e-08);
+    ps = __builtin_fma(ps, r2, 2.7557319223985893e-06);
+    ps = __builtin_fma(ps, r2, -0.0001984126984126984);
+    ps = __builtin_fma(ps, r2, 0.008333333333333333);
+    ps = __builtin_fma(ps, r2, -0.16666666666666666);
+    const double sr = __builtin_fma(r * r2, ps, r);
+    double pc = 4.110317623312165e-19;
+    pc = __builtin_fma(pc, r2, -1.5619206968586225e-16);
+    pc = __builtin_fma(pc, r2, 4.779477332387385e-14);
+    pc = __builtin_fma(pc, r2, -1.1470745597729725e-11);
+    pc = __builtin_fma(pc, r2, 2.08767569878681e-09);
+    pc = __builtin_fma(pc, r2, -2.755731922398589e-07);
+    pc = __builtin_fma(pc, r2, 2.48015873015873e-05);
+    pc = __builtin_fma(pc, r2, -0.001388888888888889);
+    pc = __builtin_fma(pc, r2, 0.041666666666666664);
+    pc = __builtin_fma(pc, r2, -0.5);
+    const double cr = __builtin_fma(r2, pc, 1.0);
+    const uint32_t q = uint32_t(int64_t(k)) & 3u;
+    const double sv = q == 0 ? sr : q == 1 ? cr : q == 2 ? -sr : -cr;
+    const double cv = q == 0 ? cr : q == 1 ? -sr : q == 2 ? -cr : sr;
+    s = float(sv);
+    c = float(cv);
+}
+
+// The raw-K transform of one row staged in the wave's LDS (rope_neox_kernel,
+// fwht_kernel, stagein.cu:105-130, 160-178, run in flush's order,
+// stagein.cu:746-783): decode into a binary32 row, rotate each head's pairs
+// at the row's position, scale and butterfly each run of `fwht` values
+// (h = 1, 2, 4, ...: (a, b) -> (a+b, a-b), as the reference's loop nest),
+// then requantize the row in place.  One wave; LDS order within a wave is
+// program order, with a wave fence between phases.
+__device__ __forceinline__ void rope_fwht_row(const GatherPlane &P, uint8_t *raw, float *fr, int64_t pos) {
+    const uint32_t l = threadIdx.x & 63, bpr = P.width / kQK;
+    const uint32_t bbytes = P.format == kFmtQ8 ? kQ8Bytes : kQ40Bytes;
+    for (uint32_t b = l; b < bpr; b += kWave) decode_block(raw + b * bbytes, P.format, fr + b * kQK);
+    wave_lds_sync();
+    const uint32_t half = P.n_rot / 2, heads = P.width / P.head_dim;
+    const float fpos = float(pos);
+    for (uint32_t e = l; e < heads * half; e += kWave) {
+        const uint32_t h = e / half, i = e % half;
+        float sn, cs;
+        rope_sincos(fpos * P.theta[i], sn, cs);
+        float *row = fr + h * P.head_dim;
+        const float x0 = row[i], x1 = row[i + half];
+        row[i] = __builtin_fmaf(x0, cs, -(x1 * sn));
+        row[i + half] = __builtin_fmaf(x0, sn, x1 * cs);
+    }
+    wave_lds_sync();
+    if (P.fwht) {
+        for (uint32_t j = l; j < P.width; j += kWave) fr[j] *= P.fwht_scale;
+        wave_lds_sync();
+        const uint32_t hn = P.fwht / 2;
+        for (uint32_t hs = 1; hs < P.fwht; hs *= 2) {
+            for (uint32_t q = l; q < P.width / 2; q += kWave) {
+                const uint32_t g = q / hn, w = q % hn;
+                const uint32_t a = g * P.fwht + (w / hs) * 2 * hs + w % hs;
+                const float x = fr[a], y = fr[a + hs];
+                fr[a] = x + y;
+                fr[a + hs] = x - y;
+            }
+            wave_lds_sync();
+        }
+    }
+    for (uint32_t b = l; b < bpr; b += kWave) {
+        if (P.format == kFmtQ8) quant_block_q8(fr + b * kQK, raw + b * kQ8Bytes);
+        else quant_block_q40(fr + b * kQK, raw + b * kQ40Bytes);
+    }
+    wave_lds_sync();
 }
 
 // Persistent: a bounded grid loops over (lane, slot, plane, chunk) items, so
@@ -1680,6 +1801,15 @@ __global__ __launch_bounds__(256) void k_gather(GatherArgs a) {
         }
         wave_copy(src, wl, sbytes);
         wave_lds_sync();
+        if (P.mode == kModeRopeFwht) {
+            // binary32 row after the staged rows (16-byte aligned)
+            float *fr = reinterpret_cast<float *>(wl + ((sbytes + 15u) & ~15u));
+            for (uint32_t r = 0; r < nr; ++r)
+                rope_fwht_row(P, wl + r * P.src_row, fr, P.pos_base + int64_t(first + r0 + r));
+            wave_copy(wl, dst, sbytes);
+            wave_lds_sync();  // the slice is refilled by the next item
+            continue;
+        }
         const uint32_t bpr = P.width / kQK;
         const uint32_t bbytes = P.format == kFmtQ8 ? kQ8Bytes : kQ41Bytes;
         const uint32_t nblocks = nr * bpr;
@@ -1913,7 +2043,8 @@ hipError_t launch_gather(const GatherArgs &a, hipStream_t s) {
     for (uint32_t i = 0; i < a.n_planes; ++i) {
         const GatherPlane &p = a.plane[i];
         if (p.mode == kModeCopy || p.format == kFmtF16) continue;
-        const uint32_t need = (a.chunk_rows * p.src_row + 15u) & ~15u;
+        uint32_t need = (a.chunk_rows * p.src_row + 15u) & ~15u;
+        if (p.mode == kModeRopeFwht) need += p.width * 4;  // the binary32 row
         g.lds_per_wave = need > g.lds_per_wave ? need : g.lds_per_wave;
     }
     const uint32_t wpb = a.threads / kWave;

@@ -56,6 +56,13 @@ def _load_oracle() -> C.CDLL:
         "orc_dequant_q4_1": (None, [_P, _P]),
         "orc_quant_q8_0": (None, [_P, _P]),
         "orc_dequant_q4_0": (None, [_P, _P]),
+        "orc_quant_q4_0": (None, [_P, _P]),
+        "orc_rope_sincos": (None, [C.c_float, _P, _P]),
+        "orc_rope_neox_row": (None, [_P, _u32, _u32, _u32, _P, C.c_float]),
+        "orc_fwht_row": (None, [_P, _u32, _u32]),
+        "orc_rope_fwht_rows": (C.c_int, [_P, C.c_int, _u32, _u32, C.c_int64, _u32, _u32, _P, _u32, _P]),
+        "orc_gather_rope": (C.c_int, [_P, C.c_int, _u32, _u64, _u32, _P, _u32, _u32, _u32, _P, _u32,
+                                      C.c_int64, _P]),
         "orc_dequant_q5_0": (None, [_P, _P]),
         "orc_attention_page_mass": (C.c_int, [_P, C.c_int, C.c_size_t, C.c_size_t, _P, C.c_int, C.c_size_t,
                                               C.c_size_t, _P, C.c_int, C.c_size_t, _u32, _u32, _u32, _u32,
@@ -254,6 +261,56 @@ def attention_page_mass(q: np.ndarray, q_fmt: int, q_row_stride: int, q_head_str
                                        k_row_stride, k_head_stride, _ptr(mask), mask_fmt, mask_row_stride,
                                        head_dim, query_heads, kv_heads, tokens, page_tokens, scale, softcap,
                                        _ptr(r), len(r), _ptr(out)))
+    return out
+
+
+def quant_q4_0(x: np.ndarray) -> np.ndarray:
+    x = _c(x, np.float32)
+    out = np.zeros(Q4_0_BYTES, np.uint8)
+    lib.orc_quant_q4_0(_ptr(x), _ptr(out))
+    return out
+
+
+def rope_sincos(angle: float):
+    s, c = C.c_float(), C.c_float()
+    lib.orc_rope_sincos(angle, C.byref(s), C.byref(c))
+    return s.value, c.value
+
+
+def rope_neox_row(row: np.ndarray, head_dim: int, n_rot: int, theta: np.ndarray, pos: float) -> np.ndarray:
+    r = np.array(row, np.float32)
+    th = _c(theta, np.float32)
+    lib.orc_rope_neox_row(_ptr(r), r.size, head_dim, n_rot, _ptr(th), pos)
+    return r
+
+
+def fwht_row(row: np.ndarray, n: int) -> np.ndarray:
+    r = np.array(row, np.float32)
+    lib.orc_fwht_row(_ptr(r), r.size, n)
+    return r
+
+
+def rope_fwht_rows(rows: np.ndarray, fmt: int, width: int, n: int, pos0: int, head_dim: int, n_rot: int,
+                   theta: np.ndarray, fwht: int) -> np.ndarray:
+    rows = _c(rows, np.uint8)
+    th = _c(theta if theta is not None else np.zeros(1), np.float32)
+    out = np.zeros_like(rows)
+    _check(lib.orc_rope_fwht_rows(_ptr(rows), fmt, width, n, pos0, head_dim, n_rot, _ptr(th), fwht, _ptr(out)))
+    return out
+
+
+def gather_rope(history: np.ndarray, fmt: int, width: int, tokens: int, page_tokens: int,
+                selected: Sequence[int], head_dim: int, n_rot: int, theta: np.ndarray, fwht: int,
+                pos_base: int = 0, slots: Optional[np.ndarray] = None) -> np.ndarray:
+    """Slots [k][page_tokens][row] of the raw-K transform gather; rows past a
+    partial last page keep `slots`' bytes (zero by default)."""
+    h = _c(history, np.uint8)
+    sel = _c(np.asarray(selected), np.uint32)
+    th = _c(theta if theta is not None else np.zeros(1), np.float32)
+    row = width // QK * (Q8_0_BYTES if fmt == FMT_Q8_0 else Q4_0_BYTES)
+    out = np.zeros(len(sel) * page_tokens * row, np.uint8) if slots is None else np.array(slots, np.uint8)
+    _check(lib.orc_gather_rope(_ptr(h), fmt, width, tokens, page_tokens, _ptr(sel), len(sel), head_dim, n_rot,
+                               _ptr(th), fwht, pos_base, _ptr(out)))
     return out
 
 

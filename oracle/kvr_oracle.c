@@ -664,3 +664,149 @@ int orc_attention_page_mass(const uint8_t *q, int q_fmt, size_t q_row_stride, si
     free(query), free(key), free(bias), free(logits);
     return ORC_OK;
 }
+
+/* ---------------------------------------------------------------------- */
+/* Raw-K stage-in transform (kvmem_stagein_enqueue_k + flush,              */
+/* src/adapter/llama-kvmem-stagein.cu:105-234, 746-783, 817-858): decode   */
+/* q8_0/q4_0, NeoX RoPE at each token's position, Walsh-Hadamard over runs */
+/* of `fwht` values (scaled by 1/sqrt(fwht) first, butterflies in the      */
+/* reference's loop order), requantize to the source format.               */
+/* ---------------------------------------------------------------------- */
+
+/* sin and cos of a binary32 angle, each rounded once from a binary64
+ * evaluation: reduction by the nearest multiple k of pi/2 (Cody-Waite, two
+ * binary64 parts, fused), Taylor polynomials of degree 21 / 20 on
+ * |r| <= pi/4, quadrant k mod 4.  The device runs the same operations
+ * (within 1 ulp of the reference's sincosf, which is not reproducible on
+ * another machine). */
+void orc_rope_sincos(float angle, float *s, float *c) {
+    const double x = angle;
+    const double k = rint(x * 0.6366197723675814);
+    double r = fma(-k, 1.5707963267948966, x);
+    r = fma(-k, 6.123233995736766e-17, r);
+    const double r2 = r * r;
+    double ps = 1.9572941063391263e-20;
+    ps = fma(ps, r2, -8.22063524662433e-18);
+    ps = fma(ps, r2, 2.8114572543455206e-15);
+    ps = fma(ps, r2, -7.647163731819816e-13);
+    ps = fma(ps, r2, 1.6059043836821613e-10);
+    ps = fma(ps, r2, -2.505210838544172e-08);
+    ps = fma(ps, r2, 2.7557319223985893e-06);
+    ps = fma(ps, r2, -0.0001984126984126984);
+    ps = fma(ps, r2, 0.008333333333333333);
+    ps = fma(ps, r2, -0.16666666666666666);
+    const double sr = fma(r * r2, ps, r);
+    double pc = 4.110317623312165e-19;
+    pc = fma(pc, r2, -1.5619206968586225e-16);
+    pc = fma(pc, r2, 4.779477332387385e-14);
+    pc = fma(pc, r2, -1.1470745597729725e-11);
+    pc = fma(pc, r2, 2.08767569878681e-09);
+    pc = fma(pc, r2, -2.755731922398589e-07);
+    pc = fma(pc, r2, 2.48015873015873e-05);
+    pc = fma(pc, r2, -0.001388888888888889);
+    pc = fma(pc, r2, 0.041666666666666664);
+    pc = fma(pc, r2, -0.5);
+    const double cr = fma(r2, pc, 1.0);
+    const unsigned q = (unsigned)((int64_t)k) & 3u;
+    *s = (float)(q == 0 ? sr : q == 1 ? cr : q == 2 ? -sr : -cr);
+    *c = (float)(q == 0 ? cr : q == 1 ? -sr : q == 2 ? -cr : sr);
+}
+
+/* quant_q4_0 (stagein.cu:201-234); the reference's x*id + 8.5 is taken as
+ * one fused multiply-add (a CUDA compiler contracts it by default). */
+void orc_quant_q4_0(const float *x, uint8_t *block) {
+    float amax = 0.0f, vmax = 0.0f;
+    for (int j = 0; j < ORC_QK; ++j)
+        if (amax < fabsf(x[j])) {
+            amax = fabsf(x[j]);
+            vmax = x[j];
+        }
+    const float d = vmax / -8.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    store_u16(block, orc_f32_to_f16(d));
+    for (int j = 0; j < ORC_QK / 2; ++j) {
+        int x0 = (int)fmaf(x[j], id, 8.5f), x1 = (int)fmaf(x[j + ORC_QK / 2], id, 8.5f);
+        if (x0 > 15) x0 = 15;
+        if (x1 > 15) x1 = 15;
+        block[2 + j] = (uint8_t)((x0 & 15) | ((x1 & 15) << 4));
+    }
+}
+
+/* NeoX rotation of one token row (rope_neox_kernel, stagein.cu:160-178):
+ * in each head, (i, i + n_rot/2) by pos*theta[i]; x0*c - x1*s and
+ * x0*s + x1*c with the first product fused. */
+void orc_rope_neox_row(float *row, uint32_t width, uint32_t head_dim, uint32_t n_rot, const float *theta,
+                       float pos) {
+    const uint32_t half = n_rot / 2;
+    for (uint32_t h = 0; h < width / head_dim; ++h) {
+        float *x = row + (size_t)h * head_dim;
+        for (uint32_t i = 0; i < half; ++i) {
+            float s, c;
+            orc_rope_sincos(pos * theta[i], &s, &c);
+            const float x0 = x[i], x1 = x[i + half];
+            x[i] = fmaf(x0, c, -(x1 * s));
+            x[i + half] = fmaf(x0, s, x1 * c);
+        }
+    }
+}
+
+/* fwht_kernel (stagein.cu:105-130) on each run of n values of a row. */
+void orc_fwht_row(float *row, uint32_t width, uint32_t n) {
+    const float scale = 1.0f / sqrtf((float)n);
+    for (uint32_t g = 0; g < width / n; ++g) {
+        float *t = row + (size_t)g * n;
+        for (uint32_t i = 0; i < n; ++i) t[i] = t[i] * scale;
+        for (uint32_t h = 1; h < n; h *= 2)
+            for (uint32_t i = 0; i < n; i += 2 * h)
+                for (uint32_t j = 0; j < h; ++j) {
+                    const float a = t[i + j], b = t[i + j + h];
+                    t[i + j] = a + b;
+                    t[i + j + h] = a - b;
+                }
+    }
+}
+
+int orc_rope_fwht_rows(const uint8_t *rows, int fmt, uint32_t width, uint32_t n, int64_t pos0,
+                       uint32_t head_dim, uint32_t n_rot, const float *theta, uint32_t fwht, uint8_t *out) {
+    if ((fmt != ORC_FMT_Q8_0 && fmt != ORC_FMT_Q4_0) || !width || width % ORC_QK || !head_dim ||
+        width % head_dim || n_rot % 2 || n_rot > head_dim || (n_rot && !theta) ||
+        (fwht && (width % fwht || (fwht != 64 && fwht != 128 && fwht != 256 && fwht != 512))))
+        return ORC_ERR_ARG;
+    const uint32_t bb = fmt == ORC_FMT_Q8_0 ? ORC_Q8_0_BYTES : ORC_Q4_0_BYTES, bpr = width / ORC_QK;
+    float *row = (float *)malloc(sizeof(float) * width);
+    if (!row) return ORC_ERR_ARG;
+    for (uint32_t t = 0; t < n; ++t) {
+        const uint8_t *in = rows + (size_t)t * bpr * bb;
+        uint8_t *o = out + (size_t)t * bpr * bb;
+        for (uint32_t b = 0; b < bpr; ++b) {
+            if (fmt == ORC_FMT_Q8_0) orc_dequant_q8_0(in + (size_t)b * bb, row + (size_t)b * ORC_QK);
+            else orc_dequant_q4_0(in + (size_t)b * bb, row + (size_t)b * ORC_QK);
+        }
+        orc_rope_neox_row(row, width, head_dim, n_rot, theta, (float)(pos0 + t));
+        if (fwht) orc_fwht_row(row, width, fwht);
+        for (uint32_t b = 0; b < bpr; ++b) {
+            if (fmt == ORC_FMT_Q8_0) orc_quant_q8_0(row + (size_t)b * ORC_QK, o + (size_t)b * bb);
+            else orc_quant_q4_0(row + (size_t)b * ORC_QK, o + (size_t)b * bb);
+        }
+    }
+    free(row);
+    return ORC_OK;
+}
+
+/* The gather with the raw-K transform: slot s of the selection holds page
+ * selected[s]'s rows transformed at their positions pos_base + t. */
+int orc_gather_rope(const uint8_t *history, int fmt, uint32_t width, uint64_t tokens, uint32_t page_tokens,
+                    const uint32_t *selected, uint32_t k, uint32_t head_dim, uint32_t n_rot,
+                    const float *theta, uint32_t fwht, int64_t pos_base, uint8_t *slots) {
+    const uint32_t bb = fmt == ORC_FMT_Q8_0 ? ORC_Q8_0_BYTES : ORC_Q4_0_BYTES;
+    const size_t row = (size_t)width / ORC_QK * bb;
+    for (uint32_t s = 0; s < k; ++s) {
+        const uint64_t first = (uint64_t)selected[s] * page_tokens;
+        if (first >= tokens) continue;
+        const uint32_t valid = (uint32_t)(tokens - first < page_tokens ? tokens - first : page_tokens);
+        const int rc = orc_rope_fwht_rows(history + first * row, fmt, width, valid, pos_base + (int64_t)first,
+                                          head_dim, n_rot, theta, fwht, slots + (size_t)s * page_tokens * row);
+        if (rc) return rc;
+    }
+    return ORC_OK;
+}

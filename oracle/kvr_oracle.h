@@ -26,6 +26,16 @@
  *                                    no reference test holds q4_1 bytes)
  *   orc_dequant_q4_0 / q5_0          hand-built blocks with known codes (the
  *                                    layouts of llama-kvmem-attention-cuda.cu:31-56)
+ *   orc_rope_sincos                  numpy sin/cos of the binary32 angle (within
+ *                                    1 ulp; the device runs the same operations)
+ *   orc_rope_neox_row / orc_fwht_row the rotation's closed form (pair norms,
+ *                                    angle 0 is the identity, a rotation and its
+ *                                    inverse); Walsh-Hadamard applied twice is
+ *                                    the identity, a unit vector gives a
+ *                                    Hadamard row
+ *   orc_quant_q4_0 / orc_rope_fwht_rows  hand-built blocks; the transform with
+ *                                    no rotation and no Walsh-Hadamard returns
+ *                                    blocks whose extreme code is full scale
  *   orc_attention_page_mass          closed forms (uniform logits -> token
  *                                    shares, two-token logistic, softcap tanh,
  *                                    masked tokens and pages, mass sums to 1)
@@ -107,6 +117,18 @@ void orc_dequant_q4_1(const uint8_t *block, float *y);
 void orc_quant_q8_0(const float *x, uint8_t *block);
 void orc_dequant_q4_0(const uint8_t *block, float *y);
 void orc_dequant_q5_0(const uint8_t *block, float *y);
+void orc_quant_q4_0(const float *x, uint8_t *block);
+
+/* ---- raw-K stage-in transform ------------------------------------------- */
+void orc_rope_sincos(float angle, float *s, float *c);
+void orc_rope_neox_row(float *row, uint32_t width, uint32_t head_dim, uint32_t n_rot, const float *theta,
+                       float pos);
+void orc_fwht_row(float *row, uint32_t width, uint32_t n);
+int orc_rope_fwht_rows(const uint8_t *rows, int fmt, uint32_t width, uint32_t n, int64_t pos0,
+                       uint32_t head_dim, uint32_t n_rot, const float *theta, uint32_t fwht, uint8_t *out);
+int orc_gather_rope(const uint8_t *history, int fmt, uint32_t width, uint64_t tokens, uint32_t page_tokens,
+                    const uint32_t *selected, uint32_t k, uint32_t head_dim, uint32_t n_rot,
+                    const float *theta, uint32_t fwht, int64_t pos_base, uint8_t *slots);
 
 /* ---- sampled attention (attention-feedback observer) ------------------ */
 /* out: double [n_rows][ceil(tokens/page_tokens)].  Operands are host copies
