@@ -386,6 +386,10 @@ WORKLOADS = {
     # 8 lanes x 262144 tokens, 40/8 heads, 4 query rows (matrix-core logits), top-64 per lane
     "lanes8": dict(layers=1, repeat=8, lanes=8, T=262144, HQ=40, HKV=8, D=128, PT=256, R=4, K=64,
                    agg="mean", kfmt="f16", vfmt="f16", kmode="copy", vmode="copy", resident=False),
+    # raw q8_0 K staged with the transform (decode, NeoX RoPE at the original
+    # position, Walsh-Hadamard over 128, requantize) + fp16 V copied
+    "rawk": dict(layers=16, repeat=1, lanes=1, T=131072, HQ=32, HKV=8, D=128, PT=256, R=1, K=32,
+                 agg="mean", kfmt="q8_0", vfmt="f16", kmode="rope_fwht", vmode="copy", resident=False),
     # 40 layers x 1048576 tokens, 16/2 heads, D 256, q8_0 K + fp16 V, resident
     # summaries, top-48 (pinned history aliased over a ring of 4 layers)
     "layerwise40": dict(layers=40, repeat=1, lanes=1, T=1048576, HQ=16, HKV=2, D=256, PT=256, R=1, K=48,
@@ -412,7 +416,10 @@ def run_workload(args):
     fmt = {"f16": K.FMT_F16, "f16_scaled": K.FMT_F16, "q8_0": K.FMT_Q8_0, "q4_1": K.FMT_Q4_1}
     row = lambda f: K.row_bytes(fmt[f], W)
     kfmt, vfmt = fmt[w["kfmt"]], fmt[w["vfmt"]]
-    mode = {"copy": K.GATHER_COPY, "dequant": K.GATHER_DEQUANT_F16}
+    mode = {"copy": K.GATHER_COPY, "dequant": K.GATHER_DEQUANT_F16, "rope_fwht": K.GATHER_ROPE_FWHT}
+    # rotation angles of the raw-K transform: theta_i = 10000^(-2i/D)
+    theta = torch.from_numpy((10000.0 ** (-np.arange(D // 2) * 2 / D)).astype(np.float32)).cuda()
+    rope = dict(head_dim=D, n_rot=D, theta=theta, fwht=128, pos_base=0) if w["kmode"] == "rope_fwht" else None
     agg = {"mean": K.AGG_MEAN, "max": K.AGG_MAX}[w["agg"]]
     seed = args.seed
     log(f"workload {args.workload}: {L} layer(s) x {NL} lane(s) x {T} tokens, Hq {HQ}/Hkv {HKV}, D {D}, "
@@ -484,7 +491,7 @@ def run_workload(args):
     log(f"inputs ready ({ring} pinned K/V set(s) of {kb >> 20} + {vb >> 20} MiB)")
 
     def desc(l, with_planes, ev=(None, None), se=None):
-        planes = [K.make_plane(pins[l % ring][0], kfmt, W, T, mode[w["kmode"]], kslots[l]),
+        planes = [K.make_plane(pins[l % ring][0], kfmt, W, T, mode[w["kmode"]], kslots[l], rope=rope),
                   K.make_plane(pins[l % ring][1], vfmt, W, T, mode[w["vmode"]], vslots[l])]
         src = dict(keys=None, pages=P, page_tokens=PT, lanes=NL) if w["resident"] else \
             dict(keys=K.make_keys(dev_k[l], kfmt, T, HKV, D, PT, lanes=NL))
@@ -534,10 +541,11 @@ def run_workload(args):
     stage = []
     for rep in range(2):
         for l in range(L):
-            planes = [K.make_plane(pins[l % ring][0], kfmt, W, T, mode[w["kmode"]], kslots[l]),
+            planes = [K.make_plane(pins[l % ring][0], kfmt, W, T, mode[w["kmode"]], kslots[l], rope=rope),
                       K.make_plane(pins[l % ring][1], vfmt, W, T, mode[w["vmode"]], vslots[l])]
             hip.record(ev_a, ctx.copy_stream)
-            ctx.stage_in(planes, PT, sel[l], cnt[l], KSEL, lanes=NL)
+            ctx.stage_in(planes, PT, sel[l], cnt[l], KSEL, lanes=NL,
+                         engine={"auto": K.ENGINE_AUTO, "kernel": K.ENGINE_KERNEL, "sdma": K.ENGINE_SDMA}[args.engine])
             hip.record(ev_b, ctx.copy_stream)
             ctx.check()
             if rep:

@@ -108,7 +108,7 @@ typedef enum kvr_gather_mode {
  * Walsh-Hadamard transformed. */
 typedef struct kvr_rope {
     uint32_t head_dim;     /* width is a multiple of it */
-    uint32_t n_rot;        /* even, at most head_dim (0: no rotation) */
+    uint32_t n_rot;        /* even, at most head_dim and 512 (0: no rotation) */
     const float *theta;    /* dev, n_rot/2 values */
     uint32_t fwht;         /* 0, 64, 128, 256 or 512; divides width */
     int64_t pos_base;

@@ -45,6 +45,7 @@ struct kvr_context {
     // tuning
     uint32_t gather_wgs = 0;  // 0: by mode (kDefaultGatherWgs / kDefaultDecodeGatherWgs)
     uint32_t chunk_rows = 8;
+    bool chunk_rows_set = false;  // chosen by the caller (else by the planes)
     uint32_t gather_threads = 0;  // 0: by mode
 };
 
@@ -441,9 +442,9 @@ kvr_status check_planes(const kvr_plane *planes, uint32_t n, uint32_t lanes, uin
             // kvmem_stagein_enqueue_k / rope_neox / fwht_ok (stagein.cu:477-479, 534-541, 817-831)
             const kvr_rope *r = p.rope;
             if (!r || !r->head_dim || p.width % r->head_dim || r->n_rot % 2 || r->n_rot > r->head_dim ||
-                (r->n_rot && !r->theta))
+                r->n_rot > 512 || (r->n_rot && !r->theta))
                 return fail(KVR_ERR_INVALID, "plane %u: raw-K transform needs head_dim dividing the width, an even "
-                                             "n_rot <= head_dim and its theta", i);
+                                             "n_rot <= min(head_dim, 512) and its theta", i);
             if (r->fwht && ((r->fwht != 64 && r->fwht != 128 && r->fwht != 256 && r->fwht != 512) ||
                             p.width % r->fwht))
                 return fail(KVR_ERR_INVALID, "plane %u: Walsh-Hadamard size must be 64, 128, 256 or 512 and "
@@ -498,6 +499,15 @@ kvr_status check_planes(const kvr_plane *planes, uint32_t n, uint32_t lanes, uin
 constexpr uint32_t kDefaultGatherWgs = 16, kDefaultGatherThreads = 64;               // copies
 constexpr uint32_t kDefaultDecodeGatherWgs = 32, kDefaultDecodeGatherThreads = 256;  // decoding planes
 constexpr uint32_t kDefaultChunkRows = 8;
+// The raw-K transform is a chain of dependent LDS phases per row: one row
+// per work item and a grid of 1024 workgroups keep many waves per SIMD to
+// hide them (8 rows per item and 32 workgroups left one wave per SIMD).
+constexpr uint32_t kRawKChunkRows = 1, kRawKGatherWgs = 1024;
+bool has_raw_k(const PlanePlan *pp, uint32_t n) {
+    for (uint32_t i = 0; i < n; ++i)
+        if (pp[i].g.mode == KVR_GATHER_ROPE_FWHT) return true;
+    return false;
+}
 
 // Rows per gather work item: the context's setting, bounded by the page and
 // by the LDS a staged decode needs (source rows + requantized rows).
@@ -526,14 +536,19 @@ kvr_status enqueue_gather_kernel(kvr_context *ctx, const PlanePlan *pp, uint32_t
     ga.lanes = lanes;
     ga.k = k;
     ga.page_tokens = page_tokens;
-    ga.chunk_rows = gather_chunk_rows(ctx->chunk_rows, 256, pp, n, page_tokens);
+    const bool raw_k = has_raw_k(pp, n);
+    ga.chunk_rows = gather_chunk_rows(ctx->chunk_rows_set || !raw_k ? ctx->chunk_rows : kRawKChunkRows, 256, pp, n,
+                                      page_tokens);
     ga.chunks = (page_tokens + ga.chunk_rows - 1) / ga.chunk_rows;
     ga.selected = selected;
     ga.count = count;
     bool decode = false;
     for (uint32_t i = 0; i < n; ++i)
         decode = decode || (pp[i].g.mode != KVR_GATHER_COPY && pp[i].g.format != KVR_FMT_F16);
-    ga.workgroups = ctx->gather_wgs ? ctx->gather_wgs : decode ? kDefaultDecodeGatherWgs : kDefaultGatherWgs;
+    ga.workgroups = ctx->gather_wgs ? ctx->gather_wgs
+                    : raw_k         ? kRawKGatherWgs
+                    : decode        ? kDefaultDecodeGatherWgs
+                                    : kDefaultGatherWgs;
     ga.threads = ctx->gather_threads ? ctx->gather_threads : decode ? kDefaultDecodeGatherThreads
                                                                      : kDefaultGatherThreads;
     KVR_HIP(kvr::launch_gather(ga, s));
@@ -628,7 +643,9 @@ kvr_status enqueue_gather_sdma(kvr_context *ctx, PlanePlan *pp, uint32_t n, uint
         ga.lanes = lanes;
         ga.k = k;
         ga.page_tokens = page_tokens;
-        ga.chunk_rows = gather_chunk_rows(ctx->chunk_rows, 256, &p, 1, page_tokens);
+        const bool raw_k = p.g.mode == KVR_GATHER_ROPE_FWHT;
+        ga.chunk_rows = gather_chunk_rows(ctx->chunk_rows_set || !raw_k ? ctx->chunk_rows : kRawKChunkRows, 256, &p,
+                                          1, page_tokens);
         ga.chunks = (page_tokens + ga.chunk_rows - 1) / ga.chunk_rows;
         ga.workgroups = 1024;  // HBM -> HBM: use the whole GPU
         ga.threads = 256;
@@ -736,6 +753,7 @@ kvr_status kvr_set_option(kvr_context *ctx, kvr_option option, int64_t value) {
     case KVR_OPT_GATHER_CHUNK_ROWS:
         if (value < 0 || value > 64) return fail(KVR_ERR_INVALID, "gather chunk rows must be in [0, 64]");
         ctx->chunk_rows = value ? uint32_t(value) : kDefaultChunkRows;
+        ctx->chunk_rows_set = value != 0;
         return KVR_OK;
     case KVR_OPT_GATHER_THREADS:
         if (value != 0 && value != 64 && value != 128 && value != 256)

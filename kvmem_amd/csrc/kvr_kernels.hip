@@ -1683,31 +1683,62 @@ __device__ __forceinline__ void rope_sincos(float angle, float &s, float &c) {
 // (h = 1, 2, 4, ...: (a, b) -> (a+b, a-b), as the reference's loop nest),
 // then requantize the row in place.  One wave; LDS order within a wave is
 // program order, with a wave fence between phases.
-__device__ __forceinline__ void rope_fwht_row(const GatherPlane &P, uint8_t *raw, float *fr, int64_t pos) {
-    const uint32_t l = threadIdx.x & 63, bpr = P.width / kQK;
-    const uint32_t bbytes = P.format == kFmtQ8 ? kQ8Bytes : kQ40Bytes;
-    for (uint32_t b = l; b < bpr; b += kWave) decode_block(raw + b * bbytes, P.format, fr + b * kQK);
+// The transform's parameters of one work item, read once: uniform values
+// and the lane's own rotation angle (theta of pair index = lane).
+struct RopeRow {
+    uint32_t width, head_dim, half, fwht, fwht_log2;
+    float fwht_scale;
+    bool q8;
+    float theta_l[4];  // pair indices lane + 64k (half <= 256)
+};
+__device__ __forceinline__ void rope_fwht_row(const RopeRow &P, uint8_t *raw, float *fr, int64_t pos) {
+    const uint32_t l = threadIdx.x & 63;
+    const bool q8 = P.q8;
+    const uint32_t bbytes = q8 ? kQ8Bytes : kQ40Bytes;
+    // one element per lane, consecutive across the wave (a lane per block
+    // would put the 32 lanes' row accesses in one LDS bank)
+#pragma unroll 4
+    for (uint32_t e = l; e < P.width; e += kWave) {
+        const uint8_t *blk = raw + (e / kQK) * bbytes;
+        const uint32_t j = e % kQK;
+        const float d = h2f(ld_u16(blk));
+        const uint8_t byte = blk[2 + (q8 ? j : j % 16)];
+        const int code = q8 ? int(int8_t(byte)) : int(j < 16 ? byte & 15 : byte >> 4) - 8;
+        fr[e] = float(code) * d;
+    }
     wave_lds_sync();
-    const uint32_t half = P.n_rot / 2, heads = P.width / P.head_dim;
+    // the angle depends on the pair index and the position, not the head:
+    // one sin/cos per pair index, applied to every head
+    const uint32_t half = P.half, heads = P.width / P.head_dim;
     const float fpos = float(pos);
-    for (uint32_t e = l; e < heads * half; e += kWave) {
-        const uint32_t h = e / half, i = e % half;
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) {
+        const uint32_t i = l + k * kWave;
+        if (i >= half) break;
         float sn, cs;
-        rope_sincos(fpos * P.theta[i], sn, cs);
-        float *row = fr + h * P.head_dim;
-        const float x0 = row[i], x1 = row[i + half];
-        row[i] = __builtin_fmaf(x0, cs, -(x1 * sn));
-        row[i + half] = __builtin_fmaf(x0, sn, x1 * cs);
+        rope_sincos(fpos * P.theta_l[k], sn, cs);
+#pragma unroll 4
+        for (uint32_t h = 0; h < heads; ++h) {
+            float *row = fr + h * P.head_dim;
+            const float x0 = row[i], x1 = row[i + half];
+            row[i] = __builtin_fmaf(x0, cs, -(x1 * sn));
+            row[i + half] = __builtin_fmaf(x0, sn, x1 * cs);
+        }
     }
     wave_lds_sync();
     if (P.fwht) {
+#pragma unroll 4
         for (uint32_t j = l; j < P.width; j += kWave) fr[j] *= P.fwht_scale;
         wave_lds_sync();
-        const uint32_t hn = P.fwht / 2;
-        for (uint32_t hs = 1; hs < P.fwht; hs *= 2) {
+        // sizes are powers of two: butterfly q of a stage is run q >> (log2 - 1),
+        // index w within it; pairs (a, a + hs)
+        const uint32_t lh = P.fwht_log2 - 1;
+        for (uint32_t ls = 0; ls <= lh; ++ls) {
+            const uint32_t hs = 1u << ls;
+#pragma unroll 4
             for (uint32_t q = l; q < P.width / 2; q += kWave) {
-                const uint32_t g = q / hn, w = q % hn;
-                const uint32_t a = g * P.fwht + (w / hs) * 2 * hs + w % hs;
+                const uint32_t g = q >> lh, w = q & ((1u << lh) - 1u);
+                const uint32_t a = (g << P.fwht_log2) + ((w >> ls) << (ls + 1)) + (w & (hs - 1u));
                 const float x = fr[a], y = fr[a + hs];
                 fr[a] = x + y;
                 fr[a + hs] = x - y;
@@ -1715,9 +1746,49 @@ __device__ __forceinline__ void rope_fwht_row(const GatherPlane &P, uint8_t *raw
             wave_lds_sync();
         }
     }
-    for (uint32_t b = l; b < bpr; b += kWave) {
-        if (P.format == kFmtQ8) quant_block_q8(fr + b * kQK, raw + b * kQ8Bytes);
-        else quant_block_q40(fr + b * kQK, raw + b * kQ40Bytes);
+    // requantize: each half wave one block, lane j its element
+    for (uint32_t e0 = 0; e0 < P.width; e0 += kWave) {
+        const uint32_t e = e0 + l, j = l % kQK;
+        const bool on = e < P.width;  // uniform per half wave (width % 32 == 0)
+        const float x = on ? fr[e] : 0.0f;
+        uint8_t *blk = raw + (min(e, P.width - 1) / kQK) * bbytes;
+        if (q8) {
+            // quant_q8_0 (stagein.cu:181-199): d = amax/127, q = roundf(x*id)
+            float amax = dpp::group_reduce(fabsf(x), 16, dpp::Max());
+            amax = fmaxf(amax, __shfl_xor(amax, 16, kWave));
+            const float d = amax / 127.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+            if (on) {
+                blk[2 + j] = uint8_t(int8_t(roundf(x * id)));
+                if (j == 0) {
+                    const uint16_t dh = f2h(d);
+                    blk[0] = uint8_t(dh);
+                    blk[1] = uint8_t(dh >> 8);
+                }
+            }
+        } else {
+            // quant_q4_0 (stagein.cu:201-234): the first element of largest
+            // magnitude sets d = v / -8 (argmax key: |x| bits, then lower index)
+            uint64_t key = (uint64_t(__float_as_uint(fabsf(x))) << 32) | (31u - j);
+            key = dpp::group_reduce(key, 16, dpp::Max());
+            const uint64_t other = (uint64_t(uint32_t(__shfl_xor(int(key >> 32), 16, kWave))) << 32) |
+                                   uint32_t(__shfl_xor(int(uint32_t(key)), 16, kWave));
+            key = other > key ? other : key;
+            const uint32_t src = (l & 32u) | (31u - uint32_t(key & 31u));
+            const float vmax = __shfl(x, int(src), kWave);
+            const float d = vmax / -8.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+            const int c = min(int(__builtin_fmaf(x, id, 8.5f)), 15);
+            const int hi = __shfl_down(c, 16, kWave);  // element j + 16 of the block
+            if (on && j < 16) {
+                blk[2 + j] = uint8_t((c & 15) | ((hi & 15) << 4));
+                if (j == 0) {
+                    const uint16_t dh = f2h(d);
+                    blk[0] = uint8_t(dh);
+                    blk[1] = uint8_t(dh >> 8);
+                }
+            }
+        }
     }
     wave_lds_sync();
 }
@@ -1766,7 +1837,9 @@ __device__ __forceinline__ void wave_copy(const uint8_t *src, uint8_t *dst, uint
 // (no workgroup barrier), decode whole blocks from there and write fp16
 // rows, or requantize in place and copy the slice out.
 __global__ __launch_bounds__(256) void k_gather(GatherArgs a) {
-    const uint32_t wave = threadIdx.x >> 6, l = threadIdx.x & 63, wpb = blockDim.x >> 6;
+    // the wave index as a scalar: every work item's fields are uniform
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63,
+                   wpb = blockDim.x >> 6;
     uint8_t *wl = gather_lds + wave * a.lds_per_wave;
     const uint32_t per_lane = a.k * a.n_planes * a.chunks;
     const uint64_t total = uint64_t(a.lanes) * per_lane;
@@ -1804,8 +1877,18 @@ __global__ __launch_bounds__(256) void k_gather(GatherArgs a) {
         if (P.mode == kModeRopeFwht) {
             // binary32 row after the staged rows (16-byte aligned)
             float *fr = reinterpret_cast<float *>(wl + ((sbytes + 15u) & ~15u));
+            RopeRow R;
+            R.width = P.width;
+            R.head_dim = P.head_dim;
+            R.half = P.n_rot / 2;
+            R.fwht = P.fwht;
+            R.fwht_log2 = P.fwht ? 31u - __builtin_clz(P.fwht) : 0u;
+            R.fwht_scale = P.fwht_scale;
+            R.q8 = P.format == kFmtQ8;
+#pragma unroll
+            for (uint32_t k = 0; k < 4; ++k) R.theta_l[k] = l + k * kWave < R.half ? P.theta[l + k * kWave] : 0.0f;
             for (uint32_t r = 0; r < nr; ++r)
-                rope_fwht_row(P, wl + r * P.src_row, fr, P.pos_base + int64_t(first + r0 + r));
+                rope_fwht_row(R, wl + r * P.src_row, fr, P.pos_base + int64_t(first + r0 + r));
             wave_copy(wl, dst, sbytes);
             wave_lds_sync();  // the slice is refilled by the next item
             continue;
