@@ -127,6 +127,16 @@ bool kvmem_stagein_h2d_bytes(void *gpu_dst, const void *host, size_t n);
 void kvmem_stagein_sync();
 bool kvmem_stagein_sync_checked();
 bool kvmem_stagein_enqueue_v(const void *packed, size_t nbytes, uint8_t *dst, int64_t *set_us);
+// A packed raw K record (llama-kvmem-stagein.h:37-42): nt token rows of
+// n_embd values in q8_0 or q4_0 (`ty`), rotated (NeoX, n_rot_rope dims of
+// each n_embd_head head, positions pos0 + t, theta of n_theta = n_rot_rope/2
+// host values), Walsh-Hadamard over runs of nrot (0: none), requantized into
+// dst on flush.  The record is copied into the slab; the caller's buffer is
+// reusable on return.
+bool kvmem_stagein_enqueue_k(kvr_format ty, const void *packed, size_t nbytes, uint8_t *dst, int64_t nt,
+                             int64_t n_embd, int nrot, int n_head, int n_embd_head, int n_rot_rope, int32_t pos0,
+                             const float *theta, int n_theta, int64_t *copy_us, int64_t *rope_us,
+                             int64_t *hadamard_us, int64_t *set_us);
 bool kvmem_stagein_flush(int64_t *copy_us, int64_t *rope_us, int64_t *hadamard_us, int64_t *set_us);
 bool kvmem_d2d_batched(const void *const *src, void *const *dst, const size_t *nbytes, int n);
 

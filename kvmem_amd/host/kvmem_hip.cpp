@@ -447,6 +447,18 @@ struct kvmem_gpu_state {
     std::vector<const void *> src;
     std::vector<void *> dst;
     std::vector<size_t> bytes;
+    // raw K records of the current slab: each is one gather launch on flush
+    struct KRecord {
+        const uint8_t *rows;
+        uint8_t *dst;
+        kvr_format ty;
+        uint32_t nt, n_embd, nrot, head_dim, n_rot;
+        int32_t pos0;
+    };
+    std::vector<KRecord> krec;
+    float *theta = nullptr;         // device copy of the rotation angles
+    std::vector<float> theta_host;  // what it holds
+    uint32_t *sel = nullptr;        // device {0, 1}: page 0, one page
     // decode running mean-K
     float *acc = nullptr;
     uint32_t *acc_count = nullptr;
@@ -481,6 +493,12 @@ void release_slabs(kvmem_gpu_state *st) {
     st->src.clear();
     st->dst.clear();
     st->bytes.clear();
+    st->krec.clear();
+    if (st->theta) (void)hipFree(st->theta);
+    if (st->sel) (void)hipFree(st->sel);
+    st->theta = nullptr;
+    st->sel = nullptr;
+    st->theta_host.clear();
 }
 
 int64_t micros_since(std::chrono::steady_clock::time_point t0) {
@@ -559,12 +577,40 @@ bool kvmem_stagein_flush(int64_t *copy_us, int64_t *rope_us, int64_t *hadamard_u
     if (hadamard_us) *hadamard_us = 0;
     kvmem_gpu_state *st = g_state;
     if (!st) return report("flush", "stage-in is not ready");
-    if (st->src.empty()) return true;
+    if (st->src.empty() && st->krec.empty()) return true;
     const hipStream_t s = copy_stream(st);
-    // one launch moves every queued record from the pinned slab to its rows
-    if (kvr_d2d_batched(st->ctx, st->src.data(), st->dst.data(), st->bytes.data(), uint32_t(st->src.size()), s) !=
-        KVR_OK)
+    // one launch moves every queued V record from the pinned slab to its rows
+    if (!st->src.empty() &&
+        kvr_d2d_batched(st->ctx, st->src.data(), st->dst.data(), st->bytes.data(), uint32_t(st->src.size()), s) !=
+            KVR_OK)
         return report_kvr("flush");
+    // each raw K record: one gather launch reading the slab over the host
+    // link, transforming and writing its rows (dequant, RoPE, Walsh-Hadamard
+    // and quant in one pass)
+    const auto tk = std::chrono::steady_clock::now();
+    for (const auto &r : st->krec) {
+        kvr_rope rope{};
+        rope.head_dim = r.head_dim;
+        rope.n_rot = r.n_rot;
+        rope.theta = st->theta;
+        rope.fwht = r.nrot;
+        rope.pos_base = r.pos0;
+        kvr_plane plane{};
+        plane.history = r.rows;
+        plane.format = r.ty;
+        plane.width = r.n_embd;
+        plane.tokens = r.nt;
+        plane.mode = KVR_GATHER_ROPE_FWHT;
+        plane.slots = r.dst;
+        plane.rope = &rope;
+        if (kvr_stage_in(st->ctx, &plane, 1, 1, r.nt, st->sel, st->sel + 1, 1, KVR_ENGINE_KERNEL, s) != KVR_OK) {
+            st->krec.clear();
+            return report_kvr("flush raw K");
+        }
+    }
+    const bool had_k = !st->krec.empty();
+    st->krec.clear();
+    if (had_k && rope_us) *rope_us += micros_since(tk);
     if (hipError_t e = hipEventRecord(st->slab_done[st->cur], s); e != hipSuccess) return report_hip("flush", e);
     st->slab_busy[st->cur] = true;
     st->src.clear();
@@ -590,7 +636,7 @@ bool kvmem_stagein_enqueue_v(const void *packed, size_t nbytes, uint8_t *dst, in
     if (!packed || !dst) return report("enqueue", "null record or destination");
     if (!nbytes) return true;
     if (nbytes > kvmem_gpu_state::kSlab) return report("enqueue", "record larger than the 32 MiB slab");
-    if (st->used + nbytes > kvmem_gpu_state::kSlab || st->src.size() >= 8192)
+    if (st->used + nbytes > kvmem_gpu_state::kSlab || st->src.size() + st->krec.size() >= 8192)
         if (!kvmem_stagein_flush(nullptr, nullptr, nullptr, nullptr)) return false;
     uint8_t *slot = st->slab[st->cur] + st->used;
     std::memcpy(slot, packed, nbytes);
@@ -598,6 +644,57 @@ bool kvmem_stagein_enqueue_v(const void *packed, size_t nbytes, uint8_t *dst, in
     st->dst.push_back(dst);
     st->bytes.push_back(nbytes);
     st->used += (nbytes + 15) / 16 * 16;  // keep records 16-byte aligned in the slab
+    if (set_us) *set_us += micros_since(t0);
+    return true;
+}
+
+bool kvmem_stagein_enqueue_k(kvr_format ty, const void *packed, size_t nbytes, uint8_t *dst, int64_t nt,
+                             int64_t n_embd, int nrot, int n_head, int n_embd_head, int n_rot_rope, int32_t pos0,
+                             const float *theta, int n_theta, int64_t *copy_us, int64_t *rope_us,
+                             int64_t *hadamard_us, int64_t *set_us) {
+    const auto t0 = std::chrono::steady_clock::now();
+    kvmem_gpu_state *st = g_state;
+    if (!st || !st->slab[0]) return report("enqueue K", "stage-in is not ready");
+    // stagein.cu:817-831: quantized K only, a Walsh-Hadamard size it
+    // provides, heads that tile the row
+    if (!packed || !dst || (ty != KVR_FMT_Q8_0 && ty != KVR_FMT_Q4_0))
+        return report("enqueue K", "null record or a K type other than q8_0 / q4_0");
+    if (nrot > 0 && nrot != 64 && nrot != 128 && nrot != 256 && nrot != 512)
+        return report("enqueue K", "Walsh-Hadamard size must be 64, 128, 256 or 512");
+    if (int64_t(n_head) * n_embd_head != n_embd || nt <= 0 || n_embd <= 0 || n_embd > UINT32_MAX ||
+        nt > UINT32_MAX)
+        return report("enqueue K", "head geometry does not tile the row");
+    if (n_rot_rope < 0 || n_rot_rope % 2 || n_rot_rope > n_embd_head || (n_rot_rope && (!theta || n_theta != n_rot_rope / 2)))
+        return report("enqueue K", "rotation needs an even n_rot <= head dim and n_rot/2 angles");
+    const size_t row = size_t(n_embd) / 32 * (ty == KVR_FMT_Q8_0 ? 34 : 18);
+    if (n_embd % 32 || nbytes != size_t(nt) * row) return report("enqueue K", "record size does not match its rows");
+    if (nbytes > kvmem_gpu_state::kSlab) return report("enqueue K", "record larger than the 32 MiB slab");
+    if (!st->sel) {
+        const uint32_t init[2] = {0, 1};
+        if (hipError_t e = hipMalloc(&st->sel, sizeof init); e != hipSuccess) return report_hip("enqueue K", e);
+        if (hipError_t e = hipMemcpy(st->sel, init, sizeof init, hipMemcpyHostToDevice); e != hipSuccess)
+            return report_hip("enqueue K", e);
+    }
+    if (n_rot_rope && !std::equal(theta, theta + n_theta, st->theta_host.begin(), st->theta_host.end())) {
+        // new angles: queued records still use the old ones, so flush first
+        if (!kvmem_stagein_flush(copy_us, rope_us, hadamard_us, set_us)) return false;
+        kvmem_stagein_sync();
+        if (st->theta) (void)hipFree(st->theta);
+        st->theta = nullptr;
+        if (hipError_t e = hipMalloc(&st->theta, size_t(n_theta) * sizeof(float)); e != hipSuccess)
+            return report_hip("enqueue K", e);
+        if (hipError_t e = hipMemcpy(st->theta, theta, size_t(n_theta) * sizeof(float), hipMemcpyHostToDevice);
+            e != hipSuccess)
+            return report_hip("enqueue K", e);
+        st->theta_host.assign(theta, theta + n_theta);
+    }
+    if (st->used + nbytes > kvmem_gpu_state::kSlab || st->src.size() + st->krec.size() >= 8192)
+        if (!kvmem_stagein_flush(copy_us, rope_us, hadamard_us, set_us)) return false;
+    uint8_t *slot = st->slab[st->cur] + st->used;
+    std::memcpy(slot, packed, nbytes);
+    st->krec.push_back({slot, dst, ty, uint32_t(nt), uint32_t(n_embd), uint32_t(nrot), uint32_t(n_embd_head),
+                        uint32_t(n_rot_rope), pos0});
+    st->used += (nbytes + 15) / 16 * 16;
     if (set_us) *set_us += micros_since(t0);
     return true;
 }

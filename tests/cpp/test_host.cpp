@@ -568,6 +568,56 @@ void attention() {
     require(!sampler.score(tq, bad, tm, scale, 0.0f, block, rows, out), "q4_1 keys accepted");
 }
 
+// kvmem_stagein_enqueue_k through the slab: raw q8_0 K records rotated,
+// Walsh-Hadamard transformed and requantized on flush, beside a V record;
+// bytes equal to the oracle's transform.  Rejections as the reference's.
+void stagein_raw_k() {
+    require(kh::kvmem_stagein_gpu_ready(0, 0), "gpu_ready");
+    const uint32_t nt = 37, n_embd = 256, head = 64, n_rot = 64, nrot = 64, row = n_embd / 32 * 34;
+    std::vector<float> theta(n_rot / 2);
+    for (uint32_t i = 0; i < n_rot / 2; ++i) theta[i] = std::pow(10000.0f, -2.0f * float(i) / float(n_rot));
+    const int32_t pos0[3] = {0, 4096, 777777};
+    std::vector<std::vector<uint8_t>> recs(3);
+    std::vector<Dev<uint8_t> *> dsts;
+    for (int r = 0; r < 3; ++r) {
+        recs[r].resize(size_t(nt) * row);
+        orc_synth_q8_0(12, 60 + r, uint64_t(nt) * n_embd / 32, 0.01f, 0.05f, recs[r].data());
+        dsts.push_back(new Dev<uint8_t>(recs[r].size()));
+    }
+    std::vector<uint8_t> v(4096, 0x5A);
+    Dev<uint8_t> vd(v.size());
+    for (int r = 0; r < 3; ++r)
+        require(kh::kvmem_stagein_enqueue_k(KVR_FMT_Q8_0, recs[r].data(), recs[r].size(), dsts[r]->p, nt, n_embd,
+                                            nrot, n_embd / head, head, n_rot, pos0[r], theta.data(),
+                                            int(theta.size()), nullptr, nullptr, nullptr, nullptr),
+                "enqueue_k");
+    require(kh::kvmem_stagein_enqueue_v(v.data(), v.size(), vd.p, nullptr), "enqueue_v");
+    int64_t copy_us = 0, rope_us = 0, had_us = 0, set_us = 0;
+    require(kh::kvmem_stagein_flush(&copy_us, &rope_us, &had_us, &set_us), "flush");
+    kh::kvmem_stagein_sync();
+    require(kh::kvmem_stagein_sync_checked(), "sync_checked");
+    for (int r = 0; r < 3; ++r) {
+        std::vector<uint8_t> want(recs[r].size());
+        require(orc_rope_fwht_rows(recs[r].data(), ORC_FMT_Q8_0, n_embd, nt, pos0[r], head, n_rot, theta.data(),
+                                   nrot, want.data()) == ORC_OK,
+                "oracle transform");
+        require(dsts[r]->down() == want, "raw K record differs from the oracle's transform");
+    }
+    require(vd.down() == v, "V record");
+    std::vector<uint8_t> scratch(size_t(nt) * row);
+    require(!kh::kvmem_stagein_enqueue_k(KVR_FMT_Q4_1, scratch.data(), scratch.size(), dsts[0]->p, nt, n_embd, 0,
+                                         4, head, 0, 0, nullptr, 0, nullptr, nullptr, nullptr, nullptr),
+            "q4_1 K accepted");
+    require(!kh::kvmem_stagein_enqueue_k(KVR_FMT_Q8_0, scratch.data(), scratch.size(), dsts[0]->p, nt, n_embd, 32,
+                                         4, head, 0, 0, nullptr, 0, nullptr, nullptr, nullptr, nullptr),
+            "Walsh-Hadamard 32 accepted");
+    require(!kh::kvmem_stagein_enqueue_k(KVR_FMT_Q8_0, scratch.data(), scratch.size(), dsts[0]->p, nt, n_embd, 0,
+                                         3, head, 0, 0, nullptr, 0, nullptr, nullptr, nullptr, nullptr),
+            "heads not tiling the row accepted");
+    for (auto *d : dsts) delete d;
+    kh::kvmem_stagein_gpu_free();
+}
+
 }  // namespace
 
 int main(int argc, char **argv) {
@@ -578,7 +628,7 @@ int main(int argc, char **argv) {
     if (gpu)
         tests = {{"qualification", qualification}, {"current_layer", current_layer}, {"pick", pick},
                  {"stagein", stagein},           {"meank", meank},                 {"transfer", transfer},
-                 {"capture", capture}, {"attention", attention}};
+                 {"capture", capture}, {"attention", attention}, {"stagein_raw_k", stagein_raw_k}};
     for (auto &[name, fn] : tests) {
         std::cout << "RUN  " << name << std::endl;
         try {
