@@ -140,6 +140,19 @@ bool kvmem_stagein_enqueue_k(kvr_format ty, const void *packed, size_t nbytes, u
 bool kvmem_stagein_flush(int64_t *copy_us, int64_t *rope_us, int64_t *hadamard_us, int64_t *set_us);
 bool kvmem_d2d_batched(const void *const *src, void *const *dst, const size_t *nbytes, int n);
 
+// Stage-out (llama-kvmem-stagein.h:44-50): device records packed back to
+// back into one of the two pinned slabs.  submit launches one batched copy
+// that writes them over the host link (no device staging slab) and returns
+// the slot; wait fences it; slot_base is the slot's host memory.  Not mixed
+// with pending stage-in records (either side refuses while the other has
+// records queued).
+bool kvmem_stageout_enqueue(const void *gpu_src, size_t nbytes);
+size_t kvmem_stageout_used();
+int kvmem_stageout_submit(int64_t *copy_us);
+bool kvmem_stageout_wait(int slot, int64_t *copy_us);
+const uint8_t *kvmem_stageout_slot_base(int slot);
+void kvmem_stageout_clear();
+
 // Decode running mean-K (stagein.cu:270-320, 1041-1114): one binary32 sum of
 // n_embd channels per layer on the device, added in token order and zeroed
 // by kvmem_meank_zero.  `ty` is the K element type (F32, F16 or BF16; the

@@ -459,6 +459,12 @@ struct kvmem_gpu_state {
     float *theta = nullptr;         // device copy of the rotation angles
     std::vector<float> theta_host;  // what it holds
     uint32_t *sel = nullptr;        // device {0, 1}: page 0, one page
+    // stage-out records of the current slot: (device source, slot offset, bytes)
+    std::vector<const void *> out_src;
+    std::vector<size_t> out_off, out_bytes;
+    size_t out_used = 0;
+    int out_cur = 0;
+    hipEvent_t out_done[2] = {nullptr, nullptr};
     // decode running mean-K
     float *acc = nullptr;
     uint32_t *acc_count = nullptr;
@@ -494,6 +500,14 @@ void release_slabs(kvmem_gpu_state *st) {
     st->dst.clear();
     st->bytes.clear();
     st->krec.clear();
+    st->out_src.clear();
+    st->out_off.clear();
+    st->out_bytes.clear();
+    st->out_used = 0;
+    for (int i = 0; i < 2; ++i) {
+        if (st->out_done[i]) (void)hipEventDestroy(st->out_done[i]);
+        st->out_done[i] = nullptr;
+    }
     if (st->theta) (void)hipFree(st->theta);
     if (st->sel) (void)hipFree(st->sel);
     st->theta = nullptr;
@@ -633,11 +647,14 @@ bool kvmem_stagein_enqueue_v(const void *packed, size_t nbytes, uint8_t *dst, in
     const auto t0 = std::chrono::steady_clock::now();
     kvmem_gpu_state *st = g_state;
     if (!st || !st->slab[0]) return report("enqueue", "stage-in is not ready");
+    if (!st->out_src.empty()) return report("enqueue", "stage-out records are pending");
     if (!packed || !dst) return report("enqueue", "null record or destination");
     if (!nbytes) return true;
     if (nbytes > kvmem_gpu_state::kSlab) return report("enqueue", "record larger than the 32 MiB slab");
     if (st->used + nbytes > kvmem_gpu_state::kSlab || st->src.size() + st->krec.size() >= 8192)
         if (!kvmem_stagein_flush(nullptr, nullptr, nullptr, nullptr)) return false;
+    // a fresh slab may still be the target of a stage-out copy
+    if (st->used == 0 && st->out_done[st->cur]) (void)hipEventSynchronize(st->out_done[st->cur]);
     uint8_t *slot = st->slab[st->cur] + st->used;
     std::memcpy(slot, packed, nbytes);
     st->src.push_back(slot);
@@ -655,6 +672,7 @@ bool kvmem_stagein_enqueue_k(kvr_format ty, const void *packed, size_t nbytes, u
     const auto t0 = std::chrono::steady_clock::now();
     kvmem_gpu_state *st = g_state;
     if (!st || !st->slab[0]) return report("enqueue K", "stage-in is not ready");
+    if (!st->out_src.empty()) return report("enqueue K", "stage-out records are pending");
     // stagein.cu:817-831: quantized K only, a Walsh-Hadamard size it
     // provides, heads that tile the row
     if (!packed || !dst || (ty != KVR_FMT_Q8_0 && ty != KVR_FMT_Q4_0))
@@ -690,6 +708,8 @@ bool kvmem_stagein_enqueue_k(kvr_format ty, const void *packed, size_t nbytes, u
     }
     if (st->used + nbytes > kvmem_gpu_state::kSlab || st->src.size() + st->krec.size() >= 8192)
         if (!kvmem_stagein_flush(copy_us, rope_us, hadamard_us, set_us)) return false;
+    // a fresh slab may still be the target of a stage-out copy
+    if (st->used == 0 && st->out_done[st->cur]) (void)hipEventSynchronize(st->out_done[st->cur]);
     uint8_t *slot = st->slab[st->cur] + st->used;
     std::memcpy(slot, packed, nbytes);
     st->krec.push_back({slot, dst, ty, uint32_t(nt), uint32_t(n_embd), uint32_t(nrot), uint32_t(n_embd_head),
@@ -697,6 +717,76 @@ bool kvmem_stagein_enqueue_k(kvr_format ty, const void *packed, size_t nbytes, u
     st->used += (nbytes + 15) / 16 * 16;
     if (set_us) *set_us += micros_since(t0);
     return true;
+}
+
+bool kvmem_stageout_enqueue(const void *gpu_src, size_t nbytes) {
+    kvmem_gpu_state *st = g_state;
+    // stagein.cu:883-905: no stage-in records pending, the record fits the slot
+    if (!st || !st->slab[0] || !st->slab[1] || !gpu_src || !nbytes || !st->src.empty() || !st->krec.empty())
+        return false;
+    if (nbytes > kvmem_gpu_state::kSlab || st->out_used + nbytes > kvmem_gpu_state::kSlab) return false;
+    st->out_src.push_back(gpu_src);
+    st->out_off.push_back(st->out_used);
+    st->out_bytes.push_back(nbytes);
+    st->out_used += nbytes;
+    return true;
+}
+
+size_t kvmem_stageout_used() { return g_state ? g_state->out_used : 0; }
+
+int kvmem_stageout_submit(int64_t *copy_us) {
+    const auto t0 = std::chrono::steady_clock::now();
+    kvmem_gpu_state *st = g_state;
+    if (!st || st->out_src.empty()) return -1;
+    const int slot = st->out_cur;
+    const hipStream_t s = copy_stream(st);
+    // a stage-in flush still reading this slab finishes first
+    if (st->slab_busy[slot]) {
+        if (hipError_t e = hipEventSynchronize(st->slab_done[slot]); e != hipSuccess) return report_hip("stage-out", e), -1;
+        st->slab_busy[slot] = false;
+    }
+    if (!st->out_done[slot] && hipEventCreateWithFlags(&st->out_done[slot], hipEventDisableTiming) != hipSuccess)
+        return report("stage-out", "event"), -1;
+    void *base = nullptr;
+    if (hipError_t e = hipHostGetDevicePointer(&base, st->slab[slot], 0); e != hipSuccess)
+        return report_hip("stage-out", e), -1;
+    std::vector<void *> dst(st->out_src.size());
+    for (size_t i = 0; i < dst.size(); ++i) dst[i] = static_cast<uint8_t *>(base) + st->out_off[i];
+    // one launch writes every record over the host link into the slot
+    if (kvr_d2d_batched(st->ctx, st->out_src.data(), dst.data(), st->out_bytes.data(), uint32_t(dst.size()), s) !=
+        KVR_OK)
+        return report_kvr("stage-out"), -1;
+    if (hipError_t e = hipEventRecord(st->out_done[slot], s); e != hipSuccess) return report_hip("stage-out", e), -1;
+    st->out_src.clear();
+    st->out_off.clear();
+    st->out_bytes.clear();
+    st->out_used = 0;
+    st->out_cur = 1 - slot;
+    if (copy_us) *copy_us += micros_since(t0);
+    return slot;
+}
+
+bool kvmem_stageout_wait(int slot, int64_t *copy_us) {
+    if (slot < 0) return true;
+    kvmem_gpu_state *st = g_state;
+    if (!st || slot > 1 || !st->out_done[slot]) return false;
+    const auto t0 = std::chrono::steady_clock::now();
+    if (hipError_t e = hipEventSynchronize(st->out_done[slot]); e != hipSuccess) return report_hip("stage-out wait", e);
+    if (copy_us) *copy_us += micros_since(t0);
+    return true;
+}
+
+const uint8_t *kvmem_stageout_slot_base(int slot) {
+    if (!g_state || slot < 0 || slot > 1) return nullptr;
+    return g_state->slab[slot];
+}
+
+void kvmem_stageout_clear() {
+    if (!g_state) return;
+    g_state->out_src.clear();
+    g_state->out_off.clear();
+    g_state->out_bytes.clear();
+    g_state->out_used = 0;
 }
 
 bool kvmem_d2d_batched(const void *const *src, void *const *dst, const size_t *nbytes, int n) {

@@ -618,6 +618,50 @@ void stagein_raw_k() {
     kh::kvmem_stagein_gpu_free();
 }
 
+// Stage-out (kvmem_stageout_*): device records packed into the pinned slot
+// by one batched copy, two submits alternating slots; refused beside
+// pending stage-in records, as the reference does.
+void stageout() {
+    require(kh::kvmem_stagein_gpu_ready(0, 0), "gpu_ready");
+    std::mt19937_64 rng(9);
+    for (int round = 0; round < 2; ++round) {
+        std::vector<std::vector<uint8_t>> recs;
+        std::vector<Dev<uint8_t> *> devs;
+        size_t total = 0;
+        for (int i = 0; i < 7; ++i) {
+            std::vector<uint8_t> r(1 + rng() % 200000);
+            for (auto &b : r) b = uint8_t(rng());
+            devs.push_back(new Dev<uint8_t>(r));
+            total += r.size();
+            recs.push_back(std::move(r));
+        }
+        for (size_t i = 0; i < recs.size(); ++i)
+            require(kh::kvmem_stageout_enqueue(devs[i]->p, recs[i].size()), "stageout enqueue");
+        require(kh::kvmem_stageout_used() == total, "stageout used");
+        const int slot = kh::kvmem_stageout_submit(nullptr);
+        require(slot == round, "slots alternate");
+        require(kh::kvmem_stageout_wait(slot, nullptr), "stageout wait");
+        const uint8_t *base = kh::kvmem_stageout_slot_base(slot);
+        size_t off = 0;
+        for (const auto &r : recs) {
+            require(std::memcmp(base + off, r.data(), r.size()) == 0, "staged-out bytes differ");
+            off += r.size();
+        }
+        for (auto *d : devs) delete d;
+    }
+    std::vector<uint8_t> v(64, 1);
+    Dev<uint8_t> vd(v.size());
+    require(kh::kvmem_stagein_enqueue_v(v.data(), v.size(), vd.p, nullptr), "enqueue_v");
+    require(!kh::kvmem_stageout_enqueue(vd.p, 64), "stage-out accepted beside a pending stage-in record");
+    require(kh::kvmem_stagein_flush(nullptr, nullptr, nullptr, nullptr), "flush");
+    kh::kvmem_stagein_sync();
+    require(kh::kvmem_stageout_enqueue(vd.p, 64), "stage-out after the flush");
+    require(!kh::kvmem_stagein_enqueue_v(v.data(), v.size(), vd.p, nullptr), "stage-in accepted beside stage-out");
+    kh::kvmem_stageout_clear();
+    require(kh::kvmem_stageout_used() == 0, "cleared");
+    kh::kvmem_stagein_gpu_free();
+}
+
 }  // namespace
 
 int main(int argc, char **argv) {
@@ -628,7 +672,8 @@ int main(int argc, char **argv) {
     if (gpu)
         tests = {{"qualification", qualification}, {"current_layer", current_layer}, {"pick", pick},
                  {"stagein", stagein},           {"meank", meank},                 {"transfer", transfer},
-                 {"capture", capture}, {"attention", attention}, {"stagein_raw_k", stagein_raw_k}};
+                 {"capture", capture}, {"attention", attention}, {"stagein_raw_k", stagein_raw_k},
+                 {"stageout", stageout}};
     for (auto &[name, fn] : tests) {
         std::cout << "RUN  " << name << std::endl;
         try {

@@ -25,4 +25,4 @@ def test_host_layer_cpu():
 @pytest.mark.gpu
 def test_host_layer_gpu():
     out = _run("--gpu", 110)
-    assert out.count("PASS") == 9
+    assert out.count("PASS") == 10
