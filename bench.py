@@ -587,6 +587,64 @@ def run_workload(args):
 ATTN_WORKLOADS = {"attn128k": "f16", "attn128k_q8": "q8_0"}
 
 
+def run_stageout(args):
+    """Stage-out (--workload stageout32m): 64 scattered 512 KiB device records
+    packed into one 32 MiB pinned slot by one kvr_d2d_batched launch that
+    writes over the host link, against a measured device-to-host copy peak."""
+    import torch
+    import kvmem_amd as K
+    from kvmem_amd.hip import runtime
+
+    hip = runtime()
+    ctx = K.Context(0)
+    n, rec = 64, 512 << 10
+    src = torch.empty(n * 2 * rec, dtype=torch.uint8, device="cuda")  # records at every other 512 KiB
+    torch.cuda.synchronize()
+    ctx.synth_normal_f16(args.seed, 6000, src.numel() // 2, src)
+    slot = K.PinnedBuffer(n * rec)
+    srcs = [src.data_ptr() + (2 * i) * rec for i in range(n)]
+    dsts = [slot.ptr + i * rec for i in range(n)]
+    sizes = [rec] * n
+    ev_a, ev_b = hip.event(), hip.event()
+    for _ in range(args.warmup):
+        ctx.d2d_batched(srcs, dsts, sizes, ctx.copy_stream)
+    ctx.check()
+    times = []
+    for _ in range(args.steps):
+        hip.record(ev_a, ctx.copy_stream)
+        ctx.d2d_batched(srcs, dsts, sizes, ctx.copy_stream)
+        hip.record(ev_b, ctx.copy_stream)
+        ctx.check()
+        times.append(hip.elapsed_ms(ev_a, ev_b) * 1e3)
+    torch.cuda.synchronize()
+    got = slot.numpy()
+    ok = all(np.array_equal(got[i * rec:(i + 1) * rec], src[2 * i * rec:(2 * i + 1) * rec].cpu().numpy())
+             for i in (0, n // 2, n - 1))
+    # device-to-host copy peak: 1 GiB into pinned memory, best of 5
+    big = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    pin = torch.empty(1 << 30, dtype=torch.uint8, pin_memory=True)
+    best = 0.0
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        pin.copy_(big, non_blocking=True)
+        e1.record()
+        torch.cuda.synchronize()
+        best = max(best, (1 << 30) / (e0.elapsed_time(e1) * 1e-3) / 1e9)
+    us = float(np.median(times))
+    gbps = n * rec / (us * 1e-6) / 1e9
+    log(f"stage-out {n} x {rec >> 10} KiB: {us:.1f} us = {gbps:.2f} GB/s; D2H peak {best:.2f} GB/s; bytes ok {ok}")
+    line = {"metric": "stage-out GB/s (device records -> pinned slot) vs measured D2H peak", "value": round(gbps, 3),
+            "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(us / 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "bytes", "data": f"synthetic seeded (device generator), seed {args.seed}",
+            "config": {"workload": "stageout32m", "records": n, "record_bytes": rec},
+            "d2h_peak_GBps": round(best, 3), "frac_d2h": round(gbps / best, 4), "bytes_match": bool(ok)}
+    slot.free()
+    ctx.close()
+    print(json.dumps(line), flush=True)
+
+
 def run_attention(args):
     import torch
     import kvmem_amd as K
@@ -698,7 +756,8 @@ def main():
     ap.add_argument("--gather-threads", type=int, default=0, help="gather workgroup size (0 = default)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workload", choices=["resident64", *WORKLOADS, *ATTN_WORKLOADS], default="resident64",
+    ap.add_argument("--workload", choices=["resident64", *WORKLOADS, *ATTN_WORKLOADS, "stageout32m"],
+                    default="resident64",
                     help="resident64 (default): the 64-layer 128K stack; the others are the remaining "
                          "workloads, each measured the same way")
     ap.add_argument("--pmc-pass", action="store_true",
@@ -715,6 +774,9 @@ def main():
         return
     if args.workload in ATTN_WORKLOADS:
         run_attention(args)
+        return
+    if args.workload == "stageout32m":
+        run_stageout(args)
         return
     if args.workload != "resident64":
         run_workload(args)
