@@ -60,7 +60,9 @@ typedef enum kvr_status {
     KVR_ERR_WORKSPACE = 5,   /* borrowed workspace too small for the call       */
     KVR_ERR_HIP = 6,         /* HIP runtime error                               */
     KVR_ERR_SCORES = 7,      /* negative or non-finite score without signed mode*/
-    KVR_ERR_UNSUPPORTED = 8  /* format/mode combination not provided            */
+    KVR_ERR_UNSUPPORTED = 8, /* format/mode combination not provided            */
+    KVR_ERR_GRAPH = 9        /* invalid graph mass or weight, or a propagation  *
+                              * result below its signed residual                */
 } kvr_status;
 
 typedef enum kvr_format {
@@ -387,6 +389,65 @@ size_t kvr_attention_workspace_bytes(uint32_t n_rows, uint32_t query_heads, uint
  * `stream` (NULL: the context's select stream). */
 kvr_status kvr_attention_page_mass(kvr_context *ctx, const kvr_attention_sample *sample, float *mass,
                                    void *stream);
+
+/* ---- graph propagation and LRFU (between scoring and selection) ---------- */
+
+/* Pages per lane that kvr_propagate_scores / kvr_lrfu_preview take: one
+ * workgroup per lane holds the lane's pages in LDS (8 bytes each). */
+#define KVR_GRAPH_MAX_PAGES 8192
+
+/* One lane's accepted attention graph, flattened by page: row r moves
+ * evidence from page row_source[r] to pages edge_target[row_begin[r] ..
+ * row_begin[r+1]) in proportion to edge_mass (the sealed row's mass over its
+ * samples).  Only rows with samples and a completed source block belong here
+ * (the reference skips the others).  neighbor_weight[i] is the message-span
+ * coefficient between pages i and i+1 (1 inside one message, the cross
+ * weight across a boundary); NULL means 1 everywhere.  All pointers are
+ * device memory; rows may be empty (n_rows 0, pointers NULL). */
+typedef struct kvr_page_graph {
+    uint32_t n_rows;
+    uint32_t n_edges;                /* row_begin[n_rows]                     */
+    const uint32_t *row_source;      /* [n_rows] page ids                     */
+    const uint32_t *row_begin;       /* [n_rows + 1], nondecreasing           */
+    const uint32_t *edge_target;     /* [n_edges] page ids                    */
+    const double *edge_mass;         /* [n_edges] finite, >= 0                */
+    const double *neighbor_weight;   /* [pages - 1] in [0, 1], or NULL        */
+} kvr_page_graph;
+
+/* One hop of positive Query evidence over the graph, in place:
+ *   scores = min(raw, 0) + G(max(raw, 0))
+ * with every page of transport_mask a node (NULL: every page).  Each node
+ * gives alpha/4 of its share to each adjacent node (times the span
+ * coefficient) and alpha/2 over its graph row; pages outside the mask
+ * neither give nor receive.  alpha 0, at most one node or no positive
+ * evidence leave the scores untouched.  Transfers are summed as integers in
+ * units of at most 2^-61 of the evidence total, so every run gives the same
+ * bits; results match the reference to ~1e-15 of that total.  A non-finite score
+ * raises KVR_ERR_SCORES, an invalid mass, weight or row range or a result
+ * below its residual KVR_ERR_GRAPH at kvr_check; the scores are then left as
+ * they were.  graphs: host array of `lanes` entries (NULL: no graph rows).
+ * Replaces propagate_query_scores (kvmem/src/host/graph_recall.cpp:494-552;
+ * span_coefficient :234-247) for the frames query_score_frame builds (page i
+ * starts at token i * block_tokens).  scores, transport_mask: dev
+ * [lanes][pages]. */
+kvr_status kvr_propagate_scores(kvr_context *ctx, double *scores, uint32_t lanes, uint32_t pages,
+                                const uint8_t *transport_mask, const kvr_page_graph *graphs,
+                                double alpha, void *stream);
+
+/* LRFU preview: candidate[i] = lambda * history[i] + gate(scores[i]), where
+ * gate keeps a score at or above the top_fraction threshold (the score of
+ * ascending rank min(n-1, floor((1 - top_fraction) * n))) and clips the rest
+ * to min(score, 0); top_fraction 1 keeps every score.  history pages past
+ * history_pages count as 0 (history may be NULL when history_pages is 0).
+ * Binary64 with separate roundings, bit-identical to the reference.  A
+ * non-finite score raises KVR_ERR_SCORES at kvr_check (candidate unwritten).
+ * The caller keeps the candidate and makes it the next history on commit.
+ * Replaces LrfuHistory::preview / score (kvmem/include/kvmem/lrfu.hpp:57-90).
+ * scores, candidate: dev [lanes][pages] (candidate may be scores);
+ * history: dev [lanes][history_pages]. */
+kvr_status kvr_lrfu_preview(kvr_context *ctx, const double *scores, uint32_t lanes, uint32_t pages,
+                            const double *history, uint32_t history_pages, double lambda,
+                            double top_fraction, double *candidate, void *stream);
 
 /* ---- device copies ------------------------------------------------------- */
 

@@ -113,6 +113,13 @@ def make_keys(t, fmt: int, tokens: int, kv_heads: int, head_dim: int, page_token
     return k
 
 
+def make_page_graph(n_rows=0, n_edges=0, row_source=None, row_begin=None, edge_target=None, edge_mass=None,
+                    neighbor_weight=None) -> "_capi.PageGraph":
+    """A kvr_page_graph over device arrays (the caller keeps them alive)."""
+    return _capi.PageGraph(n_rows, n_edges, _ptr(row_source), _ptr(row_begin), _ptr(edge_target),
+                           _ptr(edge_mass), _ptr(neighbor_weight))
+
+
 def make_plane(history, fmt: int, width: int, tokens: int, mode: int, slots,
                host_lane_stride: int = 0, slot_lane_stride: int = 0, rope: Optional[dict] = None):
     """rope (for GATHER_ROPE_FWHT): dict(head_dim, n_rot, theta (device
@@ -213,6 +220,19 @@ class Context:
         arr = (C.c_uint32 * max(1, len(mandatory)))(*mandatory)
         check(lib().kvr_select_topk(self.handle, _ptr(scores), lanes, pages, k, arr, len(mandatory), tie_rule,
                                     int(signed_scores), _ptr(selected), _ptr(count), stream))
+
+    # -- graph propagation and LRFU -------------------------------------------
+    def propagate_scores(self, scores, pages, graphs: Sequence = (), alpha=0.2, transport_mask=None, lanes=1,
+                         stream=None) -> None:
+        """graphs: one _capi.PageGraph per lane (make_page_graph), or none."""
+        arr = (_capi.PageGraph * max(1, len(graphs)))(*graphs) if graphs else None
+        check(lib().kvr_propagate_scores(self.handle, _ptr(scores), lanes, pages, _ptr(transport_mask), arr,
+                                         alpha, stream))
+
+    def lrfu_preview(self, scores, pages, candidate, history=None, history_pages=0, lam=0.5, top_fraction=0.9,
+                     lanes=1, stream=None) -> None:
+        check(lib().kvr_lrfu_preview(self.handle, _ptr(scores), lanes, pages, _ptr(history), history_pages, lam,
+                                     top_fraction, _ptr(candidate), stream))
 
     # -- stage-in -----------------------------------------------------------
     def stage_in(self, planes: Sequence, page_tokens, selected, count, k, lanes=1, engine=ENGINE_AUTO,

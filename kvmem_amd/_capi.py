@@ -15,7 +15,9 @@ LIB_PATH = os.path.join(HERE, "libkvrecall.so")
 HEADER = os.path.join(ROOT, "include", "kvrecall.h")
 
 # enums
-OK, ERR_INVALID, ERR_NONFINITE, ERR_RANGE, ERR_BUDGET, ERR_WORKSPACE, ERR_HIP, ERR_SCORES, ERR_UNSUPPORTED = range(9)
+(OK, ERR_INVALID, ERR_NONFINITE, ERR_RANGE, ERR_BUDGET, ERR_WORKSPACE, ERR_HIP, ERR_SCORES, ERR_UNSUPPORTED,
+ ERR_GRAPH) = range(10)
+GRAPH_MAX_PAGES = 8192
 FMT_F16, FMT_Q8_0, FMT_Q4_1, FMT_F32, FMT_BF16, FMT_Q4_0, FMT_Q5_0 = range(7)
 AGG_MEAN, AGG_MAX, AGG_MAX_LOGIT = range(3)
 TIE_LOWER_FIRST, TIE_HIGHER_FIRST = range(2)
@@ -71,6 +73,11 @@ class AttentionSample(C.Structure):
                 ("mask_rows", C.POINTER(_u32))]
 
 
+class PageGraph(C.Structure):
+    _fields_ = [("n_rows", _u32), ("n_edges", _u32), ("row_source", _P), ("row_begin", _P),
+                ("edge_target", _P), ("edge_mass", _P), ("neighbor_weight", _P)]
+
+
 _SIGNATURES = {
     "kvr_create": (_i, [_i, C.POINTER(_P)]),
     "kvr_destroy": (_i, [_P]),
@@ -93,6 +100,8 @@ _SIGNATURES = {
     "kvr_recall_stack": (_i, [_P, C.POINTER(LayerRecall), _u32, _P, _P]),
     "kvr_attention_workspace_bytes": (_sz, [_u32, _u32, _u32]),
     "kvr_attention_page_mass": (_i, [_P, C.POINTER(AttentionSample), _P, _P]),
+    "kvr_propagate_scores": (_i, [_P, _P, _u32, _u32, _P, C.POINTER(PageGraph), C.c_double, _P]),
+    "kvr_lrfu_preview": (_i, [_P, _P, _u32, _u32, _P, _u32, C.c_double, C.c_double, _P, _P]),
     "kvr_d2d_batched": (_i, [_P, C.POINTER(_P), C.POINTER(_P), C.POINTER(_sz), _u32, _P]),
     "kvr_host_alloc": (_i, [_sz, C.POINTER(_P)]),
     "kvr_host_free": (_i, [_P]),

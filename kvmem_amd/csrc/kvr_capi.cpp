@@ -676,6 +676,7 @@ const char *kvr_status_string(kvr_status s) {
     case KVR_ERR_HIP: return "HIP runtime error";
     case KVR_ERR_SCORES: return "invalid score";
     case KVR_ERR_UNSUPPORTED: return "unsupported format or mode";
+    case KVR_ERR_GRAPH: return "invalid graph mass, weight or row, or propagation result";
     }
     return "unknown status";
 }
@@ -780,14 +781,19 @@ kvr_status kvr_check(kvr_context *ctx, void *stream) {
     KVR_HIP(hipMemcpy(st, ctx->status, sizeof st, hipMemcpyDeviceToHost));
     // A raised word holds the number of the call that raised it (graph
     // replays repeat the number their capture gave them); reporting clears it.
-    if (!st[kvr::kStatusNonfinite] && !st[kvr::kStatusRange] && !st[kvr::kStatusScores]) return KVR_OK;
+    if (!st[kvr::kStatusNonfinite] && !st[kvr::kStatusRange] && !st[kvr::kStatusScores] &&
+        !st[kvr::kStatusGraph])
+        return KVR_OK;
     KVR_HIP(hipMemset(ctx->status, 0, sizeof st));
     KVR_HIP(hipDeviceSynchronize());
     if (st[kvr::kStatusNonfinite])
         return fail(KVR_ERR_NONFINITE, "nonfinite recall operand (call %u)", st[kvr::kStatusNonfinite]);
     if (st[kvr::kStatusRange])
         return fail(KVR_ERR_RANGE, "recall operand rounds to fp16 infinity (call %u)", st[kvr::kStatusRange]);
-    return fail(KVR_ERR_SCORES, "negative or nonfinite score (call %u)", st[kvr::kStatusScores]);
+    if (st[kvr::kStatusScores])
+        return fail(KVR_ERR_SCORES, "negative or nonfinite score (call %u)", st[kvr::kStatusScores]);
+    return fail(KVR_ERR_GRAPH, "invalid graph mass, weight or row, or propagation result below its residual (call %u)",
+                st[kvr::kStatusGraph]);
 }
 
 size_t kvr_workspace_bytes(uint32_t lanes, uint32_t max_pages, uint32_t max_rows, uint32_t query_heads,
@@ -934,6 +940,78 @@ kvr_status kvr_select_topk(kvr_context *ctx, const double *scores, uint32_t lane
     sa.status = ctx->status;
     sa.epoch = ctx->epoch;
     KVR_HIP(kvr::launch_select(sa, stream_or(stream, ctx->sel)));
+    return KVR_OK;
+}
+
+namespace {
+kvr_status check_graph_frame(kvr_context *ctx, const double *scores, uint32_t pages) {
+    if (kvr_status s = check_ctx(ctx)) return s;
+    if (!scores || !pages) return fail(KVR_ERR_INVALID, "scores and pages are required");
+    if (pages > kvr::kGraphMaxPages)
+        return fail(KVR_ERR_UNSUPPORTED, "%u pages per lane exceed KVR_GRAPH_MAX_PAGES (%u)", pages,
+                    kvr::kGraphMaxPages);
+    return KVR_OK;
+}
+}  // namespace
+
+kvr_status kvr_propagate_scores(kvr_context *ctx, double *scores, uint32_t lanes, uint32_t pages,
+                                const uint8_t *transport_mask, const kvr_page_graph *graphs, double alpha,
+                                void *stream) {
+    if (kvr_status s = check_graph_frame(ctx, scores, pages)) return s;
+    lanes = lanes ? lanes : 1;
+    if (!(alpha >= 0.0 && alpha <= 1.0)) return fail(KVR_ERR_INVALID, "invalid attention decay (alpha)");
+    std::vector<kvr::GraphLane> g(lanes);
+    for (uint32_t l = 0; graphs && l < lanes; ++l) {
+        const kvr_page_graph &x = graphs[l];
+        if (x.n_rows && (!x.row_source || !x.row_begin))
+            return fail(KVR_ERR_INVALID, "graph rows need row_source and row_begin (lane %u)", l);
+        if (x.n_edges && (!x.edge_target || !x.edge_mass))
+            return fail(KVR_ERR_INVALID, "graph edges need edge_target and edge_mass (lane %u)", l);
+        g[l] = {x.n_rows, x.n_edges, x.row_source, x.row_begin, x.edge_target, x.edge_mass, x.neighbor_weight};
+    }
+    DeviceGuard guard(ctx->device);
+    ++ctx->epoch;
+    kvr::GraphLrfuArgs a{};
+    a.scores = scores;
+    a.mask = transport_mask;
+    a.pages = pages;
+    a.propagate = 1;
+    a.alpha = alpha;
+    a.status = ctx->status;
+    a.epoch = ctx->epoch;
+    KVR_HIP(kvr::launch_graph_lrfu(a, g.data(), lanes, stream_or(stream, ctx->sel)));
+    return KVR_OK;
+}
+
+kvr_status kvr_lrfu_preview(kvr_context *ctx, const double *scores, uint32_t lanes, uint32_t pages,
+                            const double *history, uint32_t history_pages, double lambda, double top_fraction,
+                            double *candidate, void *stream) {
+    if (kvr_status s = check_graph_frame(ctx, scores, pages)) return s;
+    lanes = lanes ? lanes : 1;
+    if (!candidate) return fail(KVR_ERR_INVALID, "candidate is required");
+    if (history_pages && !history) return fail(KVR_ERR_INVALID, "history_pages without history");
+    if (!(lambda >= 0.0 && lambda <= 1.0) || !(top_fraction > 0.0 && top_fraction <= 1.0))
+        return fail(KVR_ERR_INVALID, "invalid LRFU decay or hit fraction");
+    DeviceGuard guard(ctx->device);
+    ++ctx->epoch;
+    kvr::GraphLrfuArgs a{};
+    a.scores = const_cast<double *>(scores);
+    a.pages = pages;
+    a.lrfu = 1;
+    a.history = history_pages ? history : nullptr;
+    a.history_pages = history_pages;
+    a.lambda = lambda;
+    a.gate = top_fraction < 1.0;
+    if (a.gate) {
+        // the reference's rank: min(n - 1, size_t((1 - fraction) * n)) in binary64
+        const double r = (1.0 - top_fraction) * double(pages);
+        a.rank = std::min<uint32_t>(pages - 1, uint32_t(r));
+    }
+    a.candidate = candidate;
+    a.status = ctx->status;
+    a.epoch = ctx->epoch;
+    std::vector<kvr::GraphLane> g(lanes);
+    KVR_HIP(kvr::launch_graph_lrfu(a, g.data(), lanes, stream_or(stream, ctx->sel)));
     return KVR_OK;
 }
 

@@ -35,7 +35,7 @@ __device__ __forceinline__ uint32_t recall16(float v, uint16_t &h) {
 
 // Device status words, one per error class; each holds the epoch (call
 // number) of the latest call that raised it.
-enum : uint32_t { kStatusNonfinite = 0, kStatusRange = 1, kStatusScores = 2, kStatusWords = 4 };
+enum : uint32_t { kStatusNonfinite = 0, kStatusRange = 1, kStatusScores = 2, kStatusGraph = 3, kStatusWords = 4 };
 __device__ __forceinline__ void raise_status(uint32_t *status, uint32_t word, uint32_t epoch) {
     atomicMax(status + word, epoch);
 }

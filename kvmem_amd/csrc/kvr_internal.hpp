@@ -196,6 +196,36 @@ struct SynthArgs {
 };
 hipError_t launch_synth(const SynthArgs &a, hipStream_t s);
 
+// Graph propagation and LRFU preview of per-page scores: one workgroup per
+// lane, the lane's pages in LDS.
+constexpr uint32_t kGraphLanes = 16;       // lanes per launch (kernarg table)
+constexpr uint32_t kGraphMaxPages = 8192;  // 8 bytes of LDS per page
+struct GraphLane {
+    uint32_t n_rows, n_edges;
+    const uint32_t *row_source, *row_begin, *edge_target;
+    const double *edge_mass, *neighbor_weight;
+};
+struct GraphLrfuArgs {
+    double *scores;         // [lanes][pages]; propagated in place
+    const uint8_t *mask;    // [lanes][pages] transport nodes, or null (all)
+    uint32_t pages;
+    uint32_t lane0;         // first lane of this launch
+    int propagate;
+    double alpha;
+    GraphLane graph[kGraphLanes];
+    int lrfu;
+    const double *history;  // [lanes][history_pages] or null
+    uint32_t history_pages;
+    double lambda;
+    int gate;               // threshold applies (top fraction < 1)
+    uint32_t rank;          // ascending rank of the threshold score
+    double *candidate;      // [lanes][pages]
+    uint32_t *status;
+    uint32_t epoch;
+};
+// One launch per kGraphLanes lanes; `graphs` holds every lane's graph.
+hipError_t launch_graph_lrfu(GraphLrfuArgs a, const GraphLane *graphs, uint32_t lanes, hipStream_t s);
+
 // Sampled attention page masses (kvr_attention.hip).  Key formats are
 // kvr_format values; query and mask scalars are Scalar values.
 enum KeyFormat : uint32_t { kKeyF16 = 0, kKeyQ8 = 1, kKeyF32 = 3, kKeyBF16 = 4, kKeyQ4 = 5, kKeyQ5 = 6 };

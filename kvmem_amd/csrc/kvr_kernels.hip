@@ -1201,6 +1201,254 @@ __device__ __forceinline__ void wg_select(const SelectArgs &a, uint32_t lane, bo
     if (tid == 0) a.count[lane] = min(total, a.k);
 }
 
+// ---------------------------------------------------------------------------
+// Graph propagation (propagate_query_scores, kvmem/src/host/graph_recall.cpp:
+// 494-552) and LRFU preview (LrfuHistory::preview, kvmem/include/kvmem/
+// lrfu.hpp:57-79), one lane per workgroup, the lane's pages in LDS.
+//
+// Propagation is a sum of transfers: node i gives (total * seed_i) * w to
+// node j and loses as much, seed_i = max(0, raw_i) / total, w = alpha/4 times
+// the span coefficient to each adjacent node and (alpha/2 * mass) / den over
+// its graph row -- the reference's expressions, operand for operand.  The
+// reference applies the transfers one by one in its hash map's order; here
+// each is rounded to an integer count of 2^(e-62) units (2^e > total) and
+// the counts are added (adjacent ones by the receiving page itself, graph
+// edges by LDS integer atomics), so the result does not depend on the order
+// and differs from the reference's by a few units of the total's last place.
+// The LRFU threshold is the score of a given ascending rank, found by the
+// same radix select as the page selection (order-preserving keys, ±0 equal).
+// Contraction stays off: every product and sum is rounded on its own, as in
+// the reference's host build.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int64_t graph_units(double delta, int shift) {
+    return static_cast<int64_t>(rint(ldexp(delta, shift)));
+}
+
+__global__ __launch_bounds__(256) void k_graph_lrfu(GraphLrfuArgs a) {
+#pragma clang fp contract(off)
+    constexpr uint32_t B = 256, W = B / kWave;
+    __shared__ double s_sum[W];
+    __shared__ uint32_t s_cnt[W], s_bad[W];
+    __shared__ uint64_t s_red[2][W];
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t s_ctl[2];
+    const uint32_t tid = threadIdx.x, w = tid / kWave, l = tid % kWave;
+    const uint32_t lane = a.lane0 + blockIdx.x, n = a.pages;
+    const GraphLane g = a.graph[blockIdx.x];
+    double *sc = a.scores + uint64_t(lane) * n;
+    const uint8_t *mk = a.mask ? a.mask + uint64_t(lane) * n : nullptr;
+    int64_t *net = reinterpret_cast<int64_t *>(tail_keys);  // transfer units, then the values
+    double *val = reinterpret_cast<double *>(tail_keys);
+    const uint32_t C = (n + B - 1) / B, j0 = min(n, tid * C), j1 = min(n, j0 + C);
+    auto node = [&](uint32_t j) { return j < n && (!mk || mk[j]); };
+    // workgroup OR of a flag (every thread gets it)
+    auto any = [&](uint32_t flag) {
+        flag = wave_max(flag);
+        if (l == 0) s_bad[w] = flag;
+        lds_barrier();
+        uint32_t r = 0;
+#pragma unroll
+        for (uint32_t i = 0; i < W; ++i) r |= s_bad[i];
+        lds_barrier();
+        return r != 0;
+    };
+
+    if (a.propagate) {
+        double part = 0;
+        uint32_t cnt = 0, bad = 0;
+        for (uint32_t j = j0; j < j1; ++j) {
+            const double r = sc[j];
+            if (!__builtin_isfinite(r)) {
+                bad = 1;
+            } else if (node(j)) {
+                ++cnt;
+                part += 0. < r ? r : 0.;
+            }
+        }
+        part = wave_sum(part);
+        cnt = wave_sum(cnt);
+        bad = wave_max(bad);
+        if (l == 0) {
+            s_sum[w] = part;
+            s_cnt[w] = cnt;
+            s_bad[w] = bad;
+        }
+        lds_barrier();
+        double total = 0;
+        uint32_t nodes = 0;
+        bad = 0;
+#pragma unroll
+        for (uint32_t i = 0; i < W; ++i) {
+            total += s_sum[i];
+            nodes += s_cnt[i];
+            bad |= s_bad[i];
+        }
+        lds_barrier();
+        if (bad || !__builtin_isfinite(total)) {
+            if (tid == 0) raise_status(a.status, kStatusScores, a.epoch);
+            return;
+        }
+        if (nodes > 1 && total != 0. && a.alpha != 0.) {
+            int e;
+            (void)frexp(total, &e);  // total < 2^e
+            const int shift = 62 - e;
+            const double wn = a.alpha * .25, wr = a.alpha * .5;
+            auto base = [&](uint32_t j) {
+                const double r = sc[j];
+                const double seed = (0. < r ? r : 0.) / total;
+                return total * seed;
+            };
+            uint32_t gbad = 0;
+            // adjacent pages: each page sums what it receives and gives
+            for (uint32_t j = j0; j < j1; ++j) {
+                int64_t q = 0;
+                if (node(j)) {
+                    const double bj = base(j);
+                    if (j > 0 && node(j - 1)) {
+                        const double c = g.neighbor_weight ? g.neighbor_weight[j - 1] : 1.;
+                        gbad |= !(c >= 0. && c <= 1.);
+                        const double wt = wn * c;
+                        q += graph_units(base(j - 1) * wt, shift) - graph_units(bj * wt, shift);
+                    }
+                    if (node(j + 1)) {
+                        const double c = g.neighbor_weight ? g.neighbor_weight[j] : 1.;
+                        gbad |= !(c >= 0. && c <= 1.);
+                        const double wt = wn * c;
+                        q += graph_units(base(j + 1) * wt, shift) - graph_units(bj * wt, shift);
+                    }
+                }
+                net[j] = q;
+            }
+            lds_barrier();
+            // graph rows: one thread per row, its edges in order
+            for (uint32_t r = tid; r < g.n_rows; r += B) {
+                const uint32_t src = g.row_source[r];
+                const uint32_t e0 = g.row_begin[r], e1 = g.row_begin[r + 1];
+                if (e0 > e1 || e1 > g.n_edges) {
+                    gbad = 1;
+                    continue;
+                }
+                if (!node(src)) continue;
+                double den = 0;
+                for (uint32_t e = e0; e < e1; ++e) {
+                    const double m = g.edge_mass[e];
+                    gbad |= !(m >= 0. && m <= __DBL_MAX__);
+                    const uint32_t t = g.edge_target[e];
+                    if (t != src && node(t)) den += m;
+                }
+                if (!(den != 0.)) continue;
+                const double bs = base(src);
+                if (bs == 0.) continue;
+                uint64_t given = 0;
+                for (uint32_t e = e0; e < e1; ++e) {
+                    const uint32_t t = g.edge_target[e];
+                    if (t == src || !node(t)) continue;
+                    const double wt = wr * g.edge_mass[e] / den;
+                    const uint64_t q = uint64_t(graph_units(bs * wt, shift));
+                    atomicAdd(reinterpret_cast<unsigned long long *>(net + t), (unsigned long long)q);
+                    given += q;
+                }
+                atomicAdd(reinterpret_cast<unsigned long long *>(net + src), (unsigned long long)(0ull - given));
+            }
+            lds_barrier();
+            const double slack = 1e-12 * (1. < total ? total : 1.);
+            for (uint32_t j = j0; j < j1; ++j) {
+                const double r = sc[j];
+                const int64_t q = net[j];
+                double o = q ? r + ldexp(double(q), -shift) : r;
+                const double resid = r < 0. ? r : 0.;
+                gbad |= !(o >= resid - slack);
+                o = resid < o ? o : resid;
+                val[j] = o;
+            }
+            if (any(gbad)) {
+                if (tid == 0) raise_status(a.status, kStatusGraph, a.epoch);
+                return;
+            }
+            for (uint32_t j = j0; j < j1; ++j) sc[j] = val[j];
+        } else if (a.lrfu) {
+            for (uint32_t j = j0; j < j1; ++j) val[j] = sc[j];
+        }
+    } else if (a.lrfu) {
+        uint32_t bad = 0;
+        for (uint32_t j = j0; j < j1; ++j) {
+            const double v = sc[j];
+            bad |= !__builtin_isfinite(v);
+            val[j] = v;
+        }
+        if (any(bad)) {
+            if (tid == 0) raise_status(a.status, kStatusScores, a.epoch);
+            return;
+        }
+    }
+    if (!a.lrfu) return;
+
+    // LRFU: threshold key of ascending rank `rank`, i.e. the (n - rank)-th
+    // largest (every thread reads only its own chunk of val)
+    uint64_t thr = 0;
+    if (a.gate) {
+        uint64_t and_all = ~0ull, or_all = 0;
+        for (uint32_t j = j0; j < j1; ++j) {
+            const uint64_t k = order_key(val[j]);
+            and_all &= k;
+            or_all |= k;
+        }
+        and_all = wave_and(and_all);
+        or_all = wave_or(or_all);
+        if (l == 0) {
+            s_red[0][w] = and_all;
+            s_red[1][w] = or_all;
+        }
+        lds_barrier();
+#pragma unroll
+        for (uint32_t i = 0; i < W; ++i) {
+            and_all &= s_red[0][i];
+            or_all |= s_red[1][i];
+        }
+        const uint64_t diff = and_all ^ or_all;
+        uint64_t prefix = and_all;
+        if (diff) {
+            const int top = 63 - __clzll(diff);
+            prefix = and_all & ~((2ull << top) - 1);
+            uint32_t remaining = n - a.rank;
+            for (int pos = top / 8 * 8;; pos -= 8) {
+                const uint64_t hi_mask = pos + 8 >= 64 ? 0ull : ~0ull << (pos + 8);
+                const uint64_t want = prefix & hi_mask;
+                hist[tid] = 0;
+                lds_barrier();
+                for (uint32_t j = j0; j < j1; ++j) {
+                    const uint64_t k = order_key(val[j]);
+                    if ((k & hi_mask) == want) atomicAdd(&hist[(k >> pos) & 255u], 1u);
+                }
+                lds_barrier();
+                if (w == 0) {
+                    uint32_t d, rem, cnt;
+                    radix_find(hist, remaining, d, rem, cnt);
+                    if (l == 0) {
+                        s_ctl[0] = d;
+                        s_ctl[1] = rem;
+                    }
+                }
+                lds_barrier();
+                prefix |= uint64_t(s_ctl[0]) << pos;
+                remaining = s_ctl[1];
+                lds_barrier();  // hist and s_ctl are rewritten by the next pass
+                if (pos == 0) break;
+            }
+        }
+        thr = prefix;
+    }
+    const double lam = a.lambda;
+    const double *h = a.history ? a.history + uint64_t(lane) * a.history_pages : nullptr;
+    double *cd = a.candidate + uint64_t(lane) * n;
+    for (uint32_t j = j0; j < j1; ++j) {
+        const double v = val[j];
+        const double hv = j < a.history_pages ? h[j] : 0.;
+        const double kept = (!a.gate || order_key(v) >= thr) ? v : (0. < v ? 0. : v);
+        cd[j] = lam * hv + kept;
+    }
+}
+
 // Aggregation (optional) by the whole workgroup, then selection by its
 // first wave.  Keys go to LDS when the lane's pages fit.
 __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
@@ -2117,6 +2365,19 @@ hipError_t launch_select(const SelectArgs &a, hipStream_t s) {
     const size_t lds = a.pages <= kTailLdsPages ? size_t(a.pages) * 8 : 0;
     hipLaunchKernelGGL(k_select, dim3(a.lanes), dim3(256), lds, s, a);
     return hipGetLastError();
+}
+
+hipError_t launch_graph_lrfu(GraphLrfuArgs a, const GraphLane *graphs, uint32_t lanes, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error
+    const size_t lds = size_t(a.pages) * 8;
+    for (uint32_t l0 = 0; l0 < lanes; l0 += kGraphLanes) {
+        const uint32_t nl = lanes - l0 < kGraphLanes ? lanes - l0 : kGraphLanes;
+        a.lane0 = l0;
+        for (uint32_t i = 0; i < nl; ++i) a.graph[i] = graphs[l0 + i];
+        hipLaunchKernelGGL(k_graph_lrfu, dim3(nl), dim3(256), lds, s, a);
+        if (hipError_t e = hipGetLastError()) return e;
+    }
+    return hipSuccess;
 }
 
 hipError_t launch_gather(const GatherArgs &a, hipStream_t s) {

@@ -69,6 +69,9 @@ def _load_oracle() -> C.CDLL:
                                               _u32, C.c_float, C.c_float, _P, _u32, _P]),
         "orc_gather_row_bytes": (C.c_size_t, [C.c_int, C.c_int, _u32]),
         "orc_gather": (C.c_int, [_P, C.c_int, _u32, _u64, _u32, _P, _u32, C.c_int, _P]),
+        "orc_span_coefficients": (C.c_int, [_P, _P, _P, _u32, _u32, _u32, C.c_double, _P]),
+        "orc_propagate_scores": (C.c_int, [_P, _P, _u32, _u32, _P, _P, _P, _P, _P, C.c_double, _P]),
+        "orc_lrfu_preview": (C.c_int, [_P, _u32, _P, _u32, C.c_double, C.c_double, _P]),
         "orc_synth_bits": (_u64, [_u64, _u64, _u64]),
         "orc_synth_normal": (C.c_double, [_u64, _u64, _u64]),
         "orc_synth_uniform": (C.c_float, [_u64, _u64, _u64, C.c_float, C.c_float]),
@@ -105,6 +108,10 @@ def _load_ref() -> Optional[C.CDLL]:
         "ref_layerwise_scores_f16_keys": (C.c_int, [_P, _u32, _u32, _u64, _u32, _u32, _u32, _P,
                                                     _u32, _u32, C.c_float, _P]),
         "ref_pick_scored_blocks": (C.c_int, [_P, _u32, _P, _u32, _u32, C.c_int, _P, _P]),
+        "ref_propagate_query_scores": (C.c_int, [_P, _u32, _P, _u32, _u32, _P, _P, _P, _P, _u32, _P, _P, _P,
+                                                 C.c_double, C.c_double, _P]),
+        "ref_graph_accept": (C.c_int, [_u32, _u64, _u32, _P, _P, _P, _P, _u32, _u32, _u32, _P, _P, _P, _P, _P]),
+        "ref_lrfu_preview": (C.c_int, [_P, _u32, _P, _u32, C.c_double, C.c_double, _P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -214,6 +221,75 @@ def pick_scored_blocks(scores: np.ndarray, budget: int, mandatory: Sequence[int]
     _check(lib.orc_pick_scored_blocks(_ptr(scores), n, _ptr(pins), len(mandatory), budget,
                                       tie_rule, int(signed_scores), _ptr(out), C.byref(n_out)))
     return out[: n_out.value].copy()
+
+
+# ---- graph propagation and LRFU --------------------------------------------
+
+class PageGraph:
+    """A graph flattened by page: row r moves evidence from page
+    row_source[r] to pages edge_target[row_begin[r]:row_begin[r+1]] in
+    proportion to edge_mass."""
+
+    def __init__(self, rows=()):
+        """rows: iterable of (source_page, [(target_page, mass), ...])."""
+        rows = list(rows)
+        self.row_source = np.array([r[0] for r in rows], np.uint32)
+        begin = [0]
+        for _, edges in rows:
+            begin.append(begin[-1] + len(edges))
+        self.row_begin = np.array(begin, np.uint32)
+        self.edge_target = np.array([t for _, e in rows for t, _ in e], np.uint32)
+        self.edge_mass = np.array([m for _, e in rows for _, m in e], np.float64)
+
+    @classmethod
+    def from_arrays(cls, row_source, row_begin, edge_target, edge_mass):
+        g = cls()
+        g.row_source = _c(row_source, np.uint32)
+        g.row_begin = _c(row_begin, np.uint32)
+        g.edge_target = _c(edge_target, np.uint32)
+        g.edge_mass = _c(edge_mass, np.float64)
+        return g
+
+    @property
+    def n_rows(self) -> int:
+        return int(self.row_source.size)
+
+    @property
+    def n_edges(self) -> int:
+        return int(self.row_begin[-1])
+
+
+def span_coefficients(spans, block_tokens: int, pages: int, cross: float = 0.25) -> np.ndarray:
+    """spans: [(begin, end, end_known)] message spans -> [pages-1] weights."""
+    b = _c([s[0] for s in spans] or [0], np.uint64)
+    e = _c([s[1] for s in spans] or [0], np.uint64)
+    k = _c([int(s[2]) for s in spans] or [0], np.uint8)
+    out = np.ones(max(pages - 1, 1), np.float64)
+    _check(lib.orc_span_coefficients(_ptr(b), _ptr(e), _ptr(k), len(spans), block_tokens, pages, cross, _ptr(out)))
+    return out[: max(pages - 1, 0)]
+
+
+def propagate_scores(raw: np.ndarray, graph: Optional[PageGraph] = None, alpha: float = 0.2,
+                     mask: Optional[np.ndarray] = None, neighbor_weight: Optional[np.ndarray] = None) -> np.ndarray:
+    raw = _c(raw, np.float64)
+    n = raw.size
+    g = graph or PageGraph()
+    m = None if mask is None else _c(mask, np.uint8)
+    nw = None if neighbor_weight is None else _c(neighbor_weight, np.float64)
+    out = np.zeros(n, np.float64)
+    _check(lib.orc_propagate_scores(_ptr(raw), _ptr(m), n, g.n_rows, _ptr(g.row_source), _ptr(g.row_begin),
+                                    _ptr(g.edge_target), _ptr(g.edge_mass), _ptr(nw), alpha, _ptr(out)))
+    return out
+
+
+def lrfu_preview(scores: np.ndarray, history: Optional[np.ndarray] = None, lam: float = 0.5,
+                 top_fraction: float = 0.9) -> np.ndarray:
+    scores = _c(scores, np.float64)
+    h = _c(history if history is not None else [0.0], np.float64)
+    nh = 0 if history is None else h.size
+    out = np.zeros(scores.size, np.float64)
+    _check(lib.orc_lrfu_preview(_ptr(scores), scores.size, _ptr(h), nh, lam, top_fraction, _ptr(out)))
+    return out
 
 
 # ---- block formats and gather ---------------------------------------------
@@ -472,3 +548,58 @@ def ref_pick_scored_blocks(scores: np.ndarray, budget: int, mandatory: Sequence[
     _ref_check(ref.ref_pick_scored_blocks(_ptr(scores), n, _ptr(pins), len(mandatory), budget,
                                           int(signed_scores), _ptr(out), C.byref(n_out)))
     return out[: n_out.value].copy()
+
+
+def ref_propagate_query_scores(raw: np.ndarray, graph: Optional[PageGraph] = None, alpha: float = 0.2,
+                               mask: Optional[np.ndarray] = None, block_tokens: int = 64, spans=None,
+                               cross: float = 0.25) -> np.ndarray:
+    """The reference's propagate_query_scores on a page-indexed frame and
+    graph (spans None: no message spans)."""
+    raw = _c(raw, np.float64)
+    n = raw.size
+    g = graph or PageGraph()
+    m = None if mask is None else _c(mask, np.uint8)
+    sp = spans or []
+    b = _c([s[0] for s in sp] or [0], np.uint64)
+    e = _c([s[1] for s in sp] or [0], np.uint64)
+    k = _c([int(s[2]) for s in sp] or [0], np.uint8)
+    out = np.zeros(n, np.float64)
+    _ref_check(ref.ref_propagate_query_scores(_ptr(raw), n, _ptr(m), block_tokens, g.n_rows, _ptr(g.row_source),
+                                              _ptr(g.row_begin), _ptr(g.edge_target), _ptr(g.edge_mass),
+                                              0xFFFFFFFF if spans is None else len(sp), _ptr(b), _ptr(e), _ptr(k),
+                                              alpha, cross, _ptr(out)))
+    return out
+
+
+def ref_graph_accept(block_tokens: int, end: int, samples, topk: int = 4) -> PageGraph:
+    """samples: [(source_position, [(target_token_position, mass), ...])] ->
+    the rows propagation reads after one prepare_graph_accept over [0, end)."""
+    pos = _c([s[0] for s in samples] or [0], np.uint64)
+    begin = [0]
+    for _, mass in samples:
+        begin.append(begin[-1] + len(mass))
+    sb = _c(begin, np.uint32)
+    tg = _c([t for _, ms in samples for t, _ in ms] or [0], np.uint64)
+    ma = _c([w for _, ms in samples for _, w in ms] or [0], np.float64)
+    max_rows = end // block_tokens + 1
+    max_edges = max_rows * topk
+    rs = np.zeros(max_rows, np.uint32)
+    rb = np.zeros(max_rows + 1, np.uint32)
+    et = np.zeros(max(max_edges, 1), np.uint32)
+    em = np.zeros(max(max_edges, 1), np.float64)
+    nr = C.c_uint32()
+    _ref_check(ref.ref_graph_accept(block_tokens, end, len(samples), _ptr(pos), _ptr(sb), _ptr(tg), _ptr(ma), topk,
+                                    max_rows, max_edges, C.byref(nr), _ptr(rs), _ptr(rb), _ptr(et), _ptr(em)))
+    r = nr.value
+    ne = int(rb[r])
+    return PageGraph.from_arrays(rs[:r], rb[:r + 1], et[:ne], em[:ne])
+
+
+def ref_lrfu_preview(scores: np.ndarray, history: Optional[np.ndarray] = None, lam: float = 0.5,
+                     top_fraction: float = 0.9) -> np.ndarray:
+    scores = _c(scores, np.float64)
+    h = _c(history if history is not None else [0.0], np.float64)
+    nh = 0 if history is None else h.size
+    out = np.zeros(scores.size, np.float64)
+    _ref_check(ref.ref_lrfu_preview(_ptr(h), nh, _ptr(scores), scores.size, lam, top_fraction, _ptr(out)))
+    return out

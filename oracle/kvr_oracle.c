@@ -810,3 +810,133 @@ int orc_gather_rope(const uint8_t *history, int fmt, uint32_t width, uint64_t to
     }
     return ORC_OK;
 }
+
+/* ---------------------------------------------------------------------- */
+/* Graph propagation and LRFU                                              */
+/* ---------------------------------------------------------------------- */
+/* span_coefficient (graph_recall.cpp:234-247) of pages i and i+1: 1 when one
+ * span holds both, the cross weight when a span boundary falls inside the
+ * pair, else 1. */
+int orc_span_coefficients(const uint64_t *span_begin, const uint64_t *span_end,
+                          const uint8_t *end_known, uint32_t n_spans, uint32_t block_tokens,
+                          uint32_t pages, double cross, double *out) {
+    if (!block_tokens || !(cross >= 0 && cross <= 1)) return ORC_ERR_ARG;
+    for (uint32_t i = 0; i + 1 < pages; ++i) {
+        const uint64_t begin = (uint64_t)i * block_tokens;
+        const uint64_t end = (uint64_t)(i + 1) * block_tokens + block_tokens;
+        double c = 1;
+        int inside = 0;
+        for (uint32_t s = 0; s < n_spans && !inside; ++s)
+            inside = span_begin[s] <= begin && end <= span_end[s];
+        if (!inside)
+            for (uint32_t s = 0; s < n_spans; ++s)
+                if ((begin < span_begin[s] && span_begin[s] < end) ||
+                    (end_known[s] && begin < span_end[s] && span_end[s] < end)) {
+                    c = cross;
+                    break;
+                }
+        out[i] = c;
+    }
+    return ORC_OK;
+}
+
+/* propagate_query_scores (graph_recall.cpp:494-552): positive evidence moves
+ * one hop, alpha/4 to each adjacent node (:522-531) and alpha/2 over the
+ * source's graph row in proportion to its edge masses among nodes (:532-545);
+ * negative scores stay at their page (:547-551). */
+int orc_propagate_scores(const double *raw, const uint8_t *mask, uint32_t n, uint32_t n_rows,
+                         const uint32_t *row_source, const uint32_t *row_begin,
+                         const uint32_t *edge_target, const double *edge_mass,
+                         const double *neighbor_weight, double alpha, double *out) {
+#define NODE(j) ((j) < n && (!mask || mask[j]))
+    if (!(alpha >= 0 && alpha <= 1)) return ORC_ERR_ARG;
+    double total = 0;
+    uint32_t nodes = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        if (!isfinite(raw[i])) return ORC_ERR_NONFINITE;
+        if (NODE(i)) {
+            ++nodes;
+            total += 0. < raw[i] ? raw[i] : 0.;
+        }
+    }
+    if (!isfinite(total)) return ORC_ERR_NONFINITE;
+    memcpy(out, raw, sizeof(double) * n);
+    if (nodes <= 1 || total == 0 || alpha == 0) return ORC_OK;
+    double *seed = (double *)calloc(n, sizeof(double));
+    for (uint32_t i = 0; i < n; ++i)
+        if (NODE(i)) seed[i] = (0. < raw[i] ? raw[i] : 0.) / total;
+    int rc = ORC_OK;
+    for (uint32_t i = 0; i < n && rc == ORC_OK; ++i) {
+        if (!NODE(i)) continue;
+        for (int dir = -1; dir <= 1; dir += 2) {
+            if (dir < 0 && i == 0) continue;
+            const uint32_t j = dir < 0 ? i - 1 : i + 1;
+            if (!NODE(j)) continue;
+            const double c = neighbor_weight ? neighbor_weight[dir < 0 ? j : i] : 1.;
+            if (!(c >= 0 && c <= 1)) { rc = ORC_ERR_ARG; break; }
+            const double delta = total * seed[i] * (alpha * .25 * c);
+            out[i] -= delta;
+            out[j] += delta;
+        }
+    }
+    for (uint32_t r = 0; r < n_rows && rc == ORC_OK; ++r) {
+        const uint32_t src = row_source[r], e0 = row_begin[r], e1 = row_begin[r + 1];
+        if (e0 > e1) { rc = ORC_ERR_ARG; break; }
+        if (!NODE(src)) continue;
+        double den = 0;
+        for (uint32_t e = e0; e < e1; ++e) {
+            if (!(isfinite(edge_mass[e]) && edge_mass[e] >= 0)) { rc = ORC_ERR_ARG; break; }
+            if (edge_target[e] != src && NODE(edge_target[e])) den += edge_mass[e];
+        }
+        if (rc != ORC_OK || !den) continue;
+        for (uint32_t e = e0; e < e1; ++e) {
+            const uint32_t t = edge_target[e];
+            if (t == src || !NODE(t)) continue;
+            const double delta = total * seed[src] * (alpha * .5 * edge_mass[e] / den);
+            out[src] -= delta;
+            out[t] += delta;
+        }
+    }
+    free(seed);
+    if (rc != ORC_OK) return rc;
+    const double slack = 1e-12 * (1. < total ? total : 1.);
+    for (uint32_t i = 0; i < n; ++i) {
+        const double resid = raw[i] < 0. ? raw[i] : 0.;
+        if (!(isfinite(out[i]) && out[i] >= resid - slack)) return ORC_ERR_ARG;
+        out[i] = resid < out[i] ? out[i] : resid;
+    }
+    return ORC_OK;
+#undef NODE
+}
+
+static int cmp_double(const void *a, const void *b) {
+    const double x = *(const double *)a, y = *(const double *)b;
+    return x < y ? -1 : (y < x ? 1 : 0);
+}
+
+/* LrfuHistory::preview (lrfu.hpp:57-79): the threshold is the score of
+ * ascending rank min(n-1, floor((1-fraction)*n)) (nth_element); scores below
+ * it keep only their negative part. */
+int orc_lrfu_preview(const double *scores, uint32_t n, const double *history, uint32_t n_history,
+                     double lambda, double top_fraction, double *out) {
+    if (!(lambda >= 0 && lambda <= 1) || !(top_fraction > 0 && top_fraction <= 1)) return ORC_ERR_ARG;
+    for (uint32_t i = 0; i < n; ++i)
+        if (!isfinite(scores[i])) return ORC_ERR_NONFINITE;
+    if (!n) return ORC_OK;
+    double threshold = -INFINITY;
+    if (top_fraction < 1) {
+        double *ranked = (double *)malloc(sizeof(double) * n);
+        memcpy(ranked, scores, sizeof(double) * n);
+        qsort(ranked, n, sizeof(double), cmp_double);
+        const double r = (1 - top_fraction) * (double)n;
+        const size_t rank = (size_t)r < n - 1 ? (size_t)r : n - 1;
+        threshold = ranked[rank];
+        free(ranked);
+    }
+    for (uint32_t i = 0; i < n; ++i) {
+        const double h = i < n_history ? history[i] : 0;
+        const double s = scores[i];
+        out[i] = lambda * h + (s >= threshold ? s : (0. < s ? 0. : s));
+    }
+    return ORC_OK;
+}

@@ -41,6 +41,15 @@
  *                                    masked tokens and pages, mass sums to 1)
  *                                    and a per-page log-sum-exp restatement
  *                                    computed independently in the tests
+ *   orc_span_coefficients /          graph_recall_test.cpp:109-131 (graph
+ *   orc_propagate_scores             lifecycle), :167-188 (explicit transport
+ *                                    matrix, alpha 0, negative scores, masked
+ *                                    node, NaN/inf rejected), :311-322
+ *                                    (message locality) known answers; mass
+ *                                    conservation; a dense transport-matrix
+ *                                    restatement in the tests
+ *   orc_lrfu_preview                 kvmem_store_test.cpp:1176-1206 known
+ *                                    answers; the gate by a sorted rank
  *   orc_synth_*                      not a reference algorithm: the shared
  *                                    seeded input generator (moments checked)
  */
@@ -145,6 +154,28 @@ size_t orc_gather_row_bytes(int src_fmt, int mode, uint32_t width);
 int orc_gather(const uint8_t *history, int src_fmt, uint32_t width, uint64_t tokens,
                uint32_t page_tokens, const uint32_t *selected, uint32_t k, int mode,
                uint8_t *slots);
+
+/* ---- graph propagation and LRFU ------------------------------------------ */
+/* Span coefficient of each adjacent page pair (i, i+1), i < pages-1, for
+ * message spans [begin, end) (end_known[s] 0: an open span); no spans: 1.
+ * span_coefficient, graph_recall.cpp:234-247. */
+int orc_span_coefficients(const uint64_t *span_begin, const uint64_t *span_end,
+                          const uint8_t *end_known, uint32_t n_spans, uint32_t block_tokens,
+                          uint32_t pages, double cross, double *out);
+/* propagate_query_scores (graph_recall.cpp:494-552) for a frame whose page i
+ * starts at token i*block_tokens: mask = transport_mask (NULL: all), graph
+ * rows flattened by page (row_source, row_begin, edge_target, edge_mass),
+ * neighbor_weight[i] the coefficient of pages (i, i+1) (NULL: 1).  The
+ * transfers run in ascending page order (the reference's follow its hash
+ * map's iteration order). */
+int orc_propagate_scores(const double *raw, const uint8_t *mask, uint32_t n, uint32_t n_rows,
+                         const uint32_t *row_source, const uint32_t *row_begin,
+                         const uint32_t *edge_target, const double *edge_mass,
+                         const double *neighbor_weight, double alpha, double *out);
+/* LrfuHistory::preview (kvmem/include/kvmem/lrfu.hpp:57-79): the candidate
+ * lambda*history + gated scores. */
+int orc_lrfu_preview(const double *scores, uint32_t n, const double *history, uint32_t n_history,
+                     double lambda, double top_fraction, double *out);
 
 /* ---- seeded synthetic inputs (shared with the device generator) ------- */
 uint64_t orc_synth_bits(uint64_t seed, uint64_t stream, uint64_t counter);

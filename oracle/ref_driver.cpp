@@ -12,11 +12,15 @@
 //                                     (kvmem/src/host/graph_recall.cpp)
 //   KvMemStore::pick_scored_blocks    (kvmem/src/host/kvmem_store.cpp)
 //   layerwise_mean_key_scores         (kvmem/src/host/layerwise_scoring.cpp)
+//   prepare_graph_accept, propagate_query_scores
+//                                     (kvmem/src/host/graph_recall.cpp)
+//   LrfuHistory::preview / score      (kvmem/include/kvmem/lrfu.hpp)
 // Exceptions never cross this boundary: each entry returns 0 on success and a
 // nonzero code on a thrown exception, with the message in ref_last_error().
 #include "kvmem/graph_recall.hpp"
 #include "kvmem/kvmem_store.hpp"
 #include "kvmem/layerwise_scoring.hpp"
+#include "kvmem/lrfu.hpp"
 #include "kvmem/raw_kv_store.hpp"
 
 #include <cstring>
@@ -238,6 +242,96 @@ int ref_pick_scored_blocks(const double* scores, uint32_t n, const uint32_t* man
             store.pick_scored_blocks(candidates, values, pins, budget, signed_scores != 0);
         std::memcpy(out, picked.data(), sizeof(uint32_t) * picked.size());
         *n_out = uint32_t(picked.size());
+    });
+}
+
+// propagate_query_scores over a frame of n pages of block_tokens (page i
+// starts at i*block_tokens, transport mask as given, NULL: every page) and a
+// snapshot holding the given page-indexed rows as sealed rows of one sample.
+// n_spans == UINT32_MAX: no message spans (span_coefficient returns 1).
+int ref_propagate_query_scores(const double* raw, uint32_t n, const uint8_t* mask,
+                               uint32_t block_tokens, uint32_t n_rows, const uint32_t* row_source,
+                               const uint32_t* row_begin, const uint32_t* edge_target,
+                               const double* edge_mass, uint32_t n_spans, const uint64_t* span_begin,
+                               const uint64_t* span_end, const uint8_t* span_known, double alpha,
+                               double cross, double* out) {
+    return guarded([&] {
+        auto frame = kvmem::query_score_frame(uint64_t(n) * block_tokens, block_tokens, 1, 0, 0, {});
+        for (uint32_t i = 0; i < n; ++i) frame.transport_mask[i] = mask ? mask[i] : 1;
+        kvmem::GraphSnapshot graph;
+        graph.block_tokens = block_tokens;
+        graph.accepted_through = graph.completed_through = uint64_t(n) * block_tokens;
+        std::vector<kvmem::GraphRow> rows(n_rows);
+        for (uint32_t r = 0; r < n_rows; ++r) {
+            rows[r].source = uint64_t(row_source[r]) * block_tokens;
+            rows[r].samples = 1;
+            for (uint32_t e = row_begin[r]; e < row_begin[r + 1]; ++e)
+                rows[r].edges.push_back({uint64_t(edge_target[e]) * block_tokens, edge_mass[e]});
+        }
+        if (n_rows) graph.chunks.push_back(std::make_shared<const std::vector<kvmem::GraphRow>>(std::move(rows)));
+        if (n_spans != UINT32_MAX) {
+            std::vector<kvmem::GraphMessageSpan> spans(n_spans);
+            for (uint32_t s = 0; s < n_spans; ++s) spans[s] = {span_begin[s], span_end[s], span_known[s] != 0};
+            graph.set_messages(spans);
+        }
+        const std::vector<double> in(raw, raw + n);
+        const auto result = kvmem::propagate_query_scores(in, frame, graph, alpha, cross);
+        std::memcpy(out, result.data(), sizeof(double) * n);
+    });
+}
+
+// One prepare_graph_accept over tokens [0, end) with the given sampled rows
+// (row s: source position sample_pos[s], mass over token-position targets
+// sample_target[sample_begin[s] .. sample_begin[s+1])), then the snapshot's
+// rows that propagation reads (samples > 0, source block complete),
+// flattened by page.  Capacities: max_rows rows, max_edges edges.
+int ref_graph_accept(uint32_t block_tokens, uint64_t end, uint32_t n_samples, const uint64_t* sample_pos,
+                     const uint32_t* sample_begin, const uint64_t* sample_target, const double* sample_mass,
+                     uint32_t topk, uint32_t max_rows, uint32_t max_edges, uint32_t* n_rows,
+                     uint32_t* row_source, uint32_t* row_begin, uint32_t* edge_target, double* edge_mass) {
+    return guarded([&] {
+        kvmem::GraphSnapshot graph;
+        graph.block_tokens = block_tokens;
+        std::vector<kvmem::AcceptedAttentionRow> rows(n_samples);
+        for (uint32_t s = 0; s < n_samples; ++s) {
+            rows[s].source_position = sample_pos[s];
+            for (uint32_t e = sample_begin[s]; e < sample_begin[s + 1]; ++e)
+                rows[s].mass.push_back({sample_target[e], sample_mass[e]});
+        }
+        graph = kvmem::prepare_graph_accept(graph, 0, end, rows, size_t(1) << 30, topk);
+        uint32_t r = 0, e = 0;
+        row_begin[0] = 0;
+        for (const auto& chunk : graph.chunks)
+            for (const auto& row : *chunk) {
+                if (!row.samples || row.source + block_tokens > graph.completed_through) continue;
+                if (r == max_rows || e + row.edges.size() > max_edges) throw std::length_error("graph capacity");
+                row_source[r] = uint32_t(row.source / block_tokens);
+                for (const auto& edge : row.edges) {
+                    edge_target[e] = uint32_t(edge.target / block_tokens);
+                    edge_mass[e++] = edge.mass;
+                }
+                row_begin[++r] = e;
+            }
+        *n_rows = r;
+    });
+}
+
+// LrfuHistory(lambda, fraction) with committed history (n_history entries,
+// none: a fresh history), one round, one preview; out[i] = score(i).
+int ref_lrfu_preview(const double* history, uint32_t n_history, const double* scores, uint32_t n,
+                     double lambda, double fraction, double* out) {
+    return guarded([&] {
+        kvmem::LrfuHistory h(lambda, fraction);
+        if (n_history) {
+            kvmem::LrfuState state;
+            state.scores = std::make_shared<const std::vector<double>>(history, history + n_history);
+            state.round = 1;
+            state.committed = true;
+            h.restore(state);
+        }
+        h.begin_round();
+        h.preview(std::vector<double>(scores, scores + n));
+        for (uint32_t i = 0; i < n; ++i) out[i] = h.score(i);
     });
 }
 

@@ -69,7 +69,7 @@ def test_struct_layouts_match_header(tmp_path):
     field offsets of include/kvrecall.h."""
     structs = {"kvr_key_history": _capi.KeyHistory, "kvr_query": _capi.Query, "kvr_plane": _capi.Plane,
                "kvr_layer_recall": _capi.LayerRecall, "kvr_rope": _capi.Rope,
-               "kvr_attention_sample": _capi.AttentionSample}
+               "kvr_attention_sample": _capi.AttentionSample, "kvr_page_graph": _capi.PageGraph}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "kvrecall.h"', 'int main(void) {']
     for cname, py in structs.items():
         lines.append(f'printf("{cname} %zu\\n", sizeof({cname}));')

@@ -1,223 +1,216 @@
-"""Recall recorded into a HIP graph and replayed: every replay equals the
-eager call on the same buffers, replays read the buffers' current contents,
-device-side operand errors raised in a replay reach kvr_check once, and the
-calls that cannot be captured refuse before recording anything."""
+"""GPU parity of kvr_propagate_scores and kvr_lrfu_preview (graph
+propagation and the LRFU preview between scoring and selection) against the
+oracle, through the C ABI.
+
+Bars: LRFU candidates bit-exact (the same binary64 operations, no
+contraction); propagated scores within 1e-12 of the evidence total (the
+device adds its transfers as integers in units of <= 2^-61 of the total, the
+reference one by one in its hash map's order), the same bits on every run,
+and exact where the reference is exact (alpha 0, no positive evidence,
+pages outside the transport mask).  Covered: the reference's known answers
+(kvmem/tests/graph_recall_test.cpp:107-126, 167-188, 312-322;
+kvmem_store_test.cpp:1178-1200), random graphs with masks and span
+coefficients up to KVR_GRAPH_MAX_PAGES pages, several lanes, history shorter
+and longer than the frame, ties at the threshold, the selection that follows
+(signed scores, higher id first, as RecallPolicy::query), and every error.
+"""
 import numpy as np
 import pytest
-import torch
 
 import kvmem_amd as K
 import oracle as O
-from gpu_util import dev, host, zeros
-from kvmem_amd.hip import Graph, runtime
+from gpu_util import dev, host, sync, zeros
 
 pytestmark = pytest.mark.gpu
-SEED = 42
-T, HQ, HKV, D, PT, KSEL, LAYERS = 32768, 32, 8, 128, 256, 16, 2
-W = HKV * D
-PAGES = T // PT
 
 
-def _pinned(arr):
-    raw = np.ascontiguousarray(arr).view(np.uint8).ravel()
-    p = K.PinnedBuffer(raw.size)
-    p.numpy()[:] = raw
-    return p
+class DevGraph:
+    """An O.PageGraph uploaded, plus optional neighbor weights."""
+
+    def __init__(self, g: O.PageGraph, nw=None):
+        self.g = g
+        self.t = [dev(g.row_source if g.n_rows else np.zeros(1, np.uint32)),
+                  dev(g.row_begin if g.row_begin.size else np.zeros(1, np.uint32)),
+                  dev(g.edge_target if g.n_edges else np.zeros(1, np.uint32)),
+                  dev(g.edge_mass if g.n_edges else np.zeros(1))]
+        self.nw = None if nw is None else dev(np.asarray(nw, np.float64))
+        self.s = K.make_page_graph(g.n_rows, g.n_edges, *self.t, neighbor_weight=self.nw)
 
 
-@pytest.fixture(scope="module")
-def stack():
-    """Two layers of fp16 history, resident K and pinned K/V, with outputs."""
-    layers = []
-    for l in range(LAYERS):
-        keys = O.synth_normal_f16(SEED, 600 + l, T * W)
-        vals = O.synth_normal_f16(SEED, 610 + l, T * W)
-        q = O.synth_normal_f16(SEED, 620 + l, HQ * D)
-        layers.append(dict(keys=keys, vals=vals, q=q, kd=dev(keys), qd=dev(q), pk=_pinned(keys),
-                           pv=_pinned(vals), s16=zeros(PAGES * W, np.uint16),
-                           scores=zeros(PAGES, np.float64), sel=zeros(KSEL, np.uint32),
-                           cnt=zeros(1, np.uint32), ks=zeros(KSEL * PT * W, np.uint16),
-                           vs=zeros(KSEL * PT * W, np.uint16)))
-    yield layers
-    for b in layers:
-        b["pk"].free()
-        b["pv"].free()
-
-
-def _enqueue(ctx, layers, engine=K.ENGINE_KERNEL):
-    for b in layers:
-        planes = [K.make_plane(b["pk"], K.FMT_F16, W, T, K.GATHER_COPY, b["ks"]),
-                  K.make_plane(b["pv"], K.FMT_F16, W, T, K.GATHER_COPY, b["vs"])]
-        ctx.recall_layer(keys=K.make_keys(b["kd"], K.FMT_F16, T, HKV, D, PT), summaries=b["s16"],
-                         query=K.make_query(b["qd"], K.FMT_F16, 1, HQ, HKV, D), scores=b["scores"],
-                         selected=b["sel"], count=b["cnt"], k=KSEL, aggregation=K.AGG_MEAN,
-                         planes=planes, engine=engine)
-
-
-def _outputs(layers):
-    return [{n: host(b[n], np.uint8).copy() for n in ("s16", "scores", "sel", "cnt", "ks", "vs")}
-            for b in layers]
-
-
-def _clear(layers):
-    for b in layers:
-        for n in ("s16", "scores", "sel", "cnt", "ks", "vs"):
-            b[n].zero_()
-    torch.cuda.synchronize()
-
-
-def _capture(ctx, layers):
-    hip = runtime()
-    g = Graph(hip, ctx.select_stream).begin()
-    try:
-        _enqueue(ctx, layers)
-        join = hip.event()
-        hip.record(join, ctx.copy_stream)  # join the copy stream back
-        hip.wait(ctx.select_stream, join)
-    except Exception:
-        g.abort()
-        raise
-    g.end()
-    hip.destroy_event(join)
-    return g
-
-
-def _expect_oracle(b):
-    _, means = O.page_summaries(b["keys"], O.FMT_F16, T, W, PT)
-    qf = b["q"].view(np.float16).astype(np.float32).reshape(1, 1, HQ, D)
-    return O.pick_scored_blocks(O.page_softmax_scores(means[None], qf, [1], HQ, HKV, D, O.AGG_MEAN), KSEL)
-
-
-def test_graph_replays_match_eager(ctx, stack):
-    _enqueue(ctx, stack)       # eager; also sizes the workspace before capture
+def propagate(ctx, raw, graphs, alpha=.2, mask=None):
+    """raw [lanes][pages]; graphs: one DevGraph per lane (or None)."""
+    raw = np.asarray(raw, np.float64).reshape(len(graphs), -1)
+    lanes, pages = raw.shape
+    sc = dev(raw.ravel())
+    md = None if mask is None else dev(np.asarray(mask, np.uint8).ravel())
+    ctx.propagate_scores(sc, pages, [g.s if g else K.make_page_graph() for g in graphs], alpha, md, lanes)
     ctx.check()
-    eager = _outputs(stack)
-    for b, e in zip(stack, eager):
-        assert np.array_equal(e["sel"].view(np.uint32), _expect_oracle(b))
-    _clear(stack)
-    g = _capture(ctx, stack)
-    try:
-        # capture recorded work without running it
-        assert not any(host(b["cnt"], np.uint32)[0] for b in stack)
-        for rep in range(3):
-            _clear(stack)
-            g.replay()
-            ctx.check()
-            got = _outputs(stack)
-            for l in range(LAYERS):
-                for n in eager[l]:
-                    assert np.array_equal(got[l][n], eager[l][n]), (rep, l, n)
-            # eager work on the same context between replays
-            _enqueue(ctx, stack[:1])
-            ctx.check()
-    finally:
-        g.close()
+    sync()
+    return host(sc, np.float64).reshape(lanes, pages)
 
 
-def test_graph_reads_live_buffers(ctx, stack):
-    """A replay after the query buffers change scores the new queries."""
-    _enqueue(ctx, stack)
+def lrfu(ctx, scores, history=None, lam=.5, f=.9, in_place=False):
+    scores = np.asarray(scores, np.float64)
+    scores = scores.reshape(1, -1) if scores.ndim == 1 else scores
+    lanes, pages = scores.shape
+    sc = dev(scores.ravel())
+    cd = sc if in_place else zeros(scores.size, np.float64)
+    h = None if history is None else np.asarray(history, np.float64).reshape(lanes, -1)
+    hd = None if h is None else dev(h.ravel())
+    ctx.lrfu_preview(sc, pages, cd, hd, 0 if h is None else h.shape[1], lam, f, lanes)
     ctx.check()
-    g = _capture(ctx, stack)
-    saved = [b["qd"].clone() for b in stack]
-    try:
-        for b, l in zip(stack, range(LAYERS)):
-            q2 = O.synth_normal_f16(SEED, 700 + l, HQ * D)
-            b["qd"].copy_(dev(q2))
-            b["q_new"] = q2
-        torch.cuda.synchronize()
-        g.replay()
+    sync()
+    return host(cd, np.float64).reshape(lanes, pages)
+
+
+def tol(raw, mask=None):
+    pos = np.maximum(raw, 0)
+    if mask is not None:
+        pos = pos[np.asarray(mask, bool)]
+    return 1e-12 * max(1.0, pos.sum())
+
+
+def test_known_answers(ctx):
+    g = DevGraph(O.PageGraph([(1, [(0, .8)]), (2, [(1, 1.0)])]))
+    np.testing.assert_allclose(propagate(ctx, [1, 0, 1], [g])[0], [.95, .2, .85], atol=1e-15)
+    np.testing.assert_allclose(propagate(ctx, [8, 0, 1], [g], mask=[0, 1, 1])[0], [8, .15, .85], atol=1e-14)
+    t = DevGraph(O.PageGraph([(2, [(0, 1.0)])]))
+    raw = np.array([.8, -.2, .4])
+    np.testing.assert_allclose(propagate(ctx, raw, [t], alpha=.4)[0], [.8, -.08, .28], atol=1e-15)
+    assert np.array_equal(propagate(ctx, raw, [t], alpha=0)[0], raw)
+    neg = np.array([-.8, -.2, -.4])
+    assert np.array_equal(propagate(ctx, neg, [t], alpha=1)[0], neg)
+    np.testing.assert_allclose(propagate(ctx, raw, [t], alpha=.4, mask=[1, 1, 0])[0], [.72, -.12, .4], atol=1e-15)
+    w = O.span_coefficients([(0, 64, True), (64, 192, True)], 64, 3)
+    np.testing.assert_allclose(propagate(ctx, [1, 0, 0], [DevGraph(O.PageGraph(), w)])[0][:2], [.9875, .0125],
+                               atol=1e-15)
+    # LRFU
+    assert np.array_equal(lrfu(ctx, [-.8, -.6, -.2, -.2], lam=0, f=.5)[0], [-.8, -.6, -.2, -.2])
+    first = lrfu(ctx, [.1, .2, .6, .8], lam=.5, f=.5)[0]
+    assert np.array_equal(first, [0, 0, .6, .8])
+    np.testing.assert_allclose(lrfu(ctx, [-.8, -.2, .4, .8], first, lam=.5, f=.5)[0], [-.8, -.2, .7, 1.2],
+                               atol=1e-12)
+
+
+def random_case(rng, n, rows_frac=1.0):
+    raw = rng.standard_normal(n) * float(10.0 ** rng.integers(-2, 3))
+    rows = []
+    for s in rng.choice(n, size=max(1, int(n * rows_frac)) if n > 1 else 1, replace=False):
+        k = int(rng.integers(0, 5))
+        tg = rng.integers(0, n, k)
+        rows.append((int(s), [(int(t), float(m)) for t, m in zip(tg, rng.uniform(0, 1, k))]))
+    return raw, O.PageGraph(rows)
+
+
+@pytest.mark.parametrize("pages", [2, 255, 256, 257, 1000, 4096, 8192])
+def test_random_graphs(ctx, pages):
+    rng = np.random.default_rng(pages)
+    lanes = 3
+    raws, graphs, dgs, nws = [], [], [], []
+    for l in range(lanes):
+        raw, g = random_case(rng, pages, (0.0, .3, 1.0)[l])
+        nw = None if l == 0 else np.where(rng.uniform(size=pages - 1) < .2, .25, 1.0)
+        raws.append(raw)
+        graphs.append(g)
+        nws.append(nw)
+        dgs.append(DevGraph(g, nw))
+    mask = (rng.uniform(size=(lanes, pages)) < .85).astype(np.uint8)
+    mask[0] = 1
+    got = propagate(ctx, np.stack(raws), dgs, alpha=.3, mask=mask)
+    again = propagate(ctx, np.stack(raws), dgs, alpha=.3, mask=mask)
+    assert np.array_equal(got.view(np.uint64), again.view(np.uint64)), "not deterministic"
+    for l in range(lanes):
+        want = O.propagate_scores(raws[l], graphs[l], .3, mask[l], nws[l])
+        np.testing.assert_allclose(got[l], want, rtol=0, atol=tol(raws[l], mask[l]))
+        off = mask[l] == 0
+        # pages outside the mask keep their score (a -0.0 becomes +0.0, as in the reference)
+        assert np.array_equal(got[l][off], np.maximum(np.minimum(raws[l][off], 0), raws[l][off]))
+
+
+@pytest.mark.parametrize("pages", [1, 7, 256, 1000, 8192])
+def test_lrfu_bit_exact(ctx, pages):
+    rng = np.random.default_rng(500 + pages)
+    lanes = 2
+    s = np.round(rng.standard_normal((lanes, pages)), 2)  # ties at the threshold
+    for f in (.1, .5, .9, .95, 1.0):
+        for hp in (0, pages // 2, pages + 3):
+            h = rng.standard_normal((lanes, hp)) if hp else None
+            lam = float(rng.uniform(0, 1))
+            got = lrfu(ctx, s, h, lam, f)
+            for l in range(lanes):
+                want = O.lrfu_preview(s[l], None if h is None else h[l], lam, f)
+                np.testing.assert_array_equal(got[l].view(np.uint64), want.view(np.uint64))
+    # in place (candidate = scores), all scores equal, and signed zeros
+    z = np.array([[0.0, -0.0, 0.0, -0.0, -1.0, 2.0]])
+    np.testing.assert_array_equal(lrfu(ctx, z, lam=.3, f=.5, in_place=True)[0].view(np.uint64),
+                                  O.lrfu_preview(z[0], None, .3, .5).view(np.uint64))
+    e = np.full((1, 100), 0.25)
+    np.testing.assert_array_equal(lrfu(ctx, e, lam=0, f=.3)[0], O.lrfu_preview(e[0], None, 0, .3))
+
+
+def test_propagate_lrfu_select_pipeline(ctx):
+    """RecallPolicy::query (backends/radiance/adapter/recall_policy.hpp:104-130):
+    scores -> propagate -> LRFU preview -> (score desc, id desc) top budget."""
+    rng = np.random.default_rng(77)
+    pages, k = 4096, 48
+    raw, g = random_case(rng, pages, .5)
+    raw = raw / np.abs(raw).sum()
+    hist = O.lrfu_preview(rng.standard_normal(pages) * 1e-3, None, .5, .9)
+    sc = propagate(ctx, raw, [DevGraph(g)], alpha=.2)[0]
+    cand = lrfu(ctx, sc, hist, .5, .9)[0]
+    want_c = O.lrfu_preview(O.propagate_scores(raw, g, .2), hist, .5, .9)
+    np.testing.assert_allclose(cand, want_c, rtol=0, atol=3e-12)
+    cd = dev(cand)
+    sel, cnt = zeros(k, np.uint32), zeros(1, np.uint32)
+    ctx.select_topk(cd, pages, k, sel, cnt, tie_rule=K.TIE_HIGHER_FIRST, signed_scores=True)
+    ctx.check()
+    sync()
+    want = O.pick_scored_blocks(cand, k, tie_rule=O.TIE_HIGHER_FIRST, signed_scores=True)
+    np.testing.assert_array_equal(host(sel, np.uint32)[:host(cnt, np.uint32)[0]], want)
+    assert np.array_equal(want, O.pick_scored_blocks(want_c, k, tie_rule=O.TIE_HIGHER_FIRST, signed_scores=True))
+
+
+def test_errors(ctx):
+    g = DevGraph(O.PageGraph([(0, [(1, .5)])]))
+    raw = np.array([1.0, np.nan, 2.0])
+    sc = dev(raw)
+    ctx.propagate_scores(sc, 3, [g.s])
+    with pytest.raises(K.KvrError) as e:
         ctx.check()
-        for b in stack:
-            qf = b["q_new"].view(np.float16).astype(np.float32).reshape(1, 1, HQ, D)
-            _, means = O.page_summaries(b["keys"], O.FMT_F16, T, W, PT)
-            s = O.page_softmax_scores(means[None], qf, [1], HQ, HKV, D, O.AGG_MEAN)
-            got = host(b["sel"], np.uint32)
-            assert np.array_equal(got, O.pick_scored_blocks(s, KSEL))
-            assert np.array_equal(host(b["ks"], np.uint8),
-                                  O.gather(b["keys"].view(np.uint8), O.FMT_F16, W, T, PT, got, O.GATHER_COPY))
-    finally:
-        for b, q in zip(stack, saved):
-            b["qd"].copy_(q)
-        torch.cuda.synchronize()
-        g.close()
+    assert e.value.status == K._capi.ERR_SCORES
+    assert np.array_equal(host(sc, np.float64)[[0, 2]], [1.0, 2.0])  # untouched
 
-
-def test_graph_replay_error_is_reported_once(ctx, stack):
-    """A non-finite query in a replay empties that layer's selection and is
-    reported by the next kvr_check; the following good replay is clean."""
-    _enqueue(ctx, stack)
-    ctx.check()
-    g = _capture(ctx, stack)
-    saved = stack[0]["qd"].clone()
-    try:
-        bad = stack[0]["q"].copy()
-        bad[5] = 0x7E00  # fp16 NaN
-        stack[0]["qd"].copy_(dev(bad))
-        torch.cuda.synchronize()
-        g.replay()
+    def graph_error(gr):
+        s = dev(np.array([1.0, 1.0, 1.0]))
+        ctx.propagate_scores(s, 3, [gr.s])
         with pytest.raises(K.KvrError) as e:
             ctx.check()
-        assert e.value.status == K._capi.ERR_NONFINITE
-        assert host(stack[0]["cnt"], np.uint32)[0] == 0
-        stack[0]["qd"].copy_(saved)
-        torch.cuda.synchronize()
-        g.replay()
+        assert e.value.status == K._capi.ERR_GRAPH
+        assert np.array_equal(host(s, np.float64), [1.0, 1.0, 1.0])
+
+    graph_error(DevGraph(O.PageGraph([(0, [(1, -1.0)])])))
+    graph_error(DevGraph(O.PageGraph([(0, [(1, np.inf)])])))
+    graph_error(DevGraph(O.PageGraph(), [1.5, 1.0]))
+    bad = O.PageGraph.from_arrays([0], [1, 0], [1], [1.0])  # row_begin decreasing
+    gb = DevGraph(O.PageGraph([(0, [(1, 1.0)])]))
+    gb.t[1] = dev(bad.row_begin)
+    gb.s = K.make_page_graph(1, 1, *gb.t)
+    graph_error(gb)
+
+    big = zeros(K._capi.GRAPH_MAX_PAGES + 1, np.float64)
+    with pytest.raises(K.KvrError) as e:
+        ctx.propagate_scores(big, K._capi.GRAPH_MAX_PAGES + 1)
+    assert e.value.status == K._capi.ERR_UNSUPPORTED
+    with pytest.raises(K.KvrError) as e:
+        ctx.propagate_scores(dev(np.ones(3)), 3, alpha=1.5)
+    assert e.value.status == K._capi.ERR_INVALID
+    cd = zeros(3, np.float64)
+    for lam, f in ((-.1, .5), (1.1, .5), (.5, 0.0), (.5, 1.5)):
+        with pytest.raises(K.KvrError) as e:
+            ctx.lrfu_preview(dev(np.ones(3)), 3, cd, lam=lam, top_fraction=f)
+        assert e.value.status == K._capi.ERR_INVALID
+    ctx.lrfu_preview(dev(np.array([1.0, np.inf, 0.0])), 3, cd)
+    with pytest.raises(K.KvrError) as e:
         ctx.check()
-        for b in stack:
-            assert host(b["cnt"], np.uint32)[0] == KSEL
-            assert np.array_equal(host(b["sel"], np.uint32), _expect_oracle(b))
-    finally:
-        stack[0]["qd"].copy_(saved)
-        torch.cuda.synchronize()
-        g.close()
-
-
-def test_dma_engine_refuses_capture(ctx, stack):
-    _enqueue(ctx, stack[:1])
-    ctx.check()
-    hip = runtime()
-    g = Graph(hip, ctx.select_stream).begin()
-    try:
-        with pytest.raises(K.KvrError) as e:
-            _enqueue(ctx, stack[:1], engine=K.ENGINE_SDMA)
-        assert "captured" in str(e.value)
-    finally:
-        g.abort()
-    ctx.check()
-
-
-def test_workspace_growth_refuses_capture(stack):
-    """A fresh context has no workspace: growing it inside a capture fails
-    with KVR_ERR_WORKSPACE instead of allocating."""
-    c2 = K.Context(0)
-    hip = runtime()
-    g = Graph(hip, c2.select_stream).begin()
-    try:
-        with pytest.raises(K.KvrError) as e:
-            _enqueue(c2, stack[:1])
-        assert e.value.status == K._capi.ERR_WORKSPACE
-    finally:
-        g.abort()
-    c2.close()
-
-
-def test_timing_events_refuse_capture(ctx, stack):
-    """Summary timing events would not be re-recorded by replays: refused."""
-    _enqueue(ctx, stack[:1])
-    ctx.check()
-    hip = runtime()
-    ev = (hip.event(), hip.event())
-    b = stack[0]
-    g = Graph(hip, ctx.select_stream).begin()
-    try:
-        with pytest.raises(K.KvrError) as e:
-            ctx.recall_layer(keys=K.make_keys(b["kd"], K.FMT_F16, T, HKV, D, PT), summaries=b["s16"],
-                             query=K.make_query(b["qd"], K.FMT_F16, 1, HQ, HKV, D), scores=b["scores"],
-                             selected=b["sel"], count=b["cnt"], k=KSEL, summary_events=ev)
-        assert "captured" in str(e.value)
-    finally:
-        g.abort()
-    for x in ev:
-        hip.destroy_event(x)
-    ctx.check()
+    assert e.value.status == K._capi.ERR_SCORES
+    assert not host(cd, np.float64).any()
