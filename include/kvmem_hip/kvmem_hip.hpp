@@ -7,6 +7,8 @@
 //                        for src/adapter/llama-kvmem-stagein.h:12-68 (bool + stderr)
 //   RecallTransfer       the MemoryTransfer contract (kvmem/include/kvmem/memory_contract.hpp:175-187)
 //   SummaryCapture       the capture side of the attn-qk hook (src/adapter/llama-kvmem-hooks.h:74-98)
+//   GraphRecallHip::propagate_query_scores  (kvmem/include/kvmem/graph_recall.hpp:119-121)
+//   LrfuHistoryHip       for LrfuHistory (kvmem/include/kvmem/lrfu.hpp:43-101)
 // Errors follow the reference: std::invalid_argument for geometry and
 // operand errors, std::length_error for workspace limits, std::runtime_error
 // for device failures.  Reference paths are relative to the KVMem 0.19.0 tree.
@@ -108,6 +110,86 @@ public:
 private:
     struct Impl;
     std::unique_ptr<Impl> impl_;
+};
+
+// ---- graph propagation and LRFU ------------------------------------------
+// The graph types of graph_recall.hpp:47-52 (positions in tokens).
+struct GraphEdge {
+    uint64_t target = 0;
+    double mass = 0;
+};
+struct GraphRow {
+    uint64_t source = 0, samples = 0;
+    std::vector<GraphEdge> edges;
+};
+struct GraphMessageSpan {
+    uint64_t begin = 0, end = 0;
+    bool end_known = true;
+};
+// What propagation reads of a GraphSnapshot (graph_recall.hpp:73-98): the
+// sealed rows (any number of chunks), the block size, the accepted and
+// completed prefixes and the message spans (null: none).
+struct GraphView {
+    uint32_t block_tokens = 64;
+    uint64_t accepted_through = 0, completed_through = 0;
+    std::vector<const std::vector<GraphRow> *> chunks;
+    const std::vector<GraphMessageSpan> *messages = nullptr;
+};
+
+// span_coefficient (graph_recall.cpp:234-247) of every adjacent page pair
+// (i, i+1), i < pages-1: sorted spans, so O((pages + spans) log spans).
+std::vector<double> span_coefficients(const std::vector<GraphMessageSpan> &spans, uint32_t block_tokens,
+                                      uint32_t pages, double cross);
+
+// Graph propagation and the LRFU candidate on one device; synchronous on
+// return like the reference's host functions.
+class GraphRecallHip {
+public:
+    explicit GraphRecallHip(int device);
+    ~GraphRecallHip();
+    GraphRecallHip(const GraphRecallHip &) = delete;
+    GraphRecallHip &operator=(const GraphRecallHip &) = delete;
+
+    // propagate_query_scores (graph_recall.cpp:494-552) for frames whose
+    // page i starts at i * block_tokens (what query_score_frame builds), up
+    // to KVR_GRAPH_MAX_PAGES pages (std::length_error beyond).
+    std::vector<double> propagate_query_scores(const std::vector<double> &raw, const QueryScoreFrame &,
+                                               const GraphView &, double alpha = .2,
+                                               double cross_message_weight = .25);
+    // LrfuHistory::preview's candidate (lrfu.hpp:57-79): lambda * committed +
+    // the gated scores.
+    std::vector<double> lrfu_candidate(const std::vector<double> &scores, const std::vector<double> &committed,
+                                       double lambda, double top_fraction);
+    kvr_context *context() const;
+
+private:
+    struct Impl;
+    std::unique_ptr<Impl> impl_;
+};
+
+// LrfuHistory (lrfu.hpp:43-101): rounds, previews derived from committed
+// history only, one commit per round, checkpoints sharing committed scores.
+struct LrfuState {
+    std::shared_ptr<const std::vector<double>> scores = std::make_shared<const std::vector<double>>();
+    uint64_t round = 0;
+    bool committed = false;
+};
+class LrfuHistoryHip {
+public:
+    explicit LrfuHistoryHip(GraphRecallHip &device, double lambda = 0.5, double top_fraction = 0.9);
+    void begin_round();
+    void preview(const std::vector<double> &scores);
+    bool commit() noexcept;
+    double score(size_t block) const noexcept;
+    LrfuState checkpoint() const { return state_; }
+    void restore(const LrfuState &state);
+    void discard_candidate() noexcept { candidate_.reset(); }
+
+private:
+    GraphRecallHip *device_;
+    double lambda_, fraction_;
+    LrfuState state_;
+    std::shared_ptr<const std::vector<double>> candidate_;
 };
 
 // ---- stage-in entry points (llama-kvmem-stagein.h) ------------------------

@@ -449,6 +449,17 @@ kvr_status kvr_lrfu_preview(kvr_context *ctx, const double *scores, uint32_t lan
                             const double *history, uint32_t history_pages, double lambda,
                             double top_fraction, double *candidate, void *stream);
 
+/* kvr_propagate_scores then kvr_lrfu_preview of the propagated scores, in
+ * one launch: scores end propagated, candidate holds the LRFU candidate
+ * (the sequence RecallPolicy::query runs,
+ * backends/radiance/adapter/recall_policy.hpp:104-117).  Errors as the two
+ * calls; a lane whose propagation fails writes neither output (errors are
+ * per lane here and in both calls: other lanes complete). */
+kvr_status kvr_propagate_lrfu(kvr_context *ctx, double *scores, uint32_t lanes, uint32_t pages,
+                              const uint8_t *transport_mask, const kvr_page_graph *graphs, double alpha,
+                              const double *history, uint32_t history_pages, double lambda,
+                              double top_fraction, double *candidate, void *stream);
+
 /* ---- device copies ------------------------------------------------------- */
 
 /* One launch of n byte copies (16-byte path when aligned).  Replaces

@@ -234,6 +234,12 @@ class Context:
         check(lib().kvr_lrfu_preview(self.handle, _ptr(scores), lanes, pages, _ptr(history), history_pages, lam,
                                      top_fraction, _ptr(candidate), stream))
 
+    def propagate_lrfu(self, scores, pages, candidate, graphs: Sequence = (), alpha=0.2, transport_mask=None,
+                       history=None, history_pages=0, lam=0.5, top_fraction=0.9, lanes=1, stream=None) -> None:
+        arr = (_capi.PageGraph * max(1, len(graphs)))(*graphs) if graphs else None
+        check(lib().kvr_propagate_lrfu(self.handle, _ptr(scores), lanes, pages, _ptr(transport_mask), arr, alpha,
+                                       _ptr(history), history_pages, lam, top_fraction, _ptr(candidate), stream))
+
     # -- stage-in -----------------------------------------------------------
     def stage_in(self, planes: Sequence, page_tokens, selected, count, k, lanes=1, engine=ENGINE_AUTO,
                  stream=None) -> None:

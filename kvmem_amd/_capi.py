@@ -102,6 +102,8 @@ _SIGNATURES = {
     "kvr_attention_page_mass": (_i, [_P, C.POINTER(AttentionSample), _P, _P]),
     "kvr_propagate_scores": (_i, [_P, _P, _u32, _u32, _P, C.POINTER(PageGraph), C.c_double, _P]),
     "kvr_lrfu_preview": (_i, [_P, _P, _u32, _u32, _P, _u32, C.c_double, C.c_double, _P, _P]),
+    "kvr_propagate_lrfu": (_i, [_P, _P, _u32, _u32, _P, C.POINTER(PageGraph), C.c_double, _P, _u32, C.c_double,
+                                C.c_double, _P, _P]),
     "kvr_d2d_batched": (_i, [_P, C.POINTER(_P), C.POINTER(_P), C.POINTER(_sz), _u32, _P]),
     "kvr_host_alloc": (_i, [_sz, C.POINTER(_P)]),
     "kvr_host_free": (_i, [_P]),

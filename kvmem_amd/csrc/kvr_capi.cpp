@@ -954,13 +954,9 @@ kvr_status check_graph_frame(kvr_context *ctx, const double *scores, uint32_t pa
 }
 }  // namespace
 
-kvr_status kvr_propagate_scores(kvr_context *ctx, double *scores, uint32_t lanes, uint32_t pages,
-                                const uint8_t *transport_mask, const kvr_page_graph *graphs, double alpha,
-                                void *stream) {
-    if (kvr_status s = check_graph_frame(ctx, scores, pages)) return s;
-    lanes = lanes ? lanes : 1;
-    if (!(alpha >= 0.0 && alpha <= 1.0)) return fail(KVR_ERR_INVALID, "invalid attention decay (alpha)");
-    std::vector<kvr::GraphLane> g(lanes);
+namespace {
+kvr_status graph_lanes(const kvr_page_graph *graphs, uint32_t lanes, std::vector<kvr::GraphLane> &g) {
+    g.assign(lanes, kvr::GraphLane{});
     for (uint32_t l = 0; graphs && l < lanes; ++l) {
         const kvr_page_graph &x = graphs[l];
         if (x.n_rows && (!x.row_source || !x.row_begin))
@@ -969,34 +965,15 @@ kvr_status kvr_propagate_scores(kvr_context *ctx, double *scores, uint32_t lanes
             return fail(KVR_ERR_INVALID, "graph edges need edge_target and edge_mass (lane %u)", l);
         g[l] = {x.n_rows, x.n_edges, x.row_source, x.row_begin, x.edge_target, x.edge_mass, x.neighbor_weight};
     }
-    DeviceGuard guard(ctx->device);
-    ++ctx->epoch;
-    kvr::GraphLrfuArgs a{};
-    a.scores = scores;
-    a.mask = transport_mask;
-    a.pages = pages;
-    a.propagate = 1;
-    a.alpha = alpha;
-    a.status = ctx->status;
-    a.epoch = ctx->epoch;
-    KVR_HIP(kvr::launch_graph_lrfu(a, g.data(), lanes, stream_or(stream, ctx->sel)));
     return KVR_OK;
 }
 
-kvr_status kvr_lrfu_preview(kvr_context *ctx, const double *scores, uint32_t lanes, uint32_t pages,
-                            const double *history, uint32_t history_pages, double lambda, double top_fraction,
-                            double *candidate, void *stream) {
-    if (kvr_status s = check_graph_frame(ctx, scores, pages)) return s;
-    lanes = lanes ? lanes : 1;
+kvr_status lrfu_args(const double *history, uint32_t history_pages, double lambda, double top_fraction,
+                     double *candidate, uint32_t pages, kvr::GraphLrfuArgs &a) {
     if (!candidate) return fail(KVR_ERR_INVALID, "candidate is required");
     if (history_pages && !history) return fail(KVR_ERR_INVALID, "history_pages without history");
     if (!(lambda >= 0.0 && lambda <= 1.0) || !(top_fraction > 0.0 && top_fraction <= 1.0))
         return fail(KVR_ERR_INVALID, "invalid LRFU decay or hit fraction");
-    DeviceGuard guard(ctx->device);
-    ++ctx->epoch;
-    kvr::GraphLrfuArgs a{};
-    a.scores = const_cast<double *>(scores);
-    a.pages = pages;
     a.lrfu = 1;
     a.history = history_pages ? history : nullptr;
     a.history_pages = history_pages;
@@ -1008,11 +985,66 @@ kvr_status kvr_lrfu_preview(kvr_context *ctx, const double *scores, uint32_t lan
         a.rank = std::min<uint32_t>(pages - 1, uint32_t(r));
     }
     a.candidate = candidate;
+    return KVR_OK;
+}
+
+kvr_status launch_rescore(kvr_context *ctx, kvr::GraphLrfuArgs &a, const std::vector<kvr::GraphLane> &g,
+                          uint32_t lanes, void *stream) {
+    DeviceGuard guard(ctx->device);
+    ++ctx->epoch;
     a.status = ctx->status;
     a.epoch = ctx->epoch;
-    std::vector<kvr::GraphLane> g(lanes);
     KVR_HIP(kvr::launch_graph_lrfu(a, g.data(), lanes, stream_or(stream, ctx->sel)));
     return KVR_OK;
+}
+}  // namespace
+
+kvr_status kvr_propagate_scores(kvr_context *ctx, double *scores, uint32_t lanes, uint32_t pages,
+                                const uint8_t *transport_mask, const kvr_page_graph *graphs, double alpha,
+                                void *stream) {
+    if (kvr_status s = check_graph_frame(ctx, scores, pages)) return s;
+    lanes = lanes ? lanes : 1;
+    if (!(alpha >= 0.0 && alpha <= 1.0)) return fail(KVR_ERR_INVALID, "invalid attention decay (alpha)");
+    std::vector<kvr::GraphLane> g;
+    if (kvr_status s = graph_lanes(graphs, lanes, g)) return s;
+    kvr::GraphLrfuArgs a{};
+    a.scores = scores;
+    a.mask = transport_mask;
+    a.pages = pages;
+    a.propagate = 1;
+    a.alpha = alpha;
+    return launch_rescore(ctx, a, g, lanes, stream);
+}
+
+kvr_status kvr_lrfu_preview(kvr_context *ctx, const double *scores, uint32_t lanes, uint32_t pages,
+                            const double *history, uint32_t history_pages, double lambda, double top_fraction,
+                            double *candidate, void *stream) {
+    if (kvr_status s = check_graph_frame(ctx, scores, pages)) return s;
+    lanes = lanes ? lanes : 1;
+    kvr::GraphLrfuArgs a{};
+    a.scores = const_cast<double *>(scores);
+    a.pages = pages;
+    if (kvr_status s = lrfu_args(history, history_pages, lambda, top_fraction, candidate, pages, a)) return s;
+    return launch_rescore(ctx, a, std::vector<kvr::GraphLane>(lanes), lanes, stream);
+}
+
+kvr_status kvr_propagate_lrfu(kvr_context *ctx, double *scores, uint32_t lanes, uint32_t pages,
+                              const uint8_t *transport_mask, const kvr_page_graph *graphs, double alpha,
+                              const double *history, uint32_t history_pages, double lambda, double top_fraction,
+                              double *candidate, void *stream) {
+    if (kvr_status s = check_graph_frame(ctx, scores, pages)) return s;
+    lanes = lanes ? lanes : 1;
+    if (!(alpha >= 0.0 && alpha <= 1.0)) return fail(KVR_ERR_INVALID, "invalid attention decay (alpha)");
+    std::vector<kvr::GraphLane> g;
+    if (kvr_status s = graph_lanes(graphs, lanes, g)) return s;
+    kvr::GraphLrfuArgs a{};
+    a.scores = scores;
+    a.mask = transport_mask;
+    a.pages = pages;
+    a.propagate = 1;
+    a.alpha = alpha;
+    if (kvr_status s = lrfu_args(history, history_pages, lambda, top_fraction, candidate, pages, a)) return s;
+    return launch_rescore(ctx, a, g, lanes, stream);
 }
 
 kvr_status kvr_stage_in(kvr_context *ctx, const kvr_plane *planes, uint32_t n_planes, uint32_t lanes,

@@ -1204,7 +1204,7 @@ __device__ __forceinline__ void wg_select(const SelectArgs &a, uint32_t lane, bo
 // ---------------------------------------------------------------------------
 // Graph propagation (propagate_query_scores, kvmem/src/host/graph_recall.cpp:
 // 494-552) and LRFU preview (LrfuHistory::preview, kvmem/include/kvmem/
-// lrfu.hpp:57-79), one lane per workgroup, the lane's pages in LDS.
+// lrfu.hpp:57-79), one lane per 1024-thread workgroup.
 //
 // Propagation is a sum of transfers: node i gives (total * seed_i) * w to
 // node j and loses as much, seed_i = max(0, raw_i) / total, w = alpha/4 times
@@ -1224,9 +1224,14 @@ __device__ __forceinline__ int64_t graph_units(double delta, int shift) {
     return static_cast<int64_t>(rint(ldexp(delta, shift)));
 }
 
-__global__ __launch_bounds__(256) void k_graph_lrfu(GraphLrfuArgs a) {
+// Thread t owns the pages [t*C, t*C + C), C = ceil(pages/1024) <= 8, and
+// holds them with one page either side in registers; graph rows go one per
+// thread with their first four edges loaded in one round trip.
+constexpr uint32_t kGraphThreads = 1024, kGraphChunk = kGraphMaxPages / kGraphThreads;
+
+__global__ __launch_bounds__(1024) void k_graph_lrfu(GraphLrfuArgs a) {
 #pragma clang fp contract(off)
-    constexpr uint32_t B = 256, W = B / kWave;
+    constexpr uint32_t B = kGraphThreads, W = B / kWave, CH = kGraphChunk, EB = 4;
     __shared__ double s_sum[W];
     __shared__ uint32_t s_cnt[W], s_bad[W];
     __shared__ uint64_t s_red[2][W];
@@ -1237,9 +1242,9 @@ __global__ __launch_bounds__(256) void k_graph_lrfu(GraphLrfuArgs a) {
     const GraphLane g = a.graph[blockIdx.x];
     double *sc = a.scores + uint64_t(lane) * n;
     const uint8_t *mk = a.mask ? a.mask + uint64_t(lane) * n : nullptr;
-    int64_t *net = reinterpret_cast<int64_t *>(tail_keys);  // transfer units, then the values
-    double *val = reinterpret_cast<double *>(tail_keys);
-    const uint32_t C = (n + B - 1) / B, j0 = min(n, tid * C), j1 = min(n, j0 + C);
+    int64_t *net = reinterpret_cast<int64_t *>(tail_keys);  // transfer units per page
+    const uint32_t C = (n + B - 1) / B;
+    const uint32_t j0 = min(n, tid * C), cnt = min(n, j0 + C) - j0;
     auto node = [&](uint32_t j) { return j < n && (!mk || mk[j]); };
     // workgroup OR of a flag (every thread gets it)
     auto any = [&](uint32_t flag) {
@@ -1252,30 +1257,44 @@ __global__ __launch_bounds__(256) void k_graph_lrfu(GraphLrfuArgs a) {
         lds_barrier();
         return r != 0;
     };
+    // pages j0-1 .. j0+CH: ve[c] is page j0-1+c (0 outside the lane)
+    double ve[CH + 2];
+    bool ne[CH + 2];
+#pragma unroll
+    for (uint32_t c = 0; c < CH + 2; ++c) {
+        const uint32_t p = j0 + c - 1;  // wraps to UINT32_MAX for j0 = 0, c = 0
+        const bool in = (c >= 1 && c <= cnt) || ((c == 0 || c == cnt + 1) && a.propagate && cnt && p < n);
+        ve[c] = in ? sc[p] : 0.;
+        ne[c] = in && (!mk || mk[p]);
+    }
+    double v[CH];  // this thread's values: the scores, then the propagated ones
+    uint32_t bad = 0;
+#pragma unroll
+    for (uint32_t c = 0; c < CH; ++c) {
+        v[c] = ve[c + 1];
+        if (c < cnt) bad |= !__builtin_isfinite(v[c]);
+    }
 
     if (a.propagate) {
         double part = 0;
-        uint32_t cnt = 0, bad = 0;
-        for (uint32_t j = j0; j < j1; ++j) {
-            const double r = sc[j];
-            if (!__builtin_isfinite(r)) {
-                bad = 1;
-            } else if (node(j)) {
-                ++cnt;
-                part += 0. < r ? r : 0.;
+        uint32_t nodes = 0;
+#pragma unroll
+        for (uint32_t c = 0; c < CH; ++c)
+            if (c < cnt && ne[c + 1]) {
+                ++nodes;
+                part += 0. < v[c] ? v[c] : 0.;
             }
-        }
         part = wave_sum(part);
-        cnt = wave_sum(cnt);
+        nodes = wave_sum(nodes);
         bad = wave_max(bad);
         if (l == 0) {
             s_sum[w] = part;
-            s_cnt[w] = cnt;
+            s_cnt[w] = nodes;
             s_bad[w] = bad;
         }
         lds_barrier();
         double total = 0;
-        uint32_t nodes = 0;
+        nodes = 0;
         bad = 0;
 #pragma unroll
         for (uint32_t i = 0; i < W; ++i) {
@@ -1293,31 +1312,38 @@ __global__ __launch_bounds__(256) void k_graph_lrfu(GraphLrfuArgs a) {
             (void)frexp(total, &e);  // total < 2^e
             const int shift = 62 - e;
             const double wn = a.alpha * .25, wr = a.alpha * .5;
-            auto base = [&](uint32_t j) {
-                const double r = sc[j];
+            auto base = [&](double r) {
                 const double seed = (0. < r ? r : 0.) / total;
                 return total * seed;
             };
             uint32_t gbad = 0;
+            // span coefficient of the pair (j0-1+c, j0+c), c = 0..CH
+            double pw[CH + 1];
+#pragma unroll
+            for (uint32_t c = 0; c < CH + 1; ++c) {
+                const uint32_t i = j0 + c;
+                const bool in = g.neighbor_weight && i >= 1 && i < n && c <= cnt;
+                pw[c] = in ? g.neighbor_weight[i - 1] : 1.;
+            }
             // adjacent pages: each page sums what it receives and gives
-            for (uint32_t j = j0; j < j1; ++j) {
+#pragma unroll
+            for (uint32_t c = 0; c < CH; ++c) {
+                if (c >= cnt) continue;
                 int64_t q = 0;
-                if (node(j)) {
-                    const double bj = base(j);
-                    if (j > 0 && node(j - 1)) {
-                        const double c = g.neighbor_weight ? g.neighbor_weight[j - 1] : 1.;
-                        gbad |= !(c >= 0. && c <= 1.);
-                        const double wt = wn * c;
-                        q += graph_units(base(j - 1) * wt, shift) - graph_units(bj * wt, shift);
+                if (ne[c + 1]) {
+                    const double bj = base(ve[c + 1]);
+                    if (ne[c]) {
+                        gbad |= !(pw[c] >= 0. && pw[c] <= 1.);
+                        const double wt = wn * pw[c];
+                        q += graph_units(base(ve[c]) * wt, shift) - graph_units(bj * wt, shift);
                     }
-                    if (node(j + 1)) {
-                        const double c = g.neighbor_weight ? g.neighbor_weight[j] : 1.;
-                        gbad |= !(c >= 0. && c <= 1.);
-                        const double wt = wn * c;
-                        q += graph_units(base(j + 1) * wt, shift) - graph_units(bj * wt, shift);
+                    if (ne[c + 2]) {
+                        gbad |= !(pw[c + 1] >= 0. && pw[c + 1] <= 1.);
+                        const double wt = wn * pw[c + 1];
+                        q += graph_units(base(ve[c + 2]) * wt, shift) - graph_units(bj * wt, shift);
                     }
                 }
-                net[j] = q;
+                net[j0 + c] = q;
             }
             lds_barrier();
             // graph rows: one thread per row, its edges in order
@@ -1329,70 +1355,86 @@ __global__ __launch_bounds__(256) void k_graph_lrfu(GraphLrfuArgs a) {
                     continue;
                 }
                 if (!node(src)) continue;
+                const double rs = sc[src];
+                double m4[EB];
+                uint32_t t4[EB];
+#pragma unroll
+                for (uint32_t u = 0; u < EB; ++u) {
+                    const bool in = e0 + u < e1;
+                    m4[u] = in ? g.edge_mass[e0 + u] : 0.;
+                    t4[u] = in ? g.edge_target[e0 + u] : src;
+                }
+                bool n4[EB];
                 double den = 0;
-                for (uint32_t e = e0; e < e1; ++e) {
+#pragma unroll
+                for (uint32_t u = 0; u < EB; ++u) {
+                    n4[u] = t4[u] != src && node(t4[u]);
+                    if (e0 + u < e1) gbad |= !(m4[u] >= 0. && m4[u] <= __DBL_MAX__);
+                    if (n4[u]) den += m4[u];
+                }
+                for (uint32_t e = e0 + EB; e < e1; ++e) {
                     const double m = g.edge_mass[e];
                     gbad |= !(m >= 0. && m <= __DBL_MAX__);
                     const uint32_t t = g.edge_target[e];
                     if (t != src && node(t)) den += m;
                 }
                 if (!(den != 0.)) continue;
-                const double bs = base(src);
+                const double bs = base(rs);
                 if (bs == 0.) continue;
                 uint64_t given = 0;
-                for (uint32_t e = e0; e < e1; ++e) {
-                    const uint32_t t = g.edge_target[e];
-                    if (t == src || !node(t)) continue;
-                    const double wt = wr * g.edge_mass[e] / den;
+                auto give = [&](uint32_t t, double m) {
+                    const double wt = wr * m / den;
                     const uint64_t q = uint64_t(graph_units(bs * wt, shift));
                     atomicAdd(reinterpret_cast<unsigned long long *>(net + t), (unsigned long long)q);
                     given += q;
+                };
+#pragma unroll
+                for (uint32_t u = 0; u < EB; ++u)
+                    if (n4[u]) give(t4[u], m4[u]);
+                for (uint32_t e = e0 + EB; e < e1; ++e) {
+                    const uint32_t t = g.edge_target[e];
+                    if (t != src && node(t)) give(t, g.edge_mass[e]);
                 }
                 atomicAdd(reinterpret_cast<unsigned long long *>(net + src), (unsigned long long)(0ull - given));
             }
             lds_barrier();
             const double slack = 1e-12 * (1. < total ? total : 1.);
-            for (uint32_t j = j0; j < j1; ++j) {
-                const double r = sc[j];
-                const int64_t q = net[j];
+#pragma unroll
+            for (uint32_t c = 0; c < CH; ++c) {
+                if (c >= cnt) continue;
+                const double r = v[c];
+                const int64_t q = net[j0 + c];
                 double o = q ? r + ldexp(double(q), -shift) : r;
                 const double resid = r < 0. ? r : 0.;
                 gbad |= !(o >= resid - slack);
-                o = resid < o ? o : resid;
-                val[j] = o;
+                v[c] = resid < o ? o : resid;
             }
             if (any(gbad)) {
                 if (tid == 0) raise_status(a.status, kStatusGraph, a.epoch);
                 return;
             }
-            for (uint32_t j = j0; j < j1; ++j) sc[j] = val[j];
-        } else if (a.lrfu) {
-            for (uint32_t j = j0; j < j1; ++j) val[j] = sc[j];
+#pragma unroll
+            for (uint32_t c = 0; c < CH; ++c)
+                if (c < cnt) sc[j0 + c] = v[c];
         }
-    } else if (a.lrfu) {
-        uint32_t bad = 0;
-        for (uint32_t j = j0; j < j1; ++j) {
-            const double v = sc[j];
-            bad |= !__builtin_isfinite(v);
-            val[j] = v;
-        }
-        if (any(bad)) {
-            if (tid == 0) raise_status(a.status, kStatusScores, a.epoch);
-            return;
-        }
+    } else if (any(bad)) {
+        if (tid == 0) raise_status(a.status, kStatusScores, a.epoch);
+        return;
     }
     if (!a.lrfu) return;
 
     // LRFU: threshold key of ascending rank `rank`, i.e. the (n - rank)-th
-    // largest (every thread reads only its own chunk of val)
+    // largest, by a radix select over the registers
     uint64_t thr = 0;
     if (a.gate) {
         uint64_t and_all = ~0ull, or_all = 0;
-        for (uint32_t j = j0; j < j1; ++j) {
-            const uint64_t k = order_key(val[j]);
-            and_all &= k;
-            or_all |= k;
-        }
+#pragma unroll
+        for (uint32_t c = 0; c < CH; ++c)
+            if (c < cnt) {
+                const uint64_t k = order_key(v[c]);
+                and_all &= k;
+                or_all |= k;
+            }
         and_all = wave_and(and_all);
         or_all = wave_or(or_all);
         if (l == 0) {
@@ -1414,16 +1456,18 @@ __global__ __launch_bounds__(256) void k_graph_lrfu(GraphLrfuArgs a) {
             for (int pos = top / 8 * 8;; pos -= 8) {
                 const uint64_t hi_mask = pos + 8 >= 64 ? 0ull : ~0ull << (pos + 8);
                 const uint64_t want = prefix & hi_mask;
-                hist[tid] = 0;
+                if (tid < 256) hist[tid] = 0;
                 lds_barrier();
-                for (uint32_t j = j0; j < j1; ++j) {
-                    const uint64_t k = order_key(val[j]);
-                    if ((k & hi_mask) == want) atomicAdd(&hist[(k >> pos) & 255u], 1u);
-                }
+#pragma unroll
+                for (uint32_t c = 0; c < CH; ++c)
+                    if (c < cnt) {
+                        const uint64_t k = order_key(v[c]);
+                        if ((k & hi_mask) == want) atomicAdd(&hist[(k >> pos) & 255u], 1u);
+                    }
                 lds_barrier();
                 if (w == 0) {
-                    uint32_t d, rem, cnt;
-                    radix_find(hist, remaining, d, rem, cnt);
+                    uint32_t d, rem, cn;
+                    radix_find(hist, remaining, d, rem, cn);
                     if (l == 0) {
                         s_ctl[0] = d;
                         s_ctl[1] = rem;
@@ -1441,11 +1485,15 @@ __global__ __launch_bounds__(256) void k_graph_lrfu(GraphLrfuArgs a) {
     const double lam = a.lambda;
     const double *h = a.history ? a.history + uint64_t(lane) * a.history_pages : nullptr;
     double *cd = a.candidate + uint64_t(lane) * n;
-    for (uint32_t j = j0; j < j1; ++j) {
-        const double v = val[j];
-        const double hv = j < a.history_pages ? h[j] : 0.;
-        const double kept = (!a.gate || order_key(v) >= thr) ? v : (0. < v ? 0. : v);
-        cd[j] = lam * hv + kept;
+    double hv[CH];
+#pragma unroll
+    for (uint32_t c = 0; c < CH; ++c) hv[c] = (c < cnt && j0 + c < a.history_pages) ? h[j0 + c] : 0.;
+#pragma unroll
+    for (uint32_t c = 0; c < CH; ++c) {
+        if (c >= cnt) continue;
+        const double x = v[c];
+        const double kept = (!a.gate || order_key(x) >= thr) ? x : (0. < x ? 0. : x);
+        cd[j0 + c] = lam * hv[c] + kept;
     }
 }
 
@@ -2374,7 +2422,7 @@ hipError_t launch_graph_lrfu(GraphLrfuArgs a, const GraphLane *graphs, uint32_t 
         const uint32_t nl = lanes - l0 < kGraphLanes ? lanes - l0 : kGraphLanes;
         a.lane0 = l0;
         for (uint32_t i = 0; i < nl; ++i) a.graph[i] = graphs[l0 + i];
-        hipLaunchKernelGGL(k_graph_lrfu, dim3(nl), dim3(256), lds, s, a);
+        hipLaunchKernelGGL(k_graph_lrfu, dim3(nl), dim3(kGraphThreads), lds, s, a);
         if (hipError_t e = hipGetLastError()) return e;
     }
     return hipSuccess;

@@ -425,6 +425,235 @@ std::vector<uint32_t> PageSoftmaxHip::pick(const std::vector<double> &scores, ui
     return out;
 }
 
+// ---- graph propagation and LRFU -------------------------------------------
+std::vector<double> span_coefficients(const std::vector<GraphMessageSpan> &spans, uint32_t block_tokens,
+                                      uint32_t pages, double cross) {
+    require(block_tokens != 0, "invalid block size");
+    require(std::isfinite(cross) && cross >= 0 && cross <= 1, "invalid attention decay");
+    std::vector<std::pair<uint64_t, uint64_t>> by_begin;  // (begin, end) sorted by begin
+    std::vector<uint64_t> begins, known_ends;
+    for (const auto &sp : spans) {
+        by_begin.push_back({sp.begin, sp.end});
+        begins.push_back(sp.begin);
+        if (sp.end_known) known_ends.push_back(sp.end);
+    }
+    std::sort(by_begin.begin(), by_begin.end());
+    std::sort(begins.begin(), begins.end());
+    std::sort(known_ends.begin(), known_ends.end());
+    std::vector<uint64_t> reach(by_begin.size());  // max end over spans [0, i]
+    for (size_t i = 0; i < by_begin.size(); ++i)
+        reach[i] = std::max(by_begin[i].second, i ? reach[i - 1] : 0);
+    // some value of a sorted list strictly inside (lo, hi)
+    auto inside = [](const std::vector<uint64_t> &v, uint64_t lo, uint64_t hi) {
+        const auto it = std::upper_bound(v.begin(), v.end(), lo);
+        return it != v.end() && *it < hi;
+    };
+    std::vector<double> out(pages > 1 ? pages - 1 : 0, 1.0);
+    for (uint32_t i = 0; i + 1 < pages; ++i) {
+        const uint64_t begin = uint64_t(i) * block_tokens, end = uint64_t(i + 2) * block_tokens;
+        // a span holding both pages: among spans beginning at or before
+        // `begin`, the furthest end reaches `end`
+        const auto k = std::upper_bound(by_begin.begin(), by_begin.end(),
+                                        std::make_pair(begin, std::numeric_limits<uint64_t>::max())) -
+                       by_begin.begin();
+        if (k && reach[k - 1] >= end) continue;
+        if (inside(begins, begin, end) || inside(known_ends, begin, end)) out[i] = cross;
+    }
+    return out;
+}
+
+struct GraphRecallHip::Impl {
+    int device = 0;
+    kvr_context *ctx = nullptr;
+    double *scores = nullptr, *hist = nullptr, *nw = nullptr, *mass = nullptr;
+    uint8_t *mask = nullptr;
+    uint32_t *src = nullptr, *begin = nullptr, *target = nullptr;
+    size_t page_cap = 0, row_cap = 0, edge_cap = 0;
+    ~Impl() {
+        if (ctx) {
+            (void)hipSetDevice(device);
+            (void)kvr_check(ctx, nullptr);
+        }
+        for (void *p : {(void *)scores, (void *)hist, (void *)nw, (void *)mask, (void *)src, (void *)begin,
+                        (void *)target, (void *)mass})
+            if (p) (void)hipFree(p);
+        if (ctx) (void)kvr_destroy(ctx);
+    }
+    // replaces p with a device array of n elements (contents not kept)
+    template <class T> static void realloc_dev(T *&p, size_t n) {
+        if (p) hip_ok(hipFree(p), "hipFree");
+        p = nullptr;
+        hip_ok(hipMalloc(reinterpret_cast<void **>(&p), std::max<size_t>(n, 1) * sizeof(T)), "hipMalloc");
+    }
+    void pages(size_t n) {
+        if (n <= page_cap) return;
+        realloc_dev(scores, n);
+        realloc_dev(hist, n);
+        realloc_dev(nw, n);
+        realloc_dev(mask, n);
+        page_cap = n;
+    }
+    void rows(size_t r, size_t e) {
+        if (r + 1 > row_cap) {
+            realloc_dev(src, r + 1);
+            realloc_dev(begin, r + 1);
+            row_cap = r + 1;
+        }
+        if (e > edge_cap) {
+            realloc_dev(target, e);
+            realloc_dev(mass, e);
+            edge_cap = e;
+        }
+    }
+    hipStream_t stream() const { return static_cast<hipStream_t>(kvr_select_stream(ctx)); }
+};
+
+GraphRecallHip::GraphRecallHip(int device) : impl_(new Impl) {
+    impl_->device = device;
+    ok(kvr_create(device, &impl_->ctx), "kvr_create");
+}
+GraphRecallHip::~GraphRecallHip() = default;
+kvr_context *GraphRecallHip::context() const { return impl_->ctx; }
+
+std::vector<double> GraphRecallHip::propagate_query_scores(const std::vector<double> &raw,
+                                                           const QueryScoreFrame &frame, const GraphView &graph,
+                                                           double alpha, double cross) {
+    Impl &m = *impl_;
+    require(std::isfinite(alpha) && alpha >= 0 && alpha <= 1 && std::isfinite(cross) && cross >= 0 && cross <= 1,
+            "invalid attention decay");
+    const size_t n = raw.size();
+    const uint32_t bt = graph.block_tokens;
+    require(bt && frame.starts.size() == n && frame.transport_mask.size() == n &&
+                graph.accepted_through == frame.accepted_through,
+            "graph and Query have different accepted prefixes");
+    for (size_t i = 0; i < n; ++i)
+        require(frame.starts[i] == uint64_t(i) * bt, "invalid or duplicate Query graph identity");
+    if (!n) return raw;
+    if (n > KVR_GRAPH_MAX_PAGES) throw std::length_error("Query frame exceeds KVR_GRAPH_MAX_PAGES pages");
+    // the rows propagation reads, by page; targets that are no page of the
+    // frame stay as non-nodes so their masses are still checked
+    std::vector<uint32_t> src, begin{0}, target;
+    std::vector<double> mass;
+    for (const auto *chunk : graph.chunks)
+        for (const auto &row : *chunk) {
+            if (!row.samples || row.source + bt > graph.completed_through || row.source % bt) continue;
+            const uint64_t sp = row.source / bt;
+            if (sp >= n) continue;
+            src.push_back(uint32_t(sp));
+            for (const auto &e : row.edges) {
+                const uint64_t tp = e.target % bt ? UINT32_MAX : std::min<uint64_t>(e.target / bt, UINT32_MAX);
+                target.push_back(uint32_t(tp));
+                mass.push_back(e.mass);
+            }
+            begin.push_back(uint32_t(target.size()));
+        }
+    std::vector<double> nw;
+    if (graph.messages) nw = span_coefficients(*graph.messages, bt, uint32_t(n), cross);
+    DeviceBinding bind(m.device);
+    m.pages(n);
+    m.rows(src.size(), target.size());
+    const hipStream_t s = m.stream();
+    StreamDrain drain{s};
+    hip_ok(hipMemcpyAsync(m.scores, raw.data(), n * 8, hipMemcpyHostToDevice, s), "scores H2D");
+    hip_ok(hipMemcpyAsync(m.mask, frame.transport_mask.data(), n, hipMemcpyHostToDevice, s), "mask H2D");
+    kvr_page_graph g{};
+    g.n_rows = uint32_t(src.size());
+    g.n_edges = uint32_t(target.size());
+    if (g.n_rows) {
+        hip_ok(hipMemcpyAsync(m.src, src.data(), src.size() * 4, hipMemcpyHostToDevice, s), "rows H2D");
+        hip_ok(hipMemcpyAsync(m.begin, begin.data(), begin.size() * 4, hipMemcpyHostToDevice, s), "rows H2D");
+        g.row_source = m.src;
+        g.row_begin = m.begin;
+    }
+    if (g.n_edges) {
+        hip_ok(hipMemcpyAsync(m.target, target.data(), target.size() * 4, hipMemcpyHostToDevice, s), "edges H2D");
+        hip_ok(hipMemcpyAsync(m.mass, mass.data(), mass.size() * 8, hipMemcpyHostToDevice, s), "edges H2D");
+        g.edge_target = m.target;
+        g.edge_mass = m.mass;
+    }
+    if (!nw.empty()) {
+        hip_ok(hipMemcpyAsync(m.nw, nw.data(), nw.size() * 8, hipMemcpyHostToDevice, s), "weights H2D");
+        g.neighbor_weight = m.nw;
+    }
+    ok(kvr_propagate_scores(m.ctx, m.scores, 1, uint32_t(n), m.mask, &g, alpha, s), "propagate Query scores");
+    std::vector<double> out(n);
+    hip_ok(hipMemcpyAsync(out.data(), m.scores, n * 8, hipMemcpyDeviceToHost, s), "scores D2H");
+    hip_ok(hipStreamSynchronize(s), "hipStreamSynchronize");
+    drain.armed = false;
+    const kvr_status st = kvr_check(m.ctx, s);
+    if (st == KVR_ERR_SCORES) throw std::invalid_argument("nonfinite Query graph seed");
+    if (st == KVR_ERR_GRAPH) throw std::invalid_argument("invalid attention mass or graph propagation result");
+    ok(st, "propagate Query scores");
+    return out;
+}
+
+std::vector<double> GraphRecallHip::lrfu_candidate(const std::vector<double> &scores,
+                                                   const std::vector<double> &committed, double lambda,
+                                                   double top_fraction) {
+    Impl &m = *impl_;
+    const size_t n = scores.size();
+    if (!n) return {};
+    if (n > KVR_GRAPH_MAX_PAGES) throw std::length_error("LRFU frame exceeds KVR_GRAPH_MAX_PAGES pages");
+    const size_t nh = std::min(committed.size(), n);
+    DeviceBinding bind(m.device);
+    m.pages(n);
+    const hipStream_t s = m.stream();
+    StreamDrain drain{s};
+    hip_ok(hipMemcpyAsync(m.scores, scores.data(), n * 8, hipMemcpyHostToDevice, s), "scores H2D");
+    if (nh) hip_ok(hipMemcpyAsync(m.hist, committed.data(), nh * 8, hipMemcpyHostToDevice, s), "history H2D");
+    ok(kvr_lrfu_preview(m.ctx, m.scores, 1, uint32_t(n), nh ? m.hist : nullptr, uint32_t(nh), lambda, top_fraction,
+                        m.scores, s),
+       "LRFU preview");
+    std::vector<double> out(n);
+    hip_ok(hipMemcpyAsync(out.data(), m.scores, n * 8, hipMemcpyDeviceToHost, s), "candidate D2H");
+    hip_ok(hipStreamSynchronize(s), "hipStreamSynchronize");
+    drain.armed = false;
+    const kvr_status st = kvr_check(m.ctx, s);
+    if (st == KVR_ERR_SCORES) throw std::invalid_argument("nonfinite LRFU retrieval score");
+    ok(st, "LRFU preview");
+    return out;
+}
+
+LrfuHistoryHip::LrfuHistoryHip(GraphRecallHip &device, double lambda, double top_fraction)
+    : device_(&device), lambda_(lambda), fraction_(top_fraction) {
+    if (!std::isfinite(lambda) || lambda < 0 || lambda > 1 || !std::isfinite(top_fraction) || top_fraction <= 0 ||
+        top_fraction > 1)
+        throw std::invalid_argument("invalid LRFU decay or hit fraction");
+}
+void LrfuHistoryHip::begin_round() {
+    if (++state_.round == 0) throw std::overflow_error("LRFU round overflow");
+    state_.committed = false;
+    candidate_.reset();
+}
+void LrfuHistoryHip::preview(const std::vector<double> &scores) {
+    if (state_.committed) return;
+    if (!state_.round) throw std::logic_error("LRFU probe outside a round");
+    if (scores.empty()) {
+        candidate_.reset();
+        return;
+    }
+    candidate_ = std::make_shared<const std::vector<double>>(
+        device_->lrfu_candidate(scores, *state_.scores, lambda_, fraction_));
+}
+bool LrfuHistoryHip::commit() noexcept {
+    if (state_.committed || !candidate_) return false;
+    state_.scores = std::move(candidate_);
+    state_.committed = true;
+    return true;
+}
+double LrfuHistoryHip::score(size_t block) const noexcept {
+    const auto &v = candidate_ ? *candidate_ : *state_.scores;
+    return block < v.size() ? v[block] : 0;
+}
+void LrfuHistoryHip::restore(const LrfuState &state) {
+    if (!state.scores || (!state.round && (state.committed || !state.scores->empty())))
+        throw std::invalid_argument("invalid LRFU checkpoint");
+    for (double v : *state.scores)
+        if (!std::isfinite(v)) throw std::invalid_argument("nonfinite LRFU checkpoint");
+    state_ = state;
+    candidate_.reset();
+}
+
 size_t PageSoftmaxHip::device_bytes() const {
     size_t b = kvr_device_bytes(impl_->ctx);
     if (!impl_->borrowed) b += impl_->q_cap * sizeof(float) + (impl_->page_cap ? impl_->page_cap * 13 + 256 : 0);

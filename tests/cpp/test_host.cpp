@@ -662,18 +662,112 @@ void stageout() {
     kh::kvmem_stagein_gpu_free();
 }
 
+// span_coefficients (sorted sweep) against the oracle's pair-by-pair
+// restatement of span_coefficient, on random spans (some open-ended).
+void graph_spans() {
+    std::mt19937_64 rng(21);
+    for (int round = 0; round < 50; ++round) {
+        const uint32_t bt = 1 + uint32_t(rng() % 64), pages = 1 + uint32_t(rng() % 300);
+        std::vector<kh::GraphMessageSpan> spans(rng() % 20);
+        std::vector<uint64_t> b, e;
+        std::vector<uint8_t> k;
+        for (auto &sp : spans) {
+            sp.begin = rng() % (uint64_t(pages) * bt + 1);
+            sp.end = sp.begin + rng() % (uint64_t(bt) * 8 + 1);
+            sp.end_known = rng() % 4 != 0;
+            b.push_back(sp.begin);
+            e.push_back(sp.end);
+            k.push_back(sp.end_known);
+        }
+        const auto got = kh::span_coefficients(spans, bt, pages, .25);
+        std::vector<double> want(pages, 1.0);
+        require(orc_span_coefficients(b.data(), e.data(), k.data(), uint32_t(spans.size()), bt, pages, .25,
+                                      want.data()) == ORC_OK,
+                "oracle spans");
+        want.resize(pages - 1);
+        require(got == want, "span coefficients differ from the pair-by-pair restatement");
+    }
+}
+
+// GraphRecallHip / LrfuHistoryHip on the reference's known answers
+// (kvmem/tests/graph_recall_test.cpp:107-126, 312-322;
+// kvmem_store_test.cpp:1195-1202).
+void graph() {
+    kh::GraphRecallHip dev(0);
+    std::vector<kh::GraphRow> rows = {{64, 1, {{0, .8}}}, {128, 1, {{64, 1.0}}}};
+    kh::GraphView g;
+    g.block_tokens = 64;
+    g.accepted_through = g.completed_through = 192;
+    g.chunks = {&rows};
+    auto frame = kh::query_score_frame(192, 64, 2, 0, 0, {});
+    auto near = [](const std::vector<double> &a, const std::vector<double> &b) {
+        if (a.size() != b.size()) return false;
+        for (size_t i = 0; i < a.size(); ++i)
+            if (std::abs(a[i] - b[i]) > 1e-12) return false;
+        return true;
+    };
+    require(near(dev.propagate_query_scores({1, 0, 1}, frame, g), {.95, .2, .85}), "lifecycle");
+    frame.transport_mask[0] = 0;
+    require(near(dev.propagate_query_scores({8, 0, 1}, frame, g), {8, .15, .85}), "fixed page");
+    // a row whose source block is not complete is not read
+    g.completed_through = 128;
+    frame.transport_mask[0] = 1;
+    require(near(dev.propagate_query_scores({1, 0, 1}, frame, g), {.95, .1, .95}), "incomplete source read");
+    std::vector<kh::GraphRow> none;
+    std::vector<kh::GraphMessageSpan> spans = {{0, 64, true}, {64, 192, true}};
+    kh::GraphView m;
+    m.block_tokens = 64;
+    m.accepted_through = m.completed_through = 192;
+    m.chunks = {&none};
+    m.messages = &spans;
+    const auto crossed = dev.propagate_query_scores({1, 0, 0}, frame, m);
+    require(std::abs(crossed[0] - .9875) < 1e-12 && std::abs(crossed[1] - .0125) < 1e-12, "message locality");
+    bool threw = false;
+    try {
+        dev.propagate_query_scores({0, std::nan(""), 0}, frame, m);
+    } catch (const std::invalid_argument &) {
+        threw = true;
+    }
+    require(threw, "nonfinite seed accepted");
+    threw = false;
+    m.accepted_through = 128;
+    try {
+        dev.propagate_query_scores({1, 0, 0}, frame, m);
+    } catch (const std::invalid_argument &) {
+        threw = true;
+    }
+    require(threw, "mismatched accepted prefix accepted");
+
+    kh::LrfuHistoryHip h(dev, .5, .5);
+    h.begin_round();
+    h.preview({.1, .2, .6, .8});
+    require(h.score(0) == 0 && h.score(1) == 0 && h.score(2) == .6 && h.score(3) == .8, "LRFU first round");
+    require(h.commit(), "commit");
+    const auto checkpoint = h.checkpoint();
+    h.begin_round();
+    h.preview({-.8, -.2, .4, .8});
+    h.preview({-.8, -.2, .4, .8});
+    require(std::abs(h.score(0) + .8) < 1e-12 && std::abs(h.score(1) + .2) < 1e-12 &&
+                std::abs(h.score(2) - .7) < 1e-12 && std::abs(h.score(3) - 1.2) < 1e-12,
+            "LRFU second round");
+    require(h.commit() && !h.commit(), "one commit per round");
+    h.restore(checkpoint);
+    require(h.score(0) == 0 && h.score(2) == .6, "LRFU restore");
+}
+
 }  // namespace
 
 int main(int argc, char **argv) {
     const bool gpu = argc > 1 && std::string(argv[1]) == "--gpu";
     std::vector<std::pair<const char *, std::function<void()>>> tests = {
         {"frames", frames}, {"native_query_geometry", native_query_geometry},
-        {"workspace_geometry", workspace_geometry}, {"stagein_without_state", stagein_without_state}};
+        {"workspace_geometry", workspace_geometry}, {"stagein_without_state", stagein_without_state},
+        {"graph_spans", graph_spans}};
     if (gpu)
         tests = {{"qualification", qualification}, {"current_layer", current_layer}, {"pick", pick},
                  {"stagein", stagein},           {"meank", meank},                 {"transfer", transfer},
                  {"capture", capture}, {"attention", attention}, {"stagein_raw_k", stagein_raw_k},
-                 {"stageout", stageout}};
+                 {"stageout", stageout}, {"graph", graph}};
     for (auto &[name, fn] : tests) {
         std::cout << "RUN  " << name << std::endl;
         try {

@@ -170,6 +170,38 @@ def test_propagate_lrfu_select_pipeline(ctx):
     assert np.array_equal(want, O.pick_scored_blocks(want_c, k, tie_rule=O.TIE_HIGHER_FIRST, signed_scores=True))
 
 
+def test_fused_launch_matches_the_two_calls(ctx):
+    rng = np.random.default_rng(88)
+    lanes, pages = 2, 3000
+    raws, dgs = [], []
+    for _ in range(lanes):
+        raw, g = random_case(rng, pages, .6)
+        raws.append(raw)
+        dgs.append(DevGraph(g, np.where(rng.uniform(size=pages - 1) < .1, .25, 1.0)))
+    raw = np.stack(raws)
+    mask = (rng.uniform(size=(lanes, pages)) < .9).astype(np.uint8)
+    hist = rng.standard_normal((lanes, pages - 100))
+    want_s = propagate(ctx, raw, dgs, alpha=.25, mask=mask)
+    want_c = lrfu(ctx, want_s, hist, .4, .8)
+    sc, cd = dev(raw.ravel()), zeros(raw.size, np.float64)
+    ctx.propagate_lrfu(sc, pages, cd, [g.s for g in dgs], .25, dev(mask.ravel()), dev(hist.ravel()), pages - 100,
+                       .4, .8, lanes)
+    ctx.check()
+    sync()
+    assert np.array_equal(host(sc, np.float64).reshape(lanes, pages).view(np.uint64), want_s.view(np.uint64))
+    assert np.array_equal(host(cd, np.float64).reshape(lanes, pages).view(np.uint64), want_c.view(np.uint64))
+    # a propagation error writes neither output of its lane
+    bad = raw.copy()
+    bad[1, 5] = np.nan
+    sc, cd = dev(bad.ravel()), zeros(raw.size, np.float64)
+    ctx.propagate_lrfu(sc, pages, cd, [g.s for g in dgs], .25, None, None, 0, .4, .8, lanes)
+    with pytest.raises(K.KvrError) as e:
+        ctx.check()
+    assert e.value.status == K._capi.ERR_SCORES
+    assert not host(cd, np.float64).reshape(lanes, pages)[1].any()
+    assert np.array_equal(host(sc, np.float64).reshape(lanes, pages)[1].view(np.uint64), bad[1].view(np.uint64))
+
+
 def test_errors(ctx):
     g = DevGraph(O.PageGraph([(0, [(1, .5)])]))
     raw = np.array([1.0, np.nan, 2.0])
