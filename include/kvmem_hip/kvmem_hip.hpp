@@ -192,6 +192,34 @@ private:
     std::shared_ptr<const std::vector<double>> candidate_;
 };
 
+// ---- native payload records (memory_contract.hpp:39-68) -------------------
+// One record per page holds every layer's planes at fixed offsets.  The
+// types mirror the reference's; validate() restates PayloadLayout::validate
+// (kvmem/src/host/memory_contract.cpp:51-106) and throws std::invalid_argument.
+enum class PayloadPlaneKind { Key, Value, KeyScale, ValueScale, PackedKeyValue };
+struct PayloadPlane {
+    uint32_t layer = 0;
+    PayloadPlaneKind kind = PayloadPlaneKind::Key;
+    uint64_t offset = 0, bytes = 0, alignment = 1;
+    uint64_t token_stride = 0;  // 0: opaque page encoding
+    uint32_t rank = 0, head_begin = 0, head_count = 0;
+};
+struct PayloadLayout {
+    std::string format;
+    uint32_t version = 0, block_tokens = 0;
+    uint64_t record_bytes = 0, alignment = 1;
+    std::vector<PayloadPlane> planes;
+    void validate() const;
+};
+// The stage-in plane of one layer's Key or Value rows (rank `rank`) in a
+// pinned archive of records (page p's record at archive + p * record_bytes),
+// for kvr_stage_in with page_tokens = layout.block_tokens.  The plane must
+// address contiguous token rows of `format` x `width` (token_stride = the
+// row size); std::invalid_argument otherwise.
+kvr_plane record_plane(const PayloadLayout &layout, uint32_t layer, PayloadPlaneKind kind, const void *archive,
+                       kvr_format format, uint32_t width, uint64_t tokens, kvr_gather_mode mode, void *slots,
+                       uint32_t rank = 0);
+
 // ---- stage-in entry points (llama-kvmem-stagein.h) ------------------------
 // bool results with the failure on stderr, one state per execution domain
 // (thread).  The product path sends packed K and V record bytes through

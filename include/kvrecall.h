@@ -161,6 +161,14 @@ typedef struct kvr_plane {
     void *slots;            /* dev */
     size_t host_lane_stride, slot_lane_stride; /* bytes; 0 = tightly packed */
     const kvr_rope *rope;   /* KVR_GATHER_ROPE_FWHT only (else ignored) */
+    /* 0: history is token-major (page p's rows start at p * page_tokens
+     * rows).  Else page p's rows start at history + p * page_stride, one
+     * native payload record per page: history points at the plane's offset
+     * in the first record, page_stride is the record size and the plane's
+     * rows are contiguous (PayloadPlane token_stride = the row size;
+     * kvmem/include/kvmem/memory_contract.hpp:43-68).  host_lane_stride
+     * 0 then means pages * page_stride. */
+    size_t page_stride;
 } kvr_plane;
 
 /* One layer of recall for `lanes` sequences (kvr_recall_layer). */

@@ -121,11 +121,15 @@ def make_page_graph(n_rows=0, n_edges=0, row_source=None, row_begin=None, edge_t
 
 
 def make_plane(history, fmt: int, width: int, tokens: int, mode: int, slots,
-               host_lane_stride: int = 0, slot_lane_stride: int = 0, rope: Optional[dict] = None):
+               host_lane_stride: int = 0, slot_lane_stride: int = 0, rope: Optional[dict] = None,
+               history_offset: int = 0, page_stride: int = 0):
     """rope (for GATHER_ROPE_FWHT): dict(head_dim, n_rot, theta (device
-    float32 tensor of n_rot/2 values), fwht, pos_base)."""
+    float32 tensor of n_rot/2 values), fwht, pos_base).  Record sources:
+    history_offset = the plane's offset in a record, page_stride = the
+    record size."""
     p = _capi.Plane()
-    p.history = _ptr(history)
+    p.history = _ptr(history) + history_offset
+    p.page_stride = page_stride
     p.format, p.width, p.tokens, p.mode = fmt, width, tokens, mode
     p.slots = _ptr(slots)
     p.host_lane_stride, p.slot_lane_stride = host_lane_stride, slot_lane_stride

@@ -51,7 +51,7 @@ class Rope(C.Structure):
 class Plane(C.Structure):
     _fields_ = [("history", _P), ("format", _i), ("width", _u32), ("tokens", _u64), ("mode", _i),
                 ("slots", _P), ("host_lane_stride", _sz), ("slot_lane_stride", _sz),
-                ("rope", C.POINTER(Rope))]
+                ("rope", C.POINTER(Rope)), ("page_stride", _sz)]
 
 
 class LayerRecall(C.Structure):

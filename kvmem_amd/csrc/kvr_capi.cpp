@@ -463,9 +463,13 @@ kvr_status check_planes(const kvr_plane *planes, uint32_t n, uint32_t lanes, uin
             (void)hipGetLastError();
             return fail(KVR_ERR_INVALID, "plane %u: history is not pinned, device-mapped host memory", i);
         }
-        const size_t hls = p.host_lane_stride ? p.host_lane_stride : size_t(p.tokens) * srow;
+        const size_t lane_pages = size_t((p.tokens + page_tokens - 1) / page_tokens);
+        if (p.page_stride && p.page_stride < size_t(page_tokens) * srow)
+            return fail(KVR_ERR_INVALID, "plane %u: a page's rows overlap the next record (page_stride)", i);
+        const size_t src_bytes = p.page_stride ? lane_pages * p.page_stride : size_t(p.tokens) * srow;
+        const size_t hls = p.host_lane_stride ? p.host_lane_stride : src_bytes;
         const size_t sls = p.slot_lane_stride ? p.slot_lane_stride : size_t(k) * page_tokens * drow;
-        if (lanes > 1 && (hls < size_t(p.tokens) * srow || sls < size_t(k) * page_tokens * drow))
+        if (lanes > 1 && (hls < src_bytes || sls < size_t(k) * page_tokens * drow))
             return fail(KVR_ERR_INVALID, "plane %u: lane strides overlap", i);
         PlanePlan &pp = out[i];
         pp.g = kvr::GatherPlane{};
@@ -473,6 +477,7 @@ kvr_status check_planes(const kvr_plane *planes, uint32_t n, uint32_t lanes, uin
         pp.g.dst = static_cast<uint8_t *>(p.slots);
         pp.g.src_lane_stride = hls;
         pp.g.dst_lane_stride = sls;
+        pp.g.page_stride = p.page_stride;
         pp.g.tokens = p.tokens;
         pp.g.src_row = uint32_t(srow);
         pp.g.dst_row = uint32_t(drow);
@@ -609,14 +614,16 @@ kvr_status enqueue_gather_sdma(kvr_context *ctx, PlanePlan *pp, uint32_t n, uint
                 const uint32_t page = ids[slot];
                 const uint64_t first = uint64_t(page) * page_tokens;
                 if (first >= p.g.tokens) { ++slot; continue; }
-                // extend over consecutive pages that are full
+                // extend over consecutive pages that are full (token-major
+                // sources only: records put other planes between pages)
                 uint32_t run = 1;
-                while (slot + run < cnt && ids[slot + run] == page + run &&
+                while (!p.g.page_stride && slot + run < cnt && ids[slot + run] == page + run &&
                        uint64_t(page + run) * page_tokens < p.g.tokens &&
                        uint64_t(page + run) * page_tokens <= p.g.tokens - page_tokens)
                     ++run;
                 const uint64_t rows = std::min<uint64_t>(uint64_t(run) * page_tokens, p.g.tokens - first);
-                const uint8_t *src = p.host + lane * p.g.src_lane_stride + first * p.host_row;
+                const uint8_t *src = p.host + lane * p.g.src_lane_stride +
+                                     (p.g.page_stride ? uint64_t(page) * p.g.page_stride : first * p.host_row);
                 uint8_t *dst = decode ? ctx->staging + at + (size_t(lane) * k + slot) * span
                                       : p.g.dst + lane * p.g.dst_lane_stride + size_t(slot) * page_tokens * p.g.dst_row;
                 KVR_HIP(hipMemcpyAsync(dst, src, rows * p.host_row, hipMemcpyHostToDevice,

@@ -121,6 +121,7 @@ struct GatherPlane {
     uint32_t head_dim, n_rot, fwht;
     float fwht_scale;           // 1/sqrt(fwht) in binary32
     int64_t pos_base;           // position of history token 0
+    uint64_t page_stride;       // 0: token-major source; else page p at p * page_stride
 };
 
 struct GatherArgs {

@@ -2158,10 +2158,12 @@ __global__ __launch_bounds__(256) void k_gather(GatherArgs a) {
         const uint32_t r0 = chunk * a.chunk_rows;
         if (r0 >= valid) continue;
         const uint32_t nr = min(a.chunk_rows, valid - r0);
-        // Staged sources (src_page_stride != 0) hold slot s's page at s*stride.
-        const uint8_t *src = a.src_page_stride
-            ? P.src + lane * P.src_lane_stride + uint64_t(slot) * a.src_page_stride + uint64_t(r0) * P.src_row
-            : P.src + lane * P.src_lane_stride + (first + r0) * P.src_row;
+        // Staged sources (src_page_stride != 0) hold slot s's page at s*stride;
+        // record sources (P.page_stride != 0) page p at p*stride.
+        const uint64_t at = a.src_page_stride ? uint64_t(slot) * a.src_page_stride + uint64_t(r0) * P.src_row
+                            : P.page_stride   ? uint64_t(page) * P.page_stride + uint64_t(r0) * P.src_row
+                                              : (first + r0) * P.src_row;
+        const uint8_t *src = P.src + lane * P.src_lane_stride + at;
         uint8_t *dst = P.dst + lane * P.dst_lane_stride + (uint64_t(slot) * a.page_tokens + r0) * P.dst_row;
         const uint32_t sbytes = nr * P.src_row;
         if (P.mode == kModeCopy || P.format == kFmtF16) {

@@ -13,6 +13,8 @@
 #include <cstdio>
 #include <cstring>
 #include <limits>
+#include <map>
+#include <set>
 #include <stdexcept>
 
 namespace kvmem_hip {
@@ -422,6 +424,101 @@ std::vector<uint32_t> PageSoftmaxHip::pick(const std::vector<double> &scores, ui
     if (st == KVR_ERR_SCORES) throw std::invalid_argument("scores must be finite and non-negative");
     ok(st, "pick scored blocks");
     out.resize(count);
+    return out;
+}
+
+// ---- native payload records -------------------------------------------------
+namespace {
+uint64_t checked_add(uint64_t a, uint64_t b) {
+    if (b > std::numeric_limits<uint64_t>::max() - a) throw std::invalid_argument("memory size/position overflow");
+    return a + b;
+}
+uint64_t checked_mul(uint64_t a, uint64_t b) {
+    if (a && b > std::numeric_limits<uint64_t>::max() / a) throw std::invalid_argument("memory size overflow");
+    return a * b;
+}
+bool pow2(uint64_t n) { return n && !(n & (n - 1)); }
+// bytes of one token row of a gather source format (0: not a source format)
+size_t source_row_bytes(kvr_format f, uint32_t width) {
+    if (f == KVR_FMT_F16) return size_t(width) * 2;
+    if (width % 32) return 0;
+    if (f == KVR_FMT_Q8_0) return size_t(width) / 32 * 34;
+    if (f == KVR_FMT_Q4_1) return size_t(width) / 32 * 20;
+    if (f == KVR_FMT_Q4_0) return size_t(width) / 32 * 18;
+    return 0;
+}
+}  // namespace
+
+void PayloadLayout::validate() const {
+    require(!format.empty() && version && block_tokens && record_bytes && !planes.empty() && pow2(alignment) &&
+                record_bytes % alignment == 0,
+            "invalid native payload layout");
+    uint64_t end = 0;
+    using Shard = std::pair<uint32_t, uint32_t>;  // model layer, rank
+    std::map<Shard, std::set<PayloadPlaneKind>> kinds;
+    std::map<Shard, std::pair<uint32_t, uint32_t>> heads;
+    for (const auto &p : planes) {
+        require(p.bytes && pow2(p.alignment) && p.alignment <= alignment && p.offset % p.alignment == 0 &&
+                    p.offset >= end && kinds[{p.layer, p.rank}].insert(p.kind).second,
+                "overlapping/duplicate/misaligned payload plane");
+        require((p.head_count || !p.head_begin) &&
+                    uint64_t(p.head_begin) + p.head_count <= std::numeric_limits<uint32_t>::max(),
+                "invalid payload head range");
+        const auto range = std::make_pair(p.head_begin, p.head_count);
+        const auto ins = heads.emplace(Shard{p.layer, p.rank}, range);
+        require(ins.second || ins.first->second == range, "a payload shard has inconsistent head ranges");
+        require(p.kind != PayloadPlaneKind::PackedKeyValue || !p.token_stride,
+                "packed KV pages require opaque token addressing");
+        end = checked_add(p.offset, p.bytes);
+        require(end <= record_bytes && (!p.token_stride || checked_mul(p.token_stride, block_tokens) <= p.bytes),
+                "payload plane exceeds its record");
+    }
+    for (const auto &layer : kinds) {
+        const bool packed = layer.second.count(PayloadPlaneKind::PackedKeyValue) != 0;
+        const bool key = layer.second.count(PayloadPlaneKind::Key) != 0;
+        const bool value = layer.second.count(PayloadPlaneKind::Value) != 0;
+        require(packed ? layer.second.size() == 1 : (key && value),
+                "every attention layer requires key and value planes");
+    }
+    bool have_layer = false, unsharded = false;
+    uint32_t previous = 0;
+    uint64_t next_head = 0;
+    for (const auto &item : heads) {
+        const uint32_t layer = item.first.first, begin = item.second.first, count = item.second.second;
+        if (!have_layer || previous != layer) {
+            have_layer = true;
+            previous = layer;
+            next_head = 0;
+            unsharded = false;
+        } else {
+            require(!unsharded && count, "multiple payload shards need explicit head ranges");
+        }
+        require(begin == next_head, "payload heads must cover a contiguous model-order range");
+        next_head += count;
+        unsharded = !count;
+    }
+}
+
+kvr_plane record_plane(const PayloadLayout &layout, uint32_t layer, PayloadPlaneKind kind, const void *archive,
+                       kvr_format format, uint32_t width, uint64_t tokens, kvr_gather_mode mode, void *slots,
+                       uint32_t rank) {
+    layout.validate();
+    require(kind == PayloadPlaneKind::Key || kind == PayloadPlaneKind::Value,
+            "only key and value planes are gathered as token rows");
+    const PayloadPlane *plane = nullptr;
+    for (const auto &p : layout.planes)
+        if (p.layer == layer && p.kind == kind && p.rank == rank) plane = &p;
+    require(plane != nullptr, "the payload layout has no such plane");
+    const size_t row = source_row_bytes(format, width);
+    require(row && plane->token_stride == row, "the payload plane's token rows are not contiguous rows of the format");
+    kvr_plane out{};
+    out.history = static_cast<const uint8_t *>(archive) + plane->offset;
+    out.format = format;
+    out.width = width;
+    out.tokens = tokens;
+    out.mode = mode;
+    out.slots = slots;
+    out.page_stride = layout.record_bytes;
     return out;
 }
 

@@ -662,6 +662,66 @@ void stageout() {
     kh::kvmem_stagein_gpu_free();
 }
 
+// PayloadLayout::validate (kvmem/src/host/memory_contract.cpp:51-106) and
+// record_plane on the layouts it accepts and each rule it enforces.
+void payload_layout() {
+    using K = kh::PayloadPlaneKind;
+    kh::PayloadLayout ok;
+    ok.format = "test-q8k-f16v";
+    ok.version = 1;
+    ok.block_tokens = 64;
+    ok.alignment = 256;
+    ok.planes = {{0, K::Key, 0, 64 * 272, 16, 272}, {0, K::Value, 17408, 64 * 512, 16, 512},
+                 {1, K::Key, 50176, 64 * 272, 16, 272}, {1, K::Value, 67584, 64 * 512, 16, 512}};
+    ok.record_bytes = 100352;
+    ok.validate();
+    uint8_t base[16];
+    const kvr_plane p = kh::record_plane(ok, 1, K::Value, base, KVR_FMT_F16, 256, 1000, KVR_GATHER_COPY, nullptr);
+    require(p.history == base + 67584 && p.page_stride == 100352 && p.width == 256, "record plane");
+    auto rejects = [](const kh::PayloadLayout &l) {
+        try {
+            l.validate();
+        } catch (const std::invalid_argument &) {
+            return true;
+        }
+        return false;
+    };
+    auto bad = ok;
+    bad.format.clear();
+    require(rejects(bad), "empty format accepted");
+    bad = ok;
+    bad.record_bytes = 100000;  // not a multiple of the alignment
+    require(rejects(bad), "unaligned record accepted");
+    bad = ok;
+    bad.planes[1].offset = 17000;  // overlaps the key plane
+    require(rejects(bad), "overlapping planes accepted");
+    bad = ok;
+    bad.planes[1].offset = 17416;  // not 16-aligned
+    require(rejects(bad), "misaligned plane accepted");
+    bad = ok;
+    bad.planes[3].kind = K::Key;  // layer 1 without a value plane, key twice
+    require(rejects(bad), "duplicate kind accepted");
+    bad = ok;
+    bad.planes[3].kind = K::ValueScale;  // layer 1 lacks its value plane
+    require(rejects(bad), "layer without value plane accepted");
+    bad = ok;
+    bad.planes[0].token_stride = 273;  // 64 rows of 273 B exceed the plane
+    require(rejects(bad), "token rows beyond the plane accepted");
+    bad = ok;
+    bad.planes[3].bytes = 40000;  // runs past the record
+    require(rejects(bad), "plane past its record accepted");
+    bad = ok;
+    bad.planes[0].head_count = 4;  // a head range on one plane of the shard only
+    require(rejects(bad), "inconsistent head ranges accepted");
+    bool threw = false;
+    try {
+        kh::record_plane(ok, 0, K::Key, base, KVR_FMT_F16, 256, 1000, KVR_GATHER_COPY, nullptr);  // 272 B rows
+    } catch (const std::invalid_argument &) {
+        threw = true;
+    }
+    require(threw, "record plane with a mismatched row size accepted");
+}
+
 // span_coefficients (sorted sweep) against the oracle's pair-by-pair
 // restatement of span_coefficient, on random spans (some open-ended).
 void graph_spans() {
@@ -762,7 +822,7 @@ int main(int argc, char **argv) {
     std::vector<std::pair<const char *, std::function<void()>>> tests = {
         {"frames", frames}, {"native_query_geometry", native_query_geometry},
         {"workspace_geometry", workspace_geometry}, {"stagein_without_state", stagein_without_state},
-        {"graph_spans", graph_spans}};
+        {"graph_spans", graph_spans}, {"payload_layout", payload_layout}};
     if (gpu)
         tests = {{"qualification", qualification}, {"current_layer", current_layer}, {"pick", pick},
                  {"stagein", stagein},           {"meank", meank},                 {"transfer", transfer},

@@ -19,7 +19,7 @@ def _run(mode, timeout):
 
 def test_host_layer_cpu():
     out = _run("--cpu", 60)
-    assert out.count("PASS") == 5
+    assert out.count("PASS") == 6
 
 
 @pytest.mark.gpu
