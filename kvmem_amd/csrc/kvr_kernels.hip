@@ -12,6 +12,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace kvr {
 namespace {
 
@@ -1672,36 +1674,68 @@ __global__ __launch_bounds__(256) void k_probs(SelectArgs a) {
 // layer's last ones are summed, so a layer boundary costs no load latency.
 // Sums restart at each layer's first row (binary32, token order, as in
 // summary_block).
-template <int SRC>
+// Raw buffer resource over `bytes` bytes from `p` (dword 3 selects the
+// 32-bit data format, which enables untyped loads).  Loads at offsets past
+// `bytes` return zeros instead of touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const uint8_t *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(p), short(0), int(bytes), 0x00020000);
+}
+constexpr int kBufferNontemporal = 2;  // cache-policy bits of a streaming load
+
+// PAGED: every wave's 64 channel groups lie in one page (width a multiple of
+// 512 channels) and a page spans less than 4 GiB.  Then the page and its
+// rows are wave-uniform: each layer's page is read through a buffer
+// resource that ends at the page's last row, a row's address is one add of
+// a scalar row offset to the lane's column (no 64-bit address or clamp per
+// lane), and the pad rows of a page's last chunk read zeros from the
+// hardware, which add nothing (acc is never -0), so no row is masked and
+// the chunk loop has no branch.
+// Otherwise each lane keeps its own row pointer, clamped to the page's last
+// row.
+template <int SRC, bool PAGED>
 __device__ __forceinline__ void stack_summaries(const StackGroupArgs &g, uint32_t block) {
     __builtin_amdgcn_s_setprio(2);
     const SummaryArgs &a = g.s[0];
     const uint32_t gpp = a.width >> 3;
-    const uint64_t gid = uint64_t(block) * 256 + threadIdx.x;
-    if (gid >= uint64_t(a.lanes) * a.pages * gpp) return;  // no barriers follow
-    const uint32_t cg = uint32_t(gid % gpp);
-    const uint64_t rest = gid / gpp;
-    const uint32_t page = uint32_t(rest % a.pages);
-    const uint32_t lane = uint32_t(rest / a.pages);
+    uint32_t cg, page, lane;
+    if constexpr (PAGED) {
+        const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x) >> 6;
+        const uint64_t gid0 = uint64_t(block) * 256 + wave * 64;  // the wave's first channel group
+        if (gid0 >= uint64_t(a.lanes) * a.pages * gpp) return;  // whole waves; no barriers follow
+        const uint64_t rest = gid0 / gpp;
+        cg = uint32_t(gid0 % gpp) + (threadIdx.x & 63u);
+        page = uint32_t(rest % a.pages);
+        lane = uint32_t(rest / a.pages);
+    } else {
+        const uint64_t gid = uint64_t(block) * 256 + threadIdx.x;
+        if (gid >= uint64_t(a.lanes) * a.pages * gpp) return;  // no barriers follow
+        const uint64_t rest = gid / gpp;
+        cg = uint32_t(gid % gpp);
+        page = uint32_t(rest % a.pages);
+        lane = uint32_t(rest / a.pages);
+    }
     const uint32_t c0 = cg * 8;
     const uint64_t t0 = uint64_t(page) * a.page_tokens;
     const uint64_t tail = a.tokens - t0;
     const uint32_t n = tail < a.page_tokens ? uint32_t(tail) : a.page_tokens;
     const uint32_t m = g.m;
-    // this thread's first row of each layer, and the row stride
+    // this thread's column in a row, and the row stride
     const uint32_t row_bytes = SRC == kSrcKeysF16 ? a.width * 2 : (a.width >> 5) * kQ8Bytes;
     const uint32_t b = cg >> 2, s = cg & 3;  // q8_0: block and quarter (see summary_block)
     const uint32_t col = SRC == kSrcKeysF16 ? c0 * 2 : ((b * kQ8Bytes) & ~3u) + 8 * s;
     const bool odd = (b & 1) != 0;
+    // q8_0: the 8 codes sit at byte 2 (even block) or 4 (odd block) of the
+    // lane's 12 bytes; one byte permutation per dword extracts them.
+    const uint32_t code_sel = odd ? 0x07060504u : 0x05040302u;
     // per-layer fields, read with constant indices (entries past m are
-    // never used)
+    // never used); `first` is the page's first row in the lane's history
     const uint8_t *first[kStackGroup];
     float *means[kStackGroup];
     uint16_t *sums[kStackGroup];
     uint32_t epoch[kStackGroup];
 #pragma unroll
     for (uint32_t i = 0; i < kStackGroup; ++i) {
-        first[i] = g.s[i].src + lane * g.s[i].src_lane_stride + t0 * row_bytes + col;
+        first[i] = g.s[i].src + lane * g.s[i].src_lane_stride + t0 * row_bytes + (PAGED ? 0 : col);
         means[i] = g.s[i].means;
         sums[i] = g.s[i].summaries;
         epoch[i] = g.s[i].epoch;
@@ -1739,9 +1773,8 @@ __device__ __forceinline__ void stack_summaries(const StackGroupArgs &g, uint32_
             *reinterpret_cast<u32x4 *>(so + out) = v;
         }
     };
-    // Row u of a chunk is summed only when it is a real row (pad rows re-read
-    // the layer's last row and add zeros: acc is never -0, so acc + (+-0) is
-    // acc bit for bit).
+    // Row u of a chunk is summed only when it is a real row (pad rows add
+    // zeros: acc is never -0, so acc + (+-0) is acc bit for bit).
     auto consume = [&](const auto v, bool real) {
         if constexpr (SRC == kSrcKeysF16) {
             u32x4 w;
@@ -1749,48 +1782,76 @@ __device__ __forceinline__ void stack_summaries(const StackGroupArgs &g, uint32_
             for (int k = 0; k < 4; ++k) w[k] = real ? v[k] : 0u;
             add_f16x8(acc, w);
         } else {
-            const uint32_t lo = odd ? v[1] : __builtin_amdgcn_alignbyte(v[1], v[0], 2);
-            const uint32_t hi = odd ? v[2] : __builtin_amdgcn_alignbyte(v[2], v[1], 2);
+            const uint32_t lo = __builtin_amdgcn_perm(v[1], v[0], code_sel);
+            const uint32_t hi = __builtin_amdgcn_perm(v[2], v[1], code_sel);
             const uint32_t dw = dpp::move<dpp::kQuadBcast0>(v[0]);
             const uint32_t d = odd ? dw >> 16 : dw & 0xffffu;
             add_q8x8(acc, real ? lo : 0u, real ? hi : 0u, h2f(uint16_t(real ? d : 0u)));
         }
-    };
-    auto load = [&](const uint8_t *p) {
-        if constexpr (SRC == kSrcKeysF16)
-            return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
-        else
-            return __builtin_nontemporal_load(reinterpret_cast<const u32x3a *>(p));
     };
     // Each layer is read in chunks of D rows, the last one padded: then a
     // layer ends on a chunk boundary, its epilogue runs once outside the
     // unrolled steps, and the next chunk's loads (the next layer's first
     // rows at a boundary) are already in flight when it runs.  A chunk is
     // (layer li, first row r0); `left` = n - 1 - r0 rows follow its first.
+    // PAGED: the page's n rows in the layer are one buffer resource, and
+    // row u of a chunk sits at col + coff + u*row_bytes with coff =
+    // r0*row_bytes; otherwise the chunk's first row is at cp.
     constexpr int D = SRC == kSrcKeysF16 ? kF16Rows : kQ8Rows;
     const uint32_t per_layer = (n + D - 1) / D;
     const uint32_t chunks = m * per_layer;
     const uint8_t *cp = first[0];
-    uint32_t left = n - 1;
-    auto row_ptr = [&](uint32_t u) { return cp + uint64_t(min(u, left)) * row_bytes; };
-    decltype(load(cp)) ring[D];
+    uint32_t left = n - 1, coff = 0;
+    auto page_rsrc = [&]() {
+        if constexpr (PAGED) return buffer_rsrc(cp, n * row_bytes); else return 0;
+    };
+    auto rs = page_rsrc();
+    auto load_row = [&](int u) {
+        if constexpr (PAGED) {
+            // the row offset is a scalar computed per row (no per-lane table)
+            const uint32_t off = col + __builtin_amdgcn_readfirstlane(coff + uint32_t(u) * row_bytes);
+            if constexpr (SRC == kSrcKeysF16)
+                return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kBufferNontemporal));
+            else
+                return __builtin_bit_cast(u32x3, __builtin_amdgcn_raw_buffer_load_b96(rs, off, 0, kBufferNontemporal));
+        } else {
+            const uint8_t *p = cp + uint64_t(min(uint32_t(u), left)) * row_bytes;
+            if constexpr (SRC == kSrcKeysF16)
+                return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+            else
+                return u32x3(__builtin_nontemporal_load(reinterpret_cast<const u32x3a *>(p)));
+        }
+    };
+    decltype(load_row(0)) ring[D];
 #pragma unroll
     for (int u = 0; u < D; ++u) {
-        ring[u] = load(row_ptr(u));
+        ring[u] = load_row(u);
         __builtin_amdgcn_sched_barrier(0);
     }
+    // one chunk's rows consumed while the next chunk's rows are loaded
+    auto step = [&](auto masked, uint32_t real_left) {
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+            consume(ring[u], decltype(masked)::value ? uint32_t(u) <= real_left : true);
+            ring[u] = load_row(u);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
     uint32_t li = 0, lc = 0;  // layer and chunk within it of the ring's rows
     for (uint32_t c = 0; c + 1 < chunks; ++c) {
         const uint32_t real_left = left;
         const bool wrap = lc + 1 == per_layer;
-        cp = wrap ? layer_first(li + 1) : cp + uint64_t(D) * row_bytes;
-        left = wrap ? n - 1 : left - D;
-#pragma unroll
-        for (int u = 0; u < D; ++u) {
-            consume(ring[u], uint32_t(u) <= real_left);
-            ring[u] = load(row_ptr(u));
-            __builtin_amdgcn_sched_barrier(0);
+        if constexpr (PAGED) {
+            if (wrap) {
+                cp = layer_first(li + 1);
+                rs = page_rsrc();
+            }
+            coff = wrap ? 0u : coff + D * row_bytes;
+        } else {
+            cp = wrap ? layer_first(li + 1) : cp + uint64_t(D) * row_bytes;
         }
+        left = wrap ? n - 1 : left - D;
+        step(std::integral_constant<bool, !PAGED>{}, real_left);
         if (wrap) {
             finish(li);
             ++li;
@@ -1800,7 +1861,7 @@ __device__ __forceinline__ void stack_summaries(const StackGroupArgs &g, uint32_
         }
     }
 #pragma unroll
-    for (int u = 0; u < D; ++u) consume(ring[u], uint32_t(u) <= left);
+    for (int u = 0; u < D; ++u) consume(ring[u], PAGED || uint32_t(u) <= left);
     finish(li);
 }
 
@@ -1829,7 +1890,12 @@ __global__ __launch_bounds__(256) void k_stack_group(StackGroupArgs g) {
     if constexpr (SRC == kSrcSummary) {
         for (uint32_t i = 0; i < g.m; ++i) summary_block<SRC, true>(g.s[i], blockIdx.x, q_lds_buf + (i & 1) * g.q_slot);
     } else {
-        stack_summaries<SRC>(g, blockIdx.x);
+        const SummaryArgs &a = g.s[0];
+        const uint64_t row_bytes = SRC == kSrcKeysF16 ? a.width * 2 : (a.width >> 5) * kQ8Bytes;
+        if ((a.width & 511) == 0 && (uint64_t(a.page_tokens) + 64) * row_bytes < (uint64_t(1) << 32))
+            stack_summaries<SRC, true>(g, blockIdx.x);
+        else
+            stack_summaries<SRC, false>(g, blockIdx.x);
     }
 }
 

@@ -115,6 +115,61 @@ def test_stack_equals_layers(ctx, agg):
         st.free()
 
 
+@pytest.mark.parametrize("fmt,hkv,d", [(K.FMT_Q8_0, 8, 128), (K.FMT_Q8_0, 2, 256), (K.FMT_Q8_0, 2, 128),
+                                        (K.FMT_F16, 8, 128), (K.FMT_F16, 2, 64)])
+def test_stack_keys_partial_last_page(ctx, fmt, hkv, d):
+    """Stacks of q8_0 and fp16 key histories whose last page is partial
+    (156 of 256 rows), with widths whose waves cover exactly one page (1024
+    and 512 channels: rows read through a buffer resource, pad rows past the
+    layer's end read as zeros) and narrower ones (256 and 128 channels:
+    per-lane clamped rows): five layers (a group of four, then one), equal to
+    one kvr_recall_layer per layer and to the oracle's summaries and
+    selections."""
+    n, T, PT, KSEL = 5, 8192 - 100, 256, 8
+    HQ, W = 4 * hkv, hkv * d
+    P = -(-T // PT)
+    layers = []
+    for l in range(n):
+        if fmt == K.FMT_Q8_0:
+            keys = O.synth_normal_q8_0(SEED, 700 + 2 * l, T * W // 32)
+        else:
+            keys = O.synth_normal_f16(SEED, 700 + 2 * l, T * W)
+        q = O.synth_normal_f16(SEED, 701 + 2 * l, HQ * d)
+        layers.append(dict(keys=keys, q=q, kd=dev(keys), qd=dev(q), s16=zeros(P * W, np.uint16),
+                           scores=zeros(P, np.float64), sel=zeros(KSEL, np.uint32), cnt=zeros(1, np.uint32)))
+    names = ("s16", "scores", "sel", "cnt")
+
+    def descs():
+        return [K.Context.layer_recall(
+            keys=K.make_keys(b["kd"], fmt, T, hkv, d, PT), summaries=b["s16"],
+            query=K.make_query(b["qd"], K.FMT_F16, 1, HQ, hkv, d), scores=b["scores"], selected=b["sel"],
+            count=b["cnt"], k=KSEL, aggregation=K.AGG_MEAN) for b in layers]
+
+    def outputs():
+        return [{x: host(b[x], np.uint8).copy() for x in names} for b in layers]
+
+    for desc in descs():
+        ctx.recall(desc)
+    ctx.check()
+    eager = outputs()
+    for b in layers:
+        for x in names:
+            b[x].zero_()
+    torch.cuda.synchronize()
+    keep = ctx.recall_stack(descs())
+    ctx.check()
+    del keep
+    stacked = outputs()
+    for l, (b, e, st) in enumerate(zip(layers, eager, stacked)):
+        for x in names:
+            assert np.array_equal(e[x], st[x]), (l, x)
+        _, m = O.page_summaries(b["keys"], fmt, T, W, PT)
+        assert np.array_equal(st["s16"].view(np.float16), m.ravel().astype(np.float16)), l
+        qf = b["q"].view(np.float16).astype(np.float32).reshape(1, 1, HQ, d)
+        s = O.page_softmax_scores(m[None], qf, [1], HQ, hkv, d, K.AGG_MEAN)
+        assert np.array_equal(st["sel"].view(np.uint32), O.pick_scored_blocks(s, KSEL)), l
+
+
 def test_stack_long_rows_and_single_layer(ctx):
     """4096 resident pages per layer (the tail's keys in LDS, rows in memory
     passes), and a one-layer stack."""
