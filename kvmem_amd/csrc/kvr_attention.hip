@@ -161,6 +161,7 @@ __device__ __forceinline__ void decode_block(const RawBlock<KF> &r, float *out) 
 }
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 constexpr uint32_t kPairTile = 16;   // (row, query head) pairs per workgroup: the MFMA's M
 constexpr uint32_t kTokenTile = 16;  // tokens per MFMA: its N
 constexpr float kLog2e = 1.44269504088896340736f, kLn2 = 0.693147180559945309417f;
@@ -175,6 +176,16 @@ constexpr float kLog2e = 1.44269504088896340736f, kLn2 = 0.693147180559945309417
 // 4*(l/16)+i][token l%16], i = 0..3.  Pair p0+m is sampled row (p0+m)/group
 // and query head kv*group + (p0+m)%group.
 //
+// fp16 keys take v_mfma_f32_16x16x32_f16 instead: one MFMA per 32-dim key
+// block, lane l supplying 8 dims of block b (its k slots; A and B use the
+// same slots, so the dot product is the same) straight from its 16-byte key
+// load, with no decode.  The binary32 query is split into fp16 high and low
+// parts (q = hi + lo to about 2^-22 relative) after scaling each pair by a
+// power of two that keeps its largest element below 2^15; the products of
+// fp16 parts are exact, accumulation is binary32 in the matrix core, and
+// the power of two comes back with the logit scale.  Two MFMAs (hi, lo) per
+// block: 8 per 16-token tile at head dim 128, against 32 of the f32 form.
+//
 // The workgroup's 16-token tiles, page after page, are dealt to its waves
 // in turn (flat tile f goes to wave f%4), and each wave streams its tiles
 // through one ring of loads across the pages.  Lanes keep a running max
@@ -185,6 +196,7 @@ constexpr float kLog2e = 1.44269504088896340736f, kLn2 = 0.693147180559945309417
 constexpr uint32_t kMaxPageGroup = 16;
 template <int KF, int R>
 __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
+    constexpr bool kHalf = KF == kKeyF16;  // fp16 matrix-core form
     __shared__ float part[2][kMaxPageGroup][kAttnWaves][kPairTile];  // max, sum
     const uint32_t groups = (a.pages + a.page_group - 1) / a.page_group;
     const uint32_t kv = blockIdx.x / groups, pg0 = (blockIdx.x % groups) * a.page_group;
@@ -231,7 +243,18 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
         const uint32_t t = tile_token(k, live);
         const uint8_t *row = a.k + uint64_t(t) * a.k_row_stride + uint64_t(kv) * a.k_head_stride;
 #pragma unroll
-        for (int r = 0; r < R; ++r) ring[slot][r] = load_block<KF>(row, block_of(r));
+        for (int r = 0; r < R; ++r) {
+            if constexpr (kHalf) {
+                // 16 bytes (8 dims) of each of blocks 4r..4r+3 (clamped to
+                // the head's last block; blocks past it meet zero queries)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    ring[slot][r].v[i] = *reinterpret_cast<const u32x4 *>(
+                        row + min(4u * r + i, nb - 1) * KeyBlock<KF>::kBytes + 16 * kg);
+            } else {
+                ring[slot][r] = load_block<KF>(row, block_of(r));
+            }
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) bw[slot][i] = *scalar_word(mrow[i], a.mask_scalar, t, bsh[slot][i]);
     };
@@ -239,7 +262,15 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
     // head dim or the pairs).  Its loads go first, then the ring's first
     // two tiles, then the conversion: the loop is entered with exactly the
     // two slots' loads outstanding, in slot order, as at its back edge.
+    // f32 form: element s of round r is dim 32*(4r+kg) + s.  fp16 form:
+    // dim 32*(4r + s/8) + 8*kg + s%8, kept as hi/lo fp16 parts (qh, ql).
+    auto q_dim = [&](int r, int s) {
+        return kHalf ? 32 * min(4u * r + s / 8, nb - 1) + 8 * kg + s % 8 : 32 * block_of(r) + s;
+    };
+    auto q_on = [&](int r, int s) { return 4 * r + (kHalf ? uint32_t(s) / 8 : kg) < nb; };
     float qa[R][32];
+    f16x8 qh[R][4], ql[R][4];
+    float lscale[4];  // logit scale of the lane's output pairs 4*kg + i
     {
         const uint32_t p = p0 + col;
         const uint32_t pc = min(p, npairs - 1);
@@ -249,16 +280,46 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
-            for (int s = 0; s < 32; ++s) qw[r][s] = *scalar_word(qrow, a.q_scalar, 32 * block_of(r) + s, qs[r][s]);
+            for (int s = 0; s < 32; ++s) qw[r][s] = *scalar_word(qrow, a.q_scalar, q_dim(r, s), qs[r][s]);
         __builtin_amdgcn_sched_barrier(0);
         issue(0, 0);
         issue(1, 1);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const bool on = p < npairs && 4 * r + kg < nb;
 #pragma unroll
-            for (int s = 0; s < 32; ++s) qa[r][s] = on ? scalar_value(qw[r][s], qs[r][s], a.q_scalar) : 0.0f;
+            for (int s = 0; s < 32; ++s)
+                qa[r][s] = p < npairs && q_on(r, s) ? scalar_value(qw[r][s], qs[r][s], a.q_scalar) : 0.0f;
+        }
+        if constexpr (kHalf) {
+            // the pair's largest |q| over its four lanes (col, col+16, ...)
+            float mx = 0.0f;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int s = 0; s < 32; ++s) mx = fmaxf(mx, fabsf(qa[r][s]));
+            mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+            // 2^-e brings it below 2^15 (exact; e = 0 for |q| < 2^14)
+            // (binary exponent from the bits; subnormal maxima keep e = 0)
+            const int e = min(max(int((__float_as_uint(mx) >> 23) & 0xffu) - 127 - 13, 0), 100);
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const float x = __builtin_ldexpf(qa[r][8 * i + j], -e);
+                        const _Float16 hi = _Float16(x);
+                        qh[r][i][j] = hi;
+                        ql[r][i][j] = _Float16(x - float(hi));
+                    }
+            const float own = __builtin_ldexpf(a.scale, e);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) lscale[i] = __shfl(own, 4 * kg + i, kWave);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) lscale[i] = a.scale;
         }
     }
     lds_barrier();  // partials initialized
@@ -273,7 +334,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
     auto process = [&](int slot, uint32_t k) {
         float kv32[R][32];
 #pragma unroll
-        for (int r = 0; r < R; ++r) decode_block<KF>(ring[slot][r], kv32[r]);
+        for (int r = 0; r < R; ++r)
+            if constexpr (!kHalf) decode_block<KF>(ring[slot][r], kv32[r]);
         float bias[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -284,19 +346,34 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
             // back edge copies, waiting for the loads)
             asm volatile("" : "+v"(bias[i]));
         }
+        // two accumulation chains keep two MFMAs of the wave in flight
+        f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
+        if constexpr (kHalf) {
+            // (hi chain, lo chain) on the slot's raw key words, issued
+            // before the slot's refill overwrites them
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const f16x8 kb = __builtin_bit_cast(f16x8, ring[slot][r].v[i]);
+                    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[r][i], kb, acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[r][i], kb, acc1, 0, 0, 0);
+                }
+        }
         __builtin_amdgcn_sched_barrier(0);
         issue(slot, k + 2);
         __builtin_amdgcn_sched_barrier(0);
-        // two accumulation chains (even and odd k-steps) keep two MFMAs of
-        // the wave in flight; k-steps past the head dim have zero queries
-        f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
+        if constexpr (!kHalf) {
+            // even and odd k-steps; k-steps past the head dim have zero
+            // queries
 #pragma unroll
-        for (int r = 0; r < R; ++r)
+            for (int r = 0; r < R; ++r)
 #pragma unroll
-            for (int s = 0; s < 32; s += 2) {
-                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[r][s], kv32[r][s], acc0, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[r][s + 1], kv32[r][s + 1], acc1, 0, 0, 0);
-            }
+                for (int s = 0; s < 32; s += 2) {
+                    acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[r][s], kv32[r][s], acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[r][s + 1], kv32[r][s + 1], acc1, 0, 0, 0);
+                }
+        }
         bool live;
         (void)tile_token(k, live);
         // running max and sum in base 2: logits times log2(e), v_exp_f32
@@ -305,7 +382,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const bool use = live && __builtin_isfinite(bias[i]);
-            float l = (acc0[i] + acc1[i]) * a.scale;
+            float l = (acc0[i] + acc1[i]) * lscale[i];
             if (a.softcap > 0.0f) l = a.softcap * tanhf(l / a.softcap);
             l = use ? (l + bias[i]) * kLog2e : -__builtin_inff();
             const float nm = fmaxf(m[i], l);
