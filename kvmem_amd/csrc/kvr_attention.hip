@@ -194,7 +194,10 @@ constexpr float kLog2e = 1.44269504088896340736f, kLn2 = 0.693147180559945309417
 // in LDS.  One barrier at the end, then the four waves' partials of each
 // (page, pair) give its log-sum-exp.
 constexpr uint32_t kMaxPageGroup = 16;
-template <int KF, int R>
+// G4: the query-head group is a multiple of 4, so a lane's four output
+// pairs 4*kg+i (i = 0..3, from a multiple of 16) are heads of one sampled
+// row and share its mask word: one load and one decode per tile, not four.
+template <int KF, int R, bool G4>
 __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
     constexpr bool kHalf = KF == kKeyF16;  // fp16 matrix-core form
     __shared__ float part[2][kMaxPageGroup][kAttnWaves][kPairTile];  // max, sum
@@ -256,7 +259,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
             }
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) bw[slot][i] = *scalar_word(mrow[i], a.mask_scalar, t, bsh[slot][i]);
+        for (int i = 0; i < (G4 ? 1 : 4); ++i) bw[slot][i] = *scalar_word(mrow[i], a.mask_scalar, t, bsh[slot][i]);
     };
     // A operand: pair p0+col, the 32 dims of block 4r+kg (zero past the
     // head dim or the pairs).  Its loads go first, then the ring's first
@@ -339,7 +342,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
         float bias[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            bias[i] = scalar_value(bw[slot][i], bsh[slot][i], a.mask_scalar);
+            bias[i] = G4 && i > 0 ? bias[0] : scalar_value(bw[slot][i], bsh[slot][i], a.mask_scalar);
             // pinned here: the slot's old words are consumed before its
             // refill is issued (a conversion sunk past it would keep both
             // live, and the refill would land in registers that the loop's
@@ -512,8 +515,11 @@ template <int KF>
 hipError_t launch_lse(const AttnArgs &a, hipStream_t s) {
     const uint32_t npairs = a.n_rows * a.group;
     const dim3 grid(a.kvheads * ((a.pages + a.page_group - 1) / a.page_group), (npairs + kPairTile - 1) / kPairTile);
-    if (a.dim <= 128) hipLaunchKernelGGL((k_attn_lse<KF, 1>), grid, dim3(kAttnThreads), 0, s, a);
-    else hipLaunchKernelGGL((k_attn_lse<KF, 2>), grid, dim3(kAttnThreads), 0, s, a);
+    const bool g4 = a.group % 4 == 0;
+    if (a.dim <= 128 && g4) hipLaunchKernelGGL((k_attn_lse<KF, 1, true>), grid, dim3(kAttnThreads), 0, s, a);
+    else if (a.dim <= 128) hipLaunchKernelGGL((k_attn_lse<KF, 1, false>), grid, dim3(kAttnThreads), 0, s, a);
+    else if (g4) hipLaunchKernelGGL((k_attn_lse<KF, 2, true>), grid, dim3(kAttnThreads), 0, s, a);
+    else hipLaunchKernelGGL((k_attn_lse<KF, 2, false>), grid, dim3(kAttnThreads), 0, s, a);
     return hipGetLastError();
 }
 
