@@ -334,6 +334,25 @@ kvr_status kvr_stage_in(kvr_context *ctx, const kvr_plane *planes, uint32_t n_pl
 kvr_status kvr_recall_layer(kvr_context *ctx, const kvr_layer_recall *desc,
                             void *select_stream, void *copy_stream);
 
+/* kvr_recall_layer that allocates nothing, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No reference counterpart.  The
+ * scoring logits, packed queries and per-lane counters live in a static
+ * device array of KVR_NOALLOC_SCRATCH_BYTES per GPU (held until the process
+ * ends; its first KVR_NOALLOC_MAX_LANES * 4 bytes are the counters) instead
+ * of the context's workspace; a call whose lanes*rows*query_heads*pages*8
+ * bytes of logits (+ lanes*rows*query_heads*head_dim*2 of packed queries
+ * on the matrix-core path, each rounded up to 256) do not fit fails with
+ * KVR_ERR_WORKSPACE before any launch.  The gather uses the kernel engine
+ * (KVR_ENGINE_SDMA with planes: KVR_ERR_UNSUPPORTED).  The context must have
+ * been created beforehand (kvr_create allocates; this call does not).  Every
+ * call on one GPU shares its array: calls that overlap in time on one GPU,
+ * from any context or stream, race and give undefined results. */
+#define KVR_NOALLOC_SCRATCH_BYTES (16u << 20)
+#define KVR_NOALLOC_MAX_LANES 1024
+kvr_status kvr_recall_layer_noalloc(kvr_context *ctx, const kvr_layer_recall *desc, void *select_stream,
+                                    void *copy_stream);
+
 /* n layers of recall in order, with results identical to n kvr_recall_layer
  * calls.  When every layer takes the fused vector scoring path with one
  * geometry, the layers go in groups of up to KVR_STACK_GROUP consecutive

@@ -282,6 +282,11 @@ class Context:
         """kvr_recall_layer on a prebuilt descriptor."""
         check(lib().kvr_recall_layer(self.handle, C.byref(desc), select_stream, copy_stream))
 
+    def recall_noalloc(self, desc, select_stream=None, copy_stream=None) -> None:
+        """kvr_recall_layer_noalloc on a prebuilt descriptor: the same layer
+        with its logits and counters in the library's static device scratch."""
+        check(lib().kvr_recall_layer_noalloc(self.handle, C.byref(desc), select_stream, copy_stream))
+
     def recall_layer(self, *, select_stream=None, copy_stream=None, **kw) -> None:
         self.recall(self.layer_recall(**kw), select_stream, copy_stream)
 

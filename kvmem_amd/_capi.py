@@ -28,6 +28,8 @@ MAX_INLINE_MANDATORY = 64
 MAX_PLANES = 8
 STACK_GROUP = 4
 ATTENTION_ROWS = 64
+NOALLOC_SCRATCH_BYTES = 16 << 20
+NOALLOC_MAX_LANES = 1024
 
 _P = C.c_void_p
 _u32, _u64, _sz, _i = C.c_uint32, C.c_uint64, C.c_size_t, C.c_int
@@ -98,6 +100,7 @@ _SIGNATURES = {
     "kvr_stage_in": (_i, [_P, C.POINTER(Plane), _u32, _u32, _u32, _P, _P, _u32, _i, _P]),
     "kvr_recall_layer": (_i, [_P, C.POINTER(LayerRecall), _P, _P]),
     "kvr_recall_stack": (_i, [_P, C.POINTER(LayerRecall), _u32, _P, _P]),
+    "kvr_recall_layer_noalloc": (_i, [_P, C.POINTER(LayerRecall), _P, _P]),
     "kvr_attention_workspace_bytes": (_sz, [_u32, _u32, _u32]),
     "kvr_attention_page_mass": (_i, [_P, C.POINTER(AttentionSample), _P, _P]),
     "kvr_propagate_scores": (_i, [_P, _P, _u32, _u32, _P, C.POINTER(PageGraph), C.c_double, _P]),

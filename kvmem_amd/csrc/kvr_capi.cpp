@@ -221,6 +221,8 @@ size_t qpack_bytes(uint32_t lanes, uint32_t rows, uint32_t qheads, uint32_t dim)
 
 static_assert(kvr::kMaxMandatory == KVR_MAX_INLINE_MANDATORY, "inline mandatory capacity");
 static_assert(kvr::kStackGroup == KVR_STACK_GROUP, "layers per stack launch");
+static_assert(kvr::kScratchBytes == KVR_NOALLOC_SCRATCH_BYTES, "static scratch size");
+static_assert(kvr::kScratchCounters == KVR_NOALLOC_MAX_LANES, "static scratch counters");
 
 struct Mandatory {
     uint32_t n = 0;
@@ -249,10 +251,18 @@ struct ScorePlan {
     bool mfma;
     double *logits;
     uint16_t *qpack;
+    uint32_t *counters;  // per-lane completion counters of the softmax launch
+};
+
+// Where a call's logits, packed queries and counters live: the context's
+// workspace (grown on demand) unless `fixed` names the static scratch.
+struct FixedScratch {
+    uint8_t *base;      // device address of the scratch array
+    size_t bytes;       // its size
 };
 
 kvr_status plan_score(kvr_context *ctx, const kvr_query *q, uint32_t lanes, uint32_t pages,
-                      int force_mfma, hipStream_t stream, ScorePlan &p) {
+                      int force_mfma, hipStream_t stream, ScorePlan &p, const FixedScratch *fixed = nullptr) {
     if (kvr_status s = check_query(q, lanes)) return s;
     if (!pages) return fail(KVR_ERR_INVALID, "no pages to score");
     p.q = query_args(q);
@@ -270,9 +280,21 @@ kvr_status plan_score(kvr_context *ctx, const kvr_query *q, uint32_t lanes, uint
         return fail(KVR_ERR_INVALID, "head_dim %u: vector scoring needs 8*2^i <= 512", q->head_dim);
     const size_t lb = logits_bytes(lanes, pages, q->rows, q->query_heads);
     const size_t qb = p.mfma ? qpack_bytes(lanes, q->rows, q->query_heads, q->head_dim) : 0;
+    if (fixed) {
+        // counters first, then logits and packed queries; nothing grows
+        if (lanes > kvr::kScratchCounters || kvr::kScratchCounterBytes + lb + qb > fixed->bytes)
+            return fail(KVR_ERR_WORKSPACE, "call needs %u counters and %zu bytes of logits and queries; the static "
+                                           "scratch holds %u counters and %zu bytes", lanes, lb + qb,
+                        kvr::kScratchCounters, fixed->bytes - kvr::kScratchCounterBytes);
+        p.counters = reinterpret_cast<uint32_t *>(fixed->base);
+        p.logits = reinterpret_cast<double *>(fixed->base + kvr::kScratchCounterBytes);
+        p.qpack = reinterpret_cast<uint16_t *>(fixed->base + kvr::kScratchCounterBytes + lb);
+        return KVR_OK;
+    }
     if (kvr_status s = ensure_workspace(ctx, lb + qb, stream)) return s;
     p.logits = reinterpret_cast<double *>(ctx->ws);
     p.qpack = reinterpret_cast<uint16_t *>(ctx->ws + lb);
+    p.counters = nullptr;  // the context's, sized at launch
     return KVR_OK;
 }
 
@@ -284,7 +306,7 @@ kvr::SelectArgs make_select_args(kvr_context *ctx, const ScorePlan &p, const uin
     sa.logits = p.logits;
     sa.mask = mask;
     sa.units = p.rows * (agg == KVR_AGG_MEAN ? p.qheads : p.kvheads);
-    sa.counters = ctx->counters;
+    sa.counters = p.counters ? p.counters : ctx->counters;
     sa.rows = p.rows;
     sa.qheads = p.qheads;
     sa.kvheads = p.kvheads;
@@ -314,7 +336,8 @@ kvr_status enqueue_probs_and_select(kvr_context *ctx, const ScorePlan &p, const 
                                     const Mandatory &mand, uint32_t *selected, uint32_t *count,
                                     hipStream_t s) {
     if (p.lanes > 65535) return fail(KVR_ERR_INVALID, "at most 65535 lanes per call");
-    if (kvr_status st = ensure_counters(ctx, p.lanes, s)) return st;
+    if (!p.counters)
+        if (kvr_status st = ensure_counters(ctx, p.lanes, s)) return st;
     const kvr::SelectArgs sa = make_select_args(ctx, p, mask, agg, active_layers, accumulate, scores, do_select, k,
                                                 tie, mand, selected, count);
     KVR_HIP(kvr::launch_probs(sa, s));
@@ -714,6 +737,8 @@ kvr_status kvr_create(int device, kvr_context **out) {
     if (e == hipSuccess) e = hipMalloc(&ctx->counters, kInitialCounters * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMemset(ctx->counters, 0, kInitialCounters * sizeof(uint32_t));
     if (e == hipSuccess) ctx->counters_cap = kInitialCounters;
+    // this device's address of the no-allocation entry's static scratch
+    if (e == hipSuccess) e = kvr::scratch_init(device);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         kvr_destroy(ctx);
@@ -1083,7 +1108,8 @@ struct LayerPlan {
     int src = kvr::kSrcSummary;
 };
 
-kvr_status plan_layer(kvr_context *ctx, const kvr_layer_recall *d, hipStream_t ss, hipStream_t cs, LayerPlan &L) {
+kvr_status plan_layer(kvr_context *ctx, const kvr_layer_recall *d, hipStream_t ss, hipStream_t cs, LayerPlan &L,
+                      const FixedScratch *fixed = nullptr) {
     if (!d || !d->query || !d->summaries || !d->scores || !d->selected || !d->count)
         return fail(KVR_ERR_INVALID, "recall descriptor lacks query, summaries, scores or selection outputs");
     if (d->aggregation > KVR_AGG_MAX_LOGIT) return fail(KVR_ERR_INVALID, "unknown aggregation");
@@ -1113,7 +1139,7 @@ kvr_status plan_layer(kvr_context *ctx, const kvr_layer_recall *d, hipStream_t s
     if (d->n_planes && d->engine == KVR_ENGINE_SDMA && (capturing(ss) || capturing(cs)))
         return fail(KVR_ERR_INVALID, "the DMA stage-in engine reads the selection on the host and cannot be "
                                      "captured; use the kernel engine inside graphs");
-    if (kvr_status s = plan_score(ctx, d->query, L.lanes, L.pages, d->force_mfma, ss, L.p)) return s;
+    if (kvr_status s = plan_score(ctx, d->query, L.lanes, L.pages, d->force_mfma, ss, L.p, fixed)) return s;
     if (d->keys && !L.p.mfma && !valu_dim_ok(d->keys->head_dim))
         return fail(KVR_ERR_INVALID, "head_dim %u unsupported by fused scoring", d->keys->head_dim);
     return KVR_OK;
@@ -1172,6 +1198,25 @@ kvr_status kvr_recall_layer(kvr_context *ctx, const kvr_layer_recall *d, void *s
     const hipStream_t cs = stream_or(copy_stream, ctx->copy);
     LayerPlan L;
     if (kvr_status s = plan_layer(ctx, d, ss, cs, L)) return s;
+    return enqueue_layer(ctx, L, ss, cs);
+}
+
+kvr_status kvr_recall_layer_noalloc(kvr_context *ctx, const kvr_layer_recall *d, void *select_stream,
+                                    void *copy_stream) {
+    if (kvr_status s = check_ctx(ctx)) return s;
+    if (d && d->engine == KVR_ENGINE_SDMA && d->n_planes)
+        return fail(KVR_ERR_UNSUPPORTED, "the DMA stage-in engine allocates its staging; the no-allocation entry "
+                                         "gathers with the kernel engine");
+    DeviceGuard guard(ctx->device);
+    const FixedScratch fixed{kvr::scratch_address(ctx->device), kvr::kScratchBytes};
+    if (!fixed.base) return fail(KVR_ERR_HIP, "static scratch of device %d was not set up", ctx->device);
+    const hipStream_t ss = stream_or(select_stream, ctx->sel);
+    const hipStream_t cs = stream_or(copy_stream, ctx->copy);
+    LayerPlan L;
+    if (kvr_status s = plan_layer(ctx, d, ss, cs, L, &fixed)) return s;
+    // the counters must start at zero; a previous call on this GPU leaves them
+    // so, but a clear by a kernel keeps the call safe after any abort
+    KVR_HIP(kvr::launch_fill_u32(L.p.counters, L.lanes, 0u, ss));
     return enqueue_layer(ctx, L, ss, cs);
 }
 

@@ -182,6 +182,20 @@ hipError_t launch_accumulate(const AccumulateArgs &a, hipStream_t s);
 hipError_t launch_finalize(const FinalizeArgs &a, hipStream_t s);
 hipError_t launch_copy_ops(const CopyOp *ops, uint32_t n, hipStream_t s);
 
+// ---- static scratch of the no-allocation entry (kvr_scratch.hip) ----------
+// Layout: kScratchCounters per-lane completion counters, then the logits
+// (binary64) and the packed fp16 queries of one layer.
+constexpr size_t kScratchBytes = size_t(16) << 20;
+constexpr uint32_t kScratchCounters = 1024;
+constexpr size_t kScratchCounterBytes = size_t(kScratchCounters) * sizeof(uint32_t);
+// Looks up this device's copy of the array (the device must be current);
+// once per device, later calls return at once.
+hipError_t scratch_init(int device);
+// The device address found by scratch_init, or null before it.
+uint8_t *scratch_address(int device);
+// n words at p set to v (a kernel, so the clear can sit inside a graph).
+hipError_t launch_fill_u32(uint32_t *p, uint32_t n, uint32_t v, hipStream_t s);
+
 enum SynthKind : int {
     kSynthNormalF16 = 0, kSynthScaledNormalF16 = 1, kSynthNormalF32 = 2,
     kSynthQ8 = 3, kSynthQ41 = 4, kSynthNormalQ8 = 5
