@@ -20,6 +20,7 @@
 #include <cstdint>
 #include <memory>
 #include <string>
+#include <utility>
 #include <vector>
 
 namespace kvmem_hip {
@@ -77,6 +78,20 @@ struct PageSummaries {
     uint32_t pages = 0, page_tokens = 0, kv_heads = 0, head_dim = 0;
 };
 
+// Media (image) token ranges [first, end) in recording order
+// (KvMemStore::set_media_ranges, kvmem/include/kvmem/kvmem_store.hpp:504).
+using MediaRanges = std::vector<std::pair<uint32_t, uint32_t>>;
+
+// KvMemStore::query_fixed_blocks (kvmem/src/host/kvmem_store.cpp:381-408)
+// for a store of `pages` pages of page_tokens tokens holding total_tokens
+// tokens: every page when the budget is 0 or covers them all; else sink,
+// last media range and mandatory pages with their whole media groups
+// (std::runtime_error when they do not fit, std::invalid_argument for a
+// page outside the store), then recent pages while they fit.
+std::vector<uint32_t> query_fixed_blocks(uint32_t pages, uint32_t budget, uint32_t sink, uint32_t recent,
+                                         const MediaRanges &media, uint32_t page_tokens, uint64_t total_tokens,
+                                         const std::vector<uint32_t> &mandatory);
+
 // The page-softmax scorer (page_softmax_cuda.hpp:10-32): synchronous on
 // return, owned by one adapter, one device.
 class PageSoftmaxHip {
@@ -101,13 +116,30 @@ public:
                                             const QueryScoreFrame &, void *producer_stream);
     // pick_scored_blocks (kvmem_store.cpp:418-451) on the device: mandatory
     // pages first, then by score with the tie rule; ascending ids.
+    // Mandatory pages beyond the budget: std::runtime_error, as there.
     std::vector<uint32_t> pick(const std::vector<double> &scores, uint32_t budget,
                                const std::vector<uint32_t> &mandatory = {},
                                TieRule tie = TieRule::LowerFirst, bool signed_scores = false);
+    // The same with the store's media ranges (pages of page_tokens tokens):
+    // a page in a media range is kept only with its whole group.
+    std::vector<uint32_t> pick(const std::vector<double> &scores, uint32_t budget,
+                               const std::vector<uint32_t> &mandatory, TieRule tie, bool signed_scores,
+                               const MediaRanges &media, uint32_t page_tokens);
+    // KvMemStore::pick_topk_blocks (kvmem_store.cpp:377-379): the ungrouped
+    // pick (sink, mandatory newest first and recent pages while they fit,
+    // then the best scores, higher id first on ties; :578-723), then with
+    // media ranges constrain_media (:453-502).  scores are the selection
+    // scores, one per page.
+    std::vector<uint32_t> pick_topk(const std::vector<double> &scores, uint32_t budget, uint32_t sink,
+                                    uint32_t recent, const std::vector<uint32_t> &mandatory = {},
+                                    const MediaRanges &media = {}, uint32_t page_tokens = 1,
+                                    uint64_t total_tokens = 0);
     size_t device_bytes() const;
     kvr_context *context() const;
 
 private:
+    std::vector<uint32_t> fetch_pick(const uint32_t *sel, const uint32_t *cnt, uint32_t k, void *stream,
+                                     const char *what);
     struct Impl;
     std::unique_ptr<Impl> impl_;
 };

@@ -28,7 +28,11 @@
  *    each shape once before capture, or bind a workspace: growth during
  *    capture fails with KVR_ERR_WORKSPACE.  The DMA stage-in engine reads
  *    the selection on the host and refuses capture.
- *  - A context is used by one host thread at a time.
+ *  - A context is used by one host thread at a time.  Its calls may use
+ *    different streams: a call that uses the context's workspace or
+ *    counters on another stream than the previous such call waits on the
+ *    device for what that stream has queued.  Calls on captured streams are
+ *    not ordered that way: the caller orders them.
  *
  * Reference citations are relative to the KVMem 0.19.0 source tree.
  */
@@ -44,6 +48,8 @@ extern "C" {
 
 #define KVR_VERSION_MAJOR 0
 #define KVR_VERSION_MINOR 1
+/* Host mandatory lists up to this length travel inside the launch (and may
+ * be graph-captured); longer ones are uploaded by the call. */
 #define KVR_MAX_INLINE_MANDATORY 64
 #define KVR_MAX_PLANES 8
 /* Layers whose summaries share one launch in kvr_recall_stack. */
@@ -56,7 +62,8 @@ typedef enum kvr_status {
     KVR_ERR_INVALID = 1,     /* invalid argument or geometry                    */
     KVR_ERR_NONFINITE = 2,   /* recall operand NaN/inf (recall_fp16 rejects)    */
     KVR_ERR_RANGE = 3,       /* recall operand rounds to fp16 infinity          */
-    KVR_ERR_BUDGET = 4,      /* mandatory pages exceed the selection budget     */
+    KVR_ERR_BUDGET = 4,      /* mandatory pages (with their media groups) exceed
+                              * the selection budget                           */
     KVR_ERR_WORKSPACE = 5,   /* borrowed workspace too small for the call       */
     KVR_ERR_HIP = 6,         /* HIP runtime error                               */
     KVR_ERR_SCORES = 7,      /* negative or non-finite score without signed mode*/
@@ -171,6 +178,33 @@ typedef struct kvr_plane {
     size_t page_stride;
 } kvr_plane;
 
+/* Pages a device selection keeps besides its best-scored ones, all in
+ * device memory so that the call can be graph-captured (the lists are read
+ * when the selection runs).  Replaces the `mandatory` and media-range
+ * arguments of KvMemStore::pick_scored_blocks
+ * (kvmem/src/host/kvmem_store.cpp:418-451). */
+typedef struct kvr_page_policy {
+    const uint32_t *fixed;           /* dev: pages kept first in every lane, any
+                                        order, repeats allowed, ids >= pages
+                                        ignored; each brings its whole group and
+                                        together they must fit k (else the lane's
+                                        selection is empty and kvr_check reports
+                                        KVR_ERR_BUDGET)                         */
+    uint32_t n_fixed;
+    const uint32_t *groups;          /* dev [n_groups][2]: disjoint ascending page
+                                        ranges [begin, end) kept whole or not at
+                                        all (kvr_media_page_groups); the pages
+                                        are then visited in rank order and a
+                                        group that no longer fits is skipped.
+                                        NULL: every page alone                 */
+    uint32_t n_groups;
+    const uint32_t *preferred;       /* dev [lanes][preferred_stride]: pages ranked
+                                        before every other page (the second pass
+                                        of KvMemStore::pick_topk_blocks), or NULL */
+    const uint32_t *preferred_count; /* dev [lanes]                              */
+    uint32_t preferred_stride;
+} kvr_page_policy;
+
 /* One layer of recall for `lanes` sequences (kvr_recall_layer). */
 typedef struct kvr_layer_recall {
     const kvr_key_history *keys;   /* resident keys to summarize, or NULL to
@@ -185,7 +219,10 @@ typedef struct kvr_layer_recall {
     kvr_aggregation aggregation;
     uint32_t k;                    /* selection budget per lane */
     kvr_tie_rule tie_rule;
-    const uint32_t *mandatory;     /* host, <= KVR_MAX_INLINE_MANDATORY ids */
+    const uint32_t *mandatory;     /* host, any number of ids (up to
+                                      KVR_MAX_INLINE_MANDATORY distinct ones
+                                      inside the launch; more are uploaded
+                                      and then refuse graph capture)        */
     uint32_t n_mandatory;
     double *scores;                /* dev [lanes][pages] */
     uint32_t *selected;            /* dev [lanes][k], ascending ids */
@@ -204,6 +241,11 @@ typedef struct kvr_layer_recall {
                                       stream once the selection is written,
                                       before any stage-in is enqueued (same
                                       rules as the summary events)           */
+    const kvr_page_policy *policy; /* optional device-side fixed pages, media
+                                      groups and preferred pages (besides
+                                      `mandatory`); with groups or preferred
+                                      pages the selection is its own launch
+                                      (pages <= KVR_GROUP_SELECT_PAGES)      */
 } kvr_layer_recall;
 
 /* ---- context ------------------------------------------------------------ */
@@ -300,8 +342,8 @@ kvr_status kvr_score(kvr_context *ctx, const kvr_query *q, const uint16_t *summa
 
 /* ---- selection ------------------------------------------------------------- */
 
-/* Per lane: mandatory pages first, then the top of (score desc, id by tie
- * rule) up to k pages; ids ascending.  Rejects (device side, empty result,
+/* Per lane: mandatory pages first (host list, any length), then the top of
+ * (score desc, id by tie rule) up to k pages; ids ascending.  Rejects (device side, empty result,
  * KVR_ERR_SCORES at kvr_check) a negative or non-finite score unless
  * signed_scores.  Replaces KvMemStore::pick_scored_blocks
  * (kvmem/src/host/kvmem_store.cpp:418-451) with every page a candidate.
@@ -310,6 +352,81 @@ kvr_status kvr_select_topk(kvr_context *ctx, const double *scores, uint32_t lane
                            uint32_t pages, uint32_t k, const uint32_t *mandatory,
                            uint32_t n_mandatory, kvr_tie_rule tie_rule, int signed_scores,
                            uint32_t *selected, uint32_t *count, void *stream);
+
+/* Rows of at most this many pages per lane take media groups or preferred
+ * pages; rows of at most KVR_FIXED_BITMAP_PAGES take fixed pages. */
+#define KVR_GROUP_SELECT_PAGES 4096
+#define KVR_FIXED_BITMAP_PAGES 524288
+
+/* kvr_select_topk with a device-side page policy (NULL: none).  Without
+ * groups or preferred pages it is the same one-wave/one-workgroup top-k;
+ * with them each lane's pages are put in rank order (preferred first,
+ * score desc, id by tie rule) and walked, keeping each group or lone page
+ * that still fits: KvMemStore::pick_scored_blocks with media ranges
+ * (kvmem/src/host/kvmem_store.cpp:418-451) and the fill of constrain_media
+ * (:453-502). */
+kvr_status kvr_select_pages(kvr_context *ctx, const double *scores, uint32_t lanes, uint32_t pages, uint32_t k,
+                            const kvr_page_policy *policy, kvr_tie_rule tie_rule, int signed_scores,
+                            uint32_t *selected, uint32_t *count, void *stream);
+
+/* ---- page policies on the host (no device work) ----------------------- */
+
+/* Media (image) token ranges of a history, in the order the engine recorded
+ * them: ranges[2i] is the first token of range i, ranges[2i+1] one past its
+ * last.  A range covers pages [first / page_tokens, ceil(end / page_tokens)). */
+typedef struct kvr_media {
+    const uint32_t *ranges;
+    uint32_t n_ranges;
+    uint32_t page_tokens;
+    uint64_t total_tokens;   /* tokens in the history */
+} kvr_media;
+
+typedef enum kvr_media_merge {
+    KVR_MEDIA_OVERLAP = 0,   /* ranges that share a page join, transitively
+                                (scored_media_group, kvmem_store.cpp:18-32)  */
+    KVR_MEDIA_IN_ORDER = 1   /* ranges starting at or past total_tokens or
+                                empty are dropped; a range starting before
+                                the previous group's end extends it, in list
+                                order (constrain_media, kvmem_store.cpp:453-468) */
+} kvr_media_merge;
+
+/* The page groups of `media` over `pages` pages: disjoint ascending
+ * [begin, end) pairs written to groups (room for n_ranges pairs).  The
+ * device list of kvr_page_policy.groups. */
+kvr_status kvr_media_page_groups(const kvr_media *media, uint32_t pages, kvr_media_merge merge, uint32_t *groups,
+                                 uint32_t *n_groups);
+
+/* The fixed pages of a Query pick, ascending: every page when budget is 0
+ * or at least pages; else the sink pages, the page where the last media
+ * range starts (when it starts before total_tokens) and the mandatory pages,
+ * each with its whole OVERLAP group and required to fit (KVR_ERR_BUDGET; a
+ * mandatory id >= pages: KVR_ERR_INVALID), then the newest `recent` pages
+ * newest first while their groups fit.  media may be NULL.  out: room for
+ * `pages` ids.  Replaces KvMemStore::query_fixed_blocks
+ * (kvmem/src/host/kvmem_store.cpp:381-408); the result is the fixed list of
+ * the device pick with the OVERLAP groups, tie rule higher-first. */
+kvr_status kvr_query_fixed_pages(uint32_t pages, uint32_t budget, uint32_t sink, uint32_t recent,
+                                 const kvr_media *media, const uint32_t *mandatory, uint32_t n_mandatory,
+                                 uint32_t *out, uint32_t *n_out);
+
+/* The kept part of the ungrouped top-k pick, ascending: every page when
+ * budget is 0 or at least pages; else, while the budget has room, the sink
+ * pages, the mandatory pages from the last listed to the first (ids >= pages
+ * ignored) and the newest `recent` pages newest first.  The device pick then
+ * fills the budget by score, higher id first on ties.  Replaces the fixed
+ * part of KvMemStore::pick_topk_ungrouped (kvmem_store.cpp:578-644). */
+kvr_status kvr_topk_fixed_pages(uint32_t pages, uint32_t budget, uint32_t sink, uint32_t recent,
+                                const uint32_t *mandatory, uint32_t n_mandatory, uint32_t *out, uint32_t *n_out);
+
+/* The kept part of constrain_media's pass (kvmem_store.cpp:453-490), for
+ * histories with media ranges, pages > budget and budget > 0 (else the
+ * ungrouped pick stands): the sink pages and the last IN_ORDER group are
+ * required (KVR_ERR_BUDGET), then the mandatory pages newest first, each
+ * with its group when it fits.  The device pick then takes the ungrouped
+ * pick's pages as preferred pages and the IN_ORDER groups, tie rule
+ * higher-first: KvMemStore::pick_topk_blocks (kvmem_store.cpp:377-379). */
+kvr_status kvr_media_fixed_pages(uint32_t pages, uint32_t budget, uint32_t sink, const kvr_media *media,
+                                 const uint32_t *mandatory, uint32_t n_mandatory, uint32_t *out, uint32_t *n_out);
 
 /* ---- stage-in ------------------------------------------------------------ */
 
@@ -491,7 +608,9 @@ kvr_status kvr_propagate_lrfu(kvr_context *ctx, double *scores, uint32_t lanes, 
 
 /* One launch of n byte copies (16-byte path when aligned).  Replaces
  * kvmem_d2d_batched (llama-kvmem-stagein.h:56, stagein.cu:236-261, 1006-1039).
- * src/dst/nbytes are host arrays of n entries. */
+ * src/dst/nbytes are host arrays of n entries, uploaded by the call through
+ * one of four pinned tables (so a call refuses graph capture; a table is
+ * reused once the copy launch that read it has run, on any stream). */
 kvr_status kvr_d2d_batched(kvr_context *ctx, const void *const *src, void *const *dst,
                            const size_t *nbytes, uint32_t n, void *stream);
 

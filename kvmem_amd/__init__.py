@@ -143,6 +143,69 @@ def make_plane(history, fmt: int, width: int, tokens: int, mode: int, slots,
     return p
 
 
+# ---- page policies (host helpers of include/kvrecall.h, no device work) ----
+
+def _media(ranges, page_tokens: int, total_tokens: int):
+    arr = np.ascontiguousarray(np.asarray(list(ranges) or [(0, 0)], np.uint32).reshape(-1, 2))
+    m = _capi.Media(arr.ctypes.data, len(ranges), page_tokens, total_tokens)
+    m._keep = arr
+    return m
+
+
+def _u32_arr(values):
+    return (C.c_uint32 * max(1, len(values)))(*values)
+
+
+def media_page_groups(ranges, page_tokens: int, total_tokens: int, pages: int, merge: int = 0) -> np.ndarray:
+    """kvr_media_page_groups: disjoint ascending [begin, end) page ranges,
+    shape [n][2] (merge 0: ranges sharing a page join; 1: in list order)."""
+    m = _media(ranges, page_tokens, total_tokens)
+    out = (C.c_uint32 * max(2, 2 * len(ranges)))()
+    n = C.c_uint32()
+    check(lib().kvr_media_page_groups(C.byref(m), pages, merge, out, C.byref(n)))
+    return np.frombuffer(out, np.uint32)[: 2 * n.value].reshape(-1, 2).copy()
+
+
+def query_fixed_pages(pages: int, budget: int, sink: int, recent: int, ranges=(), page_tokens: int = 256,
+                      total_tokens: int = 0, mandatory: Sequence[int] = ()) -> np.ndarray:
+    """kvr_query_fixed_pages (KvMemStore::query_fixed_blocks)."""
+    m = _media(ranges, page_tokens, total_tokens)
+    out = (C.c_uint32 * max(1, pages))()
+    n = C.c_uint32()
+    check(lib().kvr_query_fixed_pages(pages, budget, sink, recent, C.byref(m), _u32_arr(mandatory), len(mandatory),
+                                      out, C.byref(n)))
+    return np.frombuffer(out, np.uint32)[: n.value].copy()
+
+
+def topk_fixed_pages(pages: int, budget: int, sink: int, recent: int, mandatory: Sequence[int] = ()) -> np.ndarray:
+    """kvr_topk_fixed_pages (the kept part of pick_topk_ungrouped)."""
+    out = (C.c_uint32 * max(1, pages))()
+    n = C.c_uint32()
+    check(lib().kvr_topk_fixed_pages(pages, budget, sink, recent, _u32_arr(mandatory), len(mandatory), out,
+                                     C.byref(n)))
+    return np.frombuffer(out, np.uint32)[: n.value].copy()
+
+
+def media_fixed_pages(pages: int, budget: int, sink: int, ranges, page_tokens: int, total_tokens: int,
+                      mandatory: Sequence[int] = ()) -> np.ndarray:
+    """kvr_media_fixed_pages (the kept part of constrain_media)."""
+    m = _media(ranges, page_tokens, total_tokens)
+    out = (C.c_uint32 * max(1, pages))()
+    n = C.c_uint32()
+    check(lib().kvr_media_fixed_pages(pages, budget, sink, C.byref(m), _u32_arr(mandatory), len(mandatory), out,
+                                      C.byref(n)))
+    return np.frombuffer(out, np.uint32)[: n.value].copy()
+
+
+def make_policy(fixed=None, n_fixed: int = 0, groups=None, n_groups: int = 0, preferred=None,
+                preferred_count=None, preferred_stride: int = 0) -> "_capi.PagePolicy":
+    """A kvr_page_policy over device arrays (the descriptor keeps them alive)."""
+    p = _capi.PagePolicy(_ptr(fixed), n_fixed, _ptr(groups), n_groups, _ptr(preferred), _ptr(preferred_count),
+                         preferred_stride)
+    p._keep = (fixed, groups, preferred, preferred_count)
+    return p
+
+
 class Context:
     """One kvr_context: a GPU, two streams, a workspace."""
 
@@ -225,6 +288,13 @@ class Context:
         check(lib().kvr_select_topk(self.handle, _ptr(scores), lanes, pages, k, arr, len(mandatory), tie_rule,
                                     int(signed_scores), _ptr(selected), _ptr(count), stream))
 
+    def select_pages(self, scores, pages, k, selected, count, policy=None, lanes=1, tie_rule=TIE_LOWER_FIRST,
+                     signed_scores=False, stream=None) -> None:
+        """kvr_select_pages with a make_policy() descriptor (or None)."""
+        check(lib().kvr_select_pages(self.handle, _ptr(scores), lanes, pages, k,
+                                     None if policy is None else C.byref(policy), tie_rule, int(signed_scores),
+                                     _ptr(selected), _ptr(count), stream))
+
     # -- graph propagation and LRFU -------------------------------------------
     def propagate_scores(self, scores, pages, graphs: Sequence = (), alpha=0.2, transport_mask=None, lanes=1,
                          stream=None) -> None:
@@ -256,7 +326,7 @@ class Context:
                      pages=0, page_tokens=0, lanes=0, score_mask=None, aggregation=AGG_MEAN,
                      tie_rule=TIE_LOWER_FIRST, mandatory: Sequence[int] = (), planes: Sequence = (),
                      engine=ENGINE_AUTO, force_mfma=0, summary_events=(None, None),
-                     select_end=None) -> "_capi.LayerRecall":
+                     select_end=None, policy=None) -> "_capi.LayerRecall":
         """A kvr_layer_recall descriptor (holding what it points to), for
         callers that issue the same layer many times."""
         d = _capi.LayerRecall()
@@ -275,7 +345,10 @@ class Context:
         d.engine, d.force_mfma = engine, force_mfma
         d.summary_begin, d.summary_end = summary_events
         d.select_end = select_end
-        d._keep = (keys, query, summaries, means, score_mask, scores, selected, count, mand, parr, list(planes))
+        if policy is not None:
+            d.policy = C.pointer(policy)
+        d._keep = (keys, query, summaries, means, score_mask, scores, selected, count, mand, parr, list(planes),
+                   policy)
         return d
 
     def recall(self, desc, select_stream=None, copy_stream=None) -> None:

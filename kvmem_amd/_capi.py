@@ -17,6 +17,9 @@ HEADER = os.path.join(ROOT, "include", "kvrecall.h")
 # enums
 (OK, ERR_INVALID, ERR_NONFINITE, ERR_RANGE, ERR_BUDGET, ERR_WORKSPACE, ERR_HIP, ERR_SCORES, ERR_UNSUPPORTED,
  ERR_GRAPH) = range(10)
+MEDIA_OVERLAP, MEDIA_IN_ORDER = 0, 1
+GROUP_SELECT_PAGES = 4096
+FIXED_BITMAP_PAGES = 524288
 GRAPH_MAX_PAGES = 8192
 FMT_F16, FMT_Q8_0, FMT_Q4_1, FMT_F32, FMT_BF16, FMT_Q4_0, FMT_Q5_0 = range(7)
 AGG_MEAN, AGG_MAX, AGG_MAX_LOGIT = range(3)
@@ -56,6 +59,15 @@ class Plane(C.Structure):
                 ("rope", C.POINTER(Rope)), ("page_stride", _sz)]
 
 
+class PagePolicy(C.Structure):
+    _fields_ = [("fixed", _P), ("n_fixed", _u32), ("groups", _P), ("n_groups", _u32), ("preferred", _P),
+                ("preferred_count", _P), ("preferred_stride", _u32)]
+
+
+class Media(C.Structure):
+    _fields_ = [("ranges", _P), ("n_ranges", _u32), ("page_tokens", _u32), ("total_tokens", _u64)]
+
+
 class LayerRecall(C.Structure):
     _fields_ = [("keys", C.POINTER(KeyHistory)), ("summaries", _P), ("means", _P), ("pages", _u32),
                 ("page_tokens", _u32), ("lanes", _u32), ("query", C.POINTER(Query)),
@@ -63,7 +75,7 @@ class LayerRecall(C.Structure):
                 ("mandatory", C.POINTER(_u32)), ("n_mandatory", _u32), ("scores", _P),
                 ("selected", _P), ("count", _P), ("planes", C.POINTER(Plane)), ("n_planes", _u32),
                 ("engine", _i), ("force_mfma", _i), ("summary_begin", _P), ("summary_end", _P),
-                ("select_end", _P)]
+                ("select_end", _P), ("policy", C.POINTER(PagePolicy))]
 
 
 class AttentionSample(C.Structure):
@@ -97,6 +109,13 @@ _SIGNATURES = {
     "kvr_summary_finalize": (_i, [_P, _P, _P, _u32, _u32, _P, _P, _P]),
     "kvr_score": (_i, [_P, C.POINTER(Query), _P, _u32, _u32, _P, _i, _u32, _i, _P, _i, _P]),
     "kvr_select_topk": (_i, [_P, _P, _u32, _u32, _u32, C.POINTER(_u32), _u32, _i, _i, _P, _P, _P]),
+    "kvr_select_pages": (_i, [_P, _P, _u32, _u32, _u32, C.POINTER(PagePolicy), _i, _i, _P, _P, _P]),
+    "kvr_media_page_groups": (_i, [C.POINTER(Media), _u32, _i, C.POINTER(_u32), C.POINTER(_u32)]),
+    "kvr_query_fixed_pages": (_i, [_u32, _u32, _u32, _u32, C.POINTER(Media), C.POINTER(_u32), _u32,
+                                   C.POINTER(_u32), C.POINTER(_u32)]),
+    "kvr_topk_fixed_pages": (_i, [_u32, _u32, _u32, _u32, C.POINTER(_u32), _u32, C.POINTER(_u32), C.POINTER(_u32)]),
+    "kvr_media_fixed_pages": (_i, [_u32, _u32, _u32, C.POINTER(Media), C.POINTER(_u32), _u32, C.POINTER(_u32),
+                                   C.POINTER(_u32)]),
     "kvr_stage_in": (_i, [_P, C.POINTER(Plane), _u32, _u32, _u32, _P, _P, _u32, _i, _P]),
     "kvr_recall_layer": (_i, [_P, C.POINTER(LayerRecall), _P, _P]),
     "kvr_recall_stack": (_i, [_P, C.POINTER(LayerRecall), _u32, _P, _P]),

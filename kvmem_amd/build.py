@@ -28,7 +28,7 @@ HOST_TEST = os.path.join(ROOT, "tests", "cpp", "build", "test_host")
 ORACLE = os.path.join(ROOT, "oracle")
 ARCH = os.environ.get("KVR_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["kvr_kernels.hip", "kvr_attention.hip", "kvr_scratch.hip", "kvr_capi.cpp"]
+SOURCES = ["kvr_kernels.hip", "kvr_attention.hip", "kvr_scratch.hip", "kvr_capi.cpp", "kvr_policy.cpp"]
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",
     # Packed FP32 VALU ops stay disabled: the compiler's own v_pk_* forms are

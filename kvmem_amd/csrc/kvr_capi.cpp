@@ -29,10 +29,23 @@ struct kvr_context {
     uint8_t *ws = nullptr;
     size_t ws_bytes = 0;
     bool ws_borrowed = false;
-    // batched device copies
-    kvr::CopyOp *ops_dev = nullptr, *ops_pin = nullptr;
-    uint32_t ops_cap = 0;
-    hipEvent_t ops_ev = nullptr;
+    // batched device copies: a ring of op tables, each reused only after the
+    // copy launch that read it has run (its event)
+    static constexpr int kOpSlots = 4;
+    struct OpSlot {
+        kvr::CopyOp *dev = nullptr, *pin = nullptr;
+        uint32_t cap = 0;
+        hipEvent_t done = nullptr;
+    } ops[kOpSlots];
+    uint32_t ops_next = 0;
+    // host fixed-page lists longer than the inline capacity: one upload per
+    // call, reused once the previous call's readers have run (fixed_ev)
+    uint32_t *fixed_dev = nullptr, *fixed_pin = nullptr;
+    size_t fixed_cap = 0;
+    hipEvent_t fixed_ev = nullptr;
+    // the stream of the last call that used the workspace or the counters
+    hipStream_t ws_stream = nullptr;
+    hipEvent_t ws_ev = nullptr;
     // SDMA stage-in: span copies fan out over kDmaStreams streams (each can
     // drive its own DMA engine) and join back into the copy stream.
     hipStream_t dma[4] = {};
@@ -62,6 +75,17 @@ kvr_status fail(kvr_status s, const char *fmt, ...) {
     g_error = buf;
     return s;
 }
+
+}  // namespace
+
+namespace kvr {
+kvr_status set_error(kvr_status s, const char *message) {
+    g_error = message;
+    return s;
+}
+}  // namespace kvr
+
+namespace {
 
 kvr_status hip_fail(hipError_t e, const char *what) {
     return fail(KVR_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
@@ -224,9 +248,14 @@ static_assert(kvr::kStackGroup == KVR_STACK_GROUP, "layers per stack launch");
 static_assert(kvr::kScratchBytes == KVR_NOALLOC_SCRATCH_BYTES, "static scratch size");
 static_assert(kvr::kScratchCounters == KVR_NOALLOC_MAX_LANES, "static scratch counters");
 
+// A call's host mandatory pages: distinct, ascending.  Up to
+// KVR_MAX_INLINE_MANDATORY travel in the launch's arguments; a longer list
+// is uploaded (stage_fixed) and the launch reads it from `dev`.
 struct Mandatory {
     uint32_t n = 0;
     uint32_t ids[KVR_MAX_INLINE_MANDATORY];
+    std::vector<uint32_t> more;
+    const uint32_t *dev = nullptr;
 };
 
 kvr_status check_mandatory(const uint32_t *ids, uint32_t n, uint32_t pages, uint32_t k, Mandatory &m) {
@@ -238,10 +267,133 @@ kvr_status check_mandatory(const uint32_t *ids, uint32_t n, uint32_t pages, uint
     v.erase(std::unique(v.begin(), v.end()), v.end());
     if (v.size() > k)
         return fail(KVR_ERR_BUDGET, "%zu mandatory pages exceed the selection budget %u", v.size(), k);
-    if (v.size() > KVR_MAX_INLINE_MANDATORY)
-        return fail(KVR_ERR_INVALID, "at most %d mandatory pages per call", KVR_MAX_INLINE_MANDATORY);
+    if (v.size() > KVR_MAX_INLINE_MANDATORY && pages > kvr::kFixedBitmapPages)
+        return fail(KVR_ERR_UNSUPPORTED, "more than %d mandatory pages need at most %u pages per lane",
+                    KVR_MAX_INLINE_MANDATORY, kvr::kFixedBitmapPages);
     m.n = uint32_t(v.size());
-    std::copy(v.begin(), v.end(), m.ids);
+    m.more.clear();
+    m.dev = nullptr;
+    if (v.size() <= KVR_MAX_INLINE_MANDATORY) std::copy(v.begin(), v.end(), m.ids);
+    else m.more = std::move(v);
+    return KVR_OK;
+}
+
+// Uploads the long mandatory lists of one call in one copy on `s`.  The
+// pinned and device buffers are reused only after the previous call that
+// uploaded has run its readers (fixed_ev, recorded by fixed_done).  A
+// captured stream cannot take the upload: such callers pass a device list
+// (kvr_page_policy.fixed).
+kvr_status stage_fixed(kvr_context *ctx, Mandatory *const *lists, uint32_t n, hipStream_t s, bool &staged) {
+    staged = false;
+    size_t total = 0;
+    for (uint32_t i = 0; i < n; ++i) total += lists[i]->more.size();
+    if (!total) return KVR_OK;
+    if (capturing(s))
+        return fail(KVR_ERR_INVALID, "more than %d host mandatory pages are uploaded by the call and cannot be "
+                                     "captured; pass them as a device list (kvr_page_policy.fixed)",
+                    KVR_MAX_INLINE_MANDATORY);
+    KVR_HIP(hipEventSynchronize(ctx->fixed_ev));
+    if (total > ctx->fixed_cap) {
+        if (ctx->fixed_dev) KVR_HIP(hipFree(ctx->fixed_dev));
+        if (ctx->fixed_pin) KVR_HIP(hipHostFree(ctx->fixed_pin));
+        ctx->fixed_dev = ctx->fixed_pin = nullptr;
+        ctx->fixed_cap = 0;
+        KVR_HIP(hipMalloc(&ctx->fixed_dev, total * sizeof(uint32_t)));
+        KVR_HIP(hipHostMalloc(reinterpret_cast<void **>(&ctx->fixed_pin), total * sizeof(uint32_t),
+                              hipHostMallocDefault));
+        ctx->fixed_cap = total;
+    }
+    size_t at = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        Mandatory &m = *lists[i];
+        if (m.more.empty()) continue;
+        std::copy(m.more.begin(), m.more.end(), ctx->fixed_pin + at);
+        m.dev = ctx->fixed_dev + at;
+        at += m.more.size();
+    }
+    KVR_HIP(hipMemcpyAsync(ctx->fixed_dev, ctx->fixed_pin, total * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+    staged = true;
+    return KVR_OK;
+}
+
+// After the last launch that reads the uploaded lists.
+kvr_status fixed_done(kvr_context *ctx, bool staged, hipStream_t s) {
+    if (staged) KVR_HIP(hipEventRecord(ctx->fixed_ev, s));
+    return KVR_OK;
+}
+
+void put_mandatory(const Mandatory &m, kvr::SelectArgs &sa) {
+    sa.n_mandatory = 0;
+    sa.fixed = nullptr;
+    sa.n_fixed = 0;
+    if (m.more.empty()) {
+        sa.n_mandatory = m.n;
+        std::copy(m.ids, m.ids + m.n, sa.mandatory);
+    } else {
+        sa.fixed = m.dev;
+        sa.n_fixed = m.n;
+    }
+}
+
+// Calls that use the context's workspace or counters are ordered on the
+// device: a call on another stream than the previous such call first waits
+// for what that stream has queued (an event recorded now), so two streams
+// never share the buffers at once.  Captured streams are left to the
+// caller's own ordering.
+kvr_status ws_order(kvr_context *ctx, hipStream_t s) {
+    const hipStream_t prev = ctx->ws_stream;
+    ctx->ws_stream = s;
+    if (!prev || prev == s || capturing(s) || capturing(prev)) return KVR_OK;
+    KVR_HIP(hipEventRecord(ctx->ws_ev, prev));
+    KVR_HIP(hipStreamWaitEvent(s, ctx->ws_ev, 0));
+    return KVR_OK;
+}
+
+// A device-side page policy, checked on the host (its lists are read on the
+// device when the selection runs).
+struct Policy {
+    const kvr_page_policy *p = nullptr;
+    bool grouped = false;  // media groups or preferred pages: k_select_groups
+};
+
+kvr_status check_policy(const kvr_page_policy *p, uint32_t lanes, uint32_t pages, uint32_t k, Policy &out) {
+    out = Policy{};
+    if (!p) return KVR_OK;
+    if ((p->n_fixed && !p->fixed) || (p->n_groups && !p->groups))
+        return fail(KVR_ERR_INVALID, "page policy lists missing");
+    if (p->preferred && (!p->preferred_count || !p->preferred_stride))
+        return fail(KVR_ERR_INVALID, "preferred pages need their counts and a nonzero stride");
+    if (p->n_groups > pages) return fail(KVR_ERR_INVALID, "%u media groups for %u pages", p->n_groups, pages);
+    out.p = p;
+    out.grouped = p->n_groups || p->preferred;
+    if (out.grouped && pages > kvr::kGroupSelectPages)
+        return fail(KVR_ERR_UNSUPPORTED, "media groups and preferred pages need at most %u pages per lane (got %u)",
+                    kvr::kGroupSelectPages, pages);
+    if (p->n_fixed && pages > kvr::kFixedBitmapPages)
+        return fail(KVR_ERR_UNSUPPORTED, "fixed pages need at most %u pages per lane", kvr::kFixedBitmapPages);
+    (void)lanes;
+    (void)k;
+    return KVR_OK;
+}
+
+// A selection with the policy's lists.  The host mandatory pages (m) and the
+// policy's fixed list are both read (a device list replaces the inline
+// one only when the host list is empty).
+kvr_status put_policy(const Policy &pol, const Mandatory &m, kvr::SelectArgs &sa) {
+    put_mandatory(m, sa);
+    if (!pol.p) return KVR_OK;
+    const kvr_page_policy &p = *pol.p;
+    if (p.n_fixed) {
+        if (sa.fixed) return fail(KVR_ERR_INVALID, "a host mandatory list longer than %d and a device fixed list "
+                                                   "cannot be combined", KVR_MAX_INLINE_MANDATORY);
+        sa.fixed = p.fixed;
+        sa.n_fixed = p.n_fixed;
+    }
+    sa.groups = p.groups;
+    sa.n_groups = p.n_groups;
+    sa.preferred = p.preferred;
+    sa.preferred_count = p.preferred_count;
+    sa.preferred_stride = p.preferred_stride;
     return KVR_OK;
 }
 
@@ -321,8 +473,7 @@ kvr::SelectArgs make_select_args(kvr_context *ctx, const ScorePlan &p, const uin
     sa.tie_higher_first = tie == KVR_TIE_HIGHER_FIRST;
     sa.signed_scores = 0;
     sa.do_select = do_select;
-    sa.n_mandatory = mand.n;
-    std::copy(mand.ids, mand.ids + mand.n, sa.mandatory);
+    put_mandatory(mand, sa);
     sa.selected = selected;
     sa.count = count;
     sa.status = ctx->status;
@@ -334,12 +485,22 @@ kvr_status enqueue_probs_and_select(kvr_context *ctx, const ScorePlan &p, const 
                                     kvr_aggregation agg, uint32_t active_layers, int accumulate,
                                     double *scores, bool do_select, uint32_t k, kvr_tie_rule tie,
                                     const Mandatory &mand, uint32_t *selected, uint32_t *count,
-                                    hipStream_t s) {
+                                    hipStream_t s, const Policy *pol = nullptr) {
     if (p.lanes > 65535) return fail(KVR_ERR_INVALID, "at most 65535 lanes per call");
     if (!p.counters)
         if (kvr_status st = ensure_counters(ctx, p.lanes, s)) return st;
-    const kvr::SelectArgs sa = make_select_args(ctx, p, mask, agg, active_layers, accumulate, scores, do_select, k,
-                                                tie, mand, selected, count);
+    kvr::SelectArgs sa = make_select_args(ctx, p, mask, agg, active_layers, accumulate, scores, do_select, k, tie,
+                                          mand, selected, count);
+    if (pol)
+        if (kvr_status st = put_policy(*pol, mand, sa)) return st;
+    if (do_select && pol && pol->grouped) {
+        // media groups / preferred pages: the selection is its own launch
+        sa.do_select = 0;
+        KVR_HIP(kvr::launch_probs(sa, s));
+        sa.do_select = 1;
+        KVR_HIP(kvr::launch_select_groups(sa, s));
+        return KVR_OK;
+    }
     KVR_HIP(kvr::launch_probs(sa, s));
     return KVR_OK;
 }
@@ -723,7 +884,10 @@ kvr_status kvr_create(int device, kvr_context **out) {
     hipError_t e = hipStreamCreateWithFlags(&ctx->sel, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->copy, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->ev_sel, hipEventDisableTiming);
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->ops_ev, hipEventDisableTiming);
+    for (int i = 0; i < kvr_context::kOpSlots && e == hipSuccess; ++i)
+        e = hipEventCreateWithFlags(&ctx->ops[i].done, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->fixed_ev, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->ws_ev, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->dma_fork, hipEventDisableTiming);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->readback, hipStreamNonBlocking);
     for (int i = 0; i < kDmaStreams && e == hipSuccess; ++i) {
@@ -757,11 +921,19 @@ kvr_status kvr_destroy(kvr_context *ctx) {
     if (ctx->staging) (void)hipFree(ctx->staging);
     if (ctx->status) (void)hipFree(ctx->status);
     if (ctx->counters) (void)hipFree(ctx->counters);
-    if (ctx->ops_dev) (void)hipFree(ctx->ops_dev);
-    if (ctx->ops_pin) (void)hipHostFree(ctx->ops_pin);
+    for (kvr_context::OpSlot &o : ctx->ops) {
+        if (o.done) (void)hipEventSynchronize(o.done);
+        if (o.dev) (void)hipFree(o.dev);
+        if (o.pin) (void)hipHostFree(o.pin);
+        if (o.done) (void)hipEventDestroy(o.done);
+    }
+    if (ctx->fixed_ev) (void)hipEventSynchronize(ctx->fixed_ev);
+    if (ctx->fixed_dev) (void)hipFree(ctx->fixed_dev);
+    if (ctx->fixed_pin) (void)hipHostFree(ctx->fixed_pin);
+    if (ctx->fixed_ev) (void)hipEventDestroy(ctx->fixed_ev);
+    if (ctx->ws_ev) (void)hipEventDestroy(ctx->ws_ev);
     if (ctx->sel_pin) (void)hipHostFree(ctx->sel_pin);
     if (ctx->ev_sel) (void)hipEventDestroy(ctx->ev_sel);
-    if (ctx->ops_ev) (void)hipEventDestroy(ctx->ops_ev);
     for (int i = 0; i < kDmaStreams; ++i) {
         if (ctx->dma[i]) (void)hipStreamSynchronize(ctx->dma[i]);
         if (ctx->dma[i]) (void)hipStreamDestroy(ctx->dma[i]);
@@ -814,7 +986,7 @@ kvr_status kvr_check(kvr_context *ctx, void *stream) {
     // A raised word holds the number of the call that raised it (graph
     // replays repeat the number their capture gave them); reporting clears it.
     if (!st[kvr::kStatusNonfinite] && !st[kvr::kStatusRange] && !st[kvr::kStatusScores] &&
-        !st[kvr::kStatusGraph])
+        !st[kvr::kStatusGraph] && !st[kvr::kStatusBudget])
         return KVR_OK;
     KVR_HIP(hipMemset(ctx->status, 0, sizeof st));
     KVR_HIP(hipDeviceSynchronize());
@@ -824,6 +996,9 @@ kvr_status kvr_check(kvr_context *ctx, void *stream) {
         return fail(KVR_ERR_RANGE, "recall operand rounds to fp16 infinity (call %u)", st[kvr::kStatusRange]);
     if (st[kvr::kStatusScores])
         return fail(KVR_ERR_SCORES, "negative or nonfinite score (call %u)", st[kvr::kStatusScores]);
+    if (st[kvr::kStatusBudget])
+        return fail(KVR_ERR_BUDGET, "fixed pages (with their whole media groups) exceed the selection budget (call %u)",
+                    st[kvr::kStatusBudget]);
     return fail(KVR_ERR_GRAPH, "invalid graph mass, weight or row, or propagation result below its residual (call %u)",
                 st[kvr::kStatusGraph]);
 }
@@ -851,8 +1026,10 @@ kvr_status kvr_bind_workspace(kvr_context *ctx, void *workspace, size_t bytes) {
 }
 
 size_t kvr_device_bytes(kvr_context *ctx) {
-    return ctx ? ctx->ws_bytes + ctx->staging_bytes + kvr::kStatusWords * 4 + ctx->ops_cap * sizeof(kvr::CopyOp)
-               : 0;
+    if (!ctx) return 0;
+    size_t ops = 0;
+    for (const kvr_context::OpSlot &o : ctx->ops) ops += o.cap * sizeof(kvr::CopyOp);
+    return ctx->ws_bytes + ctx->staging_bytes + kvr::kStatusWords * 4 + ops + ctx->fixed_cap * sizeof(uint32_t);
 }
 
 kvr_status kvr_summary_build(kvr_context *ctx, const kvr_key_history *keys, float *means,
@@ -937,6 +1114,7 @@ kvr_status kvr_score(kvr_context *ctx, const kvr_query *q, const uint16_t *summa
     const hipStream_t s = stream_or(stream, ctx->sel);
     ScorePlan p;
     if (kvr_status st = plan_score(ctx, q, lanes, pages, force_mfma, s, p)) return st;
+    if (kvr_status st = ws_order(ctx, s)) return st;
     ++ctx->epoch;
     if (kvr_status st = enqueue_logits(ctx, p, summaries, s)) return st;
     Mandatory none;
@@ -944,18 +1122,27 @@ kvr_status kvr_score(kvr_context *ctx, const kvr_query *q, const uint16_t *summa
                                     KVR_TIE_LOWER_FIRST, none, nullptr, nullptr, s);
 }
 
-kvr_status kvr_select_topk(kvr_context *ctx, const double *scores, uint32_t lanes, uint32_t pages, uint32_t k,
-                           const uint32_t *mandatory, uint32_t n_mandatory, kvr_tie_rule tie_rule,
-                           int signed_scores, uint32_t *selected, uint32_t *count, void *stream) {
+namespace {
+kvr_status select_common(kvr_context *ctx, const double *scores, uint32_t lanes, uint32_t pages, uint32_t k,
+                         const uint32_t *mandatory, uint32_t n_mandatory, const kvr_page_policy *policy,
+                         kvr_tie_rule tie_rule, int signed_scores, uint32_t *selected, uint32_t *count,
+                         void *stream) {
     if (kvr_status s = check_ctx(ctx)) return s;
     lanes = lanes ? lanes : 1;
     if (!scores || !selected || !count || !pages)
         return fail(KVR_ERR_INVALID, "scores, selected, count and pages are required");
     if (!k) return fail(KVR_ERR_INVALID, "invalid scored selection frame (budget 0)");
     if (tie_rule > KVR_TIE_HIGHER_FIRST) return fail(KVR_ERR_INVALID, "unknown tie rule");
+    if (lanes > 65535) return fail(KVR_ERR_INVALID, "at most 65535 lanes per call");
     Mandatory m;
     if (kvr_status s = check_mandatory(mandatory, n_mandatory, pages, k, m)) return s;
+    Policy pol;
+    if (kvr_status s = check_policy(policy, lanes, pages, k, pol)) return s;
     DeviceGuard guard(ctx->device);
+    const hipStream_t st = stream_or(stream, ctx->sel);
+    Mandatory *lists[1] = {&m};
+    bool staged = false;
+    if (kvr_status s = stage_fixed(ctx, lists, 1, st, staged)) return s;
     ++ctx->epoch;
     kvr::SelectArgs sa{};
     sa.scores = const_cast<double *>(scores);
@@ -965,14 +1152,28 @@ kvr_status kvr_select_topk(kvr_context *ctx, const double *scores, uint32_t lane
     sa.tie_higher_first = tie_rule == KVR_TIE_HIGHER_FIRST;
     sa.signed_scores = signed_scores != 0;
     sa.do_select = 1;
-    sa.n_mandatory = m.n;
-    std::copy(m.ids, m.ids + m.n, sa.mandatory);
+    if (kvr_status s = put_policy(pol, m, sa)) return s;
     sa.selected = selected;
     sa.count = count;
     sa.status = ctx->status;
     sa.epoch = ctx->epoch;
-    KVR_HIP(kvr::launch_select(sa, stream_or(stream, ctx->sel)));
-    return KVR_OK;
+    KVR_HIP(pol.grouped ? kvr::launch_select_groups(sa, st) : kvr::launch_select(sa, st));
+    return fixed_done(ctx, staged, st);
+}
+}  // namespace
+
+kvr_status kvr_select_topk(kvr_context *ctx, const double *scores, uint32_t lanes, uint32_t pages, uint32_t k,
+                           const uint32_t *mandatory, uint32_t n_mandatory, kvr_tie_rule tie_rule,
+                           int signed_scores, uint32_t *selected, uint32_t *count, void *stream) {
+    return select_common(ctx, scores, lanes, pages, k, mandatory, n_mandatory, nullptr, tie_rule, signed_scores,
+                         selected, count, stream);
+}
+
+kvr_status kvr_select_pages(kvr_context *ctx, const double *scores, uint32_t lanes, uint32_t pages, uint32_t k,
+                            const kvr_page_policy *policy, kvr_tie_rule tie_rule, int signed_scores,
+                            uint32_t *selected, uint32_t *count, void *stream) {
+    return select_common(ctx, scores, lanes, pages, k, nullptr, 0, policy, tie_rule, signed_scores, selected, count,
+                         stream);
 }
 
 namespace {
@@ -1103,6 +1304,7 @@ struct LayerPlan {
     uint32_t pages = 0, page_tokens = 0, lanes = 1;
     size_t key_ls = 0;
     Mandatory m;
+    Policy pol;
     PlanePlan pp[KVR_MAX_PLANES];
     ScorePlan p;
     int src = kvr::kSrcSummary;
@@ -1132,6 +1334,10 @@ kvr_status plan_layer(kvr_context *ctx, const kvr_layer_recall *d, hipStream_t s
     }
     if (kvr_status s = check_summary_out(d->means, d->summaries)) return s;
     if (kvr_status s = check_mandatory(d->mandatory, d->n_mandatory, L.pages, d->k, L.m)) return s;
+    if (kvr_status s = check_policy(d->policy, L.lanes, L.pages, d->k, L.pol)) return s;
+    if (!L.m.more.empty() && L.pol.p && L.pol.p->n_fixed)
+        return fail(KVR_ERR_INVALID, "a host mandatory list longer than %d and a device fixed list cannot be combined",
+                    KVR_MAX_INLINE_MANDATORY);
     if (kvr_status s = check_planes(d->planes, d->n_planes, L.lanes, L.page_tokens, d->k, ctx->chunk_rows, L.pp))
         return s;
     if ((d->summary_begin || d->summary_end || d->select_end) && capturing(ss))
@@ -1184,7 +1390,7 @@ kvr_status enqueue_layer(kvr_context *ctx, LayerPlan &L, hipStream_t ss, hipStre
         if (d->summary_end) KVR_HIP(hipEventRecord(static_cast<hipEvent_t>(d->summary_end), ss));
     }
     if (kvr_status st = enqueue_probs_and_select(ctx, p, d->score_mask, d->aggregation, 1, 0, d->scores, true, d->k,
-                                                 d->tie_rule, L.m, d->selected, d->count, ss))
+                                                 d->tie_rule, L.m, d->selected, d->count, ss, &L.pol))
         return st;
     return enqueue_stage(ctx, L, ss, cs);
 }
@@ -1198,7 +1404,12 @@ kvr_status kvr_recall_layer(kvr_context *ctx, const kvr_layer_recall *d, void *s
     const hipStream_t cs = stream_or(copy_stream, ctx->copy);
     LayerPlan L;
     if (kvr_status s = plan_layer(ctx, d, ss, cs, L)) return s;
-    return enqueue_layer(ctx, L, ss, cs);
+    Mandatory *lists[1] = {&L.m};
+    bool staged = false;
+    if (kvr_status s = stage_fixed(ctx, lists, 1, ss, staged)) return s;
+    if (kvr_status s = ws_order(ctx, ss)) return s;
+    if (kvr_status s = enqueue_layer(ctx, L, ss, cs)) return s;
+    return fixed_done(ctx, staged, ss);
 }
 
 kvr_status kvr_recall_layer_noalloc(kvr_context *ctx, const kvr_layer_recall *d, void *select_stream,
@@ -1214,11 +1425,19 @@ kvr_status kvr_recall_layer_noalloc(kvr_context *ctx, const kvr_layer_recall *d,
     const hipStream_t cs = stream_or(copy_stream, ctx->copy);
     LayerPlan L;
     if (kvr_status s = plan_layer(ctx, d, ss, cs, L, &fixed)) return s;
+    if (!L.m.more.empty())
+        return fail(KVR_ERR_UNSUPPORTED, "more than %d host mandatory pages need an upload buffer; the no-allocation "
+                                         "entry takes them as a device list (kvr_page_policy.fixed)",
+                    KVR_MAX_INLINE_MANDATORY);
     // the counters must start at zero; a previous call on this GPU leaves them
     // so, but a clear by a kernel keeps the call safe after any abort
     KVR_HIP(kvr::launch_fill_u32(L.p.counters, L.lanes, 0u, ss));
     return enqueue_layer(ctx, L, ss, cs);
 }
+
+namespace {
+kvr_status enqueue_stack(kvr_context *ctx, std::vector<LayerPlan> &plans, hipStream_t ss, hipStream_t cs);
+}  // namespace
 
 kvr_status kvr_recall_stack(kvr_context *ctx, const kvr_layer_recall *layers, uint32_t n, void *select_stream,
                             void *copy_stream) {
@@ -1231,13 +1450,25 @@ kvr_status kvr_recall_stack(kvr_context *ctx, const kvr_layer_recall *layers, ui
     std::vector<LayerPlan> plans(n);
     for (uint32_t l = 0; l < n; ++l)
         if (kvr_status s = plan_layer(ctx, &layers[l], ss, cs, plans[l])) return s;
+    std::vector<Mandatory *> lists(n);
+    for (uint32_t l = 0; l < n; ++l) lists[l] = &plans[l].m;
+    bool staged = false;
+    if (kvr_status s = stage_fixed(ctx, lists.data(), n, ss, staged)) return s;
+    if (kvr_status s = ws_order(ctx, ss)) return s;
+    if (kvr_status s = enqueue_stack(ctx, plans, ss, cs)) return s;
+    return fixed_done(ctx, staged, ss);
+}
+
+namespace {
+kvr_status enqueue_stack(kvr_context *ctx, std::vector<LayerPlan> &plans, hipStream_t ss, hipStream_t cs) {
+    const uint32_t n = uint32_t(plans.size());
     // Layer l's softmax/selection rides in layer l+1's summary launch when
     // every layer takes the fused (vector) scoring path with one geometry.
     const ScorePlan &p0 = plans[0].p;
     bool fuse = n > 1;
     for (const LayerPlan &L : plans)
-        fuse = fuse && !L.p.mfma && L.p.lanes == p0.lanes && L.p.pages == p0.pages && L.p.rows == p0.rows &&
-               L.p.qheads == p0.qheads && L.p.kvheads == p0.kvheads && L.p.dim == p0.dim;
+        fuse = fuse && !L.p.mfma && !L.pol.grouped && L.p.lanes == p0.lanes && L.p.pages == p0.pages &&
+               L.p.rows == p0.rows && L.p.qheads == p0.qheads && L.p.kvheads == p0.kvheads && L.p.dim == p0.dim;
     if (!fuse) {
         for (LayerPlan &L : plans)
             if (kvr_status s = enqueue_layer(ctx, L, ss, cs)) return s;
@@ -1286,6 +1517,7 @@ kvr_status kvr_recall_stack(kvr_context *ctx, const kvr_layer_recall *layers, ui
             g.s[i] = a;
             cur[i] = make_select_args(ctx, L.p, d->score_mask, d->aggregation, 1, 0, d->scores, true, d->k,
                                       d->tie_rule, L.m, d->selected, d->count);
+            if (kvr_status st = put_policy(L.pol, L.m, cur[i])) return st;
             cur[i].counters = ctx->counters + (l % (2 * G)) * p0.lanes;
             if (!resident) {
                 cur[i].summaries = d->summaries;
@@ -1307,6 +1539,7 @@ kvr_status kvr_recall_stack(kvr_context *ctx, const kvr_layer_recall *layers, ui
     }
     return KVR_OK;
 }
+}  // namespace
 
 // ---- sampled attention ------------------------------------------------------
 
@@ -1405,6 +1638,7 @@ kvr_status kvr_attention_page_mass(kvr_context *ctx, const kvr_attention_sample 
     g.scale = a->scale;
     g.softcap = a->softcap;
     g.lse = reinterpret_cast<float *>(ctx->ws);
+    if (kvr_status st = ws_order(ctx, s)) return st;
     for (uint32_t first = 0; first < a->n_rows; first += chunk) {
         g.n_rows = std::min(chunk, a->n_rows - first);
         std::copy(a->rows + first, a->rows + first + g.n_rows, g.rows);
@@ -1422,25 +1656,29 @@ kvr_status kvr_d2d_batched(kvr_context *ctx, const void *const *src, void *const
     if (!n) return KVR_OK;
     if (!src || !dst || !nbytes) return fail(KVR_ERR_INVALID, "missing copy tables");
     DeviceGuard guard(ctx->device);
-    if (ctx->ops_cap < n) {
-        KVR_HIP(hipEventSynchronize(ctx->ops_ev));
-        if (ctx->ops_dev) KVR_HIP(hipFree(ctx->ops_dev));
-        if (ctx->ops_pin) KVR_HIP(hipHostFree(ctx->ops_pin));
-        ctx->ops_dev = ctx->ops_pin = nullptr;
-        ctx->ops_cap = 0;
-        KVR_HIP(hipMalloc(&ctx->ops_dev, sizeof(kvr::CopyOp) * n));
-        KVR_HIP(hipHostMalloc(reinterpret_cast<void **>(&ctx->ops_pin), sizeof(kvr::CopyOp) * n, hipHostMallocDefault));
-        ctx->ops_cap = n;
-    } else {
-        // the previous batch's table upload must finish before the pinned table is rewritten
-        KVR_HIP(hipEventSynchronize(ctx->ops_ev));
+    const hipStream_t s = stream_or(stream, ctx->sel);
+    if (capturing(s))
+        return fail(KVR_ERR_INVALID, "batched copies upload their op table through pinned memory and cannot be "
+                                     "captured");
+    // the slot's previous copy launch (on whatever stream) must have read
+    // its table before the table is rewritten
+    kvr_context::OpSlot &slot = ctx->ops[ctx->ops_next];
+    ctx->ops_next = (ctx->ops_next + 1) % kvr_context::kOpSlots;
+    KVR_HIP(hipEventSynchronize(slot.done));
+    if (slot.cap < n) {
+        if (slot.dev) KVR_HIP(hipFree(slot.dev));
+        if (slot.pin) KVR_HIP(hipHostFree(slot.pin));
+        slot.dev = slot.pin = nullptr;
+        slot.cap = 0;
+        KVR_HIP(hipMalloc(&slot.dev, sizeof(kvr::CopyOp) * n));
+        KVR_HIP(hipHostMalloc(reinterpret_cast<void **>(&slot.pin), sizeof(kvr::CopyOp) * n, hipHostMallocDefault));
+        slot.cap = n;
     }
     for (uint32_t i = 0; i < n; ++i)
-        ctx->ops_pin[i] = kvr::CopyOp{static_cast<const uint8_t *>(src[i]), static_cast<uint8_t *>(dst[i]), nbytes[i]};
-    const hipStream_t s = stream_or(stream, ctx->sel);
-    KVR_HIP(hipMemcpyAsync(ctx->ops_dev, ctx->ops_pin, sizeof(kvr::CopyOp) * n, hipMemcpyHostToDevice, s));
-    KVR_HIP(hipEventRecord(ctx->ops_ev, s));
-    KVR_HIP(kvr::launch_copy_ops(ctx->ops_dev, n, s));
+        slot.pin[i] = kvr::CopyOp{static_cast<const uint8_t *>(src[i]), static_cast<uint8_t *>(dst[i]), nbytes[i]};
+    KVR_HIP(hipMemcpyAsync(slot.dev, slot.pin, sizeof(kvr::CopyOp) * n, hipMemcpyHostToDevice, s));
+    KVR_HIP(kvr::launch_copy_ops(slot.dev, n, s));
+    KVR_HIP(hipEventRecord(slot.done, s));
     return KVR_OK;
 }
 

@@ -35,7 +35,9 @@ __device__ __forceinline__ uint32_t recall16(float v, uint16_t &h) {
 
 // Device status words, one per error class; each holds the epoch (call
 // number) of the latest call that raised it.
-enum : uint32_t { kStatusNonfinite = 0, kStatusRange = 1, kStatusScores = 2, kStatusGraph = 3, kStatusWords = 4 };
+enum : uint32_t {
+    kStatusNonfinite = 0, kStatusRange = 1, kStatusScores = 2, kStatusGraph = 3, kStatusBudget = 4, kStatusWords = 5
+};
 __device__ __forceinline__ void raise_status(uint32_t *status, uint32_t word, uint32_t epoch) {
     atomicMax(status + word, epoch);
 }
@@ -54,8 +56,11 @@ template <class T> __device__ __forceinline__ T load_device(const T *p) {
     return __hip_atomic_load(const_cast<T *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // Waits until this thread's vector memory operations have completed
-// (s_waitcnt vmcnt(0); expcnt and lgkmcnt left at their maxima).
-__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// (s_waitcnt vmcnt(0)).  The memory clobber keeps the compiler from moving
+// any load or store across the wait, so stores issued before it are
+// complete -- for device-scope stores, written through to the device's
+// coherence point -- before anything after it issues.
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 __device__ __forceinline__ bool epoch_failed(const uint32_t *status, uint32_t epoch) {
     // all three loads in flight together

@@ -78,8 +78,17 @@ struct SelectArgs {
     uint32_t tie_higher_first;
     int signed_scores;
     int do_select;
-    uint32_t n_mandatory;      // sorted, unique
+    uint32_t n_mandatory;      // inline fixed pages (any order)
     uint32_t mandatory[kMaxMandatory];
+    const uint32_t *fixed;     // device list of fixed pages (any order, repeats allowed) or null
+    uint32_t n_fixed;
+    // media groups (k_select_groups only): pages of a group are kept whole
+    const uint32_t *groups;    // [n_groups][2] disjoint page ranges [begin, end)
+    uint32_t n_groups;
+    // pages ranked before every other page (k_select_groups only)
+    const uint32_t *preferred;        // [lanes][preferred_stride] or null
+    const uint32_t *preferred_count;  // [lanes]
+    uint32_t preferred_stride;
     uint32_t *selected;        // [lanes][k]
     uint32_t *count;           // [lanes]
     uint32_t *status;
@@ -174,6 +183,12 @@ hipError_t launch_logits_mfma(const MfmaLogitsArgs &a, hipStream_t s);
 hipError_t launch_probs(const SelectArgs &a, hipStream_t s);
 // selection over given scores, one workgroup per lane
 hipError_t launch_select(const SelectArgs &a, hipStream_t s);
+// selection with media groups and preferred pages (rows of at most
+// kGroupSelectPages pages), one workgroup per lane
+constexpr uint32_t kGroupSelectPages = 4096;
+hipError_t launch_select_groups(const SelectArgs &a, hipStream_t s);
+// pages per lane whose fixed-page bitmap the selection tails hold (LDS)
+constexpr uint32_t kFixedBitmapPages = 524288;
 // one stack launch: `pa`'s softmax/selection beside `sa`'s summaries with
 // fused logits (sa.q and sa.logits set)
 hipError_t launch_stack_group(int source, StackGroupArgs g, hipStream_t s);

@@ -850,23 +850,12 @@ __device__ __forceinline__ uint64_t order_key(double v) {
     return (u >> 63) ? ~u : (u | 0x8000000000000000ull);
 }
 
-// Mandatory pages (ascending, at most 64, copied to LDS) met in ascending
-// page order: each query advances a cursor, so a lane's walk over its chunk
-// reads the list once.
-struct MandatoryCursor {
-    const uint32_t *ids;
-    uint32_t p, n;
-    __device__ __forceinline__ MandatoryCursor(const uint32_t *m, uint32_t count, uint32_t first) : ids(m), p(0), n(count) {
-        uint32_t hi = n;  // first entry >= `first`
-        while (p < hi) {
-            const uint32_t mid = (p + hi) >> 1;
-            if (ids[mid] < first) p = mid + 1; else hi = mid;
-        }
-    }
-    __device__ __forceinline__ bool at(uint32_t j) {
-        while (p < n && ids[p] < j) ++p;
-        return p < n && ids[p] == j;
-    }
+// Pages kept before the ranking (mandatory / fixed pages): a bitmap of the
+// lane's pages in LDS, bit j of word j/32 for page j; null when there are
+// none.
+struct FixedPages {
+    const uint32_t *bits;
+    __device__ __forceinline__ bool at(uint32_t j) const { return bits && (bits[j >> 5] >> (j & 31) & 1u); }
 };
 
 // Dynamic LDS of the selection kernels: the lane's keys (pages <= kTailLdsPages).
@@ -959,7 +948,7 @@ __device__ __forceinline__ void tie_window(const SelectArgs &a, uint32_t remaini
 // id chunk [l*C, l*C + C), C = ceil(pages/64) <= 16, and holds its keys in
 // registers.
 __device__ __forceinline__ void wave_select(const SelectArgs &a, uint32_t lane, bool lds, const double *sc,
-                                            uint32_t *hist, const uint32_t *mand_ids) {
+                                            uint32_t *hist, const FixedPages fx, uint32_t n_fixed) {
     constexpr int R = 16;
     const uint32_t l = threadIdx.x & 63, n = a.pages;
     const uint32_t C = (n + kWave - 1) / kWave;
@@ -967,23 +956,20 @@ __device__ __forceinline__ void wave_select(const SelectArgs &a, uint32_t lane, 
     auto load_key = [&](uint32_t j) -> uint64_t { return lds ? tail_keys[j] : order_key(sc[j]); };
     uint64_t kr[R];
     uint32_t cand_bits = 0;  // chunk entries that are candidates
-    {
-        MandatoryCursor mand(mand_ids, a.n_mandatory, j0);
 #pragma unroll
-        for (int c = 0; c < R; ++c) {
-            const uint32_t j = j0 + c;
-            const bool in = j < j1;
-            kr[c] = in ? load_key(j) : 0;
-            if (in && !mand.at(j)) cand_bits |= 1u << c;
-        }
+    for (int c = 0; c < R; ++c) {
+        const uint32_t j = j0 + c;
+        const bool in = j < j1;
+        kr[c] = in ? load_key(j) : 0;
+        if (in && !fx.at(j)) cand_bits |= 1u << c;
     }
     auto for_each_key = [&](auto f) {
 #pragma unroll
         for (int c = 0; c < R; ++c)
             if (cand_bits >> c & 1u) f(kr[c]);
     };
-    const uint32_t n_cand = n - a.n_mandatory;
-    const uint32_t k_eff = a.k - a.n_mandatory;  // host guarantees n_mandatory <= k
+    const uint32_t n_cand = n - n_fixed;
+    const uint32_t k_eff = a.k - n_fixed;  // the tail checked n_fixed <= k
     Threshold t;
     if (k_eff == 0) {
         t.thresh = ~0ull;  // nothing ranks
@@ -1057,7 +1043,7 @@ __device__ __forceinline__ void wave_select(const SelectArgs &a, uint32_t lane, 
 // wave_select, with thread t owning the id chunk [t*C, t*C + C),
 // C = ceil(pages/256), keys read 8 at a time from LDS or the scores.
 __device__ __forceinline__ void wg_select(const SelectArgs &a, uint32_t lane, bool lds, const double *sc,
-                                          uint32_t *hist, const uint32_t *mand_ids) {
+                                          uint32_t *hist, const FixedPages fx, uint32_t n_fixed) {
     constexpr uint32_t B = 256, W = B / kWave;
     __shared__ uint64_t s_red[2][W];
     __shared__ uint32_t s_ctl[3];
@@ -1066,19 +1052,15 @@ __device__ __forceinline__ void wg_select(const SelectArgs &a, uint32_t lane, bo
     const uint32_t n = a.pages, C = (n + B - 1) / B;
     const uint32_t j0 = min(n, tid * C), j1 = min(n, j0 + C);
     auto load_key = [&](uint32_t j) -> uint64_t { return lds ? tail_keys[j] : order_key(sc[j]); };
-    const MandatoryCursor mand0(mand_ids, a.n_mandatory, j0);
-    // chunks of up to 64 ids (rows up to 16384 pages) keep their mandatory
-    // pages as a bit mask, walked once; longer chunks walk the list per pass
+    // chunks of up to 64 ids (rows up to 16384 pages) keep their fixed
+    // pages in a register mask; longer chunks test the LDS bitmap per pass
     const bool masked = C <= 64;
     uint64_t mand_bits = 0;
-    if (masked && a.n_mandatory) {
-        MandatoryCursor mand = mand0;
+    if (masked && fx.bits)
         for (uint32_t j = j0; j < j1; ++j)
-            if (mand.at(j)) mand_bits |= 1ull << (j - j0);
-    }
+            if (fx.at(j)) mand_bits |= 1ull << (j - j0);
     // f(j, key, candidate) over this thread's chunk in id order
     auto chunk = [&](auto f) {
-        MandatoryCursor mand = mand0;
         for (uint32_t b = j0; b < j1; b += 8) {
             uint64_t kk[8];
 #pragma unroll
@@ -1086,7 +1068,7 @@ __device__ __forceinline__ void wg_select(const SelectArgs &a, uint32_t lane, bo
 #pragma unroll
             for (uint32_t u = 0; u < 8; ++u) {
                 const uint32_t j = b + u;
-                if (j < j1) f(j, kk[u], masked ? !(mand_bits >> (j - j0) & 1ull) : !mand.at(j));
+                if (j < j1) f(j, kk[u], masked ? !(mand_bits >> (j - j0) & 1ull) : !fx.at(j));
             }
         }
     };
@@ -1106,8 +1088,8 @@ __device__ __forceinline__ void wg_select(const SelectArgs &a, uint32_t lane, bo
         excl = before + incl - v;
         total = tot;
     };
-    const uint32_t n_cand = n - a.n_mandatory;
-    const uint32_t k_eff = a.k - a.n_mandatory;
+    const uint32_t n_cand = n - n_fixed;
+    const uint32_t k_eff = a.k - n_fixed;
     Threshold t;
     if (k_eff == 0) {
         t.thresh = ~0ull;
@@ -1503,11 +1485,20 @@ __global__ __launch_bounds__(1024) void k_graph_lrfu(GraphLrfuArgs a) {
 // first wave.  Keys go to LDS when the lane's pages fit.
 __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
     __shared__ uint32_t hist[256];
-    __shared__ uint32_t mand_ids[kMaxMandatory];
+    __shared__ uint32_t fixed_small[kTailLdsPages / 32];  // the fixed-page bitmap of short rows
+    __shared__ uint32_t s_fixed[4];
     const uint32_t tid = threadIdx.x, B = blockDim.x;
     const uint32_t n = a.pages;
     const bool lds = n <= kTailLdsPages;
     double *sc = a.scores + uint64_t(lane) * n;
+    // Fixed pages (the inline list and the device list) go to a bitmap: LDS
+    // beside the keys for short rows, the dynamic LDS (not holding keys) for
+    // longer ones.  Cleared here, set once the sums below are done.
+    const bool has_fixed = a.do_select && (a.n_mandatory || a.n_fixed);
+    uint32_t *fbits = lds ? fixed_small : reinterpret_cast<uint32_t *>(tail_keys);
+    const uint32_t words = (n + 31) / 32;
+    if (has_fixed)
+        for (uint32_t w = tid; w < words; w += B) fbits[w] = 0;
     // the status of this call, read early so its latency overlaps the sums
     bool failed = a.do_select && tid < kWave && epoch_failed(a.status, a.epoch);
 
@@ -1592,24 +1583,44 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
         for (uint32_t j = tid; j < n; j += B) note(j, sc[j]);
     }
     if (!a.do_select) return;
+    if (has_fixed) {
+        __syncthreads();  // the bitmap is clear
+        for (uint32_t i = tid; i < a.n_mandatory; i += B) {
+            const uint32_t id = a.mandatory[i];
+            if (id < n) atomicOr(&fbits[id >> 5], 1u << (id & 31));
+        }
+        for (uint32_t i = tid; i < a.n_fixed; i += B) {
+            const uint32_t id = a.fixed[i];  // pages past the row are ignored
+            if (id < n) atomicOr(&fbits[id >> 5], 1u << (id & 31));
+        }
+    }
     // Reject invalid scores (pick_scored_blocks, kvmem_store.cpp:425-426).
-    bad = __syncthreads_or(bad);  // also publishes the LDS keys
+    bad = __syncthreads_or(bad);  // also publishes the LDS keys and the bitmap
+    uint32_t n_fixed = 0;         // distinct fixed pages
+    if (has_fixed) {
+        uint32_t c = 0;
+        for (uint32_t w = tid; w < words; w += B) c += __popc(fbits[w]);
+        c = wave_sum(c);
+        if ((tid & (kWave - 1)) == 0) s_fixed[tid / kWave] = c;
+        __syncthreads();
+        for (uint32_t w = 0; w < B / kWave; ++w) n_fixed += s_fixed[w];
+    }
     const bool wide = n > 16 * kWave;
     if (wide) failed = __syncthreads_or(failed);
     else if (tid >= kWave) return;
     if (bad && tid == 0) raise_status(a.status, kStatusScores, a.epoch);
-    if (bad || failed) {
+    // more fixed pages than the budget (pick_scored_blocks' required keep)
+    const bool over = n_fixed > a.k;
+    if (over && !bad && !failed && tid == 0) raise_status(a.status, kStatusBudget, a.epoch);
+    if (bad || failed || over) {
         if (tid == 0) a.count[lane] = 0;
         return;
     }
-    if (tid < a.n_mandatory) mand_ids[tid] = a.mandatory[tid];
-    if (wide) {
-        lds_barrier();
-        wg_select(a, lane, lds, sc, hist, mand_ids);
-    } else {
-        wave_lds_sync();
-        wave_select(a, lane, lds, sc, hist, mand_ids);
-    }
+    const FixedPages fx{has_fixed ? fbits : nullptr};
+    if (wide)
+        wg_select(a, lane, lds, sc, hist, fx, n_fixed);
+    else
+        wave_select(a, lane, lds, sc, hist, fx, n_fixed);
 }
 
 // Softmax units -> terms; the lane's last workgroup aggregates (+ selects).
@@ -1901,6 +1912,185 @@ __global__ __launch_bounds__(256) void k_stack_group(StackGroupArgs g) {
 
 // Selection over given scores (no softmax), one workgroup per lane.
 __global__ __launch_bounds__(256) void k_select(SelectArgs a) { lane_tail(a, blockIdx.x); }
+
+// ---------------------------------------------------------------------------
+// Selection with media groups: KvMemStore::pick_scored_blocks with media
+// ranges (kvmem/src/host/kvmem_store.cpp:418-451) and the fill of
+// constrain_media (:453-502).  A page in a group is kept only together with
+// its whole group; fixed pages bring their groups and must fit; then the
+// pages are visited in rank order -- preferred pages first, then score
+// desc, then id by the tie rule -- and each visited group (or lone page)
+// is kept when it still fits the budget, else skipped.  A group is met at
+// its best-ranked page, so the lane's units are its lone pages and each
+// group's best page.  One workgroup per lane: keys and each page's group
+// bounds in LDS, the units put in rank order by a bitonic sort, then one
+// thread walks them -- whether a group fits depends on everything taken
+// before it.  Rows of up to kGroupSelectPages pages.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool bit_at(const uint32_t *bits, uint32_t j) { return bits[j >> 5] >> (j & 31) & 1u; }
+__device__ __forceinline__ void bit_set(uint32_t *bits, uint32_t j) { atomicOr(&bits[j >> 5], 1u << (j & 31)); }
+
+__host__ __device__ constexpr uint32_t pow2_ceil(uint32_t n) {
+    uint32_t p = 1;
+    while (p < n) p <<= 1;
+    return p;
+}
+// LDS of k_select_groups: keys (8 B), group begin and end (2 B each) per
+// page, the sort order (2 B per slot of a power of two), three bitmaps.
+__host__ __device__ constexpr size_t group_select_lds(uint32_t n) {
+    return size_t(n) * 12 + ((size_t(pow2_ceil(n)) * 2 + 15) & ~size_t(15)) + size_t((n + 31) / 32) * 12;
+}
+
+__global__ __launch_bounds__(256) void k_select_groups(SelectArgs a) {
+    __shared__ uint32_t s_red[4];
+    __shared__ uint32_t s_count;
+    constexpr uint32_t B = 256;
+    const uint32_t lane = blockIdx.x, tid = threadIdx.x, n = a.pages;
+    const uint32_t N = pow2_ceil(n), words = (n + 31) / 32;
+    uint64_t *key = tail_keys;                                     // [n]
+    uint16_t *glo = reinterpret_cast<uint16_t *>(key + n);         // [n] first page of the page's group
+    uint16_t *ghi = glo + n;                                       // [n] one past its last page
+    uint16_t *order = ghi + n;                                     // [N] page ids by rank
+    uint32_t *kept = reinterpret_cast<uint32_t *>(reinterpret_cast<uint8_t *>(key) + size_t(n) * 12 +
+                                                  ((size_t(N) * 2 + 15) & ~size_t(15)));  // [words]
+    uint32_t *pref = kept + words;  // preferred pages
+    uint32_t *unit = pref + words;  // pages the walk visits
+    const double *sc = a.scores + uint64_t(lane) * n;
+
+    bool failed = a.status && tid == 0 && epoch_failed(a.status, a.epoch);
+    int bad = 0;
+    for (uint32_t j = tid; j < n; j += B) {
+        const double v = sc[j];
+        bad |= !__builtin_isfinite(v) || (!a.signed_scores && v < 0.0);
+        key[j] = order_key(v);
+        glo[j] = uint16_t(j);
+        ghi[j] = uint16_t(j + 1);
+    }
+    for (uint32_t w = tid; w < words; w += B) kept[w] = pref[w] = unit[w] = 0;
+    __syncthreads();
+    for (uint32_t g = tid; g < a.n_groups; g += B) {
+        const uint32_t b = min(a.groups[2 * g], n), e = min(a.groups[2 * g + 1], n);
+        for (uint32_t j = b; j < e; ++j) {
+            glo[j] = uint16_t(b);
+            ghi[j] = uint16_t(e);
+        }
+    }
+    for (uint32_t i = tid; i < a.n_mandatory; i += B)
+        if (a.mandatory[i] < n) bit_set(kept, a.mandatory[i]);
+    for (uint32_t i = tid; i < a.n_fixed; i += B) {
+        const uint32_t id = a.fixed[i];
+        if (id < n) bit_set(kept, id);
+    }
+    if (a.preferred) {
+        const uint32_t *ids = a.preferred + uint64_t(lane) * a.preferred_stride;
+        const uint32_t cnt = min(a.preferred_count[lane], a.preferred_stride);
+        for (uint32_t i = tid; i < cnt; i += B) {
+            const uint32_t id = ids[i];
+            if (id < n) bit_set(pref, id);
+        }
+    }
+    bad = __syncthreads_or(bad);
+    failed = __syncthreads_or(failed);
+    if (bad || failed) {
+        if (bad && tid == 0) raise_status(a.status, kStatusScores, a.epoch);
+        if (tid == 0) a.count[lane] = 0;
+        return;
+    }
+    // u ranks before v
+    auto better = [&](uint32_t u, uint32_t v) -> bool {
+        const bool cu = u < n && bit_at(unit, u), cv = v < n && bit_at(unit, v);
+        if (cu != cv) return cu;
+        if (!cu) return false;
+        const bool pu = bit_at(pref, u), pv = bit_at(pref, v);
+        if (pu != pv) return pu;
+        if (key[u] != key[v]) return key[u] > key[v];
+        return a.tie_higher_first ? u > v : u < v;
+    };
+    auto ranks_before = [&](uint32_t u, uint32_t v) -> bool {  // among pages of one group
+        const bool pu = bit_at(pref, u), pv = bit_at(pref, v);
+        if (pu != pv) return pu;
+        if (key[u] != key[v]) return key[u] > key[v];
+        return a.tie_higher_first ? u > v : u < v;
+    };
+    // A group holding a fixed page is kept whole; else its best page is its
+    // unit.  One thread per group (the one whose page starts it).
+    for (uint32_t j = tid; j < n; j += B) {
+        const uint32_t e = ghi[j];
+        if (glo[j] != j) continue;
+        if (e == j + 1) {
+            if (!bit_at(kept, j)) bit_set(unit, j);
+            continue;
+        }
+        bool any = false;
+        for (uint32_t i = j; i < e && !any; ++i) any = bit_at(kept, i);
+        if (any) {
+            for (uint32_t i = j; i < e; ++i) bit_set(kept, i);
+        } else {
+            uint32_t best = j;
+            for (uint32_t i = j + 1; i < e; ++i)
+                if (ranks_before(i, best)) best = i;
+            bit_set(unit, best);
+        }
+    }
+    __syncthreads();
+    uint32_t c = 0;
+    for (uint32_t w = tid; w < words; w += B) c += __popc(kept[w]);
+    c = wave_sum(c);
+    if ((tid & (kWave - 1)) == 0) s_red[tid / kWave] = c;
+    for (uint32_t i = tid; i < N; i += B) order[i] = uint16_t(i);  // slots past the row: ids >= n, no unit
+    __syncthreads();
+    const uint32_t n_fixed = s_red[0] + s_red[1] + s_red[2] + s_red[3];
+    if (n_fixed > a.k) {
+        if (tid == 0) {
+            raise_status(a.status, kStatusBudget, a.epoch);
+            a.count[lane] = 0;
+        }
+        return;
+    }
+    // bitonic sort of the slots, best first; slots that hold no unit sort
+    // last (they never swap among themselves)
+    for (uint32_t size = 2; size <= N; size <<= 1) {
+        for (uint32_t stride = size >> 1; stride; stride >>= 1) {
+            for (uint32_t i = tid; i < N / 2; i += B) {
+                const uint32_t x = ((i & ~(stride - 1)) << 1) | (i & (stride - 1)), y = x + stride;
+                const uint32_t u = order[x], v = order[y];
+                const bool desc = (x & size) == 0;
+                if (desc ? better(v, u) : better(u, v)) {
+                    order[x] = uint16_t(v);
+                    order[y] = uint16_t(u);
+                }
+            }
+            lds_barrier();
+        }
+    }
+    if (tid == 0) {
+        uint32_t cnt = n_fixed;
+        for (uint32_t i = 0; i < N && cnt < a.k; ++i) {
+            const uint32_t u = order[i];
+            if (u >= n || !bit_at(unit, u)) break;
+            const uint32_t b = glo[u], e = ghi[u];
+            if (cnt + (e - b) > a.k) continue;
+            for (uint32_t p = b; p < e; ++p) kept[p >> 5] |= 1u << (p & 31);
+            cnt += e - b;
+        }
+        s_count = cnt;
+    }
+    __syncthreads();
+    // kept pages in ascending order: each thread a run of whole words
+    const uint32_t wpt = (words + B - 1) / B, w0 = min(words, tid * wpt), w1 = min(words, w0 + wpt);
+    uint32_t mine = 0;
+    for (uint32_t w = w0; w < w1; ++w) mine += __popc(kept[w]);
+    const uint32_t incl = wave_inclusive_scan(mine);
+    if ((tid & (kWave - 1)) == kWave - 1) s_red[tid / kWave] = incl;
+    __syncthreads();
+    uint32_t o = incl - mine;
+    for (uint32_t w = 0; w < tid / kWave; ++w) o += s_red[w];
+    uint32_t *out = a.selected + uint64_t(lane) * a.k;
+    for (uint32_t w = w0; w < w1; ++w)
+        for (uint32_t bits = kept[w]; bits; bits &= bits - 1)
+            if (o < a.k) out[o++] = w * 32 + uint32_t(__ffs(bits) - 1);
+    if (tid == 0) a.count[lane] = min(s_count, a.k);
+}
 
 // ---------------------------------------------------------------------------
 // Stage-in gather.  One workgroup copies `chunk_rows` token rows of one
@@ -2424,11 +2614,18 @@ hipError_t launch_logits_mfma(const MfmaLogitsArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Dynamic LDS of a selection tail: the keys of rows up to kTailLdsPages
+// pages; for longer rows with fixed pages, their bitmap.
+inline size_t tail_lds_bytes(const SelectArgs &a) {
+    if (a.pages <= kTailLdsPages) return size_t(a.pages) * 8;
+    return a.do_select && (a.n_mandatory || a.n_fixed) ? size_t((a.pages + 31) / 32) * 4 : 0;
+}
+
 hipError_t launch_probs(const SelectArgs &a, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch\'s error
     const uint32_t upb = units_per_block(a.pages);
     const dim3 grid((a.units + upb - 1) / upb, a.lanes), block(256);
-    const size_t lds = a.pages <= kTailLdsPages ? size_t(a.pages) * 8 : 0;
+    const size_t lds = tail_lds_bytes(a);
     if (a.pages <= 64) hipLaunchKernelGGL(k_probs<1>, grid, block, lds, s, a);
     else if (a.pages <= 128) hipLaunchKernelGGL(k_probs<2>, grid, block, lds, s, a);
     else if (a.pages <= 256) hipLaunchKernelGGL(k_probs<4>, grid, block, lds, s, a);
@@ -2447,7 +2644,8 @@ hipError_t launch_stack_group(int source, StackGroupArgs g, hipStream_t s) {
     const uint32_t probs_blocks = g.mp ? g.mp * g.probs_per_lane * pa.lanes : 0;
     const dim3 grid(unsigned(sb + probs_blocks)), block(256);
     const size_t q_lds_bytes = g.m && source == kSrcSummary && sa.q_stage ? size_t(2) * g.q_slot * 2 : 0;
-    const size_t keys = g.mp && pa.pages <= kTailLdsPages ? size_t(pa.pages) * 8 : 0;  // the tails' keys
+    size_t keys = 0;  // the tails' keys or fixed-page bitmaps
+    for (uint32_t i = 0; i < g.mp; ++i) keys = tail_lds_bytes(g.p[i]) > keys ? tail_lds_bytes(g.p[i]) : keys;
     size_t lds = q_lds_bytes > keys ? q_lds_bytes : keys;
     for (uint32_t i = 0; i < g.mp; ++i) {  // softmax workgroups' logits rows
         const SelectArgs &p = g.p[i];
@@ -2478,8 +2676,13 @@ hipError_t launch_stack_group(int source, StackGroupArgs g, hipStream_t s) {
 
 hipError_t launch_select(const SelectArgs &a, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch\'s error
-    const size_t lds = a.pages <= kTailLdsPages ? size_t(a.pages) * 8 : 0;
-    hipLaunchKernelGGL(k_select, dim3(a.lanes), dim3(256), lds, s, a);
+    hipLaunchKernelGGL(k_select, dim3(a.lanes), dim3(256), tail_lds_bytes(a), s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_select_groups(const SelectArgs &a, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch\'s error
+    hipLaunchKernelGGL(k_select_groups, dim3(a.lanes), dim3(256), group_select_lds(a.pages), s, a);
     return hipGetLastError();
 }
 

@@ -24,7 +24,8 @@ namespace {
     std::string msg = std::string(what) + ": " + kvr_last_error();
     switch (s) {
     case KVR_ERR_WORKSPACE: throw std::length_error(msg);
-    case KVR_ERR_HIP: throw std::runtime_error(msg);
+    case KVR_ERR_HIP:
+    case KVR_ERR_BUDGET: throw std::runtime_error(msg);  // the reference's required-keep failure
     default: throw std::invalid_argument(msg);
     }
 }
@@ -154,6 +155,9 @@ struct PageSoftmaxHip::Impl {
     uint8_t *mask = nullptr;
     double *scores = nullptr;
     uint32_t *sel = nullptr, *cnt = nullptr;
+    // page-policy lists of media-aware picks: fixed pages [pages], groups
+    // [pages][2], the grouped pass's selection [pages] and count
+    uint32_t *fixed = nullptr, *groups = nullptr, *sel2 = nullptr, *cnt2 = nullptr;
     size_t page_cap = 0;
     std::vector<void *> owned;
 
@@ -184,22 +188,39 @@ struct PageSoftmaxHip::Impl {
             q_cap = qf;
         }
         if (pages > page_cap) {
-            const size_t bytes = align256(pages) + align256(size_t(pages) * 8) + align256(size_t(pages) * 4) + 256;
             void *p = nullptr;
-            hip_ok(hipMalloc(&p, bytes), "hipMalloc scores");
+            hip_ok(hipMalloc(&p, page_bytes(pages)), "hipMalloc scores");
             owned.push_back(p);
-            uint8_t *b = static_cast<uint8_t *>(p);
-            mask = b;
-            scores = reinterpret_cast<double *>(b + align256(pages));
-            sel = reinterpret_cast<uint32_t *>(b + align256(pages) + align256(size_t(pages) * 8));
-            cnt = reinterpret_cast<uint32_t *>(b + bytes - 256);
-            page_cap = pages;
+            carve_pages(static_cast<uint8_t *>(p), pages);
         }
     }
 
+    // Per-page buffers: mask, scores, selection and count, then the policy
+    // lists.
+    static size_t page_bytes(uint32_t pages) {
+        return align256(pages) + align256(size_t(pages) * 8) + 2 * align256(size_t(pages) * 4) + 256 +
+               align256(size_t(pages) * 8) + align256(size_t(pages) * 4) + 256;
+    }
+    void carve_pages(uint8_t *b, uint32_t pages) {
+        mask = b;
+        b += align256(pages);
+        scores = reinterpret_cast<double *>(b);
+        b += align256(size_t(pages) * 8);
+        sel = reinterpret_cast<uint32_t *>(b);
+        b += align256(size_t(pages) * 4);
+        fixed = reinterpret_cast<uint32_t *>(b);
+        b += align256(size_t(pages) * 4);
+        cnt = reinterpret_cast<uint32_t *>(b);
+        cnt2 = cnt + 1;
+        b += 256;
+        groups = reinterpret_cast<uint32_t *>(b);
+        b += align256(size_t(pages) * 8);
+        sel2 = reinterpret_cast<uint32_t *>(b);
+        page_cap = pages;
+    }
+
     static size_t carve_bytes(uint32_t max_blocks, uint32_t qheads, uint32_t dim) {
-        return align256(size_t(kRowsPerLaunch) * qheads * dim * sizeof(float)) + align256(max_blocks) +
-               align256(size_t(max_blocks) * 8) + align256(size_t(max_blocks) * 4) + 256;
+        return align256(size_t(kRowsPerLaunch) * qheads * dim * sizeof(float)) + page_bytes(max_blocks);
     }
 
     // Rows of one kvr_score call within the logits budget of the workspace.
@@ -269,14 +290,7 @@ PageSoftmaxHip::PageSoftmaxHip(int device, void *workspace, size_t bytes, uint32
     m.q = reinterpret_cast<float *>(b);
     m.q_cap = size_t(rows) * qheads * dim;
     b += align256(size_t(kRowsPerLaunch) * qheads * dim * sizeof(float));
-    m.mask = b;
-    b += align256(max_blocks);
-    m.scores = reinterpret_cast<double *>(b);
-    b += align256(size_t(max_blocks) * 8);
-    m.sel = reinterpret_cast<uint32_t *>(b);
-    b += align256(size_t(max_blocks) * 4);
-    m.cnt = reinterpret_cast<uint32_t *>(b);
-    m.page_cap = max_blocks;
+    m.carve_pages(b, max_blocks);
 }
 
 PageSoftmaxHip::~PageSoftmaxHip() = default;
@@ -391,39 +405,179 @@ std::vector<double> PageSoftmaxHip::score_current_layer(const PageSummaries &sum
     return out;
 }
 
+namespace {
+// Distinct ascending page ids, each below n.
+std::vector<uint32_t> distinct_pages(const std::vector<uint32_t> &ids, uint32_t n, const char *what) {
+    std::vector<uint32_t> v(ids);
+    std::sort(v.begin(), v.end());
+    v.erase(std::unique(v.begin(), v.end()), v.end());
+    for (uint32_t id : v) require(id < n, what);
+    return v;
+}
+
+kvr_media media_of(const MediaRanges &media, uint32_t page_tokens, uint64_t total_tokens,
+                   std::vector<uint32_t> &flat) {
+    flat.clear();
+    for (const auto &r : media) {
+        flat.push_back(r.first);
+        flat.push_back(r.second);
+    }
+    kvr_media m{};
+    m.ranges = flat.data();
+    m.n_ranges = uint32_t(media.size());
+    m.page_tokens = page_tokens;
+    m.total_tokens = total_tokens;
+    return m;
+}
+
+kvr_tie_rule tie_of(TieRule t) { return t == TieRule::HigherFirst ? KVR_TIE_HIGHER_FIRST : KVR_TIE_LOWER_FIRST; }
+}  // namespace
+
+std::vector<uint32_t> query_fixed_blocks(uint32_t pages, uint32_t budget, uint32_t sink, uint32_t recent,
+                                         const MediaRanges &media, uint32_t page_tokens, uint64_t total_tokens,
+                                         const std::vector<uint32_t> &mandatory) {
+    require(page_tokens, "page_tokens must be nonzero");
+    std::vector<uint32_t> flat;
+    const kvr_media m = media_of(media, page_tokens, total_tokens, flat);
+    std::vector<uint32_t> out(std::max<uint32_t>(pages, 1));
+    uint32_t n = 0;
+    ok(kvr_query_fixed_pages(pages, budget, sink, recent, &m, mandatory.data(), uint32_t(mandatory.size()),
+                             out.data(), &n),
+       "query fixed pages");
+    out.resize(n);
+    return out;
+}
+
+// Reads back a device selection of up to k pages; operand and budget
+// errors of the device pick come back as the reference's exceptions.
+std::vector<uint32_t> PageSoftmaxHip::fetch_pick(const uint32_t *sel, const uint32_t *cnt, uint32_t k, void *stream,
+                                                 const char *what) {
+    Impl &m = *impl_;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    std::vector<uint32_t> out(k);
+    uint32_t count = 0;
+    hip_ok(hipMemcpyAsync(out.data(), sel, size_t(k) * 4, hipMemcpyDeviceToHost, s), "selection D2H");
+    hip_ok(hipMemcpyAsync(&count, cnt, 4, hipMemcpyDeviceToHost, s), "count D2H");
+    hip_ok(hipStreamSynchronize(s), "hipStreamSynchronize");
+    const kvr_status st = kvr_check(m.ctx, s);
+    if (st == KVR_ERR_SCORES) throw std::invalid_argument("scores must be finite and non-negative");
+    ok(st, what);
+    out.resize(count);
+    return out;
+}
+
 std::vector<uint32_t> PageSoftmaxHip::pick(const std::vector<double> &scores, uint32_t budget,
                                            const std::vector<uint32_t> &mandatory, TieRule tie,
                                            bool signed_scores) {
+    return pick(scores, budget, mandatory, tie, signed_scores, {}, 1);
+}
+
+std::vector<uint32_t> PageSoftmaxHip::pick(const std::vector<double> &scores, uint32_t budget,
+                                           const std::vector<uint32_t> &mandatory, TieRule tie, bool signed_scores,
+                                           const MediaRanges &media, uint32_t page_tokens) {
     Impl &m = *impl_;
     const uint32_t n = uint32_t(scores.size());
     require(budget, "invalid scored selection frame (budget 0)");
-    require(mandatory.size() <= KVR_MAX_INLINE_MANDATORY, "more mandatory pages than one call carries");
+    require(page_tokens, "page_tokens must be nonzero");
     if (!n) return {};
-    std::vector<uint32_t> mand(mandatory);
-    std::sort(mand.begin(), mand.end());
-    mand.erase(std::unique(mand.begin(), mand.end()), mand.end());
-    for (uint32_t id : mand) require(id < n, "mandatory page outside the scored index");
-    if (mand.size() > budget) throw std::invalid_argument("mandatory pages exceed the selection budget");
+    const std::vector<uint32_t> mand = distinct_pages(mandatory, n, "mandatory page outside the scored index");
     const uint32_t k = std::min(budget, n);
     DeviceBinding bind(m.device);
     m.reserve(0, n);
     const hipStream_t s = m.stream();
     StreamDrain drain{s};
     hip_ok(hipMemcpyAsync(m.scores, scores.data(), size_t(n) * 8, hipMemcpyHostToDevice, s), "scores H2D");
-    ok(kvr_select_topk(m.ctx, m.scores, 1, n, k, mand.data(), uint32_t(mand.size()),
-                       tie == TieRule::HigherFirst ? KVR_TIE_HIGHER_FIRST : KVR_TIE_LOWER_FIRST, signed_scores,
-                       m.sel, m.cnt, s),
-       "pick scored blocks");
-    std::vector<uint32_t> out(k);
-    uint32_t count = 0;
-    hip_ok(hipMemcpyAsync(out.data(), m.sel, size_t(k) * 4, hipMemcpyDeviceToHost, s), "selection D2H");
-    hip_ok(hipMemcpyAsync(&count, m.cnt, 4, hipMemcpyDeviceToHost, s), "count D2H");
-    hip_ok(hipStreamSynchronize(s), "hipStreamSynchronize");
+    std::vector<uint32_t> flat, groups(2 * std::max<size_t>(media.size(), 1));
+    uint32_t n_groups = 0;
+    if (!media.empty()) {
+        const kvr_media md = media_of(media, page_tokens, uint64_t(n) * page_tokens, flat);
+        ok(kvr_media_page_groups(&md, n, KVR_MEDIA_OVERLAP, groups.data(), &n_groups), "media groups");
+    }
+    if (!n_groups) {
+        if (mand.size() > budget)
+            throw std::runtime_error("mandatory scored content is cold, incomplete or exceeds budget");
+        ok(kvr_select_topk(m.ctx, m.scores, 1, n, k, mand.data(), uint32_t(mand.size()), tie_of(tie), signed_scores,
+                           m.sel, m.cnt, s),
+           "pick scored blocks");
+    } else {
+        hip_ok(hipMemcpyAsync(m.groups, groups.data(), size_t(n_groups) * 8, hipMemcpyHostToDevice, s), "groups H2D");
+        if (!mand.empty())
+            hip_ok(hipMemcpyAsync(m.fixed, mand.data(), mand.size() * 4, hipMemcpyHostToDevice, s), "fixed H2D");
+        kvr_page_policy pol{};
+        pol.fixed = m.fixed;
+        pol.n_fixed = uint32_t(mand.size());
+        pol.groups = m.groups;
+        pol.n_groups = n_groups;
+        ok(kvr_select_pages(m.ctx, m.scores, 1, n, k, &pol, tie_of(tie), signed_scores, m.sel, m.cnt, s),
+           "pick scored blocks");
+    }
+    auto out = fetch_pick(m.sel, m.cnt, k, s, "pick scored blocks");
     drain.armed = false;
-    const kvr_status st = kvr_check(m.ctx, s);
-    if (st == KVR_ERR_SCORES) throw std::invalid_argument("scores must be finite and non-negative");
-    ok(st, "pick scored blocks");
-    out.resize(count);
+    return out;
+}
+
+std::vector<uint32_t> PageSoftmaxHip::pick_topk(const std::vector<double> &scores, uint32_t budget, uint32_t sink,
+                                                uint32_t recent, const std::vector<uint32_t> &mandatory,
+                                                const MediaRanges &media, uint32_t page_tokens,
+                                                uint64_t total_tokens) {
+    Impl &m = *impl_;
+    const uint32_t n = uint32_t(scores.size());
+    require(page_tokens, "page_tokens must be nonzero");
+    if (!n) return {};
+    if (!budget || n <= budget) {
+        std::vector<uint32_t> all(n);
+        for (uint32_t i = 0; i < n; ++i) all[i] = i;
+        return all;
+    }
+    // pick_topk_ungrouped: the kept pages on the host, the fill on the device
+    std::vector<uint32_t> kept(n);
+    uint32_t n_kept = 0;
+    ok(kvr_topk_fixed_pages(n, budget, sink, recent, mandatory.data(), uint32_t(mandatory.size()), kept.data(),
+                            &n_kept),
+       "top-k fixed pages");
+    DeviceBinding bind(m.device);
+    m.reserve(0, n);
+    const hipStream_t s = m.stream();
+    StreamDrain drain{s};
+    hip_ok(hipMemcpyAsync(m.scores, scores.data(), size_t(n) * 8, hipMemcpyHostToDevice, s), "scores H2D");
+    if (n_kept)
+        hip_ok(hipMemcpyAsync(m.fixed, kept.data(), size_t(n_kept) * 4, hipMemcpyHostToDevice, s), "fixed H2D");
+    kvr_page_policy first{};
+    first.fixed = m.fixed;
+    first.n_fixed = n_kept;
+    ok(kvr_select_pages(m.ctx, m.scores, 1, n, budget, &first, KVR_TIE_HIGHER_FIRST, 1, m.sel, m.cnt, s),
+       "pick top-k blocks");
+    if (media.empty()) {
+        auto out = fetch_pick(m.sel, m.cnt, budget, s, "pick top-k blocks");
+        drain.armed = false;
+        return out;
+    }
+    // constrain_media: the ungrouped pick's pages first, media groups whole
+    std::vector<uint32_t> flat, groups(2 * media.size());
+    const kvr_media md = media_of(media, page_tokens, total_tokens, flat);
+    uint32_t n_groups = 0, n_fixed = 0;
+    std::vector<uint32_t> fixed(n);
+    ok(kvr_media_page_groups(&md, n, KVR_MEDIA_IN_ORDER, groups.data(), &n_groups), "media groups");
+    ok(kvr_media_fixed_pages(n, budget, sink, &md, mandatory.data(), uint32_t(mandatory.size()), fixed.data(),
+                             &n_fixed),
+       "media fixed pages");
+    hip_ok(hipStreamSynchronize(s), "hipStreamSynchronize");  // m.fixed is rewritten below
+    if (n_groups)
+        hip_ok(hipMemcpyAsync(m.groups, groups.data(), size_t(n_groups) * 8, hipMemcpyHostToDevice, s), "groups H2D");
+    if (n_fixed)
+        hip_ok(hipMemcpyAsync(m.fixed, fixed.data(), size_t(n_fixed) * 4, hipMemcpyHostToDevice, s), "fixed H2D");
+    kvr_page_policy second{};
+    second.fixed = m.fixed;
+    second.n_fixed = n_fixed;
+    second.groups = m.groups;
+    second.n_groups = n_groups;
+    second.preferred = m.sel;
+    second.preferred_count = m.cnt;
+    second.preferred_stride = budget;
+    ok(kvr_select_pages(m.ctx, m.scores, 1, n, budget, &second, KVR_TIE_HIGHER_FIRST, 1, m.sel2, m.cnt2, s),
+       "pick top-k blocks");
+    auto out = fetch_pick(m.sel2, m.cnt2, budget, s, "pick top-k blocks");
+    drain.armed = false;
     return out;
 }
 

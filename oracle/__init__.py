@@ -52,6 +52,11 @@ def _load_oracle() -> C.CDLL:
                                               C.c_float, C.c_int, _P]),
         "orc_page_logits": (C.c_int, [_P, _P, _u32, _u32, _u32, _u32, _u32, C.c_float, _P]),
         "orc_pick_scored_blocks": (C.c_int, [_P, _u32, _P, _u32, _u32, C.c_int, C.c_int, _P, _P]),
+        "orc_media_group": (None, [_u32, _u32, _u32, _P, _u32, _P, _P]),
+        "orc_query_fixed_blocks": (C.c_int, [_u32, _u32, _u32, _u32, _P, _u32, _u64, _u32, _P, _u32, _P, _P]),
+        "orc_pick_scored_grouped": (C.c_int, [_P, _u32, _P, _u32, _u32, C.c_int, C.c_int, _P, _u32, _u32, _P, _P]),
+        "orc_pick_topk_ungrouped": (C.c_int, [_P, _u32, _u32, _u32, _u32, _P, _u32, _P, _P]),
+        "orc_constrain_media": (C.c_int, [_P, _u32, _P, _u32, _u32, _u32, _P, _u32, _u64, _u32, _P, _u32, _P, _P]),
         "orc_dequant_q8_0": (None, [_P, _P]),
         "orc_dequant_q4_1": (None, [_P, _P]),
         "orc_quant_q8_0": (None, [_P, _P]),
@@ -108,6 +113,9 @@ def _load_ref() -> Optional[C.CDLL]:
         "ref_layerwise_scores_f16_keys": (C.c_int, [_P, _u32, _u32, _u64, _u32, _u32, _u32, _P,
                                                     _u32, _u32, C.c_float, _P]),
         "ref_pick_scored_blocks": (C.c_int, [_P, _u32, _P, _u32, _u32, C.c_int, _P, _P]),
+        "ref_query_fixed_blocks": (C.c_int, [_u64, _u32, _u32, _u32, _u32, _P, _u32, _P, _u32, _P, _P]),
+        "ref_pick_scored_grouped": (C.c_int, [_P, _u64, _u32, _P, _u32, _P, _u32, _u32, C.c_int, _P, _P]),
+        "ref_pick_topk_blocks": (C.c_int, [_P, _u64, _u32, _u32, _u32, _u32, _P, _u32, _P, _u32, _P, _P]),
         "ref_propagate_query_scores": (C.c_int, [_P, _u32, _P, _u32, _u32, _P, _P, _P, _P, _u32, _P, _P, _P,
                                                  C.c_double, C.c_double, _P]),
         "ref_graph_accept": (C.c_int, [_u32, _u64, _u32, _P, _P, _P, _P, _u32, _u32, _u32, _P, _P, _P, _P, _P]),
@@ -220,6 +228,106 @@ def pick_scored_blocks(scores: np.ndarray, budget: int, mandatory: Sequence[int]
     n_out = C.c_uint32()
     _check(lib.orc_pick_scored_blocks(_ptr(scores), n, _ptr(pins), len(mandatory), budget,
                                       tie_rule, int(signed_scores), _ptr(out), C.byref(n_out)))
+    return out[: n_out.value].copy()
+
+
+# ---- page policies (media groups, fixed pages) --------------------------------
+# Media ranges are token ranges: a sequence of (first, end) pairs.
+
+def _ranges(ranges) -> np.ndarray:
+    return _c(np.asarray(list(ranges) or [(0, 0)], np.uint32).reshape(-1, 2), np.uint32)
+
+
+def media_group(page: int, pages: int, page_tokens: int, ranges) -> tuple:
+    """scored_media_group: the page range [begin, end) kept with `page`."""
+    r = _ranges(ranges)
+    b, e = C.c_uint32(), C.c_uint32()
+    lib.orc_media_group(page, pages, page_tokens, _ptr(r), len(ranges), C.byref(b), C.byref(e))
+    return b.value, e.value
+
+
+def _out(n: int):
+    return np.zeros(max(n, 1), np.uint32), C.c_uint32()
+
+
+def query_fixed_blocks(pages: int, budget: int, sink: int, recent: int, ranges, total_tokens: int,
+                       page_tokens: int, mandatory: Sequence[int] = ()) -> np.ndarray:
+    r, m = _ranges(ranges), _c(list(mandatory) or [0], np.uint32)
+    out, n_out = _out(pages)
+    _check(lib.orc_query_fixed_blocks(pages, budget, sink, recent, _ptr(r), len(ranges), total_tokens, page_tokens,
+                                      _ptr(m), len(mandatory), _ptr(out), C.byref(n_out)))
+    return out[: n_out.value].copy()
+
+
+def pick_scored_grouped(scores: np.ndarray, budget: int, mandatory: Sequence[int] = (), ranges=(),
+                        page_tokens: int = 256, tie_rule: int = TIE_HIGHER_FIRST,
+                        signed_scores: bool = False) -> np.ndarray:
+    scores = _c(scores, np.float64)
+    n = scores.shape[0]
+    r, m = _ranges(ranges), _c(list(mandatory) or [0], np.uint32)
+    out, n_out = _out(n)
+    _check(lib.orc_pick_scored_grouped(_ptr(scores), n, _ptr(m), len(mandatory), budget, tie_rule,
+                                       int(signed_scores), _ptr(r), len(ranges), page_tokens, _ptr(out),
+                                       C.byref(n_out)))
+    return out[: n_out.value].copy()
+
+
+def pick_topk_ungrouped(scores: np.ndarray, budget: int, sink: int = 0, recent: int = 0,
+                        mandatory: Sequence[int] = ()) -> np.ndarray:
+    scores = _c(scores, np.float64)
+    n = scores.shape[0]
+    m = _c(list(mandatory) or [0], np.uint32)
+    out, n_out = _out(n)
+    _check(lib.orc_pick_topk_ungrouped(_ptr(scores), n, budget, sink, recent, _ptr(m), len(mandatory), _ptr(out),
+                                       C.byref(n_out)))
+    return out[: n_out.value].copy()
+
+
+def constrain_media(selected: Sequence[int], scores: np.ndarray, budget: int, sink: int, ranges, total_tokens: int,
+                    page_tokens: int, mandatory: Sequence[int] = ()) -> np.ndarray:
+    scores = _c(scores, np.float64)
+    n = scores.shape[0]
+    sel = _c(list(selected) or [0], np.uint32)
+    r, m = _ranges(ranges), _c(list(mandatory) or [0], np.uint32)
+    out, n_out = _out(n)
+    _check(lib.orc_constrain_media(_ptr(sel), len(selected), _ptr(scores), n, budget, sink, _ptr(r), len(ranges),
+                                   total_tokens, page_tokens, _ptr(m), len(mandatory), _ptr(out), C.byref(n_out)))
+    return out[: n_out.value].copy()
+
+
+def pick_topk_blocks(scores: np.ndarray, budget: int, sink: int, recent: int, ranges, total_tokens: int,
+                     page_tokens: int, mandatory: Sequence[int] = ()) -> np.ndarray:
+    """KvMemStore::pick_topk_blocks: the ungrouped pick, then constrain_media."""
+    sel = pick_topk_ungrouped(scores, budget, sink, recent, mandatory)
+    return constrain_media(sel, scores, budget, sink, ranges, total_tokens, page_tokens, mandatory)
+
+
+def ref_query_fixed_blocks(total_tokens: int, page_tokens: int, budget: int, sink: int, recent: int, ranges,
+                           mandatory: Sequence[int] = ()) -> np.ndarray:
+    r, m = _ranges(ranges), _c(list(mandatory) or [0], np.uint32)
+    out, n_out = _out(int(-(-total_tokens // page_tokens)))
+    _ref_check(ref.ref_query_fixed_blocks(total_tokens, page_tokens, budget, sink, recent, _ptr(r), len(ranges),
+                                          _ptr(m), len(mandatory), _ptr(out), C.byref(n_out)))
+    return out[: n_out.value].copy()
+
+
+def ref_pick_scored_grouped(scores: np.ndarray, total_tokens: int, page_tokens: int, ranges, budget: int,
+                            mandatory: Sequence[int] = (), signed_scores: bool = False) -> np.ndarray:
+    scores = _c(scores, np.float64)
+    r, m = _ranges(ranges), _c(list(mandatory) or [0], np.uint32)
+    out, n_out = _out(scores.shape[0])
+    _ref_check(ref.ref_pick_scored_grouped(_ptr(scores), total_tokens, page_tokens, _ptr(r), len(ranges), _ptr(m),
+                                           len(mandatory), budget, int(signed_scores), _ptr(out), C.byref(n_out)))
+    return out[: n_out.value].copy()
+
+
+def ref_pick_topk_blocks(scores: np.ndarray, total_tokens: int, page_tokens: int, budget: int, sink: int,
+                         recent: int, ranges, mandatory: Sequence[int] = ()) -> np.ndarray:
+    scores = _c(scores, np.float64)
+    r, m = _ranges(ranges), _c(list(mandatory) or [0], np.uint32)
+    out, n_out = _out(scores.shape[0])
+    _ref_check(ref.ref_pick_topk_blocks(_ptr(scores), total_tokens, page_tokens, budget, sink, recent, _ptr(r),
+                                        len(ranges), _ptr(m), len(mandatory), _ptr(out), C.byref(n_out)))
     return out[: n_out.value].copy()
 
 

@@ -399,6 +399,218 @@ int orc_pick_scored_blocks(const double *scores, uint32_t n, const uint32_t *man
 }
 
 /* ---------------------------------------------------------------------- */
+/* Page policies around the scored pick (kvmem_store.cpp).  Media ranges    */
+/* are token ranges [first, end), ranges[2*i], ranges[2*i+1].               */
+/* ---------------------------------------------------------------------- */
+
+/* scored_media_group (kvmem_store.cpp:18-32): the pages kept together with */
+/* page id -- every range sharing a page with the group joins it, until     */
+/* nothing changes; a page in no range is alone.                            */
+void orc_media_group(uint32_t id, uint32_t n, uint32_t page_tokens, const uint32_t *ranges,
+                     uint32_t n_ranges, uint32_t *begin_out, uint32_t *end_out) {
+    uint32_t begin = id, end = id + 1;
+    int changed;
+    do {
+        const uint32_t old_begin = begin, old_end = end;
+        for (uint32_t r = 0; r < n_ranges; ++r) {
+            const uint32_t lo = ranges[2 * r] / page_tokens;
+            const uint64_t up = ((uint64_t)ranges[2 * r + 1] + page_tokens - 1) / page_tokens;
+            const uint32_t hi = up < n ? (uint32_t)up : n;
+            if (lo < end && begin < hi) {
+                if (lo < begin) begin = lo;
+                if (hi > end) end = hi;
+            }
+        }
+        changed = old_begin != begin || old_end != end;
+    } while (changed);
+    *begin_out = begin;
+    *end_out = end;
+}
+
+/* keep() of query_fixed_blocks / pick_scored_blocks: the page's whole media */
+/* group, or nothing when it does not fit (an error when required).         */
+static int keep_group(uint8_t *kept, uint32_t *count, uint32_t id, int required, uint32_t n, uint32_t budget,
+                      uint32_t page_tokens, const uint32_t *ranges, uint32_t n_ranges) {
+    if (id >= n) return ORC_ERR_ARG;
+    uint32_t begin, end;
+    orc_media_group(id, n, page_tokens, ranges, n_ranges, &begin, &end);
+    uint32_t need = 0;
+    for (uint32_t b = begin; b < end; ++b) need += !kept[b];
+    if (*count + need > budget) return required ? ORC_ERR_BUDGET : ORC_OK;
+    for (uint32_t b = begin; b < end; ++b)
+        if (!kept[b]) { kept[b] = 1; ++*count; }
+    return ORC_OK;
+}
+
+static uint32_t emit_kept(const uint8_t *kept, uint32_t n, uint32_t *out) {
+    uint32_t o = 0;
+    for (uint32_t i = 0; i < n; ++i)
+        if (kept[i]) out[o++] = i;
+    return o;
+}
+
+/* KvMemStore::query_fixed_blocks (kvmem_store.cpp:381-408): every page when */
+/* the budget is 0 or covers them all; else the sink pages, the page where  */
+/* the last media range starts (when it starts before total_tokens) and the */
+/* mandatory pages, each with its whole media group and required to fit,    */
+/* then the newest `recent` pages newest first, each kept only if it fits.  */
+int orc_query_fixed_blocks(uint32_t n, uint32_t budget, uint32_t sink, uint32_t recent, const uint32_t *ranges,
+                           uint32_t n_ranges, uint64_t total_tokens, uint32_t page_tokens,
+                           const uint32_t *mandatory, uint32_t n_mandatory, uint32_t *out, uint32_t *n_out) {
+    *n_out = 0;
+    if (!page_tokens) return ORC_ERR_ARG;
+    if (!budget || n <= budget) {
+        for (uint32_t i = 0; i < n; ++i) out[i] = i;
+        *n_out = n;
+        return ORC_OK;
+    }
+    uint8_t *kept = (uint8_t *)calloc(n, 1);
+    uint32_t count = 0;
+    int st = ORC_OK;
+    for (uint32_t i = 0; st == ORC_OK && i < (n < sink ? n : sink); ++i)
+        st = keep_group(kept, &count, i, 1, n, budget, page_tokens, ranges, n_ranges);
+    if (st == ORC_OK && n_ranges && ranges[2 * (n_ranges - 1)] < total_tokens)
+        st = keep_group(kept, &count, ranges[2 * (n_ranges - 1)] / page_tokens, 1, n, budget, page_tokens, ranges,
+                        n_ranges);
+    for (uint32_t i = 0; st == ORC_OK && i < n_mandatory; ++i)
+        st = keep_group(kept, &count, mandatory[i], 1, n, budget, page_tokens, ranges, n_ranges);
+    for (uint32_t i = 0; st == ORC_OK && i < (n < recent ? n : recent); ++i)
+        st = keep_group(kept, &count, n - 1 - i, 0, n, budget, page_tokens, ranges, n_ranges);
+    if (st == ORC_OK) *n_out = emit_kept(kept, n, out);
+    free(kept);
+    return st;
+}
+
+/* KvMemStore::pick_scored_blocks (kvmem_store.cpp:418-451) with media      */
+/* groups and every page a candidate (so every group is complete): the      */
+/* mandatory pages' groups are required, then pages in (score desc, id by   */
+/* tie rule) order each keep their whole group when it fits, else nothing.  */
+int orc_pick_scored_grouped(const double *scores, uint32_t n, const uint32_t *mandatory, uint32_t n_mandatory,
+                            uint32_t budget, int tie_rule, int signed_scores, const uint32_t *ranges,
+                            uint32_t n_ranges, uint32_t page_tokens, uint32_t *out, uint32_t *n_out) {
+    *n_out = 0;
+    if (!budget || !page_tokens || (n && !scores)) return ORC_ERR_ARG;
+    for (uint32_t i = 0; i < n; ++i)
+        if (!isfinite(scores[i]) || (!signed_scores && scores[i] < 0)) return ORC_ERR_ARG;
+    uint8_t *kept = (uint8_t *)calloc(n ? n : 1, 1);
+    uint32_t count = 0;
+    int st = ORC_OK;
+    for (uint32_t i = 0; st == ORC_OK && i < n_mandatory; ++i)
+        st = keep_group(kept, &count, mandatory[i], 1, n, budget, page_tokens, ranges, n_ranges);
+    uint32_t *ids = (uint32_t *)malloc(sizeof(uint32_t) * (n ? n : 1));
+    uint32_t *tmp = (uint32_t *)malloc(sizeof(uint32_t) * (n ? n : 1));
+    for (uint32_t i = 0; i < n; ++i) ids[i] = i;
+    rank_sort(ids, tmp, n, scores, tie_rule);
+    for (uint32_t i = 0; st == ORC_OK && i < n; ++i)
+        st = keep_group(kept, &count, ids[i], 0, n, budget, page_tokens, ranges, n_ranges);
+    if (st == ORC_OK) *n_out = emit_kept(kept, n, out);
+    free(kept); free(ids); free(tmp);
+    return st;
+}
+
+/* KvMemStore::pick_topk_ungrouped (kvmem_store.cpp:578-723), TopK policy:  */
+/* every page when the budget is 0 or covers them all; else, while pages    */
+/* remain in the budget, the sink pages, the mandatory pages last to first  */
+/* and the newest `recent` pages newest first; then the best remaining      */
+/* pages by (score desc, higher id first) fill the budget.                  */
+int orc_pick_topk_ungrouped(const double *scores, uint32_t n, uint32_t budget, uint32_t sink, uint32_t recent,
+                            const uint32_t *mandatory, uint32_t n_mandatory, uint32_t *out, uint32_t *n_out) {
+    *n_out = 0;
+    if (!n) return ORC_OK;
+    if (!budget || n <= budget) {
+        for (uint32_t i = 0; i < n; ++i) out[i] = i;
+        *n_out = n;
+        return ORC_OK;
+    }
+    uint8_t *kept = (uint8_t *)calloc(n, 1);
+    uint32_t count = 0;
+#define ORC_KEEP(id) do { const uint32_t k_ = (id); if (k_ < n && !kept[k_]) { kept[k_] = 1; ++count; } } while (0)
+    for (uint32_t i = 0; i < (sink < n ? sink : n) && count < budget; ++i) ORC_KEEP(i);
+    for (uint32_t i = n_mandatory; i > 0 && count < budget; --i) ORC_KEEP(mandatory[i - 1]);
+    for (uint32_t i = 0; i < (recent < n ? recent : n) && count < budget; ++i) ORC_KEEP(n - 1 - i);
+    if (count < budget) {
+        uint32_t *ids = (uint32_t *)malloc(sizeof(uint32_t) * n);
+        uint32_t *tmp = (uint32_t *)malloc(sizeof(uint32_t) * n);
+        uint32_t m = 0;
+        for (uint32_t i = 0; i < n; ++i)
+            if (!kept[i]) ids[m++] = i;
+        rank_sort(ids, tmp, m, scores, ORC_TIE_HIGHER_FIRST);
+        const uint32_t need = budget - count;
+        for (uint32_t i = 0; i < m && i < need; ++i) ORC_KEEP(ids[i]);
+        free(ids); free(tmp);
+    }
+#undef ORC_KEEP
+    *n_out = emit_kept(kept, n, out);
+    free(kept);
+    return ORC_OK;
+}
+
+/* KvMemStore::constrain_media (kvmem_store.cpp:453-502) with recency off   */
+/* (the pick_topk_blocks pass, :377-379): media ranges merge in list order  */
+/* into page groups (a range starting before the last group's end extends   */
+/* it); the sink pages and the last group are required, the mandatory pages */
+/* newest first, then `selected` and then every other page, each in (score  */
+/* desc, higher id first) order, keep their whole group when it fits.       */
+int orc_constrain_media(const uint32_t *selected, uint32_t n_selected, const double *scores, uint32_t n,
+                        uint32_t budget, uint32_t sink, const uint32_t *ranges, uint32_t n_ranges,
+                        uint64_t total_tokens, uint32_t page_tokens, const uint32_t *mandatory,
+                        uint32_t n_mandatory, uint32_t *out, uint32_t *n_out) {
+    *n_out = 0;
+    if (!page_tokens) return ORC_ERR_ARG;
+    if (!n_ranges || n <= budget || budget == 0) {
+        memcpy(out, selected, sizeof(uint32_t) * n_selected);
+        *n_out = n_selected;
+        return ORC_OK;
+    }
+    uint32_t *gb = (uint32_t *)malloc(sizeof(uint32_t) * (n_ranges + 1));
+    uint32_t *ge = (uint32_t *)malloc(sizeof(uint32_t) * (n_ranges + 1));
+    uint32_t ng = 0;
+    for (uint32_t r = 0; r < n_ranges; ++r) {
+        const uint32_t first_tok = ranges[2 * r], end_tok = ranges[2 * r + 1];
+        if (first_tok >= total_tokens || end_tok <= first_tok) continue;
+        const uint32_t first = first_tok / page_tokens;
+        const uint32_t up = (end_tok + page_tokens - 1) / page_tokens;
+        const uint32_t end = up < n ? up : n;
+        if (ng && first < ge[ng - 1]) { if (end > ge[ng - 1]) ge[ng - 1] = end; }
+        else { gb[ng] = first; ge[ng] = end; ++ng; }
+    }
+    uint32_t *lo = (uint32_t *)malloc(sizeof(uint32_t) * n), *hi = (uint32_t *)malloc(sizeof(uint32_t) * n);
+    for (uint32_t i = 0; i < n; ++i) { lo[i] = i; hi[i] = i + 1; }
+    for (uint32_t g = 0; g < ng; ++g)
+        for (uint32_t i = gb[g]; i < ge[g]; ++i) { lo[i] = gb[g]; hi[i] = ge[g]; }
+    uint8_t *kept = (uint8_t *)calloc(n, 1);
+    uint32_t count = 0;
+    int st = ORC_OK;
+#define ORC_KEEP(id, required) do { const uint32_t k_ = (id); if (st == ORC_OK && k_ < n) { uint32_t need_ = 0; \
+        for (uint32_t i_ = lo[k_]; i_ < hi[k_]; ++i_) need_ += !kept[i_]; \
+        if (count + need_ > budget) { if (required) st = ORC_ERR_BUDGET; } \
+        else { for (uint32_t i_ = lo[k_]; i_ < hi[k_]; ++i_) kept[i_] = 1; count += need_; } } } while (0)
+    for (uint32_t i = 0; i < (n < sink ? n : sink); ++i) ORC_KEEP(i, 1);
+    if (ng) ORC_KEEP(gb[ng - 1], 1);
+    uint32_t *newest = (uint32_t *)malloc(sizeof(uint32_t) * (n_mandatory ? n_mandatory : 1));
+    memcpy(newest, mandatory, sizeof(uint32_t) * n_mandatory);
+    for (uint32_t i = 1; i < n_mandatory; ++i)  /* sort descending */
+        for (uint32_t j = i; j > 0 && newest[j - 1] < newest[j]; --j) {
+            const uint32_t t = newest[j]; newest[j] = newest[j - 1]; newest[j - 1] = t;
+        }
+    for (uint32_t i = 0; i < n_mandatory; ++i) ORC_KEEP(newest[i], 0);
+    uint32_t *ids = (uint32_t *)malloc(sizeof(uint32_t) * (n + n_selected + 1));
+    uint32_t *tmp = (uint32_t *)malloc(sizeof(uint32_t) * (n + n_selected + 1));
+    memcpy(ids, selected, sizeof(uint32_t) * n_selected);
+    rank_sort(ids, tmp, n_selected, scores, ORC_TIE_HIGHER_FIRST);
+    for (uint32_t i = 0; i < n_selected; ++i) ORC_KEEP(ids[i], 0);
+    uint32_t m = 0;
+    for (uint32_t i = 0; i < n; ++i)
+        if (!kept[i]) ids[m++] = i;
+    rank_sort(ids, tmp, m, scores, ORC_TIE_HIGHER_FIRST);
+    for (uint32_t i = 0; i < m; ++i) ORC_KEEP(ids[i], 0);
+#undef ORC_KEEP
+    if (st == ORC_OK) *n_out = emit_kept(kept, n, out);
+    free(gb); free(ge); free(lo); free(hi); free(kept); free(newest); free(ids); free(tmp);
+    return st;
+}
+
+/* ---------------------------------------------------------------------- */
 /* Gather: the selected pages' token rows, ascending page order, into       */
 /* consecutive slot rows: slot i holds page selected[i] at rows             */
 /* [i*page_tokens, i*page_tokens + valid).  Rows past a short last page are */

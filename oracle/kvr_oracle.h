@@ -21,6 +21,14 @@
  *                                    closed form on a two-page example
  *   orc_pick_scored_blocks           brute force on tiny inputs +
  *                                    layerwise_selection_test.cpp:184-194 ties
+ *   orc_media_group / orc_query_fixed_blocks / orc_pick_scored_grouped /
+ *   orc_pick_topk_ungrouped / orc_constrain_media
+ *                                    the reference's own KvMemStore
+ *                                    (query_fixed_blocks, pick_scored_blocks,
+ *                                    pick_topk_blocks) in oracle/_ref on random
+ *                                    stores with media ranges; kvmem_store_test
+ *                                    known answers; brute-force subset search
+ *                                    on tiny grouped inputs
  *   orc_dequant_q8_0 / orc_quant_q8_0 exact-product closed form, stagein.cu formulas
  *   orc_dequant_q4_1                 closed form y = nib*d + m (ggml q4_1 layout;
  *                                    no reference test holds q4_1 bytes)
@@ -119,6 +127,21 @@ int orc_page_logits(const float *means, const float *query, uint32_t rows,
 int orc_pick_scored_blocks(const double *scores, uint32_t n, const uint32_t *mandatory,
                            uint32_t n_mandatory, uint32_t budget, int tie_rule,
                            int signed_scores, uint32_t *out, uint32_t *n_out);
+
+void orc_media_group(uint32_t id, uint32_t n, uint32_t page_tokens, const uint32_t *ranges,
+                     uint32_t n_ranges, uint32_t *begin, uint32_t *end);
+int orc_query_fixed_blocks(uint32_t n, uint32_t budget, uint32_t sink, uint32_t recent, const uint32_t *ranges,
+                           uint32_t n_ranges, uint64_t total_tokens, uint32_t page_tokens,
+                           const uint32_t *mandatory, uint32_t n_mandatory, uint32_t *out, uint32_t *n_out);
+int orc_pick_scored_grouped(const double *scores, uint32_t n, const uint32_t *mandatory, uint32_t n_mandatory,
+                            uint32_t budget, int tie_rule, int signed_scores, const uint32_t *ranges,
+                            uint32_t n_ranges, uint32_t page_tokens, uint32_t *out, uint32_t *n_out);
+int orc_pick_topk_ungrouped(const double *scores, uint32_t n, uint32_t budget, uint32_t sink, uint32_t recent,
+                            const uint32_t *mandatory, uint32_t n_mandatory, uint32_t *out, uint32_t *n_out);
+int orc_constrain_media(const uint32_t *selected, uint32_t n_selected, const double *scores, uint32_t n,
+                        uint32_t budget, uint32_t sink, const uint32_t *ranges, uint32_t n_ranges,
+                        uint64_t total_tokens, uint32_t page_tokens, const uint32_t *mandatory,
+                        uint32_t n_mandatory, uint32_t *out, uint32_t *n_out);
 
 /* ---- block formats ------------------------------------------------------ */
 void orc_dequant_q8_0(const uint8_t *block, float *y);

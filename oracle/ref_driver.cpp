@@ -10,7 +10,8 @@
 //                                     (kvmem/src/host/raw_kv_store.cpp)
 //   query_score_frame, recall_fp16, page_softmax_scores
 //                                     (kvmem/src/host/graph_recall.cpp)
-//   KvMemStore::pick_scored_blocks    (kvmem/src/host/kvmem_store.cpp)
+//   KvMemStore::pick_scored_blocks, query_fixed_blocks, pick_topk_blocks
+//                                     (kvmem/src/host/kvmem_store.cpp)
 //   layerwise_mean_key_scores         (kvmem/src/host/layerwise_scoring.cpp)
 //   prepare_graph_accept, propagate_query_scores
 //                                     (kvmem/src/host/graph_recall.cpp)
@@ -242,6 +243,77 @@ int ref_pick_scored_blocks(const double* scores, uint32_t n, const uint32_t* man
             store.pick_scored_blocks(candidates, values, pins, budget, signed_scores != 0);
         std::memcpy(out, picked.data(), sizeof(uint32_t) * picked.size());
         *n_out = uint32_t(picked.size());
+    });
+}
+
+}  // extern "C"
+
+namespace {
+// A KvMemStore of ceil(total_tokens / page_tokens) pages, a selection budget
+// of `budget` pages, the given sink/recent bands and media token ranges
+// (ranges[2i], ranges[2i+1]).
+std::unique_ptr<kvmem::KvMemStore> policy_store(uint64_t total_tokens, uint32_t page_tokens, uint32_t budget,
+                                                uint32_t sink, uint32_t recent, const uint32_t* ranges,
+                                                uint32_t n_ranges) {
+    kvmem::KvMemStoreConfig cfg;
+    cfg.block_tokens = page_tokens;
+    cfg.select_budget = budget * page_tokens;
+    cfg.sink_blocks = sink;
+    cfg.recent_blocks = recent;
+    auto store = std::make_unique<kvmem::KvMemStore>(cfg);
+    store->register_append(uint32_t(total_tokens));
+    std::vector<std::pair<uint32_t, uint32_t>> media;
+    for (uint32_t r = 0; r < n_ranges; ++r) media.emplace_back(ranges[2 * r], ranges[2 * r + 1]);
+    store->set_media_ranges(std::move(media));
+    return store;
+}
+
+void copy_out(const std::vector<uint32_t>& v, uint32_t* out, uint32_t* n_out) {
+    std::memcpy(out, v.data(), sizeof(uint32_t) * v.size());
+    *n_out = uint32_t(v.size());
+}
+}  // namespace
+
+extern "C" {
+
+// KvMemStore::query_fixed_blocks of such a store.
+int ref_query_fixed_blocks(uint64_t total_tokens, uint32_t page_tokens, uint32_t budget, uint32_t sink,
+                           uint32_t recent, const uint32_t* ranges, uint32_t n_ranges, const uint32_t* mandatory,
+                           uint32_t n_mandatory, uint32_t* out, uint32_t* n_out) {
+    return guarded([&] {
+        auto store = policy_store(total_tokens, page_tokens, budget, sink, recent, ranges, n_ranges);
+        copy_out(store->query_fixed_blocks(std::vector<uint32_t>(mandatory, mandatory + n_mandatory)), out, n_out);
+    });
+}
+
+// KvMemStore::pick_scored_blocks over every page of such a store (media
+// groups apply).
+int ref_pick_scored_grouped(const double* scores, uint64_t total_tokens, uint32_t page_tokens,
+                            const uint32_t* ranges, uint32_t n_ranges, const uint32_t* mandatory,
+                            uint32_t n_mandatory, uint32_t budget, int signed_scores, uint32_t* out,
+                            uint32_t* n_out) {
+    return guarded([&] {
+        auto store = policy_store(total_tokens, page_tokens, budget, 0, 0, ranges, n_ranges);
+        const uint32_t n = store->block_count();
+        std::vector<uint32_t> candidates(n);
+        std::iota(candidates.begin(), candidates.end(), 0u);
+        copy_out(store->pick_scored_blocks(candidates, std::vector<double>(scores, scores + n),
+                                           std::vector<uint32_t>(mandatory, mandatory + n_mandatory), budget,
+                                           signed_scores != 0),
+                 out, n_out);
+    });
+}
+
+// KvMemStore::pick_topk_blocks(mandatory) of such a store whose pages carry
+// the given selection scores (pick_topk_ungrouped, then constrain_media when
+// media ranges exist).
+int ref_pick_topk_blocks(const double* scores, uint64_t total_tokens, uint32_t page_tokens, uint32_t budget,
+                         uint32_t sink, uint32_t recent, const uint32_t* ranges, uint32_t n_ranges,
+                         const uint32_t* mandatory, uint32_t n_mandatory, uint32_t* out, uint32_t* n_out) {
+    return guarded([&] {
+        auto store = policy_store(total_tokens, page_tokens, budget, sink, recent, ranges, n_ranges);
+        store->set_attn_scores(std::vector<double>(scores, scores + store->block_count()));
+        copy_out(store->pick_topk_blocks(std::vector<uint32_t>(mandatory, mandatory + n_mandatory)), out, n_out);
     });
 }
 

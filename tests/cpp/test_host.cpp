@@ -332,7 +332,7 @@ void pick() {
     require(scorer.pick({-.8, -.2, -.5}, 2, {}, kh::TieRule::HigherFirst, true) == std::vector<uint32_t>({1, 2}),
             "signed order");
     rejects<std::invalid_argument>([&] { scorer.pick({-.8, -.2, -.5}, 2); }, "negative scores accepted");
-    rejects<std::invalid_argument>([&] { scorer.pick({1, 2, 3}, 1, {0, 1}); }, "mandatory over budget accepted");
+    rejects<std::runtime_error>([&] { scorer.pick({1, 2, 3}, 1, {0, 1}); }, "mandatory over budget accepted");
     require(scorer.pick({3, 1, 2}, 10) == std::vector<uint32_t>({0, 1, 2}), "budget above page count");
 }
 
