@@ -178,6 +178,17 @@ typedef struct kvr_plane {
     size_t page_stride;
 } kvr_plane;
 
+/* Half-page scoring (layerwise Mean-K on a grid of half the transport page,
+ * kvmem/src/host/layerwise_selection.cpp:14-75): the summaries are half
+ * pages, one softmax runs over every half, and each transport page's score
+ * is its halves' masses folded. */
+typedef enum kvr_half_fold {
+    KVR_HALF_NONE = 0,  /* summaries are the transport pages                */
+    KVR_HALF_SUM = 1,   /* left + right (layerwise_tile_scores, :60-72)     */
+    KVR_HALF_MAX = 2    /* the larger half (layerwise_max_page_scores,
+                           :24-30, for a Query scored in one call)          */
+} kvr_half_fold;
+
 /* Pages a device selection keeps besides its best-scored ones, all in
  * device memory so that the call can be graph-captured (the lists are read
  * when the selection runs).  Replaces the `mandatory` and media-range
@@ -246,6 +257,15 @@ typedef struct kvr_layer_recall {
                                       `mandatory`); with groups or preferred
                                       pages the selection is its own launch
                                       (pages <= KVR_GROUP_SELECT_PAGES)      */
+    kvr_half_fold half_fold;       /* KVR_HALF_NONE, or the key history's (or
+                                      resident summaries') pages are half
+                                      transport pages: the history holds whole
+                                      transport pages of two summary pages;
+                                      summaries and the softmax cover the
+                                      halves; score_mask, mandatory, policy,
+                                      scores, the selection and the gather
+                                      (2 * page_tokens rows per slot) are per
+                                      transport page                         */
 } kvr_layer_recall;
 
 /* ---- context ------------------------------------------------------------ */
@@ -352,6 +372,16 @@ kvr_status kvr_select_topk(kvr_context *ctx, const double *scores, uint32_t lane
                            uint32_t pages, uint32_t k, const uint32_t *mandatory,
                            uint32_t n_mandatory, kvr_tie_rule tie_rule, int signed_scores,
                            uint32_t *selected, uint32_t *count, void *stream);
+
+/* Half-page masses [lanes][2 * pages] (kvr_score over the half pages, with
+ * `accumulate` over Query tiles) folded into page scores [lanes][pages]:
+ * layerwise_tile_scores' left + right or, at the end of a tiled Query,
+ * layerwise_max_page_scores (kvmem/src/host/layerwise_selection.cpp:24-75).
+ * A negative or non-finite half, or mass on a page outside score_mask
+ * ([pages] or NULL), raises KVR_ERR_SCORES at kvr_check and leaves that
+ * lane's scores unwritten. */
+kvr_status kvr_fold_half_pages(kvr_context *ctx, const double *halves, uint32_t lanes, uint32_t pages,
+                               const uint8_t *score_mask, kvr_half_fold rule, double *scores, void *stream);
 
 /* Rows of at most this many pages per lane take media groups or preferred
  * pages; rows of at most KVR_FIXED_BITMAP_PAGES take fixed pages. */

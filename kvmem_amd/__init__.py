@@ -288,6 +288,11 @@ class Context:
         check(lib().kvr_select_topk(self.handle, _ptr(scores), lanes, pages, k, arr, len(mandatory), tie_rule,
                                     int(signed_scores), _ptr(selected), _ptr(count), stream))
 
+    def fold_half_pages(self, halves, pages, scores, rule, lanes=1, score_mask=None, stream=None) -> None:
+        """kvr_fold_half_pages: [lanes][2*pages] half masses -> [lanes][pages]."""
+        check(lib().kvr_fold_half_pages(self.handle, _ptr(halves), lanes, pages, _ptr(score_mask), rule,
+                                        _ptr(scores), stream))
+
     def select_pages(self, scores, pages, k, selected, count, policy=None, lanes=1, tie_rule=TIE_LOWER_FIRST,
                      signed_scores=False, stream=None) -> None:
         """kvr_select_pages with a make_policy() descriptor (or None)."""
@@ -326,7 +331,7 @@ class Context:
                      pages=0, page_tokens=0, lanes=0, score_mask=None, aggregation=AGG_MEAN,
                      tie_rule=TIE_LOWER_FIRST, mandatory: Sequence[int] = (), planes: Sequence = (),
                      engine=ENGINE_AUTO, force_mfma=0, summary_events=(None, None),
-                     select_end=None, policy=None) -> "_capi.LayerRecall":
+                     select_end=None, policy=None, half_fold=0) -> "_capi.LayerRecall":
         """A kvr_layer_recall descriptor (holding what it points to), for
         callers that issue the same layer many times."""
         d = _capi.LayerRecall()
@@ -347,6 +352,7 @@ class Context:
         d.select_end = select_end
         if policy is not None:
             d.policy = C.pointer(policy)
+        d.half_fold = half_fold
         d._keep = (keys, query, summaries, means, score_mask, scores, selected, count, mand, parr, list(planes),
                    policy)
         return d

@@ -18,6 +18,7 @@ HEADER = os.path.join(ROOT, "include", "kvrecall.h")
 (OK, ERR_INVALID, ERR_NONFINITE, ERR_RANGE, ERR_BUDGET, ERR_WORKSPACE, ERR_HIP, ERR_SCORES, ERR_UNSUPPORTED,
  ERR_GRAPH) = range(10)
 MEDIA_OVERLAP, MEDIA_IN_ORDER = 0, 1
+HALF_NONE, HALF_SUM, HALF_MAX = 0, 1, 2
 GROUP_SELECT_PAGES = 4096
 FIXED_BITMAP_PAGES = 524288
 GRAPH_MAX_PAGES = 8192
@@ -75,7 +76,7 @@ class LayerRecall(C.Structure):
                 ("mandatory", C.POINTER(_u32)), ("n_mandatory", _u32), ("scores", _P),
                 ("selected", _P), ("count", _P), ("planes", C.POINTER(Plane)), ("n_planes", _u32),
                 ("engine", _i), ("force_mfma", _i), ("summary_begin", _P), ("summary_end", _P),
-                ("select_end", _P), ("policy", C.POINTER(PagePolicy))]
+                ("select_end", _P), ("policy", C.POINTER(PagePolicy)), ("half_fold", _i)]
 
 
 class AttentionSample(C.Structure):
@@ -109,6 +110,7 @@ _SIGNATURES = {
     "kvr_summary_finalize": (_i, [_P, _P, _P, _u32, _u32, _P, _P, _P]),
     "kvr_score": (_i, [_P, C.POINTER(Query), _P, _u32, _u32, _P, _i, _u32, _i, _P, _i, _P]),
     "kvr_select_topk": (_i, [_P, _P, _u32, _u32, _u32, C.POINTER(_u32), _u32, _i, _i, _P, _P, _P]),
+    "kvr_fold_half_pages": (_i, [_P, _P, _u32, _u32, _P, _i, _P, _P]),
     "kvr_select_pages": (_i, [_P, _P, _u32, _u32, _u32, C.POINTER(PagePolicy), _i, _i, _P, _P, _P]),
     "kvr_media_page_groups": (_i, [C.POINTER(Media), _u32, _i, C.POINTER(_u32), C.POINTER(_u32)]),
     "kvr_query_fixed_pages": (_i, [_u32, _u32, _u32, _u32, C.POINTER(Media), C.POINTER(_u32), _u32,

@@ -404,6 +404,7 @@ struct ScorePlan {
     double *logits;
     uint16_t *qpack;
     uint32_t *counters;  // per-lane completion counters of the softmax launch
+    uint32_t fold;       // kvr::Fold: the columns are half pages folded in pairs
 };
 
 // Where a call's logits, packed queries and counters live: the context's
@@ -417,6 +418,7 @@ kvr_status plan_score(kvr_context *ctx, const kvr_query *q, uint32_t lanes, uint
                       int force_mfma, hipStream_t stream, ScorePlan &p, const FixedScratch *fixed = nullptr) {
     if (kvr_status s = check_query(q, lanes)) return s;
     if (!pages) return fail(KVR_ERR_INVALID, "no pages to score");
+    p.fold = kvr::kFoldNone;
     p.q = query_args(q);
     p.lanes = lanes;
     p.pages = pages;
@@ -459,6 +461,8 @@ kvr::SelectArgs make_select_args(kvr_context *ctx, const ScorePlan &p, const uin
     sa.mask = mask;
     sa.units = p.rows * (agg == KVR_AGG_MEAN ? p.qheads : p.kvheads);
     sa.counters = p.counters ? p.counters : ctx->counters;
+    sa.fold = p.fold;
+    sa.mask_shift = p.fold ? 1 : 0;
     sa.rows = p.rows;
     sa.qheads = p.qheads;
     sa.kvheads = p.kvheads;
@@ -494,10 +498,14 @@ kvr_status enqueue_probs_and_select(kvr_context *ctx, const ScorePlan &p, const 
     if (pol)
         if (kvr_status st = put_policy(*pol, mand, sa)) return st;
     if (do_select && pol && pol->grouped) {
-        // media groups / preferred pages: the selection is its own launch
+        // media groups / preferred pages: the selection is its own launch,
+        // over the (folded) page scores
         sa.do_select = 0;
         KVR_HIP(kvr::launch_probs(sa, s));
         sa.do_select = 1;
+        sa.pages = kvr::select_pages(sa);
+        sa.fold = kvr::kFoldNone;
+        sa.mask_shift = 0;
         KVR_HIP(kvr::launch_select_groups(sa, s));
         return KVR_OK;
     }
@@ -1162,6 +1170,28 @@ kvr_status select_common(kvr_context *ctx, const double *scores, uint32_t lanes,
 }
 }  // namespace
 
+kvr_status kvr_fold_half_pages(kvr_context *ctx, const double *halves, uint32_t lanes, uint32_t pages,
+                               const uint8_t *score_mask, kvr_half_fold rule, double *scores, void *stream) {
+    if (kvr_status s = check_ctx(ctx)) return s;
+    lanes = lanes ? lanes : 1;
+    if (!halves || !scores || !pages) return fail(KVR_ERR_INVALID, "halves, scores and pages are required");
+    if (rule != KVR_HALF_SUM && rule != KVR_HALF_MAX) return fail(KVR_ERR_INVALID, "unknown half-page fold");
+    if (lanes > 65535) return fail(KVR_ERR_INVALID, "at most 65535 lanes per call");
+    DeviceGuard guard(ctx->device);
+    ++ctx->epoch;
+    kvr::FoldArgs a{};
+    a.halves = halves;
+    a.mask = score_mask;
+    a.lanes = lanes;
+    a.pages = pages;
+    a.rule = rule == KVR_HALF_SUM ? kvr::kFoldSum : kvr::kFoldMax;
+    a.scores = scores;
+    a.status = ctx->status;
+    a.epoch = ctx->epoch;
+    KVR_HIP(kvr::launch_fold_halves(a, stream_or(stream, ctx->sel)));
+    return KVR_OK;
+}
+
 kvr_status kvr_select_topk(kvr_context *ctx, const double *scores, uint32_t lanes, uint32_t pages, uint32_t k,
                            const uint32_t *mandatory, uint32_t n_mandatory, kvr_tie_rule tie_rule,
                            int signed_scores, uint32_t *selected, uint32_t *count, void *stream) {
@@ -1301,7 +1331,9 @@ namespace {
 // One validated layer of recall: everything checked, nothing enqueued.
 struct LayerPlan {
     const kvr_layer_recall *d = nullptr;
-    uint32_t pages = 0, page_tokens = 0, lanes = 1;
+    // pages: summaries (softmax columns); page_tokens: tokens per selected
+    // page (twice the summary grid with half pages); sel_pages: pages selected
+    uint32_t pages = 0, page_tokens = 0, lanes = 1, sel_pages = 0;
     size_t key_ls = 0;
     Mandatory m;
     Policy pol;
@@ -1333,8 +1365,19 @@ kvr_status plan_layer(kvr_context *ctx, const kvr_layer_recall *d, hipStream_t s
         L.lanes = d->lanes ? d->lanes : 1;
     }
     if (kvr_status s = check_summary_out(d->means, d->summaries)) return s;
-    if (kvr_status s = check_mandatory(d->mandatory, d->n_mandatory, L.pages, d->k, L.m)) return s;
-    if (kvr_status s = check_policy(d->policy, L.lanes, L.pages, d->k, L.pol)) return s;
+    if (d->half_fold > KVR_HALF_MAX) return fail(KVR_ERR_INVALID, "unknown half-page fold");
+    L.sel_pages = L.pages;
+    if (d->half_fold) {
+        // layerwise_tile_scores (layerwise_selection.cpp:35-55): two Mean-K
+        // records per sealed transport page
+        const uint64_t tokens = d->keys ? d->keys->tokens : uint64_t(L.pages) * L.page_tokens;
+        if (L.pages % 2 || tokens != uint64_t(L.pages) * L.page_tokens)
+            return fail(KVR_ERR_INVALID, "half-page scores require whole transport pages of two summary pages");
+        L.sel_pages = L.pages / 2;
+        L.page_tokens *= 2;
+    }
+    if (kvr_status s = check_mandatory(d->mandatory, d->n_mandatory, L.sel_pages, d->k, L.m)) return s;
+    if (kvr_status s = check_policy(d->policy, L.lanes, L.sel_pages, d->k, L.pol)) return s;
     if (!L.m.more.empty() && L.pol.p && L.pol.p->n_fixed)
         return fail(KVR_ERR_INVALID, "a host mandatory list longer than %d and a device fixed list cannot be combined",
                     KVR_MAX_INLINE_MANDATORY);
@@ -1346,6 +1389,8 @@ kvr_status plan_layer(kvr_context *ctx, const kvr_layer_recall *d, hipStream_t s
         return fail(KVR_ERR_INVALID, "the DMA stage-in engine reads the selection on the host and cannot be "
                                      "captured; use the kernel engine inside graphs");
     if (kvr_status s = plan_score(ctx, d->query, L.lanes, L.pages, d->force_mfma, ss, L.p, fixed)) return s;
+    L.p.fold = d->half_fold == KVR_HALF_SUM ? kvr::kFoldSum : d->half_fold == KVR_HALF_MAX ? kvr::kFoldMax
+                                                                                        : kvr::kFoldNone;
     if (d->keys && !L.p.mfma && !valu_dim_ok(d->keys->head_dim))
         return fail(KVR_ERR_INVALID, "head_dim %u unsupported by fused scoring", d->keys->head_dim);
     return KVR_OK;
@@ -1467,7 +1512,8 @@ kvr_status enqueue_stack(kvr_context *ctx, std::vector<LayerPlan> &plans, hipStr
     const ScorePlan &p0 = plans[0].p;
     bool fuse = n > 1;
     for (const LayerPlan &L : plans)
-        fuse = fuse && !L.p.mfma && !L.pol.grouped && L.p.lanes == p0.lanes && L.p.pages == p0.pages &&
+        fuse = fuse && !L.p.mfma && !L.pol.grouped && L.p.fold == p0.fold && L.p.lanes == p0.lanes &&
+               L.p.pages == p0.pages &&
                L.p.rows == p0.rows && L.p.qheads == p0.qheads && L.p.kvheads == p0.kvheads && L.p.dim == p0.dim;
     if (!fuse) {
         for (LayerPlan &L : plans)

@@ -89,6 +89,12 @@ struct SelectArgs {
     const uint32_t *preferred;        // [lanes][preferred_stride] or null
     const uint32_t *preferred_count;  // [lanes]
     uint32_t preferred_stride;
+    // half-page scoring: the softmax columns are half pages (pages = 2 x the
+    // selected pages), the score mask is per selected page (column j reads
+    // mask[j >> mask_shift]); the tail folds each pair of half masses into
+    // one page score (kFoldSum: left + right, kFoldMax: the larger)
+    uint32_t fold;
+    uint32_t mask_shift;
     uint32_t *selected;        // [lanes][k]
     uint32_t *count;           // [lanes]
     uint32_t *status;
@@ -101,6 +107,10 @@ struct SelectArgs {
 
 // Softmax units per 256-thread workgroup: one per wave for rows held in
 // registers (up to 1024 pages), the whole workgroup for longer rows.
+enum Fold : uint32_t { kFoldNone = 0, kFoldSum = 1, kFoldMax = 2 };
+// Pages the selection runs over (half-page columns fold in pairs).
+__host__ __device__ inline uint32_t select_pages(const SelectArgs &a) { return a.fold ? a.pages / 2 : a.pages; }
+
 constexpr uint32_t kUnitsPerBlock = 4;
 __host__ __device__ constexpr uint32_t units_per_block(uint32_t pages) { return pages <= 1024 ? kUnitsPerBlock : 1; }
 
@@ -196,6 +206,20 @@ hipError_t launch_gather(const GatherArgs &a, hipStream_t s);
 hipError_t launch_accumulate(const AccumulateArgs &a, hipStream_t s);
 hipError_t launch_finalize(const FinalizeArgs &a, hipStream_t s);
 hipError_t launch_copy_ops(const CopyOp *ops, uint32_t n, hipStream_t s);
+
+// Half-page masses [lanes][2 * pages] -> page scores [lanes][pages]
+// (layerwise_tile_scores' sum, layerwise_max_page_scores' max), with the
+// reference's validation (a negative or non-finite half, or mass on a masked
+// page, raises the scores status and leaves the lane's scores unwritten).
+struct FoldArgs {
+    const double *halves;
+    const uint8_t *mask;   // [pages] or null
+    uint32_t lanes, pages, rule;
+    double *scores;
+    uint32_t *status;
+    uint32_t epoch;
+};
+hipError_t launch_fold_halves(const FoldArgs &a, hipStream_t s);
 
 // ---- static scratch of the no-allocation entry (kvr_scratch.hip) ----------
 // Layout: kScratchCounters per-lane completion counters, then the logits

@@ -627,7 +627,7 @@ __device__ __forceinline__ void unit_terms_regs(const SelectArgs &a, double *lan
     uint8_t mv[NPL];
     if (a.mask) {
 #pragma unroll
-        for (int i = 0; i < NPL; ++i) mv[i] = a.mask[at(i)];
+        for (int i = 0; i < NPL; ++i) mv[i] = a.mask[at(i) >> a.mask_shift];
     } else {
 #pragma unroll
         for (int i = 0; i < NPL; ++i) mv[i] = 1;
@@ -740,7 +740,7 @@ __device__ __forceinline__ void unit_terms_loop(const SelectArgs &a, double *lan
                 for (int i = 0; i < T; ++i) {
                     const uint32_t j = min(base + l + i * S, n - 1);
                     x[i] = own || a.summaries ? load_device(row + j) : row[j];
-                    mk[i] = a.mask[j];
+                    mk[i] = a.mask[j >> a.mask_shift];
                 }
 #pragma unroll
                 for (int i = 0; i < T; ++i) on[i] = mk[i] != 0;
@@ -947,10 +947,10 @@ __device__ __forceinline__ void tie_window(const SelectArgs &a, uint32_t remaini
 // Selection of one lane by one wave, for up to 16*64 pages.  Lane l owns the
 // id chunk [l*C, l*C + C), C = ceil(pages/64) <= 16, and holds its keys in
 // registers.
-__device__ __forceinline__ void wave_select(const SelectArgs &a, uint32_t lane, bool lds, const double *sc,
+__device__ __forceinline__ void wave_select(const SelectArgs &a, uint32_t lane, uint32_t n, bool lds, const double *sc,
                                             uint32_t *hist, const FixedPages fx, uint32_t n_fixed) {
     constexpr int R = 16;
-    const uint32_t l = threadIdx.x & 63, n = a.pages;
+    const uint32_t l = threadIdx.x & 63;
     const uint32_t C = (n + kWave - 1) / kWave;
     const uint32_t j0 = min(n, l * C), j1 = min(n, j0 + C);
     auto load_key = [&](uint32_t j) -> uint64_t { return lds ? tail_keys[j] : order_key(sc[j]); };
@@ -1042,14 +1042,14 @@ __device__ __forceinline__ void wave_select(const SelectArgs &a, uint32_t lane, 
 // longer than 1024 pages: the same threshold search and compaction as
 // wave_select, with thread t owning the id chunk [t*C, t*C + C),
 // C = ceil(pages/256), keys read 8 at a time from LDS or the scores.
-__device__ __forceinline__ void wg_select(const SelectArgs &a, uint32_t lane, bool lds, const double *sc,
+__device__ __forceinline__ void wg_select(const SelectArgs &a, uint32_t lane, uint32_t n, bool lds, const double *sc,
                                           uint32_t *hist, const FixedPages fx, uint32_t n_fixed) {
     constexpr uint32_t B = 256, W = B / kWave;
     __shared__ uint64_t s_red[2][W];
     __shared__ uint32_t s_ctl[3];
     __shared__ uint32_t s_scan[W];
     const uint32_t tid = threadIdx.x, w = tid / kWave, l = tid % kWave;
-    const uint32_t n = a.pages, C = (n + B - 1) / B;
+    const uint32_t C = (n + B - 1) / B;
     const uint32_t j0 = min(n, tid * C), j1 = min(n, j0 + C);
     auto load_key = [&](uint32_t j) -> uint64_t { return lds ? tail_keys[j] : order_key(sc[j]); };
     // chunks of up to 64 ids (rows up to 16384 pages) keep their fixed
@@ -1488,7 +1488,8 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
     __shared__ uint32_t fixed_small[kTailLdsPages / 32];  // the fixed-page bitmap of short rows
     __shared__ uint32_t s_fixed[4];
     const uint32_t tid = threadIdx.x, B = blockDim.x;
-    const uint32_t n = a.pages;
+    const uint32_t cols = a.pages;         // softmax columns (half pages when folding)
+    const uint32_t n = select_pages(a);    // pages scored and selected
     const bool lds = n <= kTailLdsPages;
     double *sc = a.scores + uint64_t(lane) * n;
     // Fixed pages (the inline list and the device list) go to a bitmap: LDS
@@ -1509,29 +1510,26 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
     };
     if (a.do_aggregate) {
         // Contributing rows in the reference's order: (row, head) for Mean,
-        // (row, kv-head group) for the group rules.  Two pages per pass and
+        // (row, kv-head group) for the group rules.  Two columns per pass and
         // up to 32 rows of loads in flight; the additions stay in order.
         const uint32_t group = a.qheads / a.kvheads;
         const bool mean = a.aggregation == kAggMean;
         const uint32_t nrows = mean ? a.rows * a.qheads : a.rows * a.kvheads;
-        const double *terms = a.logits + uint64_t(lane) * a.rows * a.qheads * n;
+        const double *terms = a.logits + uint64_t(lane) * a.rows * a.qheads * cols;
         auto row_of = [&](uint32_t i) -> uint64_t {
             return mean ? i : uint64_t(i / a.kvheads) * a.qheads + (i % a.kvheads) * group;
         };
-        for (uint32_t j0 = tid; j0 < n; j0 += 2 * B) {
-            const uint32_t j1 = j0 + B;
-            const bool has1 = j1 < n;
-            const uint32_t j1c = has1 ? j1 : j0;  // loads stay unconditional; acc1 is dropped when !has1
-            double acc0 = a.accumulate ? sc[j0] : 0.0;
-            double acc1 = has1 && a.accumulate ? sc[j1] : 0.0;
+        // acc0 += column c0's terms, acc1 += column c1's (c1 is loaded even
+        // when the caller drops acc1: the loads stay unconditional)
+        auto sum_rows = [&](uint32_t c0, uint32_t c1, double &acc0, double &acc1) {
             uint32_t i = 0;
             for (; i + 32 <= nrows; i += 32) {
                 double v0[32], v1[32];
 #pragma unroll
                 for (int u = 0; u < 32; ++u) {
-                    const uint64_t o = row_of(i + u) * n;
-                    v0[u] = load_device(terms + o + j0);
-                    v1[u] = load_device(terms + o + j1c);
+                    const uint64_t o = row_of(i + u) * cols;
+                    v0[u] = load_device(terms + o + c0);
+                    v1[u] = load_device(terms + o + c1);
                 }
 #pragma unroll
                 for (int u = 0; u < 32; ++u) {
@@ -1543,9 +1541,9 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
                 double v0[16], v1[16];
 #pragma unroll
                 for (int u = 0; u < 16; ++u) {
-                    const uint64_t o = row_of(i + u) * n;
-                    v0[u] = load_device(terms + o + j0);
-                    v1[u] = load_device(terms + o + j1c);
+                    const uint64_t o = row_of(i + u) * cols;
+                    v0[u] = load_device(terms + o + c0);
+                    v1[u] = load_device(terms + o + c1);
                 }
 #pragma unroll
                 for (int u = 0; u < 16; ++u) {
@@ -1557,9 +1555,9 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
                 double v0[8], v1[8];
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
-                    const uint64_t o = row_of(i + u) * n;
-                    v0[u] = load_device(terms + o + j0);
-                    v1[u] = load_device(terms + o + j1c);
+                    const uint64_t o = row_of(i + u) * cols;
+                    v0[u] = load_device(terms + o + c0);
+                    v1[u] = load_device(terms + o + c1);
                 }
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
@@ -1568,15 +1566,35 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
                 }
             }
             for (; i < nrows; ++i) {
-                const uint64_t o = row_of(i) * n;
-                acc0 += load_device(terms + o + j0);
-                if (has1) acc1 += load_device(terms + o + j1);
+                const uint64_t o = row_of(i) * cols;
+                acc0 += load_device(terms + o + c0);
+                acc1 += load_device(terms + o + c1);
             }
-            sc[j0] = acc0;
-            note(j0, acc0);
-            if (has1) {
-                sc[j1] = acc1;
-                note(j1, acc1);
+        };
+        if (a.fold) {
+            // a page's two half masses from zero, then folded
+            // (layerwise_selection.cpp:64-72: left + right; :24-30: the max)
+            for (uint32_t j = tid; j < n; j += B) {
+                double left = 0.0, right = 0.0;
+                sum_rows(2 * j, 2 * j + 1, left, right);
+                double v = a.fold == kFoldSum ? left + right : (left < right ? right : left);
+                if (a.accumulate) v = sc[j] + v;
+                sc[j] = v;
+                note(j, v);
+            }
+        } else {
+            for (uint32_t j0 = tid; j0 < n; j0 += 2 * B) {
+                const uint32_t j1 = j0 + B;
+                const bool has1 = j1 < n;
+                double acc0 = a.accumulate ? sc[j0] : 0.0;
+                double acc1 = has1 && a.accumulate ? sc[j1] : 0.0;
+                sum_rows(j0, has1 ? j1 : j0, acc0, acc1);  // acc1 is dropped when !has1
+                sc[j0] = acc0;
+                note(j0, acc0);
+                if (has1) {
+                    sc[j1] = acc1;
+                    note(j1, acc1);
+                }
             }
         }
     } else {
@@ -1618,9 +1636,9 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
     }
     const FixedPages fx{has_fixed ? fbits : nullptr};
     if (wide)
-        wg_select(a, lane, lds, sc, hist, fx, n_fixed);
+        wg_select(a, lane, n, lds, sc, hist, fx, n_fixed);
     else
-        wave_select(a, lane, lds, sc, hist, fx, n_fixed);
+        wave_select(a, lane, n, lds, sc, hist, fx, n_fixed);
 }
 
 // Softmax units -> terms; the lane's last workgroup aggregates (+ selects).
@@ -1912,6 +1930,28 @@ __global__ __launch_bounds__(256) void k_stack_group(StackGroupArgs g) {
 
 // Selection over given scores (no softmax), one workgroup per lane.
 __global__ __launch_bounds__(256) void k_select(SelectArgs a) { lane_tail(a, blockIdx.x); }
+
+// Half-page masses folded into page scores, one lane per workgroup row of
+// the grid (y); invalid halves make the lane's scores unwritten.
+__global__ __launch_bounds__(256) void k_fold_halves(FoldArgs a) {
+    const uint32_t lane = blockIdx.x;
+    const double *h = a.halves + uint64_t(lane) * 2 * a.pages;
+    double *out = a.scores + uint64_t(lane) * a.pages;
+    int bad = 0;
+    for (uint32_t j = threadIdx.x; j < a.pages; j += 256) {
+        const double left = h[2 * j], right = h[2 * j + 1], sum = left + right;
+        bad |= left < 0.0 || right < 0.0 || !__builtin_isfinite(sum) || (a.mask && !a.mask[j] && sum != 0.0);
+    }
+    bad = __syncthreads_or(bad);
+    if (bad) {
+        if (threadIdx.x == 0) raise_status(a.status, kStatusScores, a.epoch);
+        return;
+    }
+    for (uint32_t j = threadIdx.x; j < a.pages; j += 256) {
+        const double left = h[2 * j], right = h[2 * j + 1];
+        out[j] = a.rule == kFoldSum ? left + right : (left < right ? right : left);
+    }
+}
 
 // ---------------------------------------------------------------------------
 // Selection with media groups: KvMemStore::pick_scored_blocks with media
@@ -2617,8 +2657,9 @@ hipError_t launch_logits_mfma(const MfmaLogitsArgs &a, hipStream_t s) {
 // Dynamic LDS of a selection tail: the keys of rows up to kTailLdsPages
 // pages; for longer rows with fixed pages, their bitmap.
 inline size_t tail_lds_bytes(const SelectArgs &a) {
-    if (a.pages <= kTailLdsPages) return size_t(a.pages) * 8;
-    return a.do_select && (a.n_mandatory || a.n_fixed) ? size_t((a.pages + 31) / 32) * 4 : 0;
+    const uint32_t n = select_pages(a);
+    if (n <= kTailLdsPages) return size_t(n) * 8;
+    return a.do_select && (a.n_mandatory || a.n_fixed) ? size_t((n + 31) / 32) * 4 : 0;
 }
 
 hipError_t launch_probs(const SelectArgs &a, hipStream_t s) {
@@ -2677,6 +2718,12 @@ hipError_t launch_stack_group(int source, StackGroupArgs g, hipStream_t s) {
 hipError_t launch_select(const SelectArgs &a, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch\'s error
     hipLaunchKernelGGL(k_select, dim3(a.lanes), dim3(256), tail_lds_bytes(a), s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_fold_halves(const FoldArgs &a, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch\'s error
+    hipLaunchKernelGGL(k_fold_halves, dim3(a.lanes), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -52,6 +52,7 @@ def _load_oracle() -> C.CDLL:
                                               C.c_float, C.c_int, _P]),
         "orc_page_logits": (C.c_int, [_P, _P, _u32, _u32, _u32, _u32, _u32, C.c_float, _P]),
         "orc_pick_scored_blocks": (C.c_int, [_P, _u32, _P, _u32, _u32, C.c_int, C.c_int, _P, _P]),
+        "orc_layerwise_fold": (C.c_int, [_P, _u32, _P, C.c_int, _P]),
         "orc_media_group": (None, [_u32, _u32, _u32, _P, _u32, _P, _P]),
         "orc_query_fixed_blocks": (C.c_int, [_u32, _u32, _u32, _u32, _P, _u32, _u64, _u32, _P, _u32, _P, _P]),
         "orc_pick_scored_grouped": (C.c_int, [_P, _u32, _P, _u32, _u32, C.c_int, C.c_int, _P, _u32, _u32, _P, _P]),
@@ -113,6 +114,8 @@ def _load_ref() -> Optional[C.CDLL]:
         "ref_layerwise_scores_f16_keys": (C.c_int, [_P, _u32, _u32, _u64, _u32, _u32, _u32, _P,
                                                     _u32, _u32, C.c_float, _P]),
         "ref_pick_scored_blocks": (C.c_int, [_P, _u32, _P, _u32, _u32, C.c_int, _P, _P]),
+        "ref_layerwise_tile_scores_f16_keys": (C.c_int, [_P, _u32, _u32, _u64, _u32, _u32, _u32, _u32, _P, _u32,
+                                                         _u32, C.c_float, C.c_int, _P, _P]),
         "ref_query_fixed_blocks": (C.c_int, [_u64, _u32, _u32, _u32, _u32, _P, _u32, _P, _u32, _P, _P]),
         "ref_pick_scored_grouped": (C.c_int, [_P, _u64, _u32, _P, _u32, _P, _u32, _u32, C.c_int, _P, _P]),
         "ref_pick_topk_blocks": (C.c_int, [_P, _u64, _u32, _u32, _u32, _u32, _P, _u32, _P, _u32, _P, _P]),
@@ -229,6 +232,49 @@ def pick_scored_blocks(scores: np.ndarray, budget: int, mandatory: Sequence[int]
     _check(lib.orc_pick_scored_blocks(_ptr(scores), n, _ptr(pins), len(mandatory), budget,
                                       tie_rule, int(signed_scores), _ptr(out), C.byref(n_out)))
     return out[: n_out.value].copy()
+
+
+# ---- half-page layerwise scores ------------------------------------------------
+
+def layerwise_fold(mass: np.ndarray, score_mask: Optional[np.ndarray] = None, keep_halves: bool = False) -> np.ndarray:
+    """layerwise_tile_scores' fold of 2*count half masses (left + right), or
+    layerwise_max_page_scores (the larger half)."""
+    mass = _c(mass, np.float64)
+    count = mass.shape[0] // 2
+    out = np.zeros(max(count, 1), np.float64)
+    mask = None if score_mask is None else _c(score_mask, np.uint8)
+    _check(lib.orc_layerwise_fold(_ptr(mass), count, _ptr(mask), int(keep_halves), _ptr(out)))
+    return out[:count].copy()
+
+
+def half_page_scores(keys: np.ndarray, tokens: int, width: int, mean_tokens: int, query: np.ndarray,
+                     query_heads: int, kv_heads: int, head_dim: int, keep_halves: bool = False,
+                     score_mask: Optional[np.ndarray] = None, scale: float = 0.0) -> np.ndarray:
+    """One layer's transport-page scores from Mean-K records every
+    mean_tokens tokens: the softmax over every half page, then the fold.
+    query [rows][Hq][D] float32."""
+    _, means = page_summaries(keys, FMT_F16 if keys.dtype == np.uint16 else FMT_Q8_0, tokens, width, mean_tokens)
+    pages = means.shape[0] // 2
+    mask2 = None if score_mask is None else np.repeat(np.asarray(score_mask, np.uint8), 2)
+    q = np.asarray(query, np.float32)
+    mass = page_softmax_scores(means[None], q[None], [q.shape[0]], query_heads, kv_heads, head_dim, AGG_MEAN,
+                               mask2, scale)
+    return layerwise_fold(mass, score_mask, keep_halves)
+
+
+def ref_layerwise_tile_scores_f16_keys(keys: np.ndarray, layer: int, tokens: int, kv_heads: int, head_dim: int,
+                                       mean_tokens: int, page_tokens: int, query: np.ndarray, query_heads: int,
+                                       keep_halves: bool = False, score_mask: Optional[np.ndarray] = None,
+                                       scale: float = 0.0) -> np.ndarray:
+    keys = _c(keys, np.uint16)
+    query = _c(query, np.float32)
+    pages = (tokens + page_tokens - 1) // page_tokens
+    out = np.zeros(pages, np.float64)
+    mask = None if score_mask is None else _c(score_mask, np.uint8)
+    _ref_check(ref.ref_layerwise_tile_scores_f16_keys(_ptr(keys), keys.shape[0], layer, tokens, kv_heads, head_dim,
+                                                      mean_tokens, page_tokens, _ptr(query), query.shape[0],
+                                                      query_heads, scale, int(keep_halves), _ptr(mask), _ptr(out)))
+    return out
 
 
 # ---- page policies (media groups, fixed pages) --------------------------------

@@ -399,6 +399,28 @@ int orc_pick_scored_blocks(const double *scores, uint32_t n, const uint32_t *man
 }
 
 /* ---------------------------------------------------------------------- */
+/* Half-page layerwise scores: layerwise_tile_scores' fold                  */
+/* (layerwise_selection.cpp:60-72) and layerwise_max_page_scores (:24-30).  */
+/* mass holds 2*count half-page masses in page order (the softmax over the  */
+/* halves frame); a negative half, a non-finite pair sum or mass on a page  */
+/* outside score_mask is invalid.  keep_halves 0: out[i] = left + right;    */
+/* 1: out[i] = std::max(left, right), i.e. right when left < right.         */
+/* ---------------------------------------------------------------------- */
+int orc_layerwise_fold(const double *mass, uint32_t count, const uint8_t *score_mask, int keep_halves,
+                       double *out) {
+    for (uint32_t i = 0; i < count; ++i) {
+        const double left = mass[2 * i], right = mass[2 * i + 1], sum = left + right;
+        if (left < 0 || right < 0 || !isfinite(sum) || (score_mask && !score_mask[i] && sum != 0))
+            return ORC_ERR_ARG;
+    }
+    for (uint32_t i = 0; i < count; ++i) {
+        const double left = mass[2 * i], right = mass[2 * i + 1];
+        out[i] = keep_halves ? (left < right ? right : left) : left + right;
+    }
+    return ORC_OK;
+}
+
+/* ---------------------------------------------------------------------- */
 /* Page policies around the scored pick (kvmem_store.cpp).  Media ranges    */
 /* are token ranges [first, end), ranges[2*i], ranges[2*i+1].               */
 /* ---------------------------------------------------------------------- */

@@ -21,6 +21,11 @@
  *                                    closed form on a two-page example
  *   orc_pick_scored_blocks           brute force on tiny inputs +
  *                                    layerwise_selection_test.cpp:184-194 ties
+ *   orc_layerwise_fold               layerwise_selection_test.cpp:104-160
+ *                                    known answers (short evidence kept by
+ *                                    half pages; strongest half after the
+ *                                    whole Query); the reference's own
+ *                                    layerwise_tile_scores in oracle/_ref
  *   orc_media_group / orc_query_fixed_blocks / orc_pick_scored_grouped /
  *   orc_pick_topk_ungrouped / orc_constrain_media
  *                                    the reference's own KvMemStore
@@ -128,6 +133,8 @@ int orc_pick_scored_blocks(const double *scores, uint32_t n, const uint32_t *man
                            uint32_t n_mandatory, uint32_t budget, int tie_rule,
                            int signed_scores, uint32_t *out, uint32_t *n_out);
 
+int orc_layerwise_fold(const double *mass, uint32_t count, const uint8_t *score_mask, int keep_halves,
+                       double *out);
 void orc_media_group(uint32_t id, uint32_t n, uint32_t page_tokens, const uint32_t *ranges,
                      uint32_t n_ranges, uint32_t *begin, uint32_t *end);
 int orc_query_fixed_blocks(uint32_t n, uint32_t budget, uint32_t sink, uint32_t recent, const uint32_t *ranges,

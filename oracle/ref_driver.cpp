@@ -21,6 +21,7 @@
 #include "kvmem/graph_recall.hpp"
 #include "kvmem/kvmem_store.hpp"
 #include "kvmem/layerwise_scoring.hpp"
+#include "kvmem/layerwise_selection.hpp"
 #include "kvmem/lrfu.hpp"
 #include "kvmem/raw_kv_store.hpp"
 
@@ -219,6 +220,38 @@ int ref_layerwise_scores_f16_keys(const uint16_t* keys, uint32_t layers, uint32_
         q.attention_scale = scale;
         const auto result = kvmem::layerwise_mean_key_scores(*store, q, frame);
         std::memcpy(scores, result.data(), sizeof(double) * result.size());
+    });
+}
+
+// Half-page current-Q Mean scores: layerwise_tile_scores over transport
+// pages of page_tokens with Mean-K records every mean_tokens tokens of the
+// given fp16 keys, then (keep_halves) layerwise_max_page_scores.  score_mask
+// is per transport page (NULL: every page).  out: one score per page.
+int ref_layerwise_tile_scores_f16_keys(const uint16_t* keys, uint32_t layers, uint32_t layer, uint64_t tokens,
+                                       uint32_t kv_heads, uint32_t head_dim, uint32_t mean_tokens,
+                                       uint32_t page_tokens, const float* query, uint32_t rows,
+                                       uint32_t query_heads, float scale, int keep_halves,
+                                       const uint8_t* score_mask, double* out) {
+    return guarded([&] {
+        auto store = store_from_f16(keys, layers, tokens, kv_heads * head_dim, mean_tokens);
+        const uint32_t pages = uint32_t((tokens + page_tokens - 1) / page_tokens);
+        auto frame = kvmem::query_score_frame(tokens, page_tokens, pages, 0, 0, {});
+        if (score_mask)
+            for (uint32_t j = 0; j < pages; ++j) frame.score_mask[j] = score_mask[j];
+        kvmem::CurrentLayerQuery q;
+        q.data = query;
+        q.layer = layer;
+        q.rows = rows;
+        q.query_heads = query_heads;
+        q.kv_heads = kv_heads;
+        q.head_dim = head_dim;
+        q.attention_scale = scale;
+        auto result = kvmem::layerwise_tile_scores(frame, page_tokens, mean_tokens, keep_halves != 0,
+                                                   [&](const kvmem::QueryScoreFrame& f) {
+                                                       return kvmem::layerwise_mean_key_scores(*store, q, f);
+                                                   });
+        if (keep_halves) result = kvmem::layerwise_max_page_scores(result);
+        std::memcpy(out, result.data(), sizeof(double) * result.size());
     });
 }
 
