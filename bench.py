@@ -374,12 +374,15 @@ def pmc_pass(args):
 
 # ---------------------------------------------------------------------------
 # The other workloads (--workload).  Each prints one JSON line of the same
-# shape: value = scored-KV GB/s of the select stack, plus the per-layer
-# select latency, select+stage-in pipelined latency and stage-in GB/s.
+# shape: value = scored-KV GB/s of the select stack, the per-layer select
+# latency, select+stage-in pipelined latency and stage-in GB/s, the roofline
+# of the dominant launch, the reference's CPU select path on a bounded sample
+# and a parity check of every layer's (lane's) selection against the oracle.
 WORKLOADS = {
-    # one 32768-token layer, K = N(0,1) x per-channel U(0.5, 2), Max, top-16
-    "single32k": dict(layers=1, repeat=64, lanes=1, T=32768, HQ=32, HKV=8, D=128, PT=256, R=1, K=16,
-                      agg="max", kfmt="f16_scaled", vfmt="f16", kmode="copy", vmode="copy", resident=False),
+    # 64 distinct 32768-token layers (4 GiB of K: HBM, not the 256 MB cache),
+    # K = N(0,1) x per-channel U(0.5, 2), Max, top-16
+    "single32k": dict(layers=64, repeat=1, lanes=1, T=32768, HQ=32, HKV=8, D=128, PT=256, R=1, K=16,
+                      agg="max", kfmt="f16_scaled", vfmt="f16", kmode="copy", vmode="copy", resident=False, ring=8),
     # q8_0 K (scores from dequantized K) + q4_1-layout V, dequantized on gather
     "k8v4": dict(layers=16, repeat=1, lanes=1, T=131072, HQ=32, HKV=8, D=128, PT=256, R=1, K=32,
                  agg="mean", kfmt="q8_0", vfmt="q4_1", kmode="dequant", vmode="dequant", resident=False),
@@ -398,12 +401,78 @@ WORKLOADS = {
 }
 
 
+def _q8_rows_f32(raw: np.ndarray, width: int) -> np.ndarray:
+    """q8_0 token rows -> binary32 rows (code * d, exact)."""
+    blk = raw.reshape(-1, 34)
+    d = blk[:, :2].copy().view(np.float16).astype(np.float32)
+    return (blk[:, 2:].view(np.int8).astype(np.float32) * d).reshape(-1, width)
+
+
+def workload_checks(args, w, name, host_units, gpu_sel, gpu_scores, tie, scored_unit_bytes):
+    """Parity of every unit (layer or lane) against the oracle, and the
+    reference's own CPU select path on a bounded sample of units.
+    host_units: callables returning (kind, data, query) per unit, where kind
+    is 'f16' (uint16 keys), 'q8_0' (raw bytes) or 'summaries' (fp16)."""
+    import oracle as O
+    T, HQ, HKV, D, PT, R, KSEL = w["T"], w["HQ"], w["HKV"], w["D"], w["PT"], w["R"], w["K"]
+    W = HKV * D
+    agg = {"mean": O.AGG_MEAN, "max": O.AGG_MAX}[w["agg"]]
+    equal, worst = True, 0.0
+    ref_kind = "reference" if O.ref_available() else "port"
+    cpu_times, ref_match = [], True
+    t_start = time.perf_counter()
+    for u, fetch in enumerate(host_units):
+        kind, data, q = fetch()
+        q4 = q.reshape(1, R, HQ, D)
+        if kind == "summaries":
+            means = data.view(np.float16).astype(np.float32).reshape(1, -1, W)
+        else:
+            _, m = O.page_summaries(data, O.FMT_F16 if kind == "f16" else O.FMT_Q8_0, T, W, PT)
+            means = m[None]
+        want = O.page_softmax_scores(means, q4, [R], HQ, HKV, D, agg)
+        worst = max(worst, float(np.max(np.abs(gpu_scores[u] - want) / np.maximum(want, 1e-300))))
+        equal &= bool(np.array_equal(gpu_sel[u], O.pick_scored_blocks(want, KSEL, (), tie)))
+        if args.no_cpu or (cpu_times and time.perf_counter() - t_start > args.cpu_seconds):
+            continue
+        # the reference's select path: capture, mean-K, page softmax, pick
+        c0 = time.perf_counter()
+        if ref_kind == "reference":
+            if kind == "f16":
+                _, sc = O.ref_scores_f16_keys(data.reshape(1, T, W), T, HKV, D, PT, q4, [R], HQ, agg)
+            elif kind == "q8_0":
+                _, sc = O.ref_scores_f32_keys(_q8_rows_f32(data, W)[None], T, HKV, D, PT, q4, [R], HQ, agg)
+            else:
+                sc = O.ref_scores_from_sums(means * np.float32(PT), HKV, D, PT, q4, [R], HQ, agg)
+            pick = O.ref_pick_scored_blocks(sc, KSEL)
+        else:
+            sc, pick = want, O.pick_scored_blocks(want, KSEL, (), O.TIE_HIGHER_FIRST)
+        cpu_times.append(time.perf_counter() - c0)
+        ref_match &= bool(np.array_equal(pick, gpu_sel[u]))
+    parity = {"units_checked": len(host_units), "selections_equal": equal, "max_rel_score_diff": worst,
+              "oracle": "oracle/kvr_oracle.c summaries + page softmax + pick with the GPU's tie rule"}
+    cpu = None
+    if cpu_times:
+        per = float(np.mean(cpu_times))
+        src = {"f16": "fp16 K capture (write_layer_tokens_f16)", "q8_0": "dequantized q8_0 K capture "
+               "(write_layer_mean_k)", "summaries": "resident page sums (write_layer_mean_sum)"}[kind]
+        cpu = {"value": round(scored_unit_bytes / per / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": ref_kind,
+               "sample": f"{len(cpu_times)} of {len(host_units)} {name}s, select path ({src} + mean_k + "
+                         f"page_softmax_scores + pick_scored_blocks), {per * 1e3:.1f} ms each, single thread",
+               "select_us_per_unit": round(per * 1e6, 1), "selection_matches_gpu": ref_match,
+               "host_cpu": _cpu_model(), "host_cores": os.cpu_count()}
+    return parity, cpu
+
+
 def run_workload(args):
     import torch
     import kvmem_amd as K
     from kvmem_amd.hip import runtime
 
-    w = WORKLOADS[args.workload]
+    w = dict(WORKLOADS[args.workload])
+    if args.pmc_pass:  # a short stack: three launches of distinct layers
+        w["layers"] = min(w["layers"], 2 * K._capi.STACK_GROUP) if w["lanes"] == 1 else 1
+        w["repeat"] = 1
+        w["ring"] = min(w.get("ring", w["layers"]), w["layers"])
     hip = runtime()
     ctx = K.Context(0)
     ctx.set_option(K._capi.OPT_GATHER_WORKGROUPS, args.gather_wgs)
@@ -411,6 +480,7 @@ def run_workload(args):
     ctx.set_option(K._capi.OPT_GATHER_THREADS, args.gather_threads)
     L, NL, T, HQ, HKV, D, PT, R, KSEL = w["layers"], w["lanes"], w["T"], w["HQ"], w["HKV"], w["D"], w["PT"], \
         w["R"], w["K"]
+    G = K._capi.STACK_GROUP
     W, P = HKV * D, T // PT
     ring = w.get("ring", L)
     fmt = {"f16": K.FMT_F16, "f16_scaled": K.FMT_F16, "q8_0": K.FMT_Q8_0, "q4_1": K.FMT_Q4_1}
@@ -421,6 +491,7 @@ def run_workload(args):
     theta = torch.from_numpy((10000.0 ** (-np.arange(D // 2) * 2 / D)).astype(np.float32)).cuda()
     rope = dict(head_dim=D, n_rot=D, theta=theta, fwht=128, pos_base=0) if w["kmode"] == "rope_fwht" else None
     agg = {"mean": K.AGG_MEAN, "max": K.AGG_MAX}[w["agg"]]
+    tie = K.TIE_LOWER_FIRST
     seed = args.seed
     log(f"workload {args.workload}: {L} layer(s) x {NL} lane(s) x {T} tokens, Hq {HQ}/Hkv {HKV}, D {D}, "
         f"page {PT} ({P} pages), {R} query row(s), top-{KSEL}, K {w['kfmt']}, V {w['vfmt']}")
@@ -467,7 +538,7 @@ def run_workload(args):
         for l in range(L):
             t = torch.empty(kb, dtype=torch.uint8, device="cuda")
             torch.cuda.synchronize()
-            synth(w["kfmt"], 1000 + l % ring, lane_rows, t)
+            synth(w["kfmt"], 1000 + l, lane_rows, t)  # distinct K per layer
             dev_k.append(t)
     else:
         s16 = [s16[l % ring].clone() for l in range(L)]
@@ -479,99 +550,183 @@ def run_workload(args):
         qd.append(q)
     if not w["resident"]:
         s16 = [torch.empty(NL * P * W, dtype=torch.int16, device="cuda") for _ in range(L)]
-    scores = [torch.empty(NL * P, dtype=torch.float64, device="cuda") for _ in range(L)]
-    sel = [torch.empty(NL * KSEL, dtype=torch.int32, device="cuda") for _ in range(L)]
-    cnt = [torch.empty(NL, dtype=torch.int32, device="cuda") for _ in range(L)]
+    order = [l for l in range(L) for _ in range(w["repeat"])]
+    N = len(order)  # stack positions (a layer may be scored more than once)
+    scores = [torch.empty(NL * P, dtype=torch.float64, device="cuda") for _ in range(N)]
+    sel = [torch.empty(NL * KSEL, dtype=torch.int32, device="cuda") for _ in range(N)]
+    cnt = [torch.empty(NL, dtype=torch.int32, device="cuda") for _ in range(N)]
     kslots = [torch.empty(NL * KSEL * PT * K.gather_row_bytes(kfmt, mode[w["kmode"]], W), dtype=torch.uint8,
                           device="cuda") for _ in range(L)]
     vslots = [torch.empty(NL * KSEL * PT * K.gather_row_bytes(vfmt, mode[w["vmode"]], W), dtype=torch.uint8,
                           device="cuda") for _ in range(L)]
     torch.cuda.synchronize()
     ctx.check()
-    log(f"inputs ready ({ring} pinned K/V set(s) of {kb >> 20} + {vb >> 20} MiB)")
+    log(f"inputs ready ({L} distinct layer(s); {ring} pinned K/V set(s) of {kb >> 20} + {vb >> 20} MiB)")
 
-    def desc(l, with_planes, ev=(None, None), se=None):
+    def desc(i, with_planes, ev=(None, None), se=None):
+        l = order[i]
         planes = [K.make_plane(pins[l % ring][0], kfmt, W, T, mode[w["kmode"]], kslots[l], rope=rope),
                   K.make_plane(pins[l % ring][1], vfmt, W, T, mode[w["vmode"]], vslots[l])]
         src = dict(keys=None, pages=P, page_tokens=PT, lanes=NL) if w["resident"] else \
             dict(keys=K.make_keys(dev_k[l], kfmt, T, HKV, D, PT, lanes=NL))
         return K.Context.layer_recall(summaries=s16[l], query=K.make_query(qd[l], K.FMT_F16, R, HQ, HKV, D, lanes=NL),
-                                      scores=scores[l], selected=sel[l], count=cnt[l], k=KSEL, aggregation=agg,
-                                      planes=planes if with_planes else (), summary_events=ev, select_end=se,
-                                      **src)
+                                      scores=scores[i], selected=sel[i], count=cnt[i], k=KSEL, aggregation=agg,
+                                      tie_rule=tie, planes=planes if with_planes else (), summary_events=ev,
+                                      select_end=se, **src)
+
+    fused = R * (HQ // HKV) < 16  # vector logits: layers fuse into stack launches of G
+    if args.pmc_pass:
+        keep = ctx.recall_stack([desc(i, False) for i in range(N)])
+        ctx.check()
+        del keep
+        op = 1 << 16
+        cb = 256 << 20
+        src_t = torch.empty(cb, dtype=torch.uint8, device="cuda")
+        dst_t = torch.empty(cb, dtype=torch.uint8, device="cuda")
+        torch.cuda.synchronize()
+        n = cb // op
+        for _ in range(3):
+            ctx.d2d_batched([src_t.data_ptr() + i * op for i in range(n)], [dst_t.data_ptr() + i * op for i in range(n)],
+                            [op] * n)
+            ctx.check()
+        ctx.close()
+        print(json.dumps({"pass": "pmc", "workload": args.workload, "layers": N, "copy_bytes": cb, "copy_ops": n}),
+              flush=True)
+        return
 
     # (a) select latency of one layer: summary start -> selection written
     ev_a, ev_b = hip.event(), hip.event()
     lat = []
     for rep in range(max(3, args.steps)):
-        for l in range(min(L, 4)):
-            ctx.recall(desc(l, False, (ev_a, None), ev_b))
+        for i in range(min(N, 4)):
+            ctx.recall(desc(i, False, (ev_a, None), ev_b))
             ctx.check()
             if rep:
                 lat.append(hip.elapsed_ms(ev_a, ev_b) * 1e3)
     select_us = float(np.median(lat))
-    # (b) timed: the select stack (each layer `repeat` times)
-    order = [l for l in range(L) for _ in range(w["repeat"])]
-    descs = [desc(l, False) for l in order]
+    # (b) timed: the select stack; launch events on sampled inner positions
+    # (steady launches: each beside the previous group's softmax and top-k)
+    sampled = sorted({i for i in (N // 4, N // 2, 3 * N // 4) if (G <= i < N - G) or not fused} or {N // 2})
+    ev_t = [{i: (hip.event(), hip.event()) for i in sampled} for _ in range(args.steps)]
+    d_w = [desc(i, False) for i in range(N)]
+    d_t = [[desc(i, False, e.get(i, (None, None))) for i in range(N)] for e in ev_t]
+    keep = None
     for _ in range(args.warmup):
-        keep = ctx.recall_stack(descs)
+        keep = ctx.recall_stack(d_w)
         ctx.check()
     torch.cuda.synchronize()
+    keeps = []
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        keep = ctx.recall_stack(descs)
+    for s_ in range(args.steps):
+        keeps.append(ctx.recall_stack(d_t[s_]))
     ctx.check()
     torch.cuda.synchronize()
     ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
-    del keep
+    del keep, keeps
+    launch_us = float(np.mean([hip.elapsed_ms(*e[i]) * 1e3 for e in ev_t for i in sampled]))
     k_read = 0 if w["resident"] else lane_rows * row(w["kfmt"])
-    scored_layer = k_read + NL * P * W * 2 + NL * R * HQ * D * 2
-    value = len(order) * scored_layer / (ms_per_step * 1e-3) / 1e9
-    log(f"select {select_us:.1f} us/layer; stack {ms_per_step * 1e3 / len(order):.1f} us/layer = {value:.1f} GB/s")
+    q_bytes = NL * R * HQ * D * 2
+    scored_layer = k_read + NL * P * W * 2 + q_bytes
+    value = N * scored_layer / (ms_per_step * 1e-3) / 1e9
+    log(f"select {select_us:.1f} us/layer; stack {ms_per_step * 1e3 / N:.1f} us/layer = {value:.1f} GB/s; "
+        f"dominant launch {launch_us:.1f} us")
+    # algorithmic bytes of the dominant launch
+    logits = NL * R * HQ * P * 8
+    if not fused:
+        kernel = "k_summary<f16> (summaries of every lane; logits on the matrix cores follow)"
+        alg = k_read + NL * P * W * 2
+    elif w["resident"]:
+        # per layer: summaries + Q read, logits written by the summary
+        # workgroups and read by the softmax units, terms written in place
+        # and read back by the tail, scores written
+        kernel = f"k_stack_group<summaries> ({G} resident layers' logits beside the previous {G} layers' " \
+                 f"softmax and top-k)"
+        alg = G * (NL * P * W * 2 + q_bytes + 4 * logits + NL * P * 8)
+    else:
+        kernel = f"k_stack_group<{'q8_0' if kfmt == K.FMT_Q8_0 else 'f16'}> ({G} layers' summaries beside the " \
+                 f"previous {G} layers' logits, softmax and top-k)"
+        alg = G * (k_read + 2 * NL * P * W * 2 + q_bytes + 2 * logits + NL * P * 8)
+    achieved = alg / (launch_us * 1e-6) / 1e9
+    traffic, traffic_src = None, os.path.join(ROOT, "profiles", f"pmc_{args.workload}.json")
+    if os.path.exists(traffic_src):
+        try:
+            traffic = json.load(open(traffic_src)).get("traffic_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
     # (c) select + stage-in pipelined over the layers
-    pdescs = [desc(l, True) for l in range(L)]
+    pdescs = [desc(i, True) for i in range(N)]
     for rep in range(2):
         ctx.check()
         p0 = time.perf_counter()
         keep = ctx.recall_stack(pdescs, None, ctx.copy_stream)
         ctx.check()
-        pipe_us = (time.perf_counter() - p0) * 1e6 / L
+        pipe_us = (time.perf_counter() - p0) * 1e6 / N
     del keep
     # (d) stage-in alone
     stage = []
+    eng = {"auto": K.ENGINE_AUTO, "kernel": K.ENGINE_KERNEL, "sdma": K.ENGINE_SDMA}[args.engine]
     for rep in range(2):
-        for l in range(L):
+        for i in range(N):
+            l = order[i]
             planes = [K.make_plane(pins[l % ring][0], kfmt, W, T, mode[w["kmode"]], kslots[l], rope=rope),
                       K.make_plane(pins[l % ring][1], vfmt, W, T, mode[w["vmode"]], vslots[l])]
             hip.record(ev_a, ctx.copy_stream)
-            ctx.stage_in(planes, PT, sel[l], cnt[l], KSEL, lanes=NL,
-                         engine={"auto": K.ENGINE_AUTO, "kernel": K.ENGINE_KERNEL, "sdma": K.ENGINE_SDMA}[args.engine])
+            ctx.stage_in(planes, PT, sel[i], cnt[i], KSEL, lanes=NL, engine=eng)
             hip.record(ev_b, ctx.copy_stream)
             ctx.check()
             if rep:
                 stage.append(hip.elapsed_ms(ev_a, ev_b) * 1e3)
     stage_us = float(np.mean(stage))
     stage_bytes = NL * KSEL * PT * (row(w["kfmt"]) + row(w["vfmt"]))
-    h2d = ctx.h2d_peak_gbps(1 << 30, 5)
+    link = ctx.h2d_ceiling_gbps(1 << 30, 5)
     stage_gbps = stage_bytes / (stage_us * 1e-6) / 1e9
     log(f"pipelined {pipe_us:.1f} us/layer; stage-in {stage_us:.1f} us/layer = {stage_gbps:.2f} GB/s "
-        f"(H2D peak {h2d:.2f})")
+        f"(host link: copy {link['copy_GBps']}, kernel read {link['kernel_read_GBps']} GB/s)")
     line = {
         "metric": "select+stage-in latency/layer at 128K ctx; scored-KV GB/s vs HBM peak",
         "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f16/q8_0/q4_1 operands, f32 summaries, f64 scores",
-        "data": f"synthetic seeded (device generator), seed {seed}",
-        "config": {"workload": args.workload, **{k: v for k, v in w.items()}, "stack_layers": len(order)},
+        "data": f"synthetic seeded (device generator, Irwin-Hall 12 normals), seed {seed}",
+        "config": {"workload": args.workload, **{k: v for k, v in w.items()}, "stack_layers": N},
         "select_us_per_layer": round(select_us, 2),
-        "select_stack_us_per_layer": round(ms_per_step * 1e3 / len(order), 2),
+        "select_stack_us_per_layer": round(ms_per_step * 1e3 / N, 2),
         "scored_frac_hbm": round(value / HBM_PEAK_GBPS, 4),
         "latency_us_per_layer": round(pipe_us, 2),
         "stagein_us_per_layer": round(stage_us, 2),
         "stagein_bytes_per_layer": stage_bytes,
-        "stagein_GBps": round(stage_gbps, 3), "h2d_peak_GBps": round(h2d, 3),
-        "stagein_frac_h2d": round(stage_gbps / h2d, 4),
+        "stagein_GBps": round(stage_gbps, 3), "h2d_link": link, "h2d_peak_GBps": link["ceiling_GBps"],
+        "stagein_frac_h2d": round(stage_gbps / link["ceiling_GBps"], 4),
+        "roofline": {"bound": "hbm", "kernel": kernel, "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "bytes_per_launch": alg, "mean_launch_us": round(launch_us, 3)},
     }
+    # parity of every unit and the reference's CPU select path
+    log("parity of every layer/lane against the oracle; reference CPU baseline ...")
+    gsel = [x.cpu().numpy().view(np.uint32).reshape(NL, KSEL) for x in sel]
+    gsc = [x.cpu().numpy().reshape(NL, P) for x in scores]
+    units, usel, usc = [], [], []
+    seen = set()
+    for i in range(N):
+        l = order[i]
+        if l in seen:
+            continue
+        seen.add(l)
+        for lane in range(NL):
+            def fetch(l=l, lane=lane):
+                q = qd[l].cpu().numpy().view(np.float16).astype(np.float32).reshape(NL, R * HQ * D)[lane]
+                if w["resident"]:
+                    return "summaries", s16[l].cpu().numpy().view(np.uint16).reshape(NL, -1)[lane], q
+                raw = dev_k[l][lane * T * row(w["kfmt"]):(lane + 1) * T * row(w["kfmt"])].cpu().numpy()
+                return ("q8_0", raw, q) if kfmt == K.FMT_Q8_0 else ("f16", raw.view(np.uint16), q)
+            units.append(fetch)
+            usel.append(gsel[i][lane])
+            usc.append(gsc[i][lane])
+    parity, cpu = workload_checks(args, w, "lane" if NL > 1 else "layer", units, usel, usc, tie, scored_layer // NL)
+    line["parity"] = parity
+    if cpu:
+        line["cpu_baseline"] = cpu
+    log(f"parity: {parity}; cpu: {cpu}")
     for pk, pv in pins:
         pk.free()
         pv.free()
@@ -878,7 +1033,8 @@ def main():
                     help="resident64 (default): the 64-layer 128K stack; the others are the remaining "
                          "workloads, each measured the same way")
     ap.add_argument("--pmc-pass", action="store_true",
-                    help="only the short counter pass (one layer's selects + calibration copies)")
+                    help="only the short counter pass of the workload (a stack of three launches, or one launch, "
+                         "then three 256 MiB calibration copies)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -886,6 +1042,9 @@ def main():
             print("bench.py measures one GPU: the recall path runs on a single MI355X in this build "
                   "(multi-GPU sharding is a design note, not a measured mode). Use --gpus 1.", flush=True)
         sys.exit(2)
+    if args.pmc_pass and args.workload in WORKLOADS:
+        run_workload(args)
+        return
     if args.pmc_pass:
         pmc_pass(args)
         return

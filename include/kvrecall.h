@@ -653,6 +653,11 @@ kvr_status kvr_host_free(void *ptr);
 /* Best-of-`reps` hipMemcpyAsync bandwidth of one `bytes` pinned->device copy,
  * GB/s (10^9 B/s).  Measurement helper with no reference counterpart. */
 kvr_status kvr_h2d_peak_gbps(kvr_context *ctx, size_t bytes, int reps, double *gbps);
+/* Best-of-`reps` rate of a kernel reading `bytes` (a multiple of 16) of
+ * device-mapped pinned memory (the way the gather reads the history) and
+ * writing it to device memory, GB/s.  Measurement helper with no reference
+ * counterpart. */
+kvr_status kvr_h2d_read_peak_gbps(kvr_context *ctx, size_t bytes, int reps, double *gbps);
 
 /* ---- seeded synthetic inputs (device fill) ----------------------------- */
 /* Bit-identical to the generator of the test oracle; no reference counterpart.

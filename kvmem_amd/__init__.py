@@ -411,6 +411,17 @@ class Context:
         check(lib().kvr_h2d_peak_gbps(self.handle, nbytes, reps, C.byref(out)))
         return out.value
 
+    def h2d_read_peak_gbps(self, nbytes: int = 1 << 30, reps: int = 5) -> float:
+        """A kernel's zero-copy read rate of pinned host memory (GB/s)."""
+        out = C.c_double()
+        check(lib().kvr_h2d_read_peak_gbps(self.handle, nbytes, reps, C.byref(out)))
+        return out.value
+
+    def h2d_ceiling_gbps(self, nbytes: int = 1 << 30, reps: int = 5) -> dict:
+        """Both host-link probes; the ceiling is the larger."""
+        copy, read = self.h2d_peak_gbps(nbytes, reps), self.h2d_read_peak_gbps(nbytes, reps)
+        return {"copy_GBps": round(copy, 3), "kernel_read_GBps": round(read, 3), "ceiling_GBps": round(max(copy, read), 3)}
+
     def synth_normal_f16(self, seed, sid, count, out, stream=None):
         check(lib().kvr_synth_normal_f16(self.handle, seed, sid, count, _ptr(out), stream))
 

@@ -132,6 +132,7 @@ _SIGNATURES = {
     "kvr_host_alloc": (_i, [_sz, C.POINTER(_P)]),
     "kvr_host_free": (_i, [_P]),
     "kvr_h2d_peak_gbps": (_i, [_P, _sz, _i, C.POINTER(C.c_double)]),
+    "kvr_h2d_read_peak_gbps": (_i, [_P, _sz, _i, C.POINTER(C.c_double)]),
     "kvr_synth_normal_f16": (_i, [_P, _u64, _u64, _u64, _P, _P]),
     "kvr_synth_scaled_normal_f16": (_i, [_P, _u64, _u64, _u64, _u32, _P, _P, _P]),
     "kvr_synth_normal_f32": (_i, [_P, _u64, _u64, _u64, _P, _P]),

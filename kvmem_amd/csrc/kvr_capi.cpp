@@ -1772,6 +1772,38 @@ kvr_status kvr_h2d_peak_gbps(kvr_context *ctx, size_t bytes, int reps, double *g
     return st;
 }
 
+kvr_status kvr_h2d_read_peak_gbps(kvr_context *ctx, size_t bytes, int reps, double *gbps) {
+    if (kvr_status s = check_ctx(ctx)) return s;
+    if (!bytes || bytes % 16 || reps < 1 || !gbps) return fail(KVR_ERR_INVALID, "invalid bandwidth probe");
+    DeviceGuard guard(ctx->device);
+    void *host = nullptr, *mapped = nullptr, *dev = nullptr;
+    hipEvent_t a = nullptr, b = nullptr;
+    kvr_status st = KVR_OK;
+    hipError_t e = hipHostMalloc(&host, bytes, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipHostGetDevicePointer(&mapped, host, 0);
+    if (e == hipSuccess) e = hipMalloc(&dev, bytes);
+    if (e == hipSuccess) e = hipEventCreate(&a);
+    if (e == hipSuccess) e = hipEventCreate(&b);
+    if (e == hipSuccess) std::memset(host, 1, bytes);
+    float best = 0;
+    for (int i = 0; e == hipSuccess && i <= reps; ++i) {
+        e = hipEventRecord(a, ctx->copy);
+        if (e == hipSuccess) e = kvr::launch_link_read(mapped, dev, bytes, ctx->copy);
+        if (e == hipSuccess) e = hipEventRecord(b, ctx->copy);
+        if (e == hipSuccess) e = hipEventSynchronize(b);
+        float ms = 0;
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+        if (e == hipSuccess && i > 0 && (best == 0 || ms < best)) best = ms;  // first read warms up
+    }
+    if (e != hipSuccess) st = hip_fail(e, "H2D kernel read probe");
+    else *gbps = double(bytes) / (double(best) * 1e-3) / 1e9;
+    if (a) (void)hipEventDestroy(a);
+    if (b) (void)hipEventDestroy(b);
+    if (dev) (void)hipFree(dev);
+    if (host) (void)hipHostFree(host);
+    return st;
+}
+
 // ---- synthetic inputs -----------------------------------------------------
 namespace {
 kvr_status synth(kvr_context *ctx, kvr::SynthArgs a, uint64_t seed, uint64_t sid, void *stream) {

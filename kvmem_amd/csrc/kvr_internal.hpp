@@ -206,6 +206,8 @@ hipError_t launch_gather(const GatherArgs &a, hipStream_t s);
 hipError_t launch_accumulate(const AccumulateArgs &a, hipStream_t s);
 hipError_t launch_finalize(const FinalizeArgs &a, hipStream_t s);
 hipError_t launch_copy_ops(const CopyOp *ops, uint32_t n, hipStream_t s);
+// bytes (a multiple of 16) of device-visible pinned memory read by a kernel
+hipError_t launch_link_read(const void *src, void *dst, uint64_t bytes, hipStream_t s);
 
 // Half-page masses [lanes][2 * pages] -> page scores [lanes][pages]
 // (layerwise_tile_scores' sum, layerwise_max_page_scores' max), with the

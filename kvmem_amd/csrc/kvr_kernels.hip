@@ -2556,6 +2556,22 @@ __global__ __launch_bounds__(256) void k_finalize(FinalizeArgs a) {
 }
 
 // Batched byte copies (copy_bytes, stagein.cu:236-261): one workgroup per op.
+// Host-link read probe: device-mapped pinned memory read by the CUs in
+// 16-byte loads (four in flight per thread, grid-strided) and written to
+// device memory.
+__global__ __launch_bounds__(256) void k_link_read(const uint4 *src, uint4 *dst, uint64_t n16) {
+    const uint64_t stride = uint64_t(gridDim.x) * 256;
+    uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    for (; i + 3 * stride < n16; i += 4 * stride) {
+        const uint4 a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
+        dst[i] = a;
+        dst[i + stride] = b;
+        dst[i + 2 * stride] = c;
+        dst[i + 3 * stride] = d;
+    }
+    for (; i < n16; i += stride) dst[i] = src[i];
+}
+
 __global__ __launch_bounds__(256) void k_copy_ops(const CopyOp *ops, uint32_t n) {
     if (blockIdx.x >= n) return;
     const CopyOp op = ops[blockIdx.x];
@@ -2774,6 +2790,13 @@ hipError_t launch_accumulate(const AccumulateArgs &a, hipStream_t s) {
 hipError_t launch_finalize(const FinalizeArgs &a, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch\'s error
     hipLaunchKernelGGL(k_finalize, dim3(blocks_for(uint64_t(a.pages) * a.width)), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_link_read(const void *src, void *dst, uint64_t bytes, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error
+    hipLaunchKernelGGL(k_link_read, dim3(1024), dim3(256), 0, s, static_cast<const uint4 *>(src),
+                       static_cast<uint4 *>(dst), bytes / 16);
     return hipGetLastError();
 }
 
