@@ -121,7 +121,9 @@ struct StackGroupArgs {
     SummaryArgs s[kStackGroup];
     SelectArgs p[kStackGroup];
     uint32_t m, mp;
-    uint32_t summary_blocks;  // workgroups of one layer's summaries
+    uint32_t summary_blocks;  // summary workgroups: layer_blocks per part of the group's layers
+    uint32_t layer_blocks;    // workgroups covering one layer's summaries
+    uint32_t layers_per_part; // consecutive layers a summary workgroup walks
     uint32_t probs_per_lane;  // softmax workgroups per lane and layer
     uint32_t q_slot;          // elements of one LDS query staging buffer (multiple of 8)
 };

@@ -511,17 +511,44 @@ __device__ __forceinline__ void logits_rows_t(const SelectArgs &a, uint32_t lane
     const uint32_t k = l % lph, sub = l / lph;
     const uint32_t group = q.qheads / q.kvheads, kvh = h0 / group, W = q.kvheads * q.dim, n = a.pages;
     const double scale = q.scale;
-    // all four heads are computed (past nh: repeats of the last), nh stored
+    // all four heads are computed (past nh: repeats of the last), nh stored.
+    // The 32 query values are loaded together (one 16-byte load per head
+    // for packed fp16), the format chosen once outside the loads, and only
+    // then converted: a per-element format choice compiles to a wait per load.
     double qd[4][8];
+    uint32_t raw[4][8];
     uint32_t bad = kOperandOk;
+    const uint8_t *qrow = q.data + lane * q.lane_stride + r * q.row_stride + 8 * k * q.dim_stride;
+    auto head_at = [&](uint32_t hh) { return qrow + (h0 + min(hh, nh - 1)) * q.head_stride; };
+    if (q.packed16) {
+#pragma unroll
+        for (uint32_t hh = 0; hh < 4; ++hh) {
+            const u32x4 v = *reinterpret_cast<const u32x4 *>(head_at(hh));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                raw[hh][2 * i] = v[i] & 0xffffu;
+                raw[hh][2 * i + 1] = v[i] >> 16;
+            }
+        }
+    } else if (q.scalar == kScalarF32) {
+#pragma unroll
+        for (uint32_t hh = 0; hh < 4; ++hh)
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                raw[hh][i] = *reinterpret_cast<const uint32_t *>(head_at(hh) + i * q.dim_stride);
+    } else {
+#pragma unroll
+        for (uint32_t hh = 0; hh < 4; ++hh)
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                raw[hh][i] = *reinterpret_cast<const uint16_t *>(head_at(hh) + i * q.dim_stride);
+    }
 #pragma unroll
     for (uint32_t hh = 0; hh < 4; ++hh) {
-        const uint32_t h = h0 + min(hh, nh - 1);
-        const uint8_t *qp = q.data + lane * q.lane_stride + r * q.row_stride + h * q.head_stride + 8 * k * q.dim_stride;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             uint16_t qb = 0;
-            const uint32_t e = recall16(load_scalar(qp + i * q.dim_stride, q.scalar), qb);
+            const uint32_t e = recall16(raw_value(raw[hh][i], q.scalar), qb);
             bad = bad ? bad : e;
             qd[hh][i] = double(h2f(qb));
         }
@@ -1722,7 +1749,7 @@ constexpr int kBufferNontemporal = 2;  // cache-policy bits of a streaming load
 // Otherwise each lane keeps its own row pointer, clamped to the page's last
 // row.
 template <int SRC, bool PAGED>
-__device__ __forceinline__ void stack_summaries(const StackGroupArgs &g, uint32_t block) {
+__device__ __forceinline__ void stack_summaries(const StackGroupArgs &g, uint32_t block, uint32_t l0, uint32_t m) {
     __builtin_amdgcn_s_setprio(2);
     const SummaryArgs &a = g.s[0];
     const uint32_t gpp = a.width >> 3;
@@ -1747,7 +1774,6 @@ __device__ __forceinline__ void stack_summaries(const StackGroupArgs &g, uint32_
     const uint64_t t0 = uint64_t(page) * a.page_tokens;
     const uint64_t tail = a.tokens - t0;
     const uint32_t n = tail < a.page_tokens ? uint32_t(tail) : a.page_tokens;
-    const uint32_t m = g.m;
     // this thread's column in a row, and the row stride
     const uint32_t row_bytes = SRC == kSrcKeysF16 ? a.width * 2 : (a.width >> 5) * kQ8Bytes;
     const uint32_t b = cg >> 2, s = cg & 3;  // q8_0: block and quarter (see summary_block)
@@ -1769,7 +1795,11 @@ __device__ __forceinline__ void stack_summaries(const StackGroupArgs &g, uint32_
         sums[i] = g.s[i].summaries;
         epoch[i] = g.s[i].epoch;
     }
-    auto pick = [](uint32_t i, auto v0, auto v1, auto v2, auto v3) { return i == 1 ? v1 : i == 2 ? v2 : i == 3 ? v3 : v0; };
+    // layer i of this workgroup's part is layer l0 + i of the group
+    auto pick = [l0](uint32_t i, auto v0, auto v1, auto v2, auto v3) {
+        i += l0;
+        return i == 1 ? v1 : i == 2 ? v2 : i == 3 ? v3 : v0;
+    };
     auto layer_first = [&](uint32_t i) { return pick(i, first[0], first[1], first[2], first[3]); };
     float acc[8];
 #pragma unroll
@@ -1829,7 +1859,7 @@ __device__ __forceinline__ void stack_summaries(const StackGroupArgs &g, uint32_
     constexpr int D = SRC == kSrcKeysF16 ? kF16Rows : kQ8Rows;
     const uint32_t per_layer = (n + D - 1) / D;
     const uint32_t chunks = m * per_layer;
-    const uint8_t *cp = first[0];
+    const uint8_t *cp = layer_first(0);
     uint32_t left = n - 1, coff = 0;
     auto page_rsrc = [&]() {
         if constexpr (PAGED) return buffer_rsrc(cp, n * row_bytes); else return 0;
@@ -1914,17 +1944,22 @@ __global__ __launch_bounds__(256) void k_stack_group(StackGroupArgs g) {
         probs_block<NPL, true>(g.p[i], r % g.probs_per_lane, r / g.probs_per_lane, g.probs_per_lane);
         return;
     }
+    // The group's layers are split into parts of layers_per_part
+    // consecutive layers (one part when a layer's workgroups fill the GPU);
+    // workgroup b covers summary slot b % layer_blocks of its part's layers.
+    const uint32_t part = blockIdx.x / g.layer_blocks, blk = blockIdx.x - part * g.layer_blocks;
+    const uint32_t l0 = part * g.layers_per_part, m = min(g.m - l0, g.layers_per_part);
     // Key histories leave the logits to the softmax workgroups of the next
     // launch; resident summaries have no stream, so they compute theirs here.
     if constexpr (SRC == kSrcSummary) {
-        for (uint32_t i = 0; i < g.m; ++i) summary_block<SRC, true>(g.s[i], blockIdx.x, q_lds_buf + (i & 1) * g.q_slot);
+        for (uint32_t i = 0; i < m; ++i) summary_block<SRC, true>(g.s[l0 + i], blk, q_lds_buf + (i & 1) * g.q_slot);
     } else {
         const SummaryArgs &a = g.s[0];
         const uint64_t row_bytes = SRC == kSrcKeysF16 ? a.width * 2 : (a.width >> 5) * kQ8Bytes;
         if ((a.width & 511) == 0 && (uint64_t(a.page_tokens) + 64) * row_bytes < (uint64_t(1) << 32))
-            stack_summaries<SRC, true>(g, blockIdx.x);
+            stack_summaries<SRC, true>(g, blk, l0, m);
         else
-            stack_summaries<SRC, false>(g, blockIdx.x);
+            stack_summaries<SRC, false>(g, blk, l0, m);
     }
 }
 
@@ -2692,11 +2727,21 @@ hipError_t launch_probs(const SelectArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+constexpr uint32_t kStackSpreadBlocks = 256;  // summary workgroups that fill MI355X's 256 CUs
 hipError_t launch_stack_group(int source, StackGroupArgs g, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch\'s error
     const SummaryArgs &sa = g.s[0];
     const SelectArgs &pa = g.p[0];
-    g.summary_blocks = g.m ? blocks_for(uint64_t(sa.lanes) * sa.pages * (sa.width >> 3)) : 0;
+    // A layer whose summaries take fewer workgroups than the GPU has CUs
+    // leaves CUs idle if one workgroup walks all the group's layers: split
+    // the layers into parts until the launch has a workgroup per CU.
+    g.layer_blocks = g.m ? blocks_for(uint64_t(sa.lanes) * sa.pages * (sa.width >> 3)) : 1;
+    uint32_t parts = 1;
+    if (g.m && g.layer_blocks < kStackSpreadBlocks)
+        parts = min(g.m, (kStackSpreadBlocks + g.layer_blocks - 1) / g.layer_blocks);
+    g.layers_per_part = g.m ? (g.m + parts - 1) / parts : 1;
+    parts = g.m ? (g.m + g.layers_per_part - 1) / g.layers_per_part : 0;
+    g.summary_blocks = g.layer_blocks * parts;
     const uint32_t sb = g.summary_blocks;
     const uint32_t probs_blocks = g.mp ? g.mp * g.probs_per_lane * pa.lanes : 0;
     const dim3 grid(unsigned(sb + probs_blocks)), block(256);
