@@ -19,6 +19,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <memory>
+#include <stdexcept>
 #include <string>
 #include <utility>
 #include <vector>
@@ -27,6 +28,21 @@ namespace kvmem_hip {
 
 enum class GqaScoreAggregation { Mean, Max, MaxLogit };
 enum class TieRule { LowerFirst, HigherFirst };
+
+// Errors of the memory-backend contract (memory_contract.hpp:14-25): record
+// layouts, working-set plans and transfers throw these, with the code a
+// caller dispatches on.
+enum class MemoryErrorCode {
+    InvalidPlan, Unsupported, BudgetExceeded, Stale, Pending, TransferFailed, Disconnected, InvalidSession
+};
+class MemoryError : public std::runtime_error {
+public:
+    MemoryError(MemoryErrorCode code, const std::string &message) : std::runtime_error(message), code_(code) {}
+    MemoryErrorCode code() const noexcept { return code_; }
+
+private:
+    MemoryErrorCode code_;
+};
 
 // One accepted logical index: page starts/counts and the score and transport
 // masks (graph_recall.hpp:18-24).
@@ -226,8 +242,9 @@ private:
 
 // ---- native payload records (memory_contract.hpp:39-68) -------------------
 // One record per page holds every layer's planes at fixed offsets.  The
-// types mirror the reference's; validate() restates PayloadLayout::validate
-// (kvmem/src/host/memory_contract.cpp:51-106) and throws std::invalid_argument.
+// types mirror the reference's; validate() enforces the rules of
+// PayloadLayout::validate (kvmem/src/host/memory_contract.cpp:51-101) and
+// throws MemoryError(InvalidPlan) with the reference's messages.
 enum class PayloadPlaneKind { Key, Value, KeyScale, ValueScale, PackedKeyValue };
 struct PayloadPlane {
     uint32_t layer = 0;

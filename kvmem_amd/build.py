@@ -97,7 +97,7 @@ def build_host_test(verbose: bool = False) -> str:
     _run([hipcc, "-O2", "-std=c++17", "-Wall", "-I", os.path.join(ROOT, "include"), "-I", ORACLE, HOST_TEST_SRC,
           "-o", tmp, "-L", libdir, "-lkvmem_hip", "-lkvrecall", "-L", ORACLE, "-loracle",
           f"-Wl,-rpath,{libdir}", f"-Wl,-rpath,{ORACLE}", "-Wl,-rpath,$ORIGIN/../../../kvmem_amd",
-          "-Wl,-rpath,$ORIGIN/../../../oracle"], verbose)
+          "-Wl,-rpath,$ORIGIN/../../../oracle", "-ldl"], verbose)
     os.replace(tmp, HOST_TEST)
     return HOST_TEST
 

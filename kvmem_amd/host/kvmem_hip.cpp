@@ -7,14 +7,11 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
-#include <array>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <limits>
-#include <map>
-#include <set>
 #include <stdexcept>
 
 namespace kvmem_hip {
@@ -120,27 +117,42 @@ QueryScoreFrame query_score_frame(uint64_t accepted, uint32_t block_tokens, uint
     return f;
 }
 
+// Rules (native_layer_query.hpp:36-58):
+//  G: data, every count and the GQA group are present, the scale is finite
+//     and >= 0, and data is aligned to the scalar;
+//  S: every stride is a positive multiple of the scalar, and an axis with
+//     more than one element starts past everything the axes nested inside
+//     it reach (the axes with smaller (stride, count), ties by position), so
+//     no two elements share bytes, in any axis order; the reach stays
+//     within size_t;
+//  E: the reach of all three axes fits in `bytes`.
 void validate_native_layer_query(const NativeCurrentLayerQuery &q) {
+    const bool shaped = q.data && q.rows && q.query_heads && q.kv_heads && q.head_dim &&
+                        q.query_heads % q.kv_heads == 0;
+    const bool scaled = std::isfinite(q.attention_scale) && q.attention_scale >= 0;
     const size_t el = query_scalar_bytes(q.scalar);
-    if (!q.data || !q.rows || !q.query_heads || !q.kv_heads || !q.head_dim || q.query_heads % q.kv_heads ||
-        !std::isfinite(q.attention_scale) || q.attention_scale < 0 ||
-        reinterpret_cast<uintptr_t>(q.data) % el)
+    if (!shaped || !scaled || reinterpret_cast<uintptr_t>(q.data) % el != 0)
         throw std::invalid_argument("invalid native current-layer Query geometry");
-    // Axes by increasing stride must not overlap: each stride is at least the
-    // extent of the faster axes.
-    std::array<std::pair<size_t, uint32_t>, 3> axes{
-        {{q.row_stride, q.rows}, {q.head_stride, q.query_heads}, {q.dimension_stride, q.head_dim}}};
-    std::sort(axes.begin(), axes.end());
-    size_t extent = el;
-    for (const auto &ax : axes) {
-        const size_t stride = ax.first, count = ax.second;
-        if (!stride || stride % el || (count > 1 && stride < extent))
+
+    using wide = unsigned __int128;
+    const size_t stride[3] = {q.row_stride, q.head_stride, q.dimension_stride};
+    const uint32_t count[3] = {q.rows, q.query_heads, q.head_dim};
+    auto inside = [&](int a, int b) {  // axis a is nested inside axis b
+        if (stride[a] != stride[b]) return stride[a] < stride[b];
+        return count[a] != count[b] ? count[a] < count[b] : a < b;
+    };
+    const wide limit = std::numeric_limits<size_t>::max();
+    wide total = el;
+    for (int a = 0; a < 3; ++a) {
+        wide reach = el;  // bytes spanned by the axes nested inside a
+        for (int b = 0; b < 3; ++b)
+            if (b != a && inside(b, a)) reach += wide(stride[b]) * (count[b] - 1);
+        const wide step = wide(stride[a]) * (count[a] > 1 ? count[a] - 1 : 1);
+        if (stride[a] == 0 || stride[a] % el != 0 || (count[a] > 1 && stride[a] < reach) || step > limit - reach)
             throw std::invalid_argument("overlapping or overflowing native Query strides");
-        if (count > 1 && stride > (std::numeric_limits<size_t>::max() - extent) / (count - 1))
-            throw std::invalid_argument("overlapping or overflowing native Query strides");
-        extent += stride * (count - 1);
+        total += wide(stride[a]) * (count[a] - 1);
     }
-    if (extent > q.bytes) throw std::invalid_argument("native Query exceeds its declared byte extent");
+    if (total > q.bytes) throw std::invalid_argument("native Query exceeds its declared byte extent");
 }
 
 // ---------------------------------------------------------------------------
@@ -583,13 +595,18 @@ std::vector<uint32_t> PageSoftmaxHip::pick_topk(const std::vector<double> &score
 
 // ---- native payload records -------------------------------------------------
 namespace {
-uint64_t checked_add(uint64_t a, uint64_t b) {
-    if (b > std::numeric_limits<uint64_t>::max() - a) throw std::invalid_argument("memory size/position overflow");
-    return a + b;
+void plan_require(bool cond, const char *msg) {
+    if (!cond) throw MemoryError(MemoryErrorCode::InvalidPlan, msg);
 }
-uint64_t checked_mul(uint64_t a, uint64_t b) {
-    if (a && b > std::numeric_limits<uint64_t>::max() / a) throw std::invalid_argument("memory size overflow");
-    return a * b;
+uint64_t plan_add(uint64_t a, uint64_t b) {
+    uint64_t r;
+    plan_require(!__builtin_add_overflow(a, b, &r), "memory size/position overflow");
+    return r;
+}
+uint64_t plan_mul(uint64_t a, uint64_t b) {
+    uint64_t r;
+    plan_require(!__builtin_mul_overflow(a, b, &r), "memory size overflow");
+    return r;
 }
 bool pow2(uint64_t n) { return n && !(n & (n - 1)); }
 // bytes of one token row of a gather source format (0: not a source format)
@@ -603,53 +620,94 @@ size_t source_row_bytes(kvr_format f, uint32_t width) {
 }
 }  // namespace
 
+// Rules of a record layout (memory_contract.cpp:51-101), checked plane by
+// plane in list order and then shard by shard; the first broken rule throws
+// std::invalid_argument with its message.
+//  R1 header: format, version, block_tokens, record_bytes and at least one
+//     plane; the alignment a power of two dividing record_bytes.
+//  R2 a plane has bytes, a power-of-two alignment no larger than the
+//     record's, an aligned offset, starts at or after the previous plane's
+//     end, and its kind appears once in its shard (layer, rank).
+//  R3 a head range is [begin, begin+count) within uint32; count 0 means
+//     "all heads" and then begins at 0.
+//  R4 every plane of a shard carries the shard's head range.
+//  R5 a packed key+value plane has no token rows (token_stride 0).
+//  R6 a plane ends inside the record, and block_tokens token rows fit it.
+//  R7 a shard holds one packed key+value plane alone, or a key and a value
+//     plane (scale planes optional).
+//  R8 a layer's shards, by rank, tile its heads from 0 without gaps; a shard
+//     of "all heads" is its layer's only shard.
+namespace {
+struct PayloadShard {
+    uint32_t layer, rank, head_begin, head_count;
+    unsigned kinds;  // bit per PayloadPlaneKind
+};
+constexpr unsigned kind_bit(PayloadPlaneKind k) { return 1u << unsigned(k); }
+constexpr unsigned kKnownKinds = kind_bit(PayloadPlaneKind::Key) | kind_bit(PayloadPlaneKind::Value) |
+                                 kind_bit(PayloadPlaneKind::KeyScale) | kind_bit(PayloadPlaneKind::ValueScale) |
+                                 kind_bit(PayloadPlaneKind::PackedKeyValue);
+}  // namespace
+
 void PayloadLayout::validate() const {
-    require(!format.empty() && version && block_tokens && record_bytes && !planes.empty() && pow2(alignment) &&
-                record_bytes % alignment == 0,
-            "invalid native payload layout");
-    uint64_t end = 0;
-    using Shard = std::pair<uint32_t, uint32_t>;  // model layer, rank
-    std::map<Shard, std::set<PayloadPlaneKind>> kinds;
-    std::map<Shard, std::pair<uint32_t, uint32_t>> heads;
-    for (const auto &p : planes) {
-        require(p.bytes && pow2(p.alignment) && p.alignment <= alignment && p.offset % p.alignment == 0 &&
-                    p.offset >= end && kinds[{p.layer, p.rank}].insert(p.kind).second,
-                "overlapping/duplicate/misaligned payload plane");
-        require((p.head_count || !p.head_begin) &&
-                    uint64_t(p.head_begin) + p.head_count <= std::numeric_limits<uint32_t>::max(),
+    const bool header = !format.empty() && version != 0 && block_tokens != 0 && record_bytes != 0 &&
+                        !planes.empty() && pow2(alignment) && record_bytes % alignment == 0;
+    plan_require(header, "invalid native payload layout");
+
+    std::vector<PayloadShard> shards;  // in order of first appearance
+    auto shard_of = [&](const PayloadPlane &p) -> PayloadShard * {
+        for (auto &s : shards)
+            if (s.layer == p.layer && s.rank == p.rank) return &s;
+        return nullptr;
+    };
+    uint64_t cursor = 0;  // end of the previous plane
+    for (const PayloadPlane &p : planes) {
+        const unsigned bit = unsigned(p.kind) < 32 ? 1u << unsigned(p.kind) : 0;
+        PayloadShard *s = shard_of(p);
+        const bool placed = p.bytes != 0 && pow2(p.alignment) && p.alignment <= alignment &&
+                            p.offset % p.alignment == 0 && p.offset >= cursor;
+        plan_require(placed && !(s && (s->kinds & bit)), "overlapping/duplicate/misaligned payload plane");
+        plan_require(p.head_count != 0 ? uint64_t(p.head_begin) + p.head_count <= std::numeric_limits<uint32_t>::max()
+                                  : p.head_begin == 0,
                 "invalid payload head range");
-        const auto range = std::make_pair(p.head_begin, p.head_count);
-        const auto ins = heads.emplace(Shard{p.layer, p.rank}, range);
-        require(ins.second || ins.first->second == range, "a payload shard has inconsistent head ranges");
-        require(p.kind != PayloadPlaneKind::PackedKeyValue || !p.token_stride,
+        if (!s) {
+            shards.push_back({p.layer, p.rank, p.head_begin, p.head_count, 0});
+            s = &shards.back();
+        }
+        plan_require(s->head_begin == p.head_begin && s->head_count == p.head_count,
+                "a payload shard has inconsistent head ranges");
+        plan_require((bit & kKnownKinds) != 0, "unknown payload plane kind");
+        s->kinds |= bit;
+        plan_require(p.kind != PayloadPlaneKind::PackedKeyValue || p.token_stride == 0,
                 "packed KV pages require opaque token addressing");
-        end = checked_add(p.offset, p.bytes);
-        require(end <= record_bytes && (!p.token_stride || checked_mul(p.token_stride, block_tokens) <= p.bytes),
-                "payload plane exceeds its record");
+        cursor = plan_add(p.offset, p.bytes);
+        // the record bound is checked before the rows' size is computed: a
+        // plane past the record reports that, even when its rows overflow
+        const bool inside = cursor <= record_bytes;
+        plan_require(inside && (p.token_stride == 0 || plan_mul(p.token_stride, block_tokens) <= p.bytes),
+                     "payload plane exceeds its record");
     }
-    for (const auto &layer : kinds) {
-        const bool packed = layer.second.count(PayloadPlaneKind::PackedKeyValue) != 0;
-        const bool key = layer.second.count(PayloadPlaneKind::Key) != 0;
-        const bool value = layer.second.count(PayloadPlaneKind::Value) != 0;
-        require(packed ? layer.second.size() == 1 : (key && value),
+
+    std::sort(shards.begin(), shards.end(), [](const PayloadShard &a, const PayloadShard &b) {
+        return a.layer != b.layer ? a.layer < b.layer : a.rank < b.rank;
+    });
+    const unsigned kv = kind_bit(PayloadPlaneKind::Key) | kind_bit(PayloadPlaneKind::Value);
+    for (const PayloadShard &s : shards) {
+        const unsigned packed = kind_bit(PayloadPlaneKind::PackedKeyValue);
+        plan_require(s.kinds == packed || ((s.kinds & kv) == kv && (s.kinds & packed) == 0),
                 "every attention layer requires key and value planes");
     }
-    bool have_layer = false, unsharded = false;
-    uint32_t previous = 0;
-    uint64_t next_head = 0;
-    for (const auto &item : heads) {
-        const uint32_t layer = item.first.first, begin = item.second.first, count = item.second.second;
-        if (!have_layer || previous != layer) {
-            have_layer = true;
-            previous = layer;
-            next_head = 0;
-            unsharded = false;
-        } else {
-            require(!unsharded && count, "multiple payload shards need explicit head ranges");
+    for (size_t first = 0; first < shards.size();) {
+        size_t last = first;
+        while (last + 1 < shards.size() && shards[last + 1].layer == shards[first].layer) ++last;
+        uint64_t covered = 0;  // heads [0, covered) tiled so far
+        for (size_t i = first; i <= last; ++i) {
+            if (i > first)
+                plan_require(shards[i - 1].head_count != 0 && shards[i].head_count != 0,
+                        "multiple payload shards need explicit head ranges");
+            plan_require(shards[i].head_begin == covered, "payload heads must cover a contiguous model-order range");
+            covered += shards[i].head_count;
         }
-        require(begin == next_head, "payload heads must cover a contiguous model-order range");
-        next_head += count;
-        unsharded = !count;
+        first = last + 1;
     }
 }
 
@@ -865,44 +923,70 @@ std::vector<double> GraphRecallHip::lrfu_candidate(const std::vector<double> &sc
     return out;
 }
 
+// LRFU history (lrfu.hpp:43-101), as rules:
+//  - lambda is a decay in [0, 1], the hit fraction in (0, 1];
+//  - a round is opened by begin_round (its counter never wraps) and closed
+//    by its one commit; a candidate is derived from the committed scores
+//    only, so repeated previews in a round replace each other;
+//  - preview outside any round is a logic error, after the round's commit a
+//    no-op, and an empty score list withdraws the candidate;
+//  - reads see the candidate while there is one, else the committed
+//    scores, and 0 past their end;
+//  - a checkpoint is the committed state (shared, never copied); one from
+//    before the first round holds nothing, and restored scores are finite.
+namespace {
+bool unit_interval(double x, bool open_low) { return std::isfinite(x) && (open_low ? x > 0 : x >= 0) && x <= 1; }
+void check_lrfu_checkpoint(const LrfuState &cp) {
+    const bool before_rounds = cp.round == 0;
+    if (!cp.scores || (before_rounds && (cp.committed || !cp.scores->empty())))
+        throw std::invalid_argument("invalid LRFU checkpoint");
+    if (std::any_of(cp.scores->begin(), cp.scores->end(), [](double v) { return !std::isfinite(v); }))
+        throw std::invalid_argument("nonfinite LRFU checkpoint");
+}
+}  // namespace
+
 LrfuHistoryHip::LrfuHistoryHip(GraphRecallHip &device, double lambda, double top_fraction)
     : device_(&device), lambda_(lambda), fraction_(top_fraction) {
-    if (!std::isfinite(lambda) || lambda < 0 || lambda > 1 || !std::isfinite(top_fraction) || top_fraction <= 0 ||
-        top_fraction > 1)
+    if (!unit_interval(lambda, false) || !unit_interval(top_fraction, true))
         throw std::invalid_argument("invalid LRFU decay or hit fraction");
 }
 void LrfuHistoryHip::begin_round() {
-    if (++state_.round == 0) throw std::overflow_error("LRFU round overflow");
-    state_.committed = false;
+    if (state_.round == std::numeric_limits<uint64_t>::max()) {
+        state_.round = 0;  // the counter wrapped, as an increment would leave it
+        throw std::overflow_error("LRFU round overflow");
+    }
+    state_ = LrfuState{state_.scores, state_.round + 1, false};
     candidate_.reset();
 }
 void LrfuHistoryHip::preview(const std::vector<double> &scores) {
-    if (state_.committed) return;
-    if (!state_.round) throw std::logic_error("LRFU probe outside a round");
-    if (scores.empty()) {
-        candidate_.reset();
+    const bool open = state_.round != 0 && !state_.committed;
+    if (!open) {
+        if (state_.round == 0 && !state_.committed) throw std::logic_error("LRFU probe outside a round");
         return;
     }
-    candidate_ = std::make_shared<const std::vector<double>>(
-        device_->lrfu_candidate(scores, *state_.scores, lambda_, fraction_));
+    if (scores.empty())
+        candidate_ = nullptr;
+    else
+        candidate_ = std::make_shared<const std::vector<double>>(
+            device_->lrfu_candidate(scores, *state_.scores, lambda_, fraction_));
 }
 bool LrfuHistoryHip::commit() noexcept {
-    if (state_.committed || !candidate_) return false;
-    state_.scores = std::move(candidate_);
-    state_.committed = true;
-    return true;
+    const bool can = candidate_ != nullptr && !state_.committed;
+    if (can) {
+        state_.committed = true;
+        state_.scores.swap(candidate_);
+        candidate_ = nullptr;
+    }
+    return can;
 }
 double LrfuHistoryHip::score(size_t block) const noexcept {
-    const auto &v = candidate_ ? *candidate_ : *state_.scores;
-    return block < v.size() ? v[block] : 0;
+    const std::vector<double> &seen = candidate_ ? *candidate_ : *state_.scores;
+    return block >= seen.size() ? 0.0 : seen[block];
 }
 void LrfuHistoryHip::restore(const LrfuState &state) {
-    if (!state.scores || (!state.round && (state.committed || !state.scores->empty())))
-        throw std::invalid_argument("invalid LRFU checkpoint");
-    for (double v : *state.scores)
-        if (!std::isfinite(v)) throw std::invalid_argument("nonfinite LRFU checkpoint");
+    check_lrfu_checkpoint(state);
+    candidate_ = nullptr;
     state_ = state;
-    candidate_.reset();
 }
 
 size_t PageSoftmaxHip::device_bytes() const {

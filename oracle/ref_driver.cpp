@@ -15,7 +15,10 @@
 //   layerwise_mean_key_scores         (kvmem/src/host/layerwise_scoring.cpp)
 //   prepare_graph_accept, propagate_query_scores
 //                                     (kvmem/src/host/graph_recall.cpp)
-//   LrfuHistory::preview / score      (kvmem/include/kvmem/lrfu.hpp)
+//   LrfuHistory::preview / score, and its round/commit/restore rules
+//                                     (kvmem/include/kvmem/lrfu.hpp)
+//   PayloadLayout::validate           (kvmem/src/host/memory_contract.cpp)
+//   validate_native_layer_query       (kvmem/include/kvmem/native_layer_query.hpp)
 // Exceptions never cross this boundary: each entry returns 0 on success and a
 // nonzero code on a thrown exception, with the message in ref_last_error().
 #include "kvmem/graph_recall.hpp"
@@ -23,6 +26,8 @@
 #include "kvmem/layerwise_scoring.hpp"
 #include "kvmem/layerwise_selection.hpp"
 #include "kvmem/lrfu.hpp"
+#include "kvmem/memory_contract.hpp"
+#include "kvmem/native_layer_query.hpp"
 #include "kvmem/raw_kv_store.hpp"
 
 #include <cstring>
@@ -437,6 +442,94 @@ int ref_lrfu_preview(const double* history, uint32_t n_history, const double* sc
         h.begin_round();
         h.preview(std::vector<double>(scores, scores + n));
         for (uint32_t i = 0; i < n; ++i) out[i] = h.score(i);
+    });
+}
+
+// PayloadLayout::validate (kvmem/src/host/memory_contract.cpp:51-101) of a
+// layout whose planes are n rows of 9 values: layer, kind, offset, bytes,
+// alignment, token_stride, rank, head_begin, head_count.  Returns 0 when
+// valid, 1 with the message in ref_last_error() when it throws.
+int ref_payload_validate(const char* format, uint32_t version, uint32_t block_tokens, uint64_t record_bytes,
+                         uint64_t alignment, const uint64_t* planes, uint32_t n) {
+    return guarded([&] {
+        kvmem::PayloadLayout l;
+        l.format = format;
+        l.version = version;
+        l.block_tokens = block_tokens;
+        l.record_bytes = record_bytes;
+        l.alignment = alignment;
+        for (uint32_t i = 0; i < n; ++i) {
+            const uint64_t* r = planes + 9 * size_t(i);
+            kvmem::PayloadPlane p;
+            p.layer = uint32_t(r[0]);
+            p.kind = kvmem::PayloadPlaneKind(r[1]);
+            p.offset = r[2];
+            p.bytes = r[3];
+            p.alignment = r[4];
+            p.token_stride = r[5];
+            p.rank = uint32_t(r[6]);
+            p.head_begin = uint32_t(r[7]);
+            p.head_count = uint32_t(r[8]);
+            l.planes.push_back(p);
+        }
+        l.validate();
+    });
+}
+
+// validate_native_layer_query (kvmem/include/kvmem/native_layer_query.hpp:36-53)
+// of a Query at address `data` (never dereferenced); scalar 0 f32, 1 f16,
+// 2 bf16.
+int ref_native_query_validate(uintptr_t data, size_t bytes, uint32_t rows, uint32_t query_heads,
+                              uint32_t kv_heads, uint32_t head_dim, float scale, int scalar, size_t row_stride,
+                              size_t head_stride, size_t dimension_stride) {
+    return guarded([&] {
+        kvmem::NativeCurrentLayerQuery q;
+        q.data = reinterpret_cast<const void*>(data);
+        q.bytes = bytes;
+        q.rows = rows;
+        q.query_heads = query_heads;
+        q.kv_heads = kv_heads;
+        q.head_dim = head_dim;
+        q.attention_scale = scale;
+        q.scalar = kvmem::NativeQueryScalar(scalar);
+        q.row_stride = row_stride;
+        q.head_stride = head_stride;
+        q.dimension_stride = dimension_stride;
+        kvmem::validate_native_layer_query(q);
+    });
+}
+
+// LrfuHistory driven by a script of operations, to compare its state machine
+// with another implementation's.  ops[i]: 0 begin_round, 1 preview of the
+// next `lens[i]` values of `values`, 2 commit, 3 checkpoint (kept), 4 restore
+// of the kept checkpoint.  After each op, results[i] = 0 on success, 1 when
+// it threw (message dropped), 2 when commit returned false; scores[i * probe
+// + b] = score(b) for b < probe.
+int ref_lrfu_script(double lambda, double fraction, const int* ops, const uint32_t* lens, uint32_t n_ops,
+                    const double* values, uint32_t probe, int* results, double* scores) {
+    return guarded([&] {
+        kvmem::LrfuHistory h(lambda, fraction);
+        kvmem::LrfuState kept;
+        size_t cursor = 0;
+        for (uint32_t i = 0; i < n_ops; ++i) {
+            int r = 0;
+            try {
+                switch (ops[i]) {
+                case 0: h.begin_round(); break;
+                case 1:
+                    h.preview(std::vector<double>(values + cursor, values + cursor + lens[i]));
+                    break;
+                case 2: r = h.commit() ? 0 : 2; break;
+                case 3: kept = h.checkpoint(); break;
+                default: h.restore(kept); break;
+                }
+            } catch (const std::exception&) {
+                r = 1;
+            }
+            if (ops[i] == 1) cursor += lens[i];
+            results[i] = r;
+            for (uint32_t b = 0; b < probe; ++b) scores[size_t(i) * probe + b] = h.score(b);
+        }
     });
 }
 

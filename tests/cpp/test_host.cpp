@@ -7,6 +7,7 @@
 #include "kvmem_hip/kvmem_hip.hpp"
 #include "kvr_oracle.h"
 
+#include <dlfcn.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -16,6 +17,7 @@
 #include <cstring>
 #include <functional>
 #include <iostream>
+#include <map>
 #include <numeric>
 #include <random>
 #include <stdexcept>
@@ -681,8 +683,8 @@ void payload_layout() {
     auto rejects = [](const kh::PayloadLayout &l) {
         try {
             l.validate();
-        } catch (const std::invalid_argument &) {
-            return true;
+        } catch (const kh::MemoryError &e) {
+            return e.code() == kh::MemoryErrorCode::InvalidPlan;
         }
         return false;
     };
@@ -720,6 +722,194 @@ void payload_layout() {
         threw = true;
     }
     require(threw, "record plane with a mismatched row size accepted");
+}
+
+// ---- the reference's own validators, from oracle/_ref (when built) ---------
+struct RefBuild {
+    void *so = nullptr;
+    const char *(*last_error)() = nullptr;
+    int (*payload_validate)(const char *, uint32_t, uint32_t, uint64_t, uint64_t, const uint64_t *,
+                            uint32_t) = nullptr;
+    int (*native_query_validate)(uintptr_t, size_t, uint32_t, uint32_t, uint32_t, uint32_t, float, int, size_t,
+                                 size_t, size_t) = nullptr;
+    int (*lrfu_script)(double, double, const int *, const uint32_t *, uint32_t, const double *, uint32_t, int *,
+                       double *) = nullptr;
+};
+std::string g_exe_dir = ".";
+const RefBuild *reference_build() {
+    static RefBuild rb;
+    static bool tried = false;
+    if (!tried) {
+        tried = true;
+        const std::string path = g_exe_dir + "/../../../oracle/_ref/libkvmem_ref.so";
+        rb.so = dlopen(path.c_str(), RTLD_NOW | RTLD_LOCAL);
+        if (rb.so) {
+            rb.last_error = reinterpret_cast<decltype(rb.last_error)>(dlsym(rb.so, "ref_last_error"));
+            rb.payload_validate = reinterpret_cast<decltype(rb.payload_validate)>(dlsym(rb.so, "ref_payload_validate"));
+            rb.native_query_validate =
+                reinterpret_cast<decltype(rb.native_query_validate)>(dlsym(rb.so, "ref_native_query_validate"));
+            rb.lrfu_script = reinterpret_cast<decltype(rb.lrfu_script)>(dlsym(rb.so, "ref_lrfu_script"));
+        }
+    }
+    return rb.so && rb.payload_validate && rb.native_query_validate && rb.lrfu_script ? &rb : nullptr;
+}
+
+// PayloadLayout::validate against the reference's on random layouts: valid
+// ones (layers of one or two rank shards with explicit or "all" head ranges,
+// key/value/scale or packed planes, aligned back to back), each then mutated
+// in up to three fields.  Both must accept, or both reject with one message.
+void payload_layout_vs_reference() {
+    const RefBuild *ref = reference_build();
+    if (!ref) {
+        std::cout << "  reference build absent: nothing to compare" << std::endl;
+        return;
+    }
+    using K = kh::PayloadPlaneKind;
+    std::mt19937_64 rng(77);
+    auto pick = [&](uint64_t n) { return n ? rng() % n : 0; };
+    int accepted = 0, rejected = 0;
+    std::map<std::string, int> by_message;
+    for (int trial = 0; trial < 20000; ++trial) {
+        kh::PayloadLayout l;
+        l.format = pick(60) ? "fmt" : "";
+        l.version = pick(60) ? 1 + uint32_t(pick(7)) : 0;
+        l.block_tokens = uint32_t(1 + pick(128)) * (pick(60) ? 1 : 0);
+        l.alignment = uint64_t(1) << pick(9);
+        const uint32_t layers = 1 + uint32_t(pick(3));
+        uint64_t off = 0;
+        for (uint32_t layer = 0; layer < layers; ++layer) {
+            const uint32_t ranks = 1 + uint32_t(pick(2));
+            const bool sharded = ranks > 1 || pick(2);
+            uint32_t head = 0;
+            for (uint32_t rank = 0; rank < ranks; ++rank) {
+                const uint32_t hc = sharded && pick(12) ? 1 + uint32_t(pick(4)) : 0;
+                std::vector<K> kinds;
+                if (pick(5) == 0)
+                    kinds = {K::PackedKeyValue};
+                else {
+                    kinds = {K::Key, K::Value};
+                    if (pick(2)) kinds.push_back(K::KeyScale);
+                    if (pick(2)) kinds.push_back(K::ValueScale);
+                }
+                for (K k : kinds) {
+                    kh::PayloadPlane p;
+                    p.layer = layer * 3;
+                    p.kind = k;
+                    p.alignment = uint64_t(1) << pick(5);
+                    p.token_stride = k == K::PackedKeyValue ? 0 : 16 * (1 + pick(8));
+                    p.bytes = p.token_stride ? p.token_stride * std::max<uint32_t>(1, l.block_tokens) : 64 + pick(999);
+                    p.offset = (off + p.alignment - 1) / p.alignment * p.alignment;
+                    p.rank = rank;
+                    p.head_begin = sharded ? head : 0;
+                    p.head_count = hc;
+                    off = p.offset + p.bytes;
+                    l.planes.push_back(p);
+                }
+                head += hc;
+            }
+        }
+        l.record_bytes = (off + l.alignment - 1) / l.alignment * l.alignment + l.alignment * pick(2);
+        const int mutations = int(pick(4));
+        for (int m = 0; m < mutations && !l.planes.empty(); ++m) {
+            kh::PayloadPlane &p = l.planes[pick(l.planes.size())];
+            switch (pick(12)) {
+            case 0: p.offset += pick(3) ? pick(64) : 0 - pick(64); break;
+            case 1: p.bytes = pick(3) ? p.bytes + pick(300) : 0; break;
+            case 2: p.alignment = pick(4) ? uint64_t(1) << pick(12) : 3 + pick(5); break;
+            case 3: p.kind = K(pick(20) ? pick(5) : 5 + pick(3)); break;
+            case 4: p.head_begin = uint32_t(pick(6)); break;
+            case 5: p.head_count = pick(5) ? uint32_t(pick(6)) : 0xffffffffu; break;
+            case 6: p.token_stride = pick(3) ? p.token_stride + pick(40) : pick(2) ? 0 : ~uint64_t(0) / 3; break;
+            case 7: p.rank = uint32_t(pick(3)); break;
+            case 8: p.layer = uint32_t(pick(3) * 3); break;
+            case 9: l.record_bytes = pick(2) ? l.record_bytes - pick(512) : l.record_bytes + pick(512); break;
+            case 10: l.planes.erase(l.planes.begin() + long(pick(l.planes.size()))); break;
+            default: p.offset = pick(2) ? ~uint64_t(0) - pick(100) : p.offset; p.bytes += pick(2) ? ~uint64_t(0) / 2 : 0;
+            }
+        }
+        std::string mine;
+        try {
+            l.validate();
+        } catch (const kh::MemoryError &e) {
+            require(e.code() == kh::MemoryErrorCode::InvalidPlan, "payload error code");
+            mine = e.what();
+        }
+        std::vector<uint64_t> rows;
+        for (const auto &p : l.planes)
+            for (uint64_t v : {uint64_t(p.layer), uint64_t(p.kind), p.offset, p.bytes, p.alignment, p.token_stride,
+                               uint64_t(p.rank), uint64_t(p.head_begin), uint64_t(p.head_count)})
+                rows.push_back(v);
+        const int rc = ref->payload_validate(l.format.c_str(), l.version, l.block_tokens, l.record_bytes,
+                                             l.alignment, rows.data(), uint32_t(l.planes.size()));
+        const std::string theirs = rc ? ref->last_error() : "";
+        if (mine != theirs)
+            throw std::runtime_error("payload layout trial " + std::to_string(trial) + ": mine '" + mine +
+                                     "', reference '" + theirs + "'");
+        (mine.empty() ? accepted : rejected)++;
+        if (!mine.empty()) ++by_message[mine];
+    }
+    require(accepted > 1000 && rejected > 1000, "payload fuzz reached both outcomes");
+    require(by_message.size() == 12, "payload fuzz reached every rule");
+    std::cout << "  " << accepted << " accepted, " << rejected << " rejected, all as the reference" << std::endl;
+    for (const auto &m : by_message) std::cout << "    " << m.second << " x " << m.first << std::endl;
+}
+
+// validate_native_layer_query against the reference's on random geometries:
+// the six axis orders, padded strides, counts of 1, equal strides,
+// overlapping and huge strides, extents around the exact span.
+void native_query_vs_reference() {
+    const RefBuild *ref = reference_build();
+    if (!ref) {
+        std::cout << "  reference build absent: nothing to compare" << std::endl;
+        return;
+    }
+    std::mt19937_64 rng(78);
+    auto pick = [&](uint64_t n) { return n ? rng() % n : 0; };
+    int accepted = 0, rejected = 0;
+    for (int trial = 0; trial < 50000; ++trial) {
+        kh::NativeCurrentLayerQuery q;
+        const int scalar = int(pick(3));
+        const size_t el = scalar == 0 ? 4 : 2;
+        q.scalar = kh::NativeQueryScalar(scalar);
+        q.data = reinterpret_cast<const void *>(uintptr_t(4096) + (pick(8) ? 0 : pick(4)));
+        q.rows = uint32_t(pick(6));
+        q.kv_heads = 1 + uint32_t(pick(4)) * (pick(20) ? 1 : 0);
+        q.query_heads = q.kv_heads * uint32_t(pick(4)) + (pick(10) ? 0 : 1);
+        q.head_dim = uint32_t(1 + pick(8)) * (pick(20) ? 1 : 0);
+        q.attention_scale = pick(15) ? float(pick(100)) / 64 : (pick(2) ? -1.f : NAN);
+        uint32_t count[3] = {q.rows, q.query_heads, q.head_dim};
+        int order[3] = {0, 1, 2};
+        std::shuffle(order, order + 3, rng);
+        size_t stride[3], span = el;
+        for (int i = 0; i < 3; ++i) {
+            const int a = order[i];
+            stride[a] = span + el * pick(3) * (pick(3) == 0);
+            if (pick(8) == 0) stride[a] = pick(2) ? span - el : el * pick(3);
+            if (pick(40) == 0) stride[a] = ~size_t(0) / 2 + pick(3);
+            if (pick(40) == 0) stride[a] += 1;
+            span += stride[a] * (count[a] ? count[a] - 1 : 0);
+        }
+        q.row_stride = stride[0];
+        q.head_stride = stride[1];
+        q.dimension_stride = stride[2];
+        q.bytes = pick(4) ? span : span + el * (pick(2) ? 1 : -1);
+        std::string mine;
+        try {
+            kh::validate_native_layer_query(q);
+        } catch (const std::invalid_argument &e) {
+            mine = e.what();
+        }
+        const int rc = ref->native_query_validate(uintptr_t(q.data), q.bytes, q.rows, q.query_heads, q.kv_heads,
+                                                  q.head_dim, q.attention_scale, scalar, q.row_stride,
+                                                  q.head_stride, q.dimension_stride);
+        const std::string theirs = rc ? ref->last_error() : "";
+        if (mine != theirs)
+            throw std::runtime_error("native query trial " + std::to_string(trial) + ": mine '" + mine +
+                                     "', reference '" + theirs + "'");
+        (mine.empty() ? accepted : rejected)++;
+    }
+    require(accepted > 5000 && rejected > 5000, "native query fuzz reached both outcomes");
+    std::cout << "  " << accepted << " accepted, " << rejected << " rejected, all as the reference" << std::endl;
 }
 
 // span_coefficients (sorted sweep) against the oracle's pair-by-pair
@@ -815,19 +1005,86 @@ void graph() {
     require(h.score(0) == 0 && h.score(2) == .6, "LRFU restore");
 }
 
+// LrfuHistoryHip against the reference's LrfuHistory on random scripts of
+// rounds, previews (repeated, empty, of varying length), commits,
+// checkpoints and restores: the same outcome of every step (success, throw,
+// refused commit) and the same scores bit for bit after it.
+void lrfu_vs_reference() {
+    const RefBuild *ref = reference_build();
+    require(ref != nullptr, "the reference build (oracle/_ref) is needed for this test");
+    kh::GraphRecallHip dev(0);
+    std::mt19937_64 rng(79);
+    std::uniform_real_distribution<double> val(-1, 1);
+    const uint32_t probe = 12;
+    for (int script = 0; script < 60; ++script) {
+        const double lambda = std::vector<double>{0, .25, .5, 1}[rng() % 4];
+        const double fraction = std::vector<double>{.1, .5, .9, 1}[rng() % 4];
+        const uint32_t n_ops = 6 + uint32_t(rng() % 20);
+        std::vector<int> ops(n_ops);
+        std::vector<uint32_t> lens(n_ops, 0);
+        std::vector<double> values;
+        for (uint32_t i = 0; i < n_ops; ++i) {
+            const int r = int(rng() % 10);
+            ops[i] = r < 2 ? 0 : r < 6 ? 1 : r < 8 ? 2 : r < 9 ? 3 : 4;
+            if (ops[i] == 1) {
+                lens[i] = rng() % 8 == 0 ? 0 : 1 + uint32_t(rng() % probe);
+                for (uint32_t j = 0; j < lens[i]; ++j) values.push_back(rng() % 5 == 0 ? 0.0 : val(rng));
+            }
+        }
+        std::vector<int> want_r(n_ops);
+        std::vector<double> want_s(size_t(n_ops) * probe);
+        require(ref->lrfu_script(lambda, fraction, ops.data(), lens.data(), n_ops, values.data(), probe,
+                                 want_r.data(), want_s.data()) == 0,
+                "reference LRFU script");
+        kh::LrfuHistoryHip h(dev, lambda, fraction);
+        kh::LrfuState kept;
+        size_t cursor = 0;
+        for (uint32_t i = 0; i < n_ops; ++i) {
+            int r = 0;
+            try {
+                switch (ops[i]) {
+                case 0: h.begin_round(); break;
+                case 1: h.preview(std::vector<double>(values.begin() + long(cursor),
+                                                      values.begin() + long(cursor + lens[i])));
+                    break;
+                case 2: r = h.commit() ? 0 : 2; break;
+                case 3: kept = h.checkpoint(); break;
+                default: h.restore(kept); break;
+                }
+            } catch (const std::exception &) {
+                r = 1;
+            }
+            if (ops[i] == 1) cursor += lens[i];
+            const std::string at = "LRFU script " + std::to_string(script) + " step " + std::to_string(i);
+            require(r == want_r[i], at + ": outcome differs from the reference");
+            for (uint32_t b = 0; b < probe; ++b) {
+                const double got = h.score(b), want = want_s[size_t(i) * probe + b];
+                require(std::memcmp(&got, &want, 8) == 0, at + ": score differs from the reference");
+            }
+        }
+    }
+}
+
 }  // namespace
 
 int main(int argc, char **argv) {
     const bool gpu = argc > 1 && std::string(argv[1]) == "--gpu";
+    {
+        const std::string self = argv[0];
+        const size_t slash = self.rfind('/');
+        if (slash != std::string::npos) g_exe_dir = self.substr(0, slash);
+    }
     std::vector<std::pair<const char *, std::function<void()>>> tests = {
         {"frames", frames}, {"native_query_geometry", native_query_geometry},
         {"workspace_geometry", workspace_geometry}, {"stagein_without_state", stagein_without_state},
-        {"graph_spans", graph_spans}, {"payload_layout", payload_layout}};
+        {"graph_spans", graph_spans}, {"payload_layout", payload_layout},
+        {"payload_layout_vs_reference", payload_layout_vs_reference},
+        {"native_query_vs_reference", native_query_vs_reference}};
     if (gpu)
         tests = {{"qualification", qualification}, {"current_layer", current_layer}, {"pick", pick},
                  {"stagein", stagein},           {"meank", meank},                 {"transfer", transfer},
                  {"capture", capture}, {"attention", attention}, {"stagein_raw_k", stagein_raw_k},
-                 {"stageout", stageout}, {"graph", graph}};
+                 {"stageout", stageout}, {"graph", graph}, {"lrfu_vs_reference", lrfu_vs_reference}};
     for (auto &[name, fn] : tests) {
         std::cout << "RUN  " << name << std::endl;
         try {

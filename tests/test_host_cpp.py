@@ -19,10 +19,10 @@ def _run(mode, timeout):
 
 def test_host_layer_cpu():
     out = _run("--cpu", 60)
-    assert out.count("PASS") == 6
+    assert out.count("PASS") == 8
 
 
 @pytest.mark.gpu
 def test_host_layer_gpu():
     out = _run("--gpu", 110)
-    assert out.count("PASS") == 11
+    assert out.count("PASS") == 12
