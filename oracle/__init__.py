@@ -67,6 +67,8 @@ def _load_oracle() -> C.CDLL:
         "orc_rope_neox_row": (None, [_P, _u32, _u32, _u32, _P, C.c_float]),
         "orc_fwht_row": (None, [_P, _u32, _u32]),
         "orc_rope_fwht_rows": (C.c_int, [_P, C.c_int, _u32, _u32, C.c_int64, _u32, _u32, _P, _u32, _P]),
+        "orc_rope_fwht_rows_variant": (C.c_int, [_P, C.c_int, _u32, _u32, C.c_int64, _u32, _u32, _P, _u32,
+                                                 C.c_int, _P]),
         "orc_gather_rope": (C.c_int, [_P, C.c_int, _u32, _u64, _u32, _P, _u32, _u32, _u32, _P, _u32,
                                       C.c_int64, _P]),
         "orc_dequant_q5_0": (None, [_P, _P]),
@@ -526,6 +528,23 @@ def rope_fwht_rows(rows: np.ndarray, fmt: int, width: int, n: int, pos0: int, he
     th = _c(theta if theta is not None else np.zeros(1), np.float32)
     out = np.zeros_like(rows)
     _check(lib.orc_rope_fwht_rows(_ptr(rows), fmt, width, n, pos0, head_dim, n_rot, _ptr(th), fwht, _ptr(out)))
+    return out
+
+
+VAR_UNFUSED_ROT, VAR_UNFUSED_Q4, VAR_SIN_UP, VAR_SIN_DOWN, VAR_COS_UP, VAR_COS_DOWN, VAR_RNE = \
+    1, 2, 4, 8, 16, 32, 64
+
+
+def rope_fwht_rows_variant(rows: np.ndarray, fmt: int, width: int, n: int, pos0: int, head_dim: int, n_rot: int,
+                           theta: np.ndarray, fwht: int, variant: int) -> np.ndarray:
+    """The transform with other floating-point choices (VAR_* bits), for
+    sensitivity tests: unfused rotation or q4_0 multiply-add, sin/cos one ulp
+    off, ties to even in the requantizers."""
+    rows = _c(rows, np.uint8)
+    th = _c(theta if theta is not None else np.zeros(1), np.float32)
+    out = np.zeros_like(rows)
+    _check(lib.orc_rope_fwht_rows_variant(_ptr(rows), fmt, width, n, pos0, head_dim, n_rot, _ptr(th), fwht,
+                                          variant, _ptr(out)))
     return out
 
 

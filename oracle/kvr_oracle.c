@@ -1000,8 +1000,86 @@ void orc_fwht_row(float *row, uint32_t width, uint32_t n) {
     }
 }
 
-int orc_rope_fwht_rows(const uint8_t *rows, int fmt, uint32_t width, uint32_t n, int64_t pos0,
-                       uint32_t head_dim, uint32_t n_rot, const float *theta, uint32_t fwht, uint8_t *out) {
+/* Variants of the transform's floating-point choices, for the sensitivity
+ * tests only (variant 0 is the transform itself):
+ *   ORC_VAR_UNFUSED_ROT   x0*c - x1*s and x0*s + x1*c with every product
+ *                         and the sum rounded separately
+ *   ORC_VAR_UNFUSED_Q4    q4_0's x*id + 8.5 rounded twice
+ *   ORC_VAR_SIN_UP/_DOWN, ORC_VAR_COS_UP/_DOWN
+ *                         sin or cos one binary32 ulp away (toward +/-inf)
+ *   ORC_VAR_RNE           q8_0 codes rint(x*id), q4_0 codes rint(x*id) + 8:
+ *                         ties to even instead of the reference's rules */
+static void quant_q8_0_var(const float *x, uint8_t *block, int variant) {
+    if (!(variant & ORC_VAR_RNE)) {
+        orc_quant_q8_0(x, block);
+        return;
+    }
+    float amax = 0.0f;
+    for (int j = 0; j < ORC_QK; ++j) amax = fmaxf(amax, fabsf(x[j]));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    store_u16(block, orc_f32_to_f16(d));
+    int8_t *qs = (int8_t *)(block + 2);
+    for (int j = 0; j < ORC_QK; ++j) qs[j] = (int8_t)rintf(x[j] * id);
+}
+
+static void quant_q4_0_var(const float *x, uint8_t *block, int variant) {
+    if (!(variant & (ORC_VAR_UNFUSED_Q4 | ORC_VAR_RNE))) {
+        orc_quant_q4_0(x, block);
+        return;
+    }
+    float amax = 0.0f, vmax = 0.0f;
+    for (int j = 0; j < ORC_QK; ++j)
+        if (amax < fabsf(x[j])) {
+            amax = fabsf(x[j]);
+            vmax = x[j];
+        }
+    const float d = vmax / -8.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    store_u16(block, orc_f32_to_f16(d));
+    for (int j = 0; j < ORC_QK / 2; ++j) {
+        int q[2];
+        for (int h = 0; h < 2; ++h) {
+            const float p = x[j + h * ORC_QK / 2] * id;
+            q[h] = variant & ORC_VAR_RNE ? (int)rintf(p) + 8 : (int)(p + 8.5f);
+            if (q[h] > 15) q[h] = 15;
+        }
+        block[2 + j] = (uint8_t)((q[0] & 15) | ((q[1] & 15) << 4));
+    }
+}
+
+static void rope_row_var(float *row, uint32_t width, uint32_t head_dim, uint32_t n_rot, const float *theta,
+                         float pos, int variant) {
+    if (!(variant & (ORC_VAR_UNFUSED_ROT | ORC_VAR_SIN_UP | ORC_VAR_SIN_DOWN | ORC_VAR_COS_UP | ORC_VAR_COS_DOWN))) {
+        orc_rope_neox_row(row, width, head_dim, n_rot, theta, pos);
+        return;
+    }
+    const uint32_t half = n_rot / 2;
+    for (uint32_t h = 0; h < width / head_dim; ++h) {
+        float *x = row + (size_t)h * head_dim;
+        for (uint32_t i = 0; i < half; ++i) {
+            float s, c;
+            orc_rope_sincos(pos * theta[i], &s, &c);
+            if (variant & ORC_VAR_SIN_UP) s = nextafterf(s, INFINITY);
+            if (variant & ORC_VAR_SIN_DOWN) s = nextafterf(s, -INFINITY);
+            if (variant & ORC_VAR_COS_UP) c = nextafterf(c, INFINITY);
+            if (variant & ORC_VAR_COS_DOWN) c = nextafterf(c, -INFINITY);
+            const float x0 = x[i], x1 = x[i + half];
+            if (variant & ORC_VAR_UNFUSED_ROT) {
+                const float a = x0 * c, b = x1 * s, e = x0 * s, f = x1 * c;
+                x[i] = a - b;
+                x[i + half] = e + f;
+            } else {
+                x[i] = fmaf(x0, c, -(x1 * s));
+                x[i + half] = fmaf(x0, s, x1 * c);
+            }
+        }
+    }
+}
+
+int orc_rope_fwht_rows_variant(const uint8_t *rows, int fmt, uint32_t width, uint32_t n, int64_t pos0,
+                               uint32_t head_dim, uint32_t n_rot, const float *theta, uint32_t fwht, int variant,
+                               uint8_t *out) {
     if ((fmt != ORC_FMT_Q8_0 && fmt != ORC_FMT_Q4_0) || !width || width % ORC_QK || !head_dim ||
         width % head_dim || n_rot % 2 || n_rot > head_dim || (n_rot && !theta) ||
         (fwht && (width % fwht || (fwht != 64 && fwht != 128 && fwht != 256 && fwht != 512))))
@@ -1016,15 +1094,20 @@ int orc_rope_fwht_rows(const uint8_t *rows, int fmt, uint32_t width, uint32_t n,
             if (fmt == ORC_FMT_Q8_0) orc_dequant_q8_0(in + (size_t)b * bb, row + (size_t)b * ORC_QK);
             else orc_dequant_q4_0(in + (size_t)b * bb, row + (size_t)b * ORC_QK);
         }
-        orc_rope_neox_row(row, width, head_dim, n_rot, theta, (float)(pos0 + t));
+        rope_row_var(row, width, head_dim, n_rot, theta, (float)(pos0 + t), variant);
         if (fwht) orc_fwht_row(row, width, fwht);
         for (uint32_t b = 0; b < bpr; ++b) {
-            if (fmt == ORC_FMT_Q8_0) orc_quant_q8_0(row + (size_t)b * ORC_QK, o + (size_t)b * bb);
-            else orc_quant_q4_0(row + (size_t)b * ORC_QK, o + (size_t)b * bb);
+            if (fmt == ORC_FMT_Q8_0) quant_q8_0_var(row + (size_t)b * ORC_QK, o + (size_t)b * bb, variant);
+            else quant_q4_0_var(row + (size_t)b * ORC_QK, o + (size_t)b * bb, variant);
         }
     }
     free(row);
     return ORC_OK;
+}
+
+int orc_rope_fwht_rows(const uint8_t *rows, int fmt, uint32_t width, uint32_t n, int64_t pos0,
+                       uint32_t head_dim, uint32_t n_rot, const float *theta, uint32_t fwht, uint8_t *out) {
+    return orc_rope_fwht_rows_variant(rows, fmt, width, n, pos0, head_dim, n_rot, theta, fwht, 0, out);
 }
 
 /* The gather with the raw-K transform: slot s of the selection holds page

@@ -165,6 +165,15 @@ void orc_rope_neox_row(float *row, uint32_t width, uint32_t head_dim, uint32_t n
 void orc_fwht_row(float *row, uint32_t width, uint32_t n);
 int orc_rope_fwht_rows(const uint8_t *rows, int fmt, uint32_t width, uint32_t n, int64_t pos0,
                        uint32_t head_dim, uint32_t n_rot, const float *theta, uint32_t fwht, uint8_t *out);
+/* The same with other floating-point choices (sensitivity tests only; a
+ * bit set of ORC_VAR_*; 0 is orc_rope_fwht_rows). */
+enum {
+    ORC_VAR_UNFUSED_ROT = 1, ORC_VAR_UNFUSED_Q4 = 2, ORC_VAR_SIN_UP = 4, ORC_VAR_SIN_DOWN = 8,
+    ORC_VAR_COS_UP = 16, ORC_VAR_COS_DOWN = 32, ORC_VAR_RNE = 64
+};
+int orc_rope_fwht_rows_variant(const uint8_t *rows, int fmt, uint32_t width, uint32_t n, int64_t pos0,
+                               uint32_t head_dim, uint32_t n_rot, const float *theta, uint32_t fwht, int variant,
+                               uint8_t *out);
 int orc_gather_rope(const uint8_t *history, int fmt, uint32_t width, uint64_t tokens, uint32_t page_tokens,
                     const uint32_t *selected, uint32_t k, uint32_t head_dim, uint32_t n_rot,
                     const float *theta, uint32_t fwht, int64_t pos_base, uint8_t *slots);

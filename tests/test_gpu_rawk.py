@@ -108,3 +108,83 @@ def test_rejects(ctx):
     assert call(fwht=512) == K._capi.ERR_INVALID          # does not divide the width
     assert call(theta=None) == K._capi.ERR_INVALID
     pin.free()
+
+
+# ---- requantization at exact ties -------------------------------------------
+# The rows of tests/test_oracle_requant_ties.py: products x*id that are exact
+# half-integers after the Walsh-Hadamard transform, with the expected codes
+# stated in exact rationals (ties away from zero for q8_0, truncation after
+# +8.5 for q4_0).  A device or oracle switched to ties-to-even fails here.
+import test_oracle_requant_ties as T  # noqa: E402
+
+
+def _tie_gather(ctx, fmt, vectors, row_fn, expect_fn):
+    per_row = 4  # four 64-value runs per 256-wide row
+    rows, want = [], []
+    for i in range(0, len(vectors) - len(vectors) % per_row, per_row):
+        rows.append(b"".join(row_fn(c) for c in vectors[i:i + per_row]))
+        want.append(b"".join(expect_fn(c)[0] for c in vectors[i:i + per_row]))
+    tokens, pt, width = len(rows), 16, 256
+    hist = np.frombuffer(b"".join(rows), np.uint8)
+    pages = (tokens + pt - 1) // pt
+    sel = np.arange(pages, dtype=np.uint32)
+    row = K.row_bytes(fmt, width)
+    pin = K.PinnedBuffer(hist.size)
+    pin.numpy()[:] = hist
+    slots = zeros(pages * pt * row, np.uint8)
+    th = dev(np.zeros(1, np.float32))
+    plane = K.make_plane(pin, fmt, width, tokens, K.GATHER_ROPE_FWHT, slots,
+                         rope=dict(head_dim=64, n_rot=0, theta=th, fwht=64, pos_base=0))
+    ctx.stage_in([plane], pt, dev(sel), dev(np.array([pages], np.uint32)), pages)
+    ctx.check()
+    sync()
+    got = host(slots, np.uint8)[:tokens * row]
+    pin.free()
+    oracle = O.gather_rope(hist, fmt, width, tokens, pt, sel, 64, 0, None, 64)[:tokens * row]
+    return got, np.frombuffer(b"".join(want), np.uint8), oracle
+
+
+def test_q8_0_ties_on_device(ctx):
+    got, exact, oracle = _tie_gather(ctx, K.FMT_Q8_0, T.Q8_CODES, T.q8_row, T.expected_q8)
+    assert np.array_equal(oracle, exact)
+    assert np.array_equal(got, exact)
+
+
+def test_q4_0_ties_on_device(ctx):
+    got, exact, oracle = _tie_gather(ctx, K.FMT_Q4_0, T.Q4_CODES, T.q4_row, T.expected_q4)
+    assert np.array_equal(oracle, exact)
+    assert np.array_equal(got, exact)
+
+
+def test_requant_q8_0_half_ratio_blocks(ctx):
+    """GATHER_REQUANT_Q8_0 on blocks whose codes include +-m/2 of the block's
+    largest |code| m (x*id = +-63.5 there, the only half-integer this mode can
+    produce), over many block scales: bit-exact against the oracle."""
+    rng = np.random.default_rng(31)
+    tokens, width, pt = 512, 256, 64
+    nb = width // 32
+    blocks = np.zeros((tokens, nb, 34), np.uint8)
+    for t in range(tokens):
+        for b in range(nb):
+            m = int(rng.integers(1, 64)) * 2
+            codes = rng.integers(-m, m + 1, 32)
+            codes[0] = m if rng.integers(2) else -m
+            codes[1:9] = rng.choice([m // 2, -(m // 2)], 8)
+            blocks[t, b, :2] = np.frombuffer(np.float16(rng.uniform(0.001, 4.0)).tobytes(), np.uint8)
+            blocks[t, b, 2:] = codes.astype(np.int8).view(np.uint8)
+    hist = blocks.reshape(-1)
+    sel = np.array([0, 3, 5, 7], np.uint32)
+    row = K.row_bytes(K.FMT_Q8_0, width)
+    pin = K.PinnedBuffer(hist.size)
+    pin.numpy()[:] = hist
+    slots = zeros(len(sel) * pt * row, np.uint8)
+    plane = K.make_plane(pin, K.FMT_Q8_0, width, tokens, K.GATHER_REQUANT_Q8_0, slots)
+    ctx.stage_in([plane], pt, dev(sel), dev(np.array([len(sel)], np.uint32)), len(sel))
+    ctx.check()
+    sync()
+    want = O.gather(hist, K.FMT_Q8_0, width, tokens, pt, sel, O.GATHER_REQUANT_Q8_0)
+    got = host(slots, np.uint8)
+    pin.free()
+    assert np.array_equal(got, want)
+    codes = want.reshape(-1, 34)[:, 2:].view(np.int8)
+    assert np.count_nonzero(np.abs(codes.astype(np.int32)) == 64) > 1000  # the +-63.5 products
