@@ -18,6 +18,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <functional>
 #include <memory>
 #include <stdexcept>
 #include <string>
@@ -94,6 +95,19 @@ struct PageSummaries {
     uint32_t pages = 0, page_tokens = 0, kv_heads = 0, head_dim = 0;
 };
 
+// Host binary32 page means, the form RawKvStore keeps (mean_k,
+// raw_kv_store.cpp:606-625): `read(page, layer, out)` writes the `width`
+// (= kv_heads*head_dim) means of the page starting at token
+// page*block_tokens, for pages where `has(page)` holds.
+struct HostMeanSource {
+    uint32_t layers = 0, width = 0, block_tokens = 0;
+    std::function<bool(uint32_t page)> has;
+    std::function<void(uint32_t page, uint32_t layer, float *out)> read;
+    // tokens the page's mean covers in `layer` (mean_k_tokens), for the
+    // current-layer coverage check
+    std::function<uint32_t(uint32_t page, uint32_t layer)> tokens;
+};
+
 // Media (image) token ranges [first, end) in recording order
 // (KvMemStore::set_media_ranges, kvmem/include/kvmem/kvmem_store.hpp:504).
 using MediaRanges = std::vector<std::pair<uint32_t, uint32_t>>;
@@ -126,10 +140,51 @@ public:
     // page_softmax_scores over every layer with rows (graph_recall.cpp:322-394).
     std::vector<double> score(const PageSummaries &, PageQueryView, const QueryScoreFrame &,
                               GqaScoreAggregation = GqaScoreAggregation::Mean);
+    // PageSoftmaxCuda::score(const RawKvStore&, ...) (page_softmax_cuda.hpp:24,
+    // page_softmax.cu:202-279): the binary32 means of the frame's scored
+    // pages are read on the host one layer at a time, moved to the device
+    // and rounded there to the fp16 operands (with recall_fp16's checks),
+    // then scored as above.  A frame entry may start at any page of the
+    // store; one that is not a whole stored page is a stale index extent
+    // (std::invalid_argument).  Borrowed workspaces never allocate here
+    // either.
+    std::vector<double> score(const HostMeanSource &, PageQueryView, const QueryScoreFrame &,
+                              GqaScoreAggregation = GqaScoreAggregation::Mean);
+    // The same over any store with RawKvStore's reading interface
+    // (kvmem/include/kvmem/raw_kv_store.hpp:105-116): config().n_layer,
+    // config().n_embd_k, config().block_tokens, has_block(page) and
+    // mean_k(page, layer, float *out), so an adapter holding a RawKvStore
+    // passes it unchanged.
+    template <class Store, class = decltype(std::declval<const Store &>().mean_k(0u, 0u, (float *)nullptr))>
+    std::vector<double> score(const Store &keys, PageQueryView v, const QueryScoreFrame &frame,
+                              GqaScoreAggregation aggregation = GqaScoreAggregation::Mean) {
+        return score(mean_source(keys), v, frame, aggregation);
+    }
+    // A HostMeanSource reading a RawKvStore-like store (valid while it lives).
+    template <class Store> static HostMeanSource mean_source(const Store &keys) {
+        HostMeanSource src;
+        src.layers = uint32_t(keys.config().n_layer);
+        src.width = uint32_t(keys.config().n_embd_k);
+        src.block_tokens = uint32_t(keys.config().block_tokens);
+        src.has = [&keys](uint32_t page) { return bool(keys.has_block(page)); };
+        src.read = [&keys](uint32_t page, uint32_t layer, float *out) { keys.mean_k(page, layer, out); };
+        src.tokens = [&keys](uint32_t page, uint32_t layer) { return uint32_t(keys.mean_k_tokens(page, layer)); };
+        return src;
+    }
     // One layer's native Query on its producer stream, Mean
     // (page_softmax.cu:281-396).  The stream must not be capturing.
     std::vector<double> score_current_layer(const PageSummaries &, NativeCurrentLayerQuery,
                                             const QueryScoreFrame &, void *producer_stream);
+    // The same from host binary32 means (page_softmax.cu:281-396): every
+    // frame entry must be a whole page whose target-layer mean covers exactly
+    // its count of tokens, else std::invalid_argument.
+    std::vector<double> score_current_layer(const HostMeanSource &, NativeCurrentLayerQuery,
+                                            const QueryScoreFrame &, void *producer_stream);
+    template <class Store, class = decltype(std::declval<const Store &>().mean_k(0u, 0u, (float *)nullptr))>
+    std::vector<double> score_current_layer(const Store &keys, NativeCurrentLayerQuery q,
+                                            const QueryScoreFrame &frame, void *producer_stream) {
+        return score_current_layer(mean_source(keys), q, frame, producer_stream);
+    }
     // pick_scored_blocks (kvmem_store.cpp:418-451) on the device: mandatory
     // pages first, then by score with the tie rule; ascending ids.
     // Mandatory pages beyond the budget: std::runtime_error, as there.

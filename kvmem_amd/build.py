@@ -5,6 +5,9 @@
   tests/cpp/build/test_host  C++ test of the host layer (links the oracle as checker)
   oracle/liboracle.so        the CPU restatement used by tests (checker only)
   oracle/_ref/*.so           the reference's own host sources, when present
+  tests/cpp/build/test_reference_boundary
+                             the adapter glue against the reference's headers
+                             and host library (test only, when present)
 
 Every call recompiles (no stale-object reuse).  Objects are compiled in
 parallel and linked with hipcc.
@@ -102,6 +105,30 @@ def build_host_test(verbose: bool = False) -> str:
     return HOST_TEST
 
 
+REF_INCLUDE = os.path.join(os.environ.get("KVR_REFERENCE_ROOT", "/root/reference"), "kvmem", "include")
+REF_LIB = os.path.join(ORACLE, "_ref", "libkvmem_ref.so")
+BOUNDARY_TEST_SRC = os.path.join(ROOT, "tests", "cpp", "test_reference_boundary.cpp")
+BOUNDARY_TEST = os.path.join(ROOT, "tests", "cpp", "build", "test_reference_boundary")
+
+
+def build_boundary_test(verbose: bool = False) -> str:
+    """tests/cpp/test_reference_boundary.cpp: the adapter glue compiled against
+    the reference's own headers and linked with its host library (oracle/_ref).
+    Built only where the reference tree is present; test-only."""
+    if not (os.path.isdir(REF_INCLUDE) and os.path.exists(REF_LIB)):
+        return ""
+    hipcc = _hipcc()
+    os.makedirs(os.path.dirname(BOUNDARY_TEST), exist_ok=True)
+    tmp = BOUNDARY_TEST + ".tmp"
+    libdir = os.path.dirname(LIB)
+    refdir = os.path.dirname(REF_LIB)
+    _run([hipcc, "-O2", "-std=c++17", "-Wall", "-I", REF_INCLUDE, "-I", os.path.join(ROOT, "include"),
+          BOUNDARY_TEST_SRC, "-o", tmp, "-L", libdir, "-lkvmem_hip", "-lkvrecall", "-L", refdir, "-lkvmem_ref",
+          "-Wl,-rpath,$ORIGIN/../../../kvmem_amd", "-Wl,-rpath,$ORIGIN/../../../oracle/_ref"], verbose)
+    os.replace(tmp, BOUNDARY_TEST)
+    return BOUNDARY_TEST
+
+
 def build_oracle(verbose: bool = False) -> None:
     jobs = str(min(8, os.cpu_count() or 1))
     _run(["make", "-C", ORACLE, "-B", f"-j{jobs}", "all"], verbose)
@@ -112,6 +139,7 @@ def build_all(verbose: bool = False) -> None:
     build_host(verbose)
     build_oracle(verbose)
     build_host_test(verbose)
+    build_boundary_test(verbose)
 
 
 if __name__ == "__main__":

@@ -171,7 +171,58 @@ struct PageSoftmaxHip::Impl {
     // [pages][2], the grouped pass's selection [pages] and count
     uint32_t *fixed = nullptr, *groups = nullptr, *sel2 = nullptr, *cnt2 = nullptr;
     size_t page_cap = 0;
+    // staging of host page means: binary32 [pages][width], counts of one,
+    // fp16 operands
+    float *msum = nullptr;
+    uint32_t *mcount = nullptr;
+    uint16_t *m16 = nullptr;
+    size_t mean_cap = 0;  // elements
+    uint32_t mean_pages = 0;
     std::vector<void *> owned;
+
+    void score_layer(const uint16_t *summaries, const float *base, const PageQueryView &v, uint32_t layer,
+                     uint32_t pages, uint32_t batch, kvr_aggregation agg, uint32_t active, bool &accumulate,
+                     hipStream_t s);
+    uint32_t check_view(const PageQueryView &v, uint32_t layers);
+    hipStream_t current_layer_stream(const NativeCurrentLayerQuery &q, uint32_t pages, void *producer_stream);
+    std::vector<double> current_layer(const uint16_t *summaries, const NativeCurrentLayerQuery &q,
+                                      const QueryScoreFrame &frame, hipStream_t s);
+
+    static size_t mean_bytes(uint32_t pages, uint32_t width) {
+        return align256(size_t(pages) * width * 4) + align256(size_t(pages) * 4) + align256(size_t(pages) * width * 2);
+    }
+    void carve_means(uint8_t *b, uint32_t pages, uint32_t width) {
+        msum = reinterpret_cast<float *>(b);
+        b += align256(size_t(pages) * width * 4);
+        mcount = reinterpret_cast<uint32_t *>(b);
+        b += align256(size_t(pages) * 4);
+        m16 = reinterpret_cast<uint16_t *>(b);
+        mean_cap = size_t(pages) * width;
+        mean_pages = pages;
+    }
+    // Means staging for `pages` x `width`; the counts are all one.
+    void reserve_means(uint32_t pages, uint32_t width) {
+        const size_t need = size_t(pages) * width;
+        if (borrowed) {
+            if (need > mean_cap || pages > mean_pages)
+                throw std::length_error("page softmax exceeds its planned device workspace");
+        } else if (need > mean_cap || pages > mean_pages) {
+            hip_ok(hipStreamSynchronize(stream()), "hipStreamSynchronize");
+            void *p = nullptr;
+            hip_ok(hipMalloc(&p, mean_bytes(pages, width)), "hipMalloc page means");
+            owned.push_back(p);
+            carve_means(static_cast<uint8_t *>(p), pages, width);
+            ones_pages = 0;
+        }
+        if (ones_pages < pages) {
+            const std::vector<uint32_t> ones(pages, 1u);
+            hip_ok(hipMemcpyAsync(mcount, ones.data(), size_t(pages) * 4, hipMemcpyHostToDevice, stream()),
+                   "counts H2D");
+            hip_ok(hipStreamSynchronize(stream()), "hipStreamSynchronize");
+            ones_pages = pages;
+        }
+    }
+    uint32_t ones_pages = 0;
 
     ~Impl() {
         if (ctx) {
@@ -231,8 +282,9 @@ struct PageSoftmaxHip::Impl {
         page_cap = pages;
     }
 
-    static size_t carve_bytes(uint32_t max_blocks, uint32_t qheads, uint32_t dim) {
-        return align256(size_t(kRowsPerLaunch) * qheads * dim * sizeof(float)) + page_bytes(max_blocks);
+    static size_t carve_bytes(uint32_t max_blocks, uint32_t qheads, uint32_t kvheads, uint32_t dim) {
+        return align256(size_t(kRowsPerLaunch) * qheads * dim * sizeof(float)) + page_bytes(max_blocks) +
+               mean_bytes(max_blocks, kvheads * dim);
     }
 
     // Rows of one kvr_score call within the logits budget of the workspace.
@@ -276,7 +328,7 @@ size_t PageSoftmaxHip::workspace_bytes(uint32_t max_blocks, uint32_t qheads, uin
     const uint32_t rows =
         uint32_t(std::min<size_t>(kRowsPerLaunch, kLogitsBudget / (size_t(max_blocks) * qheads * sizeof(double))));
     return align256(kvr_workspace_bytes(1, max_blocks, rows, qheads, kvheads, dim)) +
-           Impl::carve_bytes(max_blocks, qheads, dim);
+           Impl::carve_bytes(max_blocks, qheads, kvheads, dim);
 }
 
 PageSoftmaxHip::PageSoftmaxHip(int device, void *workspace, size_t bytes, uint32_t max_blocks, uint32_t qheads,
@@ -303,34 +355,73 @@ PageSoftmaxHip::PageSoftmaxHip(int device, void *workspace, size_t bytes, uint32
     m.q_cap = size_t(rows) * qheads * dim;
     b += align256(size_t(kRowsPerLaunch) * qheads * dim * sizeof(float));
     m.carve_pages(b, max_blocks);
+    m.carve_means(b + Impl::page_bytes(max_blocks), max_blocks, kvheads * dim);
 }
 
 PageSoftmaxHip::~PageSoftmaxHip() = default;
 
-std::vector<double> PageSoftmaxHip::score(const PageSummaries &sums, PageQueryView v, const QueryScoreFrame &frame,
-                                          GqaScoreAggregation aggregation) {
-    Impl &m = *impl_;
-    const kvr_aggregation agg = to_kvr(aggregation);
-    require((v.data || v.layer_data) && v.layer_rows && v.layers && v.rows && v.head_dim && v.kv_heads &&
-                v.query_heads && v.query_heads % v.kv_heads == 0 && v.layers == sums.layers.size(),
-            "page softmax geometry mismatch");
-    if (!m.borrowed) {
-        m.qheads = v.query_heads;
-        m.kvheads = v.kv_heads;
-        m.dim = v.head_dim;
+// One layer's Query rows against its fp16 summaries, in batches of `batch`
+// rows staged through the device Query buffer; each call adds its share of
+// the scores (the first call of a score() sets them).
+void PageSoftmaxHip::Impl::score_layer(const uint16_t *summaries, const float *base, const PageQueryView &v,
+                                       uint32_t layer, uint32_t pages, uint32_t batch, kvr_aggregation agg,
+                                       uint32_t active, bool &accumulate, hipStream_t s) {
+    const size_t qw = size_t(v.query_heads) * v.head_dim;
+    for (uint32_t r0 = 0; r0 < v.layer_rows[layer]; r0 += batch) {
+        const uint32_t rows = std::min(batch, v.layer_rows[layer] - r0);
+        hip_ok(hipMemcpyAsync(q, base + size_t(r0) * qw, size_t(rows) * qw * sizeof(float), hipMemcpyHostToDevice,
+                              s),
+               "query H2D");
+        kvr_query kq{};
+        kq.data = q;
+        kq.scalar = KVR_FMT_F32;
+        kq.rows = rows;
+        kq.query_heads = v.query_heads;
+        kq.kv_heads = v.kv_heads;
+        kq.head_dim = v.head_dim;
+        kq.row_stride = qw * sizeof(float);
+        kq.head_stride = size_t(v.head_dim) * sizeof(float);
+        kq.dim_stride = sizeof(float);
+        kq.attention_scale = v.attention_scale;
+        ok(kvr_score(ctx, &kq, summaries, 1, pages, mask, agg, active, accumulate, scores, 0, s), "page softmax");
+        accumulate = true;
     }
-    require(v.query_heads == m.qheads && v.kv_heads == m.kvheads && v.head_dim == m.dim,
+}
+
+uint32_t PageSoftmaxHip::Impl::check_view(const PageQueryView &v, uint32_t layers) {
+    require((v.data || v.layer_data) && v.layer_rows && v.layers && v.rows && v.head_dim && v.kv_heads &&
+                v.query_heads && v.query_heads % v.kv_heads == 0 && v.layers == layers,
             "page softmax geometry mismatch");
-    m.check_frame(sums, frame);
-    const uint32_t n = uint32_t(frame.starts.size());
-    std::vector<double> result(n, 0.0);
-    if (std::none_of(frame.score_mask.begin(), frame.score_mask.end(), [](uint8_t x) { return x != 0; }))
-        return result;
+    if (!borrowed) {
+        qheads = v.query_heads;
+        kvheads = v.kv_heads;
+        dim = v.head_dim;
+    }
+    require(v.query_heads == qheads && v.kv_heads == kvheads && v.head_dim == dim, "page softmax geometry mismatch");
     uint32_t active = 0;
     for (uint32_t l = 0; l < v.layers; ++l) {
         require(v.layer_rows[l] <= v.rows, "page softmax row count exceeds its storage");
         active += v.layer_rows[l] != 0;
     }
+    return active;
+}
+
+static const float *query_layer(const PageQueryView &v, uint32_t l) {
+    const float *base = v.layer_data ? v.layer_data[l] : v.data + size_t(l) * v.rows * v.query_heads * v.head_dim;
+    require(base != nullptr, "missing active Query layer storage");
+    return base;
+}
+
+std::vector<double> PageSoftmaxHip::score(const PageSummaries &sums, PageQueryView v, const QueryScoreFrame &frame,
+                                          GqaScoreAggregation aggregation) {
+    Impl &m = *impl_;
+    const kvr_aggregation agg = to_kvr(aggregation);
+    const uint32_t active = m.check_view(v, uint32_t(sums.layers.size()));
+    m.check_frame(sums, frame);
+    const uint32_t n = uint32_t(frame.starts.size());
+    std::vector<double> result(n, 0.0);
+    if (std::none_of(frame.score_mask.begin(), frame.score_mask.end(), [](uint8_t x) { return x != 0; }))
+        return result;
     if (!active) return result;
     DeviceBinding bind(m.device);
     uint32_t batch = std::min(m.rows_per_call(n), v.rows);
@@ -338,67 +429,102 @@ std::vector<double> PageSoftmaxHip::score(const PageSummaries &sums, PageQueryVi
     m.reserve(batch, n);
     const hipStream_t s = m.stream();
     StreamDrain drain{s};
-    const size_t qw = size_t(v.query_heads) * v.head_dim;
     hip_ok(hipMemcpyAsync(m.mask, frame.score_mask.data(), n, hipMemcpyHostToDevice, s), "mask H2D");
     bool accumulate = false;
     for (uint32_t l = 0; l < v.layers; ++l) {
         if (!v.layer_rows[l]) continue;
         require(sums.layers[l] != nullptr, "page softmax missing active layer storage");
-        const float *base = v.layer_data ? v.layer_data[l] : v.data + size_t(l) * v.rows * qw;
-        require(base != nullptr, "missing active Query layer storage");
-        for (uint32_t r0 = 0; r0 < v.layer_rows[l]; r0 += batch) {
-            const uint32_t rows = std::min(batch, v.layer_rows[l] - r0);
-            hip_ok(hipMemcpyAsync(m.q, base + size_t(r0) * qw, size_t(rows) * qw * sizeof(float),
-                                  hipMemcpyHostToDevice, s),
-                   "query H2D");
-            kvr_query q{};
-            q.data = m.q;
-            q.scalar = KVR_FMT_F32;
-            q.rows = rows;
-            q.query_heads = v.query_heads;
-            q.kv_heads = v.kv_heads;
-            q.head_dim = v.head_dim;
-            q.row_stride = qw * sizeof(float);
-            q.head_stride = size_t(v.head_dim) * sizeof(float);
-            q.dim_stride = sizeof(float);
-            q.attention_scale = v.attention_scale;
-            ok(kvr_score(m.ctx, &q, sums.layers[l], 1, n, m.mask, agg, active, accumulate, m.scores, 0, s),
-               "page softmax");
-            accumulate = true;
-        }
+        m.score_layer(sums.layers[l], query_layer(v, l), v, l, n, batch, agg, active, accumulate, s);
     }
     result = m.fetch(n, s);
     drain.armed = false;
     return result;
 }
 
-std::vector<double> PageSoftmaxHip::score_current_layer(const PageSummaries &sums, NativeCurrentLayerQuery q,
-                                                        const QueryScoreFrame &frame, void *producer_stream) {
+std::vector<double> PageSoftmaxHip::score(const HostMeanSource &src, PageQueryView v, const QueryScoreFrame &frame,
+                                          GqaScoreAggregation aggregation) {
     Impl &m = *impl_;
-    validate_native_layer_query(q);
-    require(q.layer < sums.layers.size() && sums.layers[q.layer], "native Query layer has no summaries");
-    if (!m.borrowed) {
-        m.qheads = q.query_heads;
-        m.kvheads = q.kv_heads;
-        m.dim = q.head_dim;
+    const kvr_aggregation agg = to_kvr(aggregation);
+    require(src.has && src.read && src.block_tokens && src.width, "page softmax geometry mismatch");
+    const uint32_t active = m.check_view(v, src.layers);
+    require(uint64_t(v.kv_heads) * v.head_dim == src.width, "page softmax geometry mismatch");
+    const size_t n = frame.starts.size();
+    require(n && frame.counts.size() == n && frame.score_mask.size() == n, "page softmax geometry mismatch");
+    require(n <= std::numeric_limits<uint32_t>::max(), "page softmax geometry exceeds launch addressing");
+    // the stored page behind every scored entry: a whole page of the store
+    // inside the accepted prefix (page_softmax.cu:239-244)
+    std::vector<uint32_t> page(n, 0);
+    size_t scored = 0;
+    for (size_t i = 0; i < n; ++i) {
+        if (!frame.score_mask[i]) continue;
+        const uint64_t begin = frame.starts[i], count = frame.counts[i], acc = frame.accepted_through;
+        const uint64_t p = begin / src.block_tokens;
+        const bool whole = begin % src.block_tokens == 0 && begin < acc && count && count <= acc - begin &&
+                           p <= std::numeric_limits<uint32_t>::max() && src.has(uint32_t(p));
+        if (!whole) throw std::invalid_argument("page softmax stale index extent");
+        page[i] = uint32_t(p);
+        ++scored;
     }
-    require(q.query_heads == m.qheads && q.kv_heads == m.kvheads && q.head_dim == m.dim,
-            "native Query or score frame geometry mismatch");
-    m.check_frame(sums, frame);
-    const uint32_t n = uint32_t(frame.starts.size());
+    std::vector<double> result(n, 0.0);
+    if (!scored || !active) return result;
+    const uint32_t pages = uint32_t(n);
     DeviceBinding bind(m.device);
-    const hipStream_t s = producer_stream ? static_cast<hipStream_t>(producer_stream) : m.stream();
+    uint32_t batch = std::min(m.rows_per_call(pages), v.rows);
+    if (m.borrowed) batch = std::min<uint32_t>(batch, uint32_t(m.q_cap / (size_t(m.qheads) * m.dim)));
+    m.reserve(batch, pages);
+    m.reserve_means(pages, src.width);
+    const hipStream_t s = m.stream();
+    StreamDrain drain{s};
+    hip_ok(hipMemcpyAsync(m.mask, frame.score_mask.data(), n, hipMemcpyHostToDevice, s), "mask H2D");
+    std::vector<float> host(size_t(pages) * src.width, 0.0f);
+    bool accumulate = false;
+    for (uint32_t l = 0; l < v.layers; ++l) {
+        if (!v.layer_rows[l]) continue;
+        // the host buffer is refilled only once the previous layer's copy
+        // has been read
+        hip_ok(hipStreamSynchronize(s), "hipStreamSynchronize");
+        for (size_t i = 0; i < n; ++i)
+            if (frame.score_mask[i]) src.read(page[i], l, host.data() + i * src.width);
+        hip_ok(hipMemcpyAsync(m.msum, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice, s),
+               "means H2D");
+        // means x (1/1) is the mean itself; the finalize rounds it to the
+        // fp16 operand and raises non-finite or out-of-range values
+        ok(kvr_summary_finalize(m.ctx, m.msum, m.mcount, pages, src.width, nullptr, m.m16, s), "page means");
+        m.score_layer(m.m16, query_layer(v, l), v, l, pages, batch, agg, active, accumulate, s);
+    }
+    result = m.fetch(pages, s);
+    drain.armed = false;
+    return result;
+}
+
+// The native Query's checks that do not depend on where the summaries come
+// from: geometry against the scorer, an eager stream, Q on this device and
+// the logits budget.
+hipStream_t PageSoftmaxHip::Impl::current_layer_stream(const NativeCurrentLayerQuery &q, uint32_t pages,
+                                                       void *producer_stream) {
+    if (!borrowed) {
+        qheads = q.query_heads;
+        kvheads = q.kv_heads;
+        dim = q.head_dim;
+    }
+    require(q.query_heads == qheads && q.kv_heads == kvheads && q.head_dim == dim,
+            "native Query or score frame geometry mismatch");
+    const hipStream_t s = producer_stream ? static_cast<hipStream_t>(producer_stream) : stream();
     if (capturing(s)) throw std::invalid_argument("native Query selection requires an eager stream");
     hipPointerAttribute_t attr{};
     const hipError_t pe = hipPointerGetAttributes(&attr, q.data);
     if (pe != hipSuccess) (void)hipGetLastError();  // unknown to the runtime: ordinary host memory
-    if (pe != hipSuccess || attr.type != hipMemoryTypeDevice || attr.device != m.device)
+    if (pe != hipSuccess || attr.type != hipMemoryTypeDevice || attr.device != device)
         throw std::invalid_argument("native Query is not stored on its scoring device");
-    if (size_t(q.rows) * q.query_heads * n * sizeof(double) > kLogitsBudget)
+    if (size_t(q.rows) * q.query_heads * pages * sizeof(double) > kLogitsBudget)
         throw std::length_error("native Query exceeds planned logits range");
-    m.reserve(0, n);
-    StreamDrain drain{s};
-    hip_ok(hipMemcpyAsync(m.mask, frame.score_mask.data(), n, hipMemcpyHostToDevice, s), "mask H2D");
+    return s;
+}
+
+std::vector<double> PageSoftmaxHip::Impl::current_layer(const uint16_t *summaries, const NativeCurrentLayerQuery &q,
+                                                        const QueryScoreFrame &frame, hipStream_t s) {
+    const uint32_t n = uint32_t(frame.starts.size());
+    hip_ok(hipMemcpyAsync(mask, frame.score_mask.data(), n, hipMemcpyHostToDevice, s), "mask H2D");
     kvr_query kq{};
     kq.data = q.data;
     kq.scalar = query_format(q.scalar);
@@ -410,9 +536,60 @@ std::vector<double> PageSoftmaxHip::score_current_layer(const PageSummaries &sum
     kq.head_stride = q.head_stride;
     kq.dim_stride = q.dimension_stride;
     kq.attention_scale = q.attention_scale;
-    ok(kvr_score(m.ctx, &kq, sums.layers[q.layer], 1, n, m.mask, KVR_AGG_MEAN, 1, 0, m.scores, 0, s),
-       "page softmax");
-    auto out = m.fetch(n, s);
+    ok(kvr_score(ctx, &kq, summaries, 1, n, mask, KVR_AGG_MEAN, 1, 0, scores, 0, s), "page softmax");
+    return fetch(n, s);
+}
+
+std::vector<double> PageSoftmaxHip::score_current_layer(const PageSummaries &sums, NativeCurrentLayerQuery q,
+                                                        const QueryScoreFrame &frame, void *producer_stream) {
+    Impl &m = *impl_;
+    validate_native_layer_query(q);
+    require(q.layer < sums.layers.size() && sums.layers[q.layer], "native Query layer has no summaries");
+    DeviceBinding bind(m.device);
+    const hipStream_t s = m.current_layer_stream(q, uint32_t(std::min<size_t>(frame.starts.size(), UINT32_MAX)),
+                                                 producer_stream);
+    m.check_frame(sums, frame);
+    m.reserve(0, uint32_t(frame.starts.size()));
+    StreamDrain drain{s};
+    auto out = m.current_layer(sums.layers[q.layer], q, frame, s);
+    drain.armed = false;
+    return out;
+}
+
+std::vector<double> PageSoftmaxHip::score_current_layer(const HostMeanSource &src, NativeCurrentLayerQuery q,
+                                                        const QueryScoreFrame &frame, void *producer_stream) {
+    Impl &m = *impl_;
+    validate_native_layer_query(q);
+    const size_t n = frame.starts.size();
+    const uint32_t bt = src.block_tokens;
+    if (!src.read || !src.tokens || q.layer >= src.layers || !bt || uint64_t(q.kv_heads) * q.head_dim != src.width ||
+        frame.counts.size() != n || frame.score_mask.size() != n || frame.transport_mask.size() != n || !n ||
+        n > std::numeric_limits<uint32_t>::max() || uintptr_t(q.data) > UINTPTR_MAX - q.bytes)
+        throw std::invalid_argument("native Query or score frame geometry mismatch");
+    // every entry must be a whole page of the target layer's Mean-K as the
+    // store holds it now (page_softmax.cu:288-298)
+    std::vector<uint32_t> page(n);
+    for (size_t i = 0; i < n; ++i) {
+        const uint64_t start = frame.starts[i], count = frame.counts[i], acc = frame.accepted_through;
+        const uint64_t p = start / bt;
+        const bool covered = count && count <= bt && start % bt == 0 && start <= acc && count <= acc - start &&
+                             p <= std::numeric_limits<uint32_t>::max() && src.tokens(uint32_t(p), q.layer) == count;
+        if (!covered)
+            throw std::invalid_argument("native target-layer Mean-K coverage differs from frozen frame");
+        page[i] = uint32_t(p);
+    }
+    DeviceBinding bind(m.device);
+    const uint32_t pages = uint32_t(n);
+    const hipStream_t s = m.current_layer_stream(q, pages, producer_stream);
+    m.reserve(0, pages);
+    m.reserve_means(pages, src.width);
+    std::vector<float> host(size_t(pages) * src.width, 0.0f);
+    for (size_t i = 0; i < n; ++i)
+        if (frame.score_mask[i]) src.read(page[i], q.layer, host.data() + i * src.width);
+    StreamDrain drain{s};
+    hip_ok(hipMemcpyAsync(m.msum, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice, s), "means H2D");
+    ok(kvr_summary_finalize(m.ctx, m.msum, m.mcount, pages, src.width, nullptr, m.m16, s), "page means");
+    auto out = m.current_layer(m.m16, q, frame, s);
     drain.armed = false;
     return out;
 }
@@ -991,7 +1168,9 @@ void LrfuHistoryHip::restore(const LrfuState &state) {
 
 size_t PageSoftmaxHip::device_bytes() const {
     size_t b = kvr_device_bytes(impl_->ctx);
-    if (!impl_->borrowed) b += impl_->q_cap * sizeof(float) + (impl_->page_cap ? impl_->page_cap * 13 + 256 : 0);
+    if (!impl_->borrowed)
+        b += impl_->q_cap * sizeof(float) + (impl_->page_cap ? impl_->page_cap * 13 + 256 : 0) +
+             impl_->mean_cap * 6 + size_t(impl_->mean_pages) * 4;
     return b;
 }
 
