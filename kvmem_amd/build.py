@@ -1,7 +1,7 @@
 """Build the in-tree native libraries.
 
   kvmem_amd/libkvrecall.so   HIP kernels + the C ABI of include/kvrecall.h (gfx950)
-  kvmem_amd/libkvmem_hip.so  C++ host layer (include/kvmem_hip/kvmem_hip.hpp) over it
+  kvmem_amd/libkvmem_hip.so  C++ host layer (include/kvmem_hip/*.hpp, llama_kvmem_hooks.h) over it
   tests/cpp/build/test_host  C++ test of the host layer (links the oracle as checker)
   oracle/liboracle.so        the CPU restatement used by tests (checker only)
   oracle/_ref/*.so           the reference's own host sources, when present
@@ -25,7 +25,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "kvmem_amd", "csrc")
 LIB = os.path.join(ROOT, "kvmem_amd", "libkvrecall.so")
 HOST_LIB = os.path.join(ROOT, "kvmem_amd", "libkvmem_hip.so")
-HOST_SRC = os.path.join(ROOT, "kvmem_amd", "host", "kvmem_hip.cpp")
+HOST_SRCS = [os.path.join(ROOT, "kvmem_amd", "host", f) for f in ("kvmem_hip.cpp", "kvmem_memory.cpp", "kvmem_hooks.cpp")]
 HOST_TEST_SRC = os.path.join(ROOT, "tests", "cpp", "test_host.cpp")
 HOST_TEST = os.path.join(ROOT, "tests", "cpp", "build", "test_host")
 ORACLE = os.path.join(ROOT, "oracle")
@@ -86,23 +86,33 @@ def build_host(verbose: bool = False) -> str:
     hipcc = _hipcc()
     tmp = HOST_LIB + ".tmp"
     _run([hipcc, "-O2", "-fPIC", "-shared", "-std=c++17", "-Wall", "-I", os.path.join(ROOT, "include"),
-          HOST_SRC, "-o", tmp, "-L", os.path.dirname(LIB), "-lkvrecall", "-Wl,-rpath,$ORIGIN"], verbose)
+          *HOST_SRCS, "-o", tmp, "-L", os.path.dirname(LIB), "-lkvrecall", "-Wl,-rpath,$ORIGIN"], verbose)
     os.replace(tmp, HOST_LIB)
     return HOST_LIB
 
 
-def build_host_test(verbose: bool = False) -> str:
-    """tests/cpp/test_host.cpp against the host layer, the C ABI and the oracle."""
+MEMORY_TEST_SRC = os.path.join(ROOT, "tests", "cpp", "test_memory.cpp")
+MEMORY_TEST = os.path.join(ROOT, "tests", "cpp", "build", "test_memory")
+
+
+def _build_cpp_test(src: str, exe: str, verbose: bool) -> str:
+    """A C++ test program against the host layer, the C ABI and the oracle."""
     hipcc = _hipcc()
-    os.makedirs(os.path.dirname(HOST_TEST), exist_ok=True)
-    tmp = HOST_TEST + ".tmp"
+    os.makedirs(os.path.dirname(exe), exist_ok=True)
+    tmp = exe + ".tmp"
     libdir = os.path.dirname(LIB)
-    _run([hipcc, "-O2", "-std=c++17", "-Wall", "-I", os.path.join(ROOT, "include"), "-I", ORACLE, HOST_TEST_SRC,
+    _run([hipcc, "-O2", "-std=c++17", "-Wall", "-I", os.path.join(ROOT, "include"), "-I", ORACLE, src,
           "-o", tmp, "-L", libdir, "-lkvmem_hip", "-lkvrecall", "-L", ORACLE, "-loracle",
           f"-Wl,-rpath,{libdir}", f"-Wl,-rpath,{ORACLE}", "-Wl,-rpath,$ORIGIN/../../../kvmem_amd",
           "-Wl,-rpath,$ORIGIN/../../../oracle", "-ldl"], verbose)
-    os.replace(tmp, HOST_TEST)
-    return HOST_TEST
+    os.replace(tmp, exe)
+    return exe
+
+
+def build_host_test(verbose: bool = False) -> str:
+    """tests/cpp/test_host.cpp and tests/cpp/test_memory.cpp."""
+    _build_cpp_test(MEMORY_TEST_SRC, MEMORY_TEST, verbose)
+    return _build_cpp_test(HOST_TEST_SRC, HOST_TEST, verbose)
 
 
 REF_INCLUDE = os.path.join(os.environ.get("KVR_REFERENCE_ROOT", "/root/reference"), "kvmem", "include")
