@@ -328,6 +328,22 @@ def run(args):
     print(json.dumps(line), flush=True)
 
 
+def calibration_copies(ctx) -> int:
+    """Three device copies of 256 MiB in 64 KiB ops (k_copy_ops): known byte
+    counts that calibrate FETCH_SIZE / WRITE_SIZE in a counter pass."""
+    import torch
+    op, cb = 1 << 16, 256 << 20
+    src_t = torch.empty(cb, dtype=torch.uint8, device="cuda")
+    dst_t = torch.empty(cb, dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    n = cb // op
+    for _ in range(3):
+        ctx.d2d_batched([src_t.data_ptr() + i * op for i in range(n)], [dst_t.data_ptr() + i * op for i in range(n)],
+                        [op] * n)
+        ctx.check()
+    return cb
+
+
 def pmc_pass(args):
     """Counter pass (run under rocprofv3 --pmc): a stack of eight distinct
     128K-token layers in three launches (k_stack_group: the first group's
@@ -579,19 +595,10 @@ def run_workload(args):
         keep = ctx.recall_stack([desc(i, False) for i in range(N)])
         ctx.check()
         del keep
-        op = 1 << 16
-        cb = 256 << 20
-        src_t = torch.empty(cb, dtype=torch.uint8, device="cuda")
-        dst_t = torch.empty(cb, dtype=torch.uint8, device="cuda")
-        torch.cuda.synchronize()
-        n = cb // op
-        for _ in range(3):
-            ctx.d2d_batched([src_t.data_ptr() + i * op for i in range(n)], [dst_t.data_ptr() + i * op for i in range(n)],
-                            [op] * n)
-            ctx.check()
+        cb = calibration_copies(ctx)
         ctx.close()
-        print(json.dumps({"pass": "pmc", "workload": args.workload, "layers": N, "copy_bytes": cb, "copy_ops": n}),
-              flush=True)
+        print(json.dumps({"pass": "pmc", "workload": args.workload, "layers": N, "copy_bytes": cb,
+                          "copy_ops": cb >> 16}), flush=True)
         return
 
     # (a) select latency of one layer: summary start -> selection written
@@ -843,28 +850,51 @@ def run_attention(args):
                                 kv_heads=HKV, tokens=T, page_tokens=PT, scale=scale, softcap=0.0, rows=rows,
                                 mass=mass)
 
+    if args.pmc_pass:  # three calls, then the calibration copies
+        for _ in range(3):
+            call()
+        ctx.check()
+        cb = calibration_copies(ctx)
+        ctx.close()
+        print(json.dumps({"pass": "pmc", "workload": args.workload, "calls": 3, "copy_bytes": cb}), flush=True)
+        return
     ev_a, ev_b = hip.event(), hip.event()
     for _ in range(args.warmup):
         call()
     ctx.check()
-    times = []
+    # throughput: the K calls back to back between one pair of events on
+    # the calls' stream (both launches of every call inside)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    hip.record(ev_a, ctx.select_stream)
     for _ in range(args.steps):
+        call()
+    hip.record(ev_b, ctx.select_stream)
+    ctx.check()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    call_us = hip.elapsed_ms(ev_a, ev_b) * 1e3 / args.steps
+    # latency: one call alone between events (host launch time included)
+    alone = []
+    for _ in range(5):
         hip.record(ev_a, ctx.select_stream)
         call()
         hip.record(ev_b, ctx.select_stream)
         ctx.check()
-        times.append(hip.elapsed_ms(ev_a, ev_b) * 1e3)
-    torch.cuda.synchronize()
-    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
-    call_us = float(np.mean(times))
+        alone.append(hip.elapsed_ms(ev_a, ev_b) * 1e3)
+    alone_us = float(np.median(alone))
     R = len(rows)
     alg = T * krow + R * HQ * D * 4 + R * T * 2 + 2 * R * HQ * P * 4 + R * P * 4
     achieved = alg / (call_us * 1e-6) / 1e9
     got = mass.cpu().numpy().reshape(R, P)
-    log(f"call {call_us:.1f} us (events, both launches) = {achieved:.1f} GB/s algorithmic; "
-        f"mass sums {got.sum(axis=1).round(6).tolist()}")
+    traffic, traffic_src = None, os.path.join(ROOT, "profiles", f"pmc_{args.workload}.json")
+    if os.path.exists(traffic_src):
+        try:
+            traffic = json.load(open(traffic_src)).get("traffic_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+    log(f"call {call_us:.1f} us back to back ({args.steps} calls, both launches) = {achieved:.1f} GB/s algorithmic; "
+        f"one call alone {alone_us:.1f} us; mass sums {got.sum(axis=1).round(6).tolist()}")
     line = {
         "metric": "sampled attention page masses at 128K ctx: key GB/s vs HBM peak",
         "value": round(achieved, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -875,8 +905,9 @@ def run_attention(args):
                    "page_tokens": PT, "pages": P, "sampled_rows": rows, "ubatch": UB, "key_format": kname},
         "roofline": {"bound": "hbm", "kernel": "k_attn_lse + k_attn_mass (one call)",
                      "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None, "bytes_per_call": alg,
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic, "bytes_per_call": alg,
                      "mean_call_us": round(call_us, 3)},
+        "call_alone_us": round(alone_us, 3),
     }
     if not args.no_cpu:
         # the FP64 dense restatement on one sampled row, scaled to the call
@@ -1044,6 +1075,9 @@ def main():
         sys.exit(2)
     if args.pmc_pass and args.workload in WORKLOADS:
         run_workload(args)
+        return
+    if args.pmc_pass and args.workload in ATTN_WORKLOADS:
+        run_attention(args)
         return
     if args.pmc_pass:
         pmc_pass(args)

@@ -293,8 +293,10 @@ typedef enum kvr_option {
     KVR_OPT_GATHER_WORKGROUPS = 1, /* grid bound of the device-driven gather (default: 16
                                       for copies, 32 when a plane decodes) */
     KVR_OPT_GATHER_CHUNK_ROWS = 2, /* token rows per gather work item (default 8, <= 64) */
-    KVR_OPT_GATHER_THREADS = 3     /* gather workgroup size: 64, 128 or 256 (default: 64
+    KVR_OPT_GATHER_THREADS = 3,    /* gather workgroup size: 64, 128 or 256 (default: 64
                                       for copies, 256 when a plane decodes) */
+    KVR_OPT_ATTN_PAGE_GROUP = 4    /* pages per attention-sampler workgroup, 1..16
+                                      (default: by the call's size) */
 } kvr_option;
 
 /* Tuning knobs of a context; value 0 restores the default.  No reference

@@ -27,7 +27,7 @@ AGG_MEAN, AGG_MAX, AGG_MAX_LOGIT = range(3)
 TIE_LOWER_FIRST, TIE_HIGHER_FIRST = range(2)
 GATHER_COPY, GATHER_DEQUANT_F16, GATHER_REQUANT_Q8_0, GATHER_ROPE_FWHT = range(4)
 ENGINE_AUTO, ENGINE_KERNEL, ENGINE_SDMA = range(3)
-OPT_GATHER_WORKGROUPS, OPT_GATHER_CHUNK_ROWS, OPT_GATHER_THREADS = 1, 2, 3
+OPT_GATHER_WORKGROUPS, OPT_GATHER_CHUNK_ROWS, OPT_GATHER_THREADS, OPT_ATTN_PAGE_GROUP = 1, 2, 3, 4
 MAX_INLINE_MANDATORY = 64
 MAX_PLANES = 8
 STACK_GROUP = 4

@@ -9,15 +9,17 @@
 // per-(row, head) max and 1/sum over pages (normalize, .cu:99-115) and the
 // head average (average, .cu:116-126).
 //
-// Here the first step reads every key once: a workgroup owns one page of one
-// kv-head and every (sampled row, query head of the group) pair of a tile,
-// each lane one token of the page.  The lane decodes its token's key row
-// 32 values (one block) at a time into binary32 and folds them into all the
-// tile's dot products with the query tile in LDS (the reference re-reads the
-// page once per query head and row).  The page log-sum-exp of each pair is
-// a workgroup max and sum.  The second kernel does the normalization and
-// the head average for one row per workgroup.  All arithmetic is binary32,
-// as in the reference.
+// Here the first step reads every key once: a workgroup owns a group of up
+// to 16 pages of one kv-head and every (sampled row, query head of the
+// group) pair of a 16-pair tile.  Its four waves stream the pages' 16-token
+// tiles through a two-slot ring of loads and multiply them with the pair
+// tile's queries on the matrix cores (fp16 keys and, staged through a
+// per-wave LDS tile, q8_0 keys on v_mfma_f32_16x16x32_f16 with split
+// hi/lo queries; the other formats decoded to binary32 on
+// v_mfma_f32_16x16x4f32), keep each tile's logits and reduce them to
+// per-page log-sum-exps.  The second kernel does the normalization and the
+// head average of one sampled row per workgroup row.  Arithmetic is
+// binary32 with binary32 accumulation, as in the reference.
 #include "kvr_device.hpp"
 #include "kvr_internal.hpp"
 
@@ -186,21 +188,44 @@ constexpr float kLog2e = 1.44269504088896340736f, kLn2 = 0.693147180559945309417
 // the power of two comes back with the logit scale.  Two MFMAs (hi, lo) per
 // block: 8 per 16-token tile at head dim 128, against 32 of the f32 form.
 //
+// q8_0 keys (head dims that are multiples of 128) take the fp16 matrix
+// cores too: a wave's 16-token tile is staged through its own LDS slot with
+// coalesced 16-byte loads (the tile's rows are 34-byte blocks, not 16-byte
+// aligned), and each lane then reads its 8 codes of each block and the
+// block's fp16 scale from LDS.  Codes become fp16 exactly (0x64 high byte
+// over code + 128, less 1152); per block a hi and a lo MFMA from zero give
+// the pair's dot product with the codes, which the lane multiplies by its
+// token's block scale before adding it up.
+//
 // The workgroup's 16-token tiles, page after page, are dealt to its waves
 // in turn (flat tile f goes to wave f%4), and each wave streams its tiles
-// through one ring of loads across the pages.  Lanes keep a running max
-// and rescaled sum per pair in base 2; where a wave's next tile is on
-// another page it folds its 16 lanes per pair and leaves the page's partial
-// in LDS.  One barrier at the end, then the four waves' partials of each
-// (page, pair) give its log-sum-exp.
+// through one ring of loads across the pages.  When a page is 16, 32, 64,
+// 128 or 256 tokens (BATCH), a wave's tiles of one page come in one run of
+// n = 1, 1, 1, 2 or 4 consecutive tiles of its own: the lanes keep the
+// run's logits, and at the run's end one max over the run (16 lanes by DPP)
+// and one exponential per token give the page's partial -- one exponential
+// per token and pair.  Otherwise lanes keep a running max and rescaled sum
+// per pair in base 2 (two exponentials per token and pair) and fold their
+// 16 lanes where a wave's next tile is on another page.  Either way the
+// page's partial of each wave goes to LDS; one barrier at the end, then the
+// four waves' partials of each (page, pair) give its log-sum-exp.
+enum AttnPath : int { kPathF32 = 0, kPathF16 = 1, kPathQ8 = 2 };
 constexpr uint32_t kMaxPageGroup = 16;
 // G4: the query-head group is a multiple of 4, so a lane's four output
 // pairs 4*kg+i (i = 0..3, from a multiple of 16) are heads of one sampled
 // row and share its mask word: one load and one decode per tile, not four.
-template <int KF, int R, bool G4>
+template <int KF, int R, bool G4, int PATH, bool BATCH>
 __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
-    constexpr bool kHalf = KF == kKeyF16;  // fp16 matrix-core form
+    constexpr bool kHalf = PATH != kPathF32;  // fp16 matrix-core forms
+    constexpr bool kQ8 = PATH == kPathQ8;
+    // q8_0 staging: a token's kv-head row is RB bytes (4R blocks of 34),
+    // read as CPR 16-byte chunks (the last one ends at the row's end),
+    // NL chunks per lane for a 16-row tile
+    constexpr uint32_t RB = 136 * R, CPR = (RB + 15) / 16, CH = kTokenTile * CPR, NL = (CH + kWave - 1) / kWave;
     __shared__ float part[2][kMaxPageGroup][kAttnWaves][kPairTile];  // max, sum
+    // q8_0: one LDS tile per wave (a tile is staged and consumed within one
+    // step, and a wave's LDS operations complete in order)
+    __shared__ __align__(16) uint8_t q8_tiles[kQ8 ? kAttnWaves * kTokenTile * RB : 16];
     const uint32_t groups = (a.pages + a.page_group - 1) / a.page_group;
     const uint32_t kv = blockIdx.x / groups, pg0 = (blockIdx.x % groups) * a.page_group;
     const uint32_t npg = min(a.page_group, a.pages - pg0);
@@ -213,6 +238,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
     const uint32_t nb = a.dim / 32;
     const uint32_t T = (a.page_tokens + kTokenTile - 1) / kTokenTile;  // tiles per page
     const uint32_t nflat = npg * T;
+    // a run: the wave's consecutive tiles of one page (BATCH)
+    const uint32_t run = T <= 2 ? 1u : T / 4;
     for (uint32_t i = tid; i < npg * kAttnWaves * kPairTile; i += kAttnThreads) {
         (&part[0][0][0][0])[i] = -__builtin_inff();
         (&part[1][0][0][0])[i] = 0.0f;
@@ -223,12 +250,16 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
     // tokens past the page or the sequence are clamped to the last token
     // (in bounds) and not counted
     auto tile_page = [&](uint32_t k) { return min(w + kAttnWaves * k, nflat - 1) / T; };
-    auto tile_token = [&](uint32_t k, bool &live) {
-        const uint32_t f = w + kAttnWaves * k, fc = min(f, nflat - 1);
+    auto tile_first = [&](uint32_t k, uint32_t &end) {
+        const uint32_t fc = min(w + kAttnWaves * k, nflat - 1);
         const uint32_t pg = pg0 + fc / T;
-        const uint32_t t = pg * a.page_tokens + (fc % T) * kTokenTile + col;
-        const uint32_t end = min(pg * a.page_tokens + a.page_tokens, a.tokens);
-        live = f < nflat && t < end;
+        end = min(pg * a.page_tokens + a.page_tokens, a.tokens);
+        return pg * a.page_tokens + (fc % T) * kTokenTile;
+    };
+    auto tile_token = [&](uint32_t k, bool &live) {
+        uint32_t end;
+        const uint32_t t = tile_first(k, end) + col;
+        live = w + kAttnWaves * k < nflat && t < end;
         return min(t, end - 1);
     };
     const uint8_t *mrow[4];
@@ -236,26 +267,76 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
     for (int i = 0; i < 4; ++i)
         mrow[i] = a.mask + uint64_t(a.mask_rows[min(p0 + 4 * kg + i, npairs - 1) / a.group]) * a.mask_row_stride;
 
-    // ring of two slots: a tile's slot is decoded and refilled with the
-    // wave's tile two on before its MFMAs run
-    RawBlock<KF> ring[2][R];
-    u32x4 bw[2];  // mask words (one register tuple per slot)
-    uint32_t bsh[2][4];
+    // ring of two slots: a tile's slot is consumed and refilled with the
+    // wave's tile two on before its MFMAs run (four slots were measured
+    // slower: the registers cost a wave per SIMD)
+    constexpr int RING = 2;
+    RawBlock<KF> ring[RING][kQ8 ? 1 : R];
+    u32x4 qraw[RING][kQ8 ? NL : 1];  // q8_0: the slot's staged chunks
+    u32x4 bw[RING];                  // mask words (one register tuple per slot)
+    uint32_t bsh[RING][4];
+    // chunk j of this lane in a q8_0 tile: row rr, byte offset off in the row
+    auto chunk = [&](uint32_t j, uint32_t &rr, uint32_t &off) {
+        const uint32_t c = min(lane + kWave * j, CH - 1);  // lanes past the tile repeat its last chunk
+        rr = c / CPR;
+        off = min(16 * (c - rr * CPR), RB - 16);
+    };
+    // Matrix-core forms: a tile's keys through a buffer resource from its
+    // first token's row of this kv-head, so each lane's offsets are the same
+    // in every tile (no address arithmetic per tile) and rows past the
+    // sequence read as zeros (they are never counted).  Offsets are 32-bit:
+    // the host keeps key rows under 128 MiB.  The default cache policy: the
+    // streaming (nontemporal) one was measured 30% slower for fp16 keys.
+    const uint32_t krs = uint32_t(a.k_row_stride), head_bytes = nb * KeyBlock<KF>::kBytes;
+    auto key_rsrc = [&](uint32_t first) {
+        const uint32_t rows = min(a.tokens - first, kTokenTile);
+        return buffer_rsrc(a.k + uint64_t(first) * a.k_row_stride + uint64_t(kv) * a.k_head_stride,
+                           (rows - 1) * krs + head_bytes);
+    };
+    const uint32_t f16_off = col * krs + 16 * kg;  // fp16: the lane's token row, its 16 bytes of a block
+    uint32_t q8_off[kQ8 ? NL : 1];                 // q8_0: the lane's staged chunks
+#pragma unroll
+    for (uint32_t j = 0; j < (kQ8 ? NL : 1); ++j) {
+        uint32_t rr, off;
+        chunk(j, rr, off);
+        q8_off[j] = rr * krs + off;
+    }
     auto issue = [&](int slot, uint32_t k) {
         bool live;
         const uint32_t t = tile_token(k, live);
-        const uint8_t *row = a.k + uint64_t(t) * a.k_row_stride + uint64_t(kv) * a.k_head_stride;
+        if constexpr (kQ8) {
+            uint32_t end;
+            const auto rs = key_rsrc(tile_first(k, end));
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            if constexpr (kHalf) {
-                // 16 bytes (8 dims) of each of blocks 4r..4r+3 (clamped to
-                // the head's last block; blocks past it meet zero queries)
+            for (uint32_t j = 0; j < NL; ++j)
+                qraw[slot][j] = __builtin_bit_cast(
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, int(q8_off[j]), 0, 0));
+        } else if constexpr (PATH == kPathF16) {
+            // 16 bytes (8 dims) of each of blocks 4r..4r+3 (clamped to the
+            // head's last block; blocks past it meet zero queries)
+            uint32_t end;
+            const auto rs = key_rsrc(tile_first(k, end));
+#pragma unroll
+            for (int r = 0; r < R; ++r)
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    ring[slot][r].v[i] = *reinterpret_cast<const u32x4 *>(
-                        row + min(4u * r + i, nb - 1) * KeyBlock<KF>::kBytes + 16 * kg);
-            } else {
-                ring[slot][r] = load_block<KF>(row, block_of(r));
+                    ring[slot][r].v[i] = __builtin_bit_cast(
+                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                   rs, int(f16_off + min(4u * r + i, nb - 1) * KeyBlock<KF>::kBytes), 0, 0));
+        } else {
+            const uint8_t *row = a.k + uint64_t(t) * a.k_row_stride + uint64_t(kv) * a.k_head_stride;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                if constexpr (kHalf) {
+                    // 16 bytes (8 dims) of each of blocks 4r..4r+3 (clamped to
+                    // the head's last block; blocks past it meet zero queries)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        ring[slot][r].v[i] = *reinterpret_cast<const u32x4 *>(
+                            row + min(4u * r + i, nb - 1) * KeyBlock<KF>::kBytes + 16 * kg);
+                } else {
+                    ring[slot][r] = load_block<KF>(row, block_of(r));
+                }
             }
         }
 #pragma unroll
@@ -265,7 +346,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
     // head dim or the pairs).  Its loads go first, then the ring's first
     // two tiles, then the conversion: the loop is entered with exactly the
     // two slots' loads outstanding, in slot order, as at its back edge.
-    // f32 form: element s of round r is dim 32*(4r+kg) + s.  fp16 form:
+    // f32 form: element s of round r is dim 32*(4r+kg) + s.  fp16 forms:
     // dim 32*(4r + s/8) + 8*kg + s%8, kept as hi/lo fp16 parts (qh, ql).
     auto q_dim = [&](int r, int s) {
         return kHalf ? 32 * min(4u * r + s / 8, nb - 1) + 8 * kg + s % 8 : 32 * block_of(r) + s;
@@ -285,8 +366,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
 #pragma unroll
             for (int s = 0; s < 32; ++s) qw[r][s] = *scalar_word(qrow, a.q_scalar, q_dim(r, s), qs[r][s]);
         __builtin_amdgcn_sched_barrier(0);
-        issue(0, 0);
-        issue(1, 1);
+#pragma unroll
+        for (int r = 0; r < RING; ++r) issue(r, uint32_t(r));
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -327,17 +408,44 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
     }
     lds_barrier();  // partials initialized
 
-    float m[4], sm[4];
+    float m[4], sm[4];   // online form: running max and sum per output pair
+    float lb[4][4];      // BATCH: the run's logits, tile j of the run in lb[j]
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         m[i] = -__builtin_inff();
         sm[i] = 0.0f;
     }
     const uint32_t nk = nflat > w ? (nflat - w + kAttnWaves - 1) / kAttnWaves : 0;  // this wave's tiles
-    auto process = [&](int slot, uint32_t k) {
-        float kv32[R][32];
+    // The page's partial of this wave from the run's logits lb[t0..t1]
+    // (positions known where the call is inlined): per pair the max over
+    // the run's tokens (its 16 lanes by DPP), then the sum of exp2(l - max).
+    // A NaN logit is left out of both (fmaxf), as is a -inf one.  Stored
+    // for tiles of this wave only (padding tiles past nk are dropped).
+    auto flush = [&](uint32_t k, int t0, int t1) {
+        const uint32_t pl = tile_page(k);
 #pragma unroll
-        for (int r = 0; r < R; ++r)
+        for (int i = 0; i < 4; ++i) {
+            float bm = lb[t1][i];
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                if (t >= t0 && t < t1) bm = fmaxf(bm, lb[t][i]);
+            const float rm = dpp::group_reduce(bm, 16, dpp::FMax());
+            float sv = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                if (t >= t0 && t <= t1) sv += __builtin_amdgcn_exp2f(fmaxf(lb[t][i] - rm, -__builtin_inff()));
+            const float e = dpp::group_reduce(sv, 16, dpp::Add());
+            if (col == 0 && k < nk) {
+                part[0][pl][w][4 * kg + i] = rm;
+                part[1][pl][w][4 * kg + i] = e;
+            }
+        }
+    };
+    // process(slot, k, j): tile k (position j of a four-tile loop step)
+    auto process = [&](int slot, uint32_t k, int j) {
+        float kv32[kHalf ? 1 : R][32];
+#pragma unroll
+        for (int r = 0; r < (kHalf ? 1 : R); ++r)
             if constexpr (!kHalf) decode_block<KF>(ring[slot][r], kv32[r]);
         float bias[4];
 #pragma unroll
@@ -351,7 +459,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
         }
         // two accumulation chains keep two MFMAs of the wave in flight
         f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
-        if constexpr (kHalf) {
+        if constexpr (PATH == kPathF16) {
             // (hi chain, lo chain) on the slot's raw key words, issued
             // before the slot's refill overwrites them
 #pragma unroll
@@ -363,10 +471,63 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
                     acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[r][i], kb, acc1, 0, 0, 0);
                 }
         }
+        uint8_t *tile = q8_tiles + w * (kTokenTile * RB);
+        if constexpr (kQ8) {
+            // stage the slot's chunks in this wave's LDS tile; the slot's
+            // registers are then free for the refill
+#pragma unroll
+            for (uint32_t jj = 0; jj < NL; ++jj) {
+                uint32_t rr, off;
+                chunk(jj, rr, off);
+                uint64_t *d = reinterpret_cast<uint64_t *>(tile + rr * RB + off);
+                d[0] = uint64_t(qraw[slot][jj][0]) | (uint64_t(qraw[slot][jj][1]) << 32);
+                d[1] = uint64_t(qraw[slot][jj][2]) | (uint64_t(qraw[slot][jj][3]) << 32);
+            }
+        }
         __builtin_amdgcn_sched_barrier(0);
-        issue(slot, k + 2);
+        issue(slot, k + RING);
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (!kHalf) {
+        if constexpr (kQ8) {
+            // this lane's token is tile row `col`: per block b its fp16 scale
+            // and codes 8*kg..8*kg+7 (dword-aligned for odd blocks, two bytes
+            // into a dword for even ones)
+            const uint8_t *rowp = tile + col * RB;
+            f32x4 t[4 * R];
+            float db[4 * R];
+#pragma unroll
+            for (int b = 0; b < 4 * R; ++b) {
+                db[b] = h2f(*reinterpret_cast<const uint16_t *>(rowp + 34 * b));
+                uint32_t lo, hi;
+                if (b & 1) {
+                    const uint32_t *p = reinterpret_cast<const uint32_t *>(rowp + 34 * b + 2 + 8 * kg);
+                    lo = p[0];
+                    hi = p[1];
+                } else {
+                    const uint32_t *p = reinterpret_cast<const uint32_t *>(rowp + 34 * b + 8 * kg);
+                    const uint32_t w0 = p[0], w1 = p[1], w2 = p[2];
+                    lo = __builtin_amdgcn_alignbyte(w1, w0, 2);
+                    hi = __builtin_amdgcn_alignbyte(w2, w1, 2);
+                }
+                // int8 codes as fp16 1024 + (code + 128), less 1152: exact
+                const uint32_t xl = lo ^ 0x80808080u, xh = hi ^ 0x80808080u;
+                const u32x4 hv = {__builtin_amdgcn_perm(0x64646464u, xl, 0x04010400u),
+                                  __builtin_amdgcn_perm(0x64646464u, xl, 0x04030402u),
+                                  __builtin_amdgcn_perm(0x64646464u, xh, 0x04010400u),
+                                  __builtin_amdgcn_perm(0x64646464u, xh, 0x04030402u)};
+                const f16x8 kb = __builtin_bit_cast(f16x8, hv) - f16x8(_Float16(1152.0f));
+                const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+                t[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[b / 4][b % 4], kb, z, 0, 0, 0);
+                t[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[b / 4][b % 4], kb, t[b], 0, 0, 0);
+            }
+#pragma unroll
+            for (int b = 0; b < 4 * R; ++b)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (b & 1) acc1[i] = fmaf(t[b][i], db[b], acc1[i]);
+                    else acc0[i] = fmaf(t[b][i], db[b], acc0[i]);
+                }
+        }
+        if constexpr (PATH == kPathF32) {
             // even and odd k-steps; k-steps past the head dim have zero
             // queries
 #pragma unroll
@@ -379,51 +540,77 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
         }
         bool live;
         (void)tile_token(k, live);
-        // running max and sum in base 2: logits times log2(e), v_exp_f32
-        // (branch-free: a token left out has l = -inf, so nm = m and the
-        // sum is kept as it is)
+        float l[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const bool use = live && __builtin_isfinite(bias[i]);
-            float l = (acc0[i] + acc1[i]) * lscale[i];
-            if (a.softcap > 0.0f) l = a.softcap * tanhf(l / a.softcap);
-            l = use ? (l + bias[i]) * kLog2e : -__builtin_inff();
-            const float nm = fmaxf(m[i], l);
-            const float keep = m[i] == nm ? 1.0f : __builtin_amdgcn_exp2f(m[i] - nm);
-            sm[i] = sm[i] * keep + (use ? __builtin_amdgcn_exp2f(l - nm) : 0.0f);
-            m[i] = nm;
+            float x = (acc0[i] + acc1[i]) * lscale[i];
+            if (a.softcap > 0.0f) x = a.softcap * tanhf(x / a.softcap);
+            l[i] = use ? (x + bias[i]) * kLog2e : -__builtin_inff();
         }
-        // this wave's last tile of the page: fold the 16 lanes of each row
-        // (same pairs, different tokens) into the page's partial
-        // (the branch holds temporaries and LDS stores only: running values
-        // changed inside it would need merging copies at the loop's back
-        // edge, which wait for the ring's loads)
-        const uint32_t pl = tile_page(k);
-        const bool last = k < nk && (k + 1 == nk || tile_page(k + 1) != pl);  // (padding tiles never flush)
-        if (last) {
+        if constexpr (BATCH) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) lb[j][i] = l[i];
+            // the run ends here: its page's partial (uniform branches on the
+            // run length, each holding temporaries and LDS stores only)
+            if (run == 4) {
+                if (j == 3) flush(k, 0, 3);
+            } else if (run == 2) {
+                if (j & 1) flush(k, j - 1, j);
+            } else {
+                flush(k, j, j);
+            }
+        } else {
+            // running max and sum in base 2 (branch-free: a token left out
+            // has l = -inf, so nm = m and the sum is kept as it is)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float rm = dpp::group_reduce(m[i], 16, dpp::Max());
-                const float e = dpp::group_reduce(sm[i] > 0.0f ? sm[i] * __builtin_amdgcn_exp2f(m[i] - rm) : 0.0f,
-                                                  16, dpp::Add());
-                if (col == 0) {
-                    part[0][pl][w][4 * kg + i] = rm;
-                    part[1][pl][w][4 * kg + i] = e;
+                const float nm = fmaxf(m[i], l[i]);
+                const float keep = m[i] == nm ? 1.0f : __builtin_amdgcn_exp2f(m[i] - nm);
+                sm[i] = sm[i] * keep + (l[i] > -__builtin_inff() ? __builtin_amdgcn_exp2f(l[i] - nm) : 0.0f);
+                m[i] = nm;
+            }
+            // this wave's last tile of the page: fold the 16 lanes of each
+            // row (same pairs, different tokens) into the page's partial
+            // (the branch holds temporaries and LDS stores only: running
+            // values changed inside it would need merging copies at the
+            // loop's back edge, which wait for the ring's loads)
+            const uint32_t pl = tile_page(k);
+            const bool last = k < nk && (k + 1 == nk || tile_page(k + 1) != pl);  // (padding tiles never flush)
+            if (last) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float rm = dpp::group_reduce(m[i], 16, dpp::FMax());
+                    const float e = dpp::group_reduce(sm[i] > 0.0f ? sm[i] * __builtin_amdgcn_exp2f(m[i] - rm) : 0.0f,
+                                                      16, dpp::Add());
+                    if (col == 0) {
+                        part[0][pl][w][4 * kg + i] = rm;
+                        part[1][pl][w][4 * kg + i] = e;
+                    }
                 }
             }
-        }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            m[i] = last ? -__builtin_inff() : m[i];
-            sm[i] = last ? 0.0f : sm[i];
+            for (int i = 0; i < 4; ++i) {
+                m[i] = last ? -__builtin_inff() : m[i];
+                sm[i] = last ? 0.0f : sm[i];
+            }
         }
     };
     // straight-line body (a skipped call would make the ring slots' values
     // path-dependent, and the copies that merge them wait for the loads):
     // a tile past the wave's last is computed and not counted
-    for (uint32_t k = 0; k < nk; k += 2) {
-        process(0, k);
-        process(1, k + 1);
+    if constexpr (BATCH) {
+        for (uint32_t k = 0; k < nk; k += 4) {
+            process(0, k, 0);
+            process(1, k + 1, 1);
+            process(0, k + 2, 2);
+            process(1, k + 3, 3);
+        }
+    } else {
+        for (uint32_t k = 0; k < nk; k += 2) {
+            process(0, k, 0);
+            process(1, k + 1, 1);
+        }
     }
     lds_barrier();
     for (uint32_t i = tid; i < npg * kPairTile; i += kAttnThreads) {
@@ -447,18 +634,24 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
 
 // Masses of one sampled row over a chunk of 256 pages.  Every workgroup of
 // the row first takes, for each head, the max of its page log-sum-exps and
-// 1/sum of exp(lse - max): each wave takes four heads at a time with all
+// 1/sum of exp(lse - max): each wave takes eight heads at a time with all
 // their pages' loads in flight (up to 512 pages per pass, a running max and
 // rescaled sum beyond).  Then, for each page of its chunk, the head average
 // of exp(lse - max) * (1/sum): the reference's normalize and average
-// kernels.
+// kernels.  The row's log-sum-exps are read through one buffer resource
+// with 32-bit offsets (the host keeps a row under 4 GiB), and each batch of
+// loads is issued before the first of them is used.
 constexpr uint32_t kMassPages = 256;
-constexpr int kMassHeads = 4;
+constexpr int kMassHeads = 8;
+__device__ __forceinline__ float lse_at(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, int(off), 0, 0));
+}
 __global__ __launch_bounds__(kAttnThreads) void k_attn_mass(AttnArgs a) {
     extern __shared__ float norm[];  // [heads][2]
     const uint32_t r = blockIdx.y, tid = threadIdx.x, lane = tid % kWave;
     const uint32_t w = __builtin_amdgcn_readfirstlane(tid / kWave);
-    const float *lse = a.lse + uint64_t(r) * a.heads * a.pages;
+    const uint32_t row_bytes = a.heads * a.pages * uint32_t(sizeof(float));
+    const auto rs = buffer_rsrc(a.lse + uint64_t(r) * a.heads * a.pages, row_bytes);
     for (uint32_t h0 = w * kMassHeads; h0 < a.heads; h0 += kAttnWaves * kMassHeads) {
         float mx[kMassHeads], sum[kMassHeads];
 #pragma unroll
@@ -470,15 +663,17 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_mass(AttnArgs a) {
             float v[kMassHeads][8];
 #pragma unroll
             for (int j = 0; j < kMassHeads; ++j) {
-                const float *row = lse + uint64_t(min(h0 + j, a.heads - 1)) * a.pages;
+                const uint32_t head = min(h0 + j, a.heads - 1) * a.pages;
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const uint32_t p = q0 + u * kWave + lane;
-                    v[j][u] = p < a.pages ? row[p] : -__builtin_inff();
-                }
+                for (int u = 0; u < 8; ++u)
+                    v[j][u] = lse_at(rs, (head + min(q0 + u * kWave + lane, a.pages - 1)) * uint32_t(sizeof(float)));
             }
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int j = 0; j < kMassHeads; ++j) {
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (q0 + u * kWave + lane >= a.pages) v[j][u] = -__builtin_inff();
                 float cm = v[j][0];
 #pragma unroll
                 for (int u = 1; u < 8; ++u) cm = fmaxf(cm, v[j][u]);
@@ -492,7 +687,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_mass(AttnArgs a) {
         }
 #pragma unroll
         for (int j = 0; j < kMassHeads; ++j) {
-            const float wm = wave_max(mx[j]);
+            const float wm = wave_fmax(mx[j]);
             const float ws = wave_sum(sum[j] > 0.0f ? sum[j] * expf(mx[j] - wm) : 0.0f);
             if (lane == 0 && h0 + j < a.heads) {
                 // a head whose every page is -inf: max -inf, 1/sum NaN (as
@@ -505,27 +700,53 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_mass(AttnArgs a) {
     lds_barrier();
     const uint32_t p = blockIdx.x * kMassPages + tid;
     if (p >= a.pages) return;
+    // 32 heads' values of this page in flight at a time, added in head order
     float acc = 0.0f;
-#pragma unroll 8
-    for (uint32_t h = 0; h < a.heads; ++h) acc += expf(lse[uint64_t(h) * a.pages + p] - norm[2 * h]) * norm[2 * h + 1];
+    for (uint32_t h0 = 0; h0 < a.heads; h0 += 32) {
+        float v[32];
+#pragma unroll
+        for (uint32_t j = 0; j < 32; ++j) v[j] = lse_at(rs, (min(h0 + j, a.heads - 1) * a.pages + p) * uint32_t(sizeof(float)));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (uint32_t j = 0; j < 32; ++j)
+            if (h0 + j < a.heads) acc += expf(v[j] - norm[2 * (h0 + j)]) * norm[2 * (h0 + j) + 1];
+    }
     a.mass[uint64_t(r) * a.pages + p] = acc / float(a.heads);
 }
 
+template <int KF, int PATH, bool BATCH>
+hipError_t launch_lse_t(const AttnArgs &a, const dim3 &grid, hipStream_t s) {
+    const bool g4 = a.group % 4 == 0;
+    if (a.dim <= 128 && g4) hipLaunchKernelGGL((k_attn_lse<KF, 1, true, PATH, BATCH>), grid, dim3(kAttnThreads), 0, s, a);
+    else if (a.dim <= 128) hipLaunchKernelGGL((k_attn_lse<KF, 1, false, PATH, BATCH>), grid, dim3(kAttnThreads), 0, s, a);
+    else if (g4) hipLaunchKernelGGL((k_attn_lse<KF, 2, true, PATH, BATCH>), grid, dim3(kAttnThreads), 0, s, a);
+    else hipLaunchKernelGGL((k_attn_lse<KF, 2, false, PATH, BATCH>), grid, dim3(kAttnThreads), 0, s, a);
+    return hipGetLastError();
+}
+
+// The key path: fp16 keys on the fp16 matrix cores; q8_0 keys too when the
+// head dim is a multiple of 128 and every row is dword-aligned (the staged
+// 16-byte loads); others decoded to binary32.  BATCH when a page's tiles
+// split into equal runs per wave (pages of 16, 32, 64, 128 or 256 tokens).
 template <int KF>
 hipError_t launch_lse(const AttnArgs &a, hipStream_t s) {
     const uint32_t npairs = a.n_rows * a.group;
     const dim3 grid(a.kvheads * ((a.pages + a.page_group - 1) / a.page_group), (npairs + kPairTile - 1) / kPairTile);
-    const bool g4 = a.group % 4 == 0;
-    if (a.dim <= 128 && g4) hipLaunchKernelGGL((k_attn_lse<KF, 1, true>), grid, dim3(kAttnThreads), 0, s, a);
-    else if (a.dim <= 128) hipLaunchKernelGGL((k_attn_lse<KF, 1, false>), grid, dim3(kAttnThreads), 0, s, a);
-    else if (g4) hipLaunchKernelGGL((k_attn_lse<KF, 2, true>), grid, dim3(kAttnThreads), 0, s, a);
-    else hipLaunchKernelGGL((k_attn_lse<KF, 2, false>), grid, dim3(kAttnThreads), 0, s, a);
-    return hipGetLastError();
+    const uint32_t T = (a.page_tokens + kTokenTile - 1) / kTokenTile;
+    const bool batch = T == 1 || T == 2 || T == 4 || T == 8 || T == 16;
+    constexpr int base = KF == kKeyF16 ? kPathF16 : kPathF32;
+    if constexpr (KF == kKeyQ8) {
+        const bool staged = a.dim % 128 == 0 && (reinterpret_cast<uintptr_t>(a.k) | a.k_row_stride | a.k_head_stride) % 4 == 0;
+        if (staged) return batch ? launch_lse_t<KF, kPathQ8, true>(a, grid, s) : launch_lse_t<KF, kPathQ8, false>(a, grid, s);
+    }
+    return batch ? launch_lse_t<KF, base, true>(a, grid, s) : launch_lse_t<KF, base, false>(a, grid, s);
 }
 
 }  // namespace
 
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s) {
+    // one row's log-sum-exps are addressed with 32-bit byte offsets
+    if (uint64_t(a.heads) * a.pages * sizeof(float) > 0xffffffffull) return hipErrorInvalidValue;
     hipError_t e = hipErrorInvalidValue;
     switch (a.k_format) {
     case kKeyF16: e = launch_lse<kKeyF16>(a, s); break;

@@ -57,6 +57,7 @@ struct kvr_context {
     size_t staging_bytes = 0;
     // tuning
     uint32_t gather_wgs = 0;  // 0: by mode (kDefaultGatherWgs / kDefaultDecodeGatherWgs)
+    uint32_t attn_page_group = 0;  // 0: by the call's size
     uint32_t chunk_rows = 8;
     bool chunk_rows_set = false;  // chosen by the caller (else by the planes)
     uint32_t gather_threads = 0;  // 0: by mode
@@ -973,6 +974,10 @@ kvr_status kvr_set_option(kvr_context *ctx, kvr_option option, int64_t value) {
             return fail(KVR_ERR_INVALID, "gather workgroup size must be 64, 128 or 256");
         ctx->gather_threads = uint32_t(value);
         return KVR_OK;
+    case KVR_OPT_ATTN_PAGE_GROUP:
+        if (value < 0 || value > 16) return fail(KVR_ERR_INVALID, "attention page group must be in [0, 16]");
+        ctx->attn_page_group = uint32_t(value);
+        return KVR_OK;
     }
     return fail(KVR_ERR_INVALID, "unknown option %d", int(option));
 }
@@ -1648,6 +1653,8 @@ kvr_status kvr_attention_page_mass(kvr_context *ctx, const kvr_attention_sample 
     const size_t kal = quant ? 2 : 16;
     if (!aligned(a->k, kal) || a->k_row_stride % kal || a->k_head_stride % kal)
         return fail(KVR_ERR_INVALID, "key rows and heads must start on %zu-byte boundaries", kal);
+    if (a->k_row_stride >= (size_t(1) << 27))
+        return fail(KVR_ERR_UNSUPPORTED, "key rows of %zu bytes: at most 128 MiB", size_t(a->k_row_stride));
     const size_t krow = attention_key_row_bytes(a->k_format, a->head_dim);
     if ((a->kv_heads > 1 && a->k_head_stride < krow) ||
         (a->tokens > 1 && a->k_row_stride < size_t(a->kv_heads - 1) * a->k_head_stride + krow))
@@ -1679,8 +1686,16 @@ kvr_status kvr_attention_page_mass(kvr_context *ctx, const kvr_attention_sample 
     g.tokens = a->tokens;
     g.page_tokens = a->page_tokens;
     g.pages = pages;
-    // pages per workgroup: about 1024 workgroups per pair tile, at most 16
-    g.page_group = uint32_t(std::min<uint64_t>(16, std::max<uint64_t>(1, uint64_t(pages) * a->kv_heads / 1024)));
+    // pages per workgroup, at most 16: about 256 workgroups per pair tile
+    // for fp16 keys, 512 for q8_0 keys staged on the fp16 matrix cores,
+    // 1024 for keys decoded to binary32 (measured at 131072 tokens: the
+    // fp16 form streams longest at one wave per SIMD, the staged q8_0 form
+    // at two)
+    const uint32_t target = a->k_format == KVR_FMT_F16                              ? 256
+                            : a->k_format == KVR_FMT_Q8_0 && a->head_dim % 128 == 0 ? 512
+                                                                                     : 1024;
+    g.page_group = ctx->attn_page_group ? ctx->attn_page_group
+                                        : uint32_t(std::min<uint64_t>(16, std::max<uint64_t>(1, uint64_t(pages) * a->kv_heads / target)));
     g.scale = a->scale;
     g.softcap = a->softcap;
     g.lse = reinterpret_cast<float *>(ctx->ws);

@@ -55,6 +55,14 @@ template <class T> __device__ __forceinline__ void store_device(T *p, T v) {
 template <class T> __device__ __forceinline__ T load_device(const T *p) {
     return __hip_atomic_load(const_cast<T *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Raw buffer resource over `bytes` bytes from `p` (dword 3 selects the
+// 32-bit data format, which enables untyped loads).  Loads at offsets past
+// `bytes` return zeros instead of touching memory; offsets are 32-bit, so
+// no 64-bit address arithmetic sits between a wave's loads.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), short(0), int(bytes), 0x00020000);
+}
+constexpr int kBufferNontemporal = 2;  // cache-policy bits of a streaming load
 // Waits until this thread's vector memory operations have completed
 // (s_waitcnt vmcnt(0)).  The memory clobber keeps the compiler from moving
 // any load or store across the wait, so stores issued before it are
@@ -90,16 +98,24 @@ constexpr int kHalfMirror = 0x141;   // lane i <-> 7-i within each 8 lanes
 constexpr int kMirror = 0x140;       // lane i <-> 15-i within each row
 constexpr int kRowShr = 0x110;       // + n: lane i reads lane i-n of its row
 
+// Row shifts leave the first lanes of a row without a source: those keep
+// zero.  The other controls give every lane a source, so no old value is
+// named (bound_ctrl set, which then changes nothing) and the move can fold
+// into the instruction that consumes it (v_add_f32_dpp and the like).
+template <int CTRL>
+__device__ __forceinline__ int move32(int v) {
+    if constexpr ((CTRL & 0x1f0) == kRowShr) return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+    else return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, true);
+}
 template <int CTRL, class T>
 __device__ __forceinline__ T move(T v) {
     static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit lanes");
     if constexpr (sizeof(T) == 4) {
-        return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf,
-                                                                 false));
+        return __builtin_bit_cast(T, move32<CTRL>(__builtin_bit_cast(int, v)));
     } else {
         const uint64_t u = __builtin_bit_cast(uint64_t, v);
-        const uint32_t lo = uint32_t(__builtin_amdgcn_update_dpp(0, int(uint32_t(u)), CTRL, 0xf, 0xf, false));
-        const uint32_t hi = uint32_t(__builtin_amdgcn_update_dpp(0, int(uint32_t(u >> 32)), CTRL, 0xf, 0xf, false));
+        const uint32_t lo = uint32_t(move32<CTRL>(int(uint32_t(u))));
+        const uint32_t hi = uint32_t(move32<CTRL>(int(uint32_t(u >> 32))));
         return __builtin_bit_cast(T, (uint64_t(hi) << 32) | lo);
     }
 }
@@ -135,12 +151,15 @@ __device__ __forceinline__ T wave_reduce(T v, Op op) {
 
 struct Add { template <class T> __device__ T operator()(T a, T b) const { return a + b; } };
 struct Max { template <class T> __device__ T operator()(T a, T b) const { return b > a ? b : a; } };
+// fmaxf: a NaN operand gives the other one
+struct FMax { __device__ float operator()(float a, float b) const { return fmaxf(a, b); } };
 struct And { template <class T> __device__ T operator()(T a, T b) const { return a & b; } };
 struct Or { template <class T> __device__ T operator()(T a, T b) const { return a | b; } };
 }  // namespace dpp
 
 template <class T> __device__ __forceinline__ T wave_sum(T v) { return dpp::wave_reduce(v, dpp::Add()); }
 template <class T> __device__ __forceinline__ T wave_max(T v) { return dpp::wave_reduce(v, dpp::Max()); }
+__device__ __forceinline__ float wave_fmax(float v) { return dpp::wave_reduce(v, dpp::FMax()); }
 __device__ __forceinline__ uint64_t wave_and(uint64_t v) { return dpp::wave_reduce(v, dpp::And()); }
 __device__ __forceinline__ uint64_t wave_or(uint64_t v) { return dpp::wave_reduce(v, dpp::Or()); }
 

@@ -1730,13 +1730,6 @@ __global__ __launch_bounds__(256) void k_probs(SelectArgs a) {
 // layer's last ones are summed, so a layer boundary costs no load latency.
 // Sums restart at each layer's first row (binary32, token order, as in
 // summary_block).
-// Raw buffer resource over `bytes` bytes from `p` (dword 3 selects the
-// 32-bit data format, which enables untyped loads).  Loads at offsets past
-// `bytes` return zeros instead of touching memory.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const uint8_t *p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(p), short(0), int(bytes), 0x00020000);
-}
-constexpr int kBufferNontemporal = 2;  // cache-policy bits of a streaming load
 
 // PAGED: every wave's 64 channel groups lie in one page (width a multiple of
 // 512 channels) and a page spans less than 4 GiB.  Then the page and its

@@ -6,7 +6,7 @@ to |gpu - oracle| <= 1e-6 + 2e-4 * oracle (the reference's own check allows
 2e-3 absolute, src/adapter/llama-kvmem-attention.cpp:44-96).  Covered: every
 key format (f16, bf16, f32, q8_0, q4_0, q5_0), query and mask scalars, head
 dims 32..256, causal and fully masked pages, a fully masked row (NaN, as in
-the reference), softcap, pages longer than a workgroup, more rows than one
+the reference), softcap, pages of 1 to 16 tiles and longer than a workgroup, more rows than one
 launch holds, padded and 2-byte-offset key layouts, and the argument checks.
 """
 import math
@@ -115,6 +115,15 @@ def test_head_dims_and_groups(ctx, dim, heads, kv):
     rng = np.random.default_rng(dim + heads)
     for k_fmt in (O.FMT_F16, O.FMT_Q8_0, O.FMT_Q5_0):
         assert_close(*run_case(ctx, rng, dim=dim, heads=heads, kv=kv, tokens=700, page=32, k_fmt=k_fmt))
+
+
+@pytest.mark.parametrize("page", [16, 32, 64, 128, 256])
+def test_page_runs(ctx, page):
+    # pages of 1, 2, 4, 8 and 16 tiles: a wave's tiles of a page form runs of
+    # 1, 1, 1, 2 and 4 tiles (one exponential per token); a partial last page
+    rng = np.random.default_rng(70 + page)
+    for k_fmt in (O.FMT_F16, O.FMT_Q8_0):
+        assert_close(*run_case(ctx, rng, tokens=5 * page + 37, page=page, k_fmt=k_fmt, heads=8, kv=2))
 
 
 def test_softcap_and_long_pages(ctx):
