@@ -552,7 +552,7 @@ typedef struct kvr_attention_sample {
 
 /* Workspace of kvr_attention_page_mass for n_rows sampled rows: up to
  * KVR_ATTENTION_ROWS rows go in one launch, fewer when their page
- * log-sum-exp table would pass 32 MiB. */
+ * log-sum-exp tables (12 bytes per row, head and page) would pass 32 MiB. */
 #define KVR_ATTENTION_ROWS 64
 size_t kvr_attention_workspace_bytes(uint32_t n_rows, uint32_t query_heads, uint32_t pages);
 

@@ -223,6 +223,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
     // NL chunks per lane for a 16-row tile
     constexpr uint32_t RB = 136 * R, CPR = (RB + 15) / 16, CH = kTokenTile * CPR, NL = (CH + kWave - 1) / kWave;
     __shared__ float part[2][kMaxPageGroup][kAttnWaves][kPairTile];  // max, sum
+    __shared__ float glse[kMaxPageGroup][kPairTile];                 // the group's log-sum-exps
     // q8_0: one LDS tile per wave (a tile is staged and consumed within one
     // step, and a wave's LDS operations complete in order)
     __shared__ __align__(16) uint8_t q8_tiles[kQ8 ? kAttnWaves * kTokenTile * RB : 16];
@@ -354,7 +355,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
     auto q_on = [&](int r, int s) { return 4 * r + (kHalf ? uint32_t(s) / 8 : kg) < nb; };
     float qa[R][32];
     f16x8 qh[R][4], ql[R][4];
-    float lscale[4];  // logit scale of the lane's output pairs 4*kg + i
+    float lscale[4];   // logit scale of the lane's output pairs 4*kg + i
+    float lscale2[4];  // the same times log2(e)
     {
         const uint32_t p = p0 + col;
         const uint32_t pc = min(p, npairs - 1);
@@ -384,9 +386,12 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
                 for (int s = 0; s < 32; ++s) mx = fmaxf(mx, fabsf(qa[r][s]));
             mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
             mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-            // 2^-e brings it below 2^15 (exact; e = 0 for |q| < 2^14)
-            // (binary exponent from the bits; subnormal maxima keep e = 0)
-            const int e = min(max(int((__float_as_uint(mx) >> 23) & 0xffu) - 127 - 13, 0), 100);
+            // 2^-e brings it into [2^13, 2^15) (exact), small queries scaled
+            // up as large ones are scaled down, so the fp16 parts keep their
+            // bits (binary exponent from the bits; e in [-100, 100], so a zero
+            // or subnormal maximum stays tiny and the logit scale 2^e * scale
+            // stays a normal number)
+            const int e = min(max(int((__float_as_uint(mx) >> 23) & 0xffu) - 127 - 13, -100), 100);
 #pragma unroll
             for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -401,9 +406,13 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
             const float own = __builtin_ldexpf(a.scale, e);
 #pragma unroll
             for (int i = 0; i < 4; ++i) lscale[i] = __shfl(own, 4 * kg + i, kWave);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) lscale2[i] = lscale[i] * kLog2e;
         } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i) lscale[i] = a.scale;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) lscale2[i] = a.scale * kLog2e;
         }
     }
     lds_barrier();  // partials initialized
@@ -522,10 +531,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
 #pragma unroll
             for (int b = 0; b < 4 * R; ++b)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    if (b & 1) acc1[i] = fmaf(t[b][i], db[b], acc1[i]);
-                    else acc0[i] = fmaf(t[b][i], db[b], acc0[i]);
-                }
+                for (int i = 0; i < 4; ++i) acc0[i] = fmaf(t[b][i], db[b], acc0[i]);
         }
         if constexpr (PATH == kPathF32) {
             // even and odd k-steps; k-steps past the head dim have zero
@@ -540,13 +546,24 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
         }
         bool live;
         (void)tile_token(k, live);
+        // base-2 logits: (dot * scale + bias) * log2(e), one fma without a
+        // softcap (scale and bias premultiplied by log2(e))
         float l[4];
+        if (a.softcap > 0.0f) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const bool use = live && __builtin_isfinite(bias[i]);
-            float x = (acc0[i] + acc1[i]) * lscale[i];
-            if (a.softcap > 0.0f) x = a.softcap * tanhf(x / a.softcap);
-            l[i] = use ? (x + bias[i]) * kLog2e : -__builtin_inff();
+            for (int i = 0; i < 4; ++i) {
+                const bool use = live && __builtin_isfinite(bias[i]);
+                float x = (kQ8 ? acc0[i] : acc0[i] + acc1[i]) * lscale[i];
+                x = a.softcap * tanhf(x / a.softcap);
+                l[i] = use ? (x + bias[i]) * kLog2e : -__builtin_inff();
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const bool use = live && __builtin_isfinite(bias[i]);
+                const float b2 = G4 && i > 0 ? bias[0] * kLog2e : bias[i] * kLog2e;
+                l[i] = use ? fmaf(kQ8 ? acc0[i] : acc0[i] + acc1[i], lscale2[i], b2) : -__builtin_inff();
+            }
         }
         if constexpr (BATCH) {
 #pragma unroll
@@ -627,22 +644,39 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
         }
         // back to base e: lse = (max2 + log2(total)) * ln 2
         const uint32_t r = p / a.group, h = kv * a.group + p % a.group;
-        a.lse[(uint64_t(r) * a.heads + h) * a.pages + pg0 + pl] =
-            total > 0.0f ? (mx + __builtin_amdgcn_logf(total)) * kLn2 : -__builtin_inff();
+        const float v = total > 0.0f ? (mx + __builtin_amdgcn_logf(total)) * kLn2 : -__builtin_inff();
+        a.lse[(uint64_t(r) * a.heads + h) * a.pages + pg0 + pl] = v;
+        glse[pl][pr] = v;
+    }
+    lds_barrier();
+    // Each pair's max m of the group's page log-sum-exps and sum of
+    // exp(lse - m) (0 when every page is -inf): the normalization's max and
+    // sum over pages, taken per page group here and combined over the
+    // groups by the mass kernel.
+    if (tid < kPairTile && p0 + tid < npairs) {
+        float m = -__builtin_inff(), sum = 0.0f;
+        for (uint32_t pl = 0; pl < npg; ++pl) m = fmaxf(m, glse[pl][tid]);
+        if (m > -__builtin_inff())
+            for (uint32_t pl = 0; pl < npg; ++pl) sum += expf(glse[pl][tid] - m);
+        const uint32_t p = p0 + tid, r = p / a.group, h = kv * a.group + p % a.group;
+        float *st = a.stats + ((uint64_t(r) * a.heads + h) * groups + pg0 / a.page_group) * 2;
+        st[0] = m;
+        st[1] = sum;
     }
 }
 
 // Masses of one sampled row over a chunk of 256 pages.  Every workgroup of
-// the row first takes, for each head, the max of its page log-sum-exps and
-// 1/sum of exp(lse - max): each wave takes eight heads at a time with all
-// their pages' loads in flight (up to 512 pages per pass, a running max and
-// rescaled sum beyond).  Then, for each page of its chunk, the head average
-// of exp(lse - max) * (1/sum): the reference's normalize and average
-// kernels.  The row's log-sum-exps are read through one buffer resource
-// with 32-bit offsets (the host keeps a row under 4 GiB), and each batch of
-// loads is issued before the first of them is used.
+// the row first takes, for each head, the max M over pages of its page
+// log-sum-exps and 1/S, S = sum of exp(lse - M), from the page groups'
+// (max m, sum s) pairs: M = max of the m, S = sum of s * exp(m - M).  One
+// head per 16-lane row at a time, two heads per row with their loads in
+// flight, four groups per lane per pass (a running max and rescaled sum
+// beyond).  Then, for each page of its chunk, the head average of
+// exp(lse - M) * (1/S): the reference's normalize and average kernels.
+// The row's tables are read through buffer resources with 32-bit offsets
+// (the host keeps a row's under 4 GiB), and each batch of loads is issued
+// before the first of them is used.
 constexpr uint32_t kMassPages = 256;
-constexpr int kMassHeads = 8;
 __device__ __forceinline__ float lse_at(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
     return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, int(off), 0, 0));
 }
@@ -650,50 +684,51 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_mass(AttnArgs a) {
     extern __shared__ float norm[];  // [heads][2]
     const uint32_t r = blockIdx.y, tid = threadIdx.x, lane = tid % kWave;
     const uint32_t w = __builtin_amdgcn_readfirstlane(tid / kWave);
-    const uint32_t row_bytes = a.heads * a.pages * uint32_t(sizeof(float));
-    const auto rs = buffer_rsrc(a.lse + uint64_t(r) * a.heads * a.pages, row_bytes);
-    for (uint32_t h0 = w * kMassHeads; h0 < a.heads; h0 += kAttnWaves * kMassHeads) {
-        float mx[kMassHeads], sum[kMassHeads];
+    const uint32_t groups = (a.pages + a.page_group - 1) / a.page_group;
+    const auto rs = buffer_rsrc(a.lse + uint64_t(r) * a.heads * a.pages, a.heads * a.pages * uint32_t(sizeof(float)));
+    const auto ss = buffer_rsrc(a.stats + uint64_t(r) * a.heads * groups * 2, a.heads * groups * 2 * uint32_t(sizeof(float)));
+    const uint32_t row = w * 4 + lane / 16, c = lane % 16;  // 16 rows of 16 lanes
+    for (uint32_t h0 = row; h0 < a.heads; h0 += 32) {
+        float m[2], sum[2];
 #pragma unroll
-        for (int j = 0; j < kMassHeads; ++j) {
-            mx[j] = -__builtin_inff();
+        for (int j = 0; j < 2; ++j) {
+            m[j] = -__builtin_inff();
             sum[j] = 0.0f;
         }
-        for (uint32_t q0 = 0; q0 < a.pages; q0 += 8 * kWave) {
-            float v[kMassHeads][8];
+        for (uint32_t g0 = 0; g0 < groups; g0 += 64) {
+            float vm[2][4], vs[2][4];
 #pragma unroll
-            for (int j = 0; j < kMassHeads; ++j) {
-                const uint32_t head = min(h0 + j, a.heads - 1) * a.pages;
+            for (int j = 0; j < 2; ++j) {
+                const uint32_t h = min(h0 + 16 * j, a.heads - 1);
 #pragma unroll
-                for (int u = 0; u < 8; ++u)
-                    v[j][u] = lse_at(rs, (head + min(q0 + u * kWave + lane, a.pages - 1)) * uint32_t(sizeof(float)));
+                for (int u = 0; u < 4; ++u) {
+                    const uint32_t off = (h * groups + min(g0 + 16 * u + c, groups - 1)) * 2 * uint32_t(sizeof(float));
+                    vm[j][u] = lse_at(ss, off);
+                    vs[j][u] = lse_at(ss, off + 4);
+                }
             }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int j = 0; j < kMassHeads; ++j) {
+            for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int u = 0; u < 8; ++u)
-                    if (q0 + u * kWave + lane >= a.pages) v[j][u] = -__builtin_inff();
-                float cm = v[j][0];
-#pragma unroll
-                for (int u = 1; u < 8; ++u) cm = fmaxf(cm, v[j][u]);
-                const float nm = fmaxf(mx[j], cm);
-                float add = 0.0f;
-#pragma unroll
-                for (int u = 0; u < 8; ++u) add += v[j][u] > -__builtin_inff() ? expf(v[j][u] - nm) : 0.0f;
-                sum[j] = (sum[j] > 0.0f ? sum[j] * expf(mx[j] - nm) : 0.0f) + add;
-                mx[j] = nm;
-            }
+                for (int u = 0; u < 4; ++u) {
+                    const bool on = g0 + 16 * u + c < groups && vs[j][u] > 0.0f;
+                    const float x = on ? vm[j][u] : -__builtin_inff();
+                    const float nm = fmaxf(m[j], x);
+                    sum[j] = (sum[j] > 0.0f ? sum[j] * expf(m[j] - nm) : 0.0f) + (on ? vs[j][u] * expf(x - nm) : 0.0f);
+                    m[j] = nm;
+                }
         }
 #pragma unroll
-        for (int j = 0; j < kMassHeads; ++j) {
-            const float wm = wave_fmax(mx[j]);
-            const float ws = wave_sum(sum[j] > 0.0f ? sum[j] * expf(mx[j] - wm) : 0.0f);
-            if (lane == 0 && h0 + j < a.heads) {
+        for (int j = 0; j < 2; ++j) {
+            const float gm = dpp::group_reduce(m[j], 16, dpp::FMax());
+            const float gs = dpp::group_reduce(sum[j] > 0.0f ? sum[j] * expf(m[j] - gm) : 0.0f, 16, dpp::Add());
+            const uint32_t h = h0 + 16 * j;
+            if (c == 0 && h < a.heads) {
                 // a head whose every page is -inf: max -inf, 1/sum NaN (as
                 // the reference's normalize gives)
-                norm[2 * (h0 + j)] = wm;
-                norm[2 * (h0 + j) + 1] = wm > -__builtin_inff() ? 1.0f / ws : __builtin_nanf("");
+                norm[2 * h] = gm;
+                norm[2 * h + 1] = gm > -__builtin_inff() ? 1.0f / gs : __builtin_nanf("");
             }
         }
     }
@@ -745,8 +780,9 @@ hipError_t launch_lse(const AttnArgs &a, hipStream_t s) {
 }  // namespace
 
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s) {
-    // one row's log-sum-exps are addressed with 32-bit byte offsets
-    if (uint64_t(a.heads) * a.pages * sizeof(float) > 0xffffffffull) return hipErrorInvalidValue;
+    // one row's log-sum-exps and group pairs are addressed with 32-bit byte
+    // offsets
+    if (uint64_t(a.heads) * a.pages * 2 * sizeof(float) > 0xffffffffull) return hipErrorInvalidValue;
     hipError_t e = hipErrorInvalidValue;
     switch (a.k_format) {
     case kKeyF16: e = launch_lse<kKeyF16>(a, s); break;

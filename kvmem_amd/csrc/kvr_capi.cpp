@@ -1598,8 +1598,10 @@ namespace {
 
 constexpr size_t kAttnBudget = size_t(32) << 20;  // page log-sum-exp bytes per launch
 
+// Per sampled row of a launch: the page log-sum-exps and, at most one per
+// page, the page groups' (max, sum) pairs.
 uint32_t attention_rows_per_launch(uint32_t n_rows, uint32_t heads, uint32_t pages) {
-    const size_t per_row = std::max<size_t>(1, size_t(heads) * pages * sizeof(float));
+    const size_t per_row = std::max<size_t>(1, size_t(heads) * pages * 3 * sizeof(float));
     const size_t fit = std::max<size_t>(1, kAttnBudget / per_row);
     return uint32_t(std::min<size_t>({size_t(n_rows), fit, size_t(kvr::kAttnRows)}));
 }
@@ -1626,7 +1628,7 @@ size_t attention_key_row_bytes(kvr_format f, uint32_t dim) {
 size_t kvr_attention_workspace_bytes(uint32_t n_rows, uint32_t query_heads, uint32_t pages) {
     if (!n_rows || !query_heads || !pages) return 0;
     const uint32_t rows = attention_rows_per_launch(n_rows, query_heads, pages);
-    return align256(size_t(rows) * query_heads * pages * sizeof(float));
+    return align256(size_t(rows) * query_heads * pages * 3 * sizeof(float));
 }
 
 kvr_status kvr_attention_page_mass(kvr_context *ctx, const kvr_attention_sample *a, float *mass, void *stream) {
@@ -1661,6 +1663,9 @@ kvr_status kvr_attention_page_mass(kvr_context *ctx, const kvr_attention_sample 
         return fail(KVR_ERR_INVALID, "key strides overlap rows of %zu bytes", krow);
     const uint32_t pages = page_count(a->tokens, a->page_tokens);
     if (uint64_t(pages) * a->kv_heads > 0x7fffffffu) return fail(KVR_ERR_INVALID, "too many attention pages");
+    if (uint64_t(pages) * a->query_heads * 2 * sizeof(float) > 0xffffffffull)
+        return fail(KVR_ERR_UNSUPPORTED, "attention tables of one row (%u heads x %u pages) pass 4 GiB",
+                    a->query_heads, pages);
     const uint32_t group = a->query_heads / a->kv_heads;
     const uint32_t chunk = attention_rows_per_launch(a->n_rows, a->query_heads, pages);
     DeviceGuard guard(ctx->device);
@@ -1699,6 +1704,7 @@ kvr_status kvr_attention_page_mass(kvr_context *ctx, const kvr_attention_sample 
     g.scale = a->scale;
     g.softcap = a->softcap;
     g.lse = reinterpret_cast<float *>(ctx->ws);
+    g.stats = g.lse + size_t(chunk) * a->query_heads * pages;
     if (kvr_status st = ws_order(ctx, s)) return st;
     for (uint32_t first = 0; first < a->n_rows; first += chunk) {
         g.n_rows = std::min(chunk, a->n_rows - first);

@@ -301,6 +301,7 @@ struct AttnArgs {
     uint32_t page_group;  // pages per workgroup, 1..16
     float scale, softcap;
     float *lse;       // [n_rows][heads][pages]
+    float *stats;     // [n_rows][heads][page groups][2]: max, sum of exp(lse - max)
     float *mass;      // [n_rows][pages], this launch's first row
     uint32_t n_rows;  // <= kAttnRows
     uint32_t rows[kAttnRows];       // query rows

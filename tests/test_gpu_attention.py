@@ -54,7 +54,7 @@ def key_rows(rng, fmt, tokens, kv, dim, head_stride, row_stride):
 
 def run_case(ctx, rng, *, dim=128, heads=8, kv=2, tokens=1000, page=64, rows=(3, 0, 5), n_q_rows=6,
              k_fmt=O.FMT_F16, q_fmt=O.FMT_F32, m_fmt=O.FMT_F32, softcap=0.0, head_pad=0, row_pad=0,
-             q_row_pad=0, mask_fn=None, scale=None):
+             q_row_pad=0, mask_fn=None, scale=None, q_fn=None):
     scale = 1 / math.sqrt(dim) if scale is None else scale
     hb = dim // 32 * BLOCK_BYTES[k_fmt]
     head_stride = hb + head_pad
@@ -63,6 +63,8 @@ def run_case(ctx, rng, *, dim=128, heads=8, kv=2, tokens=1000, page=64, rows=(3,
     qel, mel = SCALAR_BYTES[q_fmt], SCALAR_BYTES[m_fmt]
     q_row_stride = heads * dim * qel + q_row_pad
     qf = rng.standard_normal((n_q_rows, q_row_stride // qel)).astype(np.float32)
+    if q_fn is not None:
+        qf = q_fn(qf).astype(np.float32)
     qraw = scalars(qf, q_fmt).view(np.uint8).reshape(-1)
     mask = np.zeros((n_q_rows, tokens), np.float32)
     for r in range(n_q_rows):
@@ -124,6 +126,23 @@ def test_page_runs(ctx, page):
     rng = np.random.default_rng(70 + page)
     for k_fmt in (O.FMT_F16, O.FMT_Q8_0):
         assert_close(*run_case(ctx, rng, tokens=5 * page + 37, page=page, k_fmt=k_fmt, heads=8, kv=2))
+
+
+def test_query_magnitudes(ctx):
+    # f32 queries from 1e-6 to 1e6: each (row, head) pair at its own
+    # magnitude and elements spread over three decades inside a pair (the
+    # fp16 matrix-core forms scale each pair by a power of two either way)
+    rng = np.random.default_rng(81)
+    heads, dim = 8, 128
+
+    def spread(q):
+        rows = q.shape[0]
+        mag = 10.0 ** rng.uniform(-6, 6, (rows, heads, 1))
+        inner = 10.0 ** rng.uniform(-1.5, 1.5, (rows, heads, dim))
+        return (q.reshape(rows, heads, dim) * mag * inner).reshape(rows, -1)
+    for k_fmt in (O.FMT_F16, O.FMT_Q8_0):
+        assert_close(*run_case(ctx, rng, heads=heads, kv=2, dim=dim, tokens=800, page=64, k_fmt=k_fmt,
+                               q_fn=spread, scale=0.05))
 
 
 def test_softcap_and_long_pages(ctx):
