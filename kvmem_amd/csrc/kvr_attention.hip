@@ -250,12 +250,18 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_lse(AttnArgs a) {
     // wave-local tile k is flat tile w + 4k: page pg0 + flat/T, tile flat%T;
     // tokens past the page or the sequence are clamped to the last token
     // (in bounds) and not counted
-    auto tile_page = [&](uint32_t k) { return min(w + kAttnWaves * k, nflat - 1) / T; };
+    // flat tile -> (page, tile of the page); BATCH pages are a power of two
+    // of tiles, so a shift (the division otherwise: dozens of scalar
+    // instructions per tile)
+    const uint32_t tsh = uint32_t(__builtin_ctz(T));
+    auto tdiv = [&](uint32_t f) { return BATCH ? f >> tsh : f / T; };
+    auto tmod = [&](uint32_t f) { return BATCH ? f & (T - 1) : f % T; };
+    auto tile_page = [&](uint32_t k) { return tdiv(min(w + kAttnWaves * k, nflat - 1)); };
     auto tile_first = [&](uint32_t k, uint32_t &end) {
         const uint32_t fc = min(w + kAttnWaves * k, nflat - 1);
-        const uint32_t pg = pg0 + fc / T;
+        const uint32_t pg = pg0 + tdiv(fc);
         end = min(pg * a.page_tokens + a.page_tokens, a.tokens);
-        return pg * a.page_tokens + (fc % T) * kTokenTile;
+        return pg * a.page_tokens + tmod(fc) * kTokenTile;
     };
     auto tile_token = [&](uint32_t k, bool &live) {
         uint32_t end;
