@@ -69,6 +69,12 @@ __device__ __forceinline__ void add_q8x8(float *acc, uint32_t lo, uint32_t hi, f
     }
 }
 
+// The summary launch's fp16 key rows take the default cache policy
+// (measured 1.4 us faster per 64 MiB layer than the streaming one); its q8_0
+// rows and the stack's keep the streaming policy, which measured faster
+// there (q8_0 summary 42.0 against 46.9 us per 131072-token layer; stack
+// 15.2 against 16.6 us per 32768-token fp16 layer, 26.8 against 29.7 per
+// 131072-token q8_0 layer).
 // Consumes rows 0..n-1 (n >= 1) in order through a ring of D loads in
 // flight: row t's load issues D rows before row t is used.  Loads past the
 // end are clamped to row n-1 (in bounds, never used), so no load sits behind
@@ -114,14 +120,16 @@ __device__ __forceinline__ void stream_rows(uint32_t n, Load load, Use use) {
 // through the fp16 operand boundary, staged once in dynamic LDS.
 extern __shared__ __align__(16) uint16_t q_lds_buf[];
 
-// One 256-thread block of the summary grid (`block` = its index in it).
-template <int SRC, bool FUSE>
+// One BS-thread block of the summary grid (`block` = its index in it):
+// 256 threads, or 64 where a launch has fewer 256-thread blocks than the GPU
+// has CUs (a lone small layer), so its blocks spread over every CU.
+template <int SRC, bool FUSE, int BS = 256>
 __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t block, uint16_t *q_lds) {
     // Above the stage-in gather's waves when both share a CU: this kernel
     // is on the select critical path, the gather is bound by the host link.
     __builtin_amdgcn_s_setprio(2);
     const uint32_t gpp = a.width >> 3;  // 8-channel groups per page
-    const uint64_t gid = uint64_t(block) * 256 + threadIdx.x;
+    const uint64_t gid = uint64_t(block) * BS + threadIdx.x;
     const uint64_t total = uint64_t(a.lanes) * a.pages * gpp;
     // Threads past the end still take part in the query-staging barrier.
     const bool active = gid < total;
@@ -141,23 +149,23 @@ __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t blo
     // nor the epilogue waits on a query round trip.
     // Packed fp16 rows of up to 4096 elements take two 16-byte loads per
     // thread (qvec); other queries kQueryPrefetch single elements (qraw).
-    constexpr uint32_t kQueryPrefetch = 16, kQueryVec = 2;
+    constexpr uint32_t kQueryPrefetch = 16, kQueryVec = 2 * (256 / BS);
     uint32_t qraw[kQueryPrefetch];
     u32x4 qvec[kQueryVec];
     uint32_t staged_lane = 0xffffffffu, nq = 0;
     bool qv = false;
     if (FUSE && a.q_stage) {
-        staged_lane = uint32_t((uint64_t(block) * 256 / gpp) / a.pages);
+        staged_lane = uint32_t((uint64_t(block) * BS / gpp) / a.pages);
         nq = a.q.rows * a.q.qheads * a.q.dim;
-        qv = a.q.packed16 && nq <= 256 * 8 * kQueryVec;
+        qv = a.q.packed16 && nq <= BS * 8 * kQueryVec;
         if (qv) {
             const u32x4 *qp = reinterpret_cast<const u32x4 *>(a.q.data + staged_lane * a.q.lane_stride);
 #pragma unroll
-            for (uint32_t j = 0; j < kQueryVec; ++j) qvec[j] = qp[min(threadIdx.x + 256 * j, nq / 8 - 1)];
+            for (uint32_t j = 0; j < kQueryVec; ++j) qvec[j] = qp[min(threadIdx.x + BS * j, nq / 8 - 1)];
         } else {
 #pragma unroll
             for (uint32_t j = 0; j < kQueryPrefetch; ++j) {
-                const uint32_t i = min(threadIdx.x + 256 * j, nq - 1);  // in bounds; extras unused
+                const uint32_t i = min(threadIdx.x + BS * j, nq - 1);  // in bounds; extras unused
                 qraw[j] = load_raw(query_elem(a.q, staged_lane, i), a.q.scalar);
             }
         }
@@ -185,7 +193,7 @@ __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t blo
                 a.src + lane * a.src_lane_stride + (t0 * a.width + c0) * 2);
             const uint64_t stride = gpp;  // 16-byte words per token row
             stream_rows<kF16Rows>(
-                n, [&](uint32_t t) { return __builtin_nontemporal_load(p + t * stride); },
+                n, [&](uint32_t t) { return p[t * stride]; },
                 [&](const u32x4 v) { add_f16x8(acc, v); });
         } else {
             // q8_0 rows: lane owns 8 codes (quarter s) of block b, and the
@@ -227,7 +235,7 @@ __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t blo
         uint32_t qbad = kOperandOk;
 #pragma unroll
         for (uint32_t j = 0; j < kQueryVec; ++j) {
-            const uint32_t i8 = threadIdx.x + 256 * j;
+            const uint32_t i8 = threadIdx.x + BS * j;
             if (i8 < nq / 8) {
 #pragma unroll
                 for (int w = 0; w < 4; ++w) {
@@ -244,7 +252,7 @@ __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t blo
             uint32_t qbad = kOperandOk;
 #pragma unroll
             for (uint32_t j = 0; j < kQueryPrefetch; ++j) {
-                const uint32_t i = threadIdx.x + 256 * j;
+                const uint32_t i = threadIdx.x + BS * j;
                 uint16_t qh = 0;
                 const uint32_t e = recall16(raw_value(qraw[j], q.scalar), qh);
                 if (i < nq) {
@@ -253,13 +261,13 @@ __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t blo
                 }
             }
             // the rest, 16 loads in flight per pass
-            for (uint32_t base = threadIdx.x + 256 * kQueryPrefetch; base < nq; base += 256 * kQueryPrefetch) {
+            for (uint32_t base = threadIdx.x + BS * kQueryPrefetch; base < nq; base += BS * kQueryPrefetch) {
 #pragma unroll
                 for (uint32_t j = 0; j < kQueryPrefetch; ++j)
-                    qraw[j] = load_raw(query_elem(q, staged_lane, min(base + 256 * j, nq - 1)), q.scalar);
+                    qraw[j] = load_raw(query_elem(q, staged_lane, min(base + BS * j, nq - 1)), q.scalar);
 #pragma unroll
                 for (uint32_t j = 0; j < kQueryPrefetch; ++j) {
-                    const uint32_t i = base + 256 * j;
+                    const uint32_t i = base + BS * j;
                     uint16_t qh = 0;
                     const uint32_t e = recall16(raw_value(qraw[j], q.scalar), qh);
                     if (i < nq) {
@@ -345,9 +353,9 @@ __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t blo
     }
 }
 
-template <int SRC, bool FUSE>
-__global__ __launch_bounds__(256) void k_summary(SummaryArgs a) {
-    summary_block<SRC, FUSE>(a, blockIdx.x, q_lds_buf);
+template <int SRC, bool FUSE, int BS>
+__global__ __launch_bounds__(BS) void k_summary(SummaryArgs a) {
+    summary_block<SRC, FUSE, BS>(a, blockIdx.x, q_lds_buf);
 }
 
 // ---------------------------------------------------------------------------
@@ -476,7 +484,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 
-constexpr uint32_t kTailLdsPages = 8192;  // keys of up to this many pages stay in LDS
+constexpr uint32_t kTailLdsPages = 7680;  // keys of up to this many pages stay in LDS (<= 64 KiB padded)
 
 // Registers: value i of a lane is page j = l + 64*i.
 template <int NPL>
@@ -887,6 +895,10 @@ struct FixedPages {
 
 // Dynamic LDS of the selection kernels: the lane's keys (pages <= kTailLdsPages).
 extern __shared__ __align__(16) uint64_t tail_keys[];
+// LDS slot of page j's key: one pad slot after every 16 keys, so the 16-key
+// chunks that consecutive threads walk start in different banks (unpadded,
+// a wave's key reads fall on two banks).
+__host__ __device__ constexpr uint32_t key_slot(uint32_t j) { return j + (j >> 4); }
 
 // One wave finds, in a complete 256-bin digit histogram, the digit `d`
 // holding the `remaining`-th best key, the rank `rem` within it and its
@@ -980,7 +992,7 @@ __device__ __forceinline__ void wave_select(const SelectArgs &a, uint32_t lane, 
     const uint32_t l = threadIdx.x & 63;
     const uint32_t C = (n + kWave - 1) / kWave;
     const uint32_t j0 = min(n, l * C), j1 = min(n, j0 + C);
-    auto load_key = [&](uint32_t j) -> uint64_t { return lds ? tail_keys[j] : order_key(sc[j]); };
+    auto load_key = [&](uint32_t j) -> uint64_t { return lds ? tail_keys[key_slot(j)] : order_key(sc[j]); };
     uint64_t kr[R];
     uint32_t cand_bits = 0;  // chunk entries that are candidates
 #pragma unroll
@@ -1078,7 +1090,7 @@ __device__ __forceinline__ void wg_select(const SelectArgs &a, uint32_t lane, ui
     const uint32_t tid = threadIdx.x, w = tid / kWave, l = tid % kWave;
     const uint32_t C = (n + B - 1) / B;
     const uint32_t j0 = min(n, tid * C), j1 = min(n, j0 + C);
-    auto load_key = [&](uint32_t j) -> uint64_t { return lds ? tail_keys[j] : order_key(sc[j]); };
+    auto load_key = [&](uint32_t j) -> uint64_t { return lds ? tail_keys[key_slot(j)] : order_key(sc[j]); };
     // chunks of up to 64 ids (rows up to 16384 pages) keep their fixed
     // pages in a register mask; longer chunks test the LDS bitmap per pass
     const bool masked = C <= 64;
@@ -1086,8 +1098,23 @@ __device__ __forceinline__ void wg_select(const SelectArgs &a, uint32_t lane, ui
     if (masked && fx.bits)
         for (uint32_t j = j0; j < j1; ++j)
             if (fx.at(j)) mand_bits |= 1ull << (j - j0);
+    // chunks of up to RK keys in LDS (every row that keeps its keys there)
+    // are read into registers once; the passes below walk the registers
+    constexpr uint32_t RK = 32;
+    const bool in_regs = lds && C <= RK;
+    uint64_t kr[RK];
+    if (in_regs) {
+#pragma unroll
+        for (uint32_t c = 0; c < RK; ++c) kr[c] = j0 + c < j1 ? tail_keys[key_slot(j0 + c)] : 0;
+    }
     // f(j, key, candidate) over this thread's chunk in id order
     auto chunk = [&](auto f) {
+        if (in_regs) {
+#pragma unroll
+            for (uint32_t c = 0; c < RK; ++c)
+                if (j0 + c < j1) f(j0 + c, kr[c], !(mand_bits >> c & 1ull));
+            return;
+        }
         for (uint32_t b = j0; b < j1; b += 8) {
             uint64_t kk[8];
 #pragma unroll
@@ -1533,7 +1560,7 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
     int bad = 0;
     auto note = [&](uint32_t j, double v) {
         bad |= !__builtin_isfinite(v) || (!a.signed_scores && v < 0.0);
-        if (lds) tail_keys[j] = order_key(v);
+        if (lds) tail_keys[key_slot(j)] = order_key(v);
     };
     if (a.do_aggregate) {
         // Contributing rows in the reference's order: (row, head) for Mean,
@@ -1608,6 +1635,36 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
                 if (a.accumulate) v = sc[j] + v;
                 sc[j] = v;
                 note(j, v);
+            }
+        } else if (nrows <= 16) {
+            // four columns per pass, their rows' loads in flight together
+            // (a long row takes a quarter of the round trips); each column's
+            // rows are still added in order
+            for (uint32_t j0 = tid; j0 < n; j0 += 4 * B) {
+                uint32_t jj[4];
+                double acc[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    jj[q] = min(j0 + q * B, n - 1);
+                    acc[q] = a.accumulate && j0 + q * B < n ? sc[jj[q]] : 0.0;
+                }
+                double v[4][16];
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (uint32_t u = 0; u < 16; ++u)
+                        v[q][u] = load_device(terms + row_of(min(u, nrows - 1)) * cols + jj[q]);
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (uint32_t u = 0; u < 16; ++u)
+                        if (u < nrows) acc[q] += v[q][u];
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (j0 + q * B < n) {
+                        sc[jj[q]] = acc[q];
+                        note(jj[q], acc[q]);
+                    }
             }
         } else {
             for (uint32_t j0 = tid; j0 < n; j0 += 2 * B) {
@@ -2666,21 +2723,30 @@ inline unsigned blocks_for(uint64_t threads, unsigned per = 256) {
 }  // namespace
 
 // ---- launchers ------------------------------------------------------------
+template <int BS>
+void launch_summary_bs(int source, bool fuse, const SummaryArgs &a, uint64_t threads, size_t lds, hipStream_t s) {
+    const dim3 grid(blocks_for(threads, BS)), block(BS);
+    if (source == kSrcKeysF16 && fuse)
+        hipLaunchKernelGGL((k_summary<kSrcKeysF16, true, BS>), grid, block, lds, s, a);
+    else if (source == kSrcKeysF16)
+        hipLaunchKernelGGL((k_summary<kSrcKeysF16, false, BS>), grid, block, 0, s, a);
+    else if (source == kSrcKeysQ8 && fuse)
+        hipLaunchKernelGGL((k_summary<kSrcKeysQ8, true, BS>), grid, block, lds, s, a);
+    else if (source == kSrcKeysQ8)
+        hipLaunchKernelGGL((k_summary<kSrcKeysQ8, false, BS>), grid, block, 0, s, a);
+    else
+        hipLaunchKernelGGL((k_summary<kSrcSummary, true, BS>), grid, block, lds, s, a);
+}
+
+constexpr uint64_t kSummarySpreadBlocks = 256;  // MI355X's CUs
 hipError_t launch_summary(int source, bool fuse, const SummaryArgs &a, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch\'s error
     const uint64_t threads = uint64_t(a.lanes) * a.pages * (a.width >> 3);
-    const dim3 grid(blocks_for(threads)), block(256);
     const size_t lds = fuse && a.q_stage ? size_t(a.q.rows) * a.q.qheads * a.q.dim * 2 : 0;  // q_lds_buf
-    if (source == kSrcKeysF16 && fuse)
-        hipLaunchKernelGGL((k_summary<kSrcKeysF16, true>), grid, block, lds, s, a);
-    else if (source == kSrcKeysF16)
-        hipLaunchKernelGGL((k_summary<kSrcKeysF16, false>), grid, block, 0, s, a);
-    else if (source == kSrcKeysQ8 && fuse)
-        hipLaunchKernelGGL((k_summary<kSrcKeysQ8, true>), grid, block, lds, s, a);
-    else if (source == kSrcKeysQ8)
-        hipLaunchKernelGGL((k_summary<kSrcKeysQ8, false>), grid, block, 0, s, a);
-    else
-        hipLaunchKernelGGL((k_summary<kSrcSummary, true>), grid, block, lds, s, a);
+    // a launch of fewer 256-thread blocks than CUs leaves CUs idle: 64-thread
+    // blocks spread the same key stream over four times as many CUs
+    if (blocks_for(threads) < kSummarySpreadBlocks) launch_summary_bs<64>(source, fuse, a, threads, lds, s);
+    else launch_summary_bs<256>(source, fuse, a, threads, lds, s);
     return hipGetLastError();
 }
 
@@ -2702,7 +2768,7 @@ hipError_t launch_logits_mfma(const MfmaLogitsArgs &a, hipStream_t s) {
 // pages; for longer rows with fixed pages, their bitmap.
 inline size_t tail_lds_bytes(const SelectArgs &a) {
     const uint32_t n = select_pages(a);
-    if (n <= kTailLdsPages) return size_t(n) * 8;
+    if (n <= kTailLdsPages) return size_t(key_slot(n) + 1) * 8;
     return a.do_select && (a.n_mandatory || a.n_fixed) ? size_t((n + 31) / 32) * 4 : 0;
 }
 
