@@ -286,7 +286,7 @@ def run(args):
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16 operands, f32 summaries, f64 scores",
-        "data": f"synthetic seeded N(0,1) (Irwin-Hall 12), seed {args.seed}",
+        "data": f"synthetic seeded N(0,1) (Box-Muller), seed {args.seed}",
         "config": {
             "workload": "resident-history scoring + recall, 64-layer stack at 131072 tokens",
             "step": "summaries + scores + softmax + top-k for every layer (scored-KV throughput); "
@@ -694,7 +694,7 @@ def run_workload(args):
         "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f16/q8_0/q4_1 operands, f32 summaries, f64 scores",
-        "data": f"synthetic seeded (device generator, Irwin-Hall 12 normals), seed {seed}",
+        "data": f"synthetic seeded (device generator, Box-Muller normals), seed {seed}",
         "config": {"workload": args.workload, **{k: v for k, v in w.items()}, "stack_layers": N},
         "select_us_per_layer": round(select_us, 2),
         "select_stack_us_per_layer": round(ms_per_step * 1e3 / N, 2),

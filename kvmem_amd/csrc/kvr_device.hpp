@@ -208,15 +208,91 @@ __host__ __device__ __forceinline__ uint64_t synth_base(uint64_t seed, uint64_t 
 __device__ __forceinline__ uint64_t synth_bits(uint64_t base, uint64_t counter) {
     return fmix64(base + (counter + 1) * kSynthG);
 }
-// Irwin-Hall(12) - 6: exact in binary64, then one rounding to binary32.
-__device__ __forceinline__ float synth_normal(uint64_t base, uint64_t index) {
-    int64_t total = 0;
-#pragma unroll
-    for (uint64_t j = 0; j < 6; ++j) {
-        const uint64_t r = synth_bits(base, index * 6 + j);
-        total += int64_t(r >> 40) + int64_t((r >> 16) & 0xffffffu);
+// N(0,1) by Box-Muller: normals 2j and 2j+1 are R cos(2 pi u2) and
+// R sin(2 pi u2), R = sqrt(-2 ln u1), where draws 2j and 2j+1 give u1 in
+// (0, 1] and u2 in [0, 1) with 53 bits each.  Everything is binary64 from
+// correctly rounded +, -, *, / only, so the oracle's statement of the same
+// steps gives the same bits on the CPU:
+//   ln x   = e ln 2 + 2 atanh(s), s = (m - 1)/(m + 1), x = m 2^e with m in
+//            (sqrt(1/2), sqrt(2)], the atanh series to s^23;
+//   sqrt y = six Newton steps y_{k+1} = (y_k + y/y_k)/2 from the power of
+//            two that halves y's exponent;
+//   2 pi t: the quarter turn q = floor(4t) and an eighth-turn reflection
+//            are exact, then Taylor series of sin and cos on [0, pi/4] (to
+//            x^15 and x^16).
+// No contraction into fused multiply-adds.  One rounding to binary32 last.
+__device__ __forceinline__ double synth_ln(double x) {
+#pragma clang fp contract(off)
+    uint64_t b = uint64_t(__double_as_longlong(x));
+    int e = int((b >> 52) & 0x7ffu) - 1023;
+    double m = __longlong_as_double((long long)((b & 0x000fffffffffffffull) | 0x3ff0000000000000ull));
+    if (m > 1.4142135623730951) {
+        m = m * 0.5;
+        e += 1;
     }
-    return float(double(total - 100663296) * 5.9604644775390625e-08);
+    const double s = (m - 1.0) / (m + 1.0), s2 = s * s;
+    double p = 1.0 / 23.0;
+    p = 1.0 / 21.0 + s2 * p;
+    p = 1.0 / 19.0 + s2 * p;
+    p = 1.0 / 17.0 + s2 * p;
+    p = 1.0 / 15.0 + s2 * p;
+    p = 1.0 / 13.0 + s2 * p;
+    p = 1.0 / 11.0 + s2 * p;
+    p = 1.0 / 9.0 + s2 * p;
+    p = 1.0 / 7.0 + s2 * p;
+    p = 1.0 / 5.0 + s2 * p;
+    p = 1.0 / 3.0 + s2 * p;
+    const double t = s2 * p;
+    return double(e) * 0.69314718055994530942 + 2.0 * (s + s * t);
+}
+__device__ __forceinline__ double synth_sqrt(double y) {
+#pragma clang fp contract(off)
+    if (y == 0.0) return 0.0;
+    const int e = int((uint64_t(__double_as_longlong(y)) >> 52) & 0x7ffu) - 1023;
+    double r = __longlong_as_double((long long)(uint64_t((e >> 1) + 1023) << 52));
+#pragma unroll
+    for (int k = 0; k < 6; ++k) r = (r + y / r) * 0.5;
+    return r;
+}
+// cos (SIN false) or sin (SIN true) of 2 pi t, t in [0, 1)
+template <bool SIN>
+__device__ __forceinline__ double synth_turn(double t) {
+#pragma clang fp contract(off)
+    const int q = int(t * 4.0);  // exact
+    double r = t - double(q) * 0.25;
+    const bool swap = r > 0.125;
+    if (swap) r = 0.25 - r;
+    const double x = r * 6.28318530717958647692, x2 = x * x;
+    double c = 1.0 / 20922789888000.0;
+    c = 1.0 / 87178291200.0 - x2 * c;
+    c = 1.0 / 479001600.0 - x2 * c;
+    c = 1.0 / 3628800.0 - x2 * c;
+    c = 1.0 / 40320.0 - x2 * c;
+    c = 1.0 / 720.0 - x2 * c;
+    c = 1.0 / 24.0 - x2 * c;
+    c = 0.5 - x2 * c;
+    c = 1.0 - x2 * c;
+    double sn = 1.0 / 1307674368000.0;
+    sn = 1.0 / 6227020800.0 - x2 * sn;
+    sn = 1.0 / 39916800.0 - x2 * sn;
+    sn = 1.0 / 362880.0 - x2 * sn;
+    sn = 1.0 / 5040.0 - x2 * sn;
+    sn = 1.0 / 120.0 - x2 * sn;
+    sn = 1.0 / 6.0 - x2 * sn;
+    sn = 1.0 - x2 * sn;
+    sn = x * sn;
+    const double cr = swap ? sn : c, sr = swap ? c : sn;  // cos and sin of 2 pi r
+    if constexpr (SIN) return q == 0 ? sr : q == 1 ? cr : q == 2 ? -sr : -cr;
+    else return q == 0 ? cr : q == 1 ? -sr : q == 2 ? -cr : sr;
+}
+__device__ __forceinline__ float synth_normal(uint64_t base, uint64_t index) {
+#pragma clang fp contract(off)
+    const uint64_t j = index >> 1;
+    const uint64_t r1 = synth_bits(base, 2 * j), r2 = synth_bits(base, 2 * j + 1);
+    const double u1 = double((r1 >> 11) + 1) * 1.1102230246251565404e-16;  // 2^-53
+    const double u2 = double(r2 >> 11) * 1.1102230246251565404e-16;
+    const double radius = synth_sqrt(-2.0 * synth_ln(u1));
+    return float(radius * ((index & 1) ? synth_turn<true>(u2) : synth_turn<false>(u2)));
 }
 __device__ __forceinline__ float synth_unit24(uint64_t r) {
     return float(r >> 40) * 5.9604644775390625e-08f;

@@ -686,10 +686,14 @@ int orc_gather(const uint8_t *history, int src_fmt, uint32_t width, uint64_t tok
 /* ---------------------------------------------------------------------- */
 /* Seeded synthetic inputs.  Not a reference algorithm: the generator the   */
 /* device side reproduces bit for bit (integer hashing plus correctly       */
-/* rounded single operations only, no transcendental functions).            */
+/* rounded single operations only, no library transcendental functions).    */
 /*   bits(seed, stream, c) = fmix(base(seed, stream) + (c + 1) * G)          */
-/*   normal(i): sum of 12 uniform 24-bit fractions minus 6 (Irwin-Hall:      */
-/*              mean 0, variance 1, exact in double), rounded once to fp32.  */
+/*   normal(2j), normal(2j+1): Box-Muller R cos(2 pi u2), R sin(2 pi u2),  */
+/*              R = sqrt(-2 ln u1), draws 2j, 2j+1 giving u1 in (0, 1] and  */
+/*              u2 in [0, 1) with 53 bits each; double from +, -, *, / only */
+/*              (ln: atanh series after an exact exponent split; sqrt: six  */
+/*              Newton steps; sin, cos: Taylor series after an exact        */
+/*              eighth-turn reduction), rounded once to fp32.               */
 /*   uniform(i): lo + u * (hi - lo) in fp32, three separate roundings.       */
 /* ---------------------------------------------------------------------- */
 #define SYN_G 0x9E3779B97F4A7C15ull
@@ -704,13 +708,77 @@ static uint64_t synth_base(uint64_t seed, uint64_t stream) {
 uint64_t orc_synth_bits(uint64_t seed, uint64_t stream, uint64_t counter) {
     return fmix64(synth_base(seed, stream) + (counter + 1) * SYN_G);
 }
+static double syn_ln(double x) {  /* x in [2^-53, 1] */
+    uint64_t b;
+    memcpy(&b, &x, 8);
+    int e = (int)((b >> 52) & 0x7ffu) - 1023;
+    b = (b & 0x000fffffffffffffull) | 0x3ff0000000000000ull;
+    double m;
+    memcpy(&m, &b, 8);
+    if (m > 1.4142135623730951) { m = m * 0.5; e += 1; }
+    const double s = (m - 1.0) / (m + 1.0), s2 = s * s;
+    static const double inv_odd[] = {1.0 / 21.0, 1.0 / 19.0, 1.0 / 17.0, 1.0 / 15.0, 1.0 / 13.0,
+                                     1.0 / 11.0, 1.0 / 9.0,  1.0 / 7.0,  1.0 / 5.0,  1.0 / 3.0};
+    double p = 1.0 / 23.0;
+    for (int k = 0; k < 10; ++k) p = inv_odd[k] + s2 * p;
+    const double t = s2 * p;
+    return (double)e * 0.69314718055994530942 + 2.0 * (s + s * t);
+}
+static double syn_sqrt(double y) {  /* y >= 0 */
+    if (y == 0.0) return 0.0;
+    uint64_t b;
+    memcpy(&b, &y, 8);
+    const int e = (int)((b >> 52) & 0x7ffu) - 1023;
+    /* e >> 1: arithmetic shift, floor(e / 2) for negative e as on the device */
+    uint64_t rb = (uint64_t)((e >> 1) + 1023) << 52;
+    double r;
+    memcpy(&r, &rb, 8);
+    for (int k = 0; k < 6; ++k) r = (r + y / r) * 0.5;
+    return r;
+}
+static void syn_turn(double t, double *cs) {  /* cos and sin of 2 pi t, t in [0, 1) */
+    const int q = (int)(t * 4.0);
+    double r = t - (double)q * 0.25;
+    const int swap = r > 0.125;
+    if (swap) r = 0.25 - r;
+    const double x = r * 6.28318530717958647692, x2 = x * x;
+    static const double cc[] = {1.0 / 87178291200.0, 1.0 / 479001600.0, 1.0 / 3628800.0, 1.0 / 40320.0,
+                                1.0 / 720.0,         1.0 / 24.0,         0.5,             1.0};
+    static const double sc[] = {1.0 / 6227020800.0, 1.0 / 39916800.0, 1.0 / 362880.0, 1.0 / 5040.0,
+                                1.0 / 120.0,        1.0 / 6.0,        1.0};
+    double c = 1.0 / 20922789888000.0;
+    for (int k = 0; k < 8; ++k) c = cc[k] - x2 * c;
+    double sn = 1.0 / 1307674368000.0;
+    for (int k = 0; k < 7; ++k) sn = sc[k] - x2 * sn;
+    sn = x * sn;
+    const double cr = swap ? sn : c, sr = swap ? c : sn;
+    cs[0] = q == 0 ? cr : q == 1 ? -sr : q == 2 ? -cr : sr;
+    cs[1] = q == 0 ? sr : q == 1 ? cr : q == 2 ? -sr : -cr;
+}
+/* normals 2j and 2j+1 */
+static void normal_pair(uint64_t base, uint64_t j, double *z) {
+    const uint64_t r1 = fmix64(base + (2 * j + 1) * SYN_G), r2 = fmix64(base + (2 * j + 2) * SYN_G);
+    const double u1 = (double)((r1 >> 11) + 1) * 1.1102230246251565404e-16; /* 2^-53 */
+    const double u2 = (double)(r2 >> 11) * 1.1102230246251565404e-16;
+    const double radius = syn_sqrt(-2.0 * syn_ln(u1));
+    double cs[2];
+    syn_turn(u2, cs);
+    z[0] = radius * cs[0];
+    z[1] = radius * cs[1];
+}
 static double normal_from_base(uint64_t base, uint64_t index) {
-    int64_t total = 0;
-    for (uint64_t j = 0; j < 6; ++j) {
-        const uint64_t r = fmix64(base + (index * 6 + j + 1) * SYN_G);
-        total += (int64_t)(r >> 40) + (int64_t)((r >> 16) & 0xffffffu);
+    double z[2];
+    normal_pair(base, index >> 1, z);
+    return z[index & 1];
+}
+/* normals first..first+count-1 into out as binary32, a pair at a time */
+static void normals_f32(uint64_t base, uint64_t first, uint64_t count, float *out) {
+    double z[2];
+    for (uint64_t i = 0; i < count; ++i) {
+        const uint64_t k = first + i;
+        if (i == 0 || (k & 1) == 0) normal_pair(base, k >> 1, z);
+        out[i] = (float)z[k & 1];
     }
-    return (double)(total - 100663296) * 5.9604644775390625e-08; /* (S - 6*2^24) * 2^-24 */
 }
 static float unit24(uint64_t r) { return (float)(r >> 40) * 5.9604644775390625e-08f; }
 static float lerp_rn(float lo, float hi, float u) {
@@ -726,22 +794,30 @@ float orc_synth_uniform(uint64_t seed, uint64_t stream, uint64_t index, float lo
 }
 void orc_synth_normal_f16(uint64_t seed, uint64_t stream, uint64_t count, uint16_t *out) {
     const uint64_t base = synth_base(seed, stream);
-    for (uint64_t i = 0; i < count; ++i) out[i] = orc_f32_to_f16((float)normal_from_base(base, i));
+    float v[256];
+    for (uint64_t i0 = 0; i0 < count; i0 += 256) {
+        const uint64_t n = count - i0 < 256 ? count - i0 : 256;
+        normals_f32(base, i0, n, v);
+        for (uint64_t i = 0; i < n; ++i) out[i0 + i] = orc_f32_to_f16(v[i]);
+    }
 }
 void orc_synth_scaled_normal_f16(uint64_t seed, uint64_t stream, uint64_t rows,
                                  uint32_t width, const float *channel_scale, uint16_t *out) {
     const uint64_t base = synth_base(seed, stream);
-    for (uint64_t t = 0; t < rows; ++t)
-        for (uint32_t c = 0; c < width; ++c) {
-            const uint64_t i = t * width + c;
-            volatile float v = (float)normal_from_base(base, i);
-            volatile float scaled = v * channel_scale[c];
-            out[i] = orc_f32_to_f16(scaled);
+    float v[256];
+    const uint64_t count = rows * width;
+    for (uint64_t i0 = 0; i0 < count; i0 += 256) {
+        const uint64_t n = count - i0 < 256 ? count - i0 : 256;
+        normals_f32(base, i0, n, v);
+        for (uint64_t i = 0; i < n; ++i) {
+            volatile float scaled = v[i] * channel_scale[(i0 + i) % width];
+            out[i0 + i] = orc_f32_to_f16(scaled);
         }
+    }
 }
 void orc_synth_normal_f32(uint64_t seed, uint64_t stream, uint64_t count, float *out) {
     const uint64_t base = synth_base(seed, stream);
-    for (uint64_t i = 0; i < count; ++i) out[i] = (float)normal_from_base(base, i);
+    normals_f32(base, 0, count, out);
 }
 void orc_synth_uniform_f32(uint64_t seed, uint64_t stream, uint64_t count, float lo,
                            float hi, float *out) {
@@ -785,7 +861,7 @@ void orc_synth_normal_q8_0(uint64_t seed, uint64_t stream, uint64_t blocks, uint
     const uint64_t base = synth_base(seed, stream);
     float x[ORC_QK];
     for (uint64_t b = 0; b < blocks; ++b) {
-        for (int j = 0; j < ORC_QK; ++j) x[j] = (float)normal_from_base(base, b * ORC_QK + (uint64_t)j);
+        normals_f32(base, b * ORC_QK, ORC_QK, x);
         orc_quant_q8_0(x, out + b * ORC_Q8_0_BYTES);
     }
 }

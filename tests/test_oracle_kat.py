@@ -282,9 +282,31 @@ def test_gather_layout():
 
 
 def test_synth_moments():
-    """The shared generator: Irwin-Hall(12) - 6 has mean 0, variance 1."""
-    x = O.synth_normal_f32(1, 2, 200_000).astype(np.float64)
-    assert abs(x.mean()) < 0.01 and abs(x.var() - 1) < 0.01 and np.abs(x).max() <= 6
+    """The shared generator's normals: Box-Muller pairs (normals 2j, 2j+1 =
+    R cos, R sin of 2 pi u2 from draws 2j, 2j+1), its ln, sqrt, sin and cos
+    built from +, -, *, / only.  Checked against numpy's log, sqrt, cos and
+    sin on the same 53-bit uniforms (a wrong series term, reduction,
+    quadrant or draw index fails it), then N(0,1) by moments, tails and a
+    Kolmogorov-Smirnov test."""
+    from scipy import stats
+    n = 200_000
+    x = O.synth_normal_f32(1, 2, n).astype(np.float64)
+    pairs = 2000
+    r1 = np.array([O.lib.orc_synth_bits(1, 2, 2 * j) for j in range(pairs)], np.uint64)
+    r2 = np.array([O.lib.orc_synth_bits(1, 2, 2 * j + 1) for j in range(pairs)], np.uint64)
+    u1 = ((r1 >> np.uint64(11)) + np.uint64(1)).astype(np.float64) * 2.0 ** -53
+    u2 = (r2 >> np.uint64(11)).astype(np.float64) * 2.0 ** -53
+    radius = np.sqrt(-2 * np.log(u1))
+    want = np.empty(2 * pairs)
+    want[0::2] = radius * np.cos(2 * np.pi * u2)
+    want[1::2] = radius * np.sin(2 * np.pi * u2)
+    np.testing.assert_allclose(x[:2 * pairs], want, rtol=1e-6, atol=1e-7)
+    # every quarter turn is hit (the sign pattern of cos and sin)
+    quarter = (u2 * 4).astype(int)
+    assert set(quarter.tolist()) == {0, 1, 2, 3}
+    assert abs(x.mean()) < 0.01 and abs(x.var() - 1) < 0.01
+    assert 0.0022 < np.mean(np.abs(x) > 3) < 0.0033  # 2 * (1 - Phi(3)) = 0.0027
+    assert stats.kstest(x, "norm").pvalue > 1e-3
     u = O.synth_uniform_f32(1, 3, 100_000, 0.5, 2.0)
     assert u.min() >= 0.5 and u.max() < 2.0 and abs(u.mean() - 1.25) < 0.01
     q = O.synth_q8_0(1, 4, 1000, 0.01, 0.05).reshape(1000, 34)
