@@ -170,6 +170,22 @@ template <class T> __device__ __forceinline__ T group_sum(T v, int width) {
     return v;
 }
 
+// group_sum(v, width) over `width` groups of G adjacent lanes, every lane
+// of a group holding its group's value: the same pairwise tree, taken at
+// lane strides G, 2G, ...  (DPP mirrors pair the groups as the xor strides
+// do: the lane read belongs to the partner group, whose lanes all agree).
+template <int G, class T> __device__ __forceinline__ T spread_group_sum(T v, int width) {
+    static_assert(G == 1 || G == 2 || G == 4, "groups within a quad");
+    const int end = G * width;
+    int s = G;
+    if (s == 1 && s < end) v += dpp::move<dpp::kQuadXor1>(v), s = 2;
+    if (s == 2 && s < end) v += dpp::move<dpp::kQuadXor2>(v), s = 4;
+    if (s == 4 && s < end) v += dpp::move<dpp::kHalfMirror>(v), s = 8;
+    if (s == 8 && s < end) v += dpp::move<dpp::kMirror>(v), s = 16;
+    for (; s < end; s <<= 1) v += __shfl_xor(v, s, kWave);
+    return v;
+}
+
 // Inclusive prefix sum over the wave: rows by DPP shifts, then the totals
 // of the rows below.
 __device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v) {

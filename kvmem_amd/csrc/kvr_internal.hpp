@@ -61,7 +61,8 @@ struct MfmaLogitsArgs {
 
 struct SelectArgs {
     // softmax units (k_probs): the lane's logits rows, overwritten with the
-    // units' aggregation terms; `units` per lane, counted in counters[lane]
+    // units' aggregation terms (short rows with few units keep the terms in
+    // LDS instead); `units` per lane, counted in counters[lane]
     double *logits;            // [lanes][rows*qheads][pages]
     const uint8_t *mask;       // [pages] or null
     uint32_t units;

@@ -20,6 +20,7 @@ namespace {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // 12-byte loads need only dword alignment on gfx950 (global_load_dwordx3).
 typedef u32x3 u32x3a __attribute__((aligned(4)));
 
@@ -59,6 +60,17 @@ __device__ __forceinline__ void add_f16x8(float *acc, const u32x4 v) {
     }
 }
 
+// The fp16 channels one summary lane owns (8, 4 or 2) as one load: 16, 8
+// or 4 bytes, so a wave reads 1 KiB, 512 B or 256 B of a row.
+template <int CPL> struct F16Lane;
+template <> struct F16Lane<8> { typedef u32x4 type; };
+template <> struct F16Lane<4> { typedef u32x2 type; };
+template <> struct F16Lane<2> { typedef uint32_t type; };
+template <int CPL> __device__ __forceinline__ uint32_t lane_word(const typename F16Lane<CPL>::type &v, int i) {
+    if constexpr (CPL == 2) return v;
+    else return v[i];
+}
+
 __device__ __forceinline__ void add_q8x8(float *acc, uint32_t lo, uint32_t hi, float d) {
     // (float)q * d is exact in binary32 (8 x 11 significant bits), so the
     // fused multiply-add below rounds exactly like "p = q*d; acc += p".
@@ -83,6 +95,8 @@ __device__ __forceinline__ void add_q8x8(float *acc, uint32_t lo, uint32_t hi, f
 // 32 rows of 12-byte loads (q8_0).  Deeper fp16 rings make the register
 // allocator copy ring slots whose loads are still in flight.
 constexpr int kF16Rows = 12, kQ8Rows = 32;
+// Narrower fp16 lanes (one 8- or 4-byte load per row) afford deeper rings.
+template <int CPL> constexpr int kF16RingRows = CPL == 8 ? kF16Rows : CPL == 4 ? 24 : 32;
 template <int D, class Load, class Use>
 __device__ __forceinline__ void stream_rows(uint32_t n, Load load, Use use) {
     decltype(load(0u)) ring[D];
@@ -123,12 +137,16 @@ extern __shared__ __align__(16) uint16_t q_lds_buf[];
 // One BS-thread block of the summary grid (`block` = its index in it):
 // 256 threads, or 64 where a launch has fewer 256-thread blocks than the GPU
 // has CUs (a lone small layer), so its blocks spread over every CU.
-template <int SRC, bool FUSE, int BS = 256>
+// CPL: fp16 channels per lane.  8 by default; a lone small fp16 layer takes
+// 4 or 2, so the same rows are read by two or four times as many waves
+// (every channel is still summed by one lane, in token order).
+template <int SRC, bool FUSE, int BS = 256, int CPL = 8>
 __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t block, uint16_t *q_lds) {
+    static_assert(CPL == 8 || (SRC == kSrcKeysF16 && (CPL == 4 || CPL == 2)), "narrow lanes read fp16 keys");
     // Above the stage-in gather's waves when both share a CU: this kernel
     // is on the select critical path, the gather is bound by the host link.
     __builtin_amdgcn_s_setprio(2);
-    const uint32_t gpp = a.width >> 3;  // 8-channel groups per page
+    const uint32_t gpp = a.width / CPL;  // channel groups per page
     const uint64_t gid = uint64_t(block) * BS + threadIdx.x;
     const uint64_t total = uint64_t(a.lanes) * a.pages * gpp;
     // Threads past the end still take part in the query-staging barrier.
@@ -138,7 +156,7 @@ __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t blo
     const uint64_t rest = gclamp / gpp;
     const uint32_t page = uint32_t(rest % a.pages);
     const uint32_t lane = uint32_t(rest / a.pages);
-    const uint32_t c0 = cg * 8;
+    const uint32_t c0 = cg * CPL;
     uint16_t hb[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     float mean[8];
     uint32_t sbad = kOperandOk;
@@ -173,7 +191,7 @@ __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t blo
 
     if (!active) {
         // nothing to summarize; stays for the barrier below
-    } else if (SRC == kSrcSummary) {
+    } else if constexpr (SRC == kSrcSummary) {
         const u32x4 v = *reinterpret_cast<const u32x4 *>(
             a.src + lane * a.src_lane_stride + (uint64_t(page) * a.width + c0) * 2);
 #pragma unroll
@@ -188,13 +206,44 @@ __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t blo
         float acc[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-        if (SRC == kSrcKeysF16) {
-            const u32x4 *p = reinterpret_cast<const u32x4 *>(
-                a.src + lane * a.src_lane_stride + (t0 * a.width + c0) * 2);
-            const uint64_t stride = gpp;  // 16-byte words per token row
-            stream_rows<kF16Rows>(
-                n, [&](uint32_t t) { return p[t * stride]; },
-                [&](const u32x4 v) { add_f16x8(acc, v); });
+        if constexpr (SRC == kSrcKeysF16) {
+            typedef typename F16Lane<CPL>::type V;
+            auto add_row = [&](const V v) {
+#pragma unroll
+                for (int i = 0; i < CPL / 2; ++i) {
+                    const uint32_t w = lane_word<CPL>(v, i);
+                    acc[2 * i] += h2f(uint16_t(w & 0xffffu));
+                    acc[2 * i + 1] += h2f(uint16_t(w >> 16));
+                }
+            };
+            const uint32_t row_bytes = a.width * 2;
+            if (a.width % (kWave * CPL) == 0 && uint64_t(a.page_tokens) * row_bytes < (1ull << 32)) {
+                // Every wave's lanes read one page (whole waves are active
+                // or not): the page is one buffer resource, and a row's
+                // offset is a scalar added to the lane's column, so a load
+                // costs no vector address arithmetic.
+                const uint32_t nu = __builtin_amdgcn_readfirstlane(n);
+                const uint8_t *first = a.src + uint64_t(__builtin_amdgcn_readfirstlane(lane)) * a.src_lane_stride +
+                                       uint64_t(__builtin_amdgcn_readfirstlane(page)) * a.page_tokens * row_bytes;
+                const auto rs = buffer_rsrc(first, nu * row_bytes);
+                const int col = int(c0 * 2);
+                stream_rows<kF16RingRows<CPL>>(
+                    nu,
+                    [&](uint32_t t) {
+                        const int soff = int(t * row_bytes);
+                        if constexpr (CPL == 8)
+                            return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(rs, col, soff, 0));
+                        else if constexpr (CPL == 4)
+                            return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b64(rs, col, soff, 0));
+                        else
+                            return V(__builtin_amdgcn_raw_buffer_load_b32(rs, col, soff, 0));
+                    },
+                    add_row);
+            } else {
+                const V *p = reinterpret_cast<const V *>(a.src + lane * a.src_lane_stride + (t0 * a.width + c0) * 2);
+                const uint64_t stride = gpp;  // lane loads per token row
+                stream_rows<kF16RingRows<CPL>>(n, [&](uint32_t t) { return p[t * stride]; }, add_row);
+            }
         } else {
             // q8_0 rows: lane owns 8 codes (quarter s) of block b, and the
             // block's four lanes (one quad) read the dword-aligned 36 bytes
@@ -221,7 +270,7 @@ __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t blo
         }
         const float inv = 1.0f / float(n);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < CPL; ++i) {
             mean[i] = acc[i] * inv;
             const uint32_t e = recall16(mean[i], hb[i]);
             sbad = sbad ? sbad : e;
@@ -282,16 +331,50 @@ __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t blo
 
     if (FUSE && a.q_stage) lds_barrier();
     if (FUSE && active) {
+        // Dot products over 8-channel groups, each summed in channel order,
+        // then over the kv-head slice's groups by one pairwise tree whatever
+        // CPL is: the logits are bit-identical to those of 8-channel lanes
+        // and of the stack's softmax-side logits.  With narrower lanes the
+        // G = 8/CPL lanes of a group each gather its 8 means by quad DPP
+        // broadcasts and compute its sums.
+        constexpr int G = 8 / CPL;
         const QueryArgs &q = a.q;
-        const uint32_t kvh = c0 / q.dim, d0 = c0 % q.dim;
+        const uint32_t c8 = c0 & ~7u;  // the group's first channel
+        const uint32_t kvh = c8 / q.dim, d0 = c8 % q.dim;
         const uint32_t group = q.qheads / q.kvheads;
-        const int lph = int(q.dim >> 3);  // lanes per kv-head slice
+        const int lph = int(q.dim >> 3);  // 8-channel groups per kv-head slice
+        uint32_t w8[4];
+        {
+            uint32_t mine[CPL / 2];
+#pragma unroll
+            for (int i = 0; i < CPL / 2; ++i) mine[i] = uint32_t(hb[2 * i]) | (uint32_t(hb[2 * i + 1]) << 16);
+            if constexpr (G == 1) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) w8[i] = mine[i];
+            } else if constexpr (G == 2) {
+                // quad_perm [g, g, 2+g, 2+g]: every lane reads lane g of its pair
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    w8[i] = dpp::move<0xA0>(mine[i]);
+                    w8[2 + i] = dpp::move<0xF5>(mine[i]);
+                }
+            } else {
+                // quad_perm [g, g, g, g]
+                w8[0] = dpp::move<0x00>(mine[0]);
+                w8[1] = dpp::move<0x55>(mine[0]);
+                w8[2] = dpp::move<0xAA>(mine[0]);
+                w8[3] = dpp::move<0xFF>(mine[0]);
+            }
+        }
         double m[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) m[i] = double(h2f(hb[i]));
+        for (int i = 0; i < 4; ++i) {
+            m[2 * i] = double(h2f(uint16_t(w8[i] & 0xffffu)));
+            m[2 * i + 1] = double(h2f(uint16_t(w8[i] >> 16)));
+        }
         uint32_t bad = kOperandOk;
         const bool from_lds = lane == staged_lane;
-        const bool writer = (cg & uint32_t(lph - 1)) == 0;
+        const bool writer = (cg & uint32_t(G * lph - 1)) == 0;
         // Four heads of the kv-head's group at a time (the last pass repeats
         // the group's last head and does not store it), so their loads and
         // cross-lane sums overlap.
@@ -323,7 +406,7 @@ __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t blo
                     }
                 }
 #pragma unroll
-                for (uint32_t u = 0; u < 4; ++u) part[u] = group_sum(part[u], lph);
+                for (uint32_t u = 0; u < 4; ++u) part[u] = spread_group_sum<G>(part[u], lph);
 #pragma unroll
                 for (uint32_t u = 0; u < 4; ++u)
                     if (writer && h0 + u < group)
@@ -339,23 +422,32 @@ __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t blo
     if (active && SRC != kSrcSummary) {
         const uint64_t out = (uint64_t(lane) * a.pages + page) * a.width + c0;
         if (a.means) {
-            float4 *m4 = reinterpret_cast<float4 *>(a.means + out);
-            m4[0] = make_float4(mean[0], mean[1], mean[2], mean[3]);
-            m4[1] = make_float4(mean[4], mean[5], mean[6], mean[7]);
+            if constexpr (CPL == 2) {
+                *reinterpret_cast<float2 *>(a.means + out) = make_float2(mean[0], mean[1]);
+            } else {
+                float4 *m4 = reinterpret_cast<float4 *>(a.means + out);
+                m4[0] = make_float4(mean[0], mean[1], mean[2], mean[3]);
+                if constexpr (CPL == 8) m4[1] = make_float4(mean[4], mean[5], mean[6], mean[7]);
+            }
         }
         if (sbad) raise_operand(a.status, sbad, a.epoch);
         if (a.summaries) {
-            u32x4 v;
+            typedef typename F16Lane<CPL>::type V;
+            V v;
+            if constexpr (CPL == 2) {
+                v = uint32_t(hb[0]) | (uint32_t(hb[1]) << 16);
+            } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) v[i] = uint32_t(hb[2 * i]) | (uint32_t(hb[2 * i + 1]) << 16);
-            *reinterpret_cast<u32x4 *>(a.summaries + out) = v;
+                for (int i = 0; i < CPL / 2; ++i) v[i] = uint32_t(hb[2 * i]) | (uint32_t(hb[2 * i + 1]) << 16);
+            }
+            *reinterpret_cast<V *>(a.summaries + out) = v;
         }
     }
 }
 
-template <int SRC, bool FUSE, int BS>
+template <int SRC, bool FUSE, int BS, int CPL = 8>
 __global__ __launch_bounds__(BS) void k_summary(SummaryArgs a) {
-    summary_block<SRC, FUSE, BS>(a, blockIdx.x, q_lds_buf);
+    summary_block<SRC, FUSE, BS, CPL>(a, blockIdx.x, q_lds_buf);
 }
 
 // ---------------------------------------------------------------------------
@@ -650,9 +742,10 @@ __host__ __device__ constexpr bool probs_lds_fits(uint32_t aggregation, uint32_t
 extern __shared__ __align__(16) double probs_lds[];
 
 // One unit by one wave, rows of up to 64*NPL pages held in registers.
+// lout: the unit's terms go to this LDS row instead of over its logits.
 template <int NPL>
 __device__ __forceinline__ void unit_terms_regs(const SelectArgs &a, double *lane_base, uint32_t unit,
-                                                const double *lrows) {
+                                                const double *lrows, double *lout = nullptr) {
     // Loads are unconditional with indices clamped into the row (values past
     // the row are read, then dropped): a load behind a per-lane branch would
     // wait for itself before the next one issues.
@@ -675,6 +768,19 @@ __device__ __forceinline__ void unit_terms_regs(const SelectArgs &a, double *lan
     // (`lrows`: the unit's first row) or at device scope
     auto logit = [&](const double *row, uint32_t j) { return a.summaries ? load_device(row + j) : row[j]; };
     auto lds_row = [&](uint32_t hh) { return lrows + uint64_t(hh) * n; };
+    // The group rules take the group's heads HP at a time (short rows), the
+    // chunk's loads in flight together and its heads' reductions in one
+    // straight run.  Past the group's end a chunk repeats its last head,
+    // which changes neither a max nor a max of softmaxes.
+    constexpr uint32_t HP = NPL <= 4 ? 4 : 1;
+    auto load_heads = [&](const double *first, uint32_t h0, uint32_t group, double (&x)[HP][NPL]) {
+#pragma unroll
+        for (uint32_t k = 0; k < HP; ++k) {
+            const uint32_t hh = min(h0 + k, group - 1);
+#pragma unroll
+            for (int i = 0; i < NPL; ++i) x[k][i] = lrows ? lds_row(hh)[at(i)] : logit(first + uint64_t(hh) * n, at(i));
+        }
+    };
     if (a.aggregation == kAggMean) {
         out = lane_base + uint64_t(unit) * n;
 #pragma unroll
@@ -693,16 +799,19 @@ __device__ __forceinline__ void unit_terms_regs(const SelectArgs &a, double *lan
             double gm[NPL];
 #pragma unroll
             for (int i = 0; i < NPL; ++i) gm[i] = 0.0;
-            for (uint32_t hh = 0; hh < group; ++hh) {
-                const double *row = out + uint64_t(hh) * n;
+            for (uint32_t h0 = 0; h0 < group; h0 += HP) {
+                double x[HP][NPL];
+                load_heads(out, h0, group, x);
 #pragma unroll
-                for (int i = 0; i < NPL; ++i) {
-                    const double x = lrows ? lds_row(hh)[at(i)] : logit(row, at(i));
-                    t[i] = on[i] ? x : 0.0;
+                for (uint32_t k = 0; k < HP; ++k) {
+#pragma unroll
+                    for (int i = 0; i < NPL; ++i) x[k][i] = on[i] ? x[k][i] : 0.0;
+                    wave_softmax_regs(x[k], on);
                 }
-                wave_softmax_regs(t, on);
 #pragma unroll
-                for (int i = 0; i < NPL; ++i) gm[i] = t[i] > gm[i] ? t[i] : gm[i];
+                for (uint32_t k = 0; k < HP; ++k)
+#pragma unroll
+                    for (int i = 0; i < NPL; ++i) gm[i] = x[k][i] > gm[i] ? x[k][i] : gm[i];
             }
             double mass = 0.0;
 #pragma unroll
@@ -713,13 +822,13 @@ __device__ __forceinline__ void unit_terms_regs(const SelectArgs &a, double *lan
         } else {
 #pragma unroll
             for (int i = 0; i < NPL; ++i) t[i] = -INFINITY;
-            for (uint32_t hh = 0; hh < group; ++hh) {
-                const double *row = out + uint64_t(hh) * n;
+            for (uint32_t h0 = 0; h0 < group; h0 += HP) {
+                double x[HP][NPL];
+                load_heads(out, h0, group, x);
 #pragma unroll
-                for (int i = 0; i < NPL; ++i) {
-                    const double x = lrows ? lds_row(hh)[at(i)] : logit(row, at(i));
-                    t[i] = fmax(t[i], on[i] ? x : -INFINITY);
-                }
+                for (uint32_t k = 0; k < HP; ++k)
+#pragma unroll
+                    for (int i = 0; i < NPL; ++i) t[i] = fmax(t[i], on[i] ? x[k][i] : -INFINITY);
             }
             wave_softmax_regs(t, on);
 #pragma unroll
@@ -730,7 +839,10 @@ __device__ __forceinline__ void unit_terms_regs(const SelectArgs &a, double *lan
 #pragma unroll
     for (int i = 0; i < NPL; ++i) {
         const uint32_t j = l + i * kWave;
-        if (j < n) store_device(out + j, t[i]);
+        if (j < n) {
+            if (lout) lout[j] = t[i];
+            else store_device(out + j, t[i]);
+        }
     }
 }
 
@@ -1535,12 +1647,15 @@ __global__ __launch_bounds__(1024) void k_graph_lrfu(GraphLrfuArgs a) {
     }
 }
 
-// Aggregation (optional) by the whole workgroup, then selection by its
-// first wave.  Keys go to LDS when the lane's pages fit.
-__device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
+// Aggregation (optional) by the whole workgroup (up to 1024 threads), then
+// selection by its first wave (up to 1024 pages) or by 256 threads.  Keys go
+// to LDS when the lane's pages fit.  LT: the terms are in LDS (`lterms`,
+// unit i's row at i*cols), not over the logits in memory.
+template <bool LT = false>
+__device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane, const double *lterms = nullptr) {
     __shared__ uint32_t hist[256];
     __shared__ uint32_t fixed_small[kTailLdsPages / 32];  // the fixed-page bitmap of short rows
-    __shared__ uint32_t s_fixed[4];
+    __shared__ uint32_t s_fixed[16];
     const uint32_t tid = threadIdx.x, B = blockDim.x;
     const uint32_t cols = a.pages;         // softmax columns (half pages when folding)
     const uint32_t n = select_pages(a);    // pages scored and selected
@@ -1573,6 +1688,12 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
         auto row_of = [&](uint32_t i) -> uint64_t {
             return mean ? i : uint64_t(i / a.kvheads) * a.qheads + (i % a.kvheads) * group;
         };
+        // contributing row i's offset, and a term at an offset
+        auto row_off = [&](uint32_t i) -> uint64_t { return (LT ? uint64_t(i) : row_of(i)) * cols; };
+        auto term = [&](uint64_t o) -> double {
+            if constexpr (LT) return lterms[o];
+            else return load_device(terms + o);
+        };
         // acc0 += column c0's terms, acc1 += column c1's (c1 is loaded even
         // when the caller drops acc1: the loads stay unconditional)
         auto sum_rows = [&](uint32_t c0, uint32_t c1, double &acc0, double &acc1) {
@@ -1581,9 +1702,9 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
                 double v0[32], v1[32];
 #pragma unroll
                 for (int u = 0; u < 32; ++u) {
-                    const uint64_t o = row_of(i + u) * cols;
-                    v0[u] = load_device(terms + o + c0);
-                    v1[u] = load_device(terms + o + c1);
+                    const uint64_t o = row_off(i + u);
+                    v0[u] = term(o + c0);
+                    v1[u] = term(o + c1);
                 }
 #pragma unroll
                 for (int u = 0; u < 32; ++u) {
@@ -1595,9 +1716,9 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
                 double v0[16], v1[16];
 #pragma unroll
                 for (int u = 0; u < 16; ++u) {
-                    const uint64_t o = row_of(i + u) * cols;
-                    v0[u] = load_device(terms + o + c0);
-                    v1[u] = load_device(terms + o + c1);
+                    const uint64_t o = row_off(i + u);
+                    v0[u] = term(o + c0);
+                    v1[u] = term(o + c1);
                 }
 #pragma unroll
                 for (int u = 0; u < 16; ++u) {
@@ -1609,9 +1730,9 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
                 double v0[8], v1[8];
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
-                    const uint64_t o = row_of(i + u) * cols;
-                    v0[u] = load_device(terms + o + c0);
-                    v1[u] = load_device(terms + o + c1);
+                    const uint64_t o = row_off(i + u);
+                    v0[u] = term(o + c0);
+                    v1[u] = term(o + c1);
                 }
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
@@ -1620,9 +1741,9 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
                 }
             }
             for (; i < nrows; ++i) {
-                const uint64_t o = row_of(i) * cols;
-                acc0 += load_device(terms + o + c0);
-                acc1 += load_device(terms + o + c1);
+                const uint64_t o = row_off(i);
+                acc0 += term(o + c0);
+                acc1 += term(o + c1);
             }
         };
         if (a.fold) {
@@ -1653,7 +1774,7 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane) {
                 for (int q = 0; q < 4; ++q)
 #pragma unroll
                     for (uint32_t u = 0; u < 16; ++u)
-                        v[q][u] = load_device(terms + row_of(min(u, nrows - 1)) * cols + jj[q]);
+                        v[q][u] = term(row_off(min(u, nrows - 1)) + jj[q]);
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
 #pragma unroll
@@ -1778,6 +1899,22 @@ __device__ __forceinline__ void probs_block(const SelectArgs &a, uint32_t unit_b
 template <int NPL>
 __global__ __launch_bounds__(256) void k_probs(SelectArgs a) {
     probs_block<NPL, false>(a, blockIdx.x, blockIdx.y, gridDim.x);
+}
+
+// Rows of up to kOnePages softmax columns with at most kOneUnits units: one
+// workgroup per lane, a wave per unit, and the terms kept in LDS after the
+// tail's keys, so no device-scope hand-off between workgroups (and no
+// second round trip through memory) sits between the softmax and the tail.
+constexpr uint32_t kOnePages = 512, kOneUnits = 8;
+template <int NPL>
+__global__ __launch_bounds__(kOneUnits * kWave) void k_probs_one(SelectArgs a) {
+    const uint32_t lane = blockIdx.x, unit = threadIdx.x >> 6;
+    double *lterms = reinterpret_cast<double *>(tail_keys + key_slot(select_pages(a)) + 1);
+    if (unit < a.units)
+        unit_terms_regs<NPL>(a, a.logits + uint64_t(lane) * a.rows * a.qheads * a.pages, unit, nullptr,
+                             lterms + uint64_t(unit) * a.pages);
+    lds_barrier();
+    lane_tail<true>(a, lane, lterms);
 }
 
 // The summary workgroups of a key-history stack group: every layer of the
@@ -2738,15 +2875,35 @@ void launch_summary_bs(int source, bool fuse, const SummaryArgs &a, uint64_t thr
         hipLaunchKernelGGL((k_summary<kSrcSummary, true, BS>), grid, block, lds, s, a);
 }
 
+template <int CPL>
+void launch_summary_narrow(bool fuse, const SummaryArgs &a, size_t lds, hipStream_t s) {
+    const dim3 grid(blocks_for(uint64_t(a.lanes) * a.pages * (a.width / CPL), 64)), block(64);
+    if (fuse) hipLaunchKernelGGL((k_summary<kSrcKeysF16, true, 64, CPL>), grid, block, lds, s, a);
+    else hipLaunchKernelGGL((k_summary<kSrcKeysF16, false, 64, CPL>), grid, block, 0, s, a);
+}
+
 constexpr uint64_t kSummarySpreadBlocks = 256;  // MI355X's CUs
 hipError_t launch_summary(int source, bool fuse, const SummaryArgs &a, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch\'s error
     const uint64_t threads = uint64_t(a.lanes) * a.pages * (a.width >> 3);
     const size_t lds = fuse && a.q_stage ? size_t(a.q.rows) * a.q.qheads * a.q.dim * 2 : 0;  // q_lds_buf
-    // a launch of fewer 256-thread blocks than CUs leaves CUs idle: 64-thread
-    // blocks spread the same key stream over four times as many CUs
-    if (blocks_for(threads) < kSummarySpreadBlocks) launch_summary_bs<64>(source, fuse, a, threads, lds, s);
-    else launch_summary_bs<256>(source, fuse, a, threads, lds, s);
+    // A launch of fewer 256-thread blocks than CUs leaves CUs idle: 64-thread
+    // blocks spread the same key stream over four times as many CUs, and
+    // fp16 rows are split over lanes of 4 or 2 channels until about four
+    // waves per CU read them (a fused kv-head slice stays within a wave).
+    if (blocks_for(threads) < kSummarySpreadBlocks) {
+        const uint64_t waves = (threads + 63) / 64;
+        const bool fits2 = a.width % 2 == 0 && (!fuse || a.q.dim / 2 <= 64);
+        const bool fits4 = a.width % 4 == 0 && (!fuse || a.q.dim / 4 <= 64);
+        if (source == kSrcKeysF16 && fits2 && 4 * waves <= 4 * kSummarySpreadBlocks)
+            launch_summary_narrow<2>(fuse, a, lds, s);
+        else if (source == kSrcKeysF16 && fits4 && 2 * waves <= 4 * kSummarySpreadBlocks)
+            launch_summary_narrow<4>(fuse, a, lds, s);
+        else
+            launch_summary_bs<64>(source, fuse, a, threads, lds, s);
+    } else {
+        launch_summary_bs<256>(source, fuse, a, threads, lds, s);
+    }
     return hipGetLastError();
 }
 
@@ -2774,6 +2931,16 @@ inline size_t tail_lds_bytes(const SelectArgs &a) {
 
 hipError_t launch_probs(const SelectArgs &a, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch\'s error
+    if (a.pages <= kOnePages && a.units >= 1 && a.units <= kOneUnits && uint64_t(a.units) * a.pages <= 4096) {
+        // few short softmax units: one workgroup per lane, terms in LDS
+        const dim3 grid(a.lanes), block(kWave * a.units);
+        const size_t lds = tail_lds_bytes(a) + size_t(a.units) * a.pages * 8;
+        if (a.pages <= 64) hipLaunchKernelGGL(k_probs_one<1>, grid, block, lds, s, a);
+        else if (a.pages <= 128) hipLaunchKernelGGL(k_probs_one<2>, grid, block, lds, s, a);
+        else if (a.pages <= 256) hipLaunchKernelGGL(k_probs_one<4>, grid, block, lds, s, a);
+        else hipLaunchKernelGGL(k_probs_one<8>, grid, block, lds, s, a);
+        return hipGetLastError();
+    }
     const uint32_t upb = units_per_block(a.pages);
     const dim3 grid((a.units + upb - 1) / upb, a.lanes), block(256);
     const size_t lds = tail_lds_bytes(a);
