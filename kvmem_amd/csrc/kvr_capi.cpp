@@ -237,8 +237,12 @@ kvr_status ensure_counters(kvr_context *ctx, uint32_t lanes, hipStream_t s) {
     return KVR_OK;
 }
 
-size_t logits_bytes(uint32_t lanes, uint32_t pages, uint32_t rows, uint32_t qheads) {
+// the logits, then two statistics per softmax row (long Mean rows)
+size_t logits_only_bytes(uint32_t lanes, uint32_t pages, uint32_t rows, uint32_t qheads) {
     return align256(size_t(lanes) * rows * qheads * pages * sizeof(double));
+}
+size_t logits_bytes(uint32_t lanes, uint32_t pages, uint32_t rows, uint32_t qheads) {
+    return logits_only_bytes(lanes, pages, rows, qheads) + align256(size_t(lanes) * rows * qheads * 2 * sizeof(double));
 }
 size_t qpack_bytes(uint32_t lanes, uint32_t rows, uint32_t qheads, uint32_t dim) {
     return align256(size_t(lanes) * rows * qheads * dim * sizeof(uint16_t));
@@ -459,6 +463,8 @@ kvr::SelectArgs make_select_args(kvr_context *ctx, const ScorePlan &p, const uin
                                  kvr_tie_rule tie, const Mandatory &mand, uint32_t *selected, uint32_t *count) {
     kvr::SelectArgs sa{};
     sa.logits = p.logits;
+    sa.stats = reinterpret_cast<double *>(reinterpret_cast<uint8_t *>(p.logits) +
+                                          logits_only_bytes(p.lanes, p.pages, p.rows, p.qheads));
     sa.mask = mask;
     sa.units = p.rows * (agg == KVR_AGG_MEAN ? p.qheads : p.kvheads);
     sa.counters = p.counters ? p.counters : ctx->counters;

@@ -64,6 +64,7 @@ struct SelectArgs {
     // units' aggregation terms (short rows with few units keep the terms in
     // LDS instead); `units` per lane, counted in counters[lane]
     double *logits;            // [lanes][rows*qheads][pages]
+    double *stats;             // [lanes][units][2]: long Mean rows' (max, sum), or null
     const uint8_t *mask;       // [pages] or null
     uint32_t units;
     uint32_t *counters;        // [lanes], zero between launches

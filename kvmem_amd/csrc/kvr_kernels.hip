@@ -872,49 +872,63 @@ __device__ __forceinline__ double block_sum(double v) {
 // tile's loads in flight together; per-head statistics first, then one pass
 // per page.  Thread t touches only pages j == t (mod 256).  Values this
 // thread stored are re-read at device scope.
+// f(j, value, on) over thread l's pages j < n of a long `row` (256 threads,
+// tiles of 16 values per thread, the tile's loads in flight together).
+// own: values this thread stored itself, re-read at device scope.
+template <class F>
+__device__ __forceinline__ void long_row_tiles(const SelectArgs &a, const double *row, bool own, F f) {
+    constexpr int T = 16;
+    constexpr uint32_t S = 256;  // threads per unit
+    const uint32_t n = a.pages, l = threadIdx.x;
+    for (uint32_t base = 0; base < n; base += S * T) {
+        double x[T];
+        bool on[T];
+        if (a.mask) {
+            uint8_t mk[T];
+#pragma unroll
+            for (int i = 0; i < T; ++i) {
+                const uint32_t j = min(base + l + i * S, n - 1);
+                x[i] = own || a.summaries ? load_device(row + j) : row[j];
+                mk[i] = a.mask[j >> a.mask_shift];
+            }
+#pragma unroll
+            for (int i = 0; i < T; ++i) on[i] = mk[i] != 0;
+        } else {
+#pragma unroll
+            for (int i = 0; i < T; ++i) {
+                const uint32_t j = min(base + l + i * S, n - 1);
+                x[i] = own || a.summaries ? load_device(row + j) : row[j];
+                on[i] = true;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < T; ++i) {
+            const uint32_t j = base + l + i * S;
+            if (j < n) f(j, x[i], on[i]);
+        }
+    }
+}
+// A long row's softmax statistics: its max m and sum s of exp(x - m) over
+// unmasked pages (per-thread partials in tile order, then block_max/sum).
+__device__ __forceinline__ void long_row_stats(const SelectArgs &a, const double *row, bool own, double &m,
+                                               double &s) {
+    double mm = -INFINITY;
+    long_row_tiles(a, row, own, [&](uint32_t, double x, bool on) { mm = on ? fmax(mm, x) : mm; });
+    m = block_max(mm);
+    double ss = 0.0;
+    long_row_tiles(a, row, own, [&](uint32_t, double x, bool on) { ss += on ? exp(x - m) : 0.0; });
+    s = block_sum(ss);
+}
+// A page's probability from its row's statistics.
+__device__ __forceinline__ double row_prob(double x, double m, double s) { return s > 0.0 ? exp(x - m) / s : 0.0; }
+
 __device__ __forceinline__ void unit_terms_loop(const SelectArgs &a, double *lane_base, uint32_t unit) {
     constexpr int T = 16;
     constexpr uint32_t S = 256;  // threads per unit
     const uint32_t n = a.pages, l = threadIdx.x;
-    // f(j, value, on) for this lane's pages j < n of `row`
-    auto tiles = [&](const double *row, bool own, auto f) {
-        for (uint32_t base = 0; base < n; base += S * T) {
-            double x[T];
-            bool on[T];
-            if (a.mask) {
-                uint8_t mk[T];
-#pragma unroll
-                for (int i = 0; i < T; ++i) {
-                    const uint32_t j = min(base + l + i * S, n - 1);
-                    x[i] = own || a.summaries ? load_device(row + j) : row[j];
-                    mk[i] = a.mask[j >> a.mask_shift];
-                }
-#pragma unroll
-                for (int i = 0; i < T; ++i) on[i] = mk[i] != 0;
-            } else {
-#pragma unroll
-                for (int i = 0; i < T; ++i) {
-                    const uint32_t j = min(base + l + i * S, n - 1);
-                    x[i] = own || a.summaries ? load_device(row + j) : row[j];
-                    on[i] = true;
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < T; ++i) {
-                const uint32_t j = base + l + i * S;
-                if (j < n) f(j, x[i], on[i]);
-            }
-        }
-    };
-    auto stats = [&](const double *row, bool own, double &m, double &s) {
-        double mm = -INFINITY;
-        tiles(row, own, [&](uint32_t, double x, bool on) { mm = on ? fmax(mm, x) : mm; });
-        m = block_max(mm);
-        double ss = 0.0;
-        tiles(row, own, [&](uint32_t, double x, bool on) { ss += on ? exp(x - m) : 0.0; });
-        s = block_sum(ss);
-    };
-    auto prob = [&](double x, double m, double s) { return s > 0.0 ? exp(x - m) / s : 0.0; };
+    auto tiles = [&](const double *row, bool own, auto f) { long_row_tiles(a, row, own, f); };
+    auto stats = [&](const double *row, bool own, double &m, double &s) { long_row_stats(a, row, own, m, s); };
+    auto prob = [&](double x, double m, double s) { return row_prob(x, m, s); };
     if (a.aggregation == kAggMean) {
         double *row = lane_base + uint64_t(unit) * n;
         double m, s;
@@ -1650,8 +1664,10 @@ __global__ __launch_bounds__(1024) void k_graph_lrfu(GraphLrfuArgs a) {
 // Aggregation (optional) by the whole workgroup (up to 1024 threads), then
 // selection by its first wave (up to 1024 pages) or by 256 threads.  Keys go
 // to LDS when the lane's pages fit.  LT: the terms are in LDS (`lterms`,
-// unit i's row at i*cols), not over the logits in memory.
-template <bool LT = false>
+// unit i's row at i*cols), not over the logits in memory.  SCORES: this
+// launch's workgroups wrote the scores (aggregated already); they are read
+// at device scope.
+template <bool LT = false, bool SCORES = false>
 __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane, const double *lterms = nullptr) {
     __shared__ uint32_t hist[256];
     __shared__ uint32_t fixed_small[kTailLdsPages / 32];  // the fixed-page bitmap of short rows
@@ -1677,7 +1693,7 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane, co
         bad |= !__builtin_isfinite(v) || (!a.signed_scores && v < 0.0);
         if (lds) tail_keys[key_slot(j)] = order_key(v);
     };
-    if (a.do_aggregate) {
+    if (!SCORES && a.do_aggregate) {
         // Contributing rows in the reference's order: (row, head) for Mean,
         // (row, kv-head group) for the group rules.  Two columns per pass and
         // up to 32 rows of loads in flight; the additions stay in order.
@@ -1803,7 +1819,18 @@ __device__ __forceinline__ void lane_tail(const SelectArgs &a, uint32_t lane, co
             }
         }
     } else {
-        for (uint32_t j = tid; j < n; j += B) note(j, sc[j]);
+        // 16 loads in flight per pass
+        for (uint32_t j0 = tid; j0 < n; j0 += 16 * B) {
+            double v[16];
+#pragma unroll
+            for (uint32_t u = 0; u < 16; ++u) {
+                const uint32_t j = min(j0 + u * B, n - 1);
+                v[u] = SCORES ? load_device(sc + j) : sc[j];
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < 16; ++u)
+                if (j0 + u * B < n) note(j0 + u * B, v[u]);
+        }
     }
     if (!a.do_select) return;
     if (has_fixed) {
@@ -1915,6 +1942,75 @@ __global__ __launch_bounds__(kOneUnits * kWave) void k_probs_one(SelectArgs a) {
                              lterms + uint64_t(unit) * a.pages);
     lds_barrier();
     lane_tail<true>(a, lane, lterms);
+}
+
+// Long Mean rows (more than 1024 pages, no half-page fold) in two launches
+// instead of k_probs' units-then-tail: the units' statistics, then page
+// slices that sum their terms over the rows and a tail that selects.  The
+// terms are never stored: each is recomputed from its row's statistics by
+// the expression k_probs stores, and a page's terms are added in row order
+// from the stored score or zero, as k_probs' tail adds them, so the scores
+// are bit-identical to k_probs' (and to the layer stack's).
+// k_unit_stats: grid (units, lanes), 256 threads.
+__global__ __launch_bounds__(256) void k_unit_stats(SelectArgs a) {
+    const uint32_t lane = blockIdx.y, unit = blockIdx.x;
+    const double *row = a.logits + (uint64_t(lane) * a.rows * a.qheads + unit) * a.pages;
+    double m, s;
+    long_row_stats(a, row, false, m, s);
+    if (threadIdx.x == 0) {
+        a.stats[(uint64_t(lane) * a.units + unit) * 2] = m;
+        a.stats[(uint64_t(lane) * a.units + unit) * 2 + 1] = s;
+    }
+}
+
+// k_mean_scores: grid (ceil(pages / kScorePages), lanes), 256 threads, a
+// thread per page per 256; the lane's last workgroup selects (dynamic LDS:
+// the tail's keys).
+constexpr uint32_t kScorePP = 1, kScorePages = 256 * kScorePP, kScoreRows = 16;
+__global__ __launch_bounds__(256) void k_mean_scores(SelectArgs a) {
+    __shared__ uint32_t s_last;
+    const uint32_t lane = blockIdx.y, n = a.pages;
+    const double *logits = a.logits + uint64_t(lane) * a.rows * a.qheads * n;
+    const double *st = a.stats + uint64_t(lane) * a.units * 2;
+    double *sc = a.scores + uint64_t(lane) * n;
+    const uint32_t j0 = blockIdx.x * kScorePages + threadIdx.x;
+    uint32_t jc[kScorePP];
+    bool on[kScorePP];
+    double acc[kScorePP];
+#pragma unroll
+    for (uint32_t i = 0; i < kScorePP; ++i) {
+        jc[i] = min(j0 + i * 256, n - 1);
+        on[i] = !a.mask || a.mask[jc[i] >> a.mask_shift];
+        acc[i] = a.accumulate ? sc[jc[i]] : 0.0;
+    }
+    for (uint32_t u0 = 0; u0 < a.units; u0 += kScoreRows) {
+        double x[kScoreRows][kScorePP];
+#pragma unroll
+        for (uint32_t k = 0; k < kScoreRows; ++k)
+#pragma unroll
+            for (uint32_t i = 0; i < kScorePP; ++i) x[k][i] = logits[uint64_t(min(u0 + k, a.units - 1)) * n + jc[i]];
+#pragma unroll
+        for (uint32_t k = 0; k < kScoreRows; ++k) {
+            if (u0 + k >= a.units) break;
+            const double m = st[2 * (u0 + k)], s = st[2 * (u0 + k) + 1];
+#pragma unroll
+            for (uint32_t i = 0; i < kScorePP; ++i) acc[i] += (on[i] ? row_prob(x[k][i], m, s) : 0.0) / a.weight;
+        }
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < kScorePP; ++i)
+        if (j0 + i * 256 < n) store_device(sc + j0 + i * 256, acc[i]);
+    // Publish (stores complete at device scope), count; the last selects.
+    wait_vmem();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t done = atomicAdd(a.counters + lane, 1u);
+        s_last = done == gridDim.x - 1;
+        if (s_last) atomicExch(a.counters + lane, 0u);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    lane_tail<false, true>(a, lane);
 }
 
 // The summary workgroups of a key-history stack group: every layer of the
@@ -2931,6 +3027,13 @@ inline size_t tail_lds_bytes(const SelectArgs &a) {
 
 hipError_t launch_probs(const SelectArgs &a, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch\'s error
+    if (a.pages > 1024 && a.aggregation == kAggMean && !a.fold && a.stats) {
+        // long Mean rows: the units' statistics, then page slices + tail
+        hipLaunchKernelGGL(k_unit_stats, dim3(a.units, a.lanes), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(k_mean_scores, dim3((a.pages + kScorePages - 1) / kScorePages, a.lanes), dim3(256),
+                           tail_lds_bytes(a), s, a);
+        return hipGetLastError();
+    }
     if (a.pages <= kOnePages && a.units >= 1 && a.units <= kOneUnits && uint64_t(a.units) * a.pages <= 4096) {
         // few short softmax units: one workgroup per lane, terms in LDS
         const dim3 grid(a.lanes), block(kWave * a.units);

@@ -37,9 +37,10 @@ def test_status_strings_and_workspace_arithmetic():
     lib = _capi.lib()
     assert lib.kvr_status_string(_capi.OK) == b"ok"
     assert lib.kvr_status_string(_capi.ERR_BUDGET).startswith(b"mandatory")
-    # logits: 1 lane x 1 row x 32 heads x 512 pages x 8 B = 131072; qpack 8192 -> 256-aligned
-    assert lib.kvr_workspace_bytes(1, 512, 1, 32, 8, 128) == 131072 + 8192
-    assert lib.kvr_workspace_bytes(0, 7, 1, 1, 1, 1) == 256 + 256
+    # logits: 1 lane x 1 row x 32 heads x 512 pages x 8 B = 131072; two
+    # statistics per softmax row: 32 x 16 B = 512; qpack 8192 -> 256-aligned
+    assert lib.kvr_workspace_bytes(1, 512, 1, 32, 8, 128) == 131072 + 512 + 8192
+    assert lib.kvr_workspace_bytes(0, 7, 1, 1, 1, 1) == 256 + 256 + 256
 
 
 def test_null_context_is_rejected():
