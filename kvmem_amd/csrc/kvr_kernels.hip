@@ -1,9 +1,10 @@
 // kvr_kernels.hip -- gfx950 kernels of the recall hot path.
 //
 // Summary kernel (HBM-bound, the dominant cost): one lane owns 8 channels of
-// one page and walks the page's token rows in order with 16-byte loads, so a
-// wave reads contiguous 1 KiB spans and every channel is summed in the
-// reference's order (binary32, token order from zero).  Scoring operands
+// one page (2 or 4 for a lone small fp16 layer) and walks the page's token
+// rows in order, so a wave reads contiguous spans of each row and every
+// channel is summed in the reference's order (binary32, token order from
+// zero).  Scoring operands
 // cross the recall fp16 boundary; logits, softmax and aggregation run in
 // binary64 (the reference's CPU precision) so selection flips only on true
 // near-ties.  Reference citations are relative to the KVMem 0.19.0 tree.
