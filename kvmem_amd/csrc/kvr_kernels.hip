@@ -1965,42 +1965,49 @@ __global__ __launch_bounds__(256) void k_unit_stats(SelectArgs a) {
 }
 
 // k_mean_scores: grid (ceil(pages / kScorePages), lanes), 256 threads, a
-// thread per page per 256; the lane's last workgroup selects (dynamic LDS:
-// the tail's keys).
-constexpr uint32_t kScorePP = 1, kScorePages = 256 * kScorePP, kScoreRows = 16;
+// quad of lanes per page: lane q of a quad computes the terms of rows q,
+// q + 4, ... (the exponentials and divisions, the bulk of the work) and the
+// quad adds them in row order from quad broadcasts, so every lane holds the
+// page's score.  The lane's last workgroup selects (dynamic LDS: the tail's
+// keys).
+constexpr uint32_t kScorePages = 64, kScoreRows = 4;  // pages per workgroup, rows per lane per pass
+__device__ __forceinline__ double quad_lane(double v, uint32_t q) {
+    switch (q) {
+        case 0: return dpp::move<0x00>(v);
+        case 1: return dpp::move<0x55>(v);
+        case 2: return dpp::move<0xAA>(v);
+        default: return dpp::move<0xFF>(v);
+    }
+}
 __global__ __launch_bounds__(256) void k_mean_scores(SelectArgs a) {
     __shared__ uint32_t s_last;
-    const uint32_t lane = blockIdx.y, n = a.pages;
+    const uint32_t lane = blockIdx.y, n = a.pages, q = threadIdx.x & 3u;
     const double *logits = a.logits + uint64_t(lane) * a.rows * a.qheads * n;
     const double *st = a.stats + uint64_t(lane) * a.units * 2;
     double *sc = a.scores + uint64_t(lane) * n;
-    const uint32_t j0 = blockIdx.x * kScorePages + threadIdx.x;
-    uint32_t jc[kScorePP];
-    bool on[kScorePP];
-    double acc[kScorePP];
+    const uint32_t j = blockIdx.x * kScorePages + (threadIdx.x >> 2), jc = min(j, n - 1);
+    const bool on = !a.mask || a.mask[jc >> a.mask_shift];
+    double acc = a.accumulate ? sc[jc] : 0.0;
+    for (uint32_t u0 = 0; u0 < a.units; u0 += 4 * kScoreRows) {
+        double x[kScoreRows], m[kScoreRows], s[kScoreRows], t[kScoreRows];
 #pragma unroll
-    for (uint32_t i = 0; i < kScorePP; ++i) {
-        jc[i] = min(j0 + i * 256, n - 1);
-        on[i] = !a.mask || a.mask[jc[i] >> a.mask_shift];
-        acc[i] = a.accumulate ? sc[jc[i]] : 0.0;
-    }
-    for (uint32_t u0 = 0; u0 < a.units; u0 += kScoreRows) {
-        double x[kScoreRows][kScorePP];
+        for (uint32_t k = 0; k < kScoreRows; ++k) {
+            const uint32_t u = min(u0 + 4 * k + q, a.units - 1);
+            x[k] = logits[uint64_t(u) * n + jc];
+            m[k] = st[2 * u];
+            s[k] = st[2 * u + 1];
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kScoreRows; ++k) t[k] = (on ? row_prob(x[k], m[k], s[k]) : 0.0) / a.weight;
 #pragma unroll
         for (uint32_t k = 0; k < kScoreRows; ++k)
 #pragma unroll
-            for (uint32_t i = 0; i < kScorePP; ++i) x[k][i] = logits[uint64_t(min(u0 + k, a.units - 1)) * n + jc[i]];
-#pragma unroll
-        for (uint32_t k = 0; k < kScoreRows; ++k) {
-            if (u0 + k >= a.units) break;
-            const double m = st[2 * (u0 + k)], s = st[2 * (u0 + k) + 1];
-#pragma unroll
-            for (uint32_t i = 0; i < kScorePP; ++i) acc[i] += (on[i] ? row_prob(x[k][i], m, s) : 0.0) / a.weight;
-        }
+            for (uint32_t r = 0; r < 4; ++r) {
+                const double v = quad_lane(t[k], r);
+                if (u0 + 4 * k + r < a.units) acc += v;
+            }
     }
-#pragma unroll
-    for (uint32_t i = 0; i < kScorePP; ++i)
-        if (j0 + i * 256 < n) store_device(sc + j0 + i * 256, acc[i]);
+    if (q == 0 && j < n) store_device(sc + j, acc);
     // Publish (stores complete at device scope), count; the last selects.
     wait_vmem();
     __syncthreads();

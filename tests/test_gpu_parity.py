@@ -151,8 +151,12 @@ def test_score_matches_oracle(ctx, shape, agg, mfma):
     assert abs(got.sum() - rows) <= rows * 1e-12 * max(1, heads)
 
 
-def test_score_mask_and_accumulate(ctx):
-    pages, rows, dim, qh, kvh, layers = 300, 3, 64, 8, 2, 2
+@pytest.mark.parametrize("pages", [300, 3000])
+def test_score_mask_and_accumulate(ctx, pages):
+    """Masked scores accumulated over two layers: rows in registers (300
+    pages; Max units in one workgroup with the terms in LDS) and long rows
+    (3000 pages; Mean through the units' statistics and page slices)."""
+    rows, dim, qh, kvh, layers = 3, 64, 8, 2, 2
     means, query = _score_inputs(pages, rows, dim, qh, kvh, layers=layers, closed_form=False)
     mask = (np.arange(pages) % 7 != 3).astype(np.uint8)
     for agg in (K.AGG_MEAN, K.AGG_MAX):
