@@ -873,50 +873,74 @@ __device__ __forceinline__ double block_sum(double v) {
 // tile's loads in flight together; per-head statistics first, then one pass
 // per page.  Thread t touches only pages j == t (mod 256).  Values this
 // thread stored are re-read at device scope.
-// f(j, value, on) over thread l's pages j < n of a long `row` (256 threads,
-// tiles of 16 values per thread, the tile's loads in flight together).
+// Tile `base` of a long `row` for thread l (256 threads, 16 values per
+// thread, the tile's loads in flight together; indices clamped into the row).
 // own: values this thread stored itself, re-read at device scope.
-template <class F>
-__device__ __forceinline__ void long_row_tiles(const SelectArgs &a, const double *row, bool own, F f) {
-    constexpr int T = 16;
-    constexpr uint32_t S = 256;  // threads per unit
+constexpr int kLongTile = 16;
+constexpr uint32_t kLongThreads = 256;
+__device__ __forceinline__ void long_row_load(const SelectArgs &a, const double *row, bool own, uint32_t base,
+                                              double (&x)[kLongTile], bool (&on)[kLongTile]) {
     const uint32_t n = a.pages, l = threadIdx.x;
-    for (uint32_t base = 0; base < n; base += S * T) {
-        double x[T];
-        bool on[T];
-        if (a.mask) {
-            uint8_t mk[T];
+    if (a.mask) {
+        uint8_t mk[kLongTile];
 #pragma unroll
-            for (int i = 0; i < T; ++i) {
-                const uint32_t j = min(base + l + i * S, n - 1);
-                x[i] = own || a.summaries ? load_device(row + j) : row[j];
-                mk[i] = a.mask[j >> a.mask_shift];
-            }
-#pragma unroll
-            for (int i = 0; i < T; ++i) on[i] = mk[i] != 0;
-        } else {
-#pragma unroll
-            for (int i = 0; i < T; ++i) {
-                const uint32_t j = min(base + l + i * S, n - 1);
-                x[i] = own || a.summaries ? load_device(row + j) : row[j];
-                on[i] = true;
-            }
+        for (int i = 0; i < kLongTile; ++i) {
+            const uint32_t j = min(base + l + i * kLongThreads, n - 1);
+            x[i] = own || a.summaries ? load_device(row + j) : row[j];
+            mk[i] = a.mask[j >> a.mask_shift];
         }
 #pragma unroll
-        for (int i = 0; i < T; ++i) {
-            const uint32_t j = base + l + i * S;
+        for (int i = 0; i < kLongTile; ++i) on[i] = mk[i] != 0;
+    } else {
+#pragma unroll
+        for (int i = 0; i < kLongTile; ++i) {
+            const uint32_t j = min(base + l + i * kLongThreads, n - 1);
+            x[i] = own || a.summaries ? load_device(row + j) : row[j];
+            on[i] = true;
+        }
+    }
+}
+// f(j, value, on) over thread l's pages j < n of a long `row`, tile by tile.
+template <class F>
+__device__ __forceinline__ void long_row_tiles(const SelectArgs &a, const double *row, bool own, F f) {
+    const uint32_t n = a.pages, l = threadIdx.x;
+    for (uint32_t base = 0; base < n; base += kLongThreads * kLongTile) {
+        double x[kLongTile];
+        bool on[kLongTile];
+        long_row_load(a, row, own, base, x, on);
+#pragma unroll
+        for (int i = 0; i < kLongTile; ++i) {
+            const uint32_t j = base + l + i * kLongThreads;
             if (j < n) f(j, x[i], on[i]);
         }
     }
 }
 // A long row's softmax statistics: its max m and sum s of exp(x - m) over
 // unmasked pages (per-thread partials in tile order, then block_max/sum).
+// KEEP: a row of one tile keeps its values in registers between the two
+// passes instead of loading them again (same values, same results; the
+// layer stack's softmax workgroups reload, which measured faster there).
+template <bool KEEP = false>
 __device__ __forceinline__ void long_row_stats(const SelectArgs &a, const double *row, bool own, double &m,
                                                double &s) {
-    double mm = -INFINITY;
+    double mm = -INFINITY, ss = 0.0;
+    if (KEEP && a.pages <= kLongThreads * kLongTile) {
+        const uint32_t l = threadIdx.x;
+        double x[kLongTile];
+        bool on[kLongTile];
+        long_row_load(a, row, own, 0, x, on);
+#pragma unroll
+        for (int i = 0; i < kLongTile; ++i)
+            if (l + i * kLongThreads < a.pages) mm = on[i] ? fmax(mm, x[i]) : mm;
+        m = block_max(mm);
+#pragma unroll
+        for (int i = 0; i < kLongTile; ++i)
+            if (l + i * kLongThreads < a.pages) ss += on[i] ? exp(x[i] - m) : 0.0;
+        s = block_sum(ss);
+        return;
+    }
     long_row_tiles(a, row, own, [&](uint32_t, double x, bool on) { mm = on ? fmax(mm, x) : mm; });
     m = block_max(mm);
-    double ss = 0.0;
     long_row_tiles(a, row, own, [&](uint32_t, double x, bool on) { ss += on ? exp(x - m) : 0.0; });
     s = block_sum(ss);
 }
@@ -1957,7 +1981,7 @@ __global__ __launch_bounds__(256) void k_unit_stats(SelectArgs a) {
     const uint32_t lane = blockIdx.y, unit = blockIdx.x;
     const double *row = a.logits + (uint64_t(lane) * a.rows * a.qheads + unit) * a.pages;
     double m, s;
-    long_row_stats(a, row, false, m, s);
+    long_row_stats<true>(a, row, false, m, s);
     if (threadIdx.x == 0) {
         a.stats[(uint64_t(lane) * a.units + unit) * 2] = m;
         a.stats[(uint64_t(lane) * a.units + unit) * 2 + 1] = s;
