@@ -82,12 +82,14 @@ __device__ __forceinline__ void add_q8x8(float *acc, uint32_t lo, uint32_t hi, f
     }
 }
 
-// The summary launch's fp16 key rows take the default cache policy
-// (measured 1.4 us faster per 64 MiB layer than the streaming one); its q8_0
-// rows and the stack's keep the streaming policy, which measured faster
-// there (q8_0 summary 42.0 against 46.9 us per 131072-token layer; stack
-// 15.2 against 16.6 us per 32768-token fp16 layer, 26.8 against 29.7 per
-// 131072-token q8_0 layer).
+// The summary launch's fp16 key rows take the default cache policy in its
+// one-wave workgroups (a lone small layer: measured 1.4 us faster per 64
+// MiB layer than the streaming one) and the streaming policy in 256-thread
+// ones (716 against 670 us per 8 lanes of 262144 tokens); its q8_0 rows and
+// the stack's take the streaming policy, which measured faster there (q8_0
+// summary 42.0 against 46.9 us per 131072-token layer; stack 15.2 against
+// 16.6 us per 32768-token fp16 layer, 26.8 against 29.7 per 131072-token
+// q8_0 layer).
 // Consumes rows 0..n-1 (n >= 1) in order through a ring of D loads in
 // flight: row t's load issues D rows before row t is used.  Loads past the
 // end are clamped to row n-1 (in bounds, never used), so no load sits behind
@@ -209,6 +211,9 @@ __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t blo
         for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
         if constexpr (SRC == kSrcKeysF16) {
             typedef typename F16Lane<CPL>::type V;
+            // streaming loads for whole-CU workgroups (a large layer), the
+            // default policy for the one-wave ones of a lone small layer
+            constexpr int kF16Policy = BS == 256 ? kBufferNontemporal : 0;
             auto add_row = [&](const V v) {
 #pragma unroll
                 for (int i = 0; i < CPL / 2; ++i) {
@@ -233,7 +238,7 @@ __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t blo
                     [&](uint32_t t) {
                         const int soff = int(t * row_bytes);
                         if constexpr (CPL == 8)
-                            return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(rs, col, soff, 0));
+                            return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(rs, col, soff, kF16Policy));
                         else if constexpr (CPL == 4)
                             return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b64(rs, col, soff, 0));
                         else
@@ -243,7 +248,9 @@ __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t blo
             } else {
                 const V *p = reinterpret_cast<const V *>(a.src + lane * a.src_lane_stride + (t0 * a.width + c0) * 2);
                 const uint64_t stride = gpp;  // lane loads per token row
-                stream_rows<kF16RingRows<CPL>>(n, [&](uint32_t t) { return p[t * stride]; }, add_row);
+                stream_rows<kF16RingRows<CPL>>(
+                    n, [&](uint32_t t) { return kF16Policy ? __builtin_nontemporal_load(p + t * stride) : p[t * stride]; },
+                    add_row);
             }
         } else {
             // q8_0 rows: lane owns 8 codes (quarter s) of block b, and the
