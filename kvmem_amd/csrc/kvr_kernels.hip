@@ -2060,6 +2060,16 @@ __global__ __launch_bounds__(256) void k_mean_scores(SelectArgs a) {
 // Sums restart at each layer's first row (binary32, token order, as in
 // summary_block).
 
+// Channels per summary lane of a key-history stack: fp16 keys whose pages
+// a wave's 64 lanes of 4 channels cover whole (widths a multiple of 256,
+// pages under 4 GiB) take 4, so twice the waves stream the same rows;
+// otherwise 8.
+__host__ __device__ inline uint32_t stack_cpl(int src, uint32_t width, uint32_t page_tokens) {
+    return src == kSrcKeysF16 && width % 256 == 0 && (uint64_t(page_tokens) + 64) * width * 2 < (uint64_t(1) << 32)
+               ? 4u
+               : 8u;
+}
+
 // PAGED: every wave's 64 channel groups lie in one page (width a multiple of
 // 512 channels) and a page spans less than 4 GiB.  Then the page and its
 // rows are wave-uniform: each layer's page is read through a buffer
@@ -2070,11 +2080,13 @@ __global__ __launch_bounds__(256) void k_mean_scores(SelectArgs a) {
 // the chunk loop has no branch.
 // Otherwise each lane keeps its own row pointer, clamped to the page's last
 // row.
-template <int SRC, bool PAGED>
+// CPL: channels per lane (stack_cpl: 4 for paged fp16 keys, else 8).
+template <int SRC, bool PAGED, int CPL = 8>
 __device__ __forceinline__ void stack_summaries(const StackGroupArgs &g, uint32_t block, uint32_t l0, uint32_t m) {
+    static_assert(CPL == 8 || (SRC == kSrcKeysF16 && PAGED && CPL == 4), "4-channel lanes read paged fp16 keys");
     __builtin_amdgcn_s_setprio(2);
     const SummaryArgs &a = g.s[0];
-    const uint32_t gpp = a.width >> 3;
+    const uint32_t gpp = a.width / CPL;
     uint32_t cg, page, lane;
     if constexpr (PAGED) {
         const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x) >> 6;
@@ -2092,7 +2104,7 @@ __device__ __forceinline__ void stack_summaries(const StackGroupArgs &g, uint32_
         page = uint32_t(rest % a.pages);
         lane = uint32_t(rest / a.pages);
     }
-    const uint32_t c0 = cg * 8;
+    const uint32_t c0 = cg * CPL;
     const uint64_t t0 = uint64_t(page) * a.page_tokens;
     const uint64_t tail = a.tokens - t0;
     const uint32_t n = tail < a.page_tokens ? uint32_t(tail) : a.page_tokens;
@@ -2134,7 +2146,7 @@ __device__ __forceinline__ void stack_summaries(const StackGroupArgs &g, uint32_
         uint16_t hb[8] = {0, 0, 0, 0, 0, 0, 0, 0};
         uint32_t bad = kOperandOk;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
+        for (int k = 0; k < CPL; ++k) {
             mean[k] = acc[k] * inv;
             const uint32_t e = recall16(mean[k], hb[k]);
             bad = bad ? bad : e;
@@ -2144,24 +2156,27 @@ __device__ __forceinline__ void stack_summaries(const StackGroupArgs &g, uint32_
         if (mo) {
             float4 *m4 = reinterpret_cast<float4 *>(mo + out);
             m4[0] = make_float4(mean[0], mean[1], mean[2], mean[3]);
-            m4[1] = make_float4(mean[4], mean[5], mean[6], mean[7]);
+            if constexpr (CPL == 8) m4[1] = make_float4(mean[4], mean[5], mean[6], mean[7]);
         }
         if (bad) raise_operand(a.status, bad, pick(i, epoch[0], epoch[1], epoch[2], epoch[3]));
         if (so) {
-            u32x4 v;
+            typedef typename F16Lane<CPL>::type V;
+            V v;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) v[k] = uint32_t(hb[2 * k]) | (uint32_t(hb[2 * k + 1]) << 16);
-            *reinterpret_cast<u32x4 *>(so + out) = v;
+            for (int k = 0; k < CPL / 2; ++k) v[k] = uint32_t(hb[2 * k]) | (uint32_t(hb[2 * k + 1]) << 16);
+            *reinterpret_cast<V *>(so + out) = v;
         }
     };
     // Row u of a chunk is summed only when it is a real row (pad rows add
     // zeros: acc is never -0, so acc + (+-0) is acc bit for bit).
     auto consume = [&](const auto v, bool real) {
         if constexpr (SRC == kSrcKeysF16) {
-            u32x4 w;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) w[k] = real ? v[k] : 0u;
-            add_f16x8(acc, w);
+            for (int k = 0; k < CPL / 2; ++k) {
+                const uint32_t w = real ? uint32_t(v[k]) : 0u;
+                acc[2 * k] += h2f(uint16_t(w & 0xffffu));
+                acc[2 * k + 1] += h2f(uint16_t(w >> 16));
+            }
         } else {
             const uint32_t lo = __builtin_amdgcn_perm(v[1], v[0], code_sel);
             const uint32_t hi = __builtin_amdgcn_perm(v[2], v[1], code_sel);
@@ -2178,7 +2193,7 @@ __device__ __forceinline__ void stack_summaries(const StackGroupArgs &g, uint32_
     // PAGED: the page's n rows in the layer are one buffer resource, and
     // row u of a chunk sits at col + coff + u*row_bytes with coff =
     // r0*row_bytes; otherwise the chunk's first row is at cp.
-    constexpr int D = SRC == kSrcKeysF16 ? kF16Rows : kQ8Rows;
+    constexpr int D = SRC == kSrcKeysF16 ? kF16RingRows<CPL> : kQ8Rows;
     const uint32_t per_layer = (n + D - 1) / D;
     const uint32_t chunks = m * per_layer;
     const uint8_t *cp = layer_first(0);
@@ -2191,7 +2206,9 @@ __device__ __forceinline__ void stack_summaries(const StackGroupArgs &g, uint32_
         if constexpr (PAGED) {
             // the row offset is a scalar computed per row (no per-lane table)
             const uint32_t off = col + __builtin_amdgcn_readfirstlane(coff + uint32_t(u) * row_bytes);
-            if constexpr (SRC == kSrcKeysF16)
+            if constexpr (SRC == kSrcKeysF16 && CPL == 4)
+                return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, kBufferNontemporal));
+            else if constexpr (SRC == kSrcKeysF16)
                 return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kBufferNontemporal));
             else
                 return __builtin_bit_cast(u32x3, __builtin_amdgcn_raw_buffer_load_b96(rs, off, 0, kBufferNontemporal));
@@ -2278,7 +2295,9 @@ __global__ __launch_bounds__(256) void k_stack_group(StackGroupArgs g) {
     } else {
         const SummaryArgs &a = g.s[0];
         const uint64_t row_bytes = SRC == kSrcKeysF16 ? a.width * 2 : (a.width >> 5) * kQ8Bytes;
-        if ((a.width & 511) == 0 && (uint64_t(a.page_tokens) + 64) * row_bytes < (uint64_t(1) << 32))
+        if (SRC == kSrcKeysF16 && stack_cpl(SRC, a.width, a.page_tokens) == 4)
+            stack_summaries<SRC, true, SRC == kSrcKeysF16 ? 4 : 8>(g, blk, l0, m);
+        else if ((a.width & 511) == 0 && (uint64_t(a.page_tokens) + 64) * row_bytes < (uint64_t(1) << 32))
             stack_summaries<SRC, true>(g, blk, l0, m);
         else
             stack_summaries<SRC, false>(g, blk, l0, m);
@@ -3103,7 +3122,7 @@ hipError_t launch_stack_group(int source, StackGroupArgs g, hipStream_t s) {
     // A layer whose summaries take fewer workgroups than the GPU has CUs
     // leaves CUs idle if one workgroup walks all the group's layers: split
     // the layers into parts until the launch has a workgroup per CU.
-    g.layer_blocks = g.m ? blocks_for(uint64_t(sa.lanes) * sa.pages * (sa.width >> 3)) : 1;
+    g.layer_blocks = g.m ? blocks_for(uint64_t(sa.lanes) * sa.pages * (sa.width / stack_cpl(source, sa.width, sa.page_tokens))) : 1;
     uint32_t parts = 1;
     if (g.m && g.layer_blocks < kStackSpreadBlocks)
         parts = min(g.m, (kStackSpreadBlocks + g.layer_blocks - 1) / g.layer_blocks);
