@@ -490,9 +490,10 @@ kvr_status kvr_recall_layer(kvr_context *ctx, const kvr_layer_recall *desc,
  * device array of KVR_NOALLOC_SCRATCH_BYTES per GPU (held until the process
  * ends; its first KVR_NOALLOC_MAX_LANES * 4 bytes are the counters) instead
  * of the context's workspace; a call whose lanes*rows*query_heads*pages*8
- * bytes of logits (+ lanes*rows*query_heads*head_dim*2 of packed queries
- * on the matrix-core path, each rounded up to 256) do not fit fails with
- * KVR_ERR_WORKSPACE before any launch.  The gather uses the kernel engine
+ * bytes of logits, lanes*rows*query_heads*16 of softmax statistics (+
+ * lanes*rows*query_heads*head_dim*2 of packed queries on the matrix-core
+ * path), each rounded up to 256, do not fit fails with KVR_ERR_WORKSPACE
+ * before any launch.  The gather uses the kernel engine
  * (KVR_ENGINE_SDMA with planes: KVR_ERR_UNSUPPORTED).  The context must have
  * been created beforehand (kvr_create allocates; this call does not).  Every
  * call on one GPU shares its array: calls that overlap in time on one GPU,
