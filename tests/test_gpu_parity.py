@@ -200,6 +200,35 @@ def test_scored_selection_long_rows(ctx, pages, agg):
     assert np.array_equal(host(sel, np.uint32), O.pick_scored_blocks(expect, k, mand, O.TIE_LOWER_FIRST))
 
 
+@pytest.mark.parametrize("pages,agg", [(200, K.AGG_MAX), (3000, K.AGG_MEAN), (3000, K.AGG_MAX)])
+@pytest.mark.parametrize("tie", [K.TIE_LOWER_FIRST, K.TIE_HIGHER_FIRST])
+def test_multi_lane_selection(ctx, pages, agg, tie):
+    """Three lanes of different summaries and queries through one call: short
+    Max rows (softmax units and tail in one workgroup per lane), long Mean rows
+    (units' statistics, then page slices and tail) and long Max rows, with a
+    score mask and mandatory pages; every lane against the oracle."""
+    lanes, rows, dim, qh, kvh, k, pt = 3, 2, 64, 8, 2, 24, 16
+    means, query = _score_inputs(pages, rows, dim, qh, kvh, layers=lanes, closed_form=False)
+    mask = (np.arange(pages) % 13 != 6).astype(np.uint8)
+    mand = (1, pages - 2)
+    s16 = dev(means.astype(np.float16).view(np.uint16).ravel())
+    qd, md = dev(query.ravel()), dev(mask)
+    out = zeros(lanes * pages, np.float64)
+    sel = zeros(lanes * k, np.uint32)
+    cnt = zeros(lanes, np.uint32)
+    ctx.recall_layer(query=K.make_query(qd, K.FMT_F32, rows, qh, kvh, dim, lanes=lanes), summaries=s16,
+                     pages=pages, page_tokens=pt, lanes=lanes, scores=out, selected=sel, count=cnt, k=k,
+                     aggregation=agg, score_mask=md, mandatory=mand, tie_rule=tie)
+    ctx.check()
+    got = host(out, np.float64).reshape(lanes, pages)
+    gsel = host(sel, np.uint32).reshape(lanes, k)
+    assert np.array_equal(host(cnt, np.uint32), [k] * lanes)
+    for l in range(lanes):
+        expect = O.page_softmax_scores(means[l:l + 1], query[l:l + 1], [rows], qh, kvh, dim, agg, score_mask=mask)
+        assert _rel_err(got[l], expect) <= REL, l
+        assert np.array_equal(gsel[l], O.pick_scored_blocks(expect, k, mand, tie)), l
+
+
 @pytest.mark.parametrize("pages,rows,dim,qh,kvh", [(300, 4, 96, 8, 2), (77, 16, 36, 4, 4)])
 def test_mfma_other_head_dims(ctx, pages, rows, dim, qh, kvh):
     """Head dims the matrix-core path handles with a run-time k-range (the
