@@ -151,6 +151,35 @@ def test_multilane_batched_recall(ctx, mfma):
     pv.free()
 
 
+@pytest.mark.parametrize("agg", [K.AGG_MEAN, K.AGG_MAX])
+def test_multilane_small_layer_fused(ctx, agg):
+    """Two lanes of a small fp16 layer (16 pages each, 4096 summary lanes of 2
+    channels in one-wave workgroups) with packed fp16 queries: fp16
+    summaries bit-exact, scores and selections per lane against the oracle."""
+    L, T, HQ, HKV, D, PT, R, KSEL = 2, 4096, 32, 8, 128, 256, 1, 5
+    W, pages = HKV * D, T // PT
+    keys = O.synth_normal_f16(SEED, 130, L * T * W)
+    q = O.synth_normal_f16(SEED, 131, L * R * HQ * D)
+    s16 = zeros(L * pages * W, np.uint16)
+    scores = zeros(L * pages, np.float64)
+    sel = zeros(L * KSEL, np.uint32)
+    cnt = zeros(L, np.uint32)
+    ctx.recall_layer(keys=K.make_keys(dev(keys), K.FMT_F16, T, HKV, D, PT, lanes=L), summaries=s16,
+                     query=K.make_query(dev(q), K.FMT_F16, R, HQ, HKV, D, lanes=L), scores=scores,
+                     selected=sel, count=cnt, k=KSEL, aggregation=agg)
+    ctx.check()
+    got16 = host(s16, np.uint16).reshape(L, pages * W)
+    got_s = host(scores, np.float64).reshape(L, pages)
+    got = host(sel, np.uint32).reshape(L, KSEL)
+    for l in range(L):
+        _, means = O.page_summaries(keys[l * T * W:(l + 1) * T * W], O.FMT_F16, T, W, PT)
+        assert np.array_equal(got16[l], means.astype(np.float16).view(np.uint16).ravel()), l
+        qf = q[l * R * HQ * D:(l + 1) * R * HQ * D].view(np.float16).astype(np.float32).reshape(1, R, HQ, D)
+        s = O.page_softmax_scores(means[None], qf, [R], HQ, HKV, D, agg)
+        assert _rel_err(got_s[l], s) <= REL, l
+        assert np.array_equal(got[l], O.pick_scored_blocks(s, KSEL)), l
+
+
 def test_layerwise_pipeline_resident_summaries(ctx):
     """Layerwise recall over resident summaries: score layer l+1 on the select
     stream while layer l's pages stream in on the copy stream.  Hq 16 / Hkv 2,
