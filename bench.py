@@ -225,6 +225,20 @@ def run(args):
         f"{stack_gpu_us / L:.1f} us/layer); stack launch ({G} layers) {kern_us_mean:.1f} us, "
         f"summary start -> selection {select_us:.1f} us")
 
+    # ---- one layer alone (kvr_recall_layer): summary start -> selection ---
+    ev_a, ev_b = hip.event(), hip.event()
+    lone = []
+    for rep in range(max(3, args.steps)):
+        for l in range(min(L, 4)):
+            ctx.recall(K.Context.layer_recall(keys=keys[l], summaries=s16[l], query=queries[l], scores=scores[l],
+                                              selected=sel[l], count=cnt[l], k=KSEL, aggregation=K.AGG_MEAN,
+                                              summary_events=(ev_a, None), select_end=ev_b))
+            ctx.check()
+            if rep:
+                lone.append(hip.elapsed_ms(ev_a, ev_b) * 1e3)
+    lone_us = float(np.median(lone))
+    log(f"one layer alone (kvr_recall_layer): summary start -> selection {lone_us:.1f} us")
+
     # ---- pipelined recall: each layer's stage-in beside the next selects ---
     ev_p = events()
     d_p = descriptors(ev_p, True)
@@ -298,6 +312,7 @@ def run(args):
             "gather_workgroups": args.gather_wgs or "16 x 64 threads (copy default)", "gather_chunk_rows": args.chunk_rows or 8,
         },
         "select_us_per_layer": round(select_us, 2),
+        "select_one_layer_us": round(lone_us, 2),
         "select_stack_us_per_layer": round(ms_per_step / L * 1e3, 2),
         "scored_frac_hbm": round(scored_gbps / HBM_PEAK_GBPS, 4),
         "latency_us_per_layer": round(pipe_us, 2),
