@@ -90,16 +90,18 @@ __device__ __forceinline__ void add_q8x8(float *acc, uint32_t lo, uint32_t hi, f
 // summary 42.0 against 46.9 us per 131072-token layer; stack 15.2 against
 // 16.6 us per 32768-token fp16 layer, 26.8 against 29.7 per 131072-token
 // q8_0 layer).
+
+// Ring depths of the summary streams: 12 rows of 16-byte loads (fp16) and
+// 32 rows of 12-byte loads (q8_0).  Deeper rings of 16-byte loads make the
+// register allocator copy ring slots whose loads are still in flight;
+// narrower fp16 lanes (one 8- or 4-byte load per row) afford 24 or 32 rows.
+constexpr int kF16Rows = 12, kQ8Rows = 32;
+template <int CPL> constexpr int kF16RingRows = CPL == 8 ? kF16Rows : CPL == 4 ? 24 : 32;
+
 // Consumes rows 0..n-1 (n >= 1) in order through a ring of D loads in
 // flight: row t's load issues D rows before row t is used.  Loads past the
 // end are clamped to row n-1 (in bounds, never used), so no load sits behind
 // a branch and the loads issue back to back.
-// Ring depths of the summary streams: 12 rows of 16-byte loads (fp16) and
-// 32 rows of 12-byte loads (q8_0).  Deeper fp16 rings make the register
-// allocator copy ring slots whose loads are still in flight.
-constexpr int kF16Rows = 12, kQ8Rows = 32;
-// Narrower fp16 lanes (one 8- or 4-byte load per row) afford deeper rings.
-template <int CPL> constexpr int kF16RingRows = CPL == 8 ? kF16Rows : CPL == 4 ? 24 : 32;
 template <int D, class Load, class Use>
 __device__ __forceinline__ void stream_rows(uint32_t n, Load load, Use use) {
     decltype(load(0u)) ring[D];
@@ -240,9 +242,9 @@ __device__ __forceinline__ void summary_block(const SummaryArgs &a, uint32_t blo
                         if constexpr (CPL == 8)
                             return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(rs, col, soff, kF16Policy));
                         else if constexpr (CPL == 4)
-                            return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b64(rs, col, soff, 0));
+                            return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b64(rs, col, soff, kF16Policy));
                         else
-                            return V(__builtin_amdgcn_raw_buffer_load_b32(rs, col, soff, 0));
+                            return V(__builtin_amdgcn_raw_buffer_load_b32(rs, col, soff, kF16Policy));
                     },
                     add_row);
             } else {
