@@ -1580,13 +1580,26 @@ kvr_status enqueue_stack(kvr_context *ctx, std::vector<LayerPlan> &plans, hipStr
                 cur[i].summaries = d->summaries;
                 cur[i].q = L.p.q;
             }
-            if (d->summary_begin) KVR_HIP(hipEventRecord(static_cast<hipEvent_t>(d->summary_begin), ss));
         }
-        const int src = g.m ? plans[first[k]].src : prev_src;
-        KVR_HIP(kvr::launch_stack_group(src, g, ss));
+        // The first of the group's layers with summary events gets them
+        // stamped by the launch itself (its start and end, no stream
+        // markers); any other layer's events bracket the launch as markers.
+        uint32_t timed = g.m;
+        for (uint32_t i = 0; i < g.m && timed == g.m; ++i) {
+            const kvr_layer_recall *d = plans[first[k] + i].d;
+            if (d->summary_begin || d->summary_end) timed = i;
+        }
         for (uint32_t i = 0; i < g.m; ++i) {
             const kvr_layer_recall *d = plans[first[k] + i].d;
-            if (d->summary_end) KVR_HIP(hipEventRecord(static_cast<hipEvent_t>(d->summary_end), ss));
+            if (i != timed && d->summary_begin) KVR_HIP(hipEventRecord(static_cast<hipEvent_t>(d->summary_begin), ss));
+        }
+        const int src = g.m ? plans[first[k]].src : prev_src;
+        const kvr_layer_recall *td = timed < g.m ? plans[first[k] + timed].d : nullptr;
+        KVR_HIP(kvr::launch_stack_group(src, g, ss, td ? static_cast<hipEvent_t>(td->summary_begin) : nullptr,
+                                        td ? static_cast<hipEvent_t>(td->summary_end) : nullptr));
+        for (uint32_t i = 0; i < g.m; ++i) {
+            const kvr_layer_recall *d = plans[first[k] + i].d;
+            if (i != timed && d->summary_end) KVR_HIP(hipEventRecord(static_cast<hipEvent_t>(d->summary_end), ss));
         }
         if (k > 0)
             for (uint32_t l = first[k - 1]; l < first[k]; ++l)

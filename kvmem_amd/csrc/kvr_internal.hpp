@@ -205,7 +205,10 @@ hipError_t launch_select_groups(const SelectArgs &a, hipStream_t s);
 constexpr uint32_t kFixedBitmapPages = 524288;
 // one stack launch: `pa`'s softmax/selection beside `sa`'s summaries with
 // fused logits (sa.q and sa.logits set)
-hipError_t launch_stack_group(int source, StackGroupArgs g, hipStream_t s);
+// start/stop (either may be null): events stamped with the launch's own
+// start and end.
+hipError_t launch_stack_group(int source, StackGroupArgs g, hipStream_t s, hipEvent_t start = nullptr,
+                              hipEvent_t stop = nullptr);
 hipError_t launch_gather(const GatherArgs &a, hipStream_t s);
 hipError_t launch_accumulate(const AccumulateArgs &a, hipStream_t s);
 hipError_t launch_finalize(const FinalizeArgs &a, hipStream_t s);

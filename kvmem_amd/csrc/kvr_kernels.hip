@@ -11,6 +11,7 @@
 #include "kvr_device.hpp"
 #include "kvr_internal.hpp"
 
+#include <hip/hip_ext.h>
 #include <math.h>
 
 #include <type_traits>
@@ -3117,7 +3118,7 @@ hipError_t launch_probs(const SelectArgs &a, hipStream_t s) {
 }
 
 constexpr uint32_t kStackSpreadBlocks = 256;  // summary workgroups that fill MI355X's 256 CUs
-hipError_t launch_stack_group(int source, StackGroupArgs g, hipStream_t s) {
+hipError_t launch_stack_group(int source, StackGroupArgs g, hipStream_t s, hipEvent_t start, hipEvent_t stop) {
     (void)hipGetLastError();  // report only this launch\'s error
     const SummaryArgs &sa = g.s[0];
     const SelectArgs &pa = g.p[0];
@@ -3147,7 +3148,12 @@ hipError_t launch_stack_group(int source, StackGroupArgs g, hipStream_t s) {
         }
     }
     const uint32_t pages = g.mp ? pa.pages : sa.pages;
-    auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, lds, s, g); };
+    // start/stop: events stamped with the kernel's own start and end (no
+    // markers on the stream between launches)
+    auto go = [&](auto kernel) {
+        if (start || stop) hipExtLaunchKernelGGL(kernel, grid, block, lds, s, start, stop, 0u, g);
+        else hipLaunchKernelGGL(kernel, grid, block, lds, s, g);
+    };
     const bool f16 = source == kSrcKeysF16, q8 = source == kSrcKeysQ8;
     if (pages <= 256) {
         if (f16) go(k_stack_group<kSrcKeysF16, 4>); else if (q8) go(k_stack_group<kSrcKeysQ8, 4>);
