@@ -511,8 +511,10 @@ kvr_status kvr_recall_layer_noalloc(kvr_context *ctx, const kvr_layer_recall *de
  * keeps 2*KVR_STACK_GROUP logits buffers: a borrowed workspace needs
  * 2*KVR_STACK_GROUP times kvr_workspace_bytes of one layer).  Each layer's selection, select_end event
  * and stage-in therefore follow the next group's launch, and a layer's
- * summary events bracket its group's launch.  Otherwise the layers run one
- * after another.  Replaces one select_layerwise_history call per attention
+ * summary events bracket its group's launch: the first layer of a group
+ * that has summary events gets them stamped with the launch's own start and
+ * end (no markers between kernels), any other layer's are recorded just
+ * before and after it.  Otherwise the layers run one after another.  Replaces one select_layerwise_history call per attention
  * layer (kvmem/src/host/layerwise_selection.cpp:185-199), each followed by
  * that layer's stage-in. */
 kvr_status kvr_recall_stack(kvr_context *ctx, const kvr_layer_recall *layers, uint32_t n,
