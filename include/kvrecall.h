@@ -242,10 +242,11 @@ typedef struct kvr_layer_recall {
     uint32_t n_planes;
     kvr_copy_engine engine;
     int force_mfma;                /* -1 never, 0 by rows*group >= 16, 1 always */
-    void *summary_begin;           /* optional hipEvent_t recorded on the select
-                                      stream just before / after the summary
-                                      kernel (with resident summaries: the
-                                      logits kernel) */
+    void *summary_begin;           /* optional hipEvent_t stamped with the
+                                      start / end of the summary kernel (with
+                                      resident summaries: recorded on the
+                                      select stream just before / after the
+                                      logits kernels) */
     void *summary_end;             /* (measurement only; may be NULL;
                                       refused while the stream is captured)  */
     void *select_end;              /* optional hipEvent_t recorded on the select

@@ -1427,16 +1427,16 @@ kvr_status enqueue_layer(kvr_context *ctx, LayerPlan &L, hipStream_t ss, hipStre
     ++ctx->epoch;
     if (d->keys) {
         auto a = summary_args(ctx, d->keys, L.pages, L.key_ls, d->means, d->summaries);
-        if (d->summary_begin) KVR_HIP(hipEventRecord(static_cast<hipEvent_t>(d->summary_begin), ss));
+        // the summary events are stamped with the kernel's own start and end
+        const hipEvent_t b = static_cast<hipEvent_t>(d->summary_begin), e = static_cast<hipEvent_t>(d->summary_end);
         if (p.mfma) {
-            KVR_HIP(kvr::launch_summary(L.src, false, a, ss));
+            KVR_HIP(kvr::launch_summary(L.src, false, a, ss, b, e));
         } else {
             a.q = p.q;
             a.q_stage = stage_query(p.q);
             a.logits = p.logits;
-            KVR_HIP(kvr::launch_summary(L.src, true, a, ss));
+            KVR_HIP(kvr::launch_summary(L.src, true, a, ss, b, e));
         }
-        if (d->summary_end) KVR_HIP(hipEventRecord(static_cast<hipEvent_t>(d->summary_end), ss));
         if (p.mfma)
             if (kvr_status st = enqueue_logits(ctx, p, d->summaries, ss)) return st;
     } else {

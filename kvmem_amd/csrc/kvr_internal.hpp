@@ -190,7 +190,10 @@ struct CopyOp {
 };
 
 // ---- launchers (kvr_kernels.hip) ------------------------------------------
-hipError_t launch_summary(int source, bool fuse, const SummaryArgs &a, hipStream_t s);
+// start/stop (either may be null): events stamped with the launch's own
+// start and end.
+hipError_t launch_summary(int source, bool fuse, const SummaryArgs &a, hipStream_t s, hipEvent_t start = nullptr,
+                          hipEvent_t stop = nullptr);
 hipError_t launch_pack_query(const PackQueryArgs &a, hipStream_t s);
 hipError_t launch_logits_mfma(const MfmaLogitsArgs &a, hipStream_t s);
 // page softmax -> terms -> aggregation (+ selection); grid (units, lanes)

@@ -3017,30 +3017,38 @@ inline unsigned blocks_for(uint64_t threads, unsigned per = 256) {
 }  // namespace
 
 // ---- launchers ------------------------------------------------------------
+// One summary launch; start/stop (either may be null) are stamped with the
+// kernel's own start and end.
+template <class Kernel>
+void launch_k_summary(Kernel kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, hipEvent_t start,
+                      hipEvent_t stop, const SummaryArgs &a) {
+    if (start || stop) hipExtLaunchKernelGGL(kernel, grid, block, uint32_t(lds), s, start, stop, 0u, a);
+    else hipLaunchKernelGGL(kernel, grid, block, lds, s, a);
+}
+
 template <int BS>
-void launch_summary_bs(int source, bool fuse, const SummaryArgs &a, uint64_t threads, size_t lds, hipStream_t s) {
+void launch_summary_bs(int source, bool fuse, const SummaryArgs &a, uint64_t threads, size_t lds, hipStream_t s,
+                       hipEvent_t start, hipEvent_t stop) {
     const dim3 grid(blocks_for(threads, BS)), block(BS);
-    if (source == kSrcKeysF16 && fuse)
-        hipLaunchKernelGGL((k_summary<kSrcKeysF16, true, BS>), grid, block, lds, s, a);
-    else if (source == kSrcKeysF16)
-        hipLaunchKernelGGL((k_summary<kSrcKeysF16, false, BS>), grid, block, 0, s, a);
-    else if (source == kSrcKeysQ8 && fuse)
-        hipLaunchKernelGGL((k_summary<kSrcKeysQ8, true, BS>), grid, block, lds, s, a);
-    else if (source == kSrcKeysQ8)
-        hipLaunchKernelGGL((k_summary<kSrcKeysQ8, false, BS>), grid, block, 0, s, a);
-    else
-        hipLaunchKernelGGL((k_summary<kSrcSummary, true, BS>), grid, block, lds, s, a);
+    auto go = [&](auto kernel, size_t l) { launch_k_summary(kernel, grid, block, l, s, start, stop, a); };
+    if (source == kSrcKeysF16 && fuse) go(k_summary<kSrcKeysF16, true, BS>, lds);
+    else if (source == kSrcKeysF16) go(k_summary<kSrcKeysF16, false, BS>, 0);
+    else if (source == kSrcKeysQ8 && fuse) go(k_summary<kSrcKeysQ8, true, BS>, lds);
+    else if (source == kSrcKeysQ8) go(k_summary<kSrcKeysQ8, false, BS>, 0);
+    else go(k_summary<kSrcSummary, true, BS>, lds);
 }
 
 template <int CPL>
-void launch_summary_narrow(bool fuse, const SummaryArgs &a, size_t lds, hipStream_t s) {
+void launch_summary_narrow(bool fuse, const SummaryArgs &a, size_t lds, hipStream_t s, hipEvent_t start,
+                           hipEvent_t stop) {
     const dim3 grid(blocks_for(uint64_t(a.lanes) * a.pages * (a.width / CPL), 64)), block(64);
-    if (fuse) hipLaunchKernelGGL((k_summary<kSrcKeysF16, true, 64, CPL>), grid, block, lds, s, a);
-    else hipLaunchKernelGGL((k_summary<kSrcKeysF16, false, 64, CPL>), grid, block, 0, s, a);
+    if (fuse) launch_k_summary(k_summary<kSrcKeysF16, true, 64, CPL>, grid, block, lds, s, start, stop, a);
+    else launch_k_summary(k_summary<kSrcKeysF16, false, 64, CPL>, grid, block, 0, s, start, stop, a);
 }
 
 constexpr uint64_t kSummarySpreadBlocks = 256;  // MI355X's CUs
-hipError_t launch_summary(int source, bool fuse, const SummaryArgs &a, hipStream_t s) {
+hipError_t launch_summary(int source, bool fuse, const SummaryArgs &a, hipStream_t s, hipEvent_t start,
+                          hipEvent_t stop) {
     (void)hipGetLastError();  // report only this launch\'s error
     const uint64_t threads = uint64_t(a.lanes) * a.pages * (a.width >> 3);
     const size_t lds = fuse && a.q_stage ? size_t(a.q.rows) * a.q.qheads * a.q.dim * 2 : 0;  // q_lds_buf
@@ -3053,13 +3061,13 @@ hipError_t launch_summary(int source, bool fuse, const SummaryArgs &a, hipStream
         const bool fits2 = a.width % 2 == 0 && (!fuse || a.q.dim / 2 <= 64);
         const bool fits4 = a.width % 4 == 0 && (!fuse || a.q.dim / 4 <= 64);
         if (source == kSrcKeysF16 && fits2 && 4 * waves <= 4 * kSummarySpreadBlocks)
-            launch_summary_narrow<2>(fuse, a, lds, s);
+            launch_summary_narrow<2>(fuse, a, lds, s, start, stop);
         else if (source == kSrcKeysF16 && fits4 && 2 * waves <= 4 * kSummarySpreadBlocks)
-            launch_summary_narrow<4>(fuse, a, lds, s);
+            launch_summary_narrow<4>(fuse, a, lds, s, start, stop);
         else
-            launch_summary_bs<64>(source, fuse, a, threads, lds, s);
+            launch_summary_bs<64>(source, fuse, a, threads, lds, s, start, stop);
     } else {
-        launch_summary_bs<256>(source, fuse, a, threads, lds, s);
+        launch_summary_bs<256>(source, fuse, a, threads, lds, s, start, stop);
     }
     return hipGetLastError();
 }
