@@ -97,7 +97,8 @@ __device__ __forceinline__ void add_q8x8(float *acc, uint32_t lo, uint32_t hi, f
 // register allocator copy ring slots whose loads are still in flight;
 // narrower fp16 lanes (one 8- or 4-byte load per row) afford 32 rows (for
 // 4-channel stack lanes 16 rows measured 178 us per steady launch, 24 rows
-// 167.4 us, 32 rows 166.7 us).
+// 167.4 us, 32 rows 166.7 us).  48 rows of q8_0 measured slower than 32
+// (k8v4 stack 27.7 against 26.7 us per layer).
 constexpr int kF16Rows = 12, kQ8Rows = 32;
 template <int CPL> constexpr int kF16RingRows = CPL == 8 ? kF16Rows : 32;
 
